@@ -1,0 +1,200 @@
+/*
+ * rfadam8.h -- C ABI of the MI355X (gfx950) 8-bit AdamW step library
+ * (librfadam8.so).
+ *
+ * The reference (rollfast, pure Python on JAX/Optax) has no native boundary:
+ * its hot path is the Python functions cited beside each entry point below,
+ * traced by jax.jit.  This ABI is what an XLA FFI custom-call handler (or any
+ * other host binding: ctypes, a C++ training loop) calls in their place.
+ *
+ * Conventions
+ *  - Every pointer argument is a device pointer unless documented otherwise;
+ *    sizes are element counts.  No torch or XLA types cross the boundary.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *    Calls only enqueue work on that stream; they never synchronise, except
+ *    rf_adam8_step (documented below) and plan creation/destruction.
+ *  - Functions return RF_OK or an error code; rf_last_error() returns the
+ *    calling thread's last message.  Nothing throws across the ABI.
+ *  - Updates are in place (JAX donation semantics): params, moment codes,
+ *    moment scales and fallback moments are read and overwritten.
+ */
+#ifndef RFADAM8_H
+#define RFADAM8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t rf_status;
+#define RF_OK 0
+#define RF_ERR_INVALID 1     /* bad argument: shape, dtype, size, null pointer */
+#define RF_ERR_HIP 2         /* a HIP runtime call failed */
+#define RF_ERR_UNSUPPORTED 3 /* valid for the reference, not implemented here */
+
+/* Element types of params, grads and fallback moments. */
+#define RF_F32 0
+#define RF_BF16 1
+
+/* Moment storage of one leaf (adam8.py:605-630 _init_moment_leaf). */
+#define RF_MOMENT_QUANTIZED 0 /* uint8 codes [nblocks*block_size] + f32 scales [nblocks] */
+#define RF_MOMENT_F32 1       /* fallback_dtype float32 */
+#define RF_MOMENT_BF16 2      /* fallback_dtype bfloat16 */
+
+/* Quantizers (adam8.py:113-187 quantize_blocks `quantizer`). */
+#define RF_Q_DYNAMIC_SIGNED 0   /* "bitsandbytes.dynamic.signed.8bit.v1", zero code 127 */
+#define RF_Q_DYNAMIC_UNSIGNED 1 /* "bitsandbytes.dynamic.unsigned.8bit.v1", zero code 0 */
+#define RF_Q_SYMMETRIC_INT8 2   /* "rollfast.symmetric_int8.neg127_pos127.v1", int8 */
+
+/* rf_adam8_hparams.flags */
+#define RF_NESTEROV 1u   /* scale_by_adam8(nesterov=True), adam8.py:341-350 */
+#define RF_DECAY_WEAK 4u /* weight decay is a Python scalar: wd*p is computed in the
+                            param dtype (JAX weak typing); otherwise in f32 */
+#define RF_LR 8u         /* chain ends with scale_by_learning_rate (adamw8) */
+#define RF_MOMENT_SR 16u /* adamw8(stochastic_rounding=True): moment requantization SR */
+#define RF_PARAM_SR 32u  /* apply_updates(stochastic=True) for bf16 params (fused step) */
+#define RF_EXACT 128u    /* IEEE div/sqrt in the update direction (bit-exact params);
+                            default uses hardware rcp/sqrt (params within 1 bf16 ulp) */
+#define RF_FED_BITS 256u /* SR consumes the leaves' *_bits arrays instead of in-kernel
+                            Threefry-2x32 */
+
+/* rf_adam8_leaf.flags */
+#define RF_LEAF_DECAY 1u /* add_decayed_weights applies to this leaf (mask True) */
+
+/* One parameter leaf and its optimizer state. */
+typedef struct rf_adam8_leaf {
+    void* param;        /* [size] param_dtype; read (decay/apply), written by the fused step */
+    const void* grad;   /* [size] grad_dtype */
+    float* updates;     /* [size] f32 output of the update-only (Optax) mode, else NULL */
+    void* mu;           /* quantized: uint8 [nblocks*block_size]; fallback: [size] f32/bf16 */
+    float* mu_scales;   /* quantized: f32 [nblocks]; fallback: NULL */
+    void* nu;           /* as mu (unsigned codebook) */
+    float* nu_scales;
+    const uint32_t* mu_bits;    /* RF_FED_BITS + RF_MOMENT_SR: [nblocks*block_size] raw bits */
+    const uint32_t* nu_bits;
+    const uint32_t* param_bits; /* RF_FED_BITS + RF_PARAM_SR: [size] raw bits */
+    int64_t size;               /* elements of the leaf (QuantizedBlocks.size) */
+    int32_t block_size;         /* QuantizedBlocks.block_size (quantized leaves) */
+    int32_t param_dtype;        /* RF_F32 | RF_BF16 */
+    int32_t grad_dtype;         /* RF_F32 | RF_BF16 */
+    int32_t moment_kind;        /* RF_MOMENT_* */
+    int32_t state_index;        /* position in the flattened moment template: the per-leaf
+                                   moment-SR key is split(key_mu|key_nu)[state_index]
+                                   (adam8.py:644-646) */
+    int32_t param_index;        /* position in the flattened params: the param-SR key is
+                                   split(key_param)[param_index] (utils.py:682) */
+    uint32_t flags;             /* RF_LEAF_* */
+    int32_t reserved;
+} rf_adam8_leaf;
+
+/* Per-step scalars.  The host derives them exactly as the reference does
+ * (adam8.py:322-339, optax add_decayed_weights / scale_by_learning_rate). */
+typedef struct rf_adam8_hparams {
+    float b1, one_minus_b1;  /* f32(b1), f32(1.0 - b1) */
+    float b2, one_minus_b2;
+    float bc1, bc2;          /* 1 - b1**count_inc, 1 - b2**count_inc (f32) */
+    float bc1_next;          /* 1 - b1**(count_inc + 1) (nesterov) */
+    float eps, eps_root;
+    float weight_decay;      /* f32(wd) */
+    float neg_lr;            /* f32(-lr) or -lr(count) of a schedule */
+    uint32_t flags;          /* RF_NESTEROV | RF_DECAY_WEAK | RF_LR | ... */
+    uint32_t key_mu[2];      /* jax.random key data of key_mu (adam8.py:306) */
+    uint32_t key_nu[2];
+    uint32_t key_param[2];   /* apply_updates key (utils.py:682) */
+} rf_adam8_hparams;
+
+typedef struct rf_adam8_plan rf_adam8_plan;
+
+/*
+ * Build a reusable launch plan over a fixed set of leaves: validates them,
+ * uploads the leaf table and its block/chunk work list to device memory
+ * once.  apply != 0: fused step (params written, `updates` unused);
+ * apply == 0: Optax update-only mode (f32 updates written, params read).
+ * Replaces scale_by_adam8.update_fn + adamw8 chain (adam8.py:304-443) and,
+ * fused, rollfast.apply_updates (utils.py:648-708).  Synchronises the
+ * current device once (table upload).
+ */
+rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply,
+                               rf_adam8_plan** out_plan);
+
+/* Enqueue one step of the plan on `stream` (one multi-tensor launch) over
+ * the pointers given at creation. */
+rf_status rf_adam8_plan_run(const rf_adam8_plan* plan, const rf_adam8_hparams* hp, void* stream);
+
+/* Enqueue one step over new buffers of the same structure (sizes, dtypes,
+ * moment kinds, block sizes, key indices and flags must equal the plan's;
+ * only pointers may change -- e.g. fresh gradient buffers each step).  The
+ * pointer table travels through a ring of pinned staging slots guarded by
+ * events: no allocation and no device synchronisation in steady state. */
+rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* leaves, int32_t n_leaves,
+                                   const rf_adam8_hparams* hp, void* stream);
+
+/* Number of kernel launches, leaves and 2048-element work units of a plan. */
+rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64_t* leaves,
+                             int64_t* units);
+
+/* Free a plan (waits for the device to be idle with respect to its tables). */
+rf_status rf_adam8_plan_destroy(rf_adam8_plan* plan);
+
+/* One-shot convenience: create a plan, run it on `stream`, wait for the
+ * stream, destroy the plan.  Allocates and synchronises: use plans in loops. */
+rf_status rf_adam8_step(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply,
+                        const rf_adam8_hparams* hp, void* stream);
+
+/*
+ * adam8.py:113-187 quantize_blocks on a device f32 array of `size` elements:
+ * values [nblocks*block_size] (uint8 codes, or int8 for the symmetric
+ * quantizer; padding included), scales f32 [nblocks].  sr != 0 selects
+ * stochastic rounding with raw bits `bits` [nblocks*block_size] when
+ * non-NULL, else in-kernel Threefry-2x32 bits of key (key0, key1).
+ */
+rf_status rf_blockwise_quantize(int32_t quantizer, const float* x, int64_t size,
+                                int32_t block_size, int32_t sr, uint32_t key0, uint32_t key1,
+                                const uint32_t* bits, void* values, float* scales, void* stream);
+
+/* adam8.py:190-204 dequantize_blocks: out [size] of out_dtype (RF_F32|RF_BF16). */
+rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const float* scales,
+                                  int64_t size, int32_t block_size, int32_t out_dtype, void* out,
+                                  void* stream);
+
+/* utils.py:342-371 _stochastic_round_bf16: out [size] bf16 bit patterns.  Uses
+ * `bits` [size] when non-NULL, else in-kernel Threefry-2x32 bits of key. */
+rf_status rf_sr_bf16(const float* x, int64_t size, uint32_t key0, uint32_t key1,
+                     const uint32_t* bits, uint16_t* out, void* stream);
+
+/* One leaf of rollfast.apply_updates (utils.py:648-708). */
+typedef struct rf_apply_leaf {
+    void* param;             /* [size] param_dtype, updated in place */
+    const float* updates;    /* [size] f32 */
+    const uint32_t* bits;    /* fed SR bits [size] or NULL */
+    int64_t size;
+    int32_t param_dtype;     /* RF_F32 | RF_BF16 */
+    int32_t param_index;     /* key = split(key)[param_index] */
+} rf_apply_leaf;
+
+/* utils.py:648-708 apply_updates over n leaves: bf16 params take
+ * f32(p) + u then SR (stochastic != 0) or RNE; f32 params take p + u. */
+rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic,
+                           uint32_t key0, uint32_t key1, void* stream);
+
+/* Host-side: the 256 f32 values of a dynamic codebook (adam8.py:461-503). */
+rf_status rf_codebook(int32_t quantizer, float* out256);
+
+/* Host-side: codes that the kernels' table lookup assigns to the normalised
+ * values whose f32 bit patterns are first_bits .. first_bits+count-1
+ * (diagnostics of the lookup tables; `out` is host memory). */
+rf_status rf_host_table_codes(int32_t quantizer, uint32_t first_bits, int64_t count, uint8_t* out);
+
+/* Library version string. */
+const char* rf_version(void);
+
+/* Thread-local message of the last failed call ("" if none). */
+const char* rf_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RFADAM8_H */

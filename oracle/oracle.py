@@ -1,0 +1,251 @@
+"""NumPy front end of the CPU oracle (``liborc_adam8.so``).
+
+TEST INFRASTRUCTURE ONLY.  The oracle restates rollfast's adam8 arithmetic
+on the CPU so the HIP library can be checked against it.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import this module; the product package ``rollfast_amd`` never does.
+
+Reference functions restated (paths relative to the rollfast source tree):
+``src/rollfast/optim/adam8.py:113-204`` (quantize/dequantize),
+``:304-443`` (scale_by_adam8 update + adamw8 chain), ``:461-569``
+(codebooks, codebook quantization), ``src/rollfast/utils.py:342-371``
+(bf16 stochastic rounding) and ``:648-708`` (apply_updates).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liborc_adam8.so")
+
+Q_SIGNED, Q_UNSIGNED, Q_SYMMETRIC = 0, 1, 2
+F32, BF16 = 0, 1
+MOM_QUANT, MOM_F32, MOM_BF16 = 0, 1, 2
+NESTEROV, DECAY, DECAY_WEAK, LR, MOMENT_SR, PARAM_SR, APPLY = 1, 2, 4, 8, 16, 32, 64
+
+
+class Hparams(ctypes.Structure):
+    _fields_ = [
+        ("b1", ctypes.c_float),
+        ("one_minus_b1", ctypes.c_float),
+        ("b2", ctypes.c_float),
+        ("one_minus_b2", ctypes.c_float),
+        ("bc1", ctypes.c_float),
+        ("bc2", ctypes.c_float),
+        ("bc1_next", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("eps_root", ctypes.c_float),
+        ("weight_decay", ctypes.c_float),
+        ("neg_lr", ctypes.c_float),
+        ("flags", ctypes.c_int32),
+    ]
+
+
+def build() -> str:
+    """Compile the oracle library in place with its Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        p = ctypes.c_void_p
+        i64 = ctypes.c_int64
+        u32 = ctypes.c_uint32
+        _lib.orc_threefry2x32.argtypes = [u32, u32, u32, u32, ctypes.POINTER(u32), ctypes.POINTER(u32)]
+        _lib.orc_random_bits.argtypes = [u32, u32, ctypes.c_uint64, i64, p]
+        _lib.orc_split.argtypes = [u32, u32, ctypes.c_int32, p]
+        _lib.orc_codebook.argtypes = [ctypes.c_int, p]
+        _lib.orc_quantize.argtypes = [ctypes.c_int, p, i64, i64, ctypes.c_int, p, p, p]
+        _lib.orc_dequantize.argtypes = [ctypes.c_int, p, p, i64, i64, p]
+        _lib.orc_nearest_code.argtypes = [ctypes.c_int, ctypes.c_float]
+        _lib.orc_nearest_code.restype = ctypes.c_int
+        _lib.orc_nearest_codes_bits.argtypes = [ctypes.c_int, u32, i64, p]
+        _lib.orc_nearest_codes_list.argtypes = [ctypes.c_int, p, i64, p]
+        _lib.orc_adam8_leaf.argtypes = [
+            ctypes.POINTER(Hparams), ctypes.c_int, p, ctypes.c_int, p, i64,
+            ctypes.c_int, p, p, p, p, i64, p, p, p, p,
+        ]
+        _lib.orc_apply_updates.argtypes = [ctypes.c_int, p, p, i64, ctypes.c_int, p]
+        _lib.orc_sr_bf16.argtypes = [p, p, i64, p]
+        _lib.orc_f32_to_bf16.argtypes = [p, i64, p]
+        _lib.orc_set_threads.argtypes = [ctypes.c_int]
+        _lib.orc_get_threads.restype = ctypes.c_int
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().orc_get_threads())
+
+
+# ------------------------------------------------------------------ PRNG --
+def threefry2x32(key, counter):
+    y0, y1 = ctypes.c_uint32(), ctypes.c_uint32()
+    lib().orc_threefry2x32(int(key[0]), int(key[1]), int(counter[0]), int(counter[1]),
+                           ctypes.byref(y0), ctypes.byref(y1))
+    return y0.value, y1.value
+
+
+def random_bits(key, n: int, offset: int = 0) -> np.ndarray:
+    out = np.empty(int(n), dtype=np.uint32)
+    lib().orc_random_bits(int(key[0]), int(key[1]), int(offset), int(n), _ptr(out))
+    return out
+
+
+def split(key, num: int) -> np.ndarray:
+    out = np.empty((int(num), 2), dtype=np.uint32)
+    lib().orc_split(int(key[0]), int(key[1]), int(num), _ptr(out))
+    return out
+
+
+# -------------------------------------------------------------- codebook --
+def codebook(signed: bool) -> np.ndarray:
+    out = np.empty(256, dtype=np.float32)
+    lib().orc_codebook(1 if signed else 0, _ptr(out))
+    return out
+
+
+def nearest_code(quantizer: int, n: float) -> int:
+    return int(lib().orc_nearest_code(quantizer, float(np.float32(n))))
+
+
+def nearest_codes_bits(quantizer: int, first_bits: int, count: int) -> np.ndarray:
+    out = np.empty(int(count), dtype=np.uint8)
+    lib().orc_nearest_codes_bits(quantizer, int(first_bits), int(count), _ptr(out))
+    return out
+
+
+def nearest_codes_list(quantizer: int, bits: np.ndarray) -> np.ndarray:
+    bits = np.ascontiguousarray(bits, dtype=np.uint32)
+    out = np.empty(bits.size, dtype=np.uint8)
+    lib().orc_nearest_codes_list(quantizer, _ptr(bits), bits.size, _ptr(out))
+    return out
+
+
+# ------------------------------------------------- quantize / dequantize --
+def nblocks_for(size: int, block_size: int) -> int:
+    return max(1, -(-int(size) // int(block_size)))
+
+
+def quantize(x: np.ndarray, block_size: int, quantizer: int = Q_SIGNED, bits=None):
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    nb = nblocks_for(x.size, block_size)
+    codes = np.empty(nb * block_size, dtype=np.uint8)
+    scales = np.empty(nb, dtype=np.float32)
+    sr = bits is not None
+    if sr:
+        bits = np.ascontiguousarray(bits, dtype=np.uint32).reshape(-1)
+        assert bits.size == nb * block_size
+    lib().orc_quantize(quantizer, _ptr(x), x.size, block_size, 1 if sr else 0,
+                       _ptr(bits), _ptr(codes), _ptr(scales))
+    if quantizer == Q_SYMMETRIC:
+        codes = codes.view(np.int8)
+    return codes.reshape(nb, block_size), scales
+
+
+def dequantize(codes: np.ndarray, scales: np.ndarray, size: int, block_size: int,
+               quantizer: int = Q_SIGNED) -> np.ndarray:
+    codes = np.ascontiguousarray(codes).reshape(-1).view(np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    out = np.empty(int(size), dtype=np.float32)
+    lib().orc_dequantize(quantizer, _ptr(codes), _ptr(scales), int(size), int(block_size), _ptr(out))
+    return out
+
+
+# ------------------------------------------------------------- bf16 ------
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size, dtype=np.uint16)
+    lib().orc_f32_to_bf16(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def sr_bf16(x: np.ndarray, bits: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    bits = np.ascontiguousarray(bits, dtype=np.uint32).reshape(-1)
+    out = np.empty(x.size, dtype=np.uint16)
+    lib().orc_sr_bf16(_ptr(x), _ptr(bits), x.size, _ptr(out))
+    return out
+
+
+# -------------------------------------------------------------- the step --
+def make_hparams(*, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0, weight_decay=0.0, lr=None,
+                 count=1, nesterov=False, decay=False, decay_weak=True, moment_sr=False,
+                 param_sr=False, apply=False) -> Hparams:
+    """Scalars exactly as the reference derives them from Python floats:
+    ``1.0 - b1`` in double then f32 (adam8.py:323), ``1 - b1**t`` in f32
+    (adam8.py:338-339, f32 pow: parity unpinned)."""
+    f32 = np.float32
+    t = f32(count)
+    hp = Hparams()
+    hp.b1 = f32(b1)
+    hp.one_minus_b1 = f32(1.0 - b1)
+    hp.b2 = f32(b2)
+    hp.one_minus_b2 = f32(1.0 - b2)
+    hp.bc1 = f32(1.0) - np.power(f32(b1), t)
+    hp.bc2 = f32(1.0) - np.power(f32(b2), t)
+    hp.bc1_next = f32(1.0) - np.power(f32(b1), f32(count + 1))
+    hp.eps = f32(eps)
+    hp.eps_root = f32(eps_root)
+    hp.weight_decay = f32(weight_decay)
+    hp.neg_lr = f32(-lr) if lr is not None else f32(0.0)
+    flags = 0
+    if nesterov:
+        flags |= NESTEROV
+    if decay:
+        flags |= DECAY
+        if decay_weak:
+            flags |= DECAY_WEAK
+    if lr is not None:
+        flags |= LR
+    if moment_sr:
+        flags |= MOMENT_SR
+    if param_sr:
+        flags |= PARAM_SR
+    if apply:
+        flags |= APPLY
+    hp.flags = flags
+    return hp
+
+
+def adam8_leaf(hp: Hparams, param: np.ndarray, pdtype: int, grad: np.ndarray, gdtype: int,
+               mkind: int, mu, mu_scales, nu, nu_scales, block_size: int = 2048,
+               mu_bits=None, nu_bits=None, p_bits=None, updates_out=None) -> None:
+    """Run one leaf of one step in place on NumPy buffers.
+
+    ``param``/``grad`` hold f32 values or bf16 bit patterns (uint16).
+    """
+    n = grad.size
+    lib().orc_adam8_leaf(ctypes.byref(hp), pdtype, _ptr(param), gdtype, _ptr(grad), n, mkind,
+                         _ptr(mu), _ptr(mu_scales), _ptr(nu), _ptr(nu_scales), int(block_size),
+                         _ptr(mu_bits), _ptr(nu_bits), _ptr(p_bits), _ptr(updates_out))
+
+
+def apply_updates(param: np.ndarray, pdtype: int, upd: np.ndarray, bits=None) -> None:
+    upd = np.ascontiguousarray(upd, dtype=np.float32).reshape(-1)
+    lib().orc_apply_updates(pdtype, _ptr(param), _ptr(upd), upd.size, 1 if bits is not None else 0,
+                            _ptr(bits))

@@ -1,0 +1,61 @@
+"""rollfast_amd: rollfast's 8-bit AdamW step on MI355X (gfx950) HIP kernels.
+
+Drop-in for the reference's adam8 hot path (rollfast ``adamw8``,
+``scale_by_adam8``, ``quantize_blocks``, ``dequantize_blocks``,
+``apply_updates``): same names, arguments, state pytree and errors, with
+torch tensors on a ROCm device in place of jax arrays.  ``adamw8_step`` fuses
+``tx.update`` and ``apply_updates`` into one HBM pass.
+"""
+
+from . import prng
+from ._base import (
+    EmptyState,
+    GradientTransformation,
+    GradientTransformationExtraArgs,
+    MaskedNode,
+    MaskedState,
+    ScaleByScheduleState,
+)
+from .optim.adam8 import (
+    DYNAMIC_SIGNED_CODEBOOK_ID,
+    DYNAMIC_UNSIGNED_CODEBOOK_ID,
+    SYMMETRIC_INT8_CODEBOOK_ID,
+    QuantizedBlocks,
+    ScaleByAdam8State,
+    adamw8,
+    adamw8_step,
+    dequantize_blocks,
+    estimate_quantized_moment_bytes,
+    quantize_blocks,
+    quantized_nbytes,
+    scale_by_adam8,
+    tree_state_nbytes,
+)
+from .utils import apply_updates, apply_updates_prefix
+
+__version__ = "0.1.0"
+
+__all__ = (
+    "DYNAMIC_SIGNED_CODEBOOK_ID",
+    "DYNAMIC_UNSIGNED_CODEBOOK_ID",
+    "SYMMETRIC_INT8_CODEBOOK_ID",
+    "EmptyState",
+    "GradientTransformation",
+    "GradientTransformationExtraArgs",
+    "MaskedNode",
+    "MaskedState",
+    "QuantizedBlocks",
+    "ScaleByAdam8State",
+    "ScaleByScheduleState",
+    "adamw8",
+    "adamw8_step",
+    "apply_updates",
+    "apply_updates_prefix",
+    "dequantize_blocks",
+    "estimate_quantized_moment_bytes",
+    "prng",
+    "quantize_blocks",
+    "quantized_nbytes",
+    "scale_by_adam8",
+    "tree_state_nbytes",
+)

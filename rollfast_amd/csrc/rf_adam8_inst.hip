@@ -1,0 +1,25 @@
+// rf_adam8_inst.hip -- instantiates k_adam8 for one (APPLY, MSR, EXACT)
+// combination, selected by -DRFI_APPLY / -DRFI_MSR / -DRFI_EXACT.  The build
+// compiles this file once per combination, in parallel, and links all of
+// them into one library; rf_host.hip picks the instance per call.
+#include "rf_device.h"
+
+#if !defined(RFI_APPLY) || !defined(RFI_MSR) || !defined(RFI_EXACT)
+#error "build with -DRFI_APPLY=0|1 -DRFI_MSR=0|1 -DRFI_EXACT=0|1"
+#endif
+
+#define RF_PICK_NAME2(a, m, e) rf_pick_adam8_a##a##_m##m##_e##e
+#define RF_PICK_NAME(a, m, e) RF_PICK_NAME2(a, m, e)
+
+namespace rf {
+
+adam_kernel_t RF_PICK_NAME(RFI_APPLY, RFI_MSR, RFI_EXACT)(bool psr, bool nest)
+{
+    constexpr bool A = RFI_APPLY != 0, M = RFI_MSR != 0, E = RFI_EXACT != 0;
+    if constexpr (A) {
+        if (psr) return nest ? &k_adam8<A, M, true, true, E> : &k_adam8<A, M, true, false, E>;
+    }
+    return nest ? &k_adam8<A, M, false, true, E> : &k_adam8<A, M, false, false, E>;
+}
+
+}  // namespace rf

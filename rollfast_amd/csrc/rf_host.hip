@@ -1,0 +1,916 @@
+// rf_host.hip -- host side of librfadam8.so: lookup-table construction,
+// per-device state, launch plans, the standalone quantize / dequantize / SR /
+// apply kernels, and the C ABI declared in include/rfadam8.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "rf_device.h"
+
+using namespace rf;
+
+#define RF_VERSION "rfadam8 0.1.0 gfx950"
+
+// ------------------------------------------------------------------ errors --
+namespace {
+thread_local std::string g_err;
+
+rf_status fail(rf_status code, const std::string& msg)
+{
+    g_err = msg;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                    \
+    do {                                                                                 \
+        hipError_t e_ = (expr);                                                          \
+        if (e_ != hipSuccess)                                                            \
+            return fail(RF_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+}  // namespace
+
+// Instances of the step kernel (rf_adam8_inst.hip, one object per variant).
+namespace rf {
+adam_kernel_t rf_pick_adam8_a0_m0_e0(bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a0_m0_e1(bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a0_m1_e0(bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a0_m1_e1(bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a1_m0_e0(bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a1_m0_e1(bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a1_m1_e0(bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a1_m1_e1(bool psr, bool nest);
+}  // namespace rf
+
+// ====================================================== standalone kernels ==
+// Standalone quantize_blocks (adam8.py:113-187): one wave per block.  Fast
+// path: 2048-element aligned blocks held in registers; otherwise two passes.
+__global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const float* __restrict__ x, int64_t size,
+                                                 int64_t bs, int64_t nblocks, int32_t sr, uint32_t k0,
+                                                 uint32_t k1, const uint32_t* __restrict__ bits,
+                                                 uint8_t* __restrict__ values, float* __restrict__ scales,
+                                                 const uint4* __restrict__ tables, int32_t vec_ok)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
+    stage_tables(lds, tables);
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    const float* cb = (const float*)(lds + (quantizer == RF_Q_DYNAMIC_UNSIGNED ? L_CBU : L_CBS));
+    for (int64_t b = wave; b < nblocks; b += nwaves) {
+        const int64_t base = b * bs;
+        const int64_t nvalid = max((int64_t)0, min(bs, size - base));
+        const bool full = vec_ok && bs == FAST_BS && nvalid == bs;
+        float xr[32];
+        uint32_t am = 0;
+        if (full) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float t8[8];
+                load8<float>(x, base + j * 512 + lane * 8, t8);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    xr[j * 8 + t] = t8[t];
+                    am = max(am, __float_as_uint(t8[t]) & 0x7FFFFFFFu);
+                }
+            }
+        } else {
+            for (int64_t j = lane; j < nvalid; j += WAVE) am = max(am, __float_as_uint(x[base + j]) & 0x7FFFFFFFu);
+        }
+        am = wave_max_u32(am);
+        const float amax = __uint_as_float(am);
+        float scale;
+        if (quantizer == RF_Q_SYMMETRIC_INT8) scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        else scale = amax > 0.0f ? amax : 1.0f;
+        if (lane == 0) scales[b] = scale;
+        const bool fast = !sr && quantizer != RF_Q_SYMMETRIC_INT8 && scale_is_fast(scale);
+        const float rs = 1.0f / scale;
+        auto code_of = [&](float xv, int64_t e) -> uint32_t {
+            if (quantizer == RF_Q_SYMMETRIC_INT8) {
+                // adam8.py:143-164 and _round_scaled :446-458
+                float s = xv / scale;
+                s = s < -127.0f ? -127.0f : (s > 127.0f ? 127.0f : s);
+                float r;
+                if (sr) {
+                    const uint32_t w = bits ? bits[e] : jax_bits(k0, k1, (uint64_t)e);
+                    const float lo = floorf(s);
+                    r = lo + (uniform_from_bits(w) < (s - lo) ? 1.0f : 0.0f);
+                } else {
+                    r = rintf(s);
+                }
+                return (uint32_t)(uint8_t)(int8_t)(r == r ? (int)r : 0);
+            }
+            if (fast) {
+                if (quantizer == RF_Q_DYNAMIC_SIGNED) return code_signed_fast(lds, xv, scale, rs);
+                return code_unsigned_fast(lds, xv > 0.0f ? xv : 0.0f, scale, rs);
+            }
+            uint32_t w = 0;
+            if (sr) w = bits ? bits[e] : jax_bits(k0, k1, (uint64_t)e);
+            return code_literal(cb, xv, scale, sr != 0, w);
+        };
+        if (full) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t e0 = base + j * 512 + lane * 8;
+                uint32_t cc[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) cc[t] = code_of(xr[j * 8 + t], e0 + t);
+                uint2 w;
+                w.x = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
+                w.y = cc[4] | (cc[5] << 8) | (cc[6] << 16) | (cc[7] << 24);
+                *(uint2*)(values + e0) = w;
+            }
+        } else {
+            for (int64_t j = lane; j < bs; j += WAVE) {
+                const int64_t e = base + j;
+                const float xv = j < nvalid ? x[e] : 0.0f;
+                values[e] = (uint8_t)code_of(xv, e);
+            }
+        }
+    }
+}
+
+// Standalone dequantize_blocks (adam8.py:190-204).
+__global__ __launch_bounds__(WG) void k_dequantize(int32_t quantizer, const uint8_t* __restrict__ values,
+                                                   const float* __restrict__ scales, int64_t size, int64_t bs,
+                                                   int32_t out_dtype, void* __restrict__ out,
+                                                   const uint4* __restrict__ tables, int32_t vec_ok)
+{
+    __shared__ __attribute__((aligned(16))) float cb[256];
+    const uint32_t off = quantizer == RF_Q_DYNAMIC_UNSIGNED ? L_CBU : L_CBS;
+    for (int i = threadIdx.x; i < 64; i += WG) ((uint4*)cb)[i] = tables[off / 16 + i];
+    __syncthreads();
+    const int64_t tid = (int64_t)blockIdx.x * WG + threadIdx.x;
+    const int64_t nthreads = (int64_t)gridDim.x * WG;
+    const bool sym = quantizer == RF_Q_SYMMETRIC_INT8;
+    const int64_t ngroups = vec_ok ? size / 8 : 0;
+    for (int64_t gi = tid; gi < ngroups; gi += nthreads) {
+        const int64_t e0 = gi * 8;
+        const uint2 w = *(const uint2*)(values + e0);
+        const float s = scales[e0 / bs];  // bs % 8 == 0: the 8 elements share a block
+        float o[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t cbyte = ((t < 4 ? w.x : w.y) >> (8 * (t & 3))) & 0xFFu;
+            const float val = sym ? (float)(int8_t)cbyte : cb[cbyte];
+            o[t] = val * s;
+        }
+        if (out_dtype == RF_BF16) {
+            uint32_t hb[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) hb[t] = f32_to_bf16_rne(o[t]);
+            store8_bf16(out, e0, hb);
+        } else {
+            store8_f32(out, e0, o);
+        }
+    }
+    for (int64_t e = ngroups * 8 + tid; e < size; e += nthreads) {
+        const uint32_t cbyte = values[e];
+        const float val = sym ? (float)(int8_t)cbyte : cb[cbyte];
+        store1(out, out_dtype, e, val * scales[e / bs]);
+    }
+}
+
+// Standalone _stochastic_round_bf16 (utils.py:342-371).
+__global__ __launch_bounds__(WG) void k_sr_bf16(const float* __restrict__ x, int64_t size, uint32_t k0,
+                                                uint32_t k1, const uint32_t* __restrict__ bits,
+                                                uint16_t* __restrict__ out, int32_t vec_ok)
+{
+    const int64_t tid = (int64_t)blockIdx.x * WG + threadIdx.x;
+    const int64_t nthreads = (int64_t)gridDim.x * WG;
+    const int64_t ngroups = vec_ok ? size / 8 : 0;
+    for (int64_t gi = tid; gi < ngroups; gi += nthreads) {
+        const int64_t e0 = gi * 8;
+        float xv[8];
+        load8<float>(x, e0, xv);
+        uint32_t rb[8];
+        if (bits) load8_u32(bits, e0, rb);
+        else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) rb[t] = jax_bits(k0, k1, (uint64_t)(e0 + t));
+        }
+        uint32_t hb[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) hb[t] = sr_bf16(xv[t], rb[t]);
+        store8_bf16(out, e0, hb);
+    }
+    for (int64_t e = ngroups * 8 + tid; e < size; e += nthreads) {
+        const uint32_t w = bits ? bits[e] : jax_bits(k0, k1, (uint64_t)e);
+        out[e] = (uint16_t)sr_bf16(x[e], w);
+    }
+}
+
+// apply_updates over a leaf table (utils.py:648-708): one workgroup-stride
+// loop per leaf (blockIdx.y = leaf).
+__global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ leaves, int32_t stochastic,
+                                              uint32_t k0, uint32_t k1)
+{
+    const rf_apply_leaf L = leaves[blockIdx.y];
+    uint32_t lk0 = 0, lk1 = 0;
+    if (stochastic) jax_split(k0, k1, (uint32_t)L.param_index, lk0, lk1);
+    const int64_t tid = (int64_t)blockIdx.x * WG + threadIdx.x;
+    const int64_t nthreads = (int64_t)gridDim.x * WG;
+    for (int64_t e = tid; e < L.size; e += nthreads) {
+        const float u = L.updates[e];
+        if (L.param_dtype == RF_BF16) {
+            const float s = bf16_bits_to_f32(((const uint16_t*)L.param)[e]) + u;
+            uint32_t r;
+            if (stochastic) r = sr_bf16(s, L.bits ? L.bits[e] : jax_bits(lk0, lk1, (uint64_t)e));
+            else r = f32_to_bf16_rne(s);
+            ((uint16_t*)L.param)[e] = (uint16_t)r;
+        } else {
+            ((float*)L.param)[e] = ((const float*)L.param)[e] + u;
+        }
+    }
+}
+
+// =================================================================== host ==
+namespace {
+
+// ---- codebooks and lookup tables (rollfast optim/adam8.py:461-503) ----
+void build_codebook(bool is_signed, float out[256])
+{
+    std::vector<double> data;
+    const int total_bits = 8, max_exponent_bits = 7;
+    const int non_sign_bits = total_bits - 1;
+    for (int index = 0; index < max_exponent_bits; ++index) {
+        const int e = -(max_exponent_bits - 1) + index;
+        const double exponent_scale = e == 0 ? 1.0 : std::pow(10.0, (double)e);
+        const int items = is_signed ? (1 << (index + non_sign_bits - max_exponent_bits)) + 1
+                                    : (1 << (index + non_sign_bits - max_exponent_bits + 1)) + 1;
+        const double step = (1.0 - 0.1) / (double)(items - 1);
+        for (int i = 0; i + 1 < items; ++i) {
+            volatile double left = 0.1 + step * (double)i;
+            volatile double right = 0.1 + step * (double)(i + 1);
+            const double mean = (left + right) / 2.0;
+            data.push_back(exponent_scale * mean);
+            if (is_signed) data.push_back(-exponent_scale * mean);
+        }
+    }
+    data.push_back(0.0);
+    data.push_back(1.0);
+    std::sort(data.begin(), data.end());
+    for (int i = 0; i < 256; ++i) out[i] = (float)data[i];
+}
+
+inline uint32_t fbits(float f)
+{
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+}
+inline float bitsf(uint32_t u)
+{
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+// Monotone key of an f32 (value order, -0 before +0).
+inline uint32_t fkey(float f)
+{
+    const uint32_t u = fbits(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+inline float unkey(uint32_t k) { return bitsf((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k); }
+
+// The reference's choice between neighbours lo < hi for lo < n <= hi.
+inline bool picks_upper(float lo, float hi, volatile float n)
+{
+    volatile float du = hi - n;
+    volatile float dl = n - lo;
+    return std::fabs((float)du) < std::fabs((float)dl);
+}
+
+// Smallest f32 n in (lo, hi] for which the upper neighbour wins.
+float upper_threshold(float lo, float hi)
+{
+    uint32_t a = fkey(lo) + 1u, b = fkey(hi);
+    while (a < b) {
+        const uint32_t mid = a + (b - a) / 2u;
+        if (picks_upper(lo, hi, unkey(mid))) b = mid;
+        else a = mid + 1u;
+    }
+    return unkey(a);
+}
+
+inline uint32_t count_le(const float* t, int n, float a)
+{
+    uint32_t c = 0;
+    for (int i = 0; i < n; ++i) c += (t[i] <= a) ? 1u : 0u;
+    return c;
+}
+
+struct HostTables {
+    std::vector<uint8_t> bytes;
+    std::string error;
+};
+
+bool fill_cells(const float* thr, int nthr, uint8_t* cand, std::string& err)
+{
+    for (uint32_t cell = CELL_LO; cell <= CELL_HI; ++cell) {
+        const float lo = bitsf(cell << CELL_SHIFT);
+        const float hi = bitsf((cell << CELL_SHIFT) | ((1u << CELL_SHIFT) - 1u));
+        const uint32_t c0 = count_le(thr, nthr, lo);
+        const uint32_t c1 = count_le(thr, nthr, hi);
+        if (c1 > c0 + 1u || (cell == CELL_LO && c0 != 0u)) {
+            err = "lookup cell " + std::to_string(cell) + " holds more than one threshold";
+            return false;
+        }
+        // The kernel compares a >= T[cand]; the threshold inside the cell (if
+        // any) is T[c0] because T is ascending and T[c0] > lo.
+        if (c0 < (uint32_t)nthr && thr[c0] <= lo) {
+            err = "threshold table is not ascending";
+            return false;
+        }
+        cand[cell - CELL_LO] = (uint8_t)c0;
+    }
+    return true;
+}
+
+HostTables build_tables()
+{
+    HostTables ht;
+    ht.bytes.assign(TABLE_BYTES, 0);
+    uint8_t* b = ht.bytes.data();
+    float cbs[256], cbu[256];
+    build_codebook(true, cbs);
+    build_codebook(false, cbu);
+    std::memcpy(b + L_CBS, cbs, 1024);
+    std::memcpy(b + L_CBU, cbu, 1024);
+    for (int i = 0; i < 255; ++i) {
+        if (!(cbs[i] < cbs[i + 1]) || !(cbu[i] < cbu[i + 1])) {
+            ht.error = "codebook is not strictly increasing";
+            return ht;
+        }
+    }
+    const float inf = INFINITY;
+    // Unsigned: thresholds t_0..t_254 between cbu[i] and cbu[i+1].
+    float tu[256];
+    for (int i = 0; i < 255; ++i) tu[i] = upper_threshold(cbu[i], cbu[i + 1]);
+    tu[255] = inf;
+    // Signed, n >= 0: pairs (cbs[127+k], cbs[128+k]), k = 0..127.
+    float tp[256];
+    for (int k = 0; k < 128; ++k) tp[k] = upper_threshold(cbs[127 + k], cbs[128 + k]);
+    for (int k = 128; k < 256; ++k) tp[k] = inf;
+    // Signed, n < 0: pair i = 126-k is (cbs[i], cbs[i+1]); in magnitude the
+    // larger code wins for a > |t_i|, i.e. a >= nextafter(|t_i|, inf).
+    float tn[256];
+    for (int k = 0; k < 127; ++k) {
+        const float t = upper_threshold(cbs[126 - k], cbs[127 - k]);
+        tn[k] = std::nextafter(std::fabs(t), inf);
+    }
+    for (int k = 127; k < 256; ++k) tn[k] = inf;
+    std::memcpy(b + L_TU, tu, 1024);
+    std::memcpy(b + L_POS + REG_T, tp, 1024);
+    std::memcpy(b + L_NEG + REG_T, tn, 1024);
+    if (!fill_cells(tu, 255, b + L_CANDU, ht.error)) return ht;
+    if (!fill_cells(tp, 128, b + L_POS + REG_CAND, ht.error)) return ht;
+    if (!fill_cells(tn, 127, b + L_NEG + REG_CAND, ht.error)) return ht;
+    return ht;
+}
+
+const HostTables& host_tables()
+{
+    static HostTables t = build_tables();
+    return t;
+}
+
+// Host emulation of code_signed_fast / code_unsigned_fast on a normalised n.
+uint32_t host_table_code(const uint8_t* tb, int32_t quantizer, float n)
+{
+    const float* cb = (const float*)(tb + (quantizer == RF_Q_DYNAMIC_UNSIGNED ? L_CBU : L_CBS));
+    if (n != n) return 254u;
+    n = n < cb[0] ? cb[0] : n;
+    n = n > cb[255] ? cb[255] : n;
+    const uint32_t nb = fbits(n);
+    if (quantizer == RF_Q_DYNAMIC_UNSIGNED) {
+        const uint32_t mag = nb & 0x7FFFFFFFu;
+        const uint32_t cell = std::max(mag >> CELL_SHIFT, CELL_LO);
+        const uint32_t cand = tb[L_CANDU - CELL_LO + cell];
+        float t;
+        std::memcpy(&t, tb + L_TU + cand * 4u, 4);
+        return cand + (bitsf(mag) >= t ? 1u : 0u);
+    }
+    const uint32_t neg = (nb & 0x80000000u) ? 0xFFFFFFFFu : 0u;
+    const uint32_t sd = neg & REGION;
+    const uint32_t cell = std::max((nb >> CELL_SHIFT) & 0xFFFFu, CELL_LO);
+    const uint32_t cand = tb[L_POS + REG_CAND - CELL_LO + sd + cell];
+    float t;
+    std::memcpy(&t, tb + L_POS + REG_T + sd + cand * 4u, 4);
+    const uint32_t c = cand + (std::fabs(n) >= t ? 1u : 0u);
+    return ((c ^ neg) + 127u - neg) & 0xFFu;
+}
+
+// ---- per-device state ----
+constexpr int MAX_DEV = 64;
+struct DevState {
+    bool ready = false;
+    uint4* tables = nullptr;
+    int num_cus = 0;
+};
+std::mutex g_mu;
+DevState g_dev[MAX_DEV];
+
+rf_status device_state(DevState** out)
+{
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= MAX_DEV) return fail(RF_ERR_INVALID, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_mu);
+    DevState& d = g_dev[dev];
+    if (!d.ready) {
+        const HostTables& ht = host_tables();
+        if (!ht.error.empty()) return fail(RF_ERR_INVALID, "table construction failed: " + ht.error);
+        HIP_TRY(hipDeviceGetAttribute(&d.num_cus, hipDeviceAttributeMultiprocessorCount, dev));
+        HIP_TRY(hipMalloc(&d.tables, TABLE_BYTES));
+        HIP_TRY(hipMemcpy(d.tables, ht.bytes.data(), TABLE_BYTES, hipMemcpyHostToDevice));
+        d.ready = true;
+    }
+    *out = &d;
+    return RF_OK;
+}
+
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+// ---- kernel selection ----
+adam_kernel_t pick_adam_kernel(bool apply, bool msr, bool psr, bool nest, bool exact)
+{
+    if (apply) {
+        if (msr) return exact ? rf_pick_adam8_a1_m1_e1(psr, nest) : rf_pick_adam8_a1_m1_e0(psr, nest);
+        return exact ? rf_pick_adam8_a1_m0_e1(psr, nest) : rf_pick_adam8_a1_m0_e0(psr, nest);
+    }
+    if (msr) return exact ? rf_pick_adam8_a0_m1_e1(false, nest) : rf_pick_adam8_a0_m1_e0(false, nest);
+    return exact ? rf_pick_adam8_a0_m0_e1(false, nest) : rf_pick_adam8_a0_m0_e0(false, nest);
+}
+
+struct OccKey {
+    const void* fn;
+    int dev;
+    int blocks;
+};
+std::vector<OccKey> g_occ;
+
+rf_status occupancy(const void* fn, int* blocks)
+{
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        for (const OccKey& k : g_occ)
+            if (k.fn == fn && k.dev == dev) {
+                *blocks = k.blocks;
+                return RF_OK;
+            }
+    }
+    int nb = 0;
+    HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, WG, 0));
+    if (nb < 1) nb = 1;
+    std::lock_guard<std::mutex> lock(g_mu);
+    g_occ.push_back({fn, dev, nb});
+    *blocks = nb;
+    return RF_OK;
+}
+
+int64_t nblocks_of(int64_t size, int64_t bs) { return size > 0 ? (size + bs - 1) / bs : 1; }
+
+}  // namespace
+
+// ---- plan ----
+// Pointer tables for rf_adam8_plan_run_leaves: each run writes the leaf table
+// into a pinned host slot and copies it to the slot's device table on the
+// stream; the slot's event guards reuse, so a run never waits for the device
+// unless RING runs are still in flight.
+constexpr int RING = 4;
+struct RingSlot {
+    rf_adam8_leaf* host = nullptr;
+    rf_adam8_leaf* dev = nullptr;
+    hipEvent_t ev = nullptr;
+    bool pending = false;
+};
+
+struct rf_adam8_plan {
+    int device = 0;
+    int32_t apply = 1;
+    int32_t n_leaves = 0;
+    int64_t total_units = 0;
+    int64_t n_segs = 0;
+    rf_adam8_leaf* d_leaves = nullptr;  // creation-time pointer table
+    Seg* d_segs = nullptr;
+    std::vector<rf_adam8_leaf> shape;   // creation-time table: the structure runs must match
+    std::vector<uint8_t> vec;           // leaf has vectorised (16-byte aligned) work units
+    bool any_param_bits = false, any_moment_bits = false;
+    RingSlot ring[RING];
+    uint32_t next = 0;
+    std::mutex mu;
+};
+
+namespace {
+
+rf_status validate_leaf(const rf_adam8_leaf& L, int32_t i, int32_t apply)
+{
+    const std::string at = "leaf " + std::to_string(i) + ": ";
+    if (L.size < 0) return fail(RF_ERR_INVALID, at + "negative size");
+    if (L.param_dtype != RF_F32 && L.param_dtype != RF_BF16) return fail(RF_ERR_UNSUPPORTED, at + "param dtype must be f32 or bf16");
+    if (L.grad_dtype != RF_F32 && L.grad_dtype != RF_BF16) return fail(RF_ERR_UNSUPPORTED, at + "grad dtype must be f32 or bf16");
+    if (L.moment_kind < RF_MOMENT_QUANTIZED || L.moment_kind > RF_MOMENT_BF16) return fail(RF_ERR_INVALID, at + "bad moment kind");
+    if (L.size > 0 && !L.grad) return fail(RF_ERR_INVALID, at + "null grad");
+    if (L.size > 0 && !L.param && (apply || (L.flags & RF_LEAF_DECAY))) return fail(RF_ERR_INVALID, at + "null param");
+    if (L.size > 0 && !apply && !L.updates) return fail(RF_ERR_INVALID, at + "null updates in update-only mode");
+    if (!L.mu || !L.nu) return fail(RF_ERR_INVALID, at + "null moment buffer");
+    if (L.moment_kind == RF_MOMENT_QUANTIZED) {
+        if (L.block_size <= 0) return fail(RF_ERR_INVALID, at + "block_size must be positive");
+        if (!L.mu_scales || !L.nu_scales) return fail(RF_ERR_INVALID, at + "null scales");
+    }
+    if (L.state_index < 0 || L.param_index < 0) return fail(RF_ERR_INVALID, at + "negative key index");
+    return RF_OK;
+}
+
+bool leaf_vec_ok(const rf_adam8_leaf& L, int32_t apply)
+{
+    const uintptr_t a = 16;
+    if (!aligned(L.grad, a)) return false;
+    if ((apply || (L.flags & RF_LEAF_DECAY)) && !aligned(L.param, a)) return false;
+    if (!apply && !aligned(L.updates, a)) return false;
+    if (L.moment_kind == RF_MOMENT_QUANTIZED) {
+        if (!aligned(L.mu, 8) || !aligned(L.nu, 8)) return false;
+        if (L.mu_bits && !aligned(L.mu_bits, a)) return false;
+        if (L.nu_bits && !aligned(L.nu_bits, a)) return false;
+    } else if (!aligned(L.mu, a) || !aligned(L.nu, a)) {
+        return false;
+    }
+    if (L.param_bits && !aligned(L.param_bits, a)) return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rf_version(void) { return RF_VERSION; }
+
+const char* rf_last_error(void) { return g_err.c_str(); }
+
+rf_status rf_codebook(int32_t quantizer, float* out256)
+{
+    if (!out256) return fail(RF_ERR_INVALID, "null output");
+    if (quantizer != RF_Q_DYNAMIC_SIGNED && quantizer != RF_Q_DYNAMIC_UNSIGNED)
+        return fail(RF_ERR_INVALID, "symmetric_int8 does not use a lookup codebook");
+    build_codebook(quantizer == RF_Q_DYNAMIC_SIGNED, out256);
+    return RF_OK;
+}
+
+rf_status rf_host_table_codes(int32_t quantizer, uint32_t first_bits, int64_t count, uint8_t* out)
+{
+    if (!out || count < 0) return fail(RF_ERR_INVALID, "bad arguments");
+    if (quantizer != RF_Q_DYNAMIC_SIGNED && quantizer != RF_Q_DYNAMIC_UNSIGNED)
+        return fail(RF_ERR_INVALID, "quantizer must be dynamic signed or unsigned");
+    const HostTables& ht = host_tables();
+    if (!ht.error.empty()) return fail(RF_ERR_INVALID, ht.error);
+    for (int64_t i = 0; i < count; ++i)
+        out[i] = (uint8_t)host_table_code(ht.bytes.data(), quantizer, bitsf(first_bits + (uint32_t)i));
+    return RF_OK;
+}
+
+rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply, rf_adam8_plan** out_plan)
+{
+    if (!out_plan) return fail(RF_ERR_INVALID, "null plan output");
+    *out_plan = nullptr;
+    if (n_leaves < 0 || (n_leaves > 0 && !leaves)) return fail(RF_ERR_INVALID, "bad leaf table");
+    DevState* ds = nullptr;
+    rf_status st = device_state(&ds);
+    if (st != RF_OK) return st;
+    std::vector<Seg> segs;
+    int64_t units = 0;
+    auto add = [&](int32_t leaf, int32_t kind, int64_t first, int64_t count) {
+        if (count <= 0) return;
+        Seg s{};
+        s.unit_start = units;
+        s.first = first;
+        s.leaf = leaf;
+        s.kind = kind;
+        segs.push_back(s);
+        units += count;
+    };
+    bool any_pb = false, any_mb = false;
+    std::vector<uint8_t> vecs;
+    for (int32_t i = 0; i < n_leaves; ++i) {
+        const rf_adam8_leaf& L = leaves[i];
+        st = validate_leaf(L, i, apply);
+        if (st != RF_OK) return st;
+        any_pb |= L.param_bits != nullptr;
+        any_mb |= (L.mu_bits != nullptr) || (L.nu_bits != nullptr);
+        const bool vec = leaf_vec_ok(L, apply);
+        vecs.push_back(vec ? 1 : 0);
+        if (L.moment_kind == RF_MOMENT_QUANTIZED) {
+            const int64_t bs = L.block_size;
+            const int64_t nb = nblocks_of(L.size, bs);
+            if (bs == FAST_BS && vec) {
+                const int64_t nfull = L.size / bs;
+                add(i, KIND_QFAST, 0, nfull);
+                add(i, KIND_QGEN, nfull, nb - nfull);
+            } else {
+                add(i, KIND_QGEN, 0, nb);
+            }
+        } else {
+            add(i, KIND_FALLBACK, 0, (L.size + CHUNK - 1) / CHUNK);
+        }
+    }
+    Seg sentinel{};
+    sentinel.unit_start = units;
+    sentinel.leaf = -1;
+    sentinel.kind = -1;
+    segs.push_back(sentinel);
+
+    rf_adam8_plan* p = new rf_adam8_plan();
+    HIP_TRY(hipGetDevice(&p->device));
+    p->apply = apply ? 1 : 0;
+    p->n_leaves = n_leaves;
+    p->total_units = units;
+    p->n_segs = (int64_t)segs.size() - 1;
+    p->any_param_bits = any_pb;
+    p->any_moment_bits = any_mb;
+    p->shape.assign(leaves, leaves + n_leaves);
+    p->vec = vecs;
+    hipError_t e1 = hipMalloc(&p->d_leaves, sizeof(rf_adam8_leaf) * (size_t)std::max(n_leaves, 1));
+    hipError_t e2 = hipMalloc(&p->d_segs, sizeof(Seg) * segs.size());
+    if (e1 != hipSuccess || e2 != hipSuccess) {
+        if (p->d_leaves) (void)hipFree(p->d_leaves);
+        if (p->d_segs) (void)hipFree(p->d_segs);
+        delete p;
+        return fail(RF_ERR_HIP, "hipMalloc of the plan tables failed");
+    }
+    if (n_leaves > 0)
+        HIP_TRY(hipMemcpy(p->d_leaves, leaves, sizeof(rf_adam8_leaf) * (size_t)n_leaves, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(p->d_segs, segs.data(), sizeof(Seg) * segs.size(), hipMemcpyHostToDevice));
+    *out_plan = p;
+    return RF_OK;
+}
+
+rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64_t* leaves, int64_t* units)
+{
+    if (!plan) return fail(RF_ERR_INVALID, "null plan");
+    if (launches) *launches = plan->total_units > 0 ? 1 : 0;
+    if (leaves) *leaves = plan->n_leaves;
+    if (units) *units = plan->total_units;
+    return RF_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, bool any_pb, bool any_mb,
+                      const rf_adam8_hparams* hp, void* stream)
+{
+    if (plan->total_units == 0) return RF_OK;
+    const uint32_t f = hp->flags;
+    const bool msr = (f & RF_MOMENT_SR) != 0;
+    const bool psr = (f & RF_PARAM_SR) != 0 && plan->apply;
+    if ((f & RF_FED_BITS) && ((psr && !any_pb) || (msr && !any_mb)))
+        return fail(RF_ERR_INVALID, "RF_FED_BITS set but the leaves carry no random bits");
+    DevState* ds = nullptr;
+    rf_status st = device_state(&ds);
+    if (st != RF_OK) return st;
+
+    KHp k{};
+    k.b1 = hp->b1;
+    k.omb1 = hp->one_minus_b1;
+    k.b2 = hp->b2;
+    k.omb2 = hp->one_minus_b2;
+    k.bc1 = hp->bc1;
+    k.bc2 = hp->bc2;
+    k.bc1n = hp->bc1_next;
+    k.rbc1 = 1.0f / hp->bc1;
+    k.rbc2 = 1.0f / hp->bc2;
+    k.rbc1n = 1.0f / hp->bc1_next;
+    k.eps = hp->eps;
+    k.eps_root = hp->eps_root;
+    k.wd = hp->weight_decay;
+    {
+        // bf16(wd), round to nearest even (JAX weak typing of a Python scalar).
+        uint32_t u = fbits(hp->weight_decay);
+        if (std::isnan(hp->weight_decay)) u = (u & 0x80000000u) | 0x7FC00000u;
+        else u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+        k.wd16 = bitsf(u);
+    }
+    k.neg_lr = (f & RF_LR) ? hp->neg_lr : 1.0f;
+    k.flags = f;
+    k.kmu0 = hp->key_mu[0];
+    k.kmu1 = hp->key_mu[1];
+    k.knu0 = hp->key_nu[0];
+    k.knu1 = hp->key_nu[1];
+    k.kp0 = hp->key_param[0];
+    k.kp1 = hp->key_param[1];
+
+    adam_kernel_t fn = pick_adam_kernel(plan->apply != 0, msr, psr, (f & RF_NESTEROV) != 0, (f & RF_EXACT) != 0);
+    int occ = 1;
+    st = occupancy((const void*)fn, &occ);
+    if (st != RF_OK) return st;
+    const int64_t wg_needed = (plan->total_units + WAVES_PER_WG - 1) / WAVES_PER_WG;
+    const int64_t wg_resident = (int64_t)ds->num_cus * occ;
+    const int grid = (int)std::max<int64_t>(1, std::min(wg_needed, wg_resident));
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(WG), 0, (hipStream_t)stream, d_leaves, plan->d_segs,
+                       plan->total_units, k, ds->tables);
+    HIP_TRY(hipGetLastError());
+    return RF_OK;
+}
+
+bool same_structure(const rf_adam8_leaf& a, const rf_adam8_leaf& b)
+{
+    return a.size == b.size && a.block_size == b.block_size && a.param_dtype == b.param_dtype &&
+           a.grad_dtype == b.grad_dtype && a.moment_kind == b.moment_kind && a.state_index == b.state_index &&
+           a.param_index == b.param_index && a.flags == b.flags;
+}
+
+}  // namespace
+
+extern "C" {
+
+rf_status rf_adam8_plan_run(const rf_adam8_plan* plan, const rf_adam8_hparams* hp, void* stream)
+{
+    if (!plan || !hp) return fail(RF_ERR_INVALID, "null plan or hparams");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev != plan->device) return fail(RF_ERR_INVALID, "plan was created on another device");
+    return plan_launch(plan, plan->d_leaves, plan->any_param_bits, plan->any_moment_bits, hp, stream);
+}
+
+rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* leaves, int32_t n_leaves,
+                                   const rf_adam8_hparams* hp, void* stream)
+{
+    if (!plan || !hp) return fail(RF_ERR_INVALID, "null plan or hparams");
+    if (n_leaves != plan->n_leaves || (n_leaves > 0 && !leaves))
+        return fail(RF_ERR_INVALID, "leaf table does not match the plan");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev != plan->device) return fail(RF_ERR_INVALID, "plan was created on another device");
+    bool any_pb = false, any_mb = false;
+    for (int32_t i = 0; i < n_leaves; ++i) {
+        const rf_adam8_leaf& L = leaves[i];
+        if (!same_structure(L, plan->shape[i]))
+            return fail(RF_ERR_INVALID, "leaf " + std::to_string(i) + " differs in structure from the plan");
+        rf_status st = validate_leaf(L, i, plan->apply);
+        if (st != RF_OK) return st;
+        if (plan->vec[i] && !leaf_vec_ok(L, plan->apply))
+            return fail(RF_ERR_INVALID, "leaf " + std::to_string(i) + " lost the 16-byte alignment the plan relies on");
+        any_pb |= L.param_bits != nullptr;
+        any_mb |= (L.mu_bits != nullptr) || (L.nu_bits != nullptr);
+    }
+    if (plan->total_units == 0) return RF_OK;
+    std::lock_guard<std::mutex> lock(plan->mu);
+    RingSlot& slot = plan->ring[plan->next % RING];
+    plan->next++;
+    const size_t bytes = sizeof(rf_adam8_leaf) * (size_t)n_leaves;
+    if (!slot.host) {
+        HIP_TRY(hipHostMalloc((void**)&slot.host, bytes, hipHostMallocDefault));
+        HIP_TRY(hipMalloc((void**)&slot.dev, bytes));
+        HIP_TRY(hipEventCreateWithFlags(&slot.ev, hipEventDisableTiming));
+    }
+    if (slot.pending) HIP_TRY(hipEventSynchronize(slot.ev));
+    std::memcpy(slot.host, leaves, bytes);
+    HIP_TRY(hipMemcpyAsync(slot.dev, slot.host, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+    rf_status st = plan_launch(plan, slot.dev, any_pb, any_mb, hp, stream);
+    HIP_TRY(hipEventRecord(slot.ev, (hipStream_t)stream));
+    slot.pending = true;
+    return st;
+}
+
+rf_status rf_adam8_plan_destroy(rf_adam8_plan* plan)
+{
+    if (!plan) return RF_OK;
+    int cur = 0;
+    HIP_TRY(hipGetDevice(&cur));
+    if (cur != plan->device) HIP_TRY(hipSetDevice(plan->device));
+    hipError_t e1 = hipFree(plan->d_leaves);
+    hipError_t e2 = hipFree(plan->d_segs);
+    for (RingSlot& slot : plan->ring) {
+        if (slot.ev) {
+            (void)hipEventSynchronize(slot.ev);
+            (void)hipEventDestroy(slot.ev);
+        }
+        if (slot.dev) (void)hipFree(slot.dev);
+        if (slot.host) (void)hipHostFree(slot.host);
+    }
+    if (cur != plan->device) (void)hipSetDevice(cur);
+    delete plan;
+    if (e1 != hipSuccess || e2 != hipSuccess) return fail(RF_ERR_HIP, "hipFree of the plan tables failed");
+    return RF_OK;
+}
+
+rf_status rf_adam8_step(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply, const rf_adam8_hparams* hp,
+                        void* stream)
+{
+    rf_adam8_plan* plan = nullptr;
+    rf_status st = rf_adam8_plan_create(leaves, n_leaves, apply, &plan);
+    if (st != RF_OK) return st;
+    st = rf_adam8_plan_run(plan, hp, stream);
+    if (st == RF_OK) {
+        hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+        if (e != hipSuccess) st = fail(RF_ERR_HIP, std::string("hipStreamSynchronize: ") + hipGetErrorString(e));
+    }
+    rf_status st2 = rf_adam8_plan_destroy(plan);
+    return st != RF_OK ? st : st2;
+}
+
+rf_status rf_blockwise_quantize(int32_t quantizer, const float* x, int64_t size, int32_t block_size, int32_t sr,
+                                uint32_t key0, uint32_t key1, const uint32_t* bits, void* values, float* scales,
+                                void* stream)
+{
+    if (quantizer < RF_Q_DYNAMIC_SIGNED || quantizer > RF_Q_SYMMETRIC_INT8) return fail(RF_ERR_INVALID, "unknown quantizer");
+    if (block_size <= 0) return fail(RF_ERR_INVALID, "block_size must be positive.");
+    if (size < 0) return fail(RF_ERR_INVALID, "negative size");
+    if ((size > 0 && !x) || !values || !scales) return fail(RF_ERR_INVALID, "null buffer");
+    DevState* ds = nullptr;
+    rf_status st = device_state(&ds);
+    if (st != RF_OK) return st;
+    const int64_t nb = nblocks_of(size, block_size);
+    int occ = 1;
+    st = occupancy((const void*)&k_quantize, &occ);
+    if (st != RF_OK) return st;
+    const int64_t wg_needed = (nb + WAVES_PER_WG - 1) / WAVES_PER_WG;
+    const int grid = (int)std::max<int64_t>(1, std::min(wg_needed, (int64_t)ds->num_cus * occ));
+    const int32_t vec_ok = aligned(x, 16) && aligned(values, 8) && (!bits || aligned(bits, 16));
+    hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(WG), 0, (hipStream_t)stream, quantizer, x, size,
+                       (int64_t)block_size, nb, sr, key0, key1, bits, (uint8_t*)values, scales, ds->tables, vec_ok);
+    HIP_TRY(hipGetLastError());
+    return RF_OK;
+}
+
+rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const float* scales, int64_t size,
+                                  int32_t block_size, int32_t out_dtype, void* out, void* stream)
+{
+    if (quantizer < RF_Q_DYNAMIC_SIGNED || quantizer > RF_Q_SYMMETRIC_INT8) return fail(RF_ERR_INVALID, "unknown quantizer");
+    if (block_size <= 0) return fail(RF_ERR_INVALID, "block_size must be positive.");
+    if (out_dtype != RF_F32 && out_dtype != RF_BF16) return fail(RF_ERR_UNSUPPORTED, "out dtype must be f32 or bf16");
+    if (size < 0) return fail(RF_ERR_INVALID, "negative size");
+    if (size == 0) return RF_OK;
+    if (!values || !scales || !out) return fail(RF_ERR_INVALID, "null buffer");
+    DevState* ds = nullptr;
+    rf_status st = device_state(&ds);
+    if (st != RF_OK) return st;
+    const int32_t vec_ok = (block_size % 8 == 0) && aligned(values, 8) && aligned(out, 16);
+    const int64_t work = vec_ok ? (size + 7) / 8 : size;
+    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>((work + WG - 1) / WG, (int64_t)ds->num_cus * 8));
+    hipLaunchKernelGGL(k_dequantize, dim3(grid), dim3(WG), 0, (hipStream_t)stream, quantizer,
+                       (const uint8_t*)values, scales, size, (int64_t)block_size, out_dtype, out, ds->tables, vec_ok);
+    HIP_TRY(hipGetLastError());
+    return RF_OK;
+}
+
+rf_status rf_sr_bf16(const float* x, int64_t size, uint32_t key0, uint32_t key1, const uint32_t* bits, uint16_t* out,
+                     void* stream)
+{
+    if (size < 0) return fail(RF_ERR_INVALID, "negative size");
+    if (size == 0) return RF_OK;
+    if (!x || !out) return fail(RF_ERR_INVALID, "null buffer");
+    DevState* ds = nullptr;
+    rf_status st = device_state(&ds);
+    if (st != RF_OK) return st;
+    const int32_t vec_ok = aligned(x, 16) && aligned(out, 16) && (!bits || aligned(bits, 16));
+    const int64_t work = vec_ok ? (size + 7) / 8 : size;
+    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>((work + WG - 1) / WG, (int64_t)ds->num_cus * 8));
+    hipLaunchKernelGGL(k_sr_bf16, dim3(grid), dim3(WG), 0, (hipStream_t)stream, x, size, key0, key1, bits, out,
+                       vec_ok);
+    HIP_TRY(hipGetLastError());
+    return RF_OK;
+}
+
+rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic, uint32_t key0,
+                           uint32_t key1, void* stream)
+{
+    if (n_leaves < 0 || (n_leaves > 0 && !leaves)) return fail(RF_ERR_INVALID, "bad leaf table");
+    if (n_leaves == 0) return RF_OK;
+    int64_t maxsize = 0;
+    for (int32_t i = 0; i < n_leaves; ++i) {
+        const rf_apply_leaf& L = leaves[i];
+        if (L.size < 0) return fail(RF_ERR_INVALID, "negative size");
+        if (L.param_dtype != RF_F32 && L.param_dtype != RF_BF16)
+            return fail(RF_ERR_UNSUPPORTED, "param dtype must be f32 or bf16");
+        if (L.size > 0 && (!L.param || !L.updates)) return fail(RF_ERR_INVALID, "null buffer");
+        if (L.param_index < 0) return fail(RF_ERR_INVALID, "negative key index");
+        maxsize = std::max(maxsize, L.size);
+    }
+    if (maxsize == 0) return RF_OK;
+    if (n_leaves > 65535) return fail(RF_ERR_UNSUPPORTED, "more than 65535 leaves in one apply call");
+    DevState* ds = nullptr;
+    rf_status st = device_state(&ds);
+    if (st != RF_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    rf_apply_leaf* d = nullptr;
+    HIP_TRY(hipMallocAsync((void**)&d, sizeof(rf_apply_leaf) * (size_t)n_leaves, s));
+    HIP_TRY(hipMemcpyAsync(d, leaves, sizeof(rf_apply_leaf) * (size_t)n_leaves, hipMemcpyHostToDevice, s));
+    const int gx = (int)std::max<int64_t>(1, std::min<int64_t>((maxsize + WG - 1) / WG, (int64_t)ds->num_cus * 4));
+    hipLaunchKernelGGL(k_apply, dim3(gx, n_leaves), dim3(WG), 0, s, d, stochastic, key0, key1);
+    hipError_t le = hipGetLastError();
+    HIP_TRY(hipFreeAsync(d, s));
+    if (le != hipSuccess) return fail(RF_ERR_HIP, std::string("k_apply launch: ") + hipGetErrorString(le));
+    return RF_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,64 @@
+// rf_tables.h -- codebooks and requantization lookup tables shared by the
+// gfx950 kernels (device side) and their host-side builder.
+//
+// Requantization identity.  For a dynamic codebook cb[0..255] (strictly
+// increasing) the reference picks, for a normalised value n in
+// [cb[0], cb[255]], ui = searchsorted_left(cb, n), li = ui - 1 (clipped) and
+// the upper code iff fl(|cb[ui] - n|) < fl(|n - cb[li]|)
+// (rollfast optim/adam8.py:542-569).  Inside each interval (cb[i], cb[i+1]]
+// that choice is monotone in n, so there is a smallest f32 t_i from which the
+// upper code wins, and code(n) = #{ i : n >= t_i }.  The kernels therefore
+// count thresholds instead of searching the codebook:
+//
+//   magnitude a = |n|; cell = bits(a) >> 15 (exponent + 8 mantissa bits)
+//   cand = CAND[cell]        (thresholds strictly below the cell start)
+//   count = cand + (a >= T[cand])
+//
+// The cells are narrow enough (relative width <= 2^-8, while consecutive
+// thresholds are >= 0.53 % apart) that each holds at most one threshold; the
+// builder checks this and refuses to produce tables otherwise.  The signed
+// codebook uses separate positive-side and negative-side tables because
+// exact ties go to the lower index, which is the smaller magnitude for n > 0
+// and the larger magnitude for n < 0.
+//
+// Byte layout (identical in global memory and in LDS):
+//   [L_CBS]   f32 cb_signed[256]
+//   [L_CBU]   f32 cb_unsigned[256]
+//   [L_TU]    f32 unsigned thresholds[256]        (+inf padded)
+//   [L_POS]   f32 signed n>=0 thresholds[256]     (+inf padded)
+//             u8  signed n>=0 candidates[NCELL_PAD]
+//   [L_NEG]   same for n<0 (L_NEG = L_POS + REGION)
+//   [L_CANDU] u8  unsigned candidates[NCELL_PAD]
+#pragma once
+#include <stdint.h>
+
+namespace rf {
+
+constexpr uint32_t CELL_SHIFT = 15;
+constexpr uint32_t CELL_LO = 0x6800;   // bits(2^-23) >> 15: every threshold lies above
+constexpr uint32_t CELL_HI = 0x7F00;   // bits(1.0f) >> 15
+constexpr uint32_t NCELL = CELL_HI - CELL_LO + 1;
+constexpr uint32_t NCELL_PAD = (NCELL + 15u) & ~15u;
+
+constexpr uint32_t L_CBS = 0;
+constexpr uint32_t L_CBU = 1024;
+constexpr uint32_t L_TU = 2048;
+constexpr uint32_t L_POS = 3072;
+constexpr uint32_t REG_T = 0;
+constexpr uint32_t REG_CAND = 1024;
+constexpr uint32_t REGION = 1024 + NCELL_PAD;
+constexpr uint32_t L_NEG = L_POS + REGION;
+constexpr uint32_t L_CANDU = L_NEG + REGION;
+constexpr uint32_t TABLE_BYTES = L_CANDU + NCELL_PAD;
+static_assert(TABLE_BYTES % 16 == 0, "tables are copied in 16-byte words");
+static_assert(REGION % 16 == 0, "regions stay 16-byte aligned");
+
+// Fast requantization is exact when the block scale s satisfies
+// FAST_SCALE_MIN <= s < inf: the reciprocal-and-correct division
+// q0 = x*rcp(s), r = fma(-s, q0, x), q = fma(r, rcp(s), q0) then equals the
+// IEEE quotient for every |q| >= 2^-25, and all smaller quotients map to the
+// zero code either way.  Other blocks (tiny, zero-free but subnormal-range,
+// Inf or NaN scales) take the literal search path.
+constexpr float FAST_SCALE_MIN = 0x1p-70f;
+
+}  // namespace rf

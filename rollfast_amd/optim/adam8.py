@@ -1,0 +1,863 @@
+"""AdamW with blockwise 8-bit optimizer-state moments, on MI355X HIP kernels.
+
+Host-side mirror of ``src/rollfast/optim/adam8.py`` (rollfast): the same
+public names, argument meanings, state pytree and errors.  Arrays are
+``torch`` tensors on a ROCm device (torch is used for device memory and
+streams only); every computation on them runs in ``librfadam8.so``:
+
+* ``quantize_blocks`` / ``dequantize_blocks`` -> ``rf_blockwise_quantize`` /
+  ``rf_blockwise_dequantize`` (reference ``adam8.py:113-204``);
+* ``scale_by_adam8().update`` and ``adamw8().update`` -> one multi-tensor
+  launch of the fused step kernel in update-only mode (reference
+  ``adam8.py:304-389`` and the ``optax.chain`` of ``:418-443``);
+* ``adamw8_step`` (new, no reference counterpart) -> the same kernel with the
+  parameter write of ``rollfast.apply_updates`` fused in: one HBM pass.
+
+Updates are in place (JAX donation semantics): the returned state shares its
+tensors with the input state.  The step counter and PRNG key are host NumPy
+scalars/arrays, so deriving the bias correction and the per-leaf keys never
+waits on the device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import math
+from typing import Any, Callable, Literal, NamedTuple, Optional, Union
+
+import numpy as np
+
+from .. import _lib, _tree, prng
+from .._base import (
+    NO_PARAMS_MSG,
+    EmptyState,
+    GradientTransformation,
+    GradientTransformationExtraArgs,
+    MaskedNode,
+    MaskedState,
+    ScaleByScheduleState,
+    is_passthrough_leaf as _is_passthrough_leaf,
+    safe_int32_increment,
+)
+
+SYMMETRIC_INT8_CODEBOOK_ID = "rollfast.symmetric_int8.neg127_pos127.v1"
+DYNAMIC_SIGNED_CODEBOOK_ID = "bitsandbytes.dynamic.signed.8bit.v1"
+DYNAMIC_UNSIGNED_CODEBOOK_ID = "bitsandbytes.dynamic.unsigned.8bit.v1"
+BlockLayout = Literal["shard_local", "logical_global"]
+CodebookQuantizer = Literal["dynamic_signed", "dynamic_unsigned", "symmetric_int8"]
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+# ------------------------------------------------------------- dtypes ------
+def canonicalize_dtype(dtype):
+    """Accept torch dtypes, NumPy dtypes or names ("float32", "bfloat16")."""
+    torch = _torch()
+    if isinstance(dtype, torch.dtype):
+        return dtype
+    name = getattr(dtype, "name", None) or getattr(dtype, "__name__", None) or str(dtype)
+    name = name.replace("torch.", "").replace("jnp.", "")
+    table = {
+        "float32": torch.float32,
+        "bfloat16": torch.bfloat16,
+        "float16": torch.float16,
+        "float64": torch.float64,
+        "uint8": torch.uint8,
+        "int8": torch.int8,
+        "int32": torch.int32,
+    }
+    if name not in table:
+        raise ValueError(f"unknown dtype {dtype!r}")
+    return table[name]
+
+
+def dtype_name(dtype) -> str:
+    """NumPy-style dtype name ("float32", "uint8", "bfloat16")."""
+    return str(dtype).replace("torch.", "")
+
+
+def _is_inexact(dtype) -> bool:
+    return dtype.is_floating_point or dtype.is_complex
+
+
+def _rf_dtype(dtype, what: str) -> int:
+    torch = _torch()
+    if dtype == torch.float32:
+        return _lib.RF_F32
+    if dtype == torch.bfloat16:
+        return _lib.RF_BF16
+    raise NotImplementedError(f"{what} dtype {dtype} is not supported (float32 or bfloat16)")
+
+
+# ------------------------------------------------------ QuantizedBlocks ----
+@dataclasses.dataclass(frozen=True, eq=False)
+class QuantizedBlocks:
+    """Blockwise fixed-codebook 8-bit representation for one state leaf
+    (adam8.py:28-101): ``values`` [nblocks, block_size] codes (uint8, or int8
+    for the symmetric quantizer, padding included) and ``scales`` [nblocks]."""
+
+    values: Any
+    scales: Any
+    shape: tuple
+    size: int
+    block_size: int
+    quantizer: str = "blockwise_dynamic_signed_8bit"
+    codebook_id: str = DYNAMIC_SIGNED_CODEBOOK_ID
+    qmin: int = 0
+    qmax: int = 255
+    zero_point: int = 0
+    block_layout: BlockLayout = "shard_local"
+
+    def tree_flatten(self):
+        return (self.values, self.scales), (
+            self.shape,
+            self.size,
+            self.block_size,
+            self.quantizer,
+            self.codebook_id,
+            self.qmin,
+            self.qmax,
+            self.zero_point,
+            self.block_layout,
+        )
+
+    @classmethod
+    def tree_unflatten(cls, aux_data, children):
+        shape, size, block_size, quantizer, codebook_id, qmin, qmax, zero_point, block_layout = aux_data
+        values, scales = children
+        return cls(
+            values=values,
+            scales=scales,
+            shape=shape,
+            size=size,
+            block_size=block_size,
+            quantizer=quantizer,
+            codebook_id=codebook_id,
+            qmin=qmin,
+            qmax=qmax,
+            zero_point=zero_point,
+            block_layout=block_layout,
+        )
+
+    def metadata(self) -> dict[str, Any]:
+        """Exact checkpoint metadata for this quantized state leaf."""
+        return {
+            "quantizer": self.quantizer,
+            "codebook_id": self.codebook_id,
+            "qmin": self.qmin,
+            "qmax": self.qmax,
+            "zero_point": self.zero_point,
+            "shape": self.shape,
+            "size": self.size,
+            "block_size": self.block_size,
+            "block_layout": self.block_layout,
+            "scale_dtype": dtype_name(self.scales.dtype),
+            "values_dtype": dtype_name(self.values.dtype),
+        }
+
+
+_tree.register_node(QuantizedBlocks, lambda q: q.tree_flatten(), QuantizedBlocks.tree_unflatten)
+
+
+class ScaleByAdam8State(NamedTuple):
+    """State for Adam with quantized first and second moments (adam8.py:104-110)."""
+
+    count: Any
+    mu: Any
+    nu: Any
+    key: Any
+
+
+def _is_state_leaf(x: Any) -> bool:
+    return isinstance(x, QuantizedBlocks) or _is_passthrough_leaf(x)
+
+
+_QUANTIZER_CODE = {
+    "dynamic_signed": _lib.RF_Q_DYNAMIC_SIGNED,
+    "dynamic_unsigned": _lib.RF_Q_DYNAMIC_UNSIGNED,
+    "symmetric_int8": _lib.RF_Q_SYMMETRIC_INT8,
+}
+
+
+def _codebook_id_for_quantizer(quantizer: str) -> str:
+    if quantizer == "dynamic_signed":
+        return DYNAMIC_SIGNED_CODEBOOK_ID
+    if quantizer == "dynamic_unsigned":
+        return DYNAMIC_UNSIGNED_CODEBOOK_ID
+    if quantizer == "symmetric_int8":
+        return SYMMETRIC_INT8_CODEBOOK_ID
+    raise ValueError(f"Unknown quantizer: {quantizer!r}.")
+
+
+def _zero_code_for_quantizer(quantizer: str) -> int:
+    """adam8.py:532-539: index of the codebook entry nearest zero."""
+    if quantizer == "dynamic_signed":
+        return 127
+    return 0
+
+
+def _quantizer_from_codebook_id(codebook_id: str) -> str:
+    if codebook_id == DYNAMIC_SIGNED_CODEBOOK_ID:
+        return "dynamic_signed"
+    if codebook_id == DYNAMIC_UNSIGNED_CODEBOOK_ID:
+        return "dynamic_unsigned"
+    if codebook_id == SYMMETRIC_INT8_CODEBOOK_ID:
+        return "symmetric_int8"
+    raise ValueError(f"Unknown codebook_id: {codebook_id!r}.")
+
+
+def _require_device_tensor(x, what: str):
+    torch = _torch()
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{what} must be a torch.Tensor on a ROCm device, got {type(x)}")
+    if not x.is_cuda:
+        raise ValueError(f"{what} must live on a ROCm device (got {x.device})")
+    return x
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _device_ctx(t):
+    return _torch().cuda.device(t.device)
+
+
+# ------------------------------------------------ quantize / dequantize ----
+def quantize_blocks(
+    x,
+    *,
+    block_size: int = 2048,
+    scale_dtype=None,
+    stochastic_rounding: bool = False,
+    key=None,
+    block_layout: BlockLayout = "shard_local",
+    quantizer: CodebookQuantizer = "dynamic_signed",
+    random_bits=None,
+) -> QuantizedBlocks:
+    """Quantize one array with fixed-codebook blockwise dynamic scales
+    (adam8.py:113-187).  ``random_bits`` (extension): raw ``uint32`` words
+    [nblocks*block_size] consumed by stochastic rounding instead of bits
+    generated from ``key`` in the kernel."""
+    torch = _torch()
+    if block_size <= 0:
+        raise ValueError("block_size must be positive.")
+    if block_layout not in {"shard_local", "logical_global"}:
+        raise ValueError("block_layout must be 'shard_local' or 'logical_global'.")
+    if quantizer not in {"dynamic_signed", "dynamic_unsigned", "symmetric_int8"}:
+        raise ValueError(
+            "quantizer must be 'dynamic_signed', 'dynamic_unsigned', or "
+            "'symmetric_int8'."
+        )
+    scale_dtype = torch.float32 if scale_dtype is None else canonicalize_dtype(scale_dtype)
+    if scale_dtype != torch.float32:
+        raise NotImplementedError("only float32 block scales are implemented (scale_dtype=float32)")
+    if stochastic_rounding and key is None and random_bits is None:
+        raise ValueError("stochastic rounding requires a PRNG key.")
+    _require_device_tensor(x, "x")
+    x_f32 = x.to(torch.float32).contiguous()
+    shape = tuple(x.shape)
+    size = int(x.numel())
+    blocks_count = max(1, math.ceil(size / block_size))
+    vdtype = torch.int8 if quantizer == "symmetric_int8" else torch.uint8
+    values = torch.empty((blocks_count, block_size), dtype=vdtype, device=x.device)
+    scales = torch.empty((blocks_count,), dtype=torch.float32, device=x.device)
+    k = prng.as_key(key) if key is not None else np.zeros(2, np.uint32)
+    bits = None
+    if random_bits is not None:
+        bits = _require_device_tensor(random_bits, "random_bits").contiguous()
+        if bits.dtype != torch.uint32 or bits.numel() != blocks_count * block_size:
+            raise ValueError("random_bits must be uint32 [nblocks * block_size]")
+    with _device_ctx(x):
+        _lib.check(
+            _lib.lib().rf_blockwise_quantize(
+                _QUANTIZER_CODE[quantizer], _ptr(x_f32), size, int(block_size),
+                1 if stochastic_rounding else 0, int(k[0]), int(k[1]), _ptr(bits),
+                values.data_ptr(), scales.data_ptr(), _lib.stream_ptr(),
+            ),
+            "quantize_blocks",
+        )
+    if quantizer == "symmetric_int8":
+        return QuantizedBlocks(
+            values=values, scales=scales, shape=shape, size=size, block_size=block_size,
+            quantizer="blockwise_symmetric_int8", codebook_id=SYMMETRIC_INT8_CODEBOOK_ID,
+            qmin=-127, qmax=127, zero_point=0, block_layout=block_layout,
+        )
+    return QuantizedBlocks(
+        values=values, scales=scales, shape=shape, size=size, block_size=block_size,
+        quantizer=f"blockwise_{quantizer}_8bit", codebook_id=_codebook_id_for_quantizer(quantizer),
+        qmin=0, qmax=255, zero_point=_zero_code_for_quantizer(quantizer), block_layout=block_layout,
+    )
+
+
+def dequantize_blocks(blocks: QuantizedBlocks, *, dtype=None):
+    """Dequantize a ``QuantizedBlocks`` leaf and remove deterministic padding
+    (adam8.py:190-204)."""
+    torch = _torch()
+    dtype = torch.float32 if dtype is None else canonicalize_dtype(dtype)
+    quantizer = _quantizer_from_codebook_id(blocks.codebook_id)
+    values = _require_device_tensor(blocks.values, "values").contiguous()
+    scales = blocks.scales
+    if scales.dtype != torch.float32:
+        raise NotImplementedError("only float32 block scales are implemented")
+    out_dtype = dtype if dtype in (torch.float32, torch.bfloat16) else torch.float32
+    out = torch.empty((blocks.size,), dtype=out_dtype, device=values.device)
+    with _device_ctx(values):
+        _lib.check(
+            _lib.lib().rf_blockwise_dequantize(
+                _QUANTIZER_CODE[quantizer], values.data_ptr(), scales.contiguous().data_ptr(), int(blocks.size),
+                int(blocks.block_size), _rf_dtype(out_dtype, "output"), out.data_ptr(), _lib.stream_ptr(),
+            ),
+            "dequantize_blocks",
+        )
+    out = out.reshape(blocks.shape)
+    return out if out_dtype == dtype else out.to(dtype)
+
+
+# ------------------------------------------------------ byte accounting ----
+def quantized_nbytes(blocks: QuantizedBlocks) -> int:
+    """Materialized array bytes used by one quantized state leaf (adam8.py:207-212)."""
+    return int(blocks.values.numel() * blocks.values.element_size()) + int(
+        blocks.scales.numel() * blocks.scales.element_size()
+    )
+
+
+def _leaf_nbytes(leaf) -> int:
+    if hasattr(leaf, "element_size") and hasattr(leaf, "numel"):
+        return int(leaf.numel() * leaf.element_size())
+    if hasattr(leaf, "dtype") and hasattr(leaf, "size") and hasattr(leaf, "itemsize"):
+        return int(leaf.size * leaf.itemsize)
+    return 0
+
+
+def tree_state_nbytes(tree: Any) -> int:
+    """Array storage bytes in an optimizer-state pytree (adam8.py:215-224)."""
+    total = 0
+    for leaf in _tree.leaves(tree, is_leaf=_is_state_leaf):
+        if isinstance(leaf, QuantizedBlocks):
+            total += quantized_nbytes(leaf)
+        else:
+            total += _leaf_nbytes(leaf)
+    return total
+
+
+def estimate_quantized_moment_bytes(size: int, *, block_size: int = 2048, scale_dtype=None) -> int:
+    """Bytes for one quantized moment leaf with ``size`` elements (adam8.py:227-240)."""
+    torch = _torch()
+    scale_dtype = torch.float32 if scale_dtype is None else canonicalize_dtype(scale_dtype)
+    if size <= 0:
+        return 0
+    blocks_count = max(1, math.ceil(size / block_size))
+    itemsize = torch.tensor([], dtype=scale_dtype).element_size()
+    return int(blocks_count * block_size) + int(blocks_count * itemsize)
+
+
+# ----------------------------------------------------- state construction --
+@dataclasses.dataclass(frozen=True)
+class _Config:
+    b1: Any
+    b2: Any
+    eps: Any
+    eps_root: Any
+    block_size: int
+    min_size: int
+    scale_dtype: Any
+    fallback_dtype: Any
+    stochastic_rounding: bool
+    block_layout: str
+    quantize: bool
+    nesterov: bool
+    key: Any
+    exact: bool
+
+
+def _init_moment_leaf(param, cfg: _Config, quantizer: str):
+    """adam8.py:605-630: zeros of fallback_dtype, quantized when eligible."""
+    torch = _torch()
+    if _is_passthrough_leaf(param):
+        return param
+    zeros_dtype = cfg.fallback_dtype
+    if cfg.quantize and param.numel() >= cfg.min_size and _is_inexact(param.dtype):
+        size = int(param.numel())
+        blocks_count = max(1, math.ceil(size / cfg.block_size))
+        # quantize_blocks(zeros): every block has absmax 0 -> scale 1.0 and
+        # every code is the codebook's zero code.
+        return QuantizedBlocks(
+            values=torch.full((blocks_count, cfg.block_size), _zero_code_for_quantizer(quantizer),
+                              dtype=torch.uint8, device=param.device),
+            scales=torch.ones((blocks_count,), dtype=torch.float32, device=param.device),
+            shape=tuple(param.shape),
+            size=size,
+            block_size=cfg.block_size,
+            quantizer=f"blockwise_{quantizer}_8bit",
+            codebook_id=_codebook_id_for_quantizer(quantizer),
+            qmin=0,
+            qmax=255,
+            zero_point=_zero_code_for_quantizer(quantizer),
+            block_layout=cfg.block_layout,
+        )
+    return torch.zeros(param.shape, dtype=zeros_dtype, device=param.device)
+
+
+def _init_moment_tree(params, cfg: _Config, quantizer: str):
+    return _tree.tree_map(lambda p: _init_moment_leaf(p, cfg, quantizer), params, is_leaf=_is_passthrough_leaf)
+
+
+def _as_f32(x) -> np.float32:
+    if hasattr(x, "detach"):
+        x = x.detach().cpu().item()
+    return np.float32(x)
+
+
+def _one_minus(b) -> np.float32:
+    """``1.0 - b`` as the reference evaluates it: in double for a Python
+    scalar (then f32 when it meets the f32 arrays), in f32 for an array."""
+    if isinstance(b, (int, float)):
+        return np.float32(1.0 - b)
+    return np.float32(1.0) - _as_f32(b)
+
+
+def _bias_correction(b, count: int) -> np.float32:
+    """``1.0 - b**count`` in f32 (adam8.py:338-339; f32 pow)."""
+    with np.errstate(all="ignore"):
+        return np.float32(1.0) - np.power(_as_f32(b), np.float32(count))
+
+
+# ------------------------------------------------------------ the engine ---
+class _LeafPlan:
+    """A cached ``rf_adam8_plan`` for one leaf-table structure."""
+
+    def __init__(self, table, n: int, apply: bool):
+        handle = ctypes.c_void_p()
+        _lib.check(_lib.lib().rf_adam8_plan_create(table, n, 1 if apply else 0, ctypes.byref(handle)),
+                   "rf_adam8_plan_create")
+        self.handle = handle
+        self.n = n
+
+    def run(self, table, hp, stream):
+        _lib.check(_lib.lib().rf_adam8_plan_run_leaves(self.handle, table, self.n, ctypes.byref(hp), stream),
+                   "rf_adam8_plan_run_leaves")
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value:
+            try:
+                _lib.lib().rf_adam8_plan_destroy(h)
+            except Exception:
+                pass
+            self.handle = None
+
+
+def _aligned(t, a: int) -> bool:
+    return t is None or t.data_ptr() % a == 0
+
+
+class _Engine:
+    """Builds the leaf table for a step and launches it (one launch per tree)."""
+
+    def __init__(self, cfg: _Config):
+        self.cfg = cfg
+        self._plans: dict = {}
+
+    def run(
+        self,
+        updates,
+        state: ScaleByAdam8State,
+        params,
+        *,
+        apply: bool,
+        decay_mask: Optional[list],
+        weight_decay,
+        neg_lr: Optional[np.float32],
+        param_key=None,
+        param_sr: bool = False,
+        random_bits: Optional[dict] = None,
+    ):
+        torch = _torch()
+        cfg = self.cfg
+        key_mu, key_nu, next_key = prng.split(state.key, 3)
+        count_inc = safe_int32_increment(int(np.asarray(state.count)))
+
+        g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
+        mu_leaves = _tree.flatten_up_to(g_td, state.mu) if g_td.num_leaves else []
+        nu_leaves = _tree.flatten_up_to(g_td, state.nu) if g_td.num_leaves else []
+        mu_state_leaves = _tree.leaves(state.mu, is_leaf=_is_state_leaf)
+        if len(mu_state_leaves) != len(g_leaves):
+            raise ValueError("updates and optimizer state have different tree structures")
+        p_leaves = None
+        if params is not None:
+            p_leaves = _tree.flatten_up_to(g_td, params)
+
+        n = len(g_leaves)
+        out_leaves: list = [None] * n
+        table_rows = []
+        structure = []
+        device = None
+        for i in range(n):
+            g, m, v = g_leaves[i], mu_leaves[i], nu_leaves[i]
+            if _is_passthrough_leaf(m) or _is_passthrough_leaf(g):
+                out_leaves[i] = m if _is_passthrough_leaf(m) else g
+                continue
+            _require_device_tensor(g, "gradient")
+            if device is None:
+                device = g.device
+            if g.device != device:
+                raise ValueError("all leaves must live on the same device")
+            gdt = _rf_dtype(g.dtype, "gradient")
+            if not g.is_contiguous():
+                g = g.contiguous()
+            size = int(g.numel())
+            row = _lib.Adam8Leaf()
+            row.grad = g.data_ptr()
+            row.size = size
+            row.grad_dtype = gdt
+            row.state_index = i
+            row.param_index = i
+            decays = bool(decay_mask[i]) if decay_mask is not None else False
+            p = p_leaves[i] if p_leaves is not None else None
+            if (apply or decays) and (p is None or _is_passthrough_leaf(p)):
+                raise ValueError(NO_PARAMS_MSG)
+            if apply or decays:
+                _require_device_tensor(p, "param")
+                if not p.is_contiguous():
+                    raise ValueError("params must be contiguous (they are updated in place)")
+                if int(p.numel()) != size:
+                    raise ValueError(f"param and gradient sizes differ ({p.numel()} vs {size})")
+                row.param = p.data_ptr()
+                row.param_dtype = _rf_dtype(p.dtype, "param")
+            else:
+                row.param_dtype = _lib.RF_F32
+            row.flags = _lib.RF_LEAF_DECAY if decays else 0
+            if isinstance(m, QuantizedBlocks):
+                if not isinstance(v, QuantizedBlocks):
+                    raise ValueError("first and second moment leaves differ in kind")
+                if m.codebook_id != DYNAMIC_SIGNED_CODEBOOK_ID or v.codebook_id != DYNAMIC_UNSIGNED_CODEBOOK_ID:
+                    raise NotImplementedError("moment leaves must use the dynamic signed/unsigned codebooks")
+                if m.size != size or v.size != size or m.block_size != v.block_size:
+                    raise ValueError("quantized moment leaf does not match its gradient")
+                for t in (m.values, v.values, m.scales, v.scales):
+                    _require_device_tensor(t, "moment")
+                    if not t.is_contiguous():
+                        raise ValueError("moment buffers must be contiguous (they are updated in place)")
+                if m.scales.dtype != torch.float32 or v.scales.dtype != torch.float32:
+                    raise NotImplementedError("only float32 block scales are implemented")
+                row.moment_kind = _lib.RF_MOMENT_QUANTIZED
+                row.block_size = int(m.block_size)
+                row.mu = m.values.data_ptr()
+                row.mu_scales = m.scales.data_ptr()
+                row.nu = v.values.data_ptr()
+                row.nu_scales = v.scales.data_ptr()
+                align_ok = m.values.data_ptr() % 8 == 0 and v.values.data_ptr() % 8 == 0
+            else:
+                _require_device_tensor(m, "first moment")
+                _require_device_tensor(v, "second moment")
+                if m.dtype != v.dtype or int(m.numel()) != size or int(v.numel()) != size:
+                    raise ValueError("fallback moment leaf does not match its gradient")
+                if not (m.is_contiguous() and v.is_contiguous()):
+                    raise ValueError("moment buffers must be contiguous (they are updated in place)")
+                row.moment_kind = _lib.RF_MOMENT_BF16 if m.dtype == torch.bfloat16 else _lib.RF_MOMENT_F32
+                if m.dtype not in (torch.float32, torch.bfloat16):
+                    raise NotImplementedError(f"fallback moment dtype {m.dtype} is not supported")
+                row.mu = m.data_ptr()
+                row.nu = v.data_ptr()
+                align_ok = m.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0
+            out = None
+            if not apply:
+                out = torch.empty(g.shape, dtype=torch.float32, device=g.device)
+                row.updates = out.data_ptr()
+                out_leaves[i] = out
+            if random_bits is not None and i in random_bits:
+                mb, nb, pb = random_bits[i]
+                row.mu_bits = _ptr(mb)
+                row.nu_bits = _ptr(nb)
+                row.param_bits = _ptr(pb)
+            align_ok = (
+                align_ok
+                and g.data_ptr() % 16 == 0
+                and (row.param is None or row.param % 16 == 0)
+                and (out is None or out.data_ptr() % 16 == 0)
+            )
+            table_rows.append(row)
+            structure.append((size, row.block_size, row.param_dtype, gdt, row.moment_kind, i, row.flags, align_ok,
+                              row.mu_bits is not None or row.nu_bits is not None, row.param_bits is not None))
+
+        flags = 0
+        if cfg.nesterov:
+            flags |= _lib.RF_NESTEROV
+        if neg_lr is not None:
+            flags |= _lib.RF_LR
+        if decay_mask is not None and isinstance(weight_decay, (int, float)):
+            flags |= _lib.RF_DECAY_WEAK
+        if cfg.stochastic_rounding:
+            flags |= _lib.RF_MOMENT_SR
+        if apply and param_sr:
+            flags |= _lib.RF_PARAM_SR
+        if cfg.exact:
+            flags |= _lib.RF_EXACT
+        if random_bits is not None:
+            flags |= _lib.RF_FED_BITS
+
+        hp = _lib.Adam8Hparams()
+        hp.b1 = _as_f32(cfg.b1)
+        hp.one_minus_b1 = _one_minus(cfg.b1)
+        hp.b2 = _as_f32(cfg.b2)
+        hp.one_minus_b2 = _one_minus(cfg.b2)
+        hp.bc1 = _bias_correction(cfg.b1, count_inc)
+        hp.bc2 = _bias_correction(cfg.b2, count_inc)
+        hp.bc1_next = _bias_correction(cfg.b1, safe_int32_increment(count_inc))
+        hp.eps = _as_f32(cfg.eps)
+        hp.eps_root = _as_f32(cfg.eps_root)
+        hp.weight_decay = _as_f32(weight_decay) if weight_decay is not None else np.float32(0.0)
+        hp.neg_lr = neg_lr if neg_lr is not None else np.float32(1.0)
+        hp.flags = flags
+        hp.key_mu[0], hp.key_mu[1] = int(key_mu[0]), int(key_mu[1])
+        hp.key_nu[0], hp.key_nu[1] = int(key_nu[0]), int(key_nu[1])
+        if param_key is not None:
+            pk = prng.as_key(param_key)
+            hp.key_param[0], hp.key_param[1] = int(pk[0]), int(pk[1])
+
+        if table_rows:
+            table = (_lib.Adam8Leaf * len(table_rows))(*table_rows)
+            skey = (bool(apply), device.index, tuple(structure))
+            plan = self._plans.get(skey)
+            with torch.cuda.device(device):
+                if plan is None:
+                    plan = _LeafPlan(table, len(table_rows), apply)
+                    if len(self._plans) > 64:
+                        self._plans.clear()
+                    self._plans[skey] = plan
+                plan.run(table, hp, _lib.stream_ptr())
+
+        new_state = ScaleByAdam8State(
+            count=np.asarray(count_inc, dtype=np.int32),
+            mu=state.mu,
+            nu=state.nu,
+            key=next_key,
+        )
+        out_tree = _tree.unflatten(g_td, out_leaves) if not apply else None
+        return out_tree, new_state
+
+
+def _validate(block_size, min_size, block_layout, fallback_dtype, scale_dtype):
+    torch = _torch()
+    if block_size <= 0:
+        raise ValueError("block_size must be positive.")
+    if min_size < 0:
+        raise ValueError("min_size must be non-negative.")
+    if block_layout not in {"shard_local", "logical_global"}:
+        raise ValueError("block_layout must be 'shard_local' or 'logical_global'.")
+    if scale_dtype != torch.float32:
+        raise NotImplementedError("only float32 block scales are implemented (scale_dtype=float32)")
+    if fallback_dtype not in (torch.float32, torch.bfloat16):
+        raise NotImplementedError("fallback_dtype must be float32 or bfloat16")
+
+
+class _ScaleByAdam8Update:
+    """``scale_by_adam8(...).update`` (adam8.py:304-389): Adam direction only."""
+
+    def __init__(self, engine: _Engine):
+        self.engine = engine
+
+    def __call__(self, updates, state, params=None):
+        del params
+        return self.engine.run(updates, state, None, apply=False, decay_mask=None, weight_decay=None, neg_lr=None)
+
+
+def scale_by_adam8(
+    b1=0.9,
+    b2=0.999,
+    eps=1e-8,
+    eps_root=0.0,
+    *,
+    block_size: int = 2048,
+    min_size: int = 4096,
+    scale_dtype=None,
+    fallback_dtype=None,
+    stochastic_rounding: bool = False,
+    block_layout: BlockLayout = "shard_local",
+    quantize: bool = True,
+    nesterov: bool = False,
+    key=None,
+    exact: bool = False,
+) -> GradientTransformation:
+    """Rescale gradients by Adam while storing eligible moments as 8-bit
+    blocks (adam8.py:243-391).  ``exact`` (extension): IEEE division and
+    square root in the update direction instead of the hardware
+    reciprocal/square-root (moments, codes and scales are bit-exact either
+    way)."""
+    torch = _torch()
+    scale_dtype = torch.float32 if scale_dtype is None else canonicalize_dtype(scale_dtype)
+    fallback_dtype = torch.float32 if fallback_dtype is None else canonicalize_dtype(fallback_dtype)
+    _validate(block_size, min_size, block_layout, fallback_dtype, scale_dtype)
+    cfg = _Config(b1, b2, eps, eps_root, int(block_size), int(min_size), scale_dtype, fallback_dtype,
+                  bool(stochastic_rounding), block_layout, bool(quantize), bool(nesterov), key, bool(exact))
+    engine = _Engine(cfg)
+
+    def init_fn(params):
+        key_mu, key_nu, next_key = prng.split(prng.fresh_key(cfg.key), 3)
+        del key_mu, key_nu  # zero state: quantize_blocks(zeros) draws no random bits
+        mu = _init_moment_tree(params, cfg, "dynamic_signed")
+        nu = _init_moment_tree(params, cfg, "dynamic_unsigned")
+        return ScaleByAdam8State(count=np.zeros((), dtype=np.int32), mu=mu, nu=nu, key=next_key)
+
+    return GradientTransformation(init_fn, _ScaleByAdam8Update(engine))
+
+
+def _decay_mask_leaves(mask, params, n_leaves: int) -> list:
+    """Per-leaf booleans of an optax mask (a prefix tree of bools or a
+    callable on params), aligned with the flattened params."""
+    if mask is None:
+        return [True] * n_leaves
+    mask_tree = mask(params) if callable(mask) else mask
+    m_leaves, m_td = _tree.flatten(mask_tree, is_leaf=lambda x: isinstance(x, bool))
+    subtrees = _tree.flatten_up_to(m_td, params)
+    out: list = []
+    for mval, sub in zip(m_leaves, subtrees):
+        count = len(_tree.leaves(sub, is_leaf=_is_passthrough_leaf))
+        out.extend([bool(mval)] * count)
+    if len(out) != n_leaves:
+        raise ValueError("weight_decay_mask does not match the params tree")
+    return out
+
+
+class _Adamw8Update:
+    """``adamw8(...).update``: the optax chain scale_by_adam8 ->
+    add_decayed_weights -> scale_by_learning_rate in one launch."""
+
+    def __init__(self, engine: _Engine, learning_rate, weight_decay, weight_decay_mask, wd_nonzero: bool):
+        self.engine = engine
+        self.learning_rate = learning_rate
+        self.weight_decay = weight_decay
+        self.weight_decay_mask = weight_decay_mask
+        self.wd_nonzero = wd_nonzero
+
+    def _lr(self, lr_state):
+        """(-lr as f32, new lr state) per optax scale_by_learning_rate."""
+        lr = self.learning_rate
+        if callable(lr):
+            count = int(np.asarray(lr_state.count))
+            value = _as_f32(lr(np.asarray(count, dtype=np.int32)))
+            return np.float32(-value), ScaleByScheduleState(
+                count=np.asarray(safe_int32_increment(count), dtype=np.int32))
+        return np.float32(-_as_f32(lr)) if not isinstance(lr, (int, float)) else np.float32(-lr), lr_state
+
+    def _step(self, updates, state, params, *, apply: bool, param_key=None, param_sr=False, random_bits=None):
+        adam_state = state[0]
+        lr_state = state[-1]
+        neg_lr, new_lr_state = self._lr(lr_state)
+        decay_mask = None
+        if self.wd_nonzero:
+            if params is None:
+                raise ValueError(NO_PARAMS_MSG)
+            n = len(_tree.leaves(updates, is_leaf=_is_passthrough_leaf))
+            decay_mask = _decay_mask_leaves(self.weight_decay_mask, params, n)
+        out, new_adam = self.engine.run(
+            updates, adam_state, params, apply=apply, decay_mask=decay_mask,
+            weight_decay=self.weight_decay if self.wd_nonzero else None, neg_lr=neg_lr,
+            param_key=param_key, param_sr=param_sr, random_bits=random_bits,
+        )
+        new_state = (new_adam,) + tuple(state[1:-1]) + (new_lr_state,)
+        return out, new_state
+
+    def __call__(self, updates, state, params=None, **extra_args):
+        del extra_args
+        return self._step(updates, state, params, apply=False)
+
+
+def adamw8(
+    learning_rate,
+    b1=0.9,
+    b2=0.999,
+    eps=1e-8,
+    eps_root=0.0,
+    weight_decay=1e-4,
+    weight_decay_mask: Optional[Union[Any, Callable[[Any], Any]]] = None,
+    *,
+    block_size: int = 2048,
+    min_size: int = 4096,
+    scale_dtype=None,
+    fallback_dtype=None,
+    stochastic_rounding: bool = False,
+    block_layout: BlockLayout = "shard_local",
+    quantize: bool = True,
+    nesterov: bool = False,
+    use_magma: bool = False,
+    key=None,
+    exact: bool = False,
+) -> GradientTransformationExtraArgs:
+    """AdamW whose eligible moment leaves use blockwise 8-bit codebook state
+    (adam8.py:394-443).  The state is the chain's tuple
+    ``(ScaleByAdam8State, add_decayed_weights state?, lr state)``."""
+    if use_magma:
+        raise NotImplementedError("Magma is not supported by adamw8 yet.")
+    if callable(weight_decay):
+        raise NotImplementedError("weight-decay schedules are not supported; pass a scalar")
+    inner = scale_by_adam8(
+        b1=b1, b2=b2, eps=eps, eps_root=eps_root, block_size=block_size, min_size=min_size,
+        scale_dtype=scale_dtype, fallback_dtype=fallback_dtype, stochastic_rounding=stochastic_rounding,
+        block_layout=block_layout, quantize=quantize, nesterov=nesterov, key=key, exact=exact,
+    )
+    weight_decay_is_nonzero = weight_decay > 0.0 if isinstance(weight_decay, (int, float)) else True
+    engine = inner.update.engine
+
+    def init_fn(params):
+        states = [inner.init(params)]
+        if weight_decay_is_nonzero:
+            states.append(MaskedState(EmptyState()) if weight_decay_mask is not None else EmptyState())
+        if callable(learning_rate):
+            states.append(ScaleByScheduleState(count=np.zeros((), dtype=np.int32)))
+        else:
+            states.append(EmptyState())
+        return tuple(states)
+
+    update = _Adamw8Update(engine, learning_rate, weight_decay, weight_decay_mask, weight_decay_is_nonzero)
+    return GradientTransformationExtraArgs(init_fn, update)
+
+
+def adamw8_step(tx, params, grads, state, key=None, stochastic: bool = True, *, random_bits=None):
+    """Fused ``tx.update`` + ``rollfast.apply_updates`` in one HBM pass (no
+    reference counterpart: the reference runs them as two XLA programs).
+
+    Equivalent to::
+
+        updates, state = tx.update(grads, state, params)
+        params = rollfast.apply_updates(params, updates, key, stochastic)
+
+    for ``tx = adamw8(...)``.  Params are updated in place and returned with
+    the new state.  ``random_bits`` (testing): ``{leaf_index: (mu_bits,
+    nu_bits, param_bits)}`` device uint32 arrays replacing in-kernel bits.
+    """
+    if not isinstance(tx.update, _Adamw8Update):
+        raise TypeError("adamw8_step needs a transformation built by adamw8(...)")
+    if stochastic and key is None:
+        raise ValueError(
+            "apply_updates requires a PRNG `key` when stochastic=True. "
+            "Pass stochastic=False for deterministic rounding."
+        )
+    _, new_state = tx.update._step(grads, state, params, apply=True, param_key=key, param_sr=bool(stochastic),
+                                   random_bits=random_bits)
+    return params, new_state
+
+
+__all__ = (
+    "QuantizedBlocks",
+    "BlockLayout",
+    "CodebookQuantizer",
+    "ScaleByAdam8State",
+    "DYNAMIC_SIGNED_CODEBOOK_ID",
+    "DYNAMIC_UNSIGNED_CODEBOOK_ID",
+    "SYMMETRIC_INT8_CODEBOOK_ID",
+    "adamw8",
+    "adamw8_step",
+    "dequantize_blocks",
+    "estimate_quantized_moment_bytes",
+    "quantize_blocks",
+    "quantized_nbytes",
+    "scale_by_adam8",
+    "tree_state_nbytes",
+)

@@ -1,0 +1,241 @@
+"""GPU parity of the standalone kernels against the CPU oracle:
+quantize_blocks / dequantize_blocks (rollfast optim/adam8.py:113-204),
+_stochastic_round_bf16 (utils.py:342-371) and apply_updates (:648-708).
+Integer/byte outputs (codes, bf16 bit patterns) must be bit-exact; f32
+outputs (scales, dequantized values) are compared bit for bit as well."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests._helpers import bf16_bits, to_device, to_host
+
+pytestmark = pytest.mark.gpu
+
+QUANTIZERS = {"dynamic_signed": orc.Q_SIGNED, "dynamic_unsigned": orc.Q_UNSIGNED, "symmetric_int8": orc.Q_SYMMETRIC}
+
+
+def _rf():
+    import rollfast_amd as rf
+
+    return rf
+
+
+def _edge_values(rng, n):
+    """Log-uniform magnitudes 1e-8..1e2 with random sign, plus zeros,
+    denormals, exact ties and +-absmax."""
+    mag = np.exp(rng.uniform(np.log(1e-8), np.log(1e2), size=n)).astype(np.float32)
+    x = np.where(rng.random(n) < 0.5, -mag, mag).astype(np.float32)
+    x[rng.random(n) < 0.02] = 0.0
+    x[rng.random(n) < 0.01] = np.float32(-0.0)
+    den = rng.random(n) < 0.01
+    x[den] = (rng.integers(1, 1 << 23, size=den.sum()).astype(np.uint32)).view(np.float32)
+    return x
+
+
+def _check_quantize(x, block_size, quantizer, sr=False):
+    import torch
+
+    rf = _rf()
+    key = rf.prng.PRNGKey(11)
+    xd = to_device(x, "f32")
+    qb = rf.quantize_blocks(xd, block_size=block_size, quantizer=quantizer, stochastic_rounding=sr,
+                            key=key if sr else None)
+    torch.cuda.synchronize()
+    nb = max(1, -(-x.size // block_size))
+    bits = orc.random_bits(key, nb * block_size) if sr else None
+    codes, scales = orc.quantize(x, block_size, QUANTIZERS[quantizer], bits=bits)
+    got = to_host(qb.values)
+    np.testing.assert_array_equal(got.view(np.uint8), codes.reshape(-1).view(np.uint8))
+    np.testing.assert_array_equal(to_host(qb.scales).view(np.uint32), scales.view(np.uint32))
+    back = rf.dequantize_blocks(qb)
+    torch.cuda.synchronize()
+    ref = orc.dequantize(codes, scales, x.size, block_size, QUANTIZERS[quantizer])
+    np.testing.assert_array_equal(to_host(back).view(np.uint32), ref.view(np.uint32))
+    assert tuple(back.shape) == tuple(xd.shape)
+
+
+@pytest.mark.parametrize("quantizer", list(QUANTIZERS))
+@pytest.mark.parametrize("block_size,size", [(2048, 2048 * 37), (2048, 2048 * 5 + 777), (128, 513), (1000, 4321)])
+def test_quantize_dequantize_parity(quantizer, block_size, size):
+    rng = np.random.default_rng(size + block_size)
+    _check_quantize(_edge_values(rng, size), block_size, quantizer)
+
+
+@pytest.mark.parametrize("quantizer", list(QUANTIZERS))
+def test_quantize_stochastic_rounding_parity(quantizer):
+    rng = np.random.default_rng(9)
+    _check_quantize(_edge_values(rng, 2048 * 9 + 5), 2048, quantizer, sr=True)
+
+
+def test_quantize_special_blocks():
+    """Zero blocks (scale 1), a block with -absmax (clipped to code 0), NaN and
+    Inf blocks, a tiny-scale block below the fast range, exact ties."""
+    bs = 2048
+    blocks = []
+    blocks.append(np.zeros(bs, np.float32))
+    b = np.linspace(-1, 1, bs).astype(np.float32)
+    b[0] = -2.0
+    b[1] = 2.0
+    blocks.append(b)
+    b = np.linspace(-1, 1, bs).astype(np.float32)
+    b[5] = np.nan
+    blocks.append(b)
+    b = np.linspace(-1, 1, bs).astype(np.float32)
+    b[7] = np.inf
+    blocks.append(b)
+    b = np.linspace(-1, 1, bs).astype(np.float32)
+    b[9] = -np.inf
+    blocks.append(b)
+    blocks.append((np.linspace(-1, 1, bs) * 1e-30).astype(np.float32))   # scale < 2^-70
+    blocks.append((np.linspace(-1, 1, bs) * 1e-40).astype(np.float32))   # subnormal scale
+    cb = orc.codebook(True)
+    mids = ((cb[:-1].astype(np.float64) + cb[1:]) / 2).astype(np.float32)
+    b = np.resize(np.concatenate([mids, cb, [1.0]]).astype(np.float32), bs)
+    blocks.append(b)
+    x = np.concatenate(blocks)
+    for q in QUANTIZERS:
+        _check_quantize(x, bs, q)
+
+
+def _decision_patterns(q):
+    """Bit patterns of normalised values that probe the kernel's lookup: a
+    stride-61 sweep of [-1, 1] ([0, 1] unsigned) plus +-64 patterns around
+    every midpoint of adjacent codebook entries (where the thresholds are)."""
+    cb = orc.codebook(q == orc.Q_SIGNED)
+    pats = [np.arange(0, 0x3F800001, 61, dtype=np.uint64)]
+    if q == orc.Q_SIGNED:
+        pats.append(np.arange(0x80000000, 0xBF800001, 61, dtype=np.uint64))
+    mids = ((cb[:-1].astype(np.float64) + cb[1:]) / 2).astype(np.float32).view(np.uint32).astype(np.int64)
+    near = (mids[:, None] + np.arange(-64, 65)[None, :]).reshape(-1)
+    pats.append(near.astype(np.uint64))
+    pats.append(cb.view(np.uint32).astype(np.uint64))
+    bits = np.unique(np.concatenate(pats)).astype(np.uint32)
+    vals = bits.view(np.float32)
+    keep = np.abs(vals) <= 1.0
+    if q == orc.Q_UNSIGNED:
+        keep &= vals >= 0
+    return bits[keep]
+
+
+@pytest.mark.parametrize("quantizer", ["dynamic_signed", "dynamic_unsigned"])
+def test_quantize_normalised_values_through_table_lookup(quantizer):
+    """Normalised values pass through the kernel's table lookup with scale 1
+    (each block holds 1.0) and must equal the oracle's searchsorted code."""
+    import torch
+
+    rf = _rf()
+    q = QUANTIZERS[quantizer]
+    bits = _decision_patterns(q)
+    n = bits.size
+    nb = -(-n // 2047)
+    body = np.zeros(nb * 2047, np.uint32)
+    body[:n] = bits
+    x = np.zeros((nb, 2048), np.float32)
+    x[:, :2047] = body.reshape(nb, 2047).view(np.float32)
+    x[:, 2047] = 1.0
+    qb = rf.quantize_blocks(to_device(x.reshape(-1), "f32"), quantizer=quantizer)
+    torch.cuda.synchronize()
+    got = to_host(qb.values).reshape(nb, 2048)[:, :2047].reshape(-1)[:n]
+    want = orc.nearest_codes_list(q, bits)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{quantizer}: code mismatch at bits {hex(int(bits[bad[0]]))}"
+
+
+def test_sr_bf16_parity_fed_and_threefry():
+    import torch
+
+    from rollfast_amd.utils import _stochastic_round_bf16
+
+    rf = _rf()
+    rng = np.random.default_rng(1)
+    n = 1 << 20
+    x = _edge_values(rng, n)
+    x[:4] = [np.inf, -np.inf, np.nan, np.float32(3.0e38)]
+    key = rf.prng.PRNGKey(5)
+    bits = orc.random_bits(key, n)
+    want = orc.sr_bf16(x, bits)
+    got = _stochastic_round_bf16(to_device(x, "f32"), key)
+    got_fed = _stochastic_round_bf16(to_device(x, "f32"), key, random_bits=to_device(bits, "u32"))
+    torch.cuda.synchronize()
+    w = want.copy()
+    for arr in (to_host(got), to_host(got_fed)):
+        nan = np.isnan(orc.bf16_bits_to_f32(w))
+        np.testing.assert_array_equal(arr[~nan], w[~nan])
+        assert np.isnan(orc.bf16_bits_to_f32(arr[nan])).all()
+
+
+@pytest.mark.parametrize("stochastic", [False, True])
+def test_apply_updates_parity(stochastic):
+    import torch
+
+    rf = _rf()
+    rng = np.random.default_rng(2)
+    sizes = [(4096,), (33, 7), (1,), (2048 * 3 + 5,)]
+    dtypes = ["bf16", "f32", "bf16", "f32"]
+    params, host = {}, []
+    ups, uhost = {}, []
+    for i, (s, dt) in enumerate(zip(sizes, dtypes)):
+        n = int(np.prod(s))
+        p = (rng.standard_normal(n) * 0.5).astype(np.float32)
+        p = bf16_bits(p) if dt == "bf16" else p
+        u = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+        params[f"p{i}"] = to_device(p, dt).reshape(s)
+        ups[f"p{i}"] = to_device(u, "f32").reshape(s)
+        host.append(p.copy())
+        uhost.append(u)
+    key = rf.prng.PRNGKey(0)
+    out = rf.apply_updates(params, ups, key=key if stochastic else None, stochastic=stochastic)
+    torch.cuda.synchronize()
+    keys = orc.split(key, len(sizes))
+    for i, dt in enumerate(dtypes):
+        pd = orc.BF16 if dt == "bf16" else orc.F32
+        bits = orc.random_bits(keys[i], host[i].size) if stochastic else None
+        orc.apply_updates(host[i], pd, uhost[i], bits=bits)
+        np.testing.assert_array_equal(to_host(out[f"p{i}"]).view(np.uint8), host[i].view(np.uint8))
+
+
+def test_apply_updates_sub_ulp_signal():
+    """tests/test_utils.py:89-103: ones(4096) bf16 + 2^-9 stays 1 under RNE
+    and rises in mean under stochastic rounding."""
+    import torch
+
+    rf = _rf()
+    p1 = {"w": torch.ones((4096,), dtype=torch.bfloat16, device="cuda")}
+    p2 = {"w": torch.ones((4096,), dtype=torch.bfloat16, device="cuda")}
+    u = {"w": torch.full((4096,), 2.0**-9, dtype=torch.float32, device="cuda")}
+    det = rf.apply_updates(p1, u, stochastic=False)
+    sto = rf.apply_updates(p2, u, key=rf.prng.PRNGKey(0))
+    assert torch.all(det["w"] == 1.0)
+    assert torch.any(sto["w"] > det["w"])
+    assert sto["w"].float().mean() > det["w"].float().mean()
+
+
+def test_apply_updates_skips_none_and_masked():
+    import torch
+
+    rf = _rf()
+    params = {"w": torch.ones((2,), device="cuda"), "none": torch.ones((2,), device="cuda"),
+              "masked": torch.ones((2,), device="cuda")}
+    updates = {"w": torch.ones((2,), device="cuda"), "none": None, "masked": rf.MaskedNode()}
+    out = rf.apply_updates(params, updates, key=rf.prng.PRNGKey(0), stochastic=False)
+    torch.cuda.synchronize()
+    assert torch.allclose(out["w"], torch.full((2,), 2.0, device="cuda"))
+    assert torch.allclose(out["none"], torch.ones((2,), device="cuda"))
+    assert torch.allclose(out["masked"], torch.ones((2,), device="cuda"))
+
+
+def test_apply_updates_prefix_skips_subtrees():
+    import torch
+
+    rf = _rf()
+    params = {"train": {"w": torch.ones((2,), device="cuda"), "b": torch.full((2,), 3.0, device="cuda")},
+              "static": {"name": "layer"}}
+    updates = {"train": {"w": torch.ones((2,), device="cuda"), "b": None}, "static": None}
+    out = rf.apply_updates_prefix(params, updates, stochastic=False)
+    torch.cuda.synchronize()
+    assert torch.allclose(out["train"]["w"], torch.full((2,), 2.0, device="cuda"))
+    assert torch.allclose(out["train"]["b"], torch.full((2,), 3.0, device="cuda"))
+    assert out["static"] == {"name": "layer"}

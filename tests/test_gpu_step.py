@@ -1,0 +1,341 @@
+"""GPU parity of the fused adamw8 step and the Optax-mode update against the
+CPU oracle, through the public API (rollfast_amd.adamw8 / adamw8_step) and
+the C ABI underneath.
+
+Bar (stated per assertion):
+* moment codes and block scales: bit-exact;
+* params: bit-exact with ``exact=True`` (IEEE div/sqrt), within one bf16
+  ulp otherwise (bf16 and f32 params alike);
+* Optax-mode f32 updates: bit-exact with ``exact=True``, relative error
+  <= 8 f32 ulps (hardware rcp/sqrt) otherwise.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests._helpers import (
+    OracleTree,
+    bf16_bits,
+    bf16_ulp_distance,
+    f32_within_bf16_ulp,
+    gaussian,
+    to_device,
+    to_host,
+)
+
+pytestmark = pytest.mark.gpu
+
+
+def _rf():
+    import rollfast_amd as rf
+
+    return rf
+
+
+def _leaf_np(rng, size, pdtype, std=0.02):
+    p = gaussian(rng, (size,), std)
+    return bf16_bits(p) if pdtype == "bf16" else p
+
+
+def _build(spec, seed):
+    """spec: list of (shape, pdtype, gdtype).  Returns host params and device
+    params (dict with sorted keys so flatten order == list order)."""
+    rng = np.random.default_rng(seed)
+    host, dev = {}, {}
+    for i, (shape, pd, _gd) in enumerate(spec):
+        size = int(np.prod(shape))
+        p = _leaf_np(rng, size, pd)
+        host[f"l{i:03d}"] = p
+        dev[f"l{i:03d}"] = to_device(p, pd).reshape(shape)
+    return host, dev
+
+
+def _grads(spec, seed, std=1e-2):
+    rng = np.random.default_rng(seed)
+    host, dev = [], {}
+    for i, (shape, _pd, gd) in enumerate(spec):
+        size = int(np.prod(shape))
+        g = gaussian(rng, (size,), std)
+        g = bf16_bits(g) if gd == "bf16" else g
+        host.append(g)
+        dev[f"l{i:03d}"] = to_device(g, gd).reshape(shape)
+    return host, dev
+
+
+def _oracle_from_state(spec, host_params, state_adam):
+    import rollfast_amd as rf
+
+    leaves = []
+    for i, (shape, pd, gd) in enumerate(spec):
+        name = f"l{i:03d}"
+        m = state_adam.mu[name]
+        v = state_adam.nu[name]
+        L = {"pdtype": pd, "gdtype": gd, "size": int(np.prod(shape)), "param": host_params[name].copy()}
+        if isinstance(m, rf.QuantizedBlocks):
+            L.update(kind="quant", block_size=m.block_size, mu=to_host(m.values).copy(),
+                     mu_scales=to_host(m.scales).copy(), nu=to_host(v.values).copy(),
+                     nu_scales=to_host(v.scales).copy())
+        else:
+            import torch
+
+            kind = "bf16" if m.dtype == torch.bfloat16 else "f32"
+            L.update(kind=kind, mu=to_host(m).copy(), nu=to_host(v).copy())
+        leaves.append(L)
+    return OracleTree(leaves)
+
+
+def _compare_state(spec, tree, state_adam, what):
+    import torch
+
+    import rollfast_amd as rf
+
+    for i, L in enumerate(tree.leaves):
+        name = f"l{i:03d}"
+        m, v = state_adam.mu[name], state_adam.nu[name]
+        if isinstance(m, rf.QuantizedBlocks):
+            np.testing.assert_array_equal(to_host(m.values), L["mu"], err_msg=f"{what} leaf {i} mu codes")
+            np.testing.assert_array_equal(to_host(v.values), L["nu"], err_msg=f"{what} leaf {i} nu codes")
+            np.testing.assert_array_equal(to_host(m.scales).view(np.uint32), L["mu_scales"].view(np.uint32),
+                                          err_msg=f"{what} leaf {i} mu scales")
+            np.testing.assert_array_equal(to_host(v.scales).view(np.uint32), L["nu_scales"].view(np.uint32),
+                                          err_msg=f"{what} leaf {i} nu scales")
+        else:
+            a, b = to_host(m), L["mu"]
+            if m.dtype == torch.float32:
+                a, b = a.view(np.uint32), b.view(np.uint32)
+            np.testing.assert_array_equal(a, b, err_msg=f"{what} leaf {i} fallback mu")
+            a, b = to_host(v), L["nu"]
+            if v.dtype == torch.float32:
+                a, b = a.view(np.uint32), b.view(np.uint32)
+            np.testing.assert_array_equal(a, b, err_msg=f"{what} leaf {i} fallback nu")
+
+
+def _compare_params(spec, tree, dev_params, exact, what):
+    for i, ((shape, pd, _gd), L) in enumerate(zip(spec, tree.leaves)):
+        got = to_host(dev_params[f"l{i:03d}"])
+        want = L["param"]
+        if exact:
+            np.testing.assert_array_equal(got.view(np.uint16 if pd == "bf16" else np.uint32),
+                                          want.view(np.uint16 if pd == "bf16" else np.uint32),
+                                          err_msg=f"{what} leaf {i} params (bit-exact)")
+        elif pd == "bf16":
+            d = bf16_ulp_distance(got, want)
+            assert d.max() <= 1, f"{what} leaf {i}: bf16 params differ by {d.max()} ulp"
+        else:
+            ok = f32_within_bf16_ulp(got, want)
+            assert ok.all(), f"{what} leaf {i}: f32 params beyond one bf16 ulp"
+
+
+def _run(spec, *, steps=3, exact=False, block_size=2048, min_size=4096, wd=0.01, lr=1e-3, msr=False,
+         psr=False, nesterov=False, fallback=None, seed=0, eps_root=0.0):
+    import torch
+
+    rf = _rf()
+    host_params, params = _build(spec, seed)
+    tx = rf.adamw8(learning_rate=lr, weight_decay=wd, block_size=block_size, min_size=min_size,
+                   stochastic_rounding=msr, nesterov=nesterov, exact=exact, eps_root=eps_root,
+                   fallback_dtype=fallback, key=rf.prng.PRNGKey(7))
+    state = tx.init(params)
+    for step in range(steps):
+        ghost, gdev = _grads(spec, seed + 1000 + step)
+        # Oracle starts from the device state (params too): one step compared.
+        for i, (_shape, pd, _gd) in enumerate(spec):
+            host_params[f"l{i:03d}"] = to_host(params[f"l{i:03d}"]).copy()
+        tree = _oracle_from_state(spec, host_params, state[0])
+        count_inc = int(state[0].count) + 1
+        key_mu, key_nu, _ = orc.split(state[0].key, 3)
+        n = len(spec)
+        mu_bits = nu_bits = p_bits = None
+        pkey = rf.prng.PRNGKey(100 + step)
+        if msr:
+            kmu = orc.split(key_mu, n)
+            knu = orc.split(key_nu, n)
+            mu_bits, nu_bits = [], []
+            for i, L in enumerate(tree.leaves):
+                padded = (len(L["mu"]) if L["kind"] == "quant" else L["size"])
+                mu_bits.append(orc.random_bits(kmu[i], padded))
+                nu_bits.append(orc.random_bits(knu[i], padded))
+        if psr:
+            kp = orc.split(pkey, n)
+            p_bits = [orc.random_bits(kp[i], L["size"]) for i, L in enumerate(tree.leaves)]
+        tree.step(ghost, weight_decay=wd, lr=lr, count=count_inc, nesterov=nesterov, moment_sr=msr,
+                  param_sr=psr, mu_bits=mu_bits, nu_bits=nu_bits, p_bits=p_bits, eps_root=eps_root)
+        params, state = rf.adamw8_step(tx, params, gdev, state, key=pkey if psr else None, stochastic=psr)
+        torch.cuda.synchronize()
+        _compare_state(spec, tree, state[0], f"step {step + 1}")
+        _compare_params(spec, tree, params, exact, f"step {step + 1}")
+
+
+C1 = [((1024, 1024), "f32", "f32")]
+
+
+@pytest.mark.parametrize("exact", [True, False])
+def test_c1_fp32_1024x1024_three_steps(exact):
+    """The single-step CPU-reference configuration (1024x1024 f32, block 2048,
+    lr 1e-3, wd 0.01), steps 1..3."""
+    _run(C1, steps=3, exact=exact)
+
+
+MIXED = [
+    ((64, 2048), "bf16", "bf16"),   # full 2048 blocks, vectorised path
+    ((3, 3000), "bf16", "f32"),     # 9000: 4 full blocks + partial block
+    ((768,), "bf16", "bf16"),       # below min_size: f32 fallback moments
+    ((4096,), "f32", "bf16"),       # exactly min_size: quantized
+    ((5, 1111), "f32", "f32"),      # odd size, partial block
+    ((1,), "bf16", "bf16"),         # single element fallback
+]
+
+
+@pytest.mark.parametrize("exact", [True, False])
+def test_mixed_tree_bf16_f32(exact):
+    _run(MIXED, steps=3, exact=exact)
+
+
+def test_generic_block_size_256_and_nesterov():
+    spec = [((40, 256), "bf16", "bf16"), ((1000,), "f32", "f32"), ((33, 7), "bf16", "f32")]
+    _run(spec, steps=2, block_size=256, min_size=16, nesterov=True, exact=True)
+
+
+def test_odd_block_size_and_eps_root():
+    spec = [((10, 300), "bf16", "bf16"), ((7000,), "f32", "bf16")]
+    _run(spec, steps=2, block_size=1000, min_size=100, eps_root=1e-12, exact=True)
+
+
+def test_bf16_fallback_moments():
+    spec = [((100,), "bf16", "bf16"), ((2048,), "f32", "f32")]
+    import torch
+
+    _run(spec, steps=2, min_size=1 << 20, fallback=torch.bfloat16, exact=True)
+
+
+def test_moment_stochastic_rounding_matches_threefry_bits():
+    """In-kernel Threefry bits == the oracle's jax.random.bits layout."""
+    _run(MIXED, steps=2, msr=True, exact=True)
+
+
+def test_param_stochastic_rounding_matches_threefry_bits():
+    spec = [((64, 2048), "bf16", "bf16"), ((3, 3000), "bf16", "f32"), ((768,), "bf16", "bf16")]
+    _run(spec, steps=2, psr=True, exact=True)
+
+
+def test_fast_direction_over_twenty_steps():
+    spec = [((128, 2048), "bf16", "bf16"), ((777,), "bf16", "bf16")]
+    _run(spec, steps=20, exact=False)
+
+
+# ---------------------------------------------------------- Optax mode --
+def _optax_mode(spec, *, adamw, exact, seed=3):
+    import torch
+
+    rf = _rf()
+    host_params, params = _build(spec, seed)
+    if adamw:
+        tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, min_size=1024, exact=exact)
+    else:
+        tx = rf.scale_by_adam8(min_size=1024, exact=exact)
+    state = tx.init(params)
+    for step in range(2):
+        ghost, gdev = _grads(spec, seed + 10 + step)
+        adam_state = state[0] if adamw else state
+        tree = _oracle_from_state(spec, host_params, adam_state)
+        count_inc = int(adam_state.count) + 1
+        outs = tree.step(ghost, weight_decay=0.01 if adamw else 0.0, lr=1e-3, count=count_inc, apply=False,
+                         lr_scale=adamw)
+        updates, state = tx.update(gdev, state, params)
+        torch.cuda.synchronize()
+        _compare_state(spec, tree, state[0] if adamw else state, f"optax step {step + 1}")
+        for i in range(len(spec)):
+            got = to_host(updates[f"l{i:03d}"])
+            want = outs[i]
+            if exact:
+                np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+            else:
+                rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want), 1e-30)
+                assert rel.max() <= 8 * 2.0**-23, f"leaf {i}: relative error {rel.max()}"
+        # Params untouched by the Optax-mode update.
+        for i, (_s, pd, _g) in enumerate(spec):
+            got = to_host(params[f"l{i:03d}"])
+            np.testing.assert_array_equal(got, host_params[f"l{i:03d}"])
+
+
+@pytest.mark.parametrize("exact", [True, False])
+@pytest.mark.parametrize("adamw", [True, False])
+def test_optax_mode_updates(adamw, exact):
+    spec = [((8, 2048), "bf16", "bf16"), ((3000,), "f32", "f32"), ((100,), "bf16", "f32")]
+    _optax_mode(spec, adamw=adamw, exact=exact)
+
+
+def test_fused_equals_update_plus_apply_updates():
+    """adamw8_step == tx.update + apply_updates (RNE), bit for bit."""
+    import torch
+
+    rf = _rf()
+    spec = [((16, 2048), "bf16", "bf16"), ((500,), "f32", "bf16")]
+    host, pa = _build(spec, 11)
+    _, pb = _build(spec, 11)
+    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=True)
+    sa = tx.init(pa)
+    sb = tx.init(pb)
+    for step in range(3):
+        _, g = _grads(spec, 50 + step)
+        pa, sa = rf.adamw8_step(tx, pa, g, sa, stochastic=False)
+        u, sb = tx.update(g, sb, pb)
+        pb = rf.apply_updates(pb, u, stochastic=False)
+        torch.cuda.synchronize()
+        for k in pa:
+            np.testing.assert_array_equal(to_host(pa[k]), to_host(pb[k]))
+            ma, mb = sa[0].mu[k], sb[0].mu[k]
+            if isinstance(ma, rf.QuantizedBlocks):
+                np.testing.assert_array_equal(to_host(ma.values), to_host(mb.values))
+                np.testing.assert_array_equal(to_host(ma.scales), to_host(mb.scales))
+
+
+def test_fed_bits_equal_in_kernel_bits():
+    """RF_FED_BITS with the oracle's bits gives the in-kernel-bits result."""
+    import torch
+
+    rf = _rf()
+    spec = [((8, 2048), "bf16", "bf16"), ((1500,), "bf16", "bf16")]
+    _, pa = _build(spec, 5)
+    _, pb = _build(spec, 5)
+    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, stochastic_rounding=True, min_size=1024, exact=True)
+    sa, sb = tx.init(pa), tx.init(pb)
+    _, g = _grads(spec, 77)
+    pkey = rf.prng.PRNGKey(3)
+    key_mu, key_nu, _ = orc.split(sa[0].key, 3)
+    kmu, knu, kp = orc.split(key_mu, 2), orc.split(key_nu, 2), orc.split(pkey, 2)
+    bits = {}
+    for i, name in enumerate(sorted(pa)):
+        m = sa[0].mu[name]
+        padded = m.values.numel()
+        size = pa[name].numel()
+        bits[i] = (to_device(orc.random_bits(kmu[i], padded), "u32"),
+                   to_device(orc.random_bits(knu[i], padded), "u32"),
+                   to_device(orc.random_bits(kp[i], size), "u32"))
+    pa, sa = rf.adamw8_step(tx, pa, g, sa, key=pkey, stochastic=True)
+    pb, sb = rf.adamw8_step(tx, pb, g, sb, key=pkey, stochastic=True, random_bits=bits)
+    torch.cuda.synchronize()
+    for k in pa:
+        np.testing.assert_array_equal(to_host(pa[k]), to_host(pb[k]))
+        np.testing.assert_array_equal(to_host(sa[0].mu[k].values), to_host(sb[0].mu[k].values))
+        np.testing.assert_array_equal(to_host(sa[0].nu[k].values), to_host(sb[0].nu[k].values))
+
+
+def test_state_key_and_count_evolve_like_reference():
+    rf = _rf()
+    import torch
+
+    params = {"w": torch.zeros((4096,), dtype=torch.bfloat16, device="cuda")}
+    tx = rf.adamw8(learning_rate=1e-3)
+    st = tx.init(params)
+    # init: split(PRNGKey(42), 3)[2] (adam8.py:274, utils.py:73-76)
+    np.testing.assert_array_equal(st[0].key, orc.split((0, 42), 3)[2])
+    k = st[0].key
+    for t in range(1, 4):
+        _, st = rf.adamw8_step(tx, params, {"w": torch.zeros_like(params["w"])}, st, stochastic=False)
+        k = orc.split(k, 3)[2]
+        np.testing.assert_array_equal(st[0].key, k)
+        assert int(st[0].count) == t
