@@ -13,13 +13,25 @@
 
 namespace rf {
 
-adam_kernel_t RF_PICK_NAME(RFI_APPLY, RFI_MSR, RFI_EXACT)(bool psr, bool nest)
+template <typename PT, typename GT>
+static adam_kernel_t pick(bool psr, bool nest)
 {
     constexpr bool A = RFI_APPLY != 0, M = RFI_MSR != 0, E = RFI_EXACT != 0;
     if constexpr (A) {
-        if (psr) return nest ? &k_adam8<A, M, true, true, E> : &k_adam8<A, M, true, false, E>;
+        if (psr) return nest ? &k_adam8<PT, GT, A, M, true, true, E> : &k_adam8<PT, GT, A, M, true, false, E>;
     }
-    return nest ? &k_adam8<A, M, false, true, E> : &k_adam8<A, M, false, false, E>;
+    return nest ? &k_adam8<PT, GT, A, M, false, true, E> : &k_adam8<PT, GT, A, M, false, false, E>;
+}
+
+// dtype_combo = 2*(param is bf16) + (grad is bf16)
+adam_kernel_t RF_PICK_NAME(RFI_APPLY, RFI_MSR, RFI_EXACT)(int dtype_combo, bool psr, bool nest)
+{
+    switch (dtype_combo) {
+        case 3: return pick<uint16_t, uint16_t>(psr, nest);
+        case 2: return pick<uint16_t, float>(psr, nest);
+        case 1: return pick<float, uint16_t>(psr, nest);
+        default: return pick<float, float>(psr, nest);
+    }
 }
 
 }  // namespace rf

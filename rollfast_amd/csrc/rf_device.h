@@ -39,13 +39,22 @@ constexpr int WAVES_PER_WG = WG / WAVE;
 constexpr int64_t FAST_BS = 2048;  // block size of the vectorised path
 constexpr int64_t CHUNK = 2048;    // elements per fallback (unquantized moment) work unit
 
+// Waves per SIMD the step kernel is register-allocated for (<= 512 / N VGPRs).
+#ifndef RF_STEP_WAVES_PER_EU
+#define RF_STEP_WAVES_PER_EU 4
+#endif
+
 enum : int32_t { KIND_QFAST = 0, KIND_QGEN = 1, KIND_FALLBACK = 2 };
 
 // Kernel-side scalars (derived from rf_adam8_hparams on the host).
 struct KHp {
     float b1, omb1, b2, omb2;
     float bc1, bc2, bc1n;
-    float rbc1, rbc2, rbc1n;  // f32 reciprocals for the default (non-exact) direction
+    // Default (non-exact) direction u = m / (k1 * sqrt(v + er2) + k2) with
+    // k1 = bc1 / sqrt(bc2), k2 = eps * bc1, er2 = eps_root * bc2: the same
+    // quantity as (m/bc1) / (sqrt(v/bc2 + eps_root) + eps), fewer roundings.
+    float k1, k2, er2;
+    float nb1, nomb1, rsbc2;  // nesterov: b1/bc1_next, (1-b1)/bc1, 1/sqrt(bc2)
     float eps, eps_root;
     float wd, wd16;           // f32(wd) and bf16(wd) as f32 (weak-typed decay of bf16 params)
     float neg_lr;             // f32(-lr), or 1.0 when the chain has no learning-rate scale
@@ -186,34 +195,34 @@ __device__ __forceinline__ float div_by_scale(float x, float s, float rs)
     return __builtin_fmaf(r, rs, q0);
 }
 
-// Signed dynamic codebook code of x in a block with scale s (fast path).
+// Signed dynamic codebook code of x in a block with scale s (fast path;
+// |x| <= s, so |n| <= 1).
 __device__ __forceinline__ uint32_t code_signed_fast(const uint8_t* lds, float x, float s, float rs)
 {
     const float n = div_by_scale(x, s, rs);
     const uint32_t nb = __float_as_uint(n);
-    const uint32_t neg = (uint32_t)((int32_t)nb >> 31);  // 0 or 0xFFFFFFFF
-    const uint32_t sd = neg & REGION;
-    const uint32_t cell = max((nb >> CELL_SHIFT) & 0xFFFFu, CELL_LO);
-    const uint32_t cand = lds[L_POS + REG_CAND - CELL_LO + sd + cell];
-    const float t = *(const float*)(lds + L_POS + REG_T + sd + cand * 4u);
-    const uint32_t c = cand + (fabsf(n) >= t ? 1u : 0u);
-    return (c ^ neg) + 127u - neg;  // n >= 0: 127 + c ; n < 0: 127 - c
+    const uint32_t idx = __builtin_elementwise_sub_sat((nb >> CELL_SHIFT) & 0xFFFFu, CELL_LO);
+    const uint32_t cand = lds[L_CANDS + __umul24(nb >> 31, NCELL_PAD) + idx];
+    const float t = *(const float*)(lds + L_TS + cand * 4u);
+    return cand + (n >= t ? 1u : 0u);
 }
 
 // Unsigned dynamic codebook code of x >= 0 in a block with scale s (fast path).
 __device__ __forceinline__ uint32_t code_unsigned_fast(const uint8_t* lds, float x, float s, float rs)
 {
     const float n = div_by_scale(x, s, rs);
-    const uint32_t nb = __float_as_uint(n) & 0x7FFFFFFFu;
-    const uint32_t cell = max(nb >> CELL_SHIFT, CELL_LO);
-    const uint32_t cand = lds[L_CANDU - CELL_LO + cell];
+    const uint32_t idx = __builtin_elementwise_sub_sat(__float_as_uint(n) >> CELL_SHIFT, CELL_LO);
+    const uint32_t cand = lds[L_CANDU + idx];
     const float t = *(const float*)(lds + L_TU + cand * 4u);
-    return cand + (__uint_as_float(nb) >= t ? 1u : 0u);
+    return cand + (n >= t ? 1u : 0u);
 }
 
-__device__ __forceinline__ bool scale_is_fast(float s)
+// Fast (table) requantization of a block: its absmax must be finite (a NaN
+// absmax yields scale 1 but leaves NaN or |n| > 1 elements, which only the
+// literal path handles) and the scale within the exact-division range.
+__device__ __forceinline__ bool block_is_fast(uint32_t amax_bits, float s)
 {
-    return s >= FAST_SCALE_MIN && s <= 3.4028234663852886e38f;
+    return amax_bits < 0x7F800000u && s >= FAST_SCALE_MIN;
 }
 
 // Block scale from the NaN-propagating absmax bit pattern (adam8.py:142,167):
@@ -244,17 +253,13 @@ __device__ __forceinline__ float adam_direction(const KHp& h, float m, float v, 
         const float den = sqrtf(vhat + h.eps_root) + h.eps;
         return mhat / den;
     } else {
-        float mhat;
+        const float sv = __builtin_amdgcn_sqrtf(v + h.er2);
         if constexpr (NEST) {
-            const float t1 = h.b1 * (m * h.rbc1n);
-            const float t2 = h.omb1 * (g * h.rbc1);
-            mhat = t1 + t2;
+            const float mhat = h.nb1 * m + h.nomb1 * g;
+            return mhat * __builtin_amdgcn_rcpf(__builtin_fmaf(sv, h.rsbc2, h.eps));
         } else {
-            mhat = m * h.rbc1;
+            return m * __builtin_amdgcn_rcpf(__builtin_fmaf(sv, h.k1, h.k2));
         }
-        const float vhat = v * h.rbc2;
-        const float den = __builtin_amdgcn_sqrtf(vhat + h.eps_root) + h.eps;
-        return mhat * __builtin_amdgcn_rcpf(den);
     }
 }
 
@@ -270,6 +275,20 @@ __device__ __forceinline__ float decay_and_scale(const KHp& h, float u, float p,
         u = u + wdp;
     }
     return h.neg_lr * u;  // neg_lr == 1.0 when the chain has no lr scale (exact identity)
+}
+
+// decay_and_scale over the 8 elements of a chunk with the mode fixed at
+// compile time (a Python-scalar wd times bf16 params: two products per
+// bf16 conversion instruction).
+template <int WDM>
+__device__ __forceinline__ void decay_and_scale8(const KHp& h, float (&u)[8], const float (&p)[8]);
+
+// True where a fused param update p + u nearly cancels (|p + u| < |u| / 4096):
+// only there can a few-ulp error in u move the rounded param by more than
+// one bf16 ulp.
+__device__ __forceinline__ bool cancels(float sum, float u)
+{
+    return fabsf(sum) * 4096.0f < fabsf(u);
 }
 
 // EMA moment updates (adam8.py:322-335).
@@ -345,6 +364,7 @@ __device__ __forceinline__ void store1(void* base, int32_t dtype, int64_t e, flo
 // Uniform per-unit context.
 struct UnitCtx {
     const uint8_t* lds;
+    float* wtab;  // this wave's 512-float LDS region (dequant-and-decay tables)
     int32_t wd_mode;
     bool fed;
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;  // per-leaf keys
@@ -374,6 +394,9 @@ __device__ __forceinline__ void update_one(const UnitCtx& c, const rf_adam8_leaf
     const bool need_p = APPLY || c.wd_mode != WD_OFF;
     const float p = need_p ? load1(L.param, L.param_dtype, e) : 0.0f;
     u = decay_and_scale(h, u, p, c.wd_mode);
+    if constexpr (APPLY && !EXACT) {
+        if (cancels(p + u, u)) u = decay_and_scale(h, adam_direction<NEST, true>(h, mm, vv, g), p, c.wd_mode);
+    }
     if constexpr (APPLY) {
         if (L.param_dtype == RF_BF16) {
             uint32_t rb = 0;
@@ -391,7 +414,7 @@ __device__ __forceinline__ void update_one(const UnitCtx& c, const rf_adam8_leaf
 // (or moment SR), recomputing the new moments from the old codes, which are
 // still in place.  Scales are not written here.
 template <bool MSR>
-__device__ __noinline__ void requant_literal(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
+__device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
                                              float sm, float sv, bool fast_m, bool fast_v)
 {
     const int lane = threadIdx.x & (WAVE - 1);
@@ -434,32 +457,148 @@ __device__ __noinline__ void requant_literal(const UnitCtx& c, const rf_adam8_le
 }
 
 // ================================================ work units: quantized ====
-// Full 2048-element block, vectorised (KIND_QFAST).
-template <typename PT, typename GT, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
+// Global-address-space views: loads and stores through them compile to
+// global_load/global_store (not flat), so they count only against vmcnt.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define RF_GLOBAL __attribute__((address_space(1)))
+#else
+#define RF_GLOBAL
+#endif
+
+template <typename T>
+__device__ __forceinline__ const RF_GLOBAL T* gload_ptr(const void* p, int64_t byte_off)
+{
+    return (const RF_GLOBAL T*)((const RF_GLOBAL uint8_t*)p + byte_off);
+}
+
+template <typename T>
+__device__ __forceinline__ RF_GLOBAL T* gstore_ptr(void* p, int64_t byte_off)
+{
+    return (RF_GLOBAL T*)((RF_GLOBAL uint8_t*)p + byte_off);
+}
+
+// 8 consecutive elements of a param/grad array in registers (16-byte words).
+template <typename T>
+struct Raw8 {
+    uint4 w[sizeof(T) == 2 ? 1 : 2];
+};
+
+template <typename T>
+__device__ __forceinline__ void raw8_load(Raw8<T>& r, const void* base, int64_t e0)
+{
+    const RF_GLOBAL uint4* p = gload_ptr<uint4>(base, e0 * (int64_t)sizeof(T));
+    r.w[0] = p[0];
+    if constexpr (sizeof(T) == 4) r.w[1] = p[1];
+}
+
+template <typename T>
+__device__ __forceinline__ void raw8_unpack(const Raw8<T>& r, float (&x)[8])
+{
+    if constexpr (sizeof(T) == 2) {
+        const uint32_t d[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = __uint_as_float(d[i] << 16);
+            x[2 * i + 1] = __uint_as_float(d[i] & 0xFFFF0000u);
+        }
+    } else {
+        const uint32_t d[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = __uint_as_float(d[i]);
+    }
+}
+
+// Two f32 -> bf16 (round to nearest even) in one v_cvt_pk_bf16_f32; the
+// result is the packed pair (lo, hi).
+typedef float rf_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 rf_bf2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((rf_f2){lo, hi}, rf_bf2));
+}
+
+template <int WDM>
+__device__ __forceinline__ void decay_and_scale8(const KHp& h, float (&u)[8], const float (&p)[8])
+{
+    if constexpr (WDM == WD_BF16) {
+#pragma unroll
+        for (int t = 0; t < 8; t += 2) {
+            const uint32_t w2 = pack_bf16x2_rne(h.wd16 * p[t], h.wd16 * p[t + 1]);
+            u[t] = u[t] + __uint_as_float(w2 << 16);
+            u[t + 1] = u[t + 1] + __uint_as_float(w2 & 0xFFFF0000u);
+        }
+    } else if constexpr (WDM == WD_F32) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float wdp = h.wd * p[t];
+            u[t] = u[t] + wdp;
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) u[t] = h.neg_lr * u[t];  // scale_by_learning_rate
+}
+
+// Full 2048-element block, vectorised (KIND_QFAST).  WDM (weight-decay mode)
+// is a template parameter so the per-element code has no branches.
+//
+// Per block the wave first tabulates, in its own LDS region, the decayed
+// dequantized value of every code: TM[k] = fl(b1 * fl(cb_s[k] * s_m)) and
+// TV[k] = fl(b2 * fl(cb_u[k] * s_v)) -- exactly the first product of each
+// EMA (adam8.py:200-203, :322-335) -- so an element costs one table read per
+// moment instead of a read and two multiplies.
+template <typename PT, typename GT, int WDM, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
 __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h)
 {
     constexpr int J = FAST_BS / 512;
+    constexpr bool NEED_P = APPLY || WDM != WD_OFF;
+    constexpr bool BF16P = std::is_same<PT, uint16_t>::value;
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t base = blk * FAST_BS;
-    const float* cbs = (const float*)(c.lds + L_CBS);
-    const float* cbu = (const float*)(c.lds + L_CBU);
     const float sm_old = L.mu_scales[blk];
     const float sv_old = L.nu_scales[blk];
-    const uint8_t* mcodes = (const uint8_t*)L.mu;
-    const uint8_t* vcodes = (const uint8_t*)L.nu;
-    const bool need_p = APPLY || c.wd_mode != WD_OFF;
+
+    // Chunk j+1's loads are issued before chunk j's arithmetic: two chunks
+    // (6 KB for bf16) in flight per wave without holding all four.
+    uint2 mc[2], vc[2];
+    Raw8<GT> graw[2];
+    Raw8<PT> praw[2];
+    auto issue = [&](int j, int slot) {
+        const int64_t e0 = base + j * 512 + lane * 8;
+        mc[slot] = *gload_ptr<uint2>(L.mu, e0);
+        vc[slot] = *gload_ptr<uint2>(L.nu, e0);
+        raw8_load<GT>(graw[slot], L.grad, e0);
+        if constexpr (NEED_P) raw8_load<PT>(praw[slot], L.param, e0);
+    };
+    issue(0, 0);
+
+    {
+        const float* cbs = (const float*)(c.lds + L_CBS);
+        const float* cbu = (const float*)(c.lds + L_CBU);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int k = lane + 64 * r;
+            c.wtab[k] = h.b1 * (cbs[k] * sm_old);
+            c.wtab[256 + k] = h.b2 * (cbu[k] * sv_old);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    const float* TM = c.wtab;
+    const float* TV = c.wtab + 256;
 
     float m[J][8], v[J][8];
     uint32_t am = 0, av = 0;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int64_t e0 = base + j * 512 + lane * 8;
-        const uint2 mc = *(const uint2*)(mcodes + e0);
-        const uint2 vc = *(const uint2*)(vcodes + e0);
+        const int slot = j & 1;
+        if (j + 1 < J) issue(j + 1, slot ^ 1);
         float g[8], p[8];
-        load8<GT>(L.grad, e0, g);
-        if (need_p) {
-            load8<PT>(L.param, e0, p);
+        raw8_unpack<GT>(graw[slot], g);
+        if constexpr (NEED_P) {
+            raw8_unpack<PT>(praw[slot], p);
         } else {
 #pragma unroll
             for (int t = 0; t < 8; ++t) p[t] = 0.0f;
@@ -473,36 +612,65 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                 for (int t = 0; t < 8; ++t) rb[t] = jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
             }
         }
-        float uo[8];
-        uint32_t po[8];
+        float u[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const uint32_t cm = ((t < 4 ? mc.x : mc.y) >> (8 * (t & 3))) & 0xFFu;
-            const uint32_t cv = ((t < 4 ? vc.x : vc.y) >> (8 * (t & 3))) & 0xFFu;
-            const float mp = cbs[cm] * sm_old;  // adam8.py:200-203
-            const float vp = cbu[cv] * sv_old;
-            float mm, vv;
-            ema(h, mp, vp, g[t], mm, vv);
+            const uint32_t cm = ((t < 4 ? mc[slot].x : mc[slot].y) >> (8 * (t & 3))) & 0xFFu;
+            const uint32_t cv = ((t < 4 ? vc[slot].x : vc[slot].y) >> (8 * (t & 3))) & 0xFFu;
+            const float t2 = h.omb1 * g[t];
+            const float mm = TM[cm] + t2;
+            const float gg = g[t] * g[t];
+            const float t4 = h.omb2 * gg;
+            const float vv = TV[cv] + t4;
             m[j][t] = mm;
             v[j][t] = vv;
             am = max(am, __float_as_uint(mm) & 0x7FFFFFFFu);  // NaN bits sort above Inf
             av = max(av, __float_as_uint(vv));                 // v >= 0
-            float u = adam_direction<NEST, EXACT>(h, mm, vv, g[t]);
-            u = decay_and_scale(h, u, p[t], c.wd_mode);
-            if constexpr (APPLY) po[t] = new_param_bits<PSR, PT>(p[t], u, rb[t]);
-            else uo[t] = u;
+            u[t] = adam_direction<NEST, EXACT>(h, mm, vv, g[t]);
         }
+        decay_and_scale8<WDM>(h, u, p);
         if constexpr (APPLY) {
-            if constexpr (std::is_same<PT, uint16_t>::value) {
-                store8_bf16(L.param, e0, po);
-            } else {
-                float pf[8];
+            float sum[8];
 #pragma unroll
-                for (int t = 0; t < 8; ++t) pf[t] = __uint_as_float(po[t]);
-                store8_f32(L.param, e0, pf);
+            for (int t = 0; t < 8; ++t) sum[t] = p[t] + u[t];
+            if constexpr (!EXACT) {
+                // Hardware rcp/sqrt leave u a few f32 ulps from the IEEE
+                // value; that moves the rounded param by more than one
+                // bf16 ulp only where p + u nearly cancels.  Such chunks
+                // (rare) are recomputed with IEEE arithmetic.
+                bool risky = false;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) risky |= cancels(sum[t], u[t]);
+                if (__builtin_amdgcn_ballot_w64(risky) != 0) {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        if (cancels(sum[t], u[t])) {
+                            float ue = adam_direction<NEST, true>(h, m[j][t], v[j][t], g[t]);
+                            ue = decay_and_scale(h, ue, p[t], WDM);
+                            sum[t] = p[t] + ue;
+                        }
+                    }
+                }
+            }
+            if constexpr (BF16P) {
+                uint32_t w[4];
+                if constexpr (PSR) {
+#pragma unroll
+                    for (int t = 0; t < 8; t += 2) w[t / 2] = sr_bf16(sum[t], rb[t]) | (sr_bf16(sum[t + 1], rb[t + 1]) << 16);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; t += 2) w[t / 2] = pack_bf16x2_rne(sum[t], sum[t + 1]);
+                }
+                *gstore_ptr<uint4>(L.param, e0 * 2) = make_uint4(w[0], w[1], w[2], w[3]);
+            } else {
+                RF_GLOBAL float4* q = gstore_ptr<float4>(L.param, e0 * 4);
+                q[0] = make_float4(sum[0], sum[1], sum[2], sum[3]);
+                q[1] = make_float4(sum[4], sum[5], sum[6], sum[7]);
             }
         } else {
-            store8_f32(L.updates, e0, uo);
+            RF_GLOBAL float4* q = gstore_ptr<float4>(L.updates, e0 * 4);
+            q[0] = make_float4(u[0], u[1], u[2], u[3]);
+            q[1] = make_float4(u[4], u[5], u[6], u[7]);
         }
     }
 
@@ -511,13 +679,11 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     av = wave_max_u32(av);
     const float sm = scale_from_absmax_bits(am);
     const float sv = scale_from_absmax_bits(av);
-    const bool fast_m = !MSR && scale_is_fast(sm);
-    const bool fast_v = !MSR && scale_is_fast(sv);
+    const bool fast_m = !MSR && block_is_fast(am, sm);
+    const bool fast_v = !MSR && block_is_fast(av, sv);
     if (!MSR && fast_m && fast_v) {
         const float rsm = 1.0f / sm;
         const float rsv = 1.0f / sv;
-        uint8_t* mout = (uint8_t*)L.mu;
-        uint8_t* vout = (uint8_t*)L.nu;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const int64_t e0 = base + j * 512 + lane * 8;
@@ -532,8 +698,8 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             wm.y = cm[4] | (cm[5] << 8) | (cm[6] << 16) | (cm[7] << 24);
             wv.x = cv[0] | (cv[1] << 8) | (cv[2] << 16) | (cv[3] << 24);
             wv.y = cv[4] | (cv[5] << 8) | (cv[6] << 16) | (cv[7] << 24);
-            *(uint2*)(mout + e0) = wm;
-            *(uint2*)(vout + e0) = wv;
+            *gstore_ptr<uint2>(L.mu, e0) = wm;
+            *gstore_ptr<uint2>(L.nu, e0) = wv;
         }
     } else {
         // Rare (tiny, Inf or NaN scales) or moment SR: recompute from the old
@@ -546,12 +712,28 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     }
 }
 
+// The vectorised block: the weight-decay mode is resolved once per unit into
+// a branch-free instance.
+template <typename PT, typename GT, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
+__device__ __forceinline__ void dispatch_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t idx, const KHp& h)
+{
+    const int32_t wdm = c.wd_mode;
+    if constexpr (std::is_same<PT, uint16_t>::value) {
+        if (wdm == WD_BF16) {
+            unit_qfast<PT, GT, WD_BF16, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
+            return;
+        }
+    }
+    if (wdm != WD_OFF) unit_qfast<PT, GT, WD_F32, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
+    else unit_qfast<PT, GT, WD_OFF, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
+}
+
 // Any block size, partial or unaligned blocks (KIND_QGEN).  The first pass
 // finds the new absmax, the second recomputes the moments and writes the
 // params/updates, then the codes are requantized from the old codes (still
 // in place).  Elements past `size` are the reference's zero padding.
 template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
-__device__ __noinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h)
+__device__ __forceinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h)
 {
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t bs = L.block_size;
@@ -578,8 +760,8 @@ __device__ __noinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf& L,
     av = wave_max_u32(av);
     const float sm = scale_from_absmax_bits(am);
     const float sv = scale_from_absmax_bits(av);
-    const bool fast_m = !MSR && scale_is_fast(sm);
-    const bool fast_v = !MSR && scale_is_fast(sv);
+    const bool fast_m = !MSR && block_is_fast(am, sm);
+    const bool fast_v = !MSR && block_is_fast(av, sv);
     requant_literal<MSR>(c, L, blk, h, sm, sv, fast_m, fast_v);
     if (lane == 0) {
         L.mu_scales[blk] = sm;
@@ -591,7 +773,7 @@ __device__ __noinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf& L,
 // Moments stored unquantized (adam8.py:620-630: size < min_size, a
 // non-inexact dtype or quantize=False): elementwise update of a chunk.
 template <bool APPLY, bool PSR, bool NEST, bool EXACT>
-__device__ __noinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_leaf& L, int64_t chunk, const KHp& h)
+__device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_leaf& L, int64_t chunk, const KHp& h)
 {
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t base = chunk * CHUNK;
@@ -608,20 +790,25 @@ __device__ __noinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_leaf
 }
 
 // ======================================================== step kernel ====
-template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
-__global__ __launch_bounds__(WG) void k_adam8(const rf_adam8_leaf* __restrict__ leaves,
+// One launch covers the leaves whose (param, grad) dtypes are (PT, GT)
+// (uint16_t = bf16, float = f32); the plan groups the work list by dtype.
+template <typename PT, typename GT, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVES_PER_EU))) void k_adam8(const rf_adam8_leaf* __restrict__ leaves,
                                               const Seg* __restrict__ segs, int64_t total_units, KHp h,
                                               const uint4* __restrict__ tables)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
+    __shared__ __attribute__((aligned(16))) float wtab[WAVES_PER_WG][512];
     stage_tables(lds, tables);
 
-    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const uint32_t wave_in_wg = uniform_u32(threadIdx.x / WAVE);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + wave_in_wg;
     const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
     int32_t s = 0;
     int32_t cur_leaf = -1;
     UnitCtx c;
     c.lds = lds;
+    c.wtab = wtab[wave_in_wg];
     c.fed = (h.flags & RF_FED_BITS) != 0;
     c.wd_mode = WD_OFF;
     c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;
@@ -643,14 +830,7 @@ __global__ __launch_bounds__(WG) void k_adam8(const rf_adam8_leaf* __restrict__ 
         }
         const int64_t idx = sg.first + (u - sg.unit_start);
         if (sg.kind == KIND_QFAST) {
-            const int32_t pd = L.param_dtype, gd = L.grad_dtype;
-            if (pd == RF_BF16) {
-                if (gd == RF_BF16) unit_qfast<uint16_t, uint16_t, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
-                else unit_qfast<uint16_t, float, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
-            } else {
-                if (gd == RF_BF16) unit_qfast<float, uint16_t, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
-                else unit_qfast<float, float, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
-            }
+            dispatch_qfast<PT, GT, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
         } else if (sg.kind == KIND_QGEN) {
             unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
         } else {

@@ -38,14 +38,14 @@ rf_status fail(rf_status code, const std::string& msg)
 
 // Instances of the step kernel (rf_adam8_inst.hip, one object per variant).
 namespace rf {
-adam_kernel_t rf_pick_adam8_a0_m0_e0(bool psr, bool nest);
-adam_kernel_t rf_pick_adam8_a0_m0_e1(bool psr, bool nest);
-adam_kernel_t rf_pick_adam8_a0_m1_e0(bool psr, bool nest);
-adam_kernel_t rf_pick_adam8_a0_m1_e1(bool psr, bool nest);
-adam_kernel_t rf_pick_adam8_a1_m0_e0(bool psr, bool nest);
-adam_kernel_t rf_pick_adam8_a1_m0_e1(bool psr, bool nest);
-adam_kernel_t rf_pick_adam8_a1_m1_e0(bool psr, bool nest);
-adam_kernel_t rf_pick_adam8_a1_m1_e1(bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a0_m0_e0(int dtype_combo, bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a0_m0_e1(int dtype_combo, bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a0_m1_e0(int dtype_combo, bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a0_m1_e1(int dtype_combo, bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a1_m0_e0(int dtype_combo, bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a1_m0_e1(int dtype_combo, bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a1_m1_e0(int dtype_combo, bool psr, bool nest);
+adam_kernel_t rf_pick_adam8_a1_m1_e1(int dtype_combo, bool psr, bool nest);
 }  // namespace rf
 
 // ====================================================== standalone kernels ==
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const float*
         if (quantizer == RF_Q_SYMMETRIC_INT8) scale = amax > 0.0f ? amax / 127.0f : 1.0f;
         else scale = amax > 0.0f ? amax : 1.0f;
         if (lane == 0) scales[b] = scale;
-        const bool fast = !sr && quantizer != RF_Q_SYMMETRIC_INT8 && scale_is_fast(scale);
+        const bool fast = !sr && quantizer != RF_Q_SYMMETRIC_INT8 && block_is_fast(am, scale);
         const float rs = 1.0f / scale;
         auto code_of = [&](float xv, int64_t e) -> uint32_t {
             if (quantizer == RF_Q_SYMMETRIC_INT8) {
@@ -299,10 +299,10 @@ float upper_threshold(float lo, float hi)
     return unkey(a);
 }
 
-inline uint32_t count_le(const float* t, int n, float a)
+inline uint32_t count_le(const float* t, float a)
 {
     uint32_t c = 0;
-    for (int i = 0; i < n; ++i) c += (t[i] <= a) ? 1u : 0u;
+    for (int i = 0; i < 256; ++i) c += (t[i] <= a) ? 1u : 0u;
     return c;
 }
 
@@ -311,20 +311,23 @@ struct HostTables {
     std::string error;
 };
 
-bool fill_cells(const float* thr, int nthr, uint8_t* cand, std::string& err)
+// Candidate of each magnitude cell for one sign: the number of thresholds at
+// or below the cell's low end in value space; a cell may hold at most one
+// threshold.  CELL_LO also stands for every magnitude below it.
+bool fill_cells(const float* thr, bool negative, uint8_t* cand, std::string& err)
 {
     for (uint32_t cell = CELL_LO; cell <= CELL_HI; ++cell) {
-        const float lo = bitsf(cell << CELL_SHIFT);
-        const float hi = bitsf((cell << CELL_SHIFT) | ((1u << CELL_SHIFT) - 1u));
-        const uint32_t c0 = count_le(thr, nthr, lo);
-        const uint32_t c1 = count_le(thr, nthr, hi);
-        if (c1 > c0 + 1u || (cell == CELL_LO && c0 != 0u)) {
+        const float mlo = cell == CELL_LO ? 0.0f : bitsf(cell << CELL_SHIFT);
+        const float mhi = bitsf((cell << CELL_SHIFT) | ((1u << CELL_SHIFT) - 1u));
+        const float lo = negative ? -mhi : mlo;
+        const float hi = negative ? -mlo : mhi;
+        const uint32_t c0 = count_le(thr, lo);
+        const uint32_t c1 = count_le(thr, hi);
+        if (c1 > c0 + 1u) {
             err = "lookup cell " + std::to_string(cell) + " holds more than one threshold";
             return false;
         }
-        // The kernel compares a >= T[cand]; the threshold inside the cell (if
-        // any) is T[c0] because T is ascending and T[c0] > lo.
-        if (c0 < (uint32_t)nthr && thr[c0] <= lo) {
+        if (c0 > 255u || thr[c0] <= lo) {
             err = "threshold table is not ascending";
             return false;
         }
@@ -349,29 +352,19 @@ HostTables build_tables()
             return ht;
         }
     }
-    const float inf = INFINITY;
-    // Unsigned: thresholds t_0..t_254 between cbu[i] and cbu[i+1].
-    float tu[256];
-    for (int i = 0; i < 255; ++i) tu[i] = upper_threshold(cbu[i], cbu[i + 1]);
-    tu[255] = inf;
-    // Signed, n >= 0: pairs (cbs[127+k], cbs[128+k]), k = 0..127.
-    float tp[256];
-    for (int k = 0; k < 128; ++k) tp[k] = upper_threshold(cbs[127 + k], cbs[128 + k]);
-    for (int k = 128; k < 256; ++k) tp[k] = inf;
-    // Signed, n < 0: pair i = 126-k is (cbs[i], cbs[i+1]); in magnitude the
-    // larger code wins for a > |t_i|, i.e. a >= nextafter(|t_i|, inf).
-    float tn[256];
-    for (int k = 0; k < 127; ++k) {
-        const float t = upper_threshold(cbs[126 - k], cbs[127 - k]);
-        tn[k] = std::nextafter(std::fabs(t), inf);
+    // Value-space thresholds t_i between cb[i] and cb[i+1]; t[255] = +inf.
+    float ts[256], tu[256];
+    for (int i = 0; i < 255; ++i) {
+        ts[i] = upper_threshold(cbs[i], cbs[i + 1]);
+        tu[i] = upper_threshold(cbu[i], cbu[i + 1]);
     }
-    for (int k = 127; k < 256; ++k) tn[k] = inf;
+    ts[255] = INFINITY;
+    tu[255] = INFINITY;
+    std::memcpy(b + L_TS, ts, 1024);
     std::memcpy(b + L_TU, tu, 1024);
-    std::memcpy(b + L_POS + REG_T, tp, 1024);
-    std::memcpy(b + L_NEG + REG_T, tn, 1024);
-    if (!fill_cells(tu, 255, b + L_CANDU, ht.error)) return ht;
-    if (!fill_cells(tp, 128, b + L_POS + REG_CAND, ht.error)) return ht;
-    if (!fill_cells(tn, 127, b + L_NEG + REG_CAND, ht.error)) return ht;
+    if (!fill_cells(ts, false, b + L_CANDS, ht.error)) return ht;
+    if (!fill_cells(ts, true, b + L_CANDS + NCELL_PAD, ht.error)) return ht;
+    if (!fill_cells(tu, false, b + L_CANDU, ht.error)) return ht;
     return ht;
 }
 
@@ -381,30 +374,28 @@ const HostTables& host_tables()
     return t;
 }
 
-// Host emulation of code_signed_fast / code_unsigned_fast on a normalised n.
+// Host emulation of the kernels' table lookup on a normalised n (NaN and the
+// clip to [cb[0], cb[255]] as in the literal path).
 uint32_t host_table_code(const uint8_t* tb, int32_t quantizer, float n)
 {
-    const float* cb = (const float*)(tb + (quantizer == RF_Q_DYNAMIC_UNSIGNED ? L_CBU : L_CBS));
+    const bool uns = quantizer == RF_Q_DYNAMIC_UNSIGNED;
+    const float* cb = (const float*)(tb + (uns ? L_CBU : L_CBS));
     if (n != n) return 254u;
     n = n < cb[0] ? cb[0] : n;
     n = n > cb[255] ? cb[255] : n;
     const uint32_t nb = fbits(n);
-    if (quantizer == RF_Q_DYNAMIC_UNSIGNED) {
-        const uint32_t mag = nb & 0x7FFFFFFFu;
-        const uint32_t cell = std::max(mag >> CELL_SHIFT, CELL_LO);
-        const uint32_t cand = tb[L_CANDU - CELL_LO + cell];
-        float t;
-        std::memcpy(&t, tb + L_TU + cand * 4u, 4);
-        return cand + (bitsf(mag) >= t ? 1u : 0u);
-    }
-    const uint32_t neg = (nb & 0x80000000u) ? 0xFFFFFFFFu : 0u;
-    const uint32_t sd = neg & REGION;
-    const uint32_t cell = std::max((nb >> CELL_SHIFT) & 0xFFFFu, CELL_LO);
-    const uint32_t cand = tb[L_POS + REG_CAND - CELL_LO + sd + cell];
+    const uint32_t cell = (nb >> CELL_SHIFT) & 0xFFFFu;
+    const uint32_t idx = cell > CELL_LO ? cell - CELL_LO : 0u;
+    uint32_t cand;
     float t;
-    std::memcpy(&t, tb + L_POS + REG_T + sd + cand * 4u, 4);
-    const uint32_t c = cand + (std::fabs(n) >= t ? 1u : 0u);
-    return ((c ^ neg) + 127u - neg) & 0xFFu;
+    if (uns) {
+        cand = tb[L_CANDU + idx];
+        std::memcpy(&t, tb + L_TU + cand * 4u, 4);
+    } else {
+        cand = tb[L_CANDS + (nb >> 31) * NCELL_PAD + idx];
+        std::memcpy(&t, tb + L_TS + cand * 4u, 4);
+    }
+    return cand + (n >= t ? 1u : 0u);
 }
 
 // ---- per-device state ----
@@ -439,14 +430,20 @@ rf_status device_state(DevState** out)
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
 // ---- kernel selection ----
-adam_kernel_t pick_adam_kernel(bool apply, bool msr, bool psr, bool nest, bool exact)
+// dtype_combo = 2*(param is bf16) + (grad is bf16)
+adam_kernel_t pick_adam_kernel(bool apply, bool msr, bool psr, bool nest, bool exact, int combo)
 {
     if (apply) {
-        if (msr) return exact ? rf_pick_adam8_a1_m1_e1(psr, nest) : rf_pick_adam8_a1_m1_e0(psr, nest);
-        return exact ? rf_pick_adam8_a1_m0_e1(psr, nest) : rf_pick_adam8_a1_m0_e0(psr, nest);
+        if (msr) return exact ? rf_pick_adam8_a1_m1_e1(combo, psr, nest) : rf_pick_adam8_a1_m1_e0(combo, psr, nest);
+        return exact ? rf_pick_adam8_a1_m0_e1(combo, psr, nest) : rf_pick_adam8_a1_m0_e0(combo, psr, nest);
     }
-    if (msr) return exact ? rf_pick_adam8_a0_m1_e1(false, nest) : rf_pick_adam8_a0_m1_e0(false, nest);
-    return exact ? rf_pick_adam8_a0_m0_e1(false, nest) : rf_pick_adam8_a0_m0_e0(false, nest);
+    if (msr) return exact ? rf_pick_adam8_a0_m1_e1(combo, false, nest) : rf_pick_adam8_a0_m1_e0(combo, false, nest);
+    return exact ? rf_pick_adam8_a0_m0_e1(combo, false, nest) : rf_pick_adam8_a0_m0_e0(combo, false, nest);
+}
+
+inline int dtype_combo(const rf_adam8_leaf& L)
+{
+    return 2 * (L.param_dtype == RF_BF16 ? 1 : 0) + (L.grad_dtype == RF_BF16 ? 1 : 0);
 }
 
 struct OccKey {
@@ -494,12 +491,21 @@ struct RingSlot {
     bool pending = false;
 };
 
+// One launch per (param, grad) dtype combination present in the tree; each
+// group has its own work list (ending in a sentinel) inside d_segs.
+struct PlanGroup {
+    int combo;
+    int64_t seg_offset;
+    int64_t units;
+};
+
 struct rf_adam8_plan {
     int device = 0;
     int32_t apply = 1;
     int32_t n_leaves = 0;
     int64_t total_units = 0;
     int64_t n_segs = 0;
+    std::vector<PlanGroup> groups;
     rf_adam8_leaf* d_leaves = nullptr;  // creation-time pointer table
     Seg* d_segs = nullptr;
     std::vector<rf_adam8_leaf> shape;   // creation-time table: the structure runs must match
@@ -585,17 +591,17 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     DevState* ds = nullptr;
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
-    std::vector<Seg> segs;
-    int64_t units = 0;
-    auto add = [&](int32_t leaf, int32_t kind, int64_t first, int64_t count) {
+    std::vector<Seg> gsegs[4];
+    int64_t gunits[4] = {0, 0, 0, 0};
+    auto add = [&](int32_t leaf, int combo, int32_t kind, int64_t first, int64_t count) {
         if (count <= 0) return;
-        Seg s{};
-        s.unit_start = units;
-        s.first = first;
-        s.leaf = leaf;
-        s.kind = kind;
-        segs.push_back(s);
-        units += count;
+        Seg sg{};
+        sg.unit_start = gunits[combo];
+        sg.first = first;
+        sg.leaf = leaf;
+        sg.kind = kind;
+        gsegs[combo].push_back(sg);
+        gunits[combo] += count;
     };
     bool any_pb = false, any_mb = false;
     std::vector<uint8_t> vecs;
@@ -607,32 +613,49 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
         any_mb |= (L.mu_bits != nullptr) || (L.nu_bits != nullptr);
         const bool vec = leaf_vec_ok(L, apply);
         vecs.push_back(vec ? 1 : 0);
+        const int combo = dtype_combo(L);
         if (L.moment_kind == RF_MOMENT_QUANTIZED) {
             const int64_t bs = L.block_size;
             const int64_t nb = nblocks_of(L.size, bs);
             if (bs == FAST_BS && vec) {
                 const int64_t nfull = L.size / bs;
-                add(i, KIND_QFAST, 0, nfull);
-                add(i, KIND_QGEN, nfull, nb - nfull);
+                add(i, combo, KIND_QFAST, 0, nfull);
+                add(i, combo, KIND_QGEN, nfull, nb - nfull);
             } else {
-                add(i, KIND_QGEN, 0, nb);
+                add(i, combo, KIND_QGEN, 0, nb);
             }
         } else {
-            add(i, KIND_FALLBACK, 0, (L.size + CHUNK - 1) / CHUNK);
+            add(i, combo, KIND_FALLBACK, 0, (L.size + CHUNK - 1) / CHUNK);
         }
     }
-    Seg sentinel{};
-    sentinel.unit_start = units;
-    sentinel.leaf = -1;
-    sentinel.kind = -1;
-    segs.push_back(sentinel);
+    std::vector<Seg> segs;
+    std::vector<PlanGroup> groups;
+    int64_t units = 0;
+    for (int combo = 3; combo >= 0; --combo) {
+        if (gunits[combo] == 0) continue;
+        groups.push_back({combo, (int64_t)segs.size(), gunits[combo]});
+        segs.insert(segs.end(), gsegs[combo].begin(), gsegs[combo].end());
+        Seg sentinel{};
+        sentinel.unit_start = gunits[combo];
+        sentinel.leaf = -1;
+        sentinel.kind = -1;
+        segs.push_back(sentinel);
+        units += gunits[combo];
+    }
+    if (segs.empty()) {
+        Seg sentinel{};
+        sentinel.leaf = -1;
+        sentinel.kind = -1;
+        segs.push_back(sentinel);
+    }
 
     rf_adam8_plan* p = new rf_adam8_plan();
     HIP_TRY(hipGetDevice(&p->device));
     p->apply = apply ? 1 : 0;
     p->n_leaves = n_leaves;
     p->total_units = units;
-    p->n_segs = (int64_t)segs.size() - 1;
+    p->n_segs = (int64_t)segs.size();
+    p->groups = groups;
     p->any_param_bits = any_pb;
     p->any_moment_bits = any_mb;
     p->shape.assign(leaves, leaves + n_leaves);
@@ -655,7 +678,7 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
 rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64_t* leaves, int64_t* units)
 {
     if (!plan) return fail(RF_ERR_INVALID, "null plan");
-    if (launches) *launches = plan->total_units > 0 ? 1 : 0;
+    if (launches) *launches = (int64_t)plan->groups.size();
     if (leaves) *leaves = plan->n_leaves;
     if (units) *units = plan->total_units;
     return RF_OK;
@@ -686,9 +709,15 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
     k.bc1 = hp->bc1;
     k.bc2 = hp->bc2;
     k.bc1n = hp->bc1_next;
-    k.rbc1 = 1.0f / hp->bc1;
-    k.rbc2 = 1.0f / hp->bc2;
-    k.rbc1n = 1.0f / hp->bc1_next;
+    {
+        const double bc1 = hp->bc1, bc2 = hp->bc2, bc1n = hp->bc1_next;
+        k.k1 = (float)(bc1 / std::sqrt(bc2));
+        k.k2 = (float)((double)hp->eps * bc1);
+        k.er2 = (float)((double)hp->eps_root * bc2);
+        k.nb1 = (float)((double)hp->b1 / bc1n);
+        k.nomb1 = (float)((double)hp->one_minus_b1 / bc1);
+        k.rsbc2 = (float)(1.0 / std::sqrt(bc2));
+    }
     k.eps = hp->eps;
     k.eps_root = hp->eps_root;
     k.wd = hp->weight_decay;
@@ -708,15 +737,19 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
     k.kp0 = hp->key_param[0];
     k.kp1 = hp->key_param[1];
 
-    adam_kernel_t fn = pick_adam_kernel(plan->apply != 0, msr, psr, (f & RF_NESTEROV) != 0, (f & RF_EXACT) != 0);
-    int occ = 1;
-    st = occupancy((const void*)fn, &occ);
-    if (st != RF_OK) return st;
-    const int64_t wg_needed = (plan->total_units + WAVES_PER_WG - 1) / WAVES_PER_WG;
-    const int64_t wg_resident = (int64_t)ds->num_cus * occ;
-    const int grid = (int)std::max<int64_t>(1, std::min(wg_needed, wg_resident));
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(WG), 0, (hipStream_t)stream, d_leaves, plan->d_segs,
-                       plan->total_units, k, ds->tables);
+    for (const PlanGroup& g : plan->groups) {
+        adam_kernel_t fn =
+            pick_adam_kernel(plan->apply != 0, msr, psr, (f & RF_NESTEROV) != 0, (f & RF_EXACT) != 0, g.combo);
+        int occ = 1;
+        st = occupancy((const void*)fn, &occ);
+        if (st != RF_OK) return st;
+        const int64_t wg_needed = (g.units + WAVES_PER_WG - 1) / WAVES_PER_WG;
+        const int64_t wg_resident = (int64_t)ds->num_cus * occ;
+        const int grid = (int)std::max<int64_t>(1, std::min(wg_needed, wg_resident));
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(WG), 0, (hipStream_t)stream, d_leaves, plan->d_segs + g.seg_offset,
+                           g.units, k, ds->tables);
+        HIP_TRY(hipGetLastError());
+    }
     HIP_TRY(hipGetLastError());
     return RF_OK;
 }

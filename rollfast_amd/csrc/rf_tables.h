@@ -7,28 +7,27 @@
 // the upper code iff fl(|cb[ui] - n|) < fl(|n - cb[li]|)
 // (rollfast optim/adam8.py:542-569).  Inside each interval (cb[i], cb[i+1]]
 // that choice is monotone in n, so there is a smallest f32 t_i from which the
-// upper code wins, and code(n) = #{ i : n >= t_i }.  The kernels therefore
+// upper code wins, and code(n) = #{ i : n >= t_i } (values below cb[0] count
+// zero thresholds, which is the reference's clip to code 0).  The kernels
 // count thresholds instead of searching the codebook:
 //
-//   magnitude a = |n|; cell = bits(a) >> 15 (exponent + 8 mantissa bits)
-//   cand = CAND[cell]        (thresholds strictly below the cell start)
-//   count = cand + (a >= T[cand])
+//   cell = (bits(n) >> 15) & 0xFFFF   (|n|: exponent + 8 mantissa bits)
+//   cand = CAND[sign(n)][cell]        (thresholds <= the cell's low end)
+//   code = cand + (n >= T[cand])      (T ascending, value space, T[255] = inf)
 //
 // The cells are narrow enough (relative width <= 2^-8, while consecutive
 // thresholds are >= 0.53 % apart) that each holds at most one threshold; the
-// builder checks this and refuses to produce tables otherwise.  The signed
-// codebook uses separate positive-side and negative-side tables because
-// exact ties go to the lower index, which is the smaller magnitude for n > 0
-// and the larger magnitude for n < 0.
+// builder checks this and refuses to produce tables otherwise.  Cells below
+// CELL_LO all map to CELL_LO (no threshold lies below 2^-23 in magnitude).
 //
 // Byte layout (identical in global memory and in LDS):
-//   [L_CBS]   f32 cb_signed[256]
-//   [L_CBU]   f32 cb_unsigned[256]
-//   [L_TU]    f32 unsigned thresholds[256]        (+inf padded)
-//   [L_POS]   f32 signed n>=0 thresholds[256]     (+inf padded)
-//             u8  signed n>=0 candidates[NCELL_PAD]
-//   [L_NEG]   same for n<0 (L_NEG = L_POS + REGION)
-//   [L_CANDU] u8  unsigned candidates[NCELL_PAD]
+//   [L_CBS]      f32 cb_signed[256]
+//   [L_CBU]      f32 cb_unsigned[256]
+//   [L_TS]       f32 signed thresholds T[256]     (value space, +inf padded)
+//   [L_TU]       f32 unsigned thresholds T[256]
+//   [L_CANDS]    u8  signed candidates, n >= 0    [NCELL_PAD]
+//   [L_CANDS + NCELL_PAD]  signed candidates, n < 0
+//   [L_CANDU]    u8  unsigned candidates          [NCELL_PAD]
 #pragma once
 #include <stdint.h>
 
@@ -42,16 +41,12 @@ constexpr uint32_t NCELL_PAD = (NCELL + 15u) & ~15u;
 
 constexpr uint32_t L_CBS = 0;
 constexpr uint32_t L_CBU = 1024;
-constexpr uint32_t L_TU = 2048;
-constexpr uint32_t L_POS = 3072;
-constexpr uint32_t REG_T = 0;
-constexpr uint32_t REG_CAND = 1024;
-constexpr uint32_t REGION = 1024 + NCELL_PAD;
-constexpr uint32_t L_NEG = L_POS + REGION;
-constexpr uint32_t L_CANDU = L_NEG + REGION;
+constexpr uint32_t L_TS = 2048;
+constexpr uint32_t L_TU = 3072;
+constexpr uint32_t L_CANDS = 4096;
+constexpr uint32_t L_CANDU = L_CANDS + 2 * NCELL_PAD;
 constexpr uint32_t TABLE_BYTES = L_CANDU + NCELL_PAD;
 static_assert(TABLE_BYTES % 16 == 0, "tables are copied in 16-byte words");
-static_assert(REGION % 16 == 0, "regions stay 16-byte aligned");
 
 // Fast requantization is exact when the block scale s satisfies
 // FAST_SCALE_MIN <= s < inf: the reciprocal-and-correct division

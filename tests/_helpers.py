@@ -58,11 +58,16 @@ def bf16_ulp_distance(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
     return np.abs(key(a_bits) - key(b_bits))
 
 
-def f32_within_bf16_ulp(a: np.ndarray, b: np.ndarray) -> np.ndarray:
-    """|a - b| <= one bf16 ulp of the larger magnitude (f32 params)."""
+def f32_within_bf16_ulp(a: np.ndarray, b: np.ndarray, before: np.ndarray | None = None) -> np.ndarray:
+    """|a - b| <= one bf16 ulp of the largest magnitude among the two results
+    and the param before the step (f32 params): when an update cancels the
+    param, the new value is tiny but the step's rounding error scales with
+    the operands."""
     a = a.astype(np.float64)
     b = b.astype(np.float64)
     m = np.maximum(np.abs(a), np.abs(b))
+    if before is not None:
+        m = np.maximum(m, np.abs(before.astype(np.float64)))
     e = np.floor(np.log2(np.where(m > 0, m, 1.0)))
     ulp = np.exp2(e - 7)
     return np.abs(a - b) <= ulp

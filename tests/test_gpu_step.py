@@ -113,7 +113,7 @@ def _compare_state(spec, tree, state_adam, what):
             np.testing.assert_array_equal(a, b, err_msg=f"{what} leaf {i} fallback nu")
 
 
-def _compare_params(spec, tree, dev_params, exact, what):
+def _compare_params(spec, tree, dev_params, exact, what, before):
     for i, ((shape, pd, _gd), L) in enumerate(zip(spec, tree.leaves)):
         got = to_host(dev_params[f"l{i:03d}"])
         want = L["param"]
@@ -145,6 +145,7 @@ def _run(spec, *, steps=3, exact=False, block_size=2048, min_size=4096, wd=0.01,
         for i, (_shape, pd, _gd) in enumerate(spec):
             host_params[f"l{i:03d}"] = to_host(params[f"l{i:03d}"]).copy()
         tree = _oracle_from_state(spec, host_params, state[0])
+        before = [L["param"].copy() for L in tree.leaves]
         count_inc = int(state[0].count) + 1
         key_mu, key_nu, _ = orc.split(state[0].key, 3)
         n = len(spec)
@@ -166,7 +167,7 @@ def _run(spec, *, steps=3, exact=False, block_size=2048, min_size=4096, wd=0.01,
         params, state = rf.adamw8_step(tx, params, gdev, state, key=pkey if psr else None, stochastic=psr)
         torch.cuda.synchronize()
         _compare_state(spec, tree, state[0], f"step {step + 1}")
-        _compare_params(spec, tree, params, exact, f"step {step + 1}")
+        _compare_params(spec, tree, params, exact, f"step {step + 1}", before)
 
 
 C1 = [((1024, 1024), "f32", "f32")]
