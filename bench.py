@@ -146,6 +146,9 @@ def main(argv=None):
     ap.add_argument("--param-sr", action="store_true", help="stochastic rounding of bf16 params")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy-gib", type=float, default=0.0,
+                    help="after the timed steps, run three device copies of this many GiB "
+                         "(reference kernel of known traffic for profiler byte counters)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -201,6 +204,16 @@ def main(argv=None):
     value = n_params / (ms_per_step * 1e-3)
     print(f"[bench] {ms_per_step:.3f} ms/step wall, {kernel_ms_avg:.3f} ms/step events, "
           f"{achieved / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+
+    if args.calibrate_copy_gib > 0:
+        nbytes = int(args.calibrate_copy_gib * (1 << 30))
+        src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] calibration copy: 3 x {nbytes} bytes read + written", file=sys.stderr, flush=True)
+        del src, dst
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -41,7 +41,7 @@ constexpr int64_t CHUNK = 2048;    // elements per fallback (unquantized moment)
 
 // Waves per SIMD the step kernel is register-allocated for (<= 512 / N VGPRs).
 #ifndef RF_STEP_WAVES_PER_EU
-#define RF_STEP_WAVES_PER_EU 4
+#define RF_STEP_WAVES_PER_EU 3
 #endif
 
 enum : int32_t { KIND_QFAST = 0, KIND_QGEN = 1, KIND_FALLBACK = 2 };
@@ -410,12 +410,14 @@ __device__ __forceinline__ void update_one(const UnitCtx& c, const rf_adam8_leaf
     }
 }
 
-// Codes of elements [base, base+bs) of a quantized leaf by the literal search
-// (or moment SR), recomputing the new moments from the old codes, which are
-// still in place.  Scales are not written here.
+// Requantization of one block by the literal search (or moment SR): the new
+// moments are recomputed from the old codes and scales, which are still in
+// place, with the reference's NaN-propagating absmax (adam8.py:142), then
+// every element is coded and the new scales are written.  Used for blocks of
+// any size, blocks whose scale leaves the fast range (zero-free tiny, Inf,
+// NaN) and moment SR.
 template <bool MSR>
-__device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
-                                             float sm, float sv, bool fast_m, bool fast_v)
+__device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h)
 {
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t bs = L.block_size;
@@ -427,15 +429,26 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
     const float sv_old = L.nu_scales[blk];
     uint8_t* mcodes = (uint8_t*)L.mu;
     uint8_t* vcodes = (uint8_t*)L.nu;
+    uint32_t am = 0, av = 0;
+    for (int64_t j = lane; j < nvalid; j += WAVE) {
+        const int64_t e = base + j;
+        float mm, vv;
+        ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, load1(L.grad, L.grad_dtype, e), mm, vv);
+        am = max(am, __float_as_uint(mm) & 0x7FFFFFFFu);
+        av = max(av, __float_as_uint(vv));
+    }
+    am = wave_max_u32(am);
+    av = wave_max_u32(av);
+    const float sm = scale_from_absmax_bits(am);
+    const float sv = scale_from_absmax_bits(av);
+    const bool fast_m = !MSR && block_is_fast(am, sm);
+    const bool fast_v = !MSR && block_is_fast(av, sv);
     const float rsm = 1.0f / sm;
     const float rsv = 1.0f / sv;
     for (int64_t j = lane; j < bs; j += WAVE) {
         const int64_t e = base + j;
         float mm = 0.0f, vv = 0.0f;
-        if (j < nvalid) {
-            const float g = load1(L.grad, L.grad_dtype, e);
-            ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, g, mm, vv);
-        }
+        if (j < nvalid) ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, load1(L.grad, L.grad_dtype, e), mm, vv);
         uint32_t cm, cv;
         if (fast_m) {
             cm = code_signed_fast(c.lds, mm, sm, rsm);
@@ -453,6 +466,10 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
         }
         mcodes[e] = (uint8_t)cm;
         vcodes[e] = (uint8_t)cv;
+    }
+    if (lane == 0) {
+        L.mu_scales[blk] = sm;
+        L.nu_scales[blk] = sv;
     }
 }
 
@@ -557,17 +574,28 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     const float sm_old = L.mu_scales[blk];
     const float sv_old = L.nu_scales[blk];
 
+    // Per-block uniform base pointers (SGPRs) + 32-bit lane offsets: the
+    // global accesses need no 64-bit address arithmetic per lane.
+    const RF_GLOBAL uint8_t* gB = (const RF_GLOBAL uint8_t*)L.grad + base * (int64_t)sizeof(GT);
+    const RF_GLOBAL uint8_t* pB = (const RF_GLOBAL uint8_t*)L.param + base * (int64_t)sizeof(PT);
+    const RF_GLOBAL uint8_t* mB = (const RF_GLOBAL uint8_t*)L.mu + base;
+    const RF_GLOBAL uint8_t* vB = (const RF_GLOBAL uint8_t*)L.nu + base;
+
     // Chunk j+1's loads are issued before chunk j's arithmetic: two chunks
     // (6 KB for bf16) in flight per wave without holding all four.
     uint2 mc[2], vc[2];
     Raw8<GT> graw[2];
     Raw8<PT> praw[2];
     auto issue = [&](int j, int slot) {
-        const int64_t e0 = base + j * 512 + lane * 8;
-        mc[slot] = *gload_ptr<uint2>(L.mu, e0);
-        vc[slot] = *gload_ptr<uint2>(L.nu, e0);
-        raw8_load<GT>(graw[slot], L.grad, e0);
-        if constexpr (NEED_P) raw8_load<PT>(praw[slot], L.param, e0);
+        const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
+        mc[slot] = *(const RF_GLOBAL uint2*)(mB + eo);
+        vc[slot] = *(const RF_GLOBAL uint2*)(vB + eo);
+        graw[slot].w[0] = *(const RF_GLOBAL uint4*)(gB + eo * sizeof(GT));
+        if constexpr (sizeof(GT) == 4) graw[slot].w[1] = *(const RF_GLOBAL uint4*)(gB + eo * 4 + 16);
+        if constexpr (NEED_P) {
+            praw[slot].w[0] = *(const RF_GLOBAL uint4*)(pB + eo * sizeof(PT));
+            if constexpr (sizeof(PT) == 4) praw[slot].w[1] = *(const RF_GLOBAL uint4*)(pB + eo * 4 + 16);
+        }
     };
     issue(0, 0);
 
@@ -589,10 +617,12 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     const float* TV = c.wtab + 256;
 
     float m[J][8], v[J][8];
-    uint32_t am = 0, av = 0;
+    float mx = 0.0f, mn = 0.0f;  // max / min of m: with finite inputs no NaN can occur
+    uint32_t av = 0;             // v >= 0: integer max of the bits, NaN-propagating
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int64_t e0 = base + j * 512 + lane * 8;
+        const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
         const int slot = j & 1;
         if (j + 1 < J) issue(j + 1, slot ^ 1);
         float g[8], p[8];
@@ -624,8 +654,9 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             const float vv = TV[cv] + t4;
             m[j][t] = mm;
             v[j][t] = vv;
-            am = max(am, __float_as_uint(mm) & 0x7FFFFFFFu);  // NaN bits sort above Inf
-            av = max(av, __float_as_uint(vv));                 // v >= 0
+            mx = fmaxf(mx, mm);
+            mn = fminf(mn, mm);
+            av = max(av, __float_as_uint(vv));
             u[t] = adam_direction<NEST, EXACT>(h, mm, vv, g[t]);
         }
         decay_and_scale8<WDM>(h, u, p);
@@ -661,9 +692,9 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
 #pragma unroll
                     for (int t = 0; t < 8; t += 2) w[t / 2] = pack_bf16x2_rne(sum[t], sum[t + 1]);
                 }
-                *gstore_ptr<uint4>(L.param, e0 * 2) = make_uint4(w[0], w[1], w[2], w[3]);
+                *(RF_GLOBAL uint4*)(pB + eo * 2) = make_uint4(w[0], w[1], w[2], w[3]);
             } else {
-                RF_GLOBAL float4* q = gstore_ptr<float4>(L.param, e0 * 4);
+                RF_GLOBAL float4* q = (RF_GLOBAL float4*)(pB + eo * 4);
                 q[0] = make_float4(sum[0], sum[1], sum[2], sum[3]);
                 q[1] = make_float4(sum[4], sum[5], sum[6], sum[7]);
             }
@@ -675,18 +706,23 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     }
 
     // Requantization (adam8.py:633-688 -> quantize_blocks).
-    am = wave_max_u32(am);
+    const float amf = fmaxf(mx, -mn);
+    const uint32_t am = wave_max_u32(__float_as_uint(amf));  // amf >= 0: bit order = value order
     av = wave_max_u32(av);
     const float sm = scale_from_absmax_bits(am);
     const float sv = scale_from_absmax_bits(av);
-    const bool fast_m = !MSR && block_is_fast(am, sm);
-    const bool fast_v = !MSR && block_is_fast(av, sv);
-    if (!MSR && fast_m && fast_v) {
+    // Non-finite old scales can make m NaN, which fmaxf would drop: those
+    // blocks, tiny or non-finite new scales, and moment SR go the literal way.
+    const bool old_finite = (__float_as_uint(sm_old) & 0x7FFFFFFFu) < 0x7F800000u &&
+                            (__float_as_uint(sv_old) & 0x7FFFFFFFu) < 0x7F800000u;
+    if (!MSR && old_finite && block_is_fast(am, sm) && block_is_fast(av, sv)) {
         const float rsm = 1.0f / sm;
         const float rsv = 1.0f / sv;
+        RF_GLOBAL uint8_t* mW = (RF_GLOBAL uint8_t*)L.mu + base;
+        RF_GLOBAL uint8_t* vW = (RF_GLOBAL uint8_t*)L.nu + base;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const int64_t e0 = base + j * 512 + lane * 8;
+            const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
             uint32_t cm[8], cv[8];
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
@@ -698,17 +734,15 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             wm.y = cm[4] | (cm[5] << 8) | (cm[6] << 16) | (cm[7] << 24);
             wv.x = cv[0] | (cv[1] << 8) | (cv[2] << 16) | (cv[3] << 24);
             wv.y = cv[4] | (cv[5] << 8) | (cv[6] << 16) | (cv[7] << 24);
-            *gstore_ptr<uint2>(L.mu, e0) = wm;
-            *gstore_ptr<uint2>(L.nu, e0) = wv;
+            *(RF_GLOBAL uint2*)(mW + eo) = wm;
+            *(RF_GLOBAL uint2*)(vW + eo) = wv;
+        }
+        if (lane == 0) {
+            L.mu_scales[blk] = sm;
+            L.nu_scales[blk] = sv;
         }
     } else {
-        // Rare (tiny, Inf or NaN scales) or moment SR: recompute from the old
-        // codes, which are untouched so far, and search literally.
-        requant_literal<MSR>(c, L, blk, h, sm, sv, fast_m, fast_v);
-    }
-    if (lane == 0) {
-        L.mu_scales[blk] = sm;
-        L.nu_scales[blk] = sv;
+        requant_literal<MSR>(c, L, blk, h);
     }
 }
 
@@ -746,27 +780,14 @@ __device__ __forceinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf&
     const uint8_t* mcodes = (const uint8_t*)L.mu;
     const uint8_t* vcodes = (const uint8_t*)L.nu;
 
-    uint32_t am = 0, av = 0;
     for (int64_t j = lane; j < nvalid; j += WAVE) {
         const int64_t e = base + j;
         const float g = load1(L.grad, L.grad_dtype, e);
         float mm, vv;
         ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, g, mm, vv);
-        am = max(am, __float_as_uint(mm) & 0x7FFFFFFFu);
-        av = max(av, __float_as_uint(vv));
         update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g);
     }
-    am = wave_max_u32(am);
-    av = wave_max_u32(av);
-    const float sm = scale_from_absmax_bits(am);
-    const float sv = scale_from_absmax_bits(av);
-    const bool fast_m = !MSR && block_is_fast(am, sm);
-    const bool fast_v = !MSR && block_is_fast(av, sv);
-    requant_literal<MSR>(c, L, blk, h, sm, sv, fast_m, fast_v);
-    if (lane == 0) {
-        L.mu_scales[blk] = sm;
-        L.nu_scales[blk] = sv;
-    }
+    requant_literal<MSR>(c, L, blk, h);
 }
 
 // ============================================= work units: fallback ====
@@ -789,13 +810,25 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
     }
 }
 
-// ======================================================== step kernel ====
-// One launch covers the leaves whose (param, grad) dtypes are (PT, GT)
-// (uint16_t = bf16, float = f32); the plan groups the work list by dtype.
+// ======================================================== step kernels ===
+__device__ __forceinline__ void leaf_context(UnitCtx& c, const rf_adam8_leaf& L, const KHp& h, bool msr, bool psr)
+{
+    const bool decay = (L.flags & RF_LEAF_DECAY) != 0;
+    c.wd_mode = !decay ? WD_OFF : ((L.param_dtype == RF_BF16 && (h.flags & RF_DECAY_WEAK)) ? WD_BF16 : WD_F32);
+    if (msr) {
+        jax_split(h.kmu0, h.kmu1, (uint32_t)L.state_index, c.kmu0, c.kmu1);
+        jax_split(h.knu0, h.knu1, (uint32_t)L.state_index, c.knu0, c.knu1);
+    }
+    if (psr) jax_split(h.kp0, h.kp1, (uint32_t)L.param_index, c.kp0, c.kp1);
+}
+
+// Full 2048-element blocks of the leaves whose (param, grad) dtypes are
+// (PT, GT) (uint16_t = bf16, float = f32): the hot kernel.  Persistent
+// waves walk the work list with a grid stride of one block per wave.
 template <typename PT, typename GT, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
-__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVES_PER_EU))) void k_adam8(const rf_adam8_leaf* __restrict__ leaves,
-                                              const Seg* __restrict__ segs, int64_t total_units, KHp h,
-                                              const uint4* __restrict__ tables)
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVES_PER_EU))) void k_adam8(
+    const rf_adam8_leaf* __restrict__ leaves, const Seg* __restrict__ segs, int64_t total_units, KHp h,
+    const uint4* __restrict__ tables)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
     __shared__ __attribute__((aligned(16))) float wtab[WAVES_PER_WG][512];
@@ -819,23 +852,45 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
         if (sg.leaf != cur_leaf) {
             cur_leaf = sg.leaf;
             L = leaves[cur_leaf];
-            const bool decay = (L.flags & RF_LEAF_DECAY) != 0;
-            c.wd_mode = !decay ? WD_OFF
-                               : ((L.param_dtype == RF_BF16 && (h.flags & RF_DECAY_WEAK)) ? WD_BF16 : WD_F32);
-            if constexpr (MSR) {
-                jax_split(h.kmu0, h.kmu1, (uint32_t)L.state_index, c.kmu0, c.kmu1);
-                jax_split(h.knu0, h.knu1, (uint32_t)L.state_index, c.knu0, c.knu1);
-            }
-            if constexpr (PSR) jax_split(h.kp0, h.kp1, (uint32_t)L.param_index, c.kp0, c.kp1);
+            leaf_context(c, L, h, MSR, PSR);
+        }
+        dispatch_qfast<PT, GT, APPLY, MSR, PSR, NEST, EXACT>(c, L, sg.first + (u - sg.unit_start), h);
+    }
+}
+
+// Everything else, one wave per unit: quantized blocks of other sizes,
+// partial or unaligned blocks (two passes, literal requantization) and
+// leaves with unquantized (fallback) moments.  Dtypes are read per leaf.
+template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
+__global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
+                                                  const Seg* __restrict__ segs, int64_t total_units, KHp h,
+                                                  const uint4* __restrict__ tables)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
+    stage_tables(lds, tables);
+
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    int32_t s = 0;
+    int32_t cur_leaf = -1;
+    UnitCtx c;
+    c.lds = lds;
+    c.wtab = nullptr;
+    c.fed = (h.flags & RF_FED_BITS) != 0;
+    c.wd_mode = WD_OFF;
+    c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;
+    rf_adam8_leaf L;
+    for (int64_t u = wave; u < total_units; u += nwaves) {
+        while (segs[s + 1].unit_start <= u) ++s;
+        const Seg sg = segs[s];
+        if (sg.leaf != cur_leaf) {
+            cur_leaf = sg.leaf;
+            L = leaves[cur_leaf];
+            leaf_context(c, L, h, MSR, PSR);
         }
         const int64_t idx = sg.first + (u - sg.unit_start);
-        if (sg.kind == KIND_QFAST) {
-            dispatch_qfast<PT, GT, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
-        } else if (sg.kind == KIND_QGEN) {
-            unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
-        } else {
-            unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, idx, h);
-        }
+        if (sg.kind == KIND_QGEN) unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
+        else unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, idx, h);
     }
 }
 

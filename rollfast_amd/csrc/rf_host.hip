@@ -591,8 +591,8 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     DevState* ds = nullptr;
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
-    std::vector<Seg> gsegs[4];
-    int64_t gunits[4] = {0, 0, 0, 0};
+    std::vector<Seg> gsegs[5];
+    int64_t gunits[5] = {0, 0, 0, 0, 0};
     auto add = [&](int32_t leaf, int combo, int32_t kind, int64_t first, int64_t count) {
         if (count <= 0) return;
         Seg sg{};
@@ -613,6 +613,8 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
         any_mb |= (L.mu_bits != nullptr) || (L.nu_bits != nullptr);
         const bool vec = leaf_vec_ok(L, apply);
         vecs.push_back(vec ? 1 : 0);
+        // Full aligned 2048-blocks go to the fast kernel of their dtype
+        // combination; everything else to the generic kernel (group 4).
         const int combo = dtype_combo(L);
         if (L.moment_kind == RF_MOMENT_QUANTIZED) {
             const int64_t bs = L.block_size;
@@ -620,20 +622,20 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
             if (bs == FAST_BS && vec) {
                 const int64_t nfull = L.size / bs;
                 add(i, combo, KIND_QFAST, 0, nfull);
-                add(i, combo, KIND_QGEN, nfull, nb - nfull);
+                add(i, 4, KIND_QGEN, nfull, nb - nfull);
             } else {
-                add(i, combo, KIND_QGEN, 0, nb);
+                add(i, 4, KIND_QGEN, 0, nb);
             }
         } else {
-            add(i, combo, KIND_FALLBACK, 0, (L.size + CHUNK - 1) / CHUNK);
+            add(i, 4, KIND_FALLBACK, 0, (L.size + CHUNK - 1) / CHUNK);
         }
     }
     std::vector<Seg> segs;
     std::vector<PlanGroup> groups;
     int64_t units = 0;
-    for (int combo = 3; combo >= 0; --combo) {
+    for (int combo = 4; combo >= 0; --combo) {
         if (gunits[combo] == 0) continue;
-        groups.push_back({combo, (int64_t)segs.size(), gunits[combo]});
+        groups.push_back({combo == 4 ? -1 : combo, (int64_t)segs.size(), gunits[combo]});
         segs.insert(segs.end(), gsegs[combo].begin(), gsegs[combo].end());
         Seg sentinel{};
         sentinel.unit_start = gunits[combo];
