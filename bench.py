@@ -90,6 +90,22 @@ def algorithmic_bytes(shapes, block_size=2048, min_size=4096):
     return total
 
 
+def profiled_traffic(workload, exact, param_sr):
+    """HBM bytes per launch of the step kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary of the same workload (default flags only),
+    or None when no such summary exists."""
+    if exact or param_sr:
+        return None
+    import re
+
+    name = {"llama7b_bf16_adamw8": "k_adam8_llama7b_traffic.md"}.get(workload)
+    path = os.path.join(ROOT, "profiles", name) if name else None
+    if not path or not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch = (\d+)$", open(path).read(), re.M)
+    return int(m.group(1)) if m else None
+
+
 def cpu_baseline(seconds_target=12.0, threads=None):
     """The CPU oracle (C, OpenMP over blocks) on a bounded sample of the same
     workload: the leaves of one Llama layer, one step each, repeated until
@@ -220,6 +236,7 @@ def main(argv=None):
         print("[bench] CPU oracle baseline", file=sys.stderr, flush=True)
         cpu = cpu_baseline(args.cpu_seconds)
 
+    traffic = profiled_traffic(workload, args.exact, args.param_sr)
     line = {
         "metric": METRIC,
         "value": value,
@@ -252,7 +269,8 @@ def main(argv=None):
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": "profiles/ rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated" if traffic else None,
             "algorithmic_bytes_per_step": bytes_step,
             "kernel_ms": kernel_ms_avg,
         },
