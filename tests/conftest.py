@@ -8,12 +8,21 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 
+def pytest_addoption(parser):
+    parser.addoption("--runslow", action="store_true", default=False, help="run the long CPU checks")
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X) and the built HIP library")
     config.addinivalue_line("markers", "slow: long-running CPU check")
 
 
 def pytest_collection_modifyitems(config, items):
+    if not config.getoption("--runslow"):
+        skip_slow = pytest.mark.skip(reason="long CPU check: pass --runslow")
+        for item in items:
+            if "slow" in item.keywords:
+                item.add_marker(skip_slow)
     try:
         import torch
 

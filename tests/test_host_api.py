@@ -1,0 +1,182 @@
+"""Host side of the adam8 API (no GPU): pytree order, PRNG key streams,
+state construction and metadata, byte accounting, signatures and the
+reference's error behaviour.  Anything that would run a kernel is checked
+to refuse host tensors instead of falling back to a CPU path."""
+
+from __future__ import annotations
+
+import inspect
+from typing import NamedTuple
+
+import numpy as np
+import pytest
+import torch
+
+import rollfast_amd as rf
+from oracle import oracle as orc
+from rollfast_amd import _tree, prng
+from rollfast_amd.optim import adam8 as A
+
+
+# ------------------------------------------------------------------ trees --
+class Pair(NamedTuple):
+    a: object
+    b: object
+
+
+def test_tree_flatten_order_matches_jax_conventions():
+    """dict keys sorted, sequences in order, None has no leaves, namedtuples
+    by field order (jax.tree_util flatten order)."""
+    tree = {"z": 1, "a": [2, (3, None)], "m": Pair(b=5, a=4), "n": None}
+    leaves, td = _tree.flatten(tree)
+    assert leaves == [2, 3, 4, 5, 1]
+    back = _tree.unflatten(td, [10 * x for x in leaves])
+    assert back == {"z": 10, "a": [20, (30, None)], "m": Pair(a=40, b=50), "n": None}
+    assert td.num_leaves == 5
+
+
+def test_tree_flatten_up_to_and_map():
+    params = {"w": 1, "b": 2}
+    _, td = _tree.flatten(params)
+    assert _tree.flatten_up_to(td, {"w": [1, 2], "b": (3,)}) == [(3,), [1, 2]]
+    assert _tree.tree_map(lambda x, y: x + y, params, {"w": 10, "b": 20}) == {"w": 11, "b": 22}
+
+
+def test_quantized_blocks_is_a_node_with_static_aux():
+    qb = A.QuantizedBlocks(values="V", scales="S", shape=(3,), size=3, block_size=2)
+    leaves, td = _tree.flatten({"m": qb})
+    assert leaves == ["V", "S"]
+    back = _tree.unflatten(td, ["V2", "S2"])["m"]
+    assert isinstance(back, A.QuantizedBlocks)
+    assert (back.values, back.scales, back.shape, back.size, back.block_size) == ("V2", "S2", (3,), 3, 2)
+
+
+# ------------------------------------------------------------------- PRNG --
+def test_prng_key_and_streams_match_oracle():
+    assert prng.PRNGKey(0).tolist() == [0, 0]
+    assert prng.PRNGKey(42).tolist() == [0, 42]
+    assert prng.PRNGKey(-1).tolist() == [0, 0xFFFFFFFF]
+    key = np.array([0x13198A2E, 0x03707344], np.uint32)
+    np.testing.assert_array_equal(prng.split(key, 7), orc.split(tuple(key), 7))
+    np.testing.assert_array_equal(prng.bits(key, 1000, offset=(1 << 32) - 500),
+                                  orc.random_bits(tuple(key), 1000, offset=(1 << 32) - 500))
+    y = prng.threefry2x32(np.array([0, 0], np.uint32), np.uint32(0), np.uint32(0))
+    assert (int(y[0]), int(y[1])) == (0x6B200159, 0x99BA4EFE)
+    assert prng.fresh_key(None).tolist() == [0, 42]
+
+
+# ------------------------------------------------------- state / metadata --
+def _cpu_params():
+    return {
+        "w": torch.linspace(-1.0, 1.0, 4096).reshape(64, 64),
+        "b": torch.zeros(100),
+        "h": torch.zeros(3000, dtype=torch.bfloat16),
+        "i": torch.zeros(5000, dtype=torch.int32),
+        "none": None,
+    }
+
+
+def test_scale_by_adam8_init_structure():
+    """tests/test_adam8.py:87-118 plus _init_moment_leaf (adam8.py:605-630):
+    signed mu / unsigned nu codebooks, uint8 codes at the zero code, unit
+    scales, fallback zeros for small or integer leaves, None passes through."""
+    tx = rf.scale_by_adam8(block_size=256, min_size=1, stochastic_rounding=False)
+    st = tx.init(_cpu_params())
+    assert isinstance(st, rf.ScaleByAdam8State)
+    assert int(st.count) == 0 and st.count.dtype == np.int32
+    assert st.key.dtype == np.uint32 and st.key.shape == (2,)
+    # next key of split(PRNGKey(42), 3) (adam8.py:274)
+    np.testing.assert_array_equal(st.key, prng.split(prng.PRNGKey(42), 3)[2])
+    for tree, cid, zero in ((st.mu, rf.DYNAMIC_SIGNED_CODEBOOK_ID, 127), (st.nu, rf.DYNAMIC_UNSIGNED_CODEBOOK_ID, 0)):
+        q = tree["w"]
+        assert isinstance(q, rf.QuantizedBlocks)
+        assert q.codebook_id == cid and q.zero_point == zero and (q.qmin, q.qmax) == (0, 255)
+        assert q.values.dtype == torch.uint8 and tuple(q.values.shape) == (16, 256)
+        assert bool(torch.all(q.values == zero)) and bool(torch.all(q.scales == 1.0))
+        assert q.shape == (64, 64) and q.size == 4096 and q.block_size == 256
+        assert isinstance(tree["h"], rf.QuantizedBlocks) and tuple(tree["h"].values.shape) == (12, 256)
+        assert tree["i"].dtype == torch.float32 and tree["i"].shape == (5000,)  # not inexact: fallback
+        assert tree["none"] is None
+    md = st.mu["w"].metadata()
+    assert md["quantizer"] == "blockwise_dynamic_signed_8bit"
+    assert md["block_layout"] == "shard_local"
+    assert md["values_dtype"] == "uint8" and md["scale_dtype"] == "float32"
+
+
+def test_min_size_and_fallback_dtype():
+    tx = rf.scale_by_adam8(min_size=4096, fallback_dtype=torch.bfloat16)
+    st = tx.init({"small": torch.zeros(4095), "big": torch.zeros(4096)})
+    assert st.mu["small"].dtype == torch.bfloat16
+    assert isinstance(st.mu["big"], rf.QuantizedBlocks)
+    st = rf.scale_by_adam8(quantize=False).init({"big": torch.zeros(8192)})
+    assert st.mu["big"].dtype == torch.float32
+
+
+def test_adamw8_state_tuple_layout():
+    """optax chain state: (ScaleByAdam8State, add_decayed_weights?, lr)."""
+    st = rf.adamw8(1e-3).init({"w": torch.zeros(8)})
+    assert len(st) == 3 and isinstance(st[0], rf.ScaleByAdam8State)
+    st = rf.adamw8(1e-3, weight_decay=0.0).init({"w": torch.zeros(8)})
+    assert len(st) == 2
+    st = rf.adamw8(lambda c: 1e-3, weight_decay=0.01, weight_decay_mask={"w": True}).init({"w": torch.zeros(8)})
+    assert len(st) == 3 and int(st[2].count) == 0
+
+
+def test_byte_accounting_known_answers():
+    """benchmarks/optimizer_state/adamw8.py:15-19 shapes (w0, w1 4096x64 f32,
+    bias 1024 f32): adamw8 state 1,058,828 B; unquantized 4,202,508 B
+    (adam8.py:207-240)."""
+    params = {"w0": torch.zeros(4096, 64), "w1": torch.zeros(4096, 64), "bias": torch.zeros(1024)}
+    st = rf.adamw8(1e-3, weight_decay=0.01).init(params)
+    assert rf.tree_state_nbytes(st) == 1_058_828
+    st = rf.adamw8(1e-3, weight_decay=0.01, quantize=False).init(params)
+    assert rf.tree_state_nbytes(st) == 4_202_508
+    assert rf.estimate_quantized_moment_bytes(4096 * 64) == 262_144 + 128 * 4
+    assert rf.estimate_quantized_moment_bytes(0) == 0
+    assert rf.estimate_quantized_moment_bytes(1) == 2048 + 4
+
+
+# ------------------------------------------------------------- signatures --
+def test_adamw8_signature_exposes_quantized_state_controls():
+    """tests/compat/test_optimizer_signatures.py:68-83."""
+    sig = inspect.signature(rf.adamw8)
+    for name in ("learning_rate", "b1", "b2", "eps", "weight_decay", "block_size", "min_size", "scale_dtype",
+                 "fallback_dtype", "stochastic_rounding"):
+        assert name in sig.parameters
+    defaults = {k: v.default for k, v in sig.parameters.items()}
+    assert defaults["b1"] == 0.9 and defaults["b2"] == 0.999 and defaults["eps"] == 1e-8
+    assert defaults["weight_decay"] == 1e-4 and defaults["block_size"] == 2048 and defaults["min_size"] == 4096
+    sig = inspect.signature(rf.apply_updates)
+    assert list(sig.parameters)[:4] == ["params", "updates", "key", "stochastic"]
+    assert sig.parameters["stochastic"].default is True
+
+
+# ----------------------------------------------------------------- errors --
+def test_reference_errors():
+    with pytest.raises(NotImplementedError, match="Magma"):
+        rf.adamw8(1e-3, use_magma=True)
+    with pytest.raises(ValueError, match="block_size"):
+        rf.scale_by_adam8(block_size=0)
+    with pytest.raises(ValueError, match="block_layout"):
+        rf.scale_by_adam8(block_layout="global")
+    with pytest.raises(ValueError, match="PRNG `key`"):
+        rf.apply_updates({"w": torch.zeros(2)}, {"w": torch.zeros(2)}, key=None, stochastic=True)
+    with pytest.raises(ValueError, match="quantizer"):
+        rf.quantize_blocks(torch.zeros(4), quantizer="int4")
+    with pytest.raises(ValueError, match="key"):
+        rf.quantize_blocks(torch.zeros(4), stochastic_rounding=True)
+
+
+def test_product_path_refuses_host_tensors():
+    """No CPU fallback: every kernel entry refuses tensors off the GPU."""
+    with pytest.raises(ValueError, match="ROCm device"):
+        rf.quantize_blocks(torch.zeros(4096))
+    with pytest.raises(ValueError, match="ROCm device"):
+        rf.apply_updates({"w": torch.zeros(2)}, {"w": torch.zeros(2)}, stochastic=False)
+    tx = rf.adamw8(1e-3)
+    params = {"w": torch.zeros(4096)}
+    st = tx.init(params)
+    with pytest.raises(ValueError, match="ROCm device"):
+        tx.update({"w": torch.zeros(4096)}, st, params)
+    with pytest.raises(ValueError, match="ROCm device"):
+        rf.adamw8_step(tx, params, {"w": torch.zeros(4096)}, st, stochastic=False)

@@ -1,0 +1,396 @@
+"""Pinning of the CPU oracle (no GPU).
+
+Each test fixes one oracle function by something other than the oracle's own
+formula: published known-answer vectors (Random123), exact rational
+arithmetic (codebooks), brute force over all 256 codebook entries (nearest
+code), the exact expectation over every noise value (bf16 stochastic
+rounding), float64 textbook AdamW (fallback moments), and the reference's
+own tolerance and property tests (rollfast tests/test_adam8.py,
+tests/test_utils.py).
+"""
+
+from __future__ import annotations
+
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+
+# ------------------------------------------------------------ threefry ----
+# Random123 kat_vectors, threefry2x32 with 20 rounds (the cipher under
+# jax.random's default PRNG; the same three vectors appear in JAX's own
+# random tests).
+THREEFRY_KATS = [
+    ((0x00000000, 0x00000000), (0x00000000, 0x00000000), (0x6B200159, 0x99BA4EFE)),
+    ((0xFFFFFFFF, 0xFFFFFFFF), (0xFFFFFFFF, 0xFFFFFFFF), (0x1CB996FC, 0xBB002BE7)),
+    ((0x13198A2E, 0x03707344), (0x243F6A88, 0x85A308D3), (0xC4923A9C, 0x483DF7A0)),
+]
+
+
+@pytest.mark.parametrize("key,ctr,want", THREEFRY_KATS)
+def test_threefry2x32_known_answers(key, ctr, want):
+    assert orc.threefry2x32(key, ctr) == want
+
+
+def test_random_bits_and_split_layout():
+    """bits[i] = y0 ^ y1 of threefry(key, (hi32(i), lo32(i))); split(key)[i] =
+    threefry(key, (0, i)).  Checked element by element against the KAT-pinned
+    block function, including an offset that crosses 2^32."""
+    key = (0x13198A2E, 0x03707344)
+    bits = orc.random_bits(key, 8, offset=(1 << 32) - 4)
+    for i, b in enumerate(bits):
+        idx = (1 << 32) - 4 + i
+        y0, y1 = orc.threefry2x32(key, (idx >> 32, idx & 0xFFFFFFFF))
+        assert int(b) == y0 ^ y1
+    sub = orc.split(key, 5)
+    for i in range(5):
+        assert tuple(int(v) for v in sub[i]) == orc.threefry2x32(key, (0, i))
+
+
+# ------------------------------------------------------------ codebooks ---
+def _exact_codebook(signed: bool) -> np.ndarray:
+    """The dynamic codebook of rollfast optim/adam8.py:465-503 in exact
+    rational arithmetic: 7 decades 10^(index-6) times the midpoints of
+    linspace(0.1, 1, k) (k = 2^index + 1 signed, 2^(index+1) + 1 unsigned),
+    mirrored when signed, plus 0 and 1; then rounded once to f32."""
+    vals = []
+    for index in range(7):
+        scale = Fraction(10) ** (index - 6)
+        points = 2 ** index + 1 if signed else 2 ** (index + 1) + 1
+        step = (Fraction(1) - Fraction(1, 10)) / (points - 1)
+        for k in range(points - 1):
+            mid = Fraction(1, 10) + step * k + step / 2
+            vals.append(scale * mid)
+            if signed:
+                vals.append(-scale * mid)
+    vals += [Fraction(0), Fraction(1)]
+    assert len(vals) == 256
+    vals.sort()
+    return np.array([float(v) for v in vals], dtype=np.float64).astype(np.float32)
+
+
+@pytest.mark.parametrize("signed", [True, False])
+def test_codebook_matches_exact_rational_construction(signed):
+    got = orc.codebook(signed)
+    want = _exact_codebook(signed)
+    assert got.dtype == np.float32 and got.shape == (256,)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_codebook_reference_facts():
+    s = orc.codebook(True)
+    u = orc.codebook(False)
+    assert np.all(np.diff(s) > 0) and np.all(np.diff(u) > 0)
+    assert s[0] == np.float32(-0.99296874) and s[127] == 0.0 and s[255] == 1.0
+    assert s[128] == np.float32(5.5e-7) and s[126] == np.float32(-5.5e-7)
+    assert u[0] == 0.0 and u[1] == np.float32(3.25e-7) and u[255] == 1.0
+    assert u[254] == np.float32(0.9964844)
+    # zero codes: argmin |cb| (adam8.py:532-539; tests/test_adam8.py:62,82)
+    assert int(np.argmin(np.abs(s))) == 127 and int(np.argmin(np.abs(u))) == 0
+
+
+# ---------------------------------------------------------- nearest code --
+def _brute_nearest(cb: np.ndarray, n: np.ndarray) -> np.ndarray:
+    """argmin_i fl(|cb_i - clip(n)|) over all 256 entries, ties to the lower
+    index (np.argmin returns the first minimum)."""
+    n = np.clip(n.astype(np.float32), cb[0], cb[255]).astype(np.float32)
+    d = np.abs(cb[None, :] - n[:, None]).astype(np.float32)
+    return np.argmin(d, axis=1).astype(np.uint8)
+
+
+def _probe_values(cb: np.ndarray, rng) -> np.ndarray:
+    """Every codebook entry and every f32 midpoint of neighbours, each with
+    its 3 f32 neighbours either side, plus uniform and log-uniform samples."""
+    pts = [cb]
+    mids = ((cb[:-1].astype(np.float64) + cb[1:].astype(np.float64)) / 2).astype(np.float32)
+    pts.append(mids)
+    base = np.concatenate(pts).astype(np.float32)
+    near = [base]
+    for k in range(1, 4):
+        up = base.copy()
+        dn = base.copy()
+        for _ in range(k):
+            up = np.nextafter(up, np.float32(np.inf))
+            dn = np.nextafter(dn, np.float32(-np.inf))
+        near += [up, dn]
+    lo = float(cb[0])
+    near.append(rng.uniform(lo, 1.0, 20000).astype(np.float32))
+    mag = np.exp(rng.uniform(np.log(1e-9), 0.0, 20000)).astype(np.float32)
+    near.append(mag if lo >= 0 else mag * rng.choice([-1, 1], mag.size).astype(np.float32))
+    near.append(np.array([-2.0, -1.0, 1.5, 3.0, 0.0, -0.0], np.float32))  # clipped to the ends
+    return np.concatenate(near).astype(np.float32)
+
+
+@pytest.mark.parametrize("q,signed", [(orc.Q_SIGNED, True), (orc.Q_UNSIGNED, False)])
+def test_nearest_code_brute_force(q, signed):
+    cb = orc.codebook(signed)
+    vals = _probe_values(cb, np.random.default_rng(1))
+    got = orc.nearest_codes_list(q, vals.view(np.uint32))
+    np.testing.assert_array_equal(got, _brute_nearest(cb, vals))
+
+
+def test_nearest_code_ties_go_to_the_lower_code():
+    """An input exactly halfway (in f32 distances) between two entries takes
+    the lower code (adam8.py:566-569 uses a strict <)."""
+    cb = orc.codebook(True)
+    found = 0
+    for i in range(255):
+        lo, hi = cb[i], cb[i + 1]
+        m = np.float32((np.float64(lo) + np.float64(hi)) / 2)
+        if np.float32(abs(hi - m)) == np.float32(abs(m - lo)):
+            assert orc.nearest_code(orc.Q_SIGNED, m) == i
+            found += 1
+    assert found > 100
+
+
+def test_nearest_code_nan_is_code_254():
+    """searchsorted puts NaN past the end (index 256 -> clipped 255); the
+    strict compare against NaN is false, so the lower neighbour 254 wins.
+    Documented choice: jnp.searchsorted on NaN is parity unpinned."""
+    assert orc.nearest_code(orc.Q_SIGNED, float("nan")) == 254
+    assert orc.nearest_code(orc.Q_UNSIGNED, float("nan")) == 254
+
+
+# ------------------------------------------------ quantize / dequantize ---
+def test_symmetric_int8_error_bounded_by_half_scale():
+    """tests/test_adam8.py:18-42: linspace(-3, 2, 513), block 128."""
+    x = np.linspace(-3.0, 2.0, 513, dtype=np.float32)
+    codes, scales = orc.quantize(x, 128, orc.Q_SYMMETRIC)
+    assert codes.dtype == np.int8 and scales.dtype == np.float32
+    assert codes.min() >= -127 and codes.max() <= 127
+    back = orc.dequantize(codes, scales, x.size, 128, orc.Q_SYMMETRIC)
+    assert np.max(np.abs(back - x)) <= np.max(scales) / 2 + 1e-6
+
+
+def test_dynamic_signed_error_bound():
+    """tests/test_adam8.py:45-65."""
+    x = np.linspace(-3.0, 2.0, 513, dtype=np.float32)
+    codes, scales = orc.quantize(x, 128, orc.Q_SIGNED)
+    assert codes.dtype == np.uint8 and codes.shape == (5, 128)
+    back = orc.dequantize(codes, scales, x.size, 128, orc.Q_SIGNED)
+    assert np.max(np.abs(back - x)) <= np.max(scales) * 0.01
+
+
+def test_dynamic_unsigned_nonnegative_and_error_bound():
+    """tests/test_adam8.py:68-84."""
+    x = np.linspace(0.0, 3.0, 513, dtype=np.float32)
+    codes, scales = orc.quantize(x, 128, orc.Q_UNSIGNED)
+    back = orc.dequantize(codes, scales, x.size, 128, orc.Q_UNSIGNED)
+    assert back.min() >= 0.0
+    assert np.max(np.abs(back - x)) <= np.max(scales) * 0.01
+
+
+def test_quantize_literal_definition():
+    """scale = absmax (1 for an all-zero block), code = nearest(clip(x /
+    scale)) with IEEE f32 division, padding codes = the zero code
+    (adam8.py:113-187)."""
+    rng = np.random.default_rng(3)
+    bs = 64
+    x = (rng.standard_normal(5 * bs - 17) * 0.3).astype(np.float32)
+    x[bs:2 * bs] = 0.0  # a zero block
+    cb = orc.codebook(True)
+    codes, scales = orc.quantize(x, bs, orc.Q_SIGNED)
+    xp = np.zeros(5 * bs, np.float32)
+    xp[:x.size] = x
+    blocks = xp.reshape(5, bs)
+    amax = np.max(np.abs(blocks), axis=1)
+    want_scales = np.where(amax > 0, amax, np.float32(1.0)).astype(np.float32)
+    np.testing.assert_array_equal(scales, want_scales)
+    norm = (blocks / want_scales[:, None]).astype(np.float32)
+    want_codes = _brute_nearest(cb, norm.reshape(-1)).reshape(5, bs)
+    np.testing.assert_array_equal(codes, want_codes)
+    assert np.all(codes.reshape(-1)[x.size:] == 127)
+    assert np.all(codes[1] == 127) and scales[1] == 1.0
+
+
+def test_dequantize_closed_form():
+    rng = np.random.default_rng(4)
+    bs = 32
+    codes = rng.integers(0, 256, size=(3, bs), dtype=np.uint8)
+    scales = rng.uniform(0.1, 2.0, 3).astype(np.float32)
+    for q, signed in ((orc.Q_SIGNED, True), (orc.Q_UNSIGNED, False)):
+        cb = orc.codebook(signed)
+        got = orc.dequantize(codes, scales, 3 * bs - 5, bs, q)
+        want = (cb[codes] * scales[:, None]).astype(np.float32).reshape(-1)[:3 * bs - 5]
+        np.testing.assert_array_equal(got, want)
+    sym = codes.view(np.int8)
+    got = orc.dequantize(sym, scales, 3 * bs, bs, orc.Q_SYMMETRIC)
+    np.testing.assert_array_equal(got, (sym.astype(np.float32) * scales[:, None]).reshape(-1))
+
+
+def test_moment_sr_upper_probability():
+    """Codebook SR picks the upper neighbour with probability
+    (n - cb_l) / (cb_u - cb_l) (adam8.py:557-564): a fixed value repeated
+    over 2^17 random draws lands within 5 sigma of that rate."""
+    cb = orc.codebook(True)
+    i = 200
+    n = np.float32(cb[i] + np.float32(0.3) * (cb[i + 1] - cb[i]))
+    p = float((np.float64(n) - cb[i]) / (np.float64(cb[i + 1]) - cb[i]))
+    bs = 1024
+    count = 128 * bs
+    x = np.full(count, n, np.float32)
+    x[::bs] = 1.0  # absmax of every block is exactly 1: normalised value stays n
+    bits = orc.random_bits((7, 11), count)
+    codes, _ = orc.quantize(x, bs, orc.Q_SIGNED, bits=bits)
+    sel = np.ones(count, bool)
+    sel[::bs] = False
+    c = codes.reshape(-1)[sel]
+    assert set(np.unique(c).tolist()) <= {i, i + 1}
+    rate = np.mean(c == i + 1)
+    sigma = np.sqrt(p * (1 - p) / c.size)
+    assert abs(rate - p) < 5 * sigma
+
+
+# ------------------------------------------------------------ bf16 SR -----
+def test_sr_bf16_exhaustive_noise_is_exactly_unbiased():
+    """Over all 2^16 noise values, (x + noise) & 0xFFFF0000 averages to x
+    exactly for every finite x (utils.py:365-371)."""
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([
+        rng.standard_normal(24).astype(np.float32),
+        (rng.standard_normal(8) * 1e-30).astype(np.float32),
+        np.array([1.0 + 2.0 ** -9, -3.0e38, 1e-40, -1e-42, 0.0], np.float32),
+    ]).astype(np.float32)
+    noise = np.arange(1 << 16, dtype=np.uint32)
+    for x in xs:
+        out = orc.sr_bf16(np.full(noise.size, x, np.float32), noise)
+        vals = orc.bf16_bits_to_f32(out).astype(np.float64)
+        assert vals.sum() == np.float64(x) * (1 << 16), x
+
+
+def test_sr_bf16_specials():
+    noise = np.array([0, 1, 0x7FFF, 0x8000, 0xFFFF, 0x12345678], np.uint32)
+    for x, want in ((np.inf, 0x7F80), (-np.inf, 0xFF80)):
+        out = orc.sr_bf16(np.full(noise.size, x, np.float32), noise)
+        assert np.all(out == want)
+    # NaN: the noise is zeroed and the low 16 bits truncated, so a quiet NaN
+    # stays a NaN and a payload only in the low half collapses to Inf.
+    q = np.array([0x7FC00000], np.uint32).view(np.float32)
+    assert np.all(orc.sr_bf16(np.repeat(q, 6), noise) == 0x7FC0)
+    low = np.array([0x7F800001], np.uint32).view(np.float32)
+    assert np.all(orc.sr_bf16(np.repeat(low, 6), noise) == 0x7F80)
+    # the largest finite value can round up to +Inf (no saturation)
+    big = np.array([0x7F7FFFFF], np.uint32).view(np.float32)
+    assert orc.sr_bf16(big, np.array([1], np.uint32))[0] == 0x7F80
+
+
+def test_sr_bf16_sub_ulp_signal_kat():
+    """tests/test_utils.py:89-103: ones(4096) bf16 + 2^-9 stays 1.0 under
+    nearest-even and moves up under stochastic rounding."""
+    n = 4096
+    p = orc.f32_to_bf16_bits(np.ones(n, np.float32))
+    det = p.copy()
+    orc.apply_updates(det, orc.BF16, np.full(n, 2.0 ** -9, np.float32))
+    assert np.all(det == 0x3F80)
+    sr = p.copy()
+    orc.apply_updates(sr, orc.BF16, np.full(n, 2.0 ** -9, np.float32), bits=orc.random_bits((0, 0), n))
+    v = orc.bf16_bits_to_f32(sr)
+    assert np.any(v > 1.0) and v.mean() > 1.0
+    # E[SR] = 1 + 2^-9: 1/4 of the draws move to 1 + 2^-7
+    assert abs(np.mean(v > 1.0) - 0.25) < 5 * np.sqrt(0.25 * 0.75 / n)
+
+
+def test_f32_to_bf16_round_to_nearest_even():
+    x = np.array([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, 1.0 + 2.0 ** -8 + 2.0 ** -20, -2.5, np.inf], np.float32)
+    want = np.array([0x3F80, 0x3F82, 0x3F81, 0xC020, 0x7F80], np.uint16)
+    np.testing.assert_array_equal(orc.f32_to_bf16_bits(x), want)
+
+
+# ---------------------------------------------------------- the step ------
+def _textbook_adamw(p, grads, *, b1, b2, eps, eps_root, wd, lr):
+    """float64 AdamW as optax.adamw defines it (tests/test_adam.py:32-47)."""
+    p = p.astype(np.float64).copy()
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    for t, g in enumerate(grads, start=1):
+        g = g.astype(np.float64)
+        m = b1 * m + (1 - b1) * g
+        v = b2 * v + (1 - b2) * g * g
+        mh = m / (1 - b1 ** t)
+        vh = v / (1 - b2 ** t)
+        u = mh / (np.sqrt(vh + eps_root) + eps) + wd * p
+        p = p - lr * u
+    return p
+
+
+def test_fallback_leaf_matches_textbook_adamw():
+    """f32 params with f32 (unquantized) moments: three oracle steps agree
+    with float64 AdamW to f32 rounding (reference anchor: exact fallback
+    check, tests/finetune/test_adamw8_from_plan.py:196-201, atol 1e-7)."""
+    rng = np.random.default_rng(6)
+    n = 3000
+    p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    grads = [(rng.standard_normal(n) * 1e-2).astype(np.float32) for _ in range(3)]
+    p = p0.copy()
+    mu = np.zeros(n, np.float32)
+    nu = np.zeros(n, np.float32)
+    for t, g in enumerate(grads, start=1):
+        hp = orc.make_hparams(weight_decay=0.01, lr=1e-3, count=t, decay=True, apply=True)
+        orc.adam8_leaf(hp, p, orc.F32, g, orc.F32, orc.MOM_F32, mu, None, nu, None)
+    want = _textbook_adamw(p0, grads, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0, wd=0.01, lr=1e-3)
+    np.testing.assert_allclose(p, want, rtol=0, atol=1e-7)
+
+
+def test_adamw8_second_step_is_close_to_fp32_adamw():
+    """tests/test_adam8.py:121-149: 64x64 linspace params, grads 0.125,
+    eps 1e-6, block 256, min_size 1; the second step's updates of the
+    quantized optimizer match fp32 AdamW within rtol 0.03, atol 3e-4."""
+    n = 4096
+    p0 = np.linspace(-1.0, 1.0, n, dtype=np.float32)
+    g = np.full(n, 0.125, np.float32)
+    kw = dict(b1=0.9, b2=0.999, eps=1e-6, weight_decay=0.01, lr=1e-3, decay=True)
+    # quantized
+    mu = np.full(n, 127, np.uint8)
+    nu = np.zeros(n, np.uint8)
+    ms = np.ones(16, np.float32)
+    vs = np.ones(16, np.float32)
+    p = p0.copy()
+    upd = np.empty(n, np.float32)
+    orc.adam8_leaf(orc.make_hparams(count=1, **kw), p, orc.F32, g, orc.F32, orc.MOM_QUANT, mu, ms, nu, vs, 256,
+                   updates_out=upd)
+    p1 = (p0 + upd).astype(np.float32)
+    upd_q = np.empty(n, np.float32)
+    orc.adam8_leaf(orc.make_hparams(count=2, **kw), p1.copy(), orc.F32, g, orc.F32, orc.MOM_QUANT, mu, ms, nu, vs,
+                   256, updates_out=upd_q)
+    # fp32 reference, float64 arithmetic
+    b1, b2, eps, wd, lr = 0.9, 0.999, 1e-6, 0.01, 1e-3
+    m = (1 - b1) * 0.125
+    v = (1 - b2) * 0.125 ** 2
+    u1 = -lr * ((m / (1 - b1)) / (np.sqrt(v / (1 - b2)) + eps) + wd * p0.astype(np.float64))
+    pf = p0 + u1
+    m = b1 * m + (1 - b1) * 0.125
+    v = b2 * v + (1 - b2) * 0.125 ** 2
+    u2 = -lr * ((m / (1 - b1 ** 2)) / (np.sqrt(v / (1 - b2 ** 2)) + eps) + wd * pf)
+    np.testing.assert_allclose(upd_q, u2, rtol=0.03, atol=3e-4)
+
+
+def test_quantized_moments_track_fp32_moments():
+    """After 5 quantized steps the dequantized moments stay within the
+    accumulated codebook resolution of the float64 moments: each
+    requantization adds at most 0.01 * scale (the reference's quantizer
+    bound, tests/test_adam8.py:65,84) and the EMA scales earlier errors by
+    b < 1, so 5 steps stay within 5 * 0.01 * max scale."""
+    rng = np.random.default_rng(8)
+    n, bs = 8192, 2048
+    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    mu = np.full(n, 127, np.uint8)
+    nu = np.zeros(n, np.uint8)
+    ms = np.ones(n // bs, np.float32)
+    vs = np.ones(n // bs, np.float32)
+    m = np.zeros(n)
+    v = np.zeros(n)
+    for t in range(1, 6):
+        g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+        m = 0.9 * m + 0.1 * g
+        v = 0.999 * v + 0.001 * g.astype(np.float64) ** 2
+        orc.adam8_leaf(orc.make_hparams(count=t, lr=1e-3, apply=True), p, orc.F32, g, orc.F32, orc.MOM_QUANT,
+                       mu, ms, nu, vs, bs)
+    md = orc.dequantize(mu, ms, n, bs, orc.Q_SIGNED)
+    vd = orc.dequantize(nu, vs, n, bs, orc.Q_UNSIGNED)
+    for got, want, sc in ((md, m, ms), (vd, v, vs)):
+        err = np.abs(got - want).reshape(-1, bs).max(axis=1)
+        assert np.all(err <= 5 * 0.01 * sc), (err, sc)
+        assert np.all(err > 0)  # the moments really are quantized
