@@ -1,25 +1,43 @@
 #!/usr/bin/env python
-"""Throughput of the fused 8-bit AdamW step on one MI355X.
+"""Throughput of the 8-bit AdamW step (and its standalone kernels) on one
+MI355X.
 
-Default workload: the Llama-7B-shaped bf16 pytree (32 layers, hidden 4096,
-SwiGLU MLP 11008, vocab 32000, RMSNorm vectors; 6,738,415,616 params in 291
-leaves, all quantized: uint8 codes + f32 scales per 2048-element block),
-params ~N(0, 0.02^2), grads ~N(0, 1e-3^2).  A step is one fused
-adamw8_step over the whole tree (one launch): dequantize both moments, AdamW
-update (lr 1e-3, wd 0.01, betas 0.9/0.999), bf16 params written with
-round-to-nearest-even, moments requantized.  Gradients are drawn before the
-timed region into a pool of distinct buffers that the steps cycle through.
+Default workload (``--workload llama7b``): the Llama-7B-shaped bf16 pytree
+(32 layers, hidden 4096, SwiGLU MLP 11008, vocab 32000, RMSNorm vectors;
+6,738,415,616 params in 291 leaves, all quantized: uint8 codes + f32 scales
+per 2048-element block), params ~N(0, 0.02^2), grads ~N(0, 1e-3^2).  A step
+is one fused adamw8_step over the whole tree (one launch): dequantize both
+moments, AdamW update (lr 1e-3, wd 0.01, betas 0.9/0.999), bf16 params
+written with round-to-nearest-even, moments requantized.  Gradients are
+drawn before the timed region into a pool of distinct buffers that the steps
+cycle through.
 
-Prints one JSON line: params/s (whole job), ms per step, the HBM roofline of
-the step kernel (algorithmic bytes / kernel time, measured with HIP events on
-the launch stream) and the CPU oracle's throughput on a bounded sample.
+Other workloads (one JSON line each, same fields):
+  gpt2             GPT-2-small bf16 tree (74 leaves, LayerNorms on f32
+                   fallback moments), param stochastic rounding on.
+  ragged           2256 leaves, most below min_size (fallback moments),
+                   Student-t(3) grads with per-leaf scales, 10 % zero blocks.
+  llama7b_optax    update-only (Optax) mode over the Llama tree: f32 updates
+                   written, params read for weight decay.
+  llama7b_apply    apply_updates of f32 updates to the bf16 Llama params with
+                   stochastic rounding (in-kernel Threefry bits).
+  quantize_2p30    quantize_blocks, dynamic signed, 2^30 f32 elements
+                   (log-uniform magnitudes 1e-8..1e2, random sign).
+  dequantize_2p30  dequantize_blocks of the same codes to f32.
+  sr_bf16_2p30     f32 -> bf16 stochastic rounding of 2^30 elements.
+
+Prints one JSON line: throughput (whole job), ms per step, the HBM roofline of
+the measured kernel (algorithmic bytes / kernel time from HIP events on the
+launch stream) and the CPU oracle's throughput on a bounded sample.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
+import re
 import sys
 import time
 
@@ -29,8 +47,11 @@ if ROOT not in sys.path:
 
 HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
 METRIC = "adam8 step params/sec + achieved HBM GB/s (% peak), 7B Llama pytree, 1 GPU"
+BS = 2048
+MIN_SIZE = 4096
 
 
+# ------------------------------------------------------------- shapes -----
 def llama7b_shapes():
     h, f, v, layers = 4096, 11008, 32000, 32
     shapes = [("embed", (v, h)), ("lm_head", (v, h)), ("norm", (h,))]
@@ -66,28 +87,30 @@ def ragged_shapes(seed=0):
     return shapes
 
 
-WORKLOADS = {
-    "llama7b": (llama7b_shapes, "llama7b_bf16_adamw8"),
-    "gpt2": (gpt2_small_shapes, "gpt2_small_bf16_adamw8"),
-    "ragged": (ragged_shapes, "ragged_2256_leaves_bf16_adamw8"),
-}
+def _numel(s):
+    return int(math.prod(s))
 
 
-def algorithmic_bytes(shapes, block_size=2048, min_size=4096):
-    """Bytes one step must read and write once: bf16 param r+w, bf16 grad r,
-    codes r+w (2 moments), f32 block scales r+w (2 moments); fallback leaves
-    move f32 moments instead of codes."""
+def step_bytes(shapes, pbytes=2, gbytes=2, apply=True):
+    """Bytes one step must read and write once.  Quantized leaves: param r
+    (+ w when fused), grad r, codes r+w and f32 block scales r+w for both
+    moments; update-only mode writes f32 updates instead of params.
+    Fallback leaves (below min_size) move f32 moments instead of codes."""
     total = 0
     for _, s in shapes:
-        n = 1
-        for d in s:
-            n *= d
-        if n >= min_size:
-            nb = -(-n // block_size)
-            total += n * (2 + 2 + 2) + 2 * (nb * block_size) * 2 + nb * 16
+        n = _numel(s)
+        pio = n * pbytes * (2 if apply else 1) + (0 if apply else 4 * n)
+        if n >= MIN_SIZE:
+            nb = -(-n // BS)
+            total += pio + n * gbytes + 2 * (nb * BS) * 2 + nb * 16
         else:
-            total += n * (2 + 2 + 2) + n * 16
+            total += pio + n * gbytes + n * 16
     return total
+
+
+def algorithmic_bytes(shapes):
+    """Fused-step bytes (bf16 params and grads)."""
+    return step_bytes(shapes)
 
 
 def profiled_traffic(workload, exact, param_sr):
@@ -96,8 +119,6 @@ def profiled_traffic(workload, exact, param_sr):
     or None when no such summary exists."""
     if exact or param_sr:
         return None
-    import re
-
     name = {"llama7b_bf16_adamw8": "k_adam8_llama7b_traffic.md"}.get(workload)
     path = os.path.join(ROOT, "profiles", name) if name else None
     if not path or not os.path.exists(path):
@@ -106,49 +127,300 @@ def profiled_traffic(workload, exact, param_sr):
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline(seconds_target=12.0, threads=None):
+# ------------------------------------------------------- CPU baselines ----
+def _threads(threads=None):
+    from oracle import oracle as orc
+
+    n = threads or int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    orc.set_threads(n)
+    return n
+
+
+def _timed_loop(body, seconds_target):
+    done = 0
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        done += body()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds_target:
+            return done, reps, el
+
+
+def cpu_baseline(seconds_target=12.0, threads=None, shapes=None, sample_name="the 9 leaves of one Llama-7B layer",
+                 param_sr=False):
     """The CPU oracle (C, OpenMP over blocks) on a bounded sample of the same
-    workload: the leaves of one Llama layer, one step each, repeated until
-    about `seconds_target` seconds of CPU work have run."""
+    workload (default: the 9 leaves of one Llama layer), one step per leaf,
+    repeated until about `seconds_target` seconds of CPU work have run."""
     import numpy as np
 
     from oracle import oracle as orc
 
-    nthreads = threads or int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    orc.set_threads(nthreads)
+    nthreads = _threads(threads)
     rng = np.random.default_rng(0)
-    shapes = [s for name, s in llama7b_shapes() if name.startswith("layer00.")]
+    if shapes is None:
+        shapes = [s for name, s in llama7b_shapes() if name.startswith("layer00.")]
     leaves = []
     for s in shapes:
-        n = int(np.prod(s))
-        nb = -(-n // 2048)
+        n = _numel(s)
+        nb = -(-n // BS)
+        quant = n >= MIN_SIZE
         leaves.append(dict(
-            n=n,
+            n=n, quant=quant,
             p=orc.f32_to_bf16_bits(rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)),
             g=orc.f32_to_bf16_bits(rng.standard_normal(n, dtype=np.float32) * np.float32(1e-3)),
-            mc=np.full(nb * 2048, 127, np.uint8), ms=np.ones(nb, np.float32),
-            vc=np.zeros(nb * 2048, np.uint8), vs=np.ones(nb, np.float32)))
-    done = 0
-    step = 0
-    t0 = time.perf_counter()
-    while True:
-        step += 1
-        hp = orc.make_hparams(weight_decay=0.01, lr=1e-3, count=step, decay=True, apply=True)
+            mc=np.full(nb * BS, 127, np.uint8) if quant else np.zeros(n, np.float32),
+            ms=np.ones(nb, np.float32) if quant else None,
+            vc=np.zeros(nb * BS, np.uint8) if quant else np.zeros(n, np.float32),
+            vs=np.ones(nb, np.float32) if quant else None,
+            bits=orc.random_bits((0, 1), n) if param_sr else None))
+    state = {"step": 0}
+
+    def body():
+        state["step"] += 1
+        hp = orc.make_hparams(weight_decay=0.01, lr=1e-3, count=state["step"], decay=True, apply=True,
+                              param_sr=param_sr)
+        done = 0
         for L in leaves:
-            orc.adam8_leaf(hp, L["p"], orc.BF16, L["g"], orc.BF16, orc.MOM_QUANT, L["mc"], L["ms"], L["vc"],
-                           L["vs"], 2048)
+            orc.adam8_leaf(hp, L["p"], orc.BF16, L["g"], orc.BF16, orc.MOM_QUANT if L["quant"] else orc.MOM_F32,
+                           L["mc"], L["ms"], L["vc"], L["vs"], BS, p_bits=L["bits"])
             done += L["n"]
-        el = time.perf_counter() - t0
-        if el >= seconds_target:
-            break
+        return done
+
+    done, reps, el = _timed_loop(body, seconds_target)
     return {
         "value": done / el,
         "unit": "params/s",
         "cores": nthreads,
         "kind": "port",
-        "sample": f"CPU oracle (C restatement, OpenMP, {nthreads} threads) over the 9 leaves of one Llama-7B "
-                  f"layer ({sum(L['n'] for L in leaves)} params), {step} steps in {el:.1f} s",
+        "sample": f"CPU oracle (C restatement, OpenMP, {nthreads} threads) over {sample_name} "
+                  f"({sum(L['n'] for L in leaves)} params), {reps} steps in {el:.1f} s",
     }
+
+
+def cpu_baseline_kernel(kind, seconds_target=12.0, threads=None, n=1 << 22):
+    """The CPU oracle's standalone quantize / dequantize / SR / apply over a
+    2^22-element sample of the same input distribution."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    nthreads = _threads(threads)
+    rng = np.random.default_rng(0)
+    x = (np.exp(rng.uniform(np.log(1e-8), np.log(1e2), n)) * rng.choice([-1.0, 1.0], n)).astype(np.float32)
+    if kind == "quantize":
+        def body():
+            orc.quantize(x, BS, orc.Q_SIGNED)
+            return n
+    elif kind == "dequantize":
+        codes, scales = orc.quantize(x, BS, orc.Q_SIGNED)
+
+        def body():
+            orc.dequantize(codes, scales, n, BS, orc.Q_SIGNED)
+            return n
+    elif kind == "sr_bf16":
+        def body():
+            orc.sr_bf16(x, orc.random_bits((0, 1), n))
+            return n
+    elif kind == "apply":
+        p = orc.f32_to_bf16_bits(x * np.float32(1e-3))
+        u = (x * np.float32(1e-6)).astype(np.float32)
+
+        def body():
+            orc.apply_updates(p, orc.BF16, u, bits=orc.random_bits((0, 1), n))
+            return n
+    else:
+        raise ValueError(kind)
+    done, reps, el = _timed_loop(body, seconds_target)
+    return {
+        "value": done / el,
+        "unit": "params/s" if kind == "apply" else "elements/s",
+        "cores": nthreads,
+        "kind": "port",
+        "sample": f"CPU oracle ({kind}, C, OpenMP, {nthreads} threads; Threefry bits generated on the CPU where "
+                  f"the kernel draws them) over {n} elements, {reps} reps in {el:.1f} s",
+    }
+
+
+# ------------------------------------------------------------ workloads ---
+class Workload:
+    """What one bench line measures: units per step, algorithmic HBM bytes
+    per step, the step closure, its config and its CPU baseline."""
+
+    def __init__(self, name, units, unit, nbytes, step, config, cpu, metric):
+        self.name, self.units, self.unit, self.nbytes = name, units, unit, nbytes
+        self.step, self.config, self.cpu, self.metric = step, config, cpu, metric
+
+
+def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False):
+    import numpy as np
+    import torch
+
+    import rollfast_amd as rf
+
+    shapes = shapes_fn()
+    n_params = sum(_numel(s) for _, s in shapes)
+    print(f"[bench] {workload}: {n_params} params in {len(shapes)} leaves; allocating", file=sys.stderr, flush=True)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    params = {name: (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 0.02).to(torch.bfloat16)
+              for name, s in shapes}
+    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=args.exact)
+    state = tx.init(params)
+    pool = []
+    rng = np.random.default_rng(0)
+    for k in range(args.grad_pool):
+        gen.manual_seed(1000 + k)
+        g = {}
+        for name, s in shapes:
+            if grads == "student_t":
+                # Student-t(3) = N / sqrt(chi2_3 / 3), times a log-uniform per-leaf scale
+                z = torch.randn(s, generator=gen, device="cuda")
+                c = sum(torch.randn(s, generator=gen, device="cuda") ** 2 for _ in range(3)) / 3
+                t = z / torch.sqrt(c) * float(np.exp(rng.uniform(np.log(1e-6), 0.0)))
+                flat = t.view(-1)
+                nb = flat.numel() // BS
+                if nb:
+                    zero = torch.from_numpy(rng.random(nb) < 0.1).cuda()
+                    flat[: nb * BS].view(nb, BS)[zero] = 0.0
+                g[name] = t.to(torch.bfloat16)
+            else:
+                g[name] = (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 1e-3).to(torch.bfloat16)
+        pool.append(g)
+    key = rf.prng.PRNGKey(0)
+    holder = {"params": params, "state": state, "k": 0}
+
+    def step():
+        g = pool[holder["k"] % len(pool)]
+        holder["k"] += 1
+        if optax:
+            _, holder["state"] = tx.update(g, holder["state"], holder["params"])
+        else:
+            holder["params"], holder["state"] = rf.adamw8_step(tx, holder["params"], g, holder["state"], key=key,
+                                                               stochastic=param_sr)
+
+    n_quant = sum(1 for _, s in shapes if _numel(s) >= MIN_SIZE)
+    config = {
+        "workload": workload,
+        "params": n_params,
+        "leaves": len(shapes),
+        "quantized_leaves": n_quant,
+        "block_size": BS,
+        "param_dtype": "bf16",
+        "grad_dtype": "bf16",
+        "moments": "uint8 codebook codes + f32 block scales (f32 fallback below 4096 elements)",
+        "param_rounding": "stochastic" if param_sr else "nearest-even",
+        "direction": "ieee" if args.exact else "hw rcp/sqrt",
+        "mode": "optax update-only (f32 updates)" if optax else "fused step (params written)",
+        "launches_per_step": 1,
+        "grad_pool": len(pool),
+    }
+    if shapes_fn is llama7b_shapes:
+        cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr)  # noqa: E731
+    else:
+        sub = [s for _, s in shapes][:400]
+        cpu = lambda: cpu_baseline(args.cpu_seconds, shapes=sub,  # noqa: E731
+                                   sample_name=f"the first {len(sub)} leaves", param_sr=param_sr)
+    metric = METRIC if workload == "llama7b_bf16_adamw8" else f"adam8 params/sec + achieved HBM GB/s, {workload}, 1 GPU"
+    return Workload(workload, n_params, "params/s", step_bytes(shapes, apply=not optax), step, config, cpu, metric)
+
+
+def _c5_input(n):
+    import torch
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    x = torch.empty(n, device="cuda").uniform_(math.log(1e-8), math.log(1e2), generator=gen).exp_()
+    sign = torch.rand(n, device="cuda", generator=gen) < 0.5
+    x[sign] *= -1.0
+    return x
+
+
+def _kernel_workload(args, kind):
+    import torch
+
+    from rollfast_amd import _lib
+
+    L = _lib.lib()
+    sp = _lib.stream_ptr
+    if kind == "apply":
+        shapes = llama7b_shapes()
+        n = sum(_numel(s) for _, s in shapes)
+        print(f"[bench] llama7b_apply: {n} params; allocating", file=sys.stderr, flush=True)
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(0)
+        params = [(torch.randn(s, generator=gen, device="cuda") * 0.02).to(torch.bfloat16) for _, s in shapes]
+        upd = [torch.randn(s, generator=gen, device="cuda") * 1e-5 for _, s in shapes]
+        rows = (_lib.ApplyLeaf * len(shapes))()
+        for i, (p, u) in enumerate(zip(params, upd)):
+            rows[i].param = p.data_ptr()
+            rows[i].updates = u.data_ptr()
+            rows[i].bits = None
+            rows[i].size = p.numel()
+            rows[i].param_dtype = _lib.RF_BF16
+            rows[i].param_index = i
+
+        def step():
+            _lib.check(L.rf_apply_updates(rows, len(shapes), 1, 0, 42, sp()), "apply")
+
+        name = "llama7b_bf16_apply_updates_sr"
+        return Workload(name, n, "params/s", n * (2 + 4 + 2), step,
+                        {"workload": name, "params": n, "leaves": len(shapes), "param_dtype": "bf16",
+                         "update_dtype": "f32", "rounding": "stochastic (in-kernel Threefry)",
+                         "launches_per_step": 1},
+                        lambda: cpu_baseline_kernel("apply", args.cpu_seconds),
+                        "apply_updates params/sec + achieved HBM GB/s, 7B Llama pytree bf16 SR, 1 GPU")
+    n = 1 << 30
+    nb = n // BS
+    print(f"[bench] {kind}: 2^30 elements; allocating", file=sys.stderr, flush=True)
+    x = _c5_input(n)
+    codes = torch.empty(n, dtype=torch.uint8, device="cuda")
+    scales = torch.empty(nb, dtype=torch.float32, device="cuda")
+
+    def quantize():
+        _lib.check(L.rf_blockwise_quantize(0, x.data_ptr(), n, BS, 0, 0, 0, None, codes.data_ptr(),
+                                           scales.data_ptr(), sp()), "quantize")
+
+    if kind == "quantize":
+        step = quantize
+        nbytes = n * 4 + n + nb * 4
+    elif kind == "dequantize":
+        quantize()
+        out = torch.empty(n, dtype=torch.float32, device="cuda")
+
+        def step():
+            _lib.check(L.rf_blockwise_dequantize(0, codes.data_ptr(), scales.data_ptr(), n, BS, _lib.RF_F32,
+                                                 out.data_ptr(), sp()), "dequantize")
+        nbytes = n + nb * 4 + n * 4
+    elif kind == "sr_bf16":
+        out = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+
+        def step():
+            _lib.check(L.rf_sr_bf16(x.data_ptr(), n, 0, 42, None, out.data_ptr(), sp()), "sr_bf16")
+        nbytes = n * 4 + n * 2
+    else:
+        raise ValueError(kind)
+    name = f"{kind}_2p30_f32"
+    return Workload(name, n, "elements/s", nbytes, step,
+                    {"workload": name, "elements": n, "block_size": BS, "quantizer": "dynamic_signed",
+                     "input": "log-uniform |x| in [1e-8, 1e2], random sign", "launches_per_step": 1},
+                    lambda: cpu_baseline_kernel(kind, args.cpu_seconds),
+                    f"{kind} elements/sec + achieved HBM GB/s, 2^30 f32, 1 GPU")
+
+
+WORKLOADS = {
+    "llama7b": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8", param_sr=a.param_sr),
+    "gpt2": lambda a: _tree_workload(a, gpt2_small_shapes, "gpt2_small_bf16_adamw8", param_sr=True),
+    "ragged": lambda a: _tree_workload(a, ragged_shapes, "ragged_2256_leaves_bf16_adamw8", param_sr=a.param_sr,
+                                       grads="student_t"),
+    "llama7b_optax": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_optax_update",
+                                              param_sr=False, optax=True),
+    "llama7b_apply": lambda a: _kernel_workload(a, "apply"),
+    "quantize_2p30": lambda a: _kernel_workload(a, "quantize"),
+    "dequantize_2p30": lambda a: _kernel_workload(a, "dequantize"),
+    "sr_bf16_2p30": lambda a: _kernel_workload(a, "sr_bf16"),
+}
 
 
 def main(argv=None):
@@ -174,31 +446,12 @@ def main(argv=None):
 
     import torch
 
-    import rollfast_amd as rf
-
     torch.cuda.set_device(0)
-    shapes_fn, workload = WORKLOADS[args.workload]
-    shapes = shapes_fn()
-    n_params = sum(int(torch.Size(s).numel()) for _, s in shapes)
-    print(f"[bench] {workload}: {n_params} params in {len(shapes)} leaves; allocating", file=sys.stderr, flush=True)
-
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(0)
-    params = {}
-    for name, s in shapes:
-        params[name] = (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 0.02).to(torch.bfloat16)
-    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=args.exact)
-    state = tx.init(params)
-    pool = []
-    for k in range(args.grad_pool):
-        gen.manual_seed(1000 + k)
-        pool.append({name: (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 1e-3)
-                     .to(torch.bfloat16) for name, s in shapes})
+    wl = WORKLOADS[args.workload](args)
     torch.cuda.synchronize()
-    key = rf.prng.PRNGKey(0)
     print(f"[bench] warmup {args.warmup} steps", file=sys.stderr, flush=True)
-    for w in range(args.warmup):
-        params, state = rf.adamw8_step(tx, params, pool[w % len(pool)], state, key=key, stochastic=args.param_sr)
+    for _ in range(args.warmup):
+        wl.step()
     torch.cuda.synchronize()
 
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
@@ -208,16 +461,15 @@ def main(argv=None):
     t0 = time.perf_counter()
     for k in range(args.steps):
         starts[k].record()
-        params, state = rf.adamw8_step(tx, params, pool[k % len(pool)], state, key=key, stochastic=args.param_sr)
+        wl.step()
         ends[k].record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / args.steps
     kernel_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     kernel_ms_avg = sum(kernel_ms) / len(kernel_ms)
-    bytes_step = algorithmic_bytes(shapes)
-    achieved = bytes_step / (kernel_ms_avg * 1e-3)
-    value = n_params / (ms_per_step * 1e-3)
+    achieved = wl.nbytes / (kernel_ms_avg * 1e-3)
+    value = wl.units / (ms_per_step * 1e-3)
     print(f"[bench] {ms_per_step:.3f} ms/step wall, {kernel_ms_avg:.3f} ms/step events, "
           f"{achieved / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
 
@@ -234,13 +486,13 @@ def main(argv=None):
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] CPU oracle baseline", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(args.cpu_seconds)
+        cpu = wl.cpu()
 
-    traffic = profiled_traffic(workload, args.exact, args.param_sr)
+    traffic = profiled_traffic(wl.name, args.exact, args.param_sr)
     line = {
-        "metric": METRIC,
+        "metric": wl.metric,
         "value": value,
-        "unit": "params/s",
+        "unit": wl.unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -250,19 +502,7 @@ def main(argv=None):
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {
-            "workload": workload,
-            "params": n_params,
-            "leaves": len(shapes),
-            "block_size": 2048,
-            "param_dtype": "bf16",
-            "grad_dtype": "bf16",
-            "moments": "uint8 codebook codes + f32 block scales",
-            "param_rounding": "stochastic" if args.param_sr else "nearest-even",
-            "direction": "ieee" if args.exact else "hw rcp/sqrt",
-            "launches_per_step": 1,
-            "grad_pool": len(pool),
-        },
+        "config": wl.config,
         "roofline": {
             "bound": "hbm",
             "achieved": achieved / 1e9,
@@ -271,7 +511,7 @@ def main(argv=None):
             "frac": achieved / HBM_PEAK,
             "traffic": traffic,
             "traffic_source": "profiles/ rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated" if traffic else None,
-            "algorithmic_bytes_per_step": bytes_step,
+            "algorithmic_bytes_per_step": wl.nbytes,
             "kernel_ms": kernel_ms_avg,
         },
         "cpu_baseline": cpu,

@@ -150,24 +150,39 @@ __global__ __launch_bounds__(WG) void k_dequantize(int32_t quantizer, const uint
     const int64_t nthreads = (int64_t)gridDim.x * WG;
     const bool sym = quantizer == RF_Q_SYMMETRIC_INT8;
     const int64_t ngroups = vec_ok ? size / 8 : 0;
-    for (int64_t gi = tid; gi < ngroups; gi += nthreads) {
-        const int64_t e0 = gi * 8;
-        const uint2 w = *(const uint2*)(values + e0);
-        const float s = scales[e0 / bs];  // bs % 8 == 0: the 8 elements share a block
-        float o[8];
+    // Four 8-element groups per thread and iteration, loads issued first:
+    // the code reads (1/5 of the traffic) must not serialise the writes.
+    constexpr int U = 4;
+    for (int64_t g0 = tid; g0 < ngroups; g0 += U * nthreads) {
+        uint2 w[U];
+        float s[U];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const uint32_t cbyte = ((t < 4 ? w.x : w.y) >> (8 * (t & 3))) & 0xFFu;
-            const float val = sym ? (float)(int8_t)cbyte : cb[cbyte];
-            o[t] = val * s;
+        for (int u = 0; u < U; ++u) {
+            const int64_t gi = g0 + u * nthreads;
+            if (gi < ngroups) {
+                w[u] = *(const uint2*)(values + gi * 8);
+                s[u] = scales[gi * 8 / bs];  // bs % 8 == 0: the 8 elements share a block
+            }
         }
-        if (out_dtype == RF_BF16) {
-            uint32_t hb[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) hb[t] = f32_to_bf16_rne(o[t]);
-            store8_bf16(out, e0, hb);
-        } else {
-            store8_f32(out, e0, o);
+        for (int u = 0; u < U; ++u) {
+            const int64_t gi = g0 + u * nthreads;
+            if (gi >= ngroups) break;
+            float o[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t cbyte = ((t < 4 ? w[u].x : w[u].y) >> (8 * (t & 3))) & 0xFFu;
+                const float val = sym ? (float)(int8_t)cbyte : cb[cbyte];
+                o[t] = val * s[u];
+            }
+            if (out_dtype == RF_BF16) {
+                uint32_t hb[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) hb[t] = f32_to_bf16_rne(o[t]);
+                store8_bf16(out, gi * 8, hb);
+            } else {
+                store8_f32(out, gi * 8, o);
+            }
         }
     }
     for (int64_t e = ngroups * 8 + tid; e < size; e += nthreads) {
@@ -207,7 +222,16 @@ __global__ __launch_bounds__(WG) void k_sr_bf16(const float* __restrict__ x, int
 }
 
 // apply_updates over a leaf table (utils.py:648-708): one workgroup-stride
-// loop per leaf (blockIdx.y = leaf).
+// loop per leaf (blockIdx.y = leaf); 8 elements per thread and iteration when
+// the leaf's buffers are 16-byte aligned.
+__device__ __forceinline__ uint32_t apply_bf16(float p, float u, bool stochastic, const uint32_t* bits, uint32_t lk0,
+                                               uint32_t lk1, int64_t e)
+{
+    const float s = p + u;
+    if (!stochastic) return f32_to_bf16_rne(s);
+    return sr_bf16(s, bits ? bits[e] : jax_bits(lk0, lk1, (uint64_t)e));
+}
+
 __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ leaves, int32_t stochastic,
                                               uint32_t k0, uint32_t k1)
 {
@@ -216,14 +240,39 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
     if (stochastic) jax_split(k0, k1, (uint32_t)L.param_index, lk0, lk1);
     const int64_t tid = (int64_t)blockIdx.x * WG + threadIdx.x;
     const int64_t nthreads = (int64_t)gridDim.x * WG;
-    for (int64_t e = tid; e < L.size; e += nthreads) {
+    const bool sr = stochastic != 0;
+    const bool vec = ((uintptr_t)L.param % 16 == 0) && ((uintptr_t)L.updates % 16 == 0) &&
+                     (!L.bits || (uintptr_t)L.bits % 16 == 0);
+    const int64_t ngroups = vec ? L.size / 8 : 0;
+    for (int64_t gi = tid; gi < ngroups; gi += nthreads) {
+        const int64_t e0 = gi * 8;
+        float u[8], p[8];
+        load8<float>(L.updates, e0, u);
+        if (L.param_dtype == RF_BF16) {
+            load8<uint16_t>(L.param, e0, p);
+            uint32_t h[8];
+            if (sr && L.bits) {
+                uint32_t rb[8];
+                load8_u32(L.bits, e0, rb);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) h[t] = sr_bf16(p[t] + u[t], rb[t]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) h[t] = apply_bf16(p[t], u[t], sr, nullptr, lk0, lk1, e0 + t);
+            }
+            store8_bf16(L.param, e0, h);
+        } else {
+            load8<float>(L.param, e0, p);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) p[t] = p[t] + u[t];
+            store8_f32(L.param, e0, p);
+        }
+    }
+    for (int64_t e = ngroups * 8 + tid; e < L.size; e += nthreads) {
         const float u = L.updates[e];
         if (L.param_dtype == RF_BF16) {
-            const float s = bf16_bits_to_f32(((const uint16_t*)L.param)[e]) + u;
-            uint32_t r;
-            if (stochastic) r = sr_bf16(s, L.bits ? L.bits[e] : jax_bits(lk0, lk1, (uint64_t)e));
-            else r = f32_to_bf16_rne(s);
-            ((uint16_t*)L.param)[e] = (uint16_t)r;
+            const float p = bf16_bits_to_f32(((const uint16_t*)L.param)[e]);
+            ((uint16_t*)L.param)[e] = (uint16_t)apply_bf16(p, u, sr, L.bits, lk0, lk1, e);
         } else {
             ((float*)L.param)[e] = ((const float*)L.param)[e] + u;
         }
@@ -518,6 +567,8 @@ struct rf_adam8_plan {
 
 namespace {
 
+bool release_plan(rf_adam8_plan* plan);
+
 rf_status validate_leaf(const rf_adam8_leaf& L, int32_t i, int32_t apply)
 {
     const std::string at = "leaf " + std::to_string(i) + ": ";
@@ -651,8 +702,10 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
         segs.push_back(sentinel);
     }
 
+    int device = 0;
+    HIP_TRY(hipGetDevice(&device));
     rf_adam8_plan* p = new rf_adam8_plan();
-    HIP_TRY(hipGetDevice(&p->device));
+    p->device = device;
     p->apply = apply ? 1 : 0;
     p->n_leaves = n_leaves;
     p->total_units = units;
@@ -662,17 +715,23 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     p->any_moment_bits = any_mb;
     p->shape.assign(leaves, leaves + n_leaves);
     p->vec = vecs;
-    hipError_t e1 = hipMalloc(&p->d_leaves, sizeof(rf_adam8_leaf) * (size_t)std::max(n_leaves, 1));
-    hipError_t e2 = hipMalloc(&p->d_segs, sizeof(Seg) * segs.size());
-    if (e1 != hipSuccess || e2 != hipSuccess) {
-        if (p->d_leaves) (void)hipFree(p->d_leaves);
-        if (p->d_segs) (void)hipFree(p->d_segs);
-        delete p;
-        return fail(RF_ERR_HIP, "hipMalloc of the plan tables failed");
+    // Every buffer a run needs is allocated here, so runs never allocate
+    // (pinned-host and device allocation synchronise the device).
+    const size_t table_bytes = sizeof(rf_adam8_leaf) * (size_t)std::max(n_leaves, 1);
+    hipError_t e = hipMalloc(&p->d_leaves, table_bytes);
+    if (e == hipSuccess) e = hipMalloc(&p->d_segs, sizeof(Seg) * segs.size());
+    for (RingSlot& slot : p->ring) {
+        if (e == hipSuccess) e = hipHostMalloc((void**)&slot.host, table_bytes, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipMalloc((void**)&slot.dev, table_bytes);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&slot.ev, hipEventDisableTiming);
     }
-    if (n_leaves > 0)
-        HIP_TRY(hipMemcpy(p->d_leaves, leaves, sizeof(rf_adam8_leaf) * (size_t)n_leaves, hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(p->d_segs, segs.data(), sizeof(Seg) * segs.size(), hipMemcpyHostToDevice));
+    if (e == hipSuccess && n_leaves > 0)
+        e = hipMemcpy(p->d_leaves, leaves, sizeof(rf_adam8_leaf) * (size_t)n_leaves, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(p->d_segs, segs.data(), sizeof(Seg) * segs.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        release_plan(p);
+        return fail(RF_ERR_HIP, std::string("plan allocation: ") + hipGetErrorString(e));
+    }
     *out_plan = p;
     return RF_OK;
 }
@@ -756,6 +815,25 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
     return RF_OK;
 }
 
+// Frees everything a plan owns (waiting for runs still in flight) and the
+// plan itself; true when every free succeeded.  Current device = plan's.
+bool release_plan(rf_adam8_plan* plan)
+{
+    bool ok = true;
+    for (RingSlot& slot : plan->ring) {
+        if (slot.ev) {
+            if (slot.pending) (void)hipEventSynchronize(slot.ev);
+            (void)hipEventDestroy(slot.ev);
+        }
+        if (slot.dev) ok &= hipFree(slot.dev) == hipSuccess;
+        if (slot.host) ok &= hipHostFree(slot.host) == hipSuccess;
+    }
+    if (plan->d_leaves) ok &= hipFree(plan->d_leaves) == hipSuccess;
+    if (plan->d_segs) ok &= hipFree(plan->d_segs) == hipSuccess;
+    delete plan;
+    return ok;
+}
+
 bool same_structure(const rf_adam8_leaf& a, const rf_adam8_leaf& b)
 {
     return a.size == b.size && a.block_size == b.block_size && a.param_dtype == b.param_dtype &&
@@ -802,11 +880,6 @@ rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* lea
     RingSlot& slot = plan->ring[plan->next % RING];
     plan->next++;
     const size_t bytes = sizeof(rf_adam8_leaf) * (size_t)n_leaves;
-    if (!slot.host) {
-        HIP_TRY(hipHostMalloc((void**)&slot.host, bytes, hipHostMallocDefault));
-        HIP_TRY(hipMalloc((void**)&slot.dev, bytes));
-        HIP_TRY(hipEventCreateWithFlags(&slot.ev, hipEventDisableTiming));
-    }
     if (slot.pending) HIP_TRY(hipEventSynchronize(slot.ev));
     std::memcpy(slot.host, leaves, bytes);
     HIP_TRY(hipMemcpyAsync(slot.dev, slot.host, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
@@ -821,20 +894,11 @@ rf_status rf_adam8_plan_destroy(rf_adam8_plan* plan)
     if (!plan) return RF_OK;
     int cur = 0;
     HIP_TRY(hipGetDevice(&cur));
-    if (cur != plan->device) HIP_TRY(hipSetDevice(plan->device));
-    hipError_t e1 = hipFree(plan->d_leaves);
-    hipError_t e2 = hipFree(plan->d_segs);
-    for (RingSlot& slot : plan->ring) {
-        if (slot.ev) {
-            (void)hipEventSynchronize(slot.ev);
-            (void)hipEventDestroy(slot.ev);
-        }
-        if (slot.dev) (void)hipFree(slot.dev);
-        if (slot.host) (void)hipHostFree(slot.host);
-    }
-    if (cur != plan->device) (void)hipSetDevice(cur);
-    delete plan;
-    if (e1 != hipSuccess || e2 != hipSuccess) return fail(RF_ERR_HIP, "hipFree of the plan tables failed");
+    const int dev = plan->device;
+    if (cur != dev) HIP_TRY(hipSetDevice(dev));
+    const bool ok = release_plan(plan);
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (!ok) return fail(RF_ERR_HIP, "hipFree of the plan tables failed");
     return RF_OK;
 }
 

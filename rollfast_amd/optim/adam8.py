@@ -24,6 +24,7 @@ from __future__ import annotations
 import ctypes
 import dataclasses
 import math
+import weakref
 from typing import Any, Callable, Literal, NamedTuple, Optional, Union
 
 import numpy as np
@@ -457,12 +458,186 @@ def _aligned(t, a: int) -> bool:
     return t is None or t.data_ptr() % a == 0
 
 
+def _buffer_ptrs(m, v, p) -> tuple:
+    """Device addresses of a leaf's moment buffers and param."""
+    if isinstance(m, QuantizedBlocks):
+        t = (m.values.data_ptr(), m.scales.data_ptr(), v.values.data_ptr(), v.scales.data_ptr())
+    else:
+        t = (m.data_ptr(), v.data_ptr())
+    return t + ((p.data_ptr(),) if p is not None else ())
+
+
 class _Engine:
-    """Builds the leaf table for a step and launches it (one launch per tree)."""
+    """Builds the leaf table for a step and launches it (one launch per tree).
+
+    The table of the previous call is kept with weak references to the
+    tensors it points at.  When the next call passes the same tree structure,
+    the same param and moment objects (updated in place, as this API does)
+    and grads of the same dtypes and sizes, only the grad pointers are
+    rewritten: the per-leaf validation of the first call is not repeated.
+    """
 
     def __init__(self, cfg: _Config):
         self.cfg = cfg
         self._plans: dict = {}
+        self._last = None
+
+    # -- full table build (first call, or anything changed) -----------------
+    def _build_rows(self, g_leaves, mu_leaves, nu_leaves, p_leaves, *, apply, decay_mask, random_bits):
+        torch = _torch()
+        n = len(g_leaves)
+        out_leaves: list = [None] * n
+        rows = []
+        structure = []
+        refs = []
+        device = None
+        for i in range(n):
+            g, m, v = g_leaves[i], mu_leaves[i], nu_leaves[i]
+            if _is_passthrough_leaf(m) or _is_passthrough_leaf(g):
+                out_leaves[i] = m if _is_passthrough_leaf(m) else g
+                continue
+            _require_device_tensor(g, "gradient")
+            if device is None:
+                device = g.device
+            if g.device != device:
+                raise ValueError("all leaves must live on the same device")
+            gdt = _rf_dtype(g.dtype, "gradient")
+            if not g.is_contiguous():
+                g = g.contiguous()
+            size = int(g.numel())
+            row = _lib.Adam8Leaf()
+            row.grad = g.data_ptr()
+            row.size = size
+            row.grad_dtype = gdt
+            row.state_index = i
+            row.param_index = i
+            decays = bool(decay_mask[i]) if decay_mask is not None else False
+            p = p_leaves[i] if p_leaves is not None else None
+            if (apply or decays) and (p is None or _is_passthrough_leaf(p)):
+                raise ValueError(NO_PARAMS_MSG)
+            if apply or decays:
+                _require_device_tensor(p, "param")
+                if p.device != device:
+                    raise ValueError("all leaves must live on the same device")
+                if not p.is_contiguous():
+                    raise ValueError("params must be contiguous (they are updated in place)")
+                if int(p.numel()) != size:
+                    raise ValueError(f"param and gradient sizes differ ({p.numel()} vs {size})")
+                row.param = p.data_ptr()
+                row.param_dtype = _rf_dtype(p.dtype, "param")
+            else:
+                p = None
+                row.param_dtype = _lib.RF_F32
+            row.flags = _lib.RF_LEAF_DECAY if decays else 0
+            if isinstance(m, QuantizedBlocks):
+                if not isinstance(v, QuantizedBlocks):
+                    raise ValueError("first and second moment leaves differ in kind")
+                if m.codebook_id != DYNAMIC_SIGNED_CODEBOOK_ID or v.codebook_id != DYNAMIC_UNSIGNED_CODEBOOK_ID:
+                    raise NotImplementedError("moment leaves must use the dynamic signed/unsigned codebooks")
+                if m.size != size or v.size != size or m.block_size != v.block_size:
+                    raise ValueError("quantized moment leaf does not match its gradient")
+                for t in (m.values, v.values, m.scales, v.scales):
+                    _require_device_tensor(t, "moment")
+                    if t.device != device:
+                        raise ValueError("all leaves must live on the same device")
+                    if not t.is_contiguous():
+                        raise ValueError("moment buffers must be contiguous (they are updated in place)")
+                if m.scales.dtype != torch.float32 or v.scales.dtype != torch.float32:
+                    raise NotImplementedError("only float32 block scales are implemented")
+                nb = max(1, math.ceil(size / m.block_size))
+                for t, want in ((m.values, nb * m.block_size), (v.values, nb * m.block_size), (m.scales, nb),
+                                (v.scales, nb)):
+                    if int(t.numel()) != want:
+                        raise ValueError("quantized moment buffers do not match size and block_size")
+                row.moment_kind = _lib.RF_MOMENT_QUANTIZED
+                row.block_size = int(m.block_size)
+                row.mu = m.values.data_ptr()
+                row.mu_scales = m.scales.data_ptr()
+                row.nu = v.values.data_ptr()
+                row.nu_scales = v.scales.data_ptr()
+                align_ok = m.values.data_ptr() % 8 == 0 and v.values.data_ptr() % 8 == 0
+            else:
+                _require_device_tensor(m, "first moment")
+                _require_device_tensor(v, "second moment")
+                if m.device != device or v.device != device:
+                    raise ValueError("all leaves must live on the same device")
+                if m.dtype != v.dtype or int(m.numel()) != size or int(v.numel()) != size:
+                    raise ValueError("fallback moment leaf does not match its gradient")
+                if not (m.is_contiguous() and v.is_contiguous()):
+                    raise ValueError("moment buffers must be contiguous (they are updated in place)")
+                if m.dtype not in (torch.float32, torch.bfloat16):
+                    raise NotImplementedError(f"fallback moment dtype {m.dtype} is not supported")
+                row.moment_kind = _lib.RF_MOMENT_BF16 if m.dtype == torch.bfloat16 else _lib.RF_MOMENT_F32
+                row.mu = m.data_ptr()
+                row.nu = v.data_ptr()
+                align_ok = m.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0
+            out = None
+            if not apply:
+                out = torch.empty(g.shape, dtype=torch.float32, device=g.device)
+                row.updates = out.data_ptr()
+                out_leaves[i] = out
+            if random_bits is not None and i in random_bits:
+                mb, vb, pb = random_bits[i]
+                row.mu_bits = _ptr(mb)
+                row.nu_bits = _ptr(vb)
+                row.param_bits = _ptr(pb)
+            align_ok = (
+                align_ok
+                and g.data_ptr() % 16 == 0
+                and (row.param is None or row.param % 16 == 0)
+                and (out is None or out.data_ptr() % 16 == 0)
+            )
+            rows.append(row)
+            structure.append((size, row.block_size, row.param_dtype, gdt, row.moment_kind, i, row.flags, align_ok,
+                              row.mu_bits is not None or row.nu_bits is not None, row.param_bits is not None))
+            refs.append((i, weakref.ref(m), weakref.ref(v), None if p is None else weakref.ref(p),
+                         g.dtype, size, align_ok, _buffer_ptrs(m, v, p)))
+        return rows, structure, refs, out_leaves, device
+
+    # -- cached table (same objects as the previous call) -------------------
+    def _reuse_rows(self, last, g_leaves, mu_leaves, nu_leaves, p_leaves, apply):
+        """Rewrites the grad (and, update-only mode, output) pointers of the
+        previous table when every other buffer is the same object; returns
+        the out-leaf list, or None when anything differs."""
+        torch = _torch()
+        table = last["table"]
+        device = last["device"]
+        n = len(g_leaves)
+        out_leaves: list = [None] * n
+        j = 0
+        refs = last["refs"]
+        for i in range(n):
+            g, m, v = g_leaves[i], mu_leaves[i], nu_leaves[i]
+            if j < len(refs) and refs[j][0] == i:
+                _, mref, vref, pref, gdtype, size, align_ok, ptrs = refs[j]
+                if mref() is not m or vref() is not v:
+                    return None
+                p = None
+                if pref is not None:
+                    p = p_leaves[i] if p_leaves is not None else None
+                    if pref() is not p:
+                        return None
+                # same objects, same storage (a `.data` swap changes the pointer)
+                if _buffer_ptrs(m, v, p) != ptrs:
+                    return None
+                if (not isinstance(g, torch.Tensor) or g.dtype != gdtype or g.device != device
+                        or g.numel() != size or not g.is_contiguous()):
+                    return None
+                gp = g.data_ptr()
+                if align_ok and gp % 16:
+                    return None
+                row = table[j]
+                row.grad = gp
+                if not apply:
+                    out = torch.empty(g.shape, dtype=torch.float32, device=device)
+                    row.updates = out.data_ptr()
+                    out_leaves[i] = out
+                j += 1
+            else:
+                if not (_is_passthrough_leaf(m) or _is_passthrough_leaf(g)):
+                    return None
+                out_leaves[i] = m if _is_passthrough_leaf(m) else g
+        return out_leaves if j == len(refs) else None
 
     def run(
         self,
@@ -493,98 +668,34 @@ class _Engine:
         if params is not None:
             p_leaves = _tree.flatten_up_to(g_td, params)
 
-        n = len(g_leaves)
-        out_leaves: list = [None] * n
-        table_rows = []
-        structure = []
-        device = None
-        for i in range(n):
-            g, m, v = g_leaves[i], mu_leaves[i], nu_leaves[i]
-            if _is_passthrough_leaf(m) or _is_passthrough_leaf(g):
-                out_leaves[i] = m if _is_passthrough_leaf(m) else g
-                continue
-            _require_device_tensor(g, "gradient")
-            if device is None:
-                device = g.device
-            if g.device != device:
-                raise ValueError("all leaves must live on the same device")
-            gdt = _rf_dtype(g.dtype, "gradient")
-            if not g.is_contiguous():
-                g = g.contiguous()
-            size = int(g.numel())
-            row = _lib.Adam8Leaf()
-            row.grad = g.data_ptr()
-            row.size = size
-            row.grad_dtype = gdt
-            row.state_index = i
-            row.param_index = i
-            decays = bool(decay_mask[i]) if decay_mask is not None else False
-            p = p_leaves[i] if p_leaves is not None else None
-            if (apply or decays) and (p is None or _is_passthrough_leaf(p)):
-                raise ValueError(NO_PARAMS_MSG)
-            if apply or decays:
-                _require_device_tensor(p, "param")
-                if not p.is_contiguous():
-                    raise ValueError("params must be contiguous (they are updated in place)")
-                if int(p.numel()) != size:
-                    raise ValueError(f"param and gradient sizes differ ({p.numel()} vs {size})")
-                row.param = p.data_ptr()
-                row.param_dtype = _rf_dtype(p.dtype, "param")
-            else:
-                row.param_dtype = _lib.RF_F32
-            row.flags = _lib.RF_LEAF_DECAY if decays else 0
-            if isinstance(m, QuantizedBlocks):
-                if not isinstance(v, QuantizedBlocks):
-                    raise ValueError("first and second moment leaves differ in kind")
-                if m.codebook_id != DYNAMIC_SIGNED_CODEBOOK_ID or v.codebook_id != DYNAMIC_UNSIGNED_CODEBOOK_ID:
-                    raise NotImplementedError("moment leaves must use the dynamic signed/unsigned codebooks")
-                if m.size != size or v.size != size or m.block_size != v.block_size:
-                    raise ValueError("quantized moment leaf does not match its gradient")
-                for t in (m.values, v.values, m.scales, v.scales):
-                    _require_device_tensor(t, "moment")
-                    if not t.is_contiguous():
-                        raise ValueError("moment buffers must be contiguous (they are updated in place)")
-                if m.scales.dtype != torch.float32 or v.scales.dtype != torch.float32:
-                    raise NotImplementedError("only float32 block scales are implemented")
-                row.moment_kind = _lib.RF_MOMENT_QUANTIZED
-                row.block_size = int(m.block_size)
-                row.mu = m.values.data_ptr()
-                row.mu_scales = m.scales.data_ptr()
-                row.nu = v.values.data_ptr()
-                row.nu_scales = v.scales.data_ptr()
-                align_ok = m.values.data_ptr() % 8 == 0 and v.values.data_ptr() % 8 == 0
-            else:
-                _require_device_tensor(m, "first moment")
-                _require_device_tensor(v, "second moment")
-                if m.dtype != v.dtype or int(m.numel()) != size or int(v.numel()) != size:
-                    raise ValueError("fallback moment leaf does not match its gradient")
-                if not (m.is_contiguous() and v.is_contiguous()):
-                    raise ValueError("moment buffers must be contiguous (they are updated in place)")
-                row.moment_kind = _lib.RF_MOMENT_BF16 if m.dtype == torch.bfloat16 else _lib.RF_MOMENT_F32
-                if m.dtype not in (torch.float32, torch.bfloat16):
-                    raise NotImplementedError(f"fallback moment dtype {m.dtype} is not supported")
-                row.mu = m.data_ptr()
-                row.nu = v.data_ptr()
-                align_ok = m.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0
-            out = None
-            if not apply:
-                out = torch.empty(g.shape, dtype=torch.float32, device=g.device)
-                row.updates = out.data_ptr()
-                out_leaves[i] = out
-            if random_bits is not None and i in random_bits:
-                mb, nb, pb = random_bits[i]
-                row.mu_bits = _ptr(mb)
-                row.nu_bits = _ptr(nb)
-                row.param_bits = _ptr(pb)
-            align_ok = (
-                align_ok
-                and g.data_ptr() % 16 == 0
-                and (row.param is None or row.param % 16 == 0)
-                and (out is None or out.data_ptr() % 16 == 0)
-            )
-            table_rows.append(row)
-            structure.append((size, row.block_size, row.param_dtype, gdt, row.moment_kind, i, row.flags, align_ok,
-                              row.mu_bits is not None or row.nu_bits is not None, row.param_bits is not None))
+        mask_key = None if decay_mask is None else tuple(decay_mask)
+        last = self._last
+        out_leaves = None
+        if (last is not None and random_bits is None and last["apply"] == apply and last["mask"] == mask_key
+                and last["td"] == g_td):
+            out_leaves = self._reuse_rows(last, g_leaves, mu_leaves, nu_leaves, p_leaves, apply)
+        if out_leaves is not None:
+            table, n_rows, device, plan = last["table"], last["n"], last["device"], last["plan"]
+        else:
+            self._last = None
+            rows, structure, refs, out_leaves, device = self._build_rows(
+                g_leaves, mu_leaves, nu_leaves, p_leaves, apply=apply, decay_mask=decay_mask,
+                random_bits=random_bits)
+            n_rows = len(rows)
+            table = (_lib.Adam8Leaf * n_rows)(*rows) if rows else None
+            plan = None
+            if rows:
+                skey = (bool(apply), device.index, tuple(structure))
+                plan = self._plans.get(skey)
+                if plan is None:
+                    with torch.cuda.device(device):
+                        plan = _LeafPlan(table, n_rows, apply)
+                    if len(self._plans) > 64:
+                        self._plans.clear()
+                    self._plans[skey] = plan
+                if random_bits is None:
+                    self._last = {"apply": apply, "mask": mask_key, "td": g_td, "refs": refs, "table": table,
+                                  "n": n_rows, "device": device, "plan": plan}
 
         flags = 0
         if cfg.nesterov:
@@ -621,16 +732,8 @@ class _Engine:
             pk = prng.as_key(param_key)
             hp.key_param[0], hp.key_param[1] = int(pk[0]), int(pk[1])
 
-        if table_rows:
-            table = (_lib.Adam8Leaf * len(table_rows))(*table_rows)
-            skey = (bool(apply), device.index, tuple(structure))
-            plan = self._plans.get(skey)
+        if n_rows:
             with torch.cuda.device(device):
-                if plan is None:
-                    plan = _LeafPlan(table, len(table_rows), apply)
-                    if len(self._plans) > 64:
-                        self._plans.clear()
-                    self._plans[skey] = plan
                 plan.run(table, hp, _lib.stream_ptr())
 
         new_state = ScaleByAdam8State(

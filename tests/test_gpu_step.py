@@ -340,3 +340,54 @@ def test_state_key_and_count_evolve_like_reference():
         k = orc.split(k, 3)[2]
         np.testing.assert_array_equal(st[0].key, k)
         assert int(st[0].count) == t
+
+
+def test_cached_leaf_table_follows_changes():
+    """The host reuses the previous step's leaf table when the same param and
+    moment objects come back; every kind of change must still reach the
+    kernel: a grad dtype change, params rebuilt as new tensors, a moment leaf
+    replaced by a copy, a param's storage swapped with ``.data``.  Each step
+    is compared with the oracle (bit-exact: exact mode)."""
+    import dataclasses
+
+    import torch
+
+    rf = _rf()
+    spec = [((8, 2048), "bf16", "bf16"), ((3, 3000), "f32", "bf16"), ((700,), "bf16", "bf16")]
+    host_params, params = _build(spec, 5)
+    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=True)
+    state = tx.init(params)
+
+    def change_grad_dtype(params, state):
+        return params, state, [((8, 2048), "bf16", "f32"), spec[1], spec[2]]
+
+    def new_param_tensors(params, state):
+        return {k: v.clone() for k, v in params.items()}, state, spec
+
+    def copy_moment_leaf(params, state):
+        adam = state[0]
+        m = adam.mu["l000"]
+        mu = dict(adam.mu)
+        mu["l000"] = dataclasses.replace(m, values=m.values.clone(), scales=m.scales.clone())
+        return params, (adam._replace(mu=mu),) + tuple(state[1:]), spec
+
+    def swap_param_storage(params, state):
+        params["l001"].data = params["l001"].clone()
+        return params, state, spec
+
+    plan = [None, None, change_grad_dtype, None, new_param_tensors, copy_moment_leaf, None, swap_param_storage,
+            None]
+    for step, mutate in enumerate(plan):
+        gspec = spec
+        if mutate is not None:
+            params, state, gspec = mutate(params, state)
+        ghost, gdev = _grads(gspec, 77 + step)
+        for i in range(len(spec)):
+            host_params[f"l{i:03d}"] = to_host(params[f"l{i:03d}"]).copy()
+        tree = _oracle_from_state(gspec, host_params, state[0])
+        before = [L["param"].copy() for L in tree.leaves]
+        tree.step(ghost, weight_decay=0.01, lr=1e-3, count=int(state[0].count) + 1)
+        params, state = rf.adamw8_step(tx, params, gdev, state, stochastic=False)
+        torch.cuda.synchronize()
+        _compare_state(gspec, tree, state[0], f"step {step + 1}")
+        _compare_params(gspec, tree, params, True, f"step {step + 1}", before)
