@@ -1,0 +1,187 @@
+"""GPU parity at the benchmark configurations' real shapes.
+
+* GPT-2-small bf16 tree (74 leaves, LayerNorms on f32 fallback moments),
+  param stochastic rounding with in-kernel Threefry bits, 2 steps.
+* The ragged tree (2256 leaves, most below min_size; Student-t(3) grads with
+  log-uniform per-leaf scales and 10 % all-zero blocks), 2 steps.
+* Full-size Llama-7B leaves (embedding 32000x4096 and one decoder layer:
+  q/k/v/o 4096^2, gate/up/down 11008x4096, two RMSNorm vectors), 1 step.
+* 2^30-element quantize / dequantize / bf16 SR (log-uniform magnitudes
+  1e-8..1e2, random sign).
+
+Bar: codes, scales and fallback moments bit-exact; params within one bf16
+ulp (hardware rcp/sqrt direction); SR outputs bitwise for identical bits.
+Size-independent properties back the byte checks at 2^30: the reference's
+dequantization error bound (|x - deq| <= 0.01 * block scale,
+tests/test_adam8.py:65) and SR unbiasedness.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests._helpers import OracleTree, bf16_ulp_distance, to_device, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _shapes(kind):
+    import bench
+
+    return {"gpt2": bench.gpt2_small_shapes, "ragged": bench.ragged_shapes,
+            "llama_slice": lambda: [(n, s) for n, s in bench.llama7b_shapes()
+                                    if n == "embed" or n.startswith("layer00.")]}[kind]()
+
+
+def _grads_host(rng, shapes, kind):
+    out = []
+    for _, s in shapes:
+        n = int(np.prod(s))
+        if kind == "student_t":
+            z = rng.standard_normal(n).astype(np.float32)
+            c = (rng.standard_normal((3, n)).astype(np.float32) ** 2).sum(axis=0) / np.float32(3)
+            g = (z / np.sqrt(c) * np.float32(np.exp(rng.uniform(np.log(1e-6), 0.0)))).astype(np.float32)
+            nb = n // 2048
+            if nb:
+                zero = np.nonzero(rng.random(nb) < 0.1)[0]
+                for b in zero:
+                    g[b * 2048:(b + 1) * 2048] = 0.0
+        else:
+            g = (rng.standard_normal(n).astype(np.float32) * np.float32(1e-3))
+        out.append(orc.f32_to_bf16_bits(g))
+    return out
+
+
+def _tree_run(kind, grads_kind, steps, psr):
+    import torch
+
+    import rollfast_amd as rf
+
+    shapes = _shapes(kind)
+    names = [f"l{i:05d}" for i in range(len(shapes))]
+    rng = np.random.default_rng(42)
+    host_p = [orc.f32_to_bf16_bits(rng.standard_normal(int(np.prod(s))).astype(np.float32) * np.float32(0.02))
+              for _, s in shapes]
+    params = {nm: to_device(h, "bf16").reshape(s) for nm, h, (_, s) in zip(names, host_p, shapes)}
+    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01)
+    state = tx.init(params)
+    leaves = []
+    for nm, (_, s) in zip(names, shapes):
+        n = int(np.prod(s))
+        m, v = state[0].mu[nm], state[0].nu[nm]
+        L = {"pdtype": "bf16", "gdtype": "bf16", "size": n, "param": None}
+        if isinstance(m, rf.QuantizedBlocks):
+            L.update(kind="quant", block_size=2048, mu=to_host(m.values).copy(), mu_scales=to_host(m.scales).copy(),
+                     nu=to_host(v.values).copy(), nu_scales=to_host(v.scales).copy())
+        else:
+            L.update(kind="f32", mu=to_host(m).copy(), nu=to_host(v).copy())
+        leaves.append(L)
+    tree = OracleTree(leaves)
+    for step in range(steps):
+        ghost = _grads_host(rng, shapes, grads_kind)
+        gdev = {nm: to_device(g, "bf16").reshape(s) for nm, g, (_, s) in zip(names, ghost, shapes)}
+        for i, nm in enumerate(names):  # oracle starts from the device params of this step
+            leaves[i]["param"] = to_host(params[nm]).copy()
+        pkey = rf.prng.PRNGKey(1000 + step)
+        p_bits = None
+        if psr:
+            kp = orc.split(tuple(int(k) for k in pkey), len(shapes))
+            p_bits = [orc.random_bits(tuple(kp[i]), leaves[i]["size"]) for i in range(len(shapes))]
+        tree.step(ghost, weight_decay=0.01, lr=1e-3, count=step + 1, param_sr=psr, p_bits=p_bits)
+        params, state = rf.adamw8_step(tx, params, gdev, state, key=pkey if psr else None, stochastic=psr)
+        torch.cuda.synchronize()
+        worst = 0
+        for i, nm in enumerate(names):
+            L = leaves[i]
+            m, v = state[0].mu[nm], state[0].nu[nm]
+            if L["kind"] == "quant":
+                np.testing.assert_array_equal(to_host(m.values), L["mu"], err_msg=f"step {step + 1} {nm} mu codes")
+                np.testing.assert_array_equal(to_host(v.values), L["nu"], err_msg=f"step {step + 1} {nm} nu codes")
+                np.testing.assert_array_equal(to_host(m.scales).view(np.uint32), L["mu_scales"].view(np.uint32))
+                np.testing.assert_array_equal(to_host(v.scales).view(np.uint32), L["nu_scales"].view(np.uint32))
+            else:
+                np.testing.assert_array_equal(to_host(m).view(np.uint32), L["mu"].view(np.uint32))
+                np.testing.assert_array_equal(to_host(v).view(np.uint32), L["nu"].view(np.uint32))
+            d = bf16_ulp_distance(to_host(params[nm]), L["param"])
+            worst = max(worst, int(d.max()))
+        assert worst <= 1, f"step {step + 1}: params differ by {worst} bf16 ulp"
+
+
+def test_gpt2_small_full_tree_param_sr():
+    _tree_run("gpt2", "normal", steps=2, psr=True)
+
+
+def test_ragged_tree_student_t_zero_blocks():
+    _tree_run("ragged", "student_t", steps=2, psr=False)
+
+
+def test_llama_embedding_and_layer_full_size():
+    _tree_run("llama_slice", "normal", steps=1, psr=False)
+
+
+def _c5_input(n, seed=5):
+    import torch
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    x = torch.empty(n, device="cuda").uniform_(float(np.log(1e-8)), float(np.log(1e2)), generator=gen).exp_()
+    x[torch.rand(n, device="cuda", generator=gen) < 0.5] *= -1.0
+    return x
+
+
+def test_quantize_dequantize_2p30_bitexact_and_error_bound():
+    import torch
+
+    import rollfast_amd as rf
+
+    n = 1 << 30
+    x = _c5_input(n)
+    qb = rf.quantize_blocks(x, block_size=2048)
+    back = rf.dequantize_blocks(qb)
+    # size-independent property on the device: the reference's error bound
+    err = (back - x).abs().view(-1, 2048).amax(dim=1)
+    assert bool(torch.all(err <= qb.scales * 0.01))
+    del back, err
+    xh = to_host(x)
+    del x
+    codes, scales = orc.quantize(xh, 2048, orc.Q_SIGNED)
+    np.testing.assert_array_equal(to_host(qb.scales).view(np.uint32), scales.view(np.uint32))
+    got = to_host(qb.values)
+    bad = np.count_nonzero(got != codes.reshape(-1))
+    assert bad == 0, f"{bad} codes differ over 2^30 elements"
+
+
+def test_sr_bf16_2p30_threefry_bitexact_and_unbiased():
+    import torch
+
+    import rollfast_amd as rf
+    from rollfast_amd.utils import _stochastic_round_bf16
+
+    n = 1 << 30
+    x = _c5_input(n, seed=6)
+    key = rf.prng.PRNGKey(9)
+    out = _stochastic_round_bf16(x, key)
+    got = to_host(out)
+    xh = to_host(x)
+    want = orc.sr_bf16(xh, orc.random_bits((int(key[0]), int(key[1])), n))
+    bad = np.count_nonzero(got != want)
+    assert bad == 0, f"{bad} SR outputs differ over 2^30 elements"
+    # unbiasedness: over 64 keys, the mean relative rounding error of a 2^20
+    # slice is zero within 5 standard errors, per magnitude decade
+    m = 1 << 20
+    xs = x[:m]
+    acc = torch.zeros(m, dtype=torch.float64, device="cuda")
+    for s in range(64):
+        r = _stochastic_round_bf16(xs, rf.prng.PRNGKey(100 + s)).to(torch.float64)
+        acc += (r - xs.to(torch.float64)) / xs.to(torch.float64).abs()
+    rel = (acc / 64).cpu().numpy()
+    dec = np.floor(np.log10(np.abs(xh[:m])))
+    for d in np.unique(dec):
+        sel = rel[dec == d]
+        if sel.size < 1000:
+            continue
+        # per-element relative error is at most 2^-7; its mean over 64 draws has
+        # standard deviation <= 2^-7 / 8, and the decade mean divides by sqrt(count)
+        assert abs(sel.mean()) < 5 * (2.0 ** -7 / 8) / np.sqrt(sel.size), (d, sel.mean())
