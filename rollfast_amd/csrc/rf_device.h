@@ -43,6 +43,10 @@ constexpr int64_t CHUNK = 2048;    // elements per fallback (unquantized moment)
 #ifndef RF_STEP_WAVES_PER_EU
 #define RF_STEP_WAVES_PER_EU 3
 #endif
+// Prefetch the next block's first chunk during requantization (1) or not (0).
+#ifndef RF_PREFETCH_NEXT
+#define RF_PREFETCH_NEXT 1
+#endif
 
 enum : int32_t { KIND_QFAST = 0, KIND_QGEN = 1, KIND_FALLBACK = 2 };
 
@@ -193,6 +197,20 @@ __device__ __forceinline__ float div_by_scale(float x, float s, float rs)
     const float q0 = x * rs;
     const float r = __builtin_fmaf(-s, q0, x);
     return __builtin_fmaf(r, rs, q0);
+}
+
+// Threshold-count candidates of a normalised value: the number of decision
+// thresholds at or below the low end of n's cell (signed: per sign).
+__device__ __forceinline__ uint32_t cand_signed(const uint8_t* lds, float n)
+{
+    const uint32_t nb = __float_as_uint(n);
+    const uint32_t idx = __builtin_elementwise_sub_sat((nb >> CELL_SHIFT) & 0xFFFFu, CELL_LO);
+    return lds[L_CANDS + __umul24(nb >> 31, NCELL_PAD) + idx];
+}
+
+__device__ __forceinline__ uint32_t cand_unsigned(const uint8_t* lds, float n)
+{
+    return lds[L_CANDU + __builtin_elementwise_sub_sat(__float_as_uint(n) >> CELL_SHIFT, CELL_LO)];
 }
 
 // Signed dynamic codebook code of x in a block with scale s (fast path;
@@ -563,8 +581,46 @@ __device__ __forceinline__ void decay_and_scale8(const KHp& h, float (&u)[8], co
 // TV[k] = fl(b2 * fl(cb_u[k] * s_v)) -- exactly the first product of each
 // EMA (adam8.py:200-203, :322-335) -- so an element costs one table read per
 // moment instead of a read and two multiplies.
+// Registers of two in-flight 512-element chunks (codes, grads, params).
+template <typename PT, typename GT>
+struct ChunkSlots {
+    uint2 mc[2], vc[2];
+    Raw8<GT> graw[2];
+    Raw8<PT> praw[2];
+};
+
+// Issue the loads of chunk j of block blk of leaf L into slot `slot`.
+template <typename PT, typename GT, bool NEED_P>
+__device__ __forceinline__ void issue_chunk(ChunkSlots<PT, GT>& sl, const rf_adam8_leaf& L, int64_t blk, int j,
+                                            int slot)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t base = blk * FAST_BS;
+    // Per-block uniform base pointers (SGPRs) + 32-bit lane offsets: the
+    // global accesses need no 64-bit address arithmetic per lane.
+    const RF_GLOBAL uint8_t* gB = (const RF_GLOBAL uint8_t*)L.grad + base * (int64_t)sizeof(GT);
+    const RF_GLOBAL uint8_t* pB = (const RF_GLOBAL uint8_t*)L.param + base * (int64_t)sizeof(PT);
+    const RF_GLOBAL uint8_t* mB = (const RF_GLOBAL uint8_t*)L.mu + base;
+    const RF_GLOBAL uint8_t* vB = (const RF_GLOBAL uint8_t*)L.nu + base;
+    const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
+    sl.mc[slot] = *(const RF_GLOBAL uint2*)(mB + eo);
+    sl.vc[slot] = *(const RF_GLOBAL uint2*)(vB + eo);
+    sl.graw[slot].w[0] = *(const RF_GLOBAL uint4*)(gB + eo * sizeof(GT));
+    if constexpr (sizeof(GT) == 4) sl.graw[slot].w[1] = *(const RF_GLOBAL uint4*)(gB + eo * 4 + 16);
+    if constexpr (NEED_P) {
+        sl.praw[slot].w[0] = *(const RF_GLOBAL uint4*)(pB + eo * sizeof(PT));
+        if constexpr (sizeof(PT) == 4) sl.praw[slot].w[1] = *(const RF_GLOBAL uint4*)(pB + eo * 4 + 16);
+    }
+}
+
+// `have0`: slot 0 already holds chunk 0 of this block (prefetched by the
+// previous unit).  `next_blk` >= 0: the wave's next unit is that block of
+// the same leaf; its chunk 0 is loaded into slot 0 while this block is
+// requantized, so the wave keeps memory traffic in flight through the
+// arithmetic-only requantization phase.
 template <typename PT, typename GT, int WDM, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
-__device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h)
+__device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
+                                           ChunkSlots<PT, GT>& sl, bool have0, int64_t next_blk)
 {
     constexpr int J = FAST_BS / 512;
     constexpr bool NEED_P = APPLY || WDM != WD_OFF;
@@ -573,31 +629,11 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     const int64_t base = blk * FAST_BS;
     const float sm_old = L.mu_scales[blk];
     const float sv_old = L.nu_scales[blk];
-
-    // Per-block uniform base pointers (SGPRs) + 32-bit lane offsets: the
-    // global accesses need no 64-bit address arithmetic per lane.
-    const RF_GLOBAL uint8_t* gB = (const RF_GLOBAL uint8_t*)L.grad + base * (int64_t)sizeof(GT);
-    const RF_GLOBAL uint8_t* pB = (const RF_GLOBAL uint8_t*)L.param + base * (int64_t)sizeof(PT);
-    const RF_GLOBAL uint8_t* mB = (const RF_GLOBAL uint8_t*)L.mu + base;
-    const RF_GLOBAL uint8_t* vB = (const RF_GLOBAL uint8_t*)L.nu + base;
+    RF_GLOBAL uint8_t* pB = (RF_GLOBAL uint8_t*)L.param + base * (int64_t)sizeof(PT);
 
     // Chunk j+1's loads are issued before chunk j's arithmetic: two chunks
     // (6 KB for bf16) in flight per wave without holding all four.
-    uint2 mc[2], vc[2];
-    Raw8<GT> graw[2];
-    Raw8<PT> praw[2];
-    auto issue = [&](int j, int slot) {
-        const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
-        mc[slot] = *(const RF_GLOBAL uint2*)(mB + eo);
-        vc[slot] = *(const RF_GLOBAL uint2*)(vB + eo);
-        graw[slot].w[0] = *(const RF_GLOBAL uint4*)(gB + eo * sizeof(GT));
-        if constexpr (sizeof(GT) == 4) graw[slot].w[1] = *(const RF_GLOBAL uint4*)(gB + eo * 4 + 16);
-        if constexpr (NEED_P) {
-            praw[slot].w[0] = *(const RF_GLOBAL uint4*)(pB + eo * sizeof(PT));
-            if constexpr (sizeof(PT) == 4) praw[slot].w[1] = *(const RF_GLOBAL uint4*)(pB + eo * 4 + 16);
-        }
-    };
-    issue(0, 0);
+    if (!have0) issue_chunk<PT, GT, NEED_P>(sl, L, blk, 0, 0);
 
     {
         const float* cbs = (const float*)(c.lds + L_CBS);
@@ -624,11 +660,12 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
         const int64_t e0 = base + j * 512 + lane * 8;
         const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
         const int slot = j & 1;
-        if (j + 1 < J) issue(j + 1, slot ^ 1);
+        if (j + 1 < J) issue_chunk<PT, GT, NEED_P>(sl, L, blk, j + 1, slot ^ 1);
+        else if (next_blk >= 0) issue_chunk<PT, GT, NEED_P>(sl, L, next_blk, 0, 0);  // slot 0 is free
         float g[8], p[8];
-        raw8_unpack<GT>(graw[slot], g);
+        raw8_unpack<GT>(sl.graw[slot], g);
         if constexpr (NEED_P) {
-            raw8_unpack<PT>(praw[slot], p);
+            raw8_unpack<PT>(sl.praw[slot], p);
         } else {
 #pragma unroll
             for (int t = 0; t < 8; ++t) p[t] = 0.0f;
@@ -645,8 +682,8 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
         float u[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const uint32_t cm = ((t < 4 ? mc[slot].x : mc[slot].y) >> (8 * (t & 3))) & 0xFFu;
-            const uint32_t cv = ((t < 4 ? vc[slot].x : vc[slot].y) >> (8 * (t & 3))) & 0xFFu;
+            const uint32_t cm = ((t < 4 ? sl.mc[slot].x : sl.mc[slot].y) >> (8 * (t & 3))) & 0xFFu;
+            const uint32_t cv = ((t < 4 ? sl.vc[slot].x : sl.vc[slot].y) >> (8 * (t & 3))) & 0xFFu;
             const float t2 = h.omb1 * g[t];
             const float mm = TM[cm] + t2;
             const float gg = g[t] * g[t];
@@ -723,11 +760,31 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
+            // Three batched phases (normalise + cell, candidate reads,
+            // threshold reads) keep 16 independent LDS reads in flight
+            // instead of 16 dependent read pairs.
+            float nm[8], nv[8];
             uint32_t cm[8], cv[8];
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                cm[t] = code_signed_fast(c.lds, m[j][t], sm, rsm);
-                cv[t] = code_unsigned_fast(c.lds, v[j][t], sv, rsv);
+                nm[t] = div_by_scale(m[j][t], sm, rsm);
+                nv[t] = div_by_scale(v[j][t], sv, rsv);
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                cm[t] = cand_signed(c.lds, nm[t]);
+                cv[t] = cand_unsigned(c.lds, nv[t]);
+            }
+            float tm[8], tv[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                tm[t] = *(const float*)(c.lds + L_TS + cm[t] * 4u);
+                tv[t] = *(const float*)(c.lds + L_TU + cv[t] * 4u);
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                cm[t] += nm[t] >= tm[t] ? 1u : 0u;
+                cv[t] += nv[t] >= tv[t] ? 1u : 0u;
             }
             uint2 wm, wv;
             wm.x = cm[0] | (cm[1] << 8) | (cm[2] << 16) | (cm[3] << 24);
@@ -749,17 +806,18 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
 // The vectorised block: the weight-decay mode is resolved once per unit into
 // a branch-free instance.
 template <typename PT, typename GT, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
-__device__ __forceinline__ void dispatch_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t idx, const KHp& h)
+__device__ __forceinline__ void dispatch_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t idx, const KHp& h,
+                                               ChunkSlots<PT, GT>& sl, bool have0, int64_t next_blk)
 {
     const int32_t wdm = c.wd_mode;
     if constexpr (std::is_same<PT, uint16_t>::value) {
         if (wdm == WD_BF16) {
-            unit_qfast<PT, GT, WD_BF16, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
+            unit_qfast<PT, GT, WD_BF16, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h, sl, have0, next_blk);
             return;
         }
     }
-    if (wdm != WD_OFF) unit_qfast<PT, GT, WD_F32, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
-    else unit_qfast<PT, GT, WD_OFF, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
+    if (wdm != WD_OFF) unit_qfast<PT, GT, WD_F32, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h, sl, have0, next_blk);
+    else unit_qfast<PT, GT, WD_OFF, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h, sl, have0, next_blk);
 }
 
 // Any block size, partial or unaligned blocks (KIND_QGEN).  The first pass
@@ -846,6 +904,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     c.wd_mode = WD_OFF;
     c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;
     rf_adam8_leaf L;
+    ChunkSlots<PT, GT> sl;
+    bool have0 = false;  // slot 0 holds chunk 0 of unit u
     for (int64_t u = wave; u < total_units; u += nwaves) {
         while (segs[s + 1].unit_start <= u) ++s;
         const Seg sg = segs[s];
@@ -854,7 +914,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
             L = leaves[cur_leaf];
             leaf_context(c, L, h, MSR, PSR);
         }
-        dispatch_qfast<PT, GT, APPLY, MSR, PSR, NEST, EXACT>(c, L, sg.first + (u - sg.unit_start), h);
+        // The next unit of this wave, when it is a block of the same leaf
+        // (this kernel's units are all full blocks; one segment per leaf).
+        const int64_t un = u + nwaves;
+        int64_t next_blk = -1;
+        if (RF_PREFETCH_NEXT && un < total_units && un < segs[s + 1].unit_start)
+            next_blk = sg.first + (un - sg.unit_start);
+        dispatch_qfast<PT, GT, APPLY, MSR, PSR, NEST, EXACT>(c, L, sg.first + (u - sg.unit_start), h, sl, have0,
+                                                             next_blk);
+        have0 = next_blk >= 0;
     }
 }
 
