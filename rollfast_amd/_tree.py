@@ -6,7 +6,7 @@ The reference (rollfast) walks parameter and state trees with
 Leaf order decides which PRNG subkey each leaf receives, so this module
 reproduces JAX's order exactly:
 
-* ``dict``: children in sorted key order;
+* ``dict``: children in sorted key order (``OrderedDict``: insertion order);
 * ``list`` / ``tuple``: in order; ``NamedTuple``: in field order;
 * ``None``: a node with no children (so not a leaf) unless ``is_leaf``
   says otherwise;
@@ -16,6 +16,7 @@ reproduces JAX's order exactly:
 
 from __future__ import annotations
 
+from collections import OrderedDict
 from typing import Any, Callable, Optional
 
 _NODES: dict[type, tuple[Callable, Callable]] = {}
@@ -25,30 +26,23 @@ def register_node(cls, flatten: Callable, unflatten: Callable) -> None:
     """Register ``cls`` as an internal node: ``flatten(x) -> (children, aux)``,
     ``unflatten(aux, children) -> x``."""
     _NODES[cls] = (flatten, unflatten)
-
-
-def _is_namedtuple(x) -> bool:
-    return isinstance(x, tuple) and hasattr(type(x), "_fields")
+    _TYPE_KIND.pop(cls, None)
 
 
 class TreeDef:
-    __slots__ = ("kind", "aux", "children")
+    __slots__ = ("kind", "aux", "children", "num_leaves")
 
     def __init__(self, kind, aux=None, children=()):
         self.kind = kind
         self.aux = aux
         self.children = tuple(children)
-
-    @property
-    def num_leaves(self) -> int:
-        if self.kind == "leaf":
-            return 1
-        return sum(c.num_leaves for c in self.children)
+        self.num_leaves = 1 if kind == "leaf" else sum(c.num_leaves for c in self.children)
 
     def __eq__(self, other):
-        return (
+        return self is other or (
             isinstance(other, TreeDef)
             and self.kind == other.kind
+            and self.num_leaves == other.num_leaves
             and self.aux == other.aux
             and self.children == other.children
         )
@@ -64,25 +58,54 @@ class TreeDef:
 
 _LEAF = TreeDef("leaf")
 
+# Node classification per concrete type (computed once per type): "leaf",
+# "none", "custom", "dict", "odict", "namedtuple", "tuple", "list".
+_TYPE_KIND: dict[type, str] = {type(None): "none"}
+
+
+def _type_kind(t: type) -> str:
+    k = _TYPE_KIND.get(t)
+    if k is None:
+        if t in _NODES:
+            k = "custom"
+        elif issubclass(t, OrderedDict):
+            k = "odict"
+        elif issubclass(t, dict):
+            k = "dict"
+        elif issubclass(t, tuple) and hasattr(t, "_fields"):
+            k = "namedtuple"
+        elif issubclass(t, tuple):
+            k = "tuple"
+        elif issubclass(t, list):
+            k = "list"
+        else:
+            k = "leaf"
+        _TYPE_KIND[t] = k
+    return k
+
 
 def _children(x):
     """(kind, aux, children) of an internal node, or None for a leaf."""
-    if x is None:
-        return ("none", None, [])
     t = type(x)
-    if t in _NODES:
+    k = _TYPE_KIND.get(t) or _type_kind(t)
+    if k == "leaf":
+        return None
+    if k == "none":
+        return ("none", None, [])
+    if k == "dict":
+        keys = sorted(x.keys())
+        return ("dict", (t, tuple(keys)), [x[key] for key in keys])
+    if k == "odict":
+        keys = tuple(x.keys())
+        return ("odict", (t, keys), [x[key] for key in keys])
+    if k == "custom":
         children, aux = _NODES[t][0](x)
         return ("custom", (t, aux), list(children))
-    if isinstance(x, dict):
-        keys = sorted(x.keys())
-        return ("dict", (type(x), tuple(keys)), [x[k] for k in keys])
-    if _is_namedtuple(x):
-        return ("namedtuple", type(x), list(x))
-    if isinstance(x, tuple):
+    if k == "namedtuple":
+        return ("namedtuple", t, list(x))
+    if k == "tuple":
         return ("tuple", None, list(x))
-    if isinstance(x, list):
-        return ("list", None, list(x))
-    return None
+    return ("list", None, list(x))
 
 
 def flatten(tree, is_leaf: Optional[Callable[[Any], bool]] = None):
@@ -115,6 +138,9 @@ def _build(td: TreeDef, children):
         cls, keys = td.aux
         d = dict(zip(keys, children))
         return d if cls is dict else cls(d)
+    if td.kind == "odict":
+        cls, keys = td.aux
+        return cls(zip(keys, children))
     if td.kind == "namedtuple":
         return td.aux(*children)
     if td.kind == "tuple":
@@ -157,7 +183,7 @@ def flatten_up_to(td: TreeDef, tree) -> list:
         kind, aux, children = node
         if kind != t.kind or len(children) != len(t.children):
             raise ValueError(f"tree structure mismatch: {t.kind} vs {kind}")
-        if kind == "dict" and aux[1] != t.aux[1]:
+        if kind in ("dict", "odict") and aux[1] != t.aux[1]:
             raise ValueError(f"dict keys differ: {t.aux[1]} vs {aux[1]}")
         for ct, cx in zip(t.children, children):
             rec(ct, cx)

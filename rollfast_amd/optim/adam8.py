@@ -597,47 +597,49 @@ class _Engine:
     # -- cached table (same objects as the previous call) -------------------
     def _reuse_rows(self, last, g_leaves, mu_leaves, nu_leaves, p_leaves, apply):
         """Rewrites the grad (and, update-only mode, output) pointers of the
-        previous table when every other buffer is the same object; returns
-        the out-leaf list, or None when anything differs."""
+        previous table when every other buffer is the same object on the same
+        storage; returns the out-leaf list, or None when anything differs."""
         torch = _torch()
+        Tensor = torch.Tensor
         table = last["table"]
-        device = last["device"]
+        dev = last["device"]
+        dev_index = dev.index
         n = len(g_leaves)
         out_leaves: list = [None] * n
-        j = 0
         refs = last["refs"]
-        for i in range(n):
+        if len(refs) != sum(1 for i in range(n) if not (_is_passthrough_leaf(mu_leaves[i])
+                                                        or _is_passthrough_leaf(g_leaves[i]))):
+            return None
+        for j, (i, mref, vref, pref, gdtype, size, align_ok, ptrs) in enumerate(refs):
             g, m, v = g_leaves[i], mu_leaves[i], nu_leaves[i]
-            if j < len(refs) and refs[j][0] == i:
-                _, mref, vref, pref, gdtype, size, align_ok, ptrs = refs[j]
-                if mref() is not m or vref() is not v:
+            if mref() is not m or vref() is not v:
+                return None
+            p = None
+            if pref is not None:
+                p = p_leaves[i] if p_leaves is not None else None
+                if pref() is not p:
                     return None
-                p = None
-                if pref is not None:
-                    p = p_leaves[i] if p_leaves is not None else None
-                    if pref() is not p:
-                        return None
-                # same objects, same storage (a `.data` swap changes the pointer)
-                if _buffer_ptrs(m, v, p) != ptrs:
-                    return None
-                if (not isinstance(g, torch.Tensor) or g.dtype != gdtype or g.device != device
-                        or g.numel() != size or not g.is_contiguous()):
-                    return None
-                gp = g.data_ptr()
-                if align_ok and gp % 16:
-                    return None
-                row = table[j]
-                row.grad = gp
-                if not apply:
-                    out = torch.empty(g.shape, dtype=torch.float32, device=device)
-                    row.updates = out.data_ptr()
-                    out_leaves[i] = out
-                j += 1
-            else:
-                if not (_is_passthrough_leaf(m) or _is_passthrough_leaf(g)):
-                    return None
+            # same objects, same storage (a `.data` swap changes the pointer)
+            if _buffer_ptrs(m, v, p) != ptrs:
+                return None
+            if not isinstance(g, Tensor) or g.dtype is not gdtype or g.get_device() != dev_index:
+                return None
+            if g.numel() != size or not g.is_contiguous():
+                return None
+            gp = g.data_ptr()
+            if align_ok and gp & 15:
+                return None
+            row = table[j]
+            row.grad = gp
+            if not apply:
+                out = torch.empty(g.shape, dtype=torch.float32, device=dev)
+                row.updates = out.data_ptr()
+                out_leaves[i] = out
+        for i in range(n):
+            m, g = mu_leaves[i], g_leaves[i]
+            if _is_passthrough_leaf(m) or _is_passthrough_leaf(g):
                 out_leaves[i] = m if _is_passthrough_leaf(m) else g
-        return out_leaves if j == len(refs) else None
+        return out_leaves
 
     def run(
         self,
@@ -661,9 +663,6 @@ class _Engine:
         g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
         mu_leaves = _tree.flatten_up_to(g_td, state.mu) if g_td.num_leaves else []
         nu_leaves = _tree.flatten_up_to(g_td, state.nu) if g_td.num_leaves else []
-        mu_state_leaves = _tree.leaves(state.mu, is_leaf=_is_state_leaf)
-        if len(mu_state_leaves) != len(g_leaves):
-            raise ValueError("updates and optimizer state have different tree structures")
         p_leaves = None
         if params is not None:
             p_leaves = _tree.flatten_up_to(g_td, params)
@@ -678,6 +677,8 @@ class _Engine:
             table, n_rows, device, plan = last["table"], last["n"], last["device"], last["plan"]
         else:
             self._last = None
+            if len(_tree.leaves(state.mu, is_leaf=_is_state_leaf)) != len(g_leaves):
+                raise ValueError("updates and optimizer state have different tree structures")
             rows, structure, refs, out_leaves, device = self._build_rows(
                 g_leaves, mu_leaves, nu_leaves, p_leaves, apply=apply, decay_mask=decay_mask,
                 random_bits=random_bits)

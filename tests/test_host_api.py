@@ -180,3 +180,16 @@ def test_product_path_refuses_host_tensors():
         tx.update({"w": torch.zeros(4096)}, st, params)
     with pytest.raises(ValueError, match="ROCm device"):
         rf.adamw8_step(tx, params, {"w": torch.zeros(4096)}, st, stochastic=False)
+
+
+def test_tree_ordered_dict_keeps_insertion_order():
+    from collections import OrderedDict
+
+    tree = OrderedDict([("z", 1), ("a", 2)])
+    leaves, td = _tree.flatten(tree)
+    assert leaves == [1, 2]
+    back = _tree.unflatten(td, [3, 4])
+    assert isinstance(back, OrderedDict) and list(back.items()) == [("z", 3), ("a", 4)]
+    assert _tree.flatten_up_to(td, OrderedDict([("z", "x"), ("a", "y")])) == ["x", "y"]
+    with pytest.raises(ValueError):
+        _tree.flatten_up_to(td, OrderedDict([("a", "y"), ("z", "x")]))
