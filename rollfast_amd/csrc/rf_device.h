@@ -653,7 +653,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     const float* TV = c.wtab + 256;
 
     float m[J][8], v[J][8];
-    float mx = 0.0f, mn = 0.0f;  // max / min of m: with finite inputs no NaN can occur
+    float amf = 0.0f;            // max |m| (v_max3 with |x| modifiers); with finite inputs no NaN can occur
     uint32_t av = 0;             // v >= 0: integer max of the bits, NaN-propagating
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -691,8 +691,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             const float vv = TV[cv] + t4;
             m[j][t] = mm;
             v[j][t] = vv;
-            mx = fmaxf(mx, mm);
-            mn = fminf(mn, mm);
+            amf = fmaxf(amf, fabsf(mm));
             av = max(av, __float_as_uint(vv));
             u[t] = adam_direction<NEST, EXACT>(h, mm, vv, g[t]);
         }
@@ -743,7 +742,6 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     }
 
     // Requantization (adam8.py:633-688 -> quantize_blocks).
-    const float amf = fmaxf(mx, -mn);
     const uint32_t am = wave_max_u32(__float_as_uint(amf));  // amf >= 0: bit order = value order
     av = wave_max_u32(av);
     const float sm = scale_from_absmax_bits(am);

@@ -19,6 +19,7 @@ from oracle import oracle as orc
 from tests._helpers import (
     OracleTree,
     bf16_bits,
+    bf16_to_f32,
     bf16_ulp_distance,
     f32_within_bf16_ulp,
     gaussian,
@@ -391,3 +392,72 @@ def test_cached_leaf_table_follows_changes():
         torch.cuda.synchronize()
         _compare_state(gspec, tree, state[0], f"step {step + 1}")
         _compare_params(gspec, tree, params, True, f"step {step + 1}", before)
+
+
+@pytest.mark.parametrize("exact", [True, False])
+def test_non_finite_and_extreme_gradient_blocks(exact):
+    """Blocks whose gradients hold a NaN, a +Inf, values whose square
+    overflows, all zeros, f32 denormals or values so small that the block
+    scale falls below the fast path's exact-division range.  Such blocks take
+    the literal requantization (the reference's NaN-propagating absmax gives
+    scale 1 for a NaN block); codes and scales must still match the oracle
+    bit for bit and params where finite, over two steps."""
+    import torch
+
+    rf = _rf()
+    rng = np.random.default_rng(3)
+    n = 8 * 2048
+    host_p = {"a": (rng.standard_normal(n) * 0.02).astype(np.float32),
+              "b": bf16_bits((rng.standard_normal(n) * 0.02).astype(np.float32))}
+    params = {"a": to_device(host_p["a"], "f32"), "b": to_device(host_p["b"], "bf16")}
+    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=exact)
+    state = tx.init(params)
+
+    def grads_for(step):
+        g = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+        g[1 * 2048 + 17] = np.nan
+        g[2 * 2048 + 5] = np.inf
+        g[3 * 2048:4 * 2048] *= np.float32(1e22)        # g*g overflows to +Inf
+        g[4 * 2048:5 * 2048] = 0.0
+        g[5 * 2048:6 * 2048] = np.float32(1e-40) * np.sign(g[5 * 2048:6 * 2048])
+        g[6 * 2048:7 * 2048] *= np.float32(1e-24)       # block scale < 2^-70
+        if step == 1:
+            g[7 * 2048 + 100] = -np.inf
+        return g
+
+    for step in range(2):
+        ga = grads_for(step)
+        gb = bf16_bits(grads_for(step))
+        leaves = []
+        for name, pd in (("a", "f32"), ("b", "bf16")):
+            m, v = state[0].mu[name], state[0].nu[name]
+            leaves.append({"pdtype": pd, "gdtype": pd, "kind": "quant", "size": n, "block_size": 2048,
+                           "param": to_host(params[name]).copy(), "mu": to_host(m.values).copy(),
+                           "mu_scales": to_host(m.scales).copy(), "nu": to_host(v.values).copy(),
+                           "nu_scales": to_host(v.scales).copy()})
+        tree = OracleTree(leaves)
+        tree.step([ga, gb], weight_decay=0.01, lr=1e-3, count=step + 1)
+        params, state = rf.adamw8_step(tx, params, {"a": to_device(ga, "f32"), "b": to_device(gb, "bf16")},
+                                       state, stochastic=False)
+        torch.cuda.synchronize()
+        for name, L in zip(("a", "b"), tree.leaves):
+            m, v = state[0].mu[name], state[0].nu[name]
+            np.testing.assert_array_equal(to_host(m.values), L["mu"], err_msg=f"step {step + 1} {name} mu codes")
+            np.testing.assert_array_equal(to_host(v.values), L["nu"], err_msg=f"step {step + 1} {name} nu codes")
+            np.testing.assert_array_equal(to_host(m.scales).view(np.uint32), L["mu_scales"].view(np.uint32))
+            np.testing.assert_array_equal(to_host(v.scales).view(np.uint32), L["nu_scales"].view(np.uint32))
+            got = to_host(params[name])
+            want = L["param"]
+            if name == "a":
+                gf, wf = got, want
+            else:
+                gf, wf = bf16_to_f32(got), bf16_to_f32(want)
+            np.testing.assert_array_equal(np.isnan(gf), np.isnan(wf), err_msg=f"step {step + 1} {name} NaN positions")
+            fin = np.isfinite(wf)
+            np.testing.assert_array_equal(gf[~fin & ~np.isnan(wf)], wf[~fin & ~np.isnan(wf)])
+            if exact:
+                np.testing.assert_array_equal(gf[fin].view(np.uint32), wf[fin].view(np.uint32))
+            elif name == "a":
+                assert f32_within_bf16_ulp(gf[fin], wf[fin]).all()
+            else:
+                assert bf16_ulp_distance(got[fin], want[fin]).max() <= 1
