@@ -63,23 +63,29 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const float*
     const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
     const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
     const float* cb = (const float*)(lds + (quantizer == RF_Q_DYNAMIC_UNSIGNED ? L_CBU : L_CBS));
+    auto is_full = [&](int64_t b) { return vec_ok && bs == FAST_BS && b < nblocks && b * bs + bs <= size; };
+    auto load_block = [&](int64_t b, float (&r)[32]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float t8[8];
+            load8<float>(x, b * FAST_BS + j * 512 + lane * 8, t8);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) r[j * 8 + t] = t8[t];
+        }
+    };
+    // Full 2048-blocks are double-buffered: the next block of this wave is
+    // loaded while the current one is coded.
+    float xr[32];
+    bool have = false;
     for (int64_t b = wave; b < nblocks; b += nwaves) {
         const int64_t base = b * bs;
         const int64_t nvalid = max((int64_t)0, min(bs, size - base));
-        const bool full = vec_ok && bs == FAST_BS && nvalid == bs;
-        float xr[32];
+        const bool full = is_full(b);
         uint32_t am = 0;
         if (full) {
+            if (!have) load_block(b, xr);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float t8[8];
-                load8<float>(x, base + j * 512 + lane * 8, t8);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    xr[j * 8 + t] = t8[t];
-                    am = max(am, __float_as_uint(t8[t]) & 0x7FFFFFFFu);
-                }
-            }
+            for (int i = 0; i < 32; ++i) am = max(am, __float_as_uint(xr[i]) & 0x7FFFFFFFu);
         } else {
             for (int64_t j = lane; j < nvalid; j += WAVE) am = max(am, __float_as_uint(x[base + j]) & 0x7FFFFFFFu);
         }
@@ -115,18 +121,45 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const float*
             return code_literal(cb, xv, scale, sr != 0, w);
         };
         if (full) {
+            const bool next_full = is_full(b + nwaves);
+            float xn[32];
+            if (next_full) load_block(b + nwaves, xn);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int64_t e0 = base + j * 512 + lane * 8;
                 uint32_t cc[8];
+                if (fast && quantizer != RF_Q_SYMMETRIC_INT8) {
+                    // Batched phases: normalise, candidate reads, threshold
+                    // reads (16 independent LDS reads in flight).
+                    const bool sgn = quantizer == RF_Q_DYNAMIC_SIGNED;
+                    float nv[8], tv[8];
 #pragma unroll
-                for (int t = 0; t < 8; ++t) cc[t] = code_of(xr[j * 8 + t], e0 + t);
+                    for (int t = 0; t < 8; ++t) {
+                        const float xv = xr[j * 8 + t];
+                        nv[t] = div_by_scale(sgn ? xv : (xv > 0.0f ? xv : 0.0f), scale, rs);
+                    }
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) cc[t] = sgn ? cand_signed(lds, nv[t]) : cand_unsigned(lds, nv[t]);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) tv[t] = *(const float*)(lds + (sgn ? L_TS : L_TU) + cc[t] * 4u);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) cc[t] += nv[t] >= tv[t] ? 1u : 0u;
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) cc[t] = code_of(xr[j * 8 + t], e0 + t);
+                }
                 uint2 w;
                 w.x = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
                 w.y = cc[4] | (cc[5] << 8) | (cc[6] << 16) | (cc[7] << 24);
                 *(uint2*)(values + e0) = w;
             }
+            if (next_full) {
+#pragma unroll
+                for (int i = 0; i < 32; ++i) xr[i] = xn[i];
+            }
+            have = next_full;
         } else {
+            have = false;
             for (int64_t j = lane; j < bs; j += WAVE) {
                 const int64_t e = base + j;
                 const float xv = j < nvalid ? x[e] : 0.0f;
@@ -136,56 +169,73 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const float*
     }
 }
 
-// Standalone dequantize_blocks (adam8.py:190-204).
+// Standalone dequantize_blocks (adam8.py:190-204).  Vector path: each wave
+// takes 1024-element tiles, two at a time; lane l owns elements
+// 256k + 4l .. 256k + 4l + 3 (k = 0..3), so every code load reads 256
+// contiguous bytes and every store writes 1 KB (f32) or 512 B (bf16)
+// contiguous.  Requires a power-of-two block size (>= 4) and 4-byte aligned
+// codes / 16-byte (f32) or 8-byte (bf16) aligned output.
+__device__ __forceinline__ void dq_store4(void* out, int32_t out_dtype, int64_t e, const float (&o)[4])
+{
+    if (out_dtype == RF_BF16) {
+        uint2 w;
+        w.x = f32_to_bf16_rne(o[0]) | (f32_to_bf16_rne(o[1]) << 16);
+        w.y = f32_to_bf16_rne(o[2]) | (f32_to_bf16_rne(o[3]) << 16);
+        *(uint2*)((uint16_t*)out + e) = w;
+    } else {
+        *(float4*)((float*)out + e) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 __global__ __launch_bounds__(WG) void k_dequantize(int32_t quantizer, const uint8_t* __restrict__ values,
                                                    const float* __restrict__ scales, int64_t size, int64_t bs,
-                                                   int32_t out_dtype, void* __restrict__ out,
+                                                   int32_t bs_log2, int32_t out_dtype, void* __restrict__ out,
                                                    const uint4* __restrict__ tables, int32_t vec_ok)
 {
     __shared__ __attribute__((aligned(16))) float cb[256];
     const uint32_t off = quantizer == RF_Q_DYNAMIC_UNSIGNED ? L_CBU : L_CBS;
     for (int i = threadIdx.x; i < 64; i += WG) ((uint4*)cb)[i] = tables[off / 16 + i];
     __syncthreads();
-    const int64_t tid = (int64_t)blockIdx.x * WG + threadIdx.x;
-    const int64_t nthreads = (int64_t)gridDim.x * WG;
     const bool sym = quantizer == RF_Q_SYMMETRIC_INT8;
-    const int64_t ngroups = vec_ok ? size / 8 : 0;
-    // Four 8-element groups per thread and iteration, loads issued first:
-    // the code reads (1/5 of the traffic) must not serialise the writes.
-    constexpr int U = 4;
-    for (int64_t g0 = tid; g0 < ngroups; g0 += U * nthreads) {
-        uint2 w[U];
-        float s[U];
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    const int64_t ntiles = vec_ok ? size / 1024 : 0;
+    constexpr int T = 2;  // tiles per wave and iteration
+    for (int64_t t0 = wave * T; t0 < ntiles; t0 += nwaves * T) {
+        uint32_t w[T][4];
+        float s[T][4];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t gi = g0 + u * nthreads;
-            if (gi < ngroups) {
-                w[u] = *(const uint2*)(values + gi * 8);
-                s[u] = scales[gi * 8 / bs];  // bs % 8 == 0: the 8 elements share a block
+        for (int u = 0; u < T; ++u) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int64_t e = (t0 + u) * 1024 + k * 256 + lane * 4;
+                if (t0 + u < ntiles) {
+                    w[u][k] = *(const uint32_t*)(values + e);
+                    s[u][k] = scales[e >> bs_log2];  // the 4 elements share a block (bs >= 4)
+                }
             }
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t gi = g0 + u * nthreads;
-            if (gi >= ngroups) break;
-            float o[8];
+        for (int u = 0; u < T; ++u) {
+            if (t0 + u >= ntiles) break;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const uint32_t cbyte = ((t < 4 ? w[u].x : w[u].y) >> (8 * (t & 3))) & 0xFFu;
-                const float val = sym ? (float)(int8_t)cbyte : cb[cbyte];
-                o[t] = val * s[u];
-            }
-            if (out_dtype == RF_BF16) {
-                uint32_t hb[8];
+            for (int k = 0; k < 4; ++k) {
+                const int64_t e = (t0 + u) * 1024 + k * 256 + lane * 4;
+                float o[4];
 #pragma unroll
-                for (int t = 0; t < 8; ++t) hb[t] = f32_to_bf16_rne(o[t]);
-                store8_bf16(out, gi * 8, hb);
-            } else {
-                store8_f32(out, gi * 8, o);
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t cbyte = (w[u][k] >> (8 * i)) & 0xFFu;
+                    const float val = sym ? (float)(int8_t)cbyte : cb[cbyte];
+                    o[i] = val * s[u][k];
+                }
+                dq_store4(out, out_dtype, e, o);
             }
         }
     }
-    for (int64_t e = ngroups * 8 + tid; e < size; e += nthreads) {
+    const int64_t tid = (int64_t)blockIdx.x * WG + threadIdx.x;
+    const int64_t nthreads = (int64_t)gridDim.x * WG;
+    for (int64_t e = ntiles * 1024 + tid; e < size; e += nthreads) {
         const uint32_t cbyte = values[e];
         const float val = sym ? (float)(int8_t)cbyte : cb[cbyte];
         store1(out, out_dtype, e, val * scales[e / bs]);
@@ -953,11 +1003,19 @@ rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const f
     DevState* ds = nullptr;
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
-    const int32_t vec_ok = (block_size % 8 == 0) && aligned(values, 8) && aligned(out, 16);
-    const int64_t work = vec_ok ? (size + 7) / 8 : size;
-    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>((work + WG - 1) / WG, (int64_t)ds->num_cus * 8));
+    const bool pow2 = block_size >= 4 && (block_size & (block_size - 1)) == 0;
+    int32_t bs_log2 = 0;
+    while (pow2 && (1 << bs_log2) < block_size) ++bs_log2;
+    const int32_t vec_ok = pow2 && aligned(values, 4) && aligned(out, out_dtype == RF_BF16 ? 8 : 16);
+    // Vector path: one wave per two 1024-element tiles, at most 8 waves' worth
+    // of workgroups per CU; the scalar tail needs few threads.
+    const int64_t tiles = vec_ok ? size / 1024 : 0;
+    const int64_t wg_needed = std::max<int64_t>(1, (tiles + 2 * WAVES_PER_WG - 1) / (2 * WAVES_PER_WG));
+    const int grid = (int)std::min<int64_t>(std::max<int64_t>(wg_needed, vec_ok ? 1 : (size + WG - 1) / WG),
+                                            (int64_t)ds->num_cus * 8);
     hipLaunchKernelGGL(k_dequantize, dim3(grid), dim3(WG), 0, (hipStream_t)stream, quantizer,
-                       (const uint8_t*)values, scales, size, (int64_t)block_size, out_dtype, out, ds->tables, vec_ok);
+                       (const uint8_t*)values, scales, size, (int64_t)block_size, bs_log2, out_dtype, out,
+                       ds->tables, vec_ok);
     HIP_TRY(hipGetLastError());
     return RF_OK;
 }
