@@ -61,7 +61,11 @@ typedef int32_t rf_status;
                             Threefry-2x32 */
 
 /* rf_adam8_leaf.flags */
-#define RF_LEAF_DECAY 1u /* add_decayed_weights applies to this leaf (mask True) */
+#define RF_LEAF_DECAY 1u    /* add_decayed_weights applies to this leaf (mask True) */
+#define RF_LEAF_STORE_SR 2u /* bf16 fallback moments are stored with stochastic rounding:
+                               bits of split(key_mu | key_nu)[state_index], or mu_bits /
+                               nu_bits with RF_FED_BITS (optim/adam.py:219-222 with
+                               mu_dtype=bfloat16; adamw8 rounds to nearest even) */
 
 /* One parameter leaf and its optimizer state. */
 typedef struct rf_adam8_leaf {
@@ -100,9 +104,17 @@ typedef struct rf_adam8_hparams {
     float weight_decay;      /* f32(wd) */
     float neg_lr;            /* f32(-lr) or -lr(count) of a schedule */
     uint32_t flags;          /* RF_NESTEROV | RF_DECAY_WEAK | RF_LR | ... */
-    uint32_t key_mu[2];      /* jax.random key data of key_mu (adam8.py:306) */
+    uint32_t key_mu[2];      /* jax.random key data of key_mu (adam8.py:306); with
+                                RF_LEAF_STORE_SR the first-moment storage key */
     uint32_t key_nu[2];
     uint32_t key_param[2];   /* apply_updates key (utils.py:682) */
+    float nesterov_one_minus_b1; /* weight of the bias-corrected gradient in the Nesterov
+                                    combination: f32(1.0 - b1) computed in double
+                                    (adam8.py:341-350, optim/adam.py:146-160).  adamw8
+                                    sets it equal to one_minus_b1; optim/adam.py's EMA
+                                    weight one_minus_b1 is 1 - f32(b1) in f32
+                                    (utils.py:327-335) and differs from it. */
+    uint32_t reserved;       /* 0 */
 } rf_adam8_hparams;
 
 typedef struct rf_adam8_plan rf_adam8_plan;

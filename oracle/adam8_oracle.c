@@ -332,14 +332,22 @@ enum {
     ORC_MOMENT_SR = 16,     /* adamw8(stochastic_rounding=True) */
     ORC_PARAM_SR = 32,      /* apply_updates(stochastic=True) for bf16 params */
     ORC_APPLY = 64,         /* write params (fused step) instead of updates */
+    ORC_STORE_SR = 512,     /* bf16 fallback moments stored with SR from mu_bits / nu_bits
+                               (optim/adam.py:219-222, utils.py:374-409) */
 };
 
+/* one_minus_b1 weights the gradient in the first-moment EMA; the Nesterov
+ * combination uses nest_one_minus_b1 (adam8.py:322-327 and :341-350 both use
+ * the Python double 1.0 - b1; optim/adam.py computes the EMA weight in f32,
+ * utils.py:327-335 _momentum_grad_scale, and the Nesterov weight in double,
+ * adam.py:146-160). */
 typedef struct {
     float b1, one_minus_b1, b2, one_minus_b2;
     float bc1, bc2, bc1_next;
     float eps, eps_root;
     float weight_decay, neg_lr;
     int32_t flags;
+    float nest_one_minus_b1;
 } orc_hparams;
 
 static inline float load_val(int dtype, const void* p, int64_t e)
@@ -360,7 +368,7 @@ static inline float direction_and_apply(const orc_hparams* hp, int pdtype, void*
         float mu_bc = m / hp->bc1_next;
         float g_bc = g / hp->bc1;
         float t1 = hp->b1 * mu_bc;
-        float t2 = hp->one_minus_b1 * g_bc;
+        float t2 = hp->nest_one_minus_b1 * g_bc;
         mhat = t1 + t2;
     } else {
         mhat = m / hp->bc1;
@@ -486,8 +494,12 @@ ORC_API void orc_adam8_leaf(const orc_hparams* hp,
             } else if (updates_out) {
                 updates_out[e] = u;
             }
-            /* adam8.py:688 moment.astype(fallback_dtype) */
-            if (mkind == ORC_MOM_BF16) {
+            /* adam8.py:688 moment.astype(fallback_dtype); optim/adam.py:219-222
+             * stores bf16 moments with _tree_stochastic_cast instead. */
+            if (mkind == ORC_MOM_BF16 && (hp->flags & ORC_STORE_SR)) {
+                ((uint16_t*)mu)[e] = sr_bf16_from_bits(m, mu_bits[e]);
+                ((uint16_t*)nu)[e] = sr_bf16_from_bits(v, nu_bits[e]);
+            } else if (mkind == ORC_MOM_BF16) {
                 ((uint16_t*)mu)[e] = f32_to_bf16_rne(m);
                 ((uint16_t*)nu)[e] = f32_to_bf16_rne(v);
             } else {

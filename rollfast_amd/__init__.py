@@ -2,9 +2,10 @@
 
 Drop-in for the reference's adam8 hot path (rollfast ``adamw8``,
 ``scale_by_adam8``, ``quantize_blocks``, ``dequantize_blocks``,
-``apply_updates``): same names, arguments, state pytree and errors, with
-torch tensors on a ROCm device in place of jax arrays.  ``adamw8_step`` fuses
-``tx.update`` and ``apply_updates`` into one HBM pass.
+``apply_updates``) and its full-precision sibling (``adamw``,
+``scale_by_adam``): same names, arguments, state pytree and errors, with
+torch tensors on a ROCm device in place of jax arrays.  ``adamw8_step`` /
+``adamw_step`` fuse ``tx.update`` and ``apply_updates`` into one HBM pass.
 """
 
 from . import prng
@@ -31,6 +32,7 @@ from .optim.adam8 import (
     scale_by_adam8,
     tree_state_nbytes,
 )
+from .optim.adam import ScaleByAdamState, adamw, adamw_step, scale_by_adam
 from .utils import apply_updates, apply_updates_prefix
 
 __version__ = "0.1.0"
@@ -46,9 +48,12 @@ __all__ = (
     "MaskedState",
     "QuantizedBlocks",
     "ScaleByAdam8State",
+    "ScaleByAdamState",
     "ScaleByScheduleState",
+    "adamw",
     "adamw8",
     "adamw8_step",
+    "adamw_step",
     "apply_updates",
     "apply_updates_prefix",
     "dequantize_blocks",
@@ -56,6 +61,7 @@ __all__ = (
     "prng",
     "quantize_blocks",
     "quantized_nbytes",
+    "scale_by_adam",
     "scale_by_adam8",
     "tree_state_nbytes",
 )

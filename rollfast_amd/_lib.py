@@ -27,6 +27,7 @@ RF_PARAM_SR = 32
 RF_EXACT = 128
 RF_FED_BITS = 256
 RF_LEAF_DECAY = 1
+RF_LEAF_STORE_SR = 2
 
 _p = ctypes.c_void_p
 
@@ -72,6 +73,8 @@ class Adam8Hparams(ctypes.Structure):
         ("key_mu", ctypes.c_uint32 * 2),
         ("key_nu", ctypes.c_uint32 * 2),
         ("key_param", ctypes.c_uint32 * 2),
+        ("nesterov_one_minus_b1", ctypes.c_float),
+        ("reserved", ctypes.c_uint32),
     ]
 
 
@@ -87,7 +90,7 @@ class ApplyLeaf(ctypes.Structure):
 
 
 assert ctypes.sizeof(Adam8Leaf) == 120
-assert ctypes.sizeof(Adam8Hparams) == 72
+assert ctypes.sizeof(Adam8Hparams) == 80
 assert ctypes.sizeof(ApplyLeaf) == 40
 
 # Every symbol the header declares (checked by the CPU test suite).

@@ -59,6 +59,7 @@ struct KHp {
     // quantity as (m/bc1) / (sqrt(v/bc2 + eps_root) + eps), fewer roundings.
     float k1, k2, er2;
     float nb1, nomb1, rsbc2;  // nesterov: b1/bc1_next, (1-b1)/bc1, 1/sqrt(bc2)
+    float nomb1x;             // nesterov: f32(1 - b1) (double), exact path
     float eps, eps_root;
     float wd, wd16;           // f32(wd) and bf16(wd) as f32 (weak-typed decay of bf16 params)
     float neg_lr;             // f32(-lr), or 1.0 when the chain has no learning-rate scale
@@ -262,7 +263,7 @@ __device__ __forceinline__ float adam_direction(const KHp& h, float m, float v, 
             const float a = m / h.bc1n;
             const float b = g / h.bc1;
             const float t1 = h.b1 * a;
-            const float t2 = h.omb1 * b;
+            const float t2 = h.nomb1x * b;
             mhat = t1 + t2;
         } else {
             mhat = m / h.bc1;
@@ -856,13 +857,22 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
     const int64_t base = chunk * CHUNK;
     const int64_t end = min(base + CHUNK, L.size);
     const int32_t mdt = L.moment_kind == RF_MOMENT_BF16 ? RF_BF16 : RF_F32;
+    const bool store_sr = mdt == RF_BF16 && (L.flags & RF_LEAF_STORE_SR);
     for (int64_t e = base + lane; e < end; e += WAVE) {
         const float g = load1(L.grad, L.grad_dtype, e);
         float mm, vv;
         ema(h, load1(L.mu, mdt, e), load1(L.nu, mdt, e), g, mm, vv);
         update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g);
-        store1(L.mu, mdt, e, mm);  // adam8.py:688 moment.astype(fallback_dtype)
-        store1(L.nu, mdt, e, vv);
+        if (store_sr) {
+            // optim/adam.py:219-222: _tree_stochastic_cast(moments, bfloat16, k1 | k2)
+            const uint32_t bm = c.fed ? L.mu_bits[e] : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
+            const uint32_t bv = c.fed ? L.nu_bits[e] : jax_bits(c.knu0, c.knu1, (uint64_t)e);
+            ((uint16_t*)L.mu)[e] = (uint16_t)sr_bf16(mm, bm);
+            ((uint16_t*)L.nu)[e] = (uint16_t)sr_bf16(vv, bv);
+        } else {
+            store1(L.mu, mdt, e, mm);  // adam8.py:688 moment.astype(fallback_dtype)
+            store1(L.nu, mdt, e, vv);
+        }
     }
 }
 
@@ -871,7 +881,7 @@ __device__ __forceinline__ void leaf_context(UnitCtx& c, const rf_adam8_leaf& L,
 {
     const bool decay = (L.flags & RF_LEAF_DECAY) != 0;
     c.wd_mode = !decay ? WD_OFF : ((L.param_dtype == RF_BF16 && (h.flags & RF_DECAY_WEAK)) ? WD_BF16 : WD_F32);
-    if (msr) {
+    if (msr || (L.flags & RF_LEAF_STORE_SR)) {
         jax_split(h.kmu0, h.kmu1, (uint32_t)L.state_index, c.kmu0, c.kmu1);
         jax_split(h.knu0, h.knu1, (uint32_t)L.state_index, c.knu0, c.knu1);
     }

@@ -592,6 +592,28 @@ struct RingSlot {
 
 // One launch per (param, grad) dtype combination present in the tree; each
 // group has its own work list (ending in a sentinel) inside d_segs.
+// Fed random bits present for every leaf that would read them: param bits
+// (param SR), moment bits of quantized leaves (moment SR), moment bits of bf16
+// fallback leaves stored with SR.  A leaf missing bits its flags require
+// would make the kernel read through a null pointer, so runs refuse it.
+struct BitsCover {
+    bool pb = true, mb_quant = true, mb_store = true;
+};
+
+static BitsCover bits_cover(const rf_adam8_leaf* leaves, int32_t n)
+{
+    BitsCover c;
+    for (int32_t i = 0; i < n; ++i) {
+        const rf_adam8_leaf& L = leaves[i];
+        if (L.size == 0) continue;
+        const bool mb = L.mu_bits != nullptr && L.nu_bits != nullptr;
+        if (!L.param_bits) c.pb = false;
+        if (L.moment_kind == RF_MOMENT_QUANTIZED && !mb) c.mb_quant = false;
+        if (L.moment_kind == RF_MOMENT_BF16 && (L.flags & RF_LEAF_STORE_SR) && !mb) c.mb_store = false;
+    }
+    return c;
+}
+
 struct PlanGroup {
     int combo;
     int64_t seg_offset;
@@ -609,7 +631,7 @@ struct rf_adam8_plan {
     Seg* d_segs = nullptr;
     std::vector<rf_adam8_leaf> shape;   // creation-time table: the structure runs must match
     std::vector<uint8_t> vec;           // leaf has vectorised (16-byte aligned) work units
-    bool any_param_bits = false, any_moment_bits = false;
+    BitsCover cover;  // which fed-bits arrays the creation-time table carries
     RingSlot ring[RING];
     uint32_t next = 0;
     std::mutex mu;
@@ -704,14 +726,11 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
         gsegs[combo].push_back(sg);
         gunits[combo] += count;
     };
-    bool any_pb = false, any_mb = false;
     std::vector<uint8_t> vecs;
     for (int32_t i = 0; i < n_leaves; ++i) {
         const rf_adam8_leaf& L = leaves[i];
         st = validate_leaf(L, i, apply);
         if (st != RF_OK) return st;
-        any_pb |= L.param_bits != nullptr;
-        any_mb |= (L.mu_bits != nullptr) || (L.nu_bits != nullptr);
         const bool vec = leaf_vec_ok(L, apply);
         vecs.push_back(vec ? 1 : 0);
         // Full aligned 2048-blocks go to the fast kernel of their dtype
@@ -761,8 +780,7 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     p->total_units = units;
     p->n_segs = (int64_t)segs.size();
     p->groups = groups;
-    p->any_param_bits = any_pb;
-    p->any_moment_bits = any_mb;
+    p->cover = bits_cover(leaves, n_leaves);
     p->shape.assign(leaves, leaves + n_leaves);
     p->vec = vecs;
     // Every buffer a run needs is allocated here, so runs never allocate
@@ -799,15 +817,20 @@ rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64
 
 namespace {
 
-rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, bool any_pb, bool any_mb,
+rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, const BitsCover& cover,
                       const rf_adam8_hparams* hp, void* stream)
 {
     if (plan->total_units == 0) return RF_OK;
     const uint32_t f = hp->flags;
     const bool msr = (f & RF_MOMENT_SR) != 0;
     const bool psr = (f & RF_PARAM_SR) != 0 && plan->apply;
-    if ((f & RF_FED_BITS) && ((psr && !any_pb) || (msr && !any_mb)))
-        return fail(RF_ERR_INVALID, "RF_FED_BITS set but the leaves carry no random bits");
+    if (f & RF_FED_BITS) {
+        if (psr && !cover.pb) return fail(RF_ERR_INVALID, "RF_FED_BITS with param SR: a leaf has no param_bits");
+        if (msr && !cover.mb_quant)
+            return fail(RF_ERR_INVALID, "RF_FED_BITS with moment SR: a quantized leaf has no mu_bits/nu_bits");
+        if (!cover.mb_store)
+            return fail(RF_ERR_INVALID, "RF_FED_BITS: a leaf with RF_LEAF_STORE_SR has no mu_bits/nu_bits");
+    }
     DevState* ds = nullptr;
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
@@ -826,9 +849,10 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         k.k2 = (float)((double)hp->eps * bc1);
         k.er2 = (float)((double)hp->eps_root * bc2);
         k.nb1 = (float)((double)hp->b1 / bc1n);
-        k.nomb1 = (float)((double)hp->one_minus_b1 / bc1);
+        k.nomb1 = (float)((double)hp->nesterov_one_minus_b1 / bc1);
         k.rsbc2 = (float)(1.0 / std::sqrt(bc2));
     }
+    k.nomb1x = hp->nesterov_one_minus_b1;
     k.eps = hp->eps;
     k.eps_root = hp->eps_root;
     k.wd = hp->weight_decay;
@@ -901,7 +925,7 @@ rf_status rf_adam8_plan_run(const rf_adam8_plan* plan, const rf_adam8_hparams* h
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     if (dev != plan->device) return fail(RF_ERR_INVALID, "plan was created on another device");
-    return plan_launch(plan, plan->d_leaves, plan->any_param_bits, plan->any_moment_bits, hp, stream);
+    return plan_launch(plan, plan->d_leaves, plan->cover, hp, stream);
 }
 
 rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* leaves, int32_t n_leaves,
@@ -913,7 +937,6 @@ rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* lea
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     if (dev != plan->device) return fail(RF_ERR_INVALID, "plan was created on another device");
-    bool any_pb = false, any_mb = false;
     for (int32_t i = 0; i < n_leaves; ++i) {
         const rf_adam8_leaf& L = leaves[i];
         if (!same_structure(L, plan->shape[i]))
@@ -922,9 +945,8 @@ rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* lea
         if (st != RF_OK) return st;
         if (plan->vec[i] && !leaf_vec_ok(L, plan->apply))
             return fail(RF_ERR_INVALID, "leaf " + std::to_string(i) + " lost the 16-byte alignment the plan relies on");
-        any_pb |= L.param_bits != nullptr;
-        any_mb |= (L.mu_bits != nullptr) || (L.nu_bits != nullptr);
     }
+    const BitsCover cover = bits_cover(leaves, n_leaves);
     if (plan->total_units == 0) return RF_OK;
     std::lock_guard<std::mutex> lock(plan->mu);
     RingSlot& slot = plan->ring[plan->next % RING];
@@ -933,7 +955,7 @@ rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* lea
     if (slot.pending) HIP_TRY(hipEventSynchronize(slot.ev));
     std::memcpy(slot.host, leaves, bytes);
     HIP_TRY(hipMemcpyAsync(slot.dev, slot.host, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
-    rf_status st = plan_launch(plan, slot.dev, any_pb, any_mb, hp, stream);
+    rf_status st = plan_launch(plan, slot.dev, cover, hp, stream);
     HIP_TRY(hipEventRecord(slot.ev, (hipStream_t)stream));
     slot.pending = true;
     return st;

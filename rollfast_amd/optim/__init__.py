@@ -1,4 +1,7 @@
-"""Optimizers: the 8-bit AdamW step (mirror of rollfast ``optim/adam8.py``)."""
+"""Optimizers: the 8-bit AdamW step (mirror of rollfast ``optim/adam8.py``)
+and full-precision AdamW (mirror of ``optim/adam.py``)."""
+
+from .adam import ScaleByAdamState, adamw, adamw_step, scale_by_adam
 
 from .adam8 import (
     DYNAMIC_SIGNED_CODEBOOK_ID,
@@ -17,6 +20,10 @@ from .adam8 import (
 )
 
 __all__ = (
+    "ScaleByAdamState",
+    "adamw",
+    "adamw_step",
+    "scale_by_adam",
     "DYNAMIC_SIGNED_CODEBOOK_ID",
     "DYNAMIC_UNSIGNED_CODEBOOK_ID",
     "SYMMETRIC_INT8_CODEBOOK_ID",

@@ -482,6 +482,27 @@ class _Engine:
         self._plans: dict = {}
         self._last = None
 
+    @staticmethod
+    def ema_weight(b1) -> np.float32:
+        """Gradient weight of the first-moment EMA: ``1.0 - b1`` as adam8.py:323
+        evaluates it."""
+        return _one_minus(b1)
+
+    @staticmethod
+    def split_keys(state_key):
+        """(moment-SR key of mu, of nu, next state key): adam8.py:306."""
+        key_mu, key_nu, next_key = prng.split(state_key, 3)
+        return key_mu, key_nu, next_key
+
+    @staticmethod
+    def new_state(state, count_inc, next_key):
+        return ScaleByAdam8State(count=np.asarray(count_inc, dtype=np.int32), mu=state.mu, nu=state.nu,
+                                 key=next_key)
+
+    # bf16 fallback moments are stored with stochastic rounding (adamw8 rounds
+    # them to nearest even, adam8.py:688).
+    store_sr = False
+
     # -- full table build (first call, or anything changed) -----------------
     def _build_rows(self, g_leaves, mu_leaves, nu_leaves, p_leaves, *, apply, decay_mask, random_bits):
         torch = _torch()
@@ -568,6 +589,8 @@ class _Engine:
                 if m.dtype not in (torch.float32, torch.bfloat16):
                     raise NotImplementedError(f"fallback moment dtype {m.dtype} is not supported")
                 row.moment_kind = _lib.RF_MOMENT_BF16 if m.dtype == torch.bfloat16 else _lib.RF_MOMENT_F32
+                if self.store_sr and m.dtype == torch.bfloat16:
+                    row.flags |= _lib.RF_LEAF_STORE_SR
                 row.mu = m.data_ptr()
                 row.nu = v.data_ptr()
                 align_ok = m.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0
@@ -657,7 +680,7 @@ class _Engine:
     ):
         torch = _torch()
         cfg = self.cfg
-        key_mu, key_nu, next_key = prng.split(state.key, 3)
+        key_mu, key_nu, next_key = self.split_keys(state.key)
         count_inc = safe_int32_increment(int(np.asarray(state.count)))
 
         g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
@@ -716,7 +739,8 @@ class _Engine:
 
         hp = _lib.Adam8Hparams()
         hp.b1 = _as_f32(cfg.b1)
-        hp.one_minus_b1 = _one_minus(cfg.b1)
+        hp.one_minus_b1 = self.ema_weight(cfg.b1)
+        hp.nesterov_one_minus_b1 = _one_minus(cfg.b1)
         hp.b2 = _as_f32(cfg.b2)
         hp.one_minus_b2 = _one_minus(cfg.b2)
         hp.bc1 = _bias_correction(cfg.b1, count_inc)
@@ -737,12 +761,7 @@ class _Engine:
             with torch.cuda.device(device):
                 plan.run(table, hp, _lib.stream_ptr())
 
-        new_state = ScaleByAdam8State(
-            count=np.asarray(count_inc, dtype=np.int32),
-            mu=state.mu,
-            nu=state.nu,
-            key=next_key,
-        )
+        new_state = self.new_state(state, count_inc, next_key)
         out_tree = _tree.unflatten(g_td, out_leaves) if not apply else None
         return out_tree, new_state
 

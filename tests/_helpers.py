@@ -88,13 +88,15 @@ class OracleTree:
 
     def step(self, grads, *, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0, weight_decay=0.0, lr=1e-3,
              count=1, decay_mask=None, nesterov=False, moment_sr=False, param_sr=False, apply=True,
-             mu_bits=None, nu_bits=None, p_bits=None, lr_scale=True):
+             mu_bits=None, nu_bits=None, p_bits=None, lr_scale=True, decay_weak=True, ema_weight_f32=False,
+             store_sr=False):
         outs = []
         for i, L in enumerate(self.leaves):
             decays = weight_decay != 0.0 and (decay_mask is None or decay_mask[i])
             hp = orc.make_hparams(b1=b1, b2=b2, eps=eps, eps_root=eps_root, weight_decay=weight_decay,
                                   lr=lr if lr_scale else None, count=count, nesterov=nesterov, decay=decays,
-                                  decay_weak=True, moment_sr=moment_sr, param_sr=param_sr, apply=apply)
+                                  decay_weak=decay_weak, moment_sr=moment_sr, param_sr=param_sr, apply=apply,
+                                  ema_weight_f32=ema_weight_f32, store_sr=store_sr and L["kind"] == "bf16")
             pd = orc.BF16 if L["pdtype"] == "bf16" else orc.F32
             gd = orc.BF16 if L["gdtype"] == "bf16" else orc.F32
             mk = {"quant": orc.MOM_QUANT, "f32": orc.MOM_F32, "bf16": orc.MOM_BF16}[L["kind"]]

@@ -239,3 +239,38 @@ def test_apply_updates_prefix_skips_subtrees():
     assert torch.allclose(out["train"]["w"], torch.full((2,), 2.0, device="cuda"))
     assert torch.allclose(out["train"]["b"], torch.full((2,), 3.0, device="cuda"))
     assert out["static"] == {"name": "layer"}
+
+
+def test_tree_stochastic_cast_keys_and_passthrough():
+    """utils.py:374-409: keys are split over every leaf of the flatten with
+    is_leaf=None/MaskedNode, so aux leaves consume subkeys too; aux leaves and
+    bf16 leaves come back unchanged, complex leaves become complex64, f32
+    leaves are stochastically rounded with their own subkey."""
+    import torch
+
+    from rollfast_amd._base import MaskedNode
+    from rollfast_amd.utils import _tree_stochastic_cast
+
+    rf = _rf()
+    rng = np.random.default_rng(7)
+    a = _edge_values(rng, 5000)
+    d = bf16_bits(rng.standard_normal(300).astype(np.float32))
+    e = rng.standard_normal(777).astype(np.float32)
+    mask = MaskedNode()
+    tree = {"a": to_device(a, "f32"), "b": None, "c": mask, "d": to_device(d, "bf16"),
+            "e": to_device(e, "f32"), "z": torch.ones(3, dtype=torch.complex128, device="cuda")}
+    key = rf.prng.PRNGKey(11)
+    out = _tree_stochastic_cast(tree, torch.bfloat16, key)
+    torch.cuda.synchronize()
+    # flatten order with aux leaves as leaves: a, b, c, d, e, z -> 6 subkeys
+    keys = orc.split(tuple(int(k) for k in key), 6)
+    for name, x, i in (("a", a, 0), ("e", e, 4)):
+        want = orc.sr_bf16(x, orc.random_bits(tuple(keys[i]), x.size))
+        got = to_host(out[name])
+        nan = np.isnan(orc.bf16_bits_to_f32(want))
+        np.testing.assert_array_equal(got[~nan], want[~nan], err_msg=name)
+    assert out["b"] is None and out["c"] is mask
+    assert out["d"] is tree["d"]
+    assert out["z"].dtype == torch.complex64
+    f32 = _tree_stochastic_cast({"a": tree["a"]}, torch.float32, key)["a"]
+    assert f32.dtype == torch.float32

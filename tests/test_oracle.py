@@ -394,3 +394,135 @@ def test_quantized_moments_track_fp32_moments():
         err = np.abs(got - want).reshape(-1, bs).max(axis=1)
         assert np.all(err <= 5 * 0.01 * sc), (err, sc)
         assert np.all(err > 0)  # the moments really are quantized
+
+
+# ------------------------------------------- full-precision AdamW (adam.py) --
+def _bc(b, t) -> float:
+    """1 - b**t as JAX evaluates it for a Python-float b and an int32 count:
+    in f32 from f32(b) (optax and rollfast alike; its bits against XLA's pow
+    are parity unpinned)."""
+    return float(np.float32(1.0) - np.power(np.float32(b), np.float32(t)))
+
+
+def _textbook_adam_updates(p, grads, *, b1, b2, eps, wd=0.0, lr=None, mask=True, nesterov=False):
+    """optax.scale_by_adam / optax.adamw direction in float64 (bias-correction
+    factors as JAX computes them), params advanced by the updates when lr is
+    given."""
+    p = p.astype(np.float64).copy()
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    outs = []
+    for t, g in enumerate(grads, start=1):
+        g = g.astype(np.float64)
+        m = b1 * m + (1 - b1) * g
+        v = b2 * v + (1 - b2) * g * g
+        if nesterov:
+            mh = b1 * m / _bc(b1, t + 1) + (1 - b1) * g / _bc(b1, t)
+        else:
+            mh = m / _bc(b1, t)
+        u = mh / (np.sqrt(v / _bc(b2, t)) + eps)
+        if lr is not None:
+            u = -lr * (u + (wd * p if mask else 0.0))
+            p = p + u
+        outs.append(u)
+    return outs
+
+
+def _oracle_adam_steps(p, grads, *, lr=None, wd=0.0, decay=False, nesterov=False, eps=1e-8):
+    p = p.astype(np.float32).copy()
+    mu = np.zeros(p.size, np.float32)
+    nu = np.zeros(p.size, np.float32)
+    outs = []
+    for t, g in enumerate(grads, start=1):
+        upd = np.empty(p.size, np.float32)
+        hp = orc.make_hparams(eps=eps, weight_decay=wd, lr=lr, count=t, decay=decay, nesterov=nesterov,
+                              ema_weight_f32=True)
+        orc.adam8_leaf(hp, p.copy(), orc.F32, g.astype(np.float32), orc.F32, orc.MOM_F32, mu, None, nu, None,
+                       updates_out=upd)
+        outs.append(upd)
+        p = (p + upd).astype(np.float32)
+    return outs
+
+
+@pytest.mark.parametrize("nesterov", [False, True])
+def test_scale_by_adam_matches_textbook_direction(nesterov):
+    """tests/test_adam.py:32-47: three steps of scale_by_adam against
+    optax.scale_by_adam's direction (float64 textbook here), atol 1e-6."""
+    p = np.array([1.0, -2.0], np.float32)
+    grads = [np.array([0.1, -0.2], np.float32)] * 3
+    got = _oracle_adam_steps(p, grads, nesterov=nesterov)
+    want = _textbook_adam_updates(p, grads, b1=0.9, b2=0.999, eps=1e-8, nesterov=nesterov)
+    for a, b in zip(got, want):
+        np.testing.assert_allclose(a, b, atol=1e-6)
+
+
+def test_adamw_masked_decoupled_weight_decay_matches_textbook():
+    """tests/test_adam.py:87-116: adamw(lr 0.01, wd 0.1, mask w only) over
+    three steps against optax.adamw (float64 textbook here), atol 1e-6."""
+    pw = np.array([1.0, -2.0], np.float32)
+    pb = np.array([0.5], np.float32)
+    gw = [np.array([0.1, -0.2], np.float32)] * 3
+    gb = [np.array([0.0], np.float32)] * 3
+    got_w = _oracle_adam_steps(pw, gw, lr=0.01, wd=0.1, decay=True)
+    got_b = _oracle_adam_steps(pb, gb, lr=0.01, wd=0.1, decay=False)
+    want_w = _textbook_adam_updates(pw, gw, b1=0.9, b2=0.999, eps=1e-8, wd=0.1, lr=0.01, mask=True)
+    want_b = _textbook_adam_updates(pb, gb, b1=0.9, b2=0.999, eps=1e-8, wd=0.1, lr=0.01, mask=False)
+    for a, b in zip(got_w + got_b, want_w + want_b):
+        np.testing.assert_allclose(a, b, atol=1e-6)
+
+
+def test_adam_ema_weight_conventions_differ_where_expected():
+    """optim/adam.py weights the gradient by 1 - f32(b1) computed in f32
+    (utils.py:327-335); adam8.py by the double 1.0 - b1.  For b1 = 0.9 the
+    two f32 weights differ (0x3dccccd0 vs 0x3dcccccd), so the stored first
+    moment differs in the last bits for generic gradients: the double weight
+    stays within 2^-23 (relative) of 0.1 * g, the f32 weight, itself 2.4e-7
+    off, within 2^-21."""
+    a = orc.make_hparams(ema_weight_f32=True)
+    b = orc.make_hparams()
+    assert np.float32(a.one_minus_b1).view(np.uint32) == 0x3DCCCCD0
+    assert np.float32(b.one_minus_b1).view(np.uint32) == 0x3DCCCCCD
+    assert a.nest_one_minus_b1 == b.nest_one_minus_b1 == np.float32(0.1)
+    rng = np.random.default_rng(9)
+    g = rng.standard_normal(4096).astype(np.float32)
+    ms = []
+    for hp in (a, b):
+        mu = np.zeros(g.size, np.float32)
+        nu = np.zeros(g.size, np.float32)
+        orc.adam8_leaf(hp, np.zeros(g.size, np.float32), orc.F32, g, orc.F32, orc.MOM_F32, mu, None, nu, None,
+                       updates_out=np.empty(g.size, np.float32))
+        ms.append(mu)
+    assert np.count_nonzero(ms[0] != ms[1]) > 1000
+    exact = 0.1 * g.astype(np.float64)
+    rel = [np.abs(m - exact) / np.abs(exact) for m in ms]
+    assert rel[1].max() <= 2.0 ** -23 and rel[0].max() <= 2.0 ** -21
+    assert rel[0].max() > 2.0 ** -23  # the f32 weight really is the other convention
+
+
+def test_bf16_moment_store_sr_is_the_sr_of_the_f32_moments():
+    """mu_dtype=bfloat16 (adam.py:219-222): the stored bf16 moments are
+    _stochastic_round_bf16 of the f32 moments with the fed bits."""
+    rng = np.random.default_rng(10)
+    n = 5000
+    g = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+    mb = orc.random_bits((1, 2), n)
+    vb = orc.random_bits((3, 4), n)
+    hp32 = orc.make_hparams(ema_weight_f32=True)
+    mu32 = np.zeros(n, np.float32)
+    nu32 = np.zeros(n, np.float32)
+    orc.adam8_leaf(hp32, np.zeros(n, np.float32), orc.F32, g, orc.F32, orc.MOM_F32, mu32, None, nu32, None,
+                   updates_out=np.empty(n, np.float32))
+    hp16 = orc.make_hparams(ema_weight_f32=True, store_sr=True)
+    mu16 = np.zeros(n, np.uint16)
+    nu16 = np.zeros(n, np.uint16)
+    orc.adam8_leaf(hp16, np.zeros(n, np.float32), orc.F32, g, orc.F32, orc.MOM_BF16, mu16, None, nu16, None,
+                   mu_bits=mb, nu_bits=vb, updates_out=np.empty(n, np.float32))
+    np.testing.assert_array_equal(mu16, orc.sr_bf16(mu32, mb))
+    np.testing.assert_array_equal(nu16, orc.sr_bf16(nu32, vb))
+    # without store_sr the bf16 moments are rounded to nearest even (adam8.py:688)
+    hp_rne = orc.make_hparams(ema_weight_f32=True)
+    mu16[:] = 0
+    nu16[:] = 0
+    orc.adam8_leaf(hp_rne, np.zeros(n, np.float32), orc.F32, g, orc.F32, orc.MOM_BF16, mu16, None, nu16, None,
+                   updates_out=np.empty(n, np.float32))
+    np.testing.assert_array_equal(mu16, orc.f32_to_bf16_bits(mu32))
