@@ -19,6 +19,9 @@ Other workloads (one JSON line each, same fields):
                    Student-t(3) grads with per-leaf scales, 10 % zero blocks.
   llama7b_optax    update-only (Optax) mode over the Llama tree: f32 updates
                    written, params read for weight decay.
+  llama7b_adamw_f32   full-precision AdamW (adamw, f32 moments) over the Llama
+                   tree: 22 B/param.
+  llama7b_adamw_bf16  the same with stochastically rounded bf16 moments.
   llama7b_apply    apply_updates of f32 updates to the bf16 Llama params with
                    stochastic rounding (in-kernel Threefry bits).
   quantize_2p30    quantize_blocks, dynamic signed, 2^30 f32 elements
@@ -253,7 +256,7 @@ class Workload:
         self.step, self.config, self.cpu, self.metric = step, config, cpu, metric
 
 
-def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False):
+def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None):
     import numpy as np
     import torch
 
@@ -266,7 +269,11 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     gen.manual_seed(0)
     params = {name: (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 0.02).to(torch.bfloat16)
               for name, s in shapes}
-    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=args.exact)
+    if adam_mu is None:
+        tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=args.exact)
+    else:
+        tx = rf.adamw(learning_rate=1e-3, weight_decay=0.01, exact=args.exact,
+                      mu_dtype=torch.bfloat16 if adam_mu == "bf16" else None)
     state = tx.init(params)
     pool = []
     rng = np.random.default_rng(0)
@@ -300,7 +307,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
             holder["params"], holder["state"] = rf.adamw8_step(tx, holder["params"], g, holder["state"], key=key,
                                                                stochastic=param_sr)
 
-    n_quant = sum(1 for _, s in shapes if _numel(s) >= MIN_SIZE)
+    n_quant = sum(1 for _, s in shapes if _numel(s) >= MIN_SIZE) if adam_mu is None else 0
     config = {
         "workload": workload,
         "params": n_params,
@@ -309,7 +316,9 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         "block_size": BS,
         "param_dtype": "bf16",
         "grad_dtype": "bf16",
-        "moments": "uint8 codebook codes + f32 block scales (f32 fallback below 4096 elements)",
+        "moments": ("uint8 codebook codes + f32 block scales (f32 fallback below 4096 elements)"
+                    if adam_mu is None else f"{adam_mu} (full-precision AdamW"
+                    + (", stochastically rounded storage)" if adam_mu == "bf16" else ")")),
         "param_rounding": "stochastic" if param_sr else "nearest-even",
         "direction": "ieee" if args.exact else "hw rcp/sqrt",
         "mode": "optax update-only (f32 updates)" if optax else "fused step (params written)",
@@ -323,7 +332,13 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         cpu = lambda: cpu_baseline(args.cpu_seconds, shapes=sub,  # noqa: E731
                                    sample_name=f"the first {len(sub)} leaves", param_sr=param_sr)
     metric = METRIC if workload == "llama7b_bf16_adamw8" else f"adam8 params/sec + achieved HBM GB/s, {workload}, 1 GPU"
-    return Workload(workload, n_params, "params/s", step_bytes(shapes, apply=not optax), step, config, cpu, metric)
+    if adam_mu is None:
+        nbytes = step_bytes(shapes, apply=not optax)
+    else:
+        mb = 4 if adam_mu == "f32" else 2
+        nbytes = n_params * (2 + 2 + 2 + 2 * 2 * mb)  # p r+w, g r, two moments r+w
+        cpu = None
+    return Workload(workload, n_params, "params/s", nbytes, step, config, cpu, metric)
 
 
 def _c5_input(n):
@@ -416,6 +431,10 @@ WORKLOADS = {
                                        grads="student_t"),
     "llama7b_optax": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_optax_update",
                                               param_sr=False, optax=True),
+    "llama7b_adamw_f32": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw_f32_moments",
+                                                  param_sr=False, adam_mu="f32"),
+    "llama7b_adamw_bf16": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw_bf16_moments",
+                                                   param_sr=False, adam_mu="bf16"),
     "llama7b_apply": lambda a: _kernel_workload(a, "apply"),
     "quantize_2p30": lambda a: _kernel_workload(a, "quantize"),
     "dequantize_2p30": lambda a: _kernel_workload(a, "dequantize"),
@@ -484,7 +503,7 @@ def main(argv=None):
         del src, dst
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and wl.cpu is not None:
         print("[bench] CPU oracle baseline", file=sys.stderr, flush=True)
         cpu = wl.cpu()
 

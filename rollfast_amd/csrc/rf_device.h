@@ -48,7 +48,7 @@ constexpr int64_t CHUNK = 2048;    // elements per fallback (unquantized moment)
 #define RF_PREFETCH_NEXT 1
 #endif
 
-enum : int32_t { KIND_QFAST = 0, KIND_QGEN = 1, KIND_FALLBACK = 2 };
+enum : int32_t { KIND_QFAST = 0, KIND_QGEN = 1, KIND_FALLBACK = 2, KIND_FALLBACK_VEC = 3 };
 
 // Kernel-side scalars (derived from rf_adam8_hparams on the host).
 struct KHp {
@@ -876,6 +876,148 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
     }
 }
 
+// Full 2048-element chunk of a fallback (unquantized-moment) leaf whose
+// buffers are 16-byte aligned (KIND_FALLBACK_VEC): lane l owns elements
+// j*512 + 8l .. +7 of the chunk, so every access is a 16-byte vector access;
+// the four chunks' loads are issued before any arithmetic.  Dtypes are
+// template parameters (PT params, GT grads, MT moments: uint16_t = bf16).
+template <typename PT, typename GT, typename MT, bool APPLY, bool PSR, bool NEST, bool EXACT>
+__device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_adam8_leaf& L, int64_t chunk,
+                                                  const KHp& h)
+{
+    constexpr int J = (int)(CHUNK / 512);
+    constexpr bool BF16M = std::is_same<MT, uint16_t>::value;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t base = chunk * CHUNK;
+    const int32_t wdm = c.wd_mode;
+    const bool need_p = APPLY || wdm != WD_OFF;
+    const bool store_sr = BF16M && (L.flags & RF_LEAF_STORE_SR);
+
+    // Two chunks in flight: chunk j+1's loads are issued before chunk j's
+    // arithmetic.
+    Raw8<GT> graw[2];
+    Raw8<PT> praw[2];
+    Raw8<MT> mraw[2], vraw[2];
+    auto issue = [&](int j, int slot) {
+        const int64_t e0 = base + j * 512 + lane * 8;
+        raw8_load<GT>(graw[slot], L.grad, e0);
+        if (need_p) raw8_load<PT>(praw[slot], L.param, e0);
+        raw8_load<MT>(mraw[slot], L.mu, e0);
+        raw8_load<MT>(vraw[slot], L.nu, e0);
+    };
+    issue(0, 0);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int64_t e0 = base + j * 512 + lane * 8;
+        const int slot = j & 1;
+        if (j + 1 < J) issue(j + 1, slot ^ 1);
+        float g[8], p[8], m[8], v[8], u[8];
+        raw8_unpack<GT>(graw[slot], g);
+        if (need_p) {
+            raw8_unpack<PT>(praw[slot], p);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) p[t] = 0.0f;
+        }
+        raw8_unpack<MT>(mraw[slot], m);
+        raw8_unpack<MT>(vraw[slot], v);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            float mm, vv;
+            ema(h, m[t], v[t], g[t], mm, vv);
+            m[t] = mm;
+            v[t] = vv;
+            u[t] = decay_and_scale(h, adam_direction<NEST, EXACT>(h, mm, vv, g[t]), p[t], wdm);
+        }
+        if constexpr (APPLY) {
+            float sum[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) sum[t] = p[t] + u[t];
+            if constexpr (!EXACT) {
+                bool risky = false;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) risky |= cancels(sum[t], u[t]);
+                if (__builtin_amdgcn_ballot_w64(risky) != 0) {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        if (cancels(sum[t], u[t]))
+                            sum[t] = p[t] + decay_and_scale(h, adam_direction<NEST, true>(h, m[t], v[t], g[t]), p[t],
+                                                            wdm);
+                    }
+                }
+            }
+            if constexpr (std::is_same<PT, uint16_t>::value) {
+                uint32_t hb[8];
+                if constexpr (PSR) {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const uint32_t rb = c.fed ? L.param_bits[e0 + t] : jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
+                        hb[t] = sr_bf16(sum[t], rb);
+                    }
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; t += 2) {
+                        const uint32_t w2 = pack_bf16x2_rne(sum[t], sum[t + 1]);
+                        hb[t] = w2 & 0xFFFFu;
+                        hb[t + 1] = w2 >> 16;
+                    }
+                }
+                store8_bf16(L.param, e0, hb);
+            } else {
+                store8_f32(L.param, e0, sum);
+            }
+        } else {
+            store8_f32(L.updates, e0, u);
+        }
+        // adam8.py:688 moment.astype(fallback_dtype) / optim/adam.py:219-222 SR storage
+        if constexpr (BF16M) {
+            uint32_t hm[8], hv[8];
+            if (store_sr) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const uint64_t e = (uint64_t)(e0 + t);
+                    const uint32_t bm = c.fed ? L.mu_bits[e] : jax_bits(c.kmu0, c.kmu1, e);
+                    const uint32_t bv = c.fed ? L.nu_bits[e] : jax_bits(c.knu0, c.knu1, e);
+                    hm[t] = sr_bf16(m[t], bm);
+                    hv[t] = sr_bf16(v[t], bv);
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; t += 2) {
+                    const uint32_t wm = pack_bf16x2_rne(m[t], m[t + 1]);
+                    const uint32_t wv = pack_bf16x2_rne(v[t], v[t + 1]);
+                    hm[t] = wm & 0xFFFFu;
+                    hm[t + 1] = wm >> 16;
+                    hv[t] = wv & 0xFFFFu;
+                    hv[t + 1] = wv >> 16;
+                }
+            }
+            store8_bf16(L.mu, e0, hm);
+            store8_bf16(L.nu, e0, hv);
+        } else {
+            store8_f32(L.mu, e0, m);
+            store8_f32(L.nu, e0, v);
+        }
+    }
+}
+
+template <bool APPLY, bool PSR, bool NEST, bool EXACT>
+__device__ __forceinline__ void dispatch_fallback_vec(const UnitCtx& c, const rf_adam8_leaf& L, int64_t chunk,
+                                                      const KHp& h)
+{
+    // Vectorised instances for params and grads of one dtype; other mixes
+    // take the element-wise unit (same arithmetic).
+    const int sel = (L.param_dtype == RF_BF16 ? 4 : 0) | (L.grad_dtype == RF_BF16 ? 2 : 0) |
+                    (L.moment_kind == RF_MOMENT_BF16 ? 1 : 0);
+    switch (sel) {
+    case 0: unit_fallback_vec<float, float, float, APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
+    case 1: unit_fallback_vec<float, float, uint16_t, APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
+    case 6: unit_fallback_vec<uint16_t, uint16_t, float, APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
+    case 7: unit_fallback_vec<uint16_t, uint16_t, uint16_t, APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
+    default: unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
+    }
+}
+
 // ======================================================== step kernels ===
 __device__ __forceinline__ void leaf_context(UnitCtx& c, const rf_adam8_leaf& L, const KHp& h, bool msr, bool psr)
 {
@@ -966,6 +1108,7 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
         }
         const int64_t idx = sg.first + (u - sg.unit_start);
         if (sg.kind == KIND_QGEN) unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
+        else if (sg.kind == KIND_FALLBACK_VEC) dispatch_fallback_vec<APPLY, PSR, NEST, EXACT>(c, L, idx, h);
         else unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, idx, h);
     }
 }

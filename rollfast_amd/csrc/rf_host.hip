@@ -747,7 +747,11 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
                 add(i, 4, KIND_QGEN, 0, nb);
             }
         } else {
-            add(i, 4, KIND_FALLBACK, 0, (L.size + CHUNK - 1) / CHUNK);
+            // Full chunks of aligned leaves take the vectorised unit, the
+            // tail the element-wise one.
+            const int64_t nfull = vec ? L.size / CHUNK : 0;
+            add(i, 4, KIND_FALLBACK_VEC, 0, nfull);
+            add(i, 4, KIND_FALLBACK, nfull, (L.size - nfull * CHUNK + CHUNK - 1) / CHUNK);
         }
     }
     std::vector<Seg> segs;
