@@ -114,7 +114,12 @@ typedef struct rf_adam8_hparams {
                                     sets it equal to one_minus_b1; optim/adam.py's EMA
                                     weight one_minus_b1 is 1 - f32(b1) in f32
                                     (utils.py:327-335) and differs from it. */
-    uint32_t reserved;       /* 0 */
+    float clip_max_norm;     /* > 0: the step first scales the grads by
+                                min(1, clip_max_norm / (global L2 norm + 1e-6)) with the
+                                norm over all the run's leaves (finetune/transforms.py:20-82
+                                clip_by_global_norm, fused); 0: no clipping */
+    float* clip_out;         /* optional device f32[2] receiving (scale, norm) of the clipping,
+                                or NULL */
 } rf_adam8_hparams;
 
 typedef struct rf_adam8_plan rf_adam8_plan;

@@ -257,3 +257,34 @@ def apply_updates(param: np.ndarray, pdtype: int, upd: np.ndarray, bits=None) ->
     upd = np.ascontiguousarray(upd, dtype=np.float32).reshape(-1)
     lib().orc_apply_updates(pdtype, _ptr(param), _ptr(upd), upd.size, 1 if bits is not None else 0,
                             _ptr(bits))
+
+
+# ------------------------------------------------- global-norm clipping --
+def global_norm_clip_scale(grads, max_norm: float):
+    """rollfast finetune/transforms.py:57-82 clip_by_global_norm, restated:
+    each leaf's sum of squares of its f32 values (here in float64 and rounded
+    once to f32; XLA's f32 reduction order is unspecified), leaf sums added
+    in f32 in leaf order, norm = sqrt in f32, scale = min(1, f32(max_norm) /
+    (norm + f32(1e-6))) with NaN propagating like jnp.minimum.  ``grads``:
+    list of f32 arrays (bf16 leaves already widened).  Returns (scale, norm)
+    as f32."""
+    total = np.float32(0.0)
+    with np.errstate(over="ignore", invalid="ignore"):
+        for g in grads:
+            s = np.sum(np.square(np.asarray(g, dtype=np.float64)))
+            total = np.float32(total + np.float32(s))
+        norm = np.sqrt(total, dtype=np.float32)
+        q = np.float32(np.float32(max_norm) / np.float32(norm + np.float32(1e-6)))
+    scale = q if (np.isnan(q) or q < np.float32(1.0)) else np.float32(1.0)
+    return np.float32(scale), np.float32(norm)
+
+
+def clip_leaf(g: np.ndarray, dtype: int, scale) -> np.ndarray:
+    """transforms.py:79-82 ``leaf * scale.astype(leaf.dtype)``: f32 leaves
+    multiply in f32; bf16 leaves (bit patterns) multiply by bf16(scale) with
+    one round-to-nearest-even of the exact product."""
+    if dtype == F32:
+        return (np.asarray(g, np.float32) * np.float32(scale)).astype(np.float32)
+    s16 = bf16_bits_to_f32(f32_to_bf16_bits(np.array([scale], np.float32)))[0]
+    prod = bf16_bits_to_f32(np.asarray(g, np.uint16)) * np.float32(s16)  # exact: 8 x 8 significant bits
+    return f32_to_bf16_bits(prod)

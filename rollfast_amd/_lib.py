@@ -74,7 +74,8 @@ class Adam8Hparams(ctypes.Structure):
         ("key_nu", ctypes.c_uint32 * 2),
         ("key_param", ctypes.c_uint32 * 2),
         ("nesterov_one_minus_b1", ctypes.c_float),
-        ("reserved", ctypes.c_uint32),
+        ("clip_max_norm", ctypes.c_float),
+        ("clip_out", _p),
     ]
 
 
@@ -90,7 +91,7 @@ class ApplyLeaf(ctypes.Structure):
 
 
 assert ctypes.sizeof(Adam8Leaf) == 120
-assert ctypes.sizeof(Adam8Hparams) == 80
+assert ctypes.sizeof(Adam8Hparams) == 88
 assert ctypes.sizeof(ApplyLeaf) == 40
 
 # Every symbol the header declares (checked by the CPU test suite).

@@ -65,6 +65,7 @@ struct KHp {
     float neg_lr;             // f32(-lr), or 1.0 when the chain has no learning-rate scale
     uint32_t flags;
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;
+    const float* clip;        // device (scale, norm) of global-norm clipping, or null
 };
 
 // Work list: unit u belongs to the segment s with
@@ -90,6 +91,15 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float x)
 }
 
 __device__ __forceinline__ float round_to_bf16(float x) { return bf16_bits_to_f32(f32_to_bf16_rne(x)); }
+
+// Two f32 -> bf16 (round to nearest even) in one v_cvt_pk_bf16_f32; the
+// result is the packed pair (lo, hi).
+typedef float rf_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 rf_bf2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((rf_f2){lo, hi}, rf_bf2));
+}
 
 // utils.py:365-371: noise = bits & 0xFFFF; no noise for |x| >= Inf bits;
 // (x_u32 + noise) & 0xFFFF0000 -> bf16 (exact truncation).
@@ -386,8 +396,54 @@ struct UnitCtx {
     float* wtab;  // this wave's 512-float LDS region (dequant-and-decay tables)
     int32_t wd_mode;
     bool fed;
+    bool clip;        // grads are scaled by the global-norm clipping factor
+    float cs, cs16;   // that factor as f32 and rounded to bf16
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;  // per-leaf keys
 };
+
+// Global-norm clipping of one gradient element (finetune/transforms.py:79-82,
+// leaf * scale.astype(leaf.dtype)): f32 grads multiply in f32; bf16 grads by
+// the bf16-rounded factor, the exact product rounded once to bf16.
+__device__ __forceinline__ float clip1(const UnitCtx& c, float g, bool bf16)
+{
+    return bf16 ? round_to_bf16(g * c.cs16) : g * c.cs;
+}
+
+template <typename GT>
+__device__ __forceinline__ void clip8(const UnitCtx& c, float (&g)[8])
+{
+    if (!c.clip) return;
+    if constexpr (std::is_same<GT, uint16_t>::value) {
+#pragma unroll
+        for (int t = 0; t < 8; t += 2) {
+            const uint32_t w2 = pack_bf16x2_rne(g[t] * c.cs16, g[t + 1] * c.cs16);
+            g[t] = __uint_as_float(w2 << 16);
+            g[t + 1] = __uint_as_float(w2 & 0xFFFF0000u);
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) g[t] = g[t] * c.cs;
+    }
+}
+
+// Clipped gradient element of the generic paths (runtime dtype).
+__device__ __forceinline__ float load_grad1(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e)
+{
+    const float g = load1(L.grad, L.grad_dtype, e);
+    return c.clip ? clip1(c, g, L.grad_dtype == RF_BF16) : g;
+}
+
+// Kernel-start setup of the clipping factor (one scalar load per wave).
+__device__ __forceinline__ void clip_context(UnitCtx& c, const KHp& h)
+{
+    c.clip = h.clip != nullptr;
+    c.cs = 1.0f;
+    c.cs16 = 1.0f;
+    if (c.clip) {
+        c.cs = h.clip[0];
+        c.cs16 = round_to_bf16(c.cs);
+    }
+}
 
 // The param after the update (fused) for one element.
 template <bool PSR, typename PT>
@@ -452,7 +508,7 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
     for (int64_t j = lane; j < nvalid; j += WAVE) {
         const int64_t e = base + j;
         float mm, vv;
-        ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, load1(L.grad, L.grad_dtype, e), mm, vv);
+        ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, load_grad1(c, L, e), mm, vv);
         am = max(am, __float_as_uint(mm) & 0x7FFFFFFFu);
         av = max(av, __float_as_uint(vv));
     }
@@ -467,7 +523,7 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
     for (int64_t j = lane; j < bs; j += WAVE) {
         const int64_t e = base + j;
         float mm = 0.0f, vv = 0.0f;
-        if (j < nvalid) ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, load1(L.grad, L.grad_dtype, e), mm, vv);
+        if (j < nvalid) ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, load_grad1(c, L, e), mm, vv);
         uint32_t cm, cv;
         if (fast_m) {
             cm = code_signed_fast(c.lds, mm, sm, rsm);
@@ -544,14 +600,6 @@ __device__ __forceinline__ void raw8_unpack(const Raw8<T>& r, float (&x)[8])
     }
 }
 
-// Two f32 -> bf16 (round to nearest even) in one v_cvt_pk_bf16_f32; the
-// result is the packed pair (lo, hi).
-typedef float rf_f2 __attribute__((ext_vector_type(2)));
-typedef __bf16 rf_bf2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi)
-{
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((rf_f2){lo, hi}, rf_bf2));
-}
 
 template <int WDM>
 __device__ __forceinline__ void decay_and_scale8(const KHp& h, float (&u)[8], const float (&p)[8])
@@ -665,6 +713,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
         else if (next_blk >= 0) issue_chunk<PT, GT, NEED_P>(sl, L, next_blk, 0, 0);  // slot 0 is free
         float g[8], p[8];
         raw8_unpack<GT>(sl.graw[slot], g);
+        clip8<GT>(c, g);
         if constexpr (NEED_P) {
             raw8_unpack<PT>(sl.praw[slot], p);
         } else {
@@ -839,7 +888,7 @@ __device__ __forceinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf&
 
     for (int64_t j = lane; j < nvalid; j += WAVE) {
         const int64_t e = base + j;
-        const float g = load1(L.grad, L.grad_dtype, e);
+        const float g = load_grad1(c, L, e);
         float mm, vv;
         ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, g, mm, vv);
         update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g);
@@ -859,7 +908,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
     const int32_t mdt = L.moment_kind == RF_MOMENT_BF16 ? RF_BF16 : RF_F32;
     const bool store_sr = mdt == RF_BF16 && (L.flags & RF_LEAF_STORE_SR);
     for (int64_t e = base + lane; e < end; e += WAVE) {
-        const float g = load1(L.grad, L.grad_dtype, e);
+        const float g = load_grad1(c, L, e);
         float mm, vv;
         ema(h, load1(L.mu, mdt, e), load1(L.nu, mdt, e), g, mm, vv);
         update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g);
@@ -913,6 +962,7 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
         if (j + 1 < J) issue(j + 1, slot ^ 1);
         float g[8], p[8], m[8], v[8], u[8];
         raw8_unpack<GT>(graw[slot], g);
+        clip8<GT>(c, g);
         if (need_p) {
             raw8_unpack<PT>(praw[slot], p);
         } else {
@@ -1051,6 +1101,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     c.lds = lds;
     c.wtab = wtab[wave_in_wg];
     c.fed = (h.flags & RF_FED_BITS) != 0;
+    clip_context(c, h);
     c.wd_mode = WD_OFF;
     c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;
     rf_adam8_leaf L;
@@ -1095,6 +1146,7 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
     c.lds = lds;
     c.wtab = nullptr;
     c.fed = (h.flags & RF_FED_BITS) != 0;
+    clip_context(c, h);
     c.wd_mode = WD_OFF;
     c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;
     rf_adam8_leaf L;

@@ -329,6 +329,86 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
     }
 }
 
+// Global-norm clipping pre-pass (finetune/transforms.py:57-82): sum of
+// squares of the f32 grad values, in f64 per NORM_UNIT-element unit (exact
+// products, negligible accumulation error), then per leaf rounded once to
+// f32, then the leaf sums added in f32 in leaf order; norm = sqrtf(total),
+// scale = min(1, max_norm / (norm + 1e-6)) with NaN propagating.
+constexpr int64_t NORM_UNIT = 16384;
+
+__device__ __forceinline__ double wave_sum_f64(double x)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, WAVE);
+    return x;
+}
+
+__global__ __launch_bounds__(WG) void k_gnorm_partial(const rf_adam8_leaf* __restrict__ leaves,
+                                                      const Seg* __restrict__ nsegs, int64_t nunits,
+                                                      double* __restrict__ part)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    int32_t s = 0;
+    for (int64_t u = wave; u < nunits; u += nwaves) {
+        while (nsegs[s + 1].unit_start <= u) ++s;
+        const Seg sg = nsegs[s];
+        const rf_adam8_leaf& L = leaves[sg.leaf];
+        const int64_t e_begin = (u - sg.unit_start) * NORM_UNIT;
+        const int64_t e_end = min(L.size, e_begin + NORM_UNIT);
+        double acc = 0.0;
+        const bool bf16 = L.grad_dtype == RF_BF16;
+        if (e_end - e_begin == NORM_UNIT && ((uintptr_t)L.grad & 15u) == 0) {
+            for (int64_t e0 = e_begin + lane * 8; e0 < e_end; e0 += 512) {
+                float x[8];
+                if (bf16) load8<uint16_t>(L.grad, e0, x);
+                else load8<float>(L.grad, e0, x);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc += (double)x[t] * (double)x[t];
+            }
+        } else {
+            for (int64_t e = e_begin + lane; e < e_end; e += WAVE) {
+                const double x = load1(L.grad, L.grad_dtype, e);
+                acc += x * x;
+            }
+        }
+        acc = wave_sum_f64(acc);
+        if (lane == 0) part[u] = acc;
+    }
+}
+
+__global__ __launch_bounds__(WG) void k_gnorm_leaf(const Seg* __restrict__ nsegs, int32_t nseg,
+                                                   const double* __restrict__ part, float* __restrict__ leafsum)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    for (int64_t i = wave; i < nseg; i += nwaves) {
+        double acc = 0.0;
+        for (int64_t u = nsegs[i].unit_start + lane; u < nsegs[i + 1].unit_start; u += WAVE) acc += part[u];
+        acc = wave_sum_f64(acc);
+        if (lane == 0) leafsum[i] = (float)acc;
+    }
+}
+
+__global__ void k_gnorm_finish(const float* __restrict__ leafsum, int32_t nseg, float max_norm,
+                               float* __restrict__ clip, float* __restrict__ out)
+{
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    float total = 0.0f;
+    for (int32_t i = 0; i < nseg; ++i) total = total + leafsum[i];
+    const float norm = sqrtf(total);
+    const float q = max_norm / (norm + 1e-6f);
+    const float scale = (q < 1.0f || q != q) ? q : 1.0f;  // jnp.minimum(1.0, q): NaN propagates
+    clip[0] = scale;
+    clip[1] = norm;
+    if (out) {
+        out[0] = scale;
+        out[1] = norm;
+    }
+}
+
 // =================================================================== host ==
 namespace {
 
@@ -629,6 +709,15 @@ struct rf_adam8_plan {
     std::vector<PlanGroup> groups;
     rf_adam8_leaf* d_leaves = nullptr;  // creation-time pointer table
     Seg* d_segs = nullptr;
+    // Global-norm clipping (allocated with the plan): one Seg per non-empty
+    // leaf over NORM_UNIT-element units, per-unit f64 partial sums of squares,
+    // per-leaf f32 sums and the (scale, norm) pair the step reads.
+    Seg* d_nsegs = nullptr;
+    int32_t n_nsegs = 0;
+    int64_t n_norm_units = 0;
+    double* d_npart = nullptr;
+    float* d_leafsum = nullptr;
+    float* d_clip = nullptr;
     std::vector<rf_adam8_leaf> shape;   // creation-time table: the structure runs must match
     std::vector<uint8_t> vec;           // leaf has vectorised (16-byte aligned) work units
     BitsCover cover;  // which fed-bits arrays the creation-time table carries
@@ -775,10 +864,32 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
         segs.push_back(sentinel);
     }
 
+    // Norm units for global-norm clipping: every non-empty leaf, in order.
+    std::vector<Seg> nsegs;
+    int64_t nunits = 0;
+    for (int32_t i = 0; i < n_leaves; ++i) {
+        if (leaves[i].size <= 0) continue;
+        Seg sg{};
+        sg.unit_start = nunits;
+        sg.leaf = i;
+        nsegs.push_back(sg);
+        nunits += (leaves[i].size + NORM_UNIT - 1) / NORM_UNIT;
+    }
+    const int32_t n_nsegs = (int32_t)nsegs.size();
+    {
+        Seg sentinel{};
+        sentinel.unit_start = nunits;
+        sentinel.leaf = -1;
+        sentinel.kind = -1;
+        nsegs.push_back(sentinel);
+    }
+
     int device = 0;
     HIP_TRY(hipGetDevice(&device));
     rf_adam8_plan* p = new rf_adam8_plan();
     p->device = device;
+    p->n_nsegs = n_nsegs;
+    p->n_norm_units = nunits;
     p->apply = apply ? 1 : 0;
     p->n_leaves = n_leaves;
     p->total_units = units;
@@ -797,6 +908,11 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
         if (e == hipSuccess) e = hipMalloc((void**)&slot.dev, table_bytes);
         if (e == hipSuccess) e = hipEventCreateWithFlags(&slot.ev, hipEventDisableTiming);
     }
+    if (e == hipSuccess) e = hipMalloc(&p->d_nsegs, sizeof(Seg) * nsegs.size());
+    if (e == hipSuccess) e = hipMalloc(&p->d_npart, sizeof(double) * (size_t)std::max<int64_t>(nunits, 1));
+    if (e == hipSuccess) e = hipMalloc(&p->d_leafsum, sizeof(float) * (size_t)std::max(n_nsegs, 1));
+    if (e == hipSuccess) e = hipMalloc(&p->d_clip, sizeof(float) * 2);
+    if (e == hipSuccess) e = hipMemcpy(p->d_nsegs, nsegs.data(), sizeof(Seg) * nsegs.size(), hipMemcpyHostToDevice);
     if (e == hipSuccess && n_leaves > 0)
         e = hipMemcpy(p->d_leaves, leaves, sizeof(rf_adam8_leaf) * (size_t)n_leaves, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(p->d_segs, segs.data(), sizeof(Seg) * segs.size(), hipMemcpyHostToDevice);
@@ -835,11 +951,31 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         if (!cover.mb_store)
             return fail(RF_ERR_INVALID, "RF_FED_BITS: a leaf with RF_LEAF_STORE_SR has no mu_bits/nu_bits");
     }
+    const float max_norm = hp->clip_max_norm;
+    if (!(max_norm >= 0.0f) || std::isinf(max_norm))
+        return fail(RF_ERR_INVALID, "clip_max_norm must be a finite non-negative number (0: no clipping)");
     DevState* ds = nullptr;
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
 
+    if (max_norm > 0.0f) {
+        const int64_t pw = std::max<int64_t>(1, std::min<int64_t>((plan->n_norm_units + WAVES_PER_WG - 1) / WAVES_PER_WG,
+                                                                  (int64_t)ds->num_cus * 8));
+        hipLaunchKernelGGL(k_gnorm_partial, dim3((unsigned)pw), dim3(WG), 0, (hipStream_t)stream, d_leaves,
+                           plan->d_nsegs, plan->n_norm_units, plan->d_npart);
+        HIP_TRY(hipGetLastError());
+        const int64_t lw = std::max<int64_t>(1, std::min<int64_t>((plan->n_nsegs + WAVES_PER_WG - 1) / WAVES_PER_WG,
+                                                                  (int64_t)ds->num_cus * 8));
+        hipLaunchKernelGGL(k_gnorm_leaf, dim3((unsigned)lw), dim3(WG), 0, (hipStream_t)stream, plan->d_nsegs,
+                           plan->n_nsegs, plan->d_npart, plan->d_leafsum);
+        HIP_TRY(hipGetLastError());
+        hipLaunchKernelGGL(k_gnorm_finish, dim3(1), dim3(WAVE), 0, (hipStream_t)stream, plan->d_leafsum,
+                           plan->n_nsegs, max_norm, plan->d_clip, hp->clip_out);
+        HIP_TRY(hipGetLastError());
+    }
+
     KHp k{};
+    k.clip = max_norm > 0.0f ? plan->d_clip : nullptr;
     k.b1 = hp->b1;
     k.omb1 = hp->one_minus_b1;
     k.b2 = hp->b2;
@@ -908,6 +1044,8 @@ bool release_plan(rf_adam8_plan* plan)
     }
     if (plan->d_leaves) ok &= hipFree(plan->d_leaves) == hipSuccess;
     if (plan->d_segs) ok &= hipFree(plan->d_segs) == hipSuccess;
+    for (void* q : {(void*)plan->d_nsegs, (void*)plan->d_npart, (void*)plan->d_leafsum, (void*)plan->d_clip})
+        if (q) ok &= hipFree(q) == hipSuccess;
     delete plan;
     return ok;
 }

@@ -24,7 +24,6 @@ Magma (``use_magma=True``) is not part of this build and raises
 
 from __future__ import annotations
 
-import dataclasses
 from typing import Any, Callable, NamedTuple, Optional, Union
 
 import numpy as np
@@ -234,16 +233,20 @@ def adamw(
         init_fn, _Adamw8Update(engine, learning_rate, weight_decay, weight_decay_mask, wd_nonzero))
 
 
-def adamw_step(tx, params, grads, state, key=None, stochastic: bool = True, *, random_bits=None):
+def adamw_step(tx, params, grads, state, key=None, stochastic: bool = True, *, random_bits=None,
+               clip_global_norm=None, clip_stats=None):
     """Fused ``tx.update`` + ``rollfast.apply_updates`` for ``tx = adamw(...)``
     (one HBM pass; no reference counterpart).  ``random_bits`` (testing):
     ``{leaf_index: (mu_bits, nu_bits, param_bits)}`` raw uint32 words that
-    replace the in-kernel bits of the bf16 moment storage and the param SR."""
+    replace the in-kernel bits of the bf16 moment storage and the param SR.
+    ``clip_global_norm`` / ``clip_stats``: fused global-norm clipping, as for
+    ``adamw8_step``."""
     from .adam8 import adamw8_step
 
     if not isinstance(tx.update, _Adamw8Update) or not isinstance(tx.update.engine, _AdamEngine):
         raise TypeError("adamw_step needs a transformation built by adamw(...)")
-    return adamw8_step(tx, params, grads, state, key=key, stochastic=stochastic, random_bits=random_bits)
+    return adamw8_step(tx, params, grads, state, key=key, stochastic=stochastic, random_bits=random_bits,
+                       clip_global_norm=clip_global_norm, clip_stats=clip_stats)
 
 
 __all__ = ("ScaleByAdamState", "adamw", "adamw_step", "scale_by_adam")

@@ -677,6 +677,8 @@ class _Engine:
         param_key=None,
         param_sr: bool = False,
         random_bits: Optional[dict] = None,
+        clip_global_norm: Optional[float] = None,
+        clip_stats=None,
     ):
         torch = _torch()
         cfg = self.cfg
@@ -756,6 +758,15 @@ class _Engine:
         if param_key is not None:
             pk = prng.as_key(param_key)
             hp.key_param[0], hp.key_param[1] = int(pk[0]), int(pk[1])
+        if clip_global_norm is not None:
+            if not (float(clip_global_norm) > 0.0) or not math.isfinite(float(clip_global_norm)):
+                raise ValueError("max_norm must be positive.")
+            hp.clip_max_norm = float(clip_global_norm)
+            if clip_stats is not None:
+                _require_device_tensor(clip_stats, "clip_stats")
+                if clip_stats.dtype != torch.float32 or clip_stats.numel() < 2 or not clip_stats.is_contiguous():
+                    raise ValueError("clip_stats must be a contiguous float32 device tensor of 2 elements")
+                hp.clip_out = clip_stats.data_ptr()
 
         if n_rows:
             with torch.cuda.device(device):
@@ -869,7 +880,8 @@ class _Adamw8Update:
                 count=np.asarray(safe_int32_increment(count), dtype=np.int32))
         return np.float32(-_as_f32(lr)) if not isinstance(lr, (int, float)) else np.float32(-lr), lr_state
 
-    def _step(self, updates, state, params, *, apply: bool, param_key=None, param_sr=False, random_bits=None):
+    def _step(self, updates, state, params, *, apply: bool, param_key=None, param_sr=False, random_bits=None,
+              clip_global_norm=None, clip_stats=None):
         adam_state = state[0]
         lr_state = state[-1]
         neg_lr, new_lr_state = self._lr(lr_state)
@@ -883,6 +895,7 @@ class _Adamw8Update:
             updates, adam_state, params, apply=apply, decay_mask=decay_mask,
             weight_decay=self.weight_decay if self.wd_nonzero else None, neg_lr=neg_lr,
             param_key=param_key, param_sr=param_sr, random_bits=random_bits,
+            clip_global_norm=clip_global_norm, clip_stats=clip_stats,
         )
         new_state = (new_adam,) + tuple(state[1:-1]) + (new_lr_state,)
         return out, new_state
@@ -942,7 +955,8 @@ def adamw8(
     return GradientTransformationExtraArgs(init_fn, update)
 
 
-def adamw8_step(tx, params, grads, state, key=None, stochastic: bool = True, *, random_bits=None):
+def adamw8_step(tx, params, grads, state, key=None, stochastic: bool = True, *, random_bits=None,
+                clip_global_norm: Optional[float] = None, clip_stats=None):
     """Fused ``tx.update`` + ``rollfast.apply_updates`` in one HBM pass (no
     reference counterpart: the reference runs them as two XLA programs).
 
@@ -954,6 +968,13 @@ def adamw8_step(tx, params, grads, state, key=None, stochastic: bool = True, *, 
     for ``tx = adamw8(...)``.  Params are updated in place and returned with
     the new state.  ``random_bits`` (testing): ``{leaf_index: (mu_bits,
     nu_bits, param_bits)}`` device uint32 arrays replacing in-kernel bits.
+
+    ``clip_global_norm``: the grads are first clipped by their global L2 norm
+    as rollfast's ``finetune.transforms.clip_by_global_norm(max_norm)`` does
+    (transforms.py:20-82), fused: a norm pre-pass reads the grads once and
+    the step scales them as it loads them (the grads are not modified).
+    ``clip_stats``: optional float32 device tensor of 2 elements that receives
+    (scale, norm).
     """
     if not isinstance(tx.update, _Adamw8Update):
         raise TypeError("adamw8_step needs a transformation built by adamw8(...)")
@@ -963,7 +984,8 @@ def adamw8_step(tx, params, grads, state, key=None, stochastic: bool = True, *, 
             "Pass stochastic=False for deterministic rounding."
         )
     _, new_state = tx.update._step(grads, state, params, apply=True, param_key=key, param_sr=bool(stochastic),
-                                   random_bits=random_bits)
+                                   random_bits=random_bits, clip_global_norm=clip_global_norm,
+                                   clip_stats=clip_stats)
     return params, new_state
 
 

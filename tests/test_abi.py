@@ -42,7 +42,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 def test_struct_sizes_match_header():
     assert ctypes.sizeof(_lib.Adam8Leaf) == 120
-    assert ctypes.sizeof(_lib.Adam8Hparams) == 80
+    assert ctypes.sizeof(_lib.Adam8Hparams) == 88
     assert ctypes.sizeof(_lib.ApplyLeaf) == 40
 
 

@@ -526,3 +526,50 @@ def test_bf16_moment_store_sr_is_the_sr_of_the_f32_moments():
     orc.adam8_leaf(hp_rne, np.zeros(n, np.float32), orc.F32, g, orc.F32, orc.MOM_BF16, mu16, None, nu16, None,
                    updates_out=np.empty(n, np.float32))
     np.testing.assert_array_equal(mu16, orc.f32_to_bf16_bits(mu32))
+
+
+# ----------------------------------------------- global-norm clipping -----
+def test_global_norm_clip_scale_closed_forms():
+    """finetune/transforms.py:57-82: a 3-4-12 tree has norm 13; scale =
+    max_norm / (13 + 1e-6) below 1, exactly 1 above; NaN and Inf propagate
+    as jnp.minimum and sqrt do."""
+    grads = [np.array([3.0], np.float32), np.array([4.0, 0.0], np.float32), np.array([12.0], np.float32)]
+    scale, norm = orc.global_norm_clip_scale(grads, 1.0)
+    assert norm == np.float32(13.0)
+    assert scale == np.float32(np.float32(1.0) / np.float32(np.float32(13.0) + np.float32(1e-6)))
+    assert orc.global_norm_clip_scale(grads, 100.0)[0] == np.float32(1.0)
+    nan_scale, nan_norm = orc.global_norm_clip_scale([np.array([np.nan], np.float32)], 1.0)
+    assert np.isnan(nan_scale) and np.isnan(nan_norm)
+    inf_scale, inf_norm = orc.global_norm_clip_scale([np.array([np.inf], np.float32)], 1.0)
+    assert inf_scale == 0.0 and np.isinf(inf_norm)
+
+
+def test_global_norm_matches_float64_and_leaf_order_f32_sum():
+    rng = np.random.default_rng(12)
+    grads = [rng.standard_normal(n).astype(np.float32) * np.float32(s)
+             for n, s in ((100000, 1e-3), (7, 5.0), (4096, 1e-2), (33333, 0.3))]
+    scale, norm = orc.global_norm_clip_scale(grads, 1.0)
+    exact = np.sqrt(sum(np.sum(g.astype(np.float64) ** 2) for g in grads))
+    assert abs(float(norm) - exact) <= 4 * 2.0 ** -24 * exact
+    # the leaf sums are added in f32 in leaf order
+    tot = np.float32(0.0)
+    for g in grads:
+        tot = np.float32(tot + np.float32(np.sum(g.astype(np.float64) ** 2)))
+    assert norm == np.sqrt(tot, dtype=np.float32)
+    assert scale < 1.0
+
+
+def test_clip_leaf_bf16_rounds_once_with_bf16_scale():
+    """bf16 leaves: leaf * scale.astype(bf16) -- the scale is first rounded to
+    bf16, the product of two bf16 values is exact in f32 and rounded once."""
+    rng = np.random.default_rng(13)
+    g = orc.f32_to_bf16_bits(rng.standard_normal(10000).astype(np.float32))
+    scale = np.float32(0.0123456)
+    s16 = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(np.array([scale], np.float32)))[0]
+    assert s16 != scale
+    got = orc.clip_leaf(g, orc.BF16, scale)
+    exact = orc.bf16_bits_to_f32(g).astype(np.float64) * np.float64(s16)
+    assert np.all(exact.astype(np.float32).astype(np.float64) == exact)  # the product is exact in f32
+    np.testing.assert_array_equal(got, orc.f32_to_bf16_bits(exact.astype(np.float32)))
+    f = rng.standard_normal(100).astype(np.float32)
+    np.testing.assert_array_equal(orc.clip_leaf(f, orc.F32, scale), f * scale)
