@@ -17,6 +17,8 @@ Other workloads (one JSON line each, same fields):
                    fallback moments), param stochastic rounding on.
   ragged           2256 leaves, most below min_size (fallback moments),
                    Student-t(3) grads with per-leaf scales, 10 % zero blocks.
+  llama7b_clip     the default step with fused global-norm clipping (max norm
+                   1.0): a norm pre-pass reads the grads once more (+2 B/param).
   llama7b_optax    update-only (Optax) mode over the Llama tree: f32 updates
                    written, params read for weight decay.
   llama7b_adamw_f32   full-precision AdamW (adamw, f32 moments) over the Llama
@@ -256,7 +258,7 @@ class Workload:
         self.step, self.config, self.cpu, self.metric = step, config, cpu, metric
 
 
-def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None):
+def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None, clip=None):
     import numpy as np
     import torch
 
@@ -305,7 +307,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
             _, holder["state"] = tx.update(g, holder["state"], holder["params"])
         else:
             holder["params"], holder["state"] = rf.adamw8_step(tx, holder["params"], g, holder["state"], key=key,
-                                                               stochastic=param_sr)
+                                                               stochastic=param_sr, clip_global_norm=clip)
 
     n_quant = sum(1 for _, s in shapes if _numel(s) >= MIN_SIZE) if adam_mu is None else 0
     config = {
@@ -322,9 +324,11 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         "param_rounding": "stochastic" if param_sr else "nearest-even",
         "direction": "ieee" if args.exact else "hw rcp/sqrt",
         "mode": "optax update-only (f32 updates)" if optax else "fused step (params written)",
-        "launches_per_step": 1,
+        "launches_per_step": 1 if clip is None else 4,
         "grad_pool": len(pool),
     }
+    if clip is not None:
+        config["clip_global_norm"] = clip
     if shapes_fn is llama7b_shapes:
         cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr)  # noqa: E731
     else:
@@ -333,7 +337,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
                                    sample_name=f"the first {len(sub)} leaves", param_sr=param_sr)
     metric = METRIC if workload == "llama7b_bf16_adamw8" else f"adam8 params/sec + achieved HBM GB/s, {workload}, 1 GPU"
     if adam_mu is None:
-        nbytes = step_bytes(shapes, apply=not optax)
+        nbytes = step_bytes(shapes, apply=not optax) + (n_params * 2 if clip is not None else 0)
     else:
         mb = 4 if adam_mu == "f32" else 2
         nbytes = n_params * (2 + 2 + 2 + 2 * 2 * mb)  # p r+w, g r, two moments r+w
@@ -429,6 +433,8 @@ WORKLOADS = {
     "gpt2": lambda a: _tree_workload(a, gpt2_small_shapes, "gpt2_small_bf16_adamw8", param_sr=True),
     "ragged": lambda a: _tree_workload(a, ragged_shapes, "ragged_2256_leaves_bf16_adamw8", param_sr=a.param_sr,
                                        grads="student_t"),
+    "llama7b_clip": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_clip_global_norm",
+                                             param_sr=False, clip=1.0),
     "llama7b_optax": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_optax_update",
                                               param_sr=False, optax=True),
     "llama7b_adamw_f32": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw_f32_moments",
