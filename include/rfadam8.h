@@ -28,6 +28,9 @@
 extern "C" {
 #endif
 
+/* Exported entry points (the library is built with hidden visibility). */
+#define RF_API __attribute__((visibility("default")))
+
 typedef int32_t rf_status;
 #define RF_OK 0
 #define RF_ERR_INVALID 1     /* bad argument: shape, dtype, size, null pointer */
@@ -133,31 +136,31 @@ typedef struct rf_adam8_plan rf_adam8_plan;
  * fused, rollfast.apply_updates (utils.py:648-708).  Synchronises the
  * current device once (table upload).
  */
-rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply,
+RF_API rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply,
                                rf_adam8_plan** out_plan);
 
 /* Enqueue one step of the plan on `stream` (one multi-tensor launch) over
  * the pointers given at creation. */
-rf_status rf_adam8_plan_run(const rf_adam8_plan* plan, const rf_adam8_hparams* hp, void* stream);
+RF_API rf_status rf_adam8_plan_run(const rf_adam8_plan* plan, const rf_adam8_hparams* hp, void* stream);
 
 /* Enqueue one step over new buffers of the same structure (sizes, dtypes,
  * moment kinds, block sizes, key indices and flags must equal the plan's;
  * only pointers may change -- e.g. fresh gradient buffers each step).  The
  * pointer table travels through a ring of pinned staging slots guarded by
  * events: no allocation and no device synchronisation in steady state. */
-rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* leaves, int32_t n_leaves,
+RF_API rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* leaves, int32_t n_leaves,
                                    const rf_adam8_hparams* hp, void* stream);
 
 /* Number of kernel launches, leaves and 2048-element work units of a plan. */
-rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64_t* leaves,
+RF_API rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64_t* leaves,
                              int64_t* units);
 
 /* Free a plan (waits for the device to be idle with respect to its tables). */
-rf_status rf_adam8_plan_destroy(rf_adam8_plan* plan);
+RF_API rf_status rf_adam8_plan_destroy(rf_adam8_plan* plan);
 
 /* One-shot convenience: create a plan, run it on `stream`, wait for the
  * stream, destroy the plan.  Allocates and synchronises: use plans in loops. */
-rf_status rf_adam8_step(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply,
+RF_API rf_status rf_adam8_step(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply,
                         const rf_adam8_hparams* hp, void* stream);
 
 /*
@@ -167,18 +170,18 @@ rf_status rf_adam8_step(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t a
  * stochastic rounding with raw bits `bits` [nblocks*block_size] when
  * non-NULL, else in-kernel Threefry-2x32 bits of key (key0, key1).
  */
-rf_status rf_blockwise_quantize(int32_t quantizer, const float* x, int64_t size,
+RF_API rf_status rf_blockwise_quantize(int32_t quantizer, const float* x, int64_t size,
                                 int32_t block_size, int32_t sr, uint32_t key0, uint32_t key1,
                                 const uint32_t* bits, void* values, float* scales, void* stream);
 
 /* adam8.py:190-204 dequantize_blocks: out [size] of out_dtype (RF_F32|RF_BF16). */
-rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const float* scales,
+RF_API rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const float* scales,
                                   int64_t size, int32_t block_size, int32_t out_dtype, void* out,
                                   void* stream);
 
 /* utils.py:342-371 _stochastic_round_bf16: out [size] bf16 bit patterns.  Uses
  * `bits` [size] when non-NULL, else in-kernel Threefry-2x32 bits of key. */
-rf_status rf_sr_bf16(const float* x, int64_t size, uint32_t key0, uint32_t key1,
+RF_API rf_status rf_sr_bf16(const float* x, int64_t size, uint32_t key0, uint32_t key1,
                      const uint32_t* bits, uint16_t* out, void* stream);
 
 /* One leaf of rollfast.apply_updates (utils.py:648-708). */
@@ -193,22 +196,22 @@ typedef struct rf_apply_leaf {
 
 /* utils.py:648-708 apply_updates over n leaves: bf16 params take
  * f32(p) + u then SR (stochastic != 0) or RNE; f32 params take p + u. */
-rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic,
+RF_API rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic,
                            uint32_t key0, uint32_t key1, void* stream);
 
 /* Host-side: the 256 f32 values of a dynamic codebook (adam8.py:461-503). */
-rf_status rf_codebook(int32_t quantizer, float* out256);
+RF_API rf_status rf_codebook(int32_t quantizer, float* out256);
 
 /* Host-side: codes that the kernels' table lookup assigns to the normalised
  * values whose f32 bit patterns are first_bits .. first_bits+count-1
  * (diagnostics of the lookup tables; `out` is host memory). */
-rf_status rf_host_table_codes(int32_t quantizer, uint32_t first_bits, int64_t count, uint8_t* out);
+RF_API rf_status rf_host_table_codes(int32_t quantizer, uint32_t first_bits, int64_t count, uint8_t* out);
 
 /* Library version string. */
-const char* rf_version(void);
+RF_API const char* rf_version(void);
 
 /* Thread-local message of the last failed call ("" if none). */
-const char* rf_last_error(void);
+RF_API const char* rf_last_error(void);
 
 #ifdef __cplusplus
 }

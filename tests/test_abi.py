@@ -22,7 +22,7 @@ HEADER = os.path.join(ROOT, "include", "rfadam8.h")
 def _declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    names = re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(rf_[a-z_0-9]+)\s*\(", text, flags=re.M)
+    names = re.findall(r"^\s*(?:RF_API\s+)?(?:const\s+)?[a-z_0-9]+\s*\*?\s*(rf_[a-z_0-9]+)\s*\(", text, flags=re.M)
     return sorted(set(names))
 
 
@@ -38,6 +38,20 @@ def test_library_loads_and_exports_every_declared_symbol():
         assert hasattr(L, name), name
     # nothing else with the rf_ prefix is part of the ABI contract
     assert os.path.basename(L._name) == "librfadam8.so"
+
+
+def test_dynamic_symbols_are_exactly_the_declared_entry_points():
+    """The library exports the C ABI and nothing else (hidden visibility)."""
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    path = _lib.lib()._name
+    out = subprocess.run([nm, "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.split()[1:2] == ["T"]}
+    assert exported == set(_declared_functions()), exported ^ set(_declared_functions())
 
 
 def test_struct_sizes_match_header():
