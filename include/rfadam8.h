@@ -199,6 +199,23 @@ typedef struct rf_apply_leaf {
 RF_API rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic,
                            uint32_t key0, uint32_t key1, void* stream);
 
+/* One leaf of rf_clip_by_global_norm. */
+typedef struct rf_clip_leaf {
+    const void* grad;   /* [size] dtype */
+    void* out;          /* [size] dtype: grad * scale (may equal grad: in place) */
+    int64_t size;
+    int32_t dtype;      /* RF_F32 | RF_BF16 */
+    int32_t reserved;   /* 0 */
+} rf_clip_leaf;
+
+/* finetune/transforms.py:20-82 clip_by_global_norm as a transform: the global
+ * L2 norm of all leaves, scale = min(1, max_norm / (norm + 1e-6)), out = grad *
+ * scale in the leaf dtype (bf16 leaves: times bf16(scale), one rounding).
+ * `stats` (device f32[2] or NULL) receives (scale, norm).  Enqueues on
+ * `stream`; its scratch comes from hipMallocAsync on that stream. */
+RF_API rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, float max_norm,
+                                        float* stats, void* stream);
+
 /* Host-side: the 256 f32 values of a dynamic codebook (adam8.py:461-503). */
 RF_API rf_status rf_codebook(int32_t quantizer, float* out256);
 

@@ -33,6 +33,7 @@ from .optim.adam8 import (
     tree_state_nbytes,
 )
 from .optim.adam import ScaleByAdamState, adamw, adamw_step, scale_by_adam
+from .transforms import GlobalNormClipState, clip_by_global_norm
 from .utils import apply_updates, apply_updates_prefix
 
 __version__ = "0.1.0"
@@ -42,6 +43,7 @@ __all__ = (
     "DYNAMIC_UNSIGNED_CODEBOOK_ID",
     "SYMMETRIC_INT8_CODEBOOK_ID",
     "EmptyState",
+    "GlobalNormClipState",
     "GradientTransformation",
     "GradientTransformationExtraArgs",
     "MaskedNode",
@@ -56,6 +58,7 @@ __all__ = (
     "adamw_step",
     "apply_updates",
     "apply_updates_prefix",
+    "clip_by_global_norm",
     "dequantize_blocks",
     "estimate_quantized_moment_bytes",
     "prng",

@@ -79,6 +79,16 @@ class Adam8Hparams(ctypes.Structure):
     ]
 
 
+class ClipLeaf(ctypes.Structure):
+    _fields_ = [
+        ("grad", _p),
+        ("out", _p),
+        ("size", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
 class ApplyLeaf(ctypes.Structure):
     _fields_ = [
         ("param", _p),
@@ -93,6 +103,7 @@ class ApplyLeaf(ctypes.Structure):
 assert ctypes.sizeof(Adam8Leaf) == 120
 assert ctypes.sizeof(Adam8Hparams) == 88
 assert ctypes.sizeof(ApplyLeaf) == 40
+assert ctypes.sizeof(ClipLeaf) == 32
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTS = (
@@ -106,6 +117,7 @@ EXPORTS = (
     "rf_blockwise_dequantize",
     "rf_sr_bf16",
     "rf_apply_updates",
+    "rf_clip_by_global_norm",
     "rf_codebook",
     "rf_host_table_codes",
     "rf_version",

@@ -409,6 +409,48 @@ __global__ void k_gnorm_finish(const float* __restrict__ leafsum, int32_t nseg, 
     }
 }
 
+// Standalone clip_by_global_norm: out = grad * scale per leaf (blockIdx.y =
+// leaf), with the leaf-dtype semantics of the fused path.
+__global__ __launch_bounds__(WG) void k_clip_scale(const rf_clip_leaf* __restrict__ leaves,
+                                                   const float* __restrict__ clip)
+{
+    const rf_clip_leaf L = leaves[blockIdx.y];
+    const float cs = clip[0];
+    const float cs16 = round_to_bf16(cs);
+    const int64_t tid = (int64_t)blockIdx.x * WG + threadIdx.x;
+    const int64_t nthreads = (int64_t)gridDim.x * WG;
+    const bool bf16 = L.dtype == RF_BF16;
+    const bool vec = ((uintptr_t)L.grad % 16 == 0) && ((uintptr_t)L.out % 16 == 0);
+    const int64_t ngroups = vec ? L.size / 8 : 0;
+    for (int64_t gi = tid; gi < ngroups; gi += nthreads) {
+        const int64_t e0 = gi * 8;
+        float x[8];
+        if (bf16) {
+            load8<uint16_t>(L.grad, e0, x);
+            uint32_t hb[8];
+#pragma unroll
+            for (int t = 0; t < 8; t += 2) {
+                const uint32_t w2 = pack_bf16x2_rne(x[t] * cs16, x[t + 1] * cs16);
+                hb[t] = w2 & 0xFFFFu;
+                hb[t + 1] = w2 >> 16;
+            }
+            store8_bf16(L.out, e0, hb);
+        } else {
+            load8<float>(L.grad, e0, x);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) x[t] = x[t] * cs;
+            store8_f32(L.out, e0, x);
+        }
+    }
+    for (int64_t e = ngroups * 8 + tid; e < L.size; e += nthreads) {
+        if (bf16) {
+            ((uint16_t*)L.out)[e] = (uint16_t)f32_to_bf16_rne(bf16_bits_to_f32(((const uint16_t*)L.grad)[e]) * cs16);
+        } else {
+            ((float*)L.out)[e] = ((const float*)L.grad)[e] * cs;
+        }
+    }
+}
+
 // =================================================================== host ==
 namespace {
 
@@ -1199,6 +1241,96 @@ rf_status rf_sr_bf16(const float* x, int64_t size, uint32_t key0, uint32_t key1,
     hipLaunchKernelGGL(k_sr_bf16, dim3(grid), dim3(WG), 0, (hipStream_t)stream, x, size, key0, key1, bits, out,
                        vec_ok);
     HIP_TRY(hipGetLastError());
+    return RF_OK;
+}
+
+rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, float max_norm, float* stats,
+                                 void* stream)
+{
+    if (n_leaves < 0 || (n_leaves > 0 && !leaves)) return fail(RF_ERR_INVALID, "bad leaf table");
+    if (!(max_norm > 0.0f) || std::isinf(max_norm)) return fail(RF_ERR_INVALID, "max_norm must be positive.");
+    if (n_leaves > 65535) return fail(RF_ERR_UNSUPPORTED, "more than 65535 leaves in one clip call");
+    // The norm pre-pass kernels read rf_adam8_leaf records: only grad, size
+    // and grad_dtype are used.
+    std::vector<rf_adam8_leaf> gl((size_t)n_leaves);
+    std::vector<Seg> nsegs;
+    int64_t nunits = 0, maxsize = 0;
+    for (int32_t i = 0; i < n_leaves; ++i) {
+        const rf_clip_leaf& L = leaves[i];
+        if (L.size < 0) return fail(RF_ERR_INVALID, "negative size");
+        if (L.dtype != RF_F32 && L.dtype != RF_BF16) return fail(RF_ERR_UNSUPPORTED, "dtype must be f32 or bf16");
+        if (L.size > 0 && (!L.grad || !L.out)) return fail(RF_ERR_INVALID, "null buffer");
+        gl[i] = rf_adam8_leaf{};
+        gl[i].grad = L.grad;
+        gl[i].size = L.size;
+        gl[i].grad_dtype = L.dtype;
+        maxsize = std::max(maxsize, L.size);
+        if (L.size == 0) continue;
+        Seg sg{};
+        sg.unit_start = nunits;
+        sg.leaf = i;
+        nsegs.push_back(sg);
+        nunits += (L.size + NORM_UNIT - 1) / NORM_UNIT;
+    }
+    const int32_t nseg = (int32_t)nsegs.size();
+    Seg sentinel{};
+    sentinel.unit_start = nunits;
+    sentinel.leaf = -1;
+    sentinel.kind = -1;
+    nsegs.push_back(sentinel);
+    DevState* ds = nullptr;
+    rf_status st = device_state(&ds);
+    if (st != RF_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    // One scratch allocation: leaf tables, segments, partials, leaf sums, (scale, norm).
+    const size_t o_gl = 0;
+    const size_t o_cl = o_gl + sizeof(rf_adam8_leaf) * (size_t)std::max(n_leaves, 1);
+    const size_t o_sg = (o_cl + sizeof(rf_clip_leaf) * (size_t)std::max(n_leaves, 1) + 15) & ~(size_t)15;
+    const size_t o_pt = (o_sg + sizeof(Seg) * nsegs.size() + 15) & ~(size_t)15;
+    const size_t o_ls = o_pt + sizeof(double) * (size_t)std::max<int64_t>(nunits, 1);
+    const size_t o_cp = (o_ls + sizeof(float) * (size_t)std::max(nseg, 1) + 15) & ~(size_t)15;
+    const size_t total = o_cp + 2 * sizeof(float);
+    uint8_t* scratch = nullptr;
+    HIP_TRY(hipMallocAsync((void**)&scratch, total, s));
+    std::vector<uint8_t> host(o_pt);
+    if (n_leaves > 0) {
+        std::memcpy(host.data() + o_gl, gl.data(), sizeof(rf_adam8_leaf) * (size_t)n_leaves);
+        std::memcpy(host.data() + o_cl, leaves, sizeof(rf_clip_leaf) * (size_t)n_leaves);
+    }
+    std::memcpy(host.data() + o_sg, nsegs.data(), sizeof(Seg) * nsegs.size());
+    hipError_t e = hipMemcpyAsync(scratch, host.data(), o_pt, hipMemcpyHostToDevice, s);
+    // hipMemcpyAsync from pageable memory returns once the source is consumed.
+    const rf_adam8_leaf* d_gl = (const rf_adam8_leaf*)(scratch + o_gl);
+    const rf_clip_leaf* d_cl = (const rf_clip_leaf*)(scratch + o_cl);
+    const Seg* d_sg = (const Seg*)(scratch + o_sg);
+    double* d_pt = (double*)(scratch + o_pt);
+    float* d_ls = (float*)(scratch + o_ls);
+    float* d_cp = (float*)(scratch + o_cp);
+    if (e == hipSuccess && nunits > 0) {
+        const int64_t pw = std::max<int64_t>(1, std::min<int64_t>((nunits + WAVES_PER_WG - 1) / WAVES_PER_WG,
+                                                                  (int64_t)ds->num_cus * 8));
+        hipLaunchKernelGGL(k_gnorm_partial, dim3((unsigned)pw), dim3(WG), 0, s, d_gl, d_sg, nunits, d_pt);
+        e = hipGetLastError();
+        if (e == hipSuccess) {
+            const int64_t lw = std::max<int64_t>(1, std::min<int64_t>((nseg + WAVES_PER_WG - 1) / WAVES_PER_WG,
+                                                                      (int64_t)ds->num_cus * 8));
+            hipLaunchKernelGGL(k_gnorm_leaf, dim3((unsigned)lw), dim3(WG), 0, s, d_sg, nseg, d_pt, d_ls);
+            e = hipGetLastError();
+        }
+    }
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(k_gnorm_finish, dim3(1), dim3(WAVE), 0, s, d_ls, nseg, max_norm, d_cp, stats);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess && maxsize > 0) {
+        const int gx = (int)std::max<int64_t>(1, std::min<int64_t>((maxsize / 8 + WG - 1) / WG,
+                                                                   (int64_t)ds->num_cus * 4));
+        hipLaunchKernelGGL(k_clip_scale, dim3(gx, n_leaves), dim3(WG), 0, s, d_cl, d_cp);
+        e = hipGetLastError();
+    }
+    hipError_t ef = hipFreeAsync(scratch, s);
+    if (e != hipSuccess) return fail(RF_ERR_HIP, std::string("rf_clip_by_global_norm: ") + hipGetErrorString(e));
+    if (ef != hipSuccess) return fail(RF_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(ef));
     return RF_OK;
 }
 

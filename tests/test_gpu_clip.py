@@ -198,3 +198,57 @@ def test_clip_argument_errors():
     with pytest.raises(ValueError):
         rf.adamw8_step(tx, params, g, state, stochastic=False, clip_global_norm=1.0,
                        clip_stats=torch.empty(1, device="cuda"))
+
+
+def test_clip_transform_matches_oracle_and_passes_none():
+    """rollfast_amd.clip_by_global_norm (transforms.py:20-82): every leaf is
+    leaf * scale in its dtype; None leaves pass through; the count advances."""
+    import torch
+
+    import rollfast_amd as rf
+
+    _, _, hg, dg = _trees(12, 0.05)
+    tree = dict(dg)
+    tree["none"] = None
+    tx = rf.clip_by_global_norm(1.0)
+    state = tx.init(tree)
+    stats = torch.empty(2, dtype=torch.float32, device="cuda")
+    out, state = tx.update(tree, state, None, stats=stats)
+    torch.cuda.synchronize()
+    scale, norm = orc.global_norm_clip_scale([_f32_values(g, gd) for g, (_s, _p, gd) in zip(hg, SPEC)], 1.0)
+    got = stats.cpu().numpy()
+    assert got[0] == scale and got[1] == norm and scale < 1.0
+    for i, (shape, _pd, gd) in enumerate(SPEC):
+        want = orc.clip_leaf(hg[i], orc.BF16 if gd == "bf16" else orc.F32, scale)
+        o = out[f"l{i}"]
+        assert tuple(o.shape) == shape
+        np.testing.assert_array_equal(to_host(o).view(np.uint16 if gd == "bf16" else np.uint32),
+                                      want.view(np.uint16 if gd == "bf16" else np.uint32))
+        np.testing.assert_array_equal(to_host(dg[f"l{i}"]), hg[i])  # inputs untouched
+    assert out["none"] is None
+    assert int(state.count) == 1 and isinstance(state, rf.GlobalNormClipState)
+
+
+def test_clip_transform_then_update_equals_fused_clip():
+    """clip -> tx.update -> apply_updates (the reference's chain) gives the
+    same bits as the fused adamw8_step(..., clip_global_norm=...)."""
+    import torch
+
+    import rollfast_amd as rf
+
+    _, pa, _, g = _trees(13, 0.05)
+    _, pb, _, _ = _trees(13, 0.05)
+    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=True)
+    clip = rf.clip_by_global_norm(1.0)
+    sa, sb, cs = tx.init(pa), tx.init(pb), clip.init(pb)
+    for _ in range(2):
+        pa, sa = rf.adamw8_step(tx, pa, g, sa, stochastic=False, clip_global_norm=1.0)
+        gc, cs = clip.update(g, cs)
+        u, sb = tx.update(gc, sb, pb)
+        pb = rf.apply_updates(pb, u, stochastic=False)
+        torch.cuda.synchronize()
+        for k in pa:
+            np.testing.assert_array_equal(to_host(pa[k]), to_host(pb[k]))
+            ma, mb = sa[0].mu[k], sb[0].mu[k]
+            if isinstance(ma, rf.QuantizedBlocks):
+                np.testing.assert_array_equal(to_host(ma.values), to_host(mb.values))

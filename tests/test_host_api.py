@@ -193,3 +193,12 @@ def test_tree_ordered_dict_keeps_insertion_order():
     assert _tree.flatten_up_to(td, OrderedDict([("z", "x"), ("a", "y")])) == ["x", "y"]
     with pytest.raises(ValueError):
         _tree.flatten_up_to(td, OrderedDict([("a", "y"), ("z", "x")]))
+
+
+def test_clip_by_global_norm_construction():
+    with pytest.raises(ValueError, match="max_norm must be positive"):
+        rf.clip_by_global_norm(0.0)
+    st = rf.clip_by_global_norm(1.0).init({"w": torch.zeros(2)})
+    assert int(st.count) == 0
+    with pytest.raises(ValueError, match="ROCm device"):
+        rf.clip_by_global_norm(1.0).update({"w": torch.zeros(2)}, st)
