@@ -19,6 +19,9 @@ Other workloads (one JSON line each, same fields):
                    Student-t(3) grads with per-leaf scales, 10 % zero blocks.
   llama7b_clip     the default step with fused global-norm clipping (max norm
                    1.0): a norm pre-pass reads the grads once more (+2 B/param).
+  llama7b_finetune the fine-tune builders' gradient policy around the step:
+                   clipping at 1.0 and apply_if_finite (skip non-finite
+                   steps); the finite flag is read back once per step.
   llama7b_optax    update-only (Optax) mode over the Llama tree: f32 updates
                    written, params read for weight decay.
   llama7b_adamw_f32   full-precision AdamW (adamw, f32 moments) over the Llama
@@ -258,7 +261,8 @@ class Workload:
         self.step, self.config, self.cpu, self.metric = step, config, cpu, metric
 
 
-def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None, clip=None):
+def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None, clip=None,
+                   guard=False):
     import numpy as np
     import torch
 
@@ -276,6 +280,8 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     else:
         tx = rf.adamw(learning_rate=1e-3, weight_decay=0.01, exact=args.exact,
                       mu_dtype=torch.bfloat16 if adam_mu == "bf16" else None)
+    if guard:
+        tx = rf.apply_if_finite(tx, 1)
     state = tx.init(params)
     pool = []
     rng = np.random.default_rng(0)
@@ -329,6 +335,9 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     }
     if clip is not None:
         config["clip_global_norm"] = clip
+    if guard:
+        config["nonfinite"] = "skip (apply_if_finite, max_consecutive_errors=1; one int32 read back per step)"
+        config["launches_per_step"] = 4
     if shapes_fn is llama7b_shapes:
         cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr)  # noqa: E731
     else:
@@ -337,7 +346,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
                                    sample_name=f"the first {len(sub)} leaves", param_sr=param_sr)
     metric = METRIC if workload == "llama7b_bf16_adamw8" else f"adam8 params/sec + achieved HBM GB/s, {workload}, 1 GPU"
     if adam_mu is None:
-        nbytes = step_bytes(shapes, apply=not optax) + (n_params * 2 if clip is not None else 0)
+        nbytes = step_bytes(shapes, apply=not optax) + (n_params * 2 if (clip is not None or guard) else 0)
     else:
         mb = 4 if adam_mu == "f32" else 2
         nbytes = n_params * (2 + 2 + 2 + 2 * 2 * mb)  # p r+w, g r, two moments r+w
@@ -435,6 +444,8 @@ WORKLOADS = {
                                        grads="student_t"),
     "llama7b_clip": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_clip_global_norm",
                                              param_sr=False, clip=1.0),
+    "llama7b_finetune": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_clip_skip_nonfinite",
+                                                 param_sr=False, clip=1.0, guard=True),
     "llama7b_optax": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_optax_update",
                                               param_sr=False, optax=True),
     "llama7b_adamw_f32": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw_f32_moments",

@@ -62,6 +62,13 @@ typedef int32_t rf_status;
                             default uses hardware rcp/sqrt (params within 1 bf16 ulp) */
 #define RF_FED_BITS 256u /* SR consumes the leaves' *_bits arrays instead of in-kernel
                             Threefry-2x32 */
+#define RF_SKIP_NONFINITE 512u /* optax.apply_if_finite reject branch (the wrapper of the
+                            fine-tune chain, finetune/builders.py:1605-1609): when any
+                            grad of the run is Inf or NaN, the launch leaves the moments
+                            untouched and applies a zero update instead (fused step:
+                            params become f32(p) + 0 in their dtype, so -0 turns +0;
+                            update-only mode: zero updates).  The test reads the grads
+                            before clipping. */
 
 /* rf_adam8_leaf.flags */
 #define RF_LEAF_DECAY 1u    /* add_decayed_weights applies to this leaf (mask True) */
@@ -123,6 +130,12 @@ typedef struct rf_adam8_hparams {
                                 clip_by_global_norm, fused); 0: no clipping */
     float* clip_out;         /* optional device f32[2] receiving (scale, norm) of the clipping,
                                 or NULL */
+    int32_t* finite_out;     /* optional device int32 receiving 1 when every grad of the run
+                                is finite, else 0 (optax.apply_if_finite's isfinite), or NULL */
+    int32_t* finite_host;    /* optional pinned host int32 (hipHostMalloc) receiving the same
+                                flag by a copy enqueued right after the pre-pass, before the
+                                step; rf_adam8_plan_wait_prepass waits for it, so a host that
+                                needs the flag does not wait for the whole step.  NULL: none */
 } rf_adam8_hparams;
 
 typedef struct rf_adam8_plan rf_adam8_plan;
@@ -150,6 +163,12 @@ RF_API rf_status rf_adam8_plan_run(const rf_adam8_plan* plan, const rf_adam8_hpa
  * events: no allocation and no device synchronisation in steady state. */
 RF_API rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* leaves, int32_t n_leaves,
                                    const rf_adam8_hparams* hp, void* stream);
+
+/* Wait until the pre-pass (global norm and finite flag) of the plan's latest
+ * run with a finite_host has finished and the flag is in finite_host.  The
+ * step itself may still be running.  Returns at once when no run asked for it
+ * (an empty run never writes finite_host). */
+RF_API rf_status rf_adam8_plan_wait_prepass(const rf_adam8_plan* plan);
 
 /* Number of kernel launches, leaves and 2048-element work units of a plan. */
 RF_API rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64_t* leaves,

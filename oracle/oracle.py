@@ -286,5 +286,39 @@ def clip_leaf(g: np.ndarray, dtype: int, scale) -> np.ndarray:
     if dtype == F32:
         return (np.asarray(g, np.float32) * np.float32(scale)).astype(np.float32)
     s16 = bf16_bits_to_f32(f32_to_bf16_bits(np.array([scale], np.float32)))[0]
-    prod = bf16_bits_to_f32(np.asarray(g, np.uint16)) * np.float32(s16)  # exact: 8 x 8 significant bits
+    with np.errstate(invalid="ignore", over="ignore"):  # Inf * 0 -> NaN, as on the device
+        prod = bf16_bits_to_f32(np.asarray(g, np.uint16)) * np.float32(s16)  # exact: 8 x 8 significant bits
     return f32_to_bf16_bits(prod)
+
+
+# ------------------------------------------------ optax.apply_if_finite --
+def all_finite(grads, dtypes) -> bool:
+    """optax.apply_if_finite's ``isfinite``: every element of every incoming
+    grad leaf is finite (``dtypes``: F32 arrays or BF16 bit patterns)."""
+    for g, dt in zip(grads, dtypes):
+        vals = bf16_bits_to_f32(np.asarray(g, np.uint16)) if dt == BF16 else np.asarray(g, np.float32)
+        if not np.isfinite(vals).all():
+            return False
+    return True
+
+
+def apply_if_finite_decision(notfinite_count: int, total_notfinite: int, isfinite: bool,
+                             max_consecutive_errors: int):
+    """optax.apply_if_finite's update (the guard of finetune/builders.py:
+    1605-1609): notfinite_count = 0 if finite else the int32-saturating
+    increment; the inner update applies when ``isfinite or notfinite_count >
+    max_consecutive_errors`` (else zero updates and the old inner state);
+    total_notfinite counts every non-finite step.  Returns (apply_inner,
+    notfinite_count, total_notfinite)."""
+    def inc(c):
+        return c + 1 if c < 2**31 - 1 else c
+
+    count = 0 if isfinite else inc(int(notfinite_count))
+    total = int(total_notfinite) if isfinite else inc(int(total_notfinite))
+    return bool(isfinite or count > max_consecutive_errors), count, total
+
+
+def reject_params(param: np.ndarray, pdtype: int) -> None:
+    """The rejected step's params: apply_updates(params, zeros_like(grads))
+    (utils.py:694-700), in place; only -0 changes (to +0)."""
+    apply_updates(param, pdtype, np.zeros(param.size, np.float32))

@@ -10,6 +10,7 @@ torch tensors on a ROCm device in place of jax arrays.  ``adamw8_step`` /
 
 from . import prng
 from ._base import (
+    ApplyIfFiniteState,
     EmptyState,
     GradientTransformation,
     GradientTransformationExtraArgs,
@@ -33,7 +34,7 @@ from .optim.adam8 import (
     tree_state_nbytes,
 )
 from .optim.adam import ScaleByAdamState, adamw, adamw_step, scale_by_adam
-from .transforms import GlobalNormClipState, clip_by_global_norm
+from .transforms import GlobalNormClipState, apply_if_finite, clip_by_global_norm
 from .utils import apply_updates, apply_updates_prefix
 
 __version__ = "0.1.0"
@@ -42,6 +43,7 @@ __all__ = (
     "DYNAMIC_SIGNED_CODEBOOK_ID",
     "DYNAMIC_UNSIGNED_CODEBOOK_ID",
     "SYMMETRIC_INT8_CODEBOOK_ID",
+    "ApplyIfFiniteState",
     "EmptyState",
     "GlobalNormClipState",
     "GradientTransformation",
@@ -56,6 +58,7 @@ __all__ = (
     "adamw8",
     "adamw8_step",
     "adamw_step",
+    "apply_if_finite",
     "apply_updates",
     "apply_updates_prefix",
     "clip_by_global_norm",

@@ -38,6 +38,18 @@ class MaskedState(NamedTuple):
     inner_state: Any
 
 
+class ApplyIfFiniteState(NamedTuple):
+    """State of optax.apply_if_finite (the non-finite guard of the fine-tune
+    builders, finetune/builders.py:1605-1609): consecutive and total counts of
+    steps whose grads held an Inf or NaN, whether the last one was finite, and
+    the wrapped transformation's state."""
+
+    notfinite_count: Any
+    last_finite: Any
+    total_notfinite: Any
+    inner_state: Any
+
+
 class GradientTransformation(NamedTuple):
     init: Callable
     update: Callable

@@ -26,6 +26,7 @@ RF_MOMENT_SR = 16
 RF_PARAM_SR = 32
 RF_EXACT = 128
 RF_FED_BITS = 256
+RF_SKIP_NONFINITE = 512
 RF_LEAF_DECAY = 1
 RF_LEAF_STORE_SR = 2
 
@@ -76,6 +77,8 @@ class Adam8Hparams(ctypes.Structure):
         ("nesterov_one_minus_b1", ctypes.c_float),
         ("clip_max_norm", ctypes.c_float),
         ("clip_out", _p),
+        ("finite_out", _p),
+        ("finite_host", _p),
     ]
 
 
@@ -101,7 +104,7 @@ class ApplyLeaf(ctypes.Structure):
 
 
 assert ctypes.sizeof(Adam8Leaf) == 120
-assert ctypes.sizeof(Adam8Hparams) == 88
+assert ctypes.sizeof(Adam8Hparams) == 104
 assert ctypes.sizeof(ApplyLeaf) == 40
 assert ctypes.sizeof(ClipLeaf) == 32
 
@@ -110,6 +113,7 @@ EXPORTS = (
     "rf_adam8_plan_create",
     "rf_adam8_plan_run",
     "rf_adam8_plan_run_leaves",
+    "rf_adam8_plan_wait_prepass",
     "rf_adam8_plan_info",
     "rf_adam8_plan_destroy",
     "rf_adam8_step",

@@ -66,6 +66,7 @@ struct KHp {
     uint32_t flags;
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;
     const float* clip;        // device (scale, norm) of global-norm clipping, or null
+    const float* gate;        // device flag: 1 = every grad finite, 0 = reject the step; null = no gate
 };
 
 // Work list: unit u belongs to the segment s with
@@ -1080,6 +1081,40 @@ __device__ __forceinline__ void leaf_context(UnitCtx& c, const rf_adam8_leaf& L,
     if (psr) jax_split(h.kp0, h.kp1, (uint32_t)L.param_index, c.kp0, c.kp1);
 }
 
+// optax.apply_if_finite's reject branch (zero updates, inner state kept),
+// as the launch's units see it: the moments are left untouched; the fused
+// step applies the zero update (apply_updates, utils.py:694-700: f32(p) + 0
+// rounded to the param dtype, so only -0 params change, to +0; stochastic
+// rounding of an exact value adds nothing); the update-only mode writes
+// zero updates.
+template <bool APPLY>
+__device__ void reject_units(const rf_adam8_leaf* __restrict__ leaves, const Seg* __restrict__ segs,
+                             int64_t total_units, int64_t wave, int64_t nwaves)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    int32_t s = 0;
+    for (int64_t u = wave; u < total_units; u += nwaves) {
+        while (segs[s + 1].unit_start <= u) ++s;
+        const Seg sg = segs[s];
+        const rf_adam8_leaf& L = leaves[sg.leaf];
+        const int64_t span = (sg.kind == KIND_QFAST || sg.kind == KIND_QGEN) ? (int64_t)L.block_size : CHUNK;
+        const int64_t base = (sg.first + (u - sg.unit_start)) * span;
+        const int64_t end = min(base + span, L.size);
+        for (int64_t e = base + lane; e < end; e += WAVE) {
+            if constexpr (APPLY) {
+                if (L.param_dtype == RF_BF16)
+                    ((uint16_t*)L.param)[e] = (uint16_t)sr_bf16(load1(L.param, RF_BF16, e) + 0.0f, 0u);
+                else
+                    ((float*)L.param)[e] = ((const float*)L.param)[e] + 0.0f;
+            } else {
+                L.updates[e] = 0.0f;
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ bool gate_rejects(const KHp& h) { return h.gate != nullptr && *h.gate == 0.0f; }
+
 // Full 2048-element blocks of the leaves whose (param, grad) dtypes are
 // (PT, GT) (uint16_t = bf16, float = f32): the hot kernel.  Persistent
 // waves walk the work list with a grid stride of one block per wave.
@@ -1101,6 +1136,10 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     c.lds = lds;
     c.wtab = wtab[wave_in_wg];
     c.fed = (h.flags & RF_FED_BITS) != 0;
+    if (gate_rejects(h)) {
+        reject_units<APPLY>(leaves, segs, total_units, wave, nwaves);
+        return;
+    }
     clip_context(c, h);
     c.wd_mode = WD_OFF;
     c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;
@@ -1146,6 +1185,10 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
     c.lds = lds;
     c.wtab = nullptr;
     c.fed = (h.flags & RF_FED_BITS) != 0;
+    if (gate_rejects(h)) {
+        reject_units<APPLY>(leaves, segs, total_units, wave, nwaves);
+        return;
+    }
     clip_context(c, h);
     c.wd_mode = WD_OFF;
     c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;

@@ -379,7 +379,7 @@ __global__ __launch_bounds__(WG) void k_gnorm_partial(const rf_adam8_leaf* __res
 }
 
 __global__ __launch_bounds__(WG) void k_gnorm_leaf(const Seg* __restrict__ nsegs, int32_t nseg,
-                                                   const double* __restrict__ part, float* __restrict__ leafsum)
+                                                   const double* __restrict__ part, double* __restrict__ leafsum)
 {
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
@@ -388,25 +388,36 @@ __global__ __launch_bounds__(WG) void k_gnorm_leaf(const Seg* __restrict__ nsegs
         double acc = 0.0;
         for (int64_t u = nsegs[i].unit_start + lane; u < nsegs[i + 1].unit_start; u += WAVE) acc += part[u];
         acc = wave_sum_f64(acc);
-        if (lane == 0) leafsum[i] = (float)acc;
+        if (lane == 0) leafsum[i] = acc;
     }
 }
 
-__global__ void k_gnorm_finish(const float* __restrict__ leafsum, int32_t nseg, float max_norm,
-                               float* __restrict__ clip, float* __restrict__ out)
+// clip = (scale, norm, finite as f32, finite as int32 bits).  A leaf's f64 sum of squares is finite
+// exactly when all its grads are: squares of finite f32 values (< 2^256)
+// cannot overflow an f64 sum, and an Inf or NaN element makes it Inf or NaN.
+__global__ void k_gnorm_finish(const double* __restrict__ leafsum, int32_t nseg, float max_norm,
+                               float* __restrict__ clip, float* __restrict__ out, int32_t* __restrict__ finite_out)
 {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     float total = 0.0f;
-    for (int32_t i = 0; i < nseg; ++i) total = total + leafsum[i];
+    bool finite = true;
+    for (int32_t i = 0; i < nseg; ++i) {
+        const double ls = leafsum[i];
+        finite = finite && __builtin_isfinite(ls);
+        total = total + (float)ls;
+    }
     const float norm = sqrtf(total);
     const float q = max_norm / (norm + 1e-6f);
     const float scale = (q < 1.0f || q != q) ? q : 1.0f;  // jnp.minimum(1.0, q): NaN propagates
     clip[0] = scale;
     clip[1] = norm;
+    clip[2] = finite ? 1.0f : 0.0f;
+    clip[3] = __int_as_float(finite ? 1 : 0);  // the int32 flag copied to the host
     if (out) {
         out[0] = scale;
         out[1] = norm;
     }
+    if (finite_out) *finite_out = finite ? 1 : 0;
 }
 
 // Standalone clip_by_global_norm: out = grad * scale per leaf (blockIdx.y =
@@ -758,8 +769,9 @@ struct rf_adam8_plan {
     int32_t n_nsegs = 0;
     int64_t n_norm_units = 0;
     double* d_npart = nullptr;
-    float* d_leafsum = nullptr;
-    float* d_clip = nullptr;
+    double* d_leafsum = nullptr;
+    float* d_clip = nullptr;  // (scale, norm, finite as f32, finite as int32 bits)
+    hipEvent_t ev_prepass = nullptr;  // recorded after the finite flag's copy to finite_host
     std::vector<rf_adam8_leaf> shape;   // creation-time table: the structure runs must match
     std::vector<uint8_t> vec;           // leaf has vectorised (16-byte aligned) work units
     BitsCover cover;  // which fed-bits arrays the creation-time table carries
@@ -952,8 +964,9 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     }
     if (e == hipSuccess) e = hipMalloc(&p->d_nsegs, sizeof(Seg) * nsegs.size());
     if (e == hipSuccess) e = hipMalloc(&p->d_npart, sizeof(double) * (size_t)std::max<int64_t>(nunits, 1));
-    if (e == hipSuccess) e = hipMalloc(&p->d_leafsum, sizeof(float) * (size_t)std::max(n_nsegs, 1));
-    if (e == hipSuccess) e = hipMalloc(&p->d_clip, sizeof(float) * 2);
+    if (e == hipSuccess) e = hipMalloc(&p->d_leafsum, sizeof(double) * (size_t)std::max(n_nsegs, 1));
+    if (e == hipSuccess) e = hipMalloc(&p->d_clip, sizeof(float) * 4);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&p->ev_prepass, hipEventDisableTiming);
     if (e == hipSuccess) e = hipMemcpy(p->d_nsegs, nsegs.data(), sizeof(Seg) * nsegs.size(), hipMemcpyHostToDevice);
     if (e == hipSuccess && n_leaves > 0)
         e = hipMemcpy(p->d_leaves, leaves, sizeof(rf_adam8_leaf) * (size_t)n_leaves, hipMemcpyHostToDevice);
@@ -996,11 +1009,13 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
     const float max_norm = hp->clip_max_norm;
     if (!(max_norm >= 0.0f) || std::isinf(max_norm))
         return fail(RF_ERR_INVALID, "clip_max_norm must be a finite non-negative number (0: no clipping)");
+    const bool skip = (f & RF_SKIP_NONFINITE) != 0;
     DevState* ds = nullptr;
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
 
-    if (max_norm > 0.0f) {
+    // One read of the grads gives the clipping norm and the finite flag.
+    if (max_norm > 0.0f || skip || hp->finite_out || hp->finite_host) {
         const int64_t pw = std::max<int64_t>(1, std::min<int64_t>((plan->n_norm_units + WAVES_PER_WG - 1) / WAVES_PER_WG,
                                                                   (int64_t)ds->num_cus * 8));
         hipLaunchKernelGGL(k_gnorm_partial, dim3((unsigned)pw), dim3(WG), 0, (hipStream_t)stream, d_leaves,
@@ -1012,12 +1027,19 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
                            plan->n_nsegs, plan->d_npart, plan->d_leafsum);
         HIP_TRY(hipGetLastError());
         hipLaunchKernelGGL(k_gnorm_finish, dim3(1), dim3(WAVE), 0, (hipStream_t)stream, plan->d_leafsum,
-                           plan->n_nsegs, max_norm, plan->d_clip, hp->clip_out);
+                           plan->n_nsegs, max_norm, plan->d_clip, max_norm > 0.0f ? hp->clip_out : nullptr,
+                           hp->finite_out);
         HIP_TRY(hipGetLastError());
+        if (hp->finite_host) {
+            HIP_TRY(hipMemcpyAsync(hp->finite_host, plan->d_clip + 3, sizeof(int32_t), hipMemcpyDeviceToHost,
+                                   (hipStream_t)stream));
+            HIP_TRY(hipEventRecord(plan->ev_prepass, (hipStream_t)stream));
+        }
     }
 
     KHp k{};
     k.clip = max_norm > 0.0f ? plan->d_clip : nullptr;
+    k.gate = skip ? plan->d_clip + 2 : nullptr;
     k.b1 = hp->b1;
     k.omb1 = hp->one_minus_b1;
     k.b2 = hp->b2;
@@ -1088,6 +1110,10 @@ bool release_plan(rf_adam8_plan* plan)
     if (plan->d_segs) ok &= hipFree(plan->d_segs) == hipSuccess;
     for (void* q : {(void*)plan->d_nsegs, (void*)plan->d_npart, (void*)plan->d_leafsum, (void*)plan->d_clip})
         if (q) ok &= hipFree(q) == hipSuccess;
+    if (plan->ev_prepass) {
+        (void)hipEventSynchronize(plan->ev_prepass);
+        ok &= hipEventDestroy(plan->ev_prepass) == hipSuccess;
+    }
     delete plan;
     return ok;
 }
@@ -1143,6 +1169,13 @@ rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* lea
     HIP_TRY(hipEventRecord(slot.ev, (hipStream_t)stream));
     slot.pending = true;
     return st;
+}
+
+rf_status rf_adam8_plan_wait_prepass(const rf_adam8_plan* plan)
+{
+    if (!plan) return fail(RF_ERR_INVALID, "null plan");
+    HIP_TRY(hipEventSynchronize(plan->ev_prepass));
+    return RF_OK;
 }
 
 rf_status rf_adam8_plan_destroy(rf_adam8_plan* plan)
@@ -1282,14 +1315,14 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    // One scratch allocation: leaf tables, segments, partials, leaf sums, (scale, norm).
+    // One scratch allocation: leaf tables, segments, partials, leaf sums, (scale, norm, finite, 0).
     const size_t o_gl = 0;
     const size_t o_cl = o_gl + sizeof(rf_adam8_leaf) * (size_t)std::max(n_leaves, 1);
     const size_t o_sg = (o_cl + sizeof(rf_clip_leaf) * (size_t)std::max(n_leaves, 1) + 15) & ~(size_t)15;
     const size_t o_pt = (o_sg + sizeof(Seg) * nsegs.size() + 15) & ~(size_t)15;
     const size_t o_ls = o_pt + sizeof(double) * (size_t)std::max<int64_t>(nunits, 1);
-    const size_t o_cp = (o_ls + sizeof(float) * (size_t)std::max(nseg, 1) + 15) & ~(size_t)15;
-    const size_t total = o_cp + 2 * sizeof(float);
+    const size_t o_cp = (o_ls + sizeof(double) * (size_t)std::max(nseg, 1) + 15) & ~(size_t)15;
+    const size_t total = o_cp + 4 * sizeof(float);
     uint8_t* scratch = nullptr;
     HIP_TRY(hipMallocAsync((void**)&scratch, total, s));
     std::vector<uint8_t> host(o_pt);
@@ -1304,7 +1337,7 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
     const rf_clip_leaf* d_cl = (const rf_clip_leaf*)(scratch + o_cl);
     const Seg* d_sg = (const Seg*)(scratch + o_sg);
     double* d_pt = (double*)(scratch + o_pt);
-    float* d_ls = (float*)(scratch + o_ls);
+    double* d_ls = (double*)(scratch + o_ls);
     float* d_cp = (float*)(scratch + o_cp);
     if (e == hipSuccess && nunits > 0) {
         const int64_t pw = std::max<int64_t>(1, std::min<int64_t>((nunits + WAVES_PER_WG - 1) / WAVES_PER_WG,
@@ -1319,7 +1352,7 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
         }
     }
     if (e == hipSuccess) {
-        hipLaunchKernelGGL(k_gnorm_finish, dim3(1), dim3(WAVE), 0, s, d_ls, nseg, max_norm, d_cp, stats);
+        hipLaunchKernelGGL(k_gnorm_finish, dim3(1), dim3(WAVE), 0, s, d_ls, nseg, max_norm, d_cp, stats, nullptr);
         e = hipGetLastError();
     }
     if (e == hipSuccess && maxsize > 0) {

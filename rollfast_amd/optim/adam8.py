@@ -444,6 +444,9 @@ class _LeafPlan:
         _lib.check(_lib.lib().rf_adam8_plan_run_leaves(self.handle, table, self.n, ctypes.byref(hp), stream),
                    "rf_adam8_plan_run_leaves")
 
+    def wait_prepass(self):
+        _lib.check(_lib.lib().rf_adam8_plan_wait_prepass(self.handle), "rf_adam8_plan_wait_prepass")
+
     def __del__(self):
         h = getattr(self, "handle", None)
         if h is not None and h.value:
@@ -679,6 +682,9 @@ class _Engine:
         random_bits: Optional[dict] = None,
         clip_global_norm: Optional[float] = None,
         clip_stats=None,
+        skip_nonfinite: bool = False,
+        finite_out=None,
+        finite_host=None,
     ):
         torch = _torch()
         cfg = self.cfg
@@ -738,6 +744,8 @@ class _Engine:
             flags |= _lib.RF_EXACT
         if random_bits is not None:
             flags |= _lib.RF_FED_BITS
+        if skip_nonfinite:
+            flags |= _lib.RF_SKIP_NONFINITE
 
         hp = _lib.Adam8Hparams()
         hp.b1 = _as_f32(cfg.b1)
@@ -767,10 +775,16 @@ class _Engine:
                 if clip_stats.dtype != torch.float32 or clip_stats.numel() < 2 or not clip_stats.is_contiguous():
                     raise ValueError("clip_stats must be a contiguous float32 device tensor of 2 elements")
                 hp.clip_out = clip_stats.data_ptr()
+        if finite_out is not None:
+            hp.finite_out = finite_out.data_ptr()
+        if finite_host is not None:
+            hp.finite_host = finite_host.data_ptr()
 
         if n_rows:
             with torch.cuda.device(device):
                 plan.run(table, hp, _lib.stream_ptr())
+                if finite_host is not None:
+                    plan.wait_prepass()
 
         new_state = self.new_state(state, count_inc, next_key)
         out_tree = _tree.unflatten(g_td, out_leaves) if not apply else None
@@ -797,9 +811,16 @@ class _ScaleByAdam8Update:
     def __init__(self, engine: _Engine):
         self.engine = engine
 
-    def __call__(self, updates, state, params=None):
+    def _step(self, updates, state, params, *, apply: bool, skip_nonfinite=False, finite_out=None,
+              finite_host=None):
         del params
-        return self.engine.run(updates, state, None, apply=False, decay_mask=None, weight_decay=None, neg_lr=None)
+        if apply:
+            raise TypeError("scale_by_adam8 has no learning rate: the fused step needs adamw8(...)")
+        return self.engine.run(updates, state, None, apply=False, decay_mask=None, weight_decay=None, neg_lr=None,
+                               skip_nonfinite=skip_nonfinite, finite_out=finite_out, finite_host=finite_host)
+
+    def __call__(self, updates, state, params=None):
+        return self._step(updates, state, params, apply=False)
 
 
 def scale_by_adam8(
@@ -881,7 +902,7 @@ class _Adamw8Update:
         return np.float32(-_as_f32(lr)) if not isinstance(lr, (int, float)) else np.float32(-lr), lr_state
 
     def _step(self, updates, state, params, *, apply: bool, param_key=None, param_sr=False, random_bits=None,
-              clip_global_norm=None, clip_stats=None):
+              clip_global_norm=None, clip_stats=None, skip_nonfinite=False, finite_out=None, finite_host=None):
         adam_state = state[0]
         lr_state = state[-1]
         neg_lr, new_lr_state = self._lr(lr_state)
@@ -895,7 +916,8 @@ class _Adamw8Update:
             updates, adam_state, params, apply=apply, decay_mask=decay_mask,
             weight_decay=self.weight_decay if self.wd_nonzero else None, neg_lr=neg_lr,
             param_key=param_key, param_sr=param_sr, random_bits=random_bits,
-            clip_global_norm=clip_global_norm, clip_stats=clip_stats,
+            clip_global_norm=clip_global_norm, clip_stats=clip_stats, skip_nonfinite=skip_nonfinite,
+            finite_out=finite_out, finite_host=finite_host,
         )
         new_state = (new_adam,) + tuple(state[1:-1]) + (new_lr_state,)
         return out, new_state
@@ -975,17 +997,25 @@ def adamw8_step(tx, params, grads, state, key=None, stochastic: bool = True, *, 
     the step scales them as it loads them (the grads are not modified).
     ``clip_stats``: optional float32 device tensor of 2 elements that receives
     (scale, norm).
+
+    ``tx`` may also be ``apply_if_finite(adamw8(...), n)``: a step whose
+    grads hold an Inf or NaN is then rejected on the device (moments
+    untouched, params given the zero update) and the guard's counters are
+    updated, as ``optax.apply_if_finite`` followed by ``apply_updates`` does.
     """
-    if not isinstance(tx.update, _Adamw8Update):
-        raise TypeError("adamw8_step needs a transformation built by adamw8(...)")
+    from ..transforms import _ApplyIfFiniteUpdate
+
+    upd = tx.update
+    inner = upd.inner.update if isinstance(upd, _ApplyIfFiniteUpdate) else upd
+    if not isinstance(inner, _Adamw8Update):
+        raise TypeError("adamw8_step needs a transformation built by adamw8(...) (optionally in apply_if_finite)")
     if stochastic and key is None:
         raise ValueError(
             "apply_updates requires a PRNG `key` when stochastic=True. "
             "Pass stochastic=False for deterministic rounding."
         )
-    _, new_state = tx.update._step(grads, state, params, apply=True, param_key=key, param_sr=bool(stochastic),
-                                   random_bits=random_bits, clip_global_norm=clip_global_norm,
-                                   clip_stats=clip_stats)
+    _, new_state = upd._step(grads, state, params, apply=True, param_key=key, param_sr=bool(stochastic),
+                             random_bits=random_bits, clip_global_norm=clip_global_norm, clip_stats=clip_stats)
     return params, new_state
 
 

@@ -6,6 +6,13 @@ and ``GlobalNormClipState``.  The norm and the scaling run in
 and one multi-tensor scaling launch).  The optimizer steps also take the
 same clipping fused (``adamw8_step(..., clip_global_norm=...)``), which
 reads the grads once instead of reading and writing them.
+
+``apply_if_finite`` restates ``optax.apply_if_finite``, the non-finite guard
+the fine-tune builders wrap around their chain (finetune/builders.py:
+1605-1609, ``GradientPolicy(nonfinite="skip", max_consecutive_nonfinite=1)``
+by default, finetune/config.py:226-233), for the optimizers of this package:
+the step's norm pre-pass tests every grad for Inf/NaN and the step units
+apply the reject branch on the device.
 """
 
 from __future__ import annotations
@@ -16,7 +23,13 @@ from typing import Any, NamedTuple
 import numpy as np
 
 from . import _lib, _tree
-from ._base import GradientTransformation, is_passthrough_leaf as _is_passthrough_leaf
+from ._base import (
+    ApplyIfFiniteState,
+    GradientTransformation,
+    GradientTransformationExtraArgs,
+    is_passthrough_leaf as _is_passthrough_leaf,
+    safe_int32_increment,
+)
 
 
 class GlobalNormClipState(NamedTuple):
@@ -88,4 +101,91 @@ def clip_by_global_norm(max_norm: float, *, axis_name=None, partition_axis_names
     return GradientTransformation(init_fn, update_fn)
 
 
-__all__ = ("GlobalNormClipState", "clip_by_global_norm")
+class _ApplyIfFiniteUpdate:
+    """``optax.apply_if_finite(inner, max_consecutive_errors).update``.
+
+    optax semantics: ``isfinite`` = every element of every incoming update
+    (the grads, before any clipping of the inner chain) is finite;
+    ``notfinite_count`` = 0 if finite else the saturating increment of the
+    previous count; the inner update is applied when ``isfinite or
+    notfinite_count > max_consecutive_errors``, otherwise the result is zero
+    updates (zeros like the grads) and the unchanged inner state;
+    ``total_notfinite`` counts every non-finite step.
+
+    Here the inner update runs as one launch with RF_SKIP_NONFINITE (when a
+    rejection is possible) and its finite flag: the kernels leave the moments
+    untouched on a rejected step and the fused step applies the zero update to
+    the params (``f32(p) + 0``).  The next state's counters depend on the
+    flag, so the host reads it back every step: the launch copies it to
+    pinned host memory right after the norm pre-pass, and the call waits for
+    that copy only, not for the step, which keeps running.
+    """
+
+    def __init__(self, inner, max_consecutive_errors: int):
+        self.inner = inner
+        self.max_consecutive_errors = int(max_consecutive_errors)
+        self._flag = None  # pinned host int32 the launch copies the finite flag into
+
+    def _step(self, updates, state, params, *, apply: bool, **kwargs):
+        import torch
+
+        notfinite_next = safe_int32_increment(int(np.asarray(state.notfinite_count)))
+        may_reject = not notfinite_next > self.max_consecutive_errors
+        device = None
+        for leaf in _tree.leaves(updates, is_leaf=_is_passthrough_leaf):
+            if isinstance(leaf, torch.Tensor) and leaf.is_cuda:
+                device = leaf.device
+                break
+        flag = None
+        if device is not None:
+            if self._flag is None:
+                self._flag = torch.ones(1, dtype=torch.int32, pin_memory=True)
+            flag = self._flag
+            flag[0] = 1  # a run with no elements leaves it: vacuously finite
+        out, new_inner = self.inner.update._step(updates, state.inner_state, params, apply=apply,
+                                                 skip_nonfinite=may_reject, finite_host=flag, **kwargs)
+        isfinite = True if flag is None else bool(int(flag[0]))
+        if isfinite or not may_reject:
+            inner_state = new_inner
+        else:
+            inner_state = state.inner_state
+            if not apply:
+                out = _tree.tree_map(lambda x: x if _is_passthrough_leaf(x) else torch.zeros_like(x), updates,
+                                     is_leaf=_is_passthrough_leaf)
+        total = int(np.asarray(state.total_notfinite))
+        new_state = ApplyIfFiniteState(
+            notfinite_count=np.asarray(0 if isfinite else notfinite_next, dtype=np.int32),
+            last_finite=np.asarray(isfinite, dtype=np.bool_),
+            total_notfinite=np.asarray(total if isfinite else safe_int32_increment(total), dtype=np.int32),
+            inner_state=inner_state,
+        )
+        return out, new_state
+
+    def __call__(self, updates, state, params=None, **extra_args):
+        del extra_args
+        return self._step(updates, state, params, apply=False)
+
+
+def apply_if_finite(inner: GradientTransformation, max_consecutive_errors: int) -> GradientTransformationExtraArgs:
+    """Skip steps whose grads hold an Inf or NaN, up to
+    ``max_consecutive_errors`` in a row (optax.apply_if_finite, as wrapped by
+    finetune/builders.py:1605-1609).  ``inner`` is a transformation built by
+    ``adamw8``, ``scale_by_adam8``, ``adamw`` or ``scale_by_adam``; the guarded
+    step stays one launch (``adamw8_step`` / ``adamw_step`` accept the
+    wrapped transformation too)."""
+    if not hasattr(inner.update, "_step"):
+        raise NotImplementedError(
+            "apply_if_finite wraps the transformations built by adamw8, scale_by_adam8, adamw or scale_by_adam")
+
+    def init_fn(params):
+        return ApplyIfFiniteState(
+            notfinite_count=np.zeros((), dtype=np.int32),
+            last_finite=np.asarray(True, dtype=np.bool_),
+            total_notfinite=np.zeros((), dtype=np.int32),
+            inner_state=inner.init(params),
+        )
+
+    return GradientTransformationExtraArgs(init_fn, _ApplyIfFiniteUpdate(inner, max_consecutive_errors))
+
+
+__all__ = ("ApplyIfFiniteState", "GlobalNormClipState", "apply_if_finite", "clip_by_global_norm")

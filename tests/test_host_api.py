@@ -202,3 +202,21 @@ def test_clip_by_global_norm_construction():
     assert int(st.count) == 0
     with pytest.raises(ValueError, match="ROCm device"):
         rf.clip_by_global_norm(1.0).update({"w": torch.zeros(2)}, st)
+
+
+def test_apply_if_finite_construction_and_state():
+    tx = rf.apply_if_finite(rf.adamw8(1e-3, weight_decay=0.01), 2)
+    st = tx.init({"w": torch.zeros(8)})
+    assert isinstance(st, rf.ApplyIfFiniteState)
+    assert st._fields == ("notfinite_count", "last_finite", "total_notfinite", "inner_state")
+    assert int(st.notfinite_count) == 0 and bool(st.last_finite) and int(st.total_notfinite) == 0
+    assert st.notfinite_count.dtype == np.int32 and st.last_finite.dtype == np.bool_
+    assert isinstance(st.inner_state, tuple) and isinstance(st.inner_state[0], rf.ScaleByAdam8State)
+    with pytest.raises(NotImplementedError, match="apply_if_finite wraps"):
+        rf.apply_if_finite(rf.clip_by_global_norm(1.0), 1)
+    # no CPU fallback behind the guard either
+    with pytest.raises(ValueError, match="ROCm device"):
+        tx.update({"w": torch.zeros(8)}, st, {"w": torch.zeros(8)})
+    with pytest.raises(TypeError, match="adamw8"):
+        rf.adamw8_step(rf.apply_if_finite(rf.scale_by_adam8(), 1), {"w": torch.zeros(8)}, {"w": torch.zeros(8)},
+                       None, stochastic=False)

@@ -573,3 +573,50 @@ def test_clip_leaf_bf16_rounds_once_with_bf16_scale():
     np.testing.assert_array_equal(got, orc.f32_to_bf16_bits(exact.astype(np.float32)))
     f = rng.standard_normal(100).astype(np.float32)
     np.testing.assert_array_equal(orc.clip_leaf(f, orc.F32, scale), f * scale)
+
+
+def test_apply_if_finite_decision_known_sequence():
+    """optax.apply_if_finite, documented behaviour: non-finite steps are
+    skipped until more than max_consecutive_errors of them come in a row,
+    then the update is let through; a finite step resets the consecutive
+    count but not the total."""
+    seq = [True, False, False, False, True, False, True]
+    want = {  # max_consecutive_errors -> (applied, notfinite_count, total_notfinite) per step
+        1: ([1, 0, 1, 1, 1, 0, 1], [0, 1, 2, 3, 0, 1, 0], [0, 1, 2, 3, 3, 4, 4]),
+        2: ([1, 0, 0, 1, 1, 0, 1], [0, 1, 2, 3, 0, 1, 0], [0, 1, 2, 3, 3, 4, 4]),
+    }
+    for mce, (w_apply, w_count, w_total) in want.items():
+        count = total = 0
+        got_apply, got_count, got_total = [], [], []
+        for fin in seq:
+            a, count, total = orc.apply_if_finite_decision(count, total, fin, mce)
+            got_apply.append(int(a))
+            got_count.append(count)
+            got_total.append(total)
+        assert (got_apply, got_count, got_total) == (w_apply, w_count, w_total), mce
+    # the counters saturate at the int32 maximum (optax.numerics.safe_increment)
+    assert orc.apply_if_finite_decision(2**31 - 1, 2**31 - 1, False, 1) == (True, 2**31 - 1, 2**31 - 1)
+
+
+def test_all_finite_and_reject_params():
+    f = np.array([0.5, -1.0, 3.0e38], np.float32)
+    b = orc.f32_to_bf16_bits(np.array([0.5, 2.0], np.float32))
+    assert orc.all_finite([f, b], [orc.F32, orc.BF16])
+    for bad in (np.nan, np.inf, -np.inf):
+        g = f.copy()
+        g[1] = bad
+        assert not orc.all_finite([g, b], [orc.F32, orc.BF16])
+        gb = orc.f32_to_bf16_bits(np.array([0.5, bad], np.float32))
+        assert not orc.all_finite([f, gb], [orc.F32, orc.BF16])
+    assert orc.all_finite([], [])
+    # IEEE 754 round-to-nearest: x + (+0) is x for every x except -0, which gives +0
+    p = np.array([-0.0, 0.0, 1.5, -2.0, np.inf, -np.inf, 1e-45, -1e-45], np.float32)
+    want = p.copy()
+    want[0] = 0.0
+    orc.reject_params(p, orc.F32)
+    np.testing.assert_array_equal(p.view(np.uint32), want.view(np.uint32))
+    h = np.array([0x8000, 0x0000, 0x3FC0, 0xC000, 0x7F80, 0xFF80, 0x0001, 0x8001], np.uint16)
+    want_h = h.copy()
+    want_h[0] = 0
+    orc.reject_params(h, orc.BF16)
+    np.testing.assert_array_equal(h, want_h)
