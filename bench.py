@@ -22,6 +22,9 @@ Other workloads (one JSON line each, same fields):
   llama7b_finetune the fine-tune builders' gradient policy around the step:
                    clipping at 1.0 and apply_if_finite (skip non-finite
                    steps); the finite flag is read back once per step.
+  llama7b_finetune_groups  the same around a three-group multi_transform
+                   (base / embeddings / norms with their own learning rates,
+                   decays and keys), as the fine-tune builders compose it.
   llama7b_optax    update-only (Optax) mode over the Llama tree: f32 updates
                    written, params read for weight decay.
   llama7b_adamw_f32   full-precision AdamW (adamw, f32 moments) over the Llama
@@ -262,7 +265,7 @@ class Workload:
 
 
 def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None, clip=None,
-                   guard=False):
+                   guard=False, groups=False):
     import numpy as np
     import torch
 
@@ -280,6 +283,23 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     else:
         tx = rf.adamw(learning_rate=1e-3, weight_decay=0.01, exact=args.exact,
                       mu_dtype=torch.bfloat16 if adam_mu == "bf16" else None)
+    chain_clip = None
+    if groups:
+        # the fine-tune builders' shape: groups with their own lr / decay / key
+        # (embeddings and norms undecayed), clipping and the non-finite guard
+        # around the multi_transform, all one launch
+        def group_of(name):
+            return "embed" if "embed" in name or "lm_head" in name else ("norm" if "norm" in name else "base")
+
+        labels = {name: group_of(name) for name, _ in shapes}
+        tx = rf.multi_transform({
+            "base": rf.adamw8(learning_rate=1e-3, weight_decay=0.05, exact=args.exact, key=rf.prng.PRNGKey(1)),
+            "embed": rf.adamw8(learning_rate=2e-4, weight_decay=0.0, exact=args.exact, key=rf.prng.PRNGKey(2)),
+            "norm": rf.adamw8(learning_rate=1e-3, weight_decay=0.0, exact=args.exact, key=rf.prng.PRNGKey(3)),
+        }, labels)
+        if clip is not None:
+            tx = rf.chain(rf.clip_by_global_norm(clip), tx)
+            chain_clip, clip = clip, None
     if guard:
         tx = rf.apply_if_finite(tx, 1)
     state = tx.init(params)
@@ -335,6 +355,10 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     }
     if clip is not None:
         config["clip_global_norm"] = clip
+    if groups:
+        config["groups"] = "multi_transform: base (lr 1e-3, wd 0.05), embed (lr 2e-4), norm (lr 1e-3), one launch"
+        config["clip_global_norm"] = chain_clip
+        config["launches_per_step"] = 4
     if guard:
         config["nonfinite"] = "skip (apply_if_finite, max_consecutive_errors=1; one int32 read back per step)"
         config["launches_per_step"] = 4
@@ -346,7 +370,8 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
                                    sample_name=f"the first {len(sub)} leaves", param_sr=param_sr)
     metric = METRIC if workload == "llama7b_bf16_adamw8" else f"adam8 params/sec + achieved HBM GB/s, {workload}, 1 GPU"
     if adam_mu is None:
-        nbytes = step_bytes(shapes, apply=not optax) + (n_params * 2 if (clip is not None or guard) else 0)
+        nbytes = step_bytes(shapes, apply=not optax) + (n_params * 2 if (clip is not None or guard or groups)
+                                                        else 0)
     else:
         mb = 4 if adam_mu == "f32" else 2
         nbytes = n_params * (2 + 2 + 2 + 2 * 2 * mb)  # p r+w, g r, two moments r+w
@@ -446,6 +471,8 @@ WORKLOADS = {
                                              param_sr=False, clip=1.0),
     "llama7b_finetune": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_clip_skip_nonfinite",
                                                  param_sr=False, clip=1.0, guard=True),
+    "llama7b_finetune_groups": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_grouped_finetune",
+                                                        param_sr=False, clip=1.0, guard=True, groups=True),
     "llama7b_optax": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_optax_update",
                                               param_sr=False, optax=True),
     "llama7b_adamw_f32": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw_f32_moments",

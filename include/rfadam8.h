@@ -100,8 +100,23 @@ typedef struct rf_adam8_leaf {
     int32_t param_index;        /* position in the flattened params: the param-SR key is
                                    split(key_param)[param_index] (utils.py:682) */
     uint32_t flags;             /* RF_LEAF_* */
-    int32_t reserved;
+    int32_t group;              /* index into rf_adam8_hparams.groups when n_groups > 0
+                                   (optax.multi_transform label of the leaf), else 0 */
 } rf_adam8_leaf;
+
+/* Per-group scalars of a grouped launch: optax.multi_transform over adamw8 /
+ * adamw transforms that share b1, b2, eps, eps_root and the step count but
+ * not the learning rate, weight decay or keys (the fine-tune builders' groups,
+ * finetune/builders.py:1529-1621). */
+typedef struct rf_adam8_group {
+    float neg_lr;            /* f32(-lr) of the group's learning rate or schedule (RF_LR) */
+    float weight_decay;      /* f32(wd) of the group's add_decayed_weights */
+    float one_minus_b1;      /* gradient weight of the group's first-moment EMA (adamw8:
+                                f32(1.0 - b1); optim/adam.py: 1 - f32(b1)) */
+    uint32_t reserved;       /* 0 */
+    uint32_t key_mu[2];      /* the group's moment keys, as rf_adam8_hparams.key_mu/key_nu */
+    uint32_t key_nu[2];
+} rf_adam8_group;
 
 /* Per-step scalars.  The host derives them exactly as the reference does
  * (adam8.py:322-339, optax add_decayed_weights / scale_by_learning_rate). */
@@ -136,6 +151,14 @@ typedef struct rf_adam8_hparams {
                                 flag by a copy enqueued right after the pre-pass, before the
                                 step; rf_adam8_plan_wait_prepass waits for it, so a host that
                                 needs the flag does not wait for the whole step.  NULL: none */
+    const rf_adam8_group* groups; /* host array of n_groups: leaf L takes neg_lr, weight_decay,
+                                one_minus_b1 and the moment keys from groups[L.group] instead
+                                of the fields above; NULL when n_groups == 0.  The library
+                                copies it with the leaf table (plan_run_leaves' staging ring),
+                                so it may be reused as soon as the call returns. */
+    int32_t n_groups;        /* 0: one group (the fields above); else exactly the plan's group
+                                count, 1 + the largest leaf.group at plan creation */
+    int32_t reserved0;       /* 0 */
 } rf_adam8_hparams;
 
 typedef struct rf_adam8_plan rf_adam8_plan;

@@ -34,6 +34,7 @@ from .optim.adam8 import (
     tree_state_nbytes,
 )
 from .optim.adam import ScaleByAdamState, adamw, adamw_step, scale_by_adam
+from .combine import MultiTransformState, chain, masked, multi_transform
 from .transforms import GlobalNormClipState, apply_if_finite, clip_by_global_norm
 from .utils import apply_updates, apply_updates_prefix
 
@@ -50,6 +51,7 @@ __all__ = (
     "GradientTransformationExtraArgs",
     "MaskedNode",
     "MaskedState",
+    "MultiTransformState",
     "QuantizedBlocks",
     "ScaleByAdam8State",
     "ScaleByAdamState",
@@ -61,9 +63,12 @@ __all__ = (
     "apply_if_finite",
     "apply_updates",
     "apply_updates_prefix",
+    "chain",
     "clip_by_global_norm",
     "dequantize_blocks",
     "estimate_quantized_moment_bytes",
+    "masked",
+    "multi_transform",
     "prng",
     "quantize_blocks",
     "quantized_nbytes",

@@ -53,7 +53,18 @@ class Adam8Leaf(ctypes.Structure):
         ("state_index", ctypes.c_int32),
         ("param_index", ctypes.c_int32),
         ("flags", ctypes.c_uint32),
-        ("reserved", ctypes.c_int32),
+        ("group", ctypes.c_int32),
+    ]
+
+
+class Adam8Group(ctypes.Structure):
+    _fields_ = [
+        ("neg_lr", ctypes.c_float),
+        ("weight_decay", ctypes.c_float),
+        ("one_minus_b1", ctypes.c_float),
+        ("reserved", ctypes.c_uint32),
+        ("key_mu", ctypes.c_uint32 * 2),
+        ("key_nu", ctypes.c_uint32 * 2),
     ]
 
 
@@ -79,6 +90,9 @@ class Adam8Hparams(ctypes.Structure):
         ("clip_out", _p),
         ("finite_out", _p),
         ("finite_host", _p),
+        ("groups", _p),
+        ("n_groups", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32),
     ]
 
 
@@ -104,7 +118,8 @@ class ApplyLeaf(ctypes.Structure):
 
 
 assert ctypes.sizeof(Adam8Leaf) == 120
-assert ctypes.sizeof(Adam8Hparams) == 104
+assert ctypes.sizeof(Adam8Hparams) == 120
+assert ctypes.sizeof(Adam8Group) == 32
 assert ctypes.sizeof(ApplyLeaf) == 40
 assert ctypes.sizeof(ClipLeaf) == 32
 

@@ -67,6 +67,7 @@ struct KHp {
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;
     const float* clip;        // device (scale, norm) of global-norm clipping, or null
     const float* gate;        // device flag: 1 = every grad finite, 0 = reject the step; null = no gate
+    const rf_adam8_group* groups;  // per-group lr, decay, EMA weight and keys (grouped launch), or null
 };
 
 // Work list: unit u belongs to the segment s with
@@ -1070,6 +1071,23 @@ __device__ __forceinline__ void dispatch_fallback_vec(const UnitCtx& c, const rf
 }
 
 // ======================================================== step kernels ===
+// The scalars of the leaf's group in a grouped launch (optax.multi_transform):
+// hl is the launch's KHp with the group's learning rate, weight decay, EMA
+// weight and moment keys.  Ungrouped launches keep hl == h.
+__device__ __forceinline__ void group_hparams(KHp& hl, const KHp& h, const rf_adam8_leaf& L)
+{
+    if (h.groups == nullptr) return;
+    const rf_adam8_group G = h.groups[L.group];
+    hl.neg_lr = (h.flags & RF_LR) ? G.neg_lr : 1.0f;
+    hl.wd = G.weight_decay;
+    hl.wd16 = round_to_bf16(G.weight_decay);
+    hl.omb1 = G.one_minus_b1;
+    hl.kmu0 = G.key_mu[0];
+    hl.kmu1 = G.key_mu[1];
+    hl.knu0 = G.key_nu[0];
+    hl.knu1 = G.key_nu[1];
+}
+
 __device__ __forceinline__ void leaf_context(UnitCtx& c, const rf_adam8_leaf& L, const KHp& h, bool msr, bool psr)
 {
     const bool decay = (L.flags & RF_LEAF_DECAY) != 0;
@@ -1144,6 +1162,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     c.wd_mode = WD_OFF;
     c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;
     rf_adam8_leaf L;
+    KHp hl = h;  // the current leaf's scalars (its group's, in a grouped launch)
     ChunkSlots<PT, GT> sl;
     bool have0 = false;  // slot 0 holds chunk 0 of unit u
     for (int64_t u = wave; u < total_units; u += nwaves) {
@@ -1152,7 +1171,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
         if (sg.leaf != cur_leaf) {
             cur_leaf = sg.leaf;
             L = leaves[cur_leaf];
-            leaf_context(c, L, h, MSR, PSR);
+            group_hparams(hl, h, L);
+            leaf_context(c, L, hl, MSR, PSR);
         }
         // The next unit of this wave, when it is a block of the same leaf
         // (this kernel's units are all full blocks; one segment per leaf).
@@ -1160,7 +1180,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
         int64_t next_blk = -1;
         if (RF_PREFETCH_NEXT && un < total_units && un < segs[s + 1].unit_start)
             next_blk = sg.first + (un - sg.unit_start);
-        dispatch_qfast<PT, GT, APPLY, MSR, PSR, NEST, EXACT>(c, L, sg.first + (u - sg.unit_start), h, sl, have0,
+        dispatch_qfast<PT, GT, APPLY, MSR, PSR, NEST, EXACT>(c, L, sg.first + (u - sg.unit_start), hl, sl, have0,
                                                              next_blk);
         have0 = next_blk >= 0;
     }
@@ -1193,18 +1213,20 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
     c.wd_mode = WD_OFF;
     c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;
     rf_adam8_leaf L;
+    KHp hl = h;  // the current leaf's scalars (its group's, in a grouped launch)
     for (int64_t u = wave; u < total_units; u += nwaves) {
         while (segs[s + 1].unit_start <= u) ++s;
         const Seg sg = segs[s];
         if (sg.leaf != cur_leaf) {
             cur_leaf = sg.leaf;
             L = leaves[cur_leaf];
-            leaf_context(c, L, h, MSR, PSR);
+            group_hparams(hl, h, L);
+            leaf_context(c, L, hl, MSR, PSR);
         }
         const int64_t idx = sg.first + (u - sg.unit_start);
-        if (sg.kind == KIND_QGEN) unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h);
-        else if (sg.kind == KIND_FALLBACK_VEC) dispatch_fallback_vec<APPLY, PSR, NEST, EXACT>(c, L, idx, h);
-        else unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, idx, h);
+        if (sg.kind == KIND_QGEN) unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, hl);
+        else if (sg.kind == KIND_FALLBACK_VEC) dispatch_fallback_vec<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
+        else unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
     }
 }
 

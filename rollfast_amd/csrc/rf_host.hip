@@ -717,7 +717,7 @@ int64_t nblocks_of(int64_t size, int64_t bs) { return size > 0 ? (size + bs - 1)
 // unless RING runs are still in flight.
 constexpr int RING = 4;
 struct RingSlot {
-    rf_adam8_leaf* host = nullptr;
+    rf_adam8_leaf* host = nullptr;  // leaf table, then (at group_off) the group table
     rf_adam8_leaf* dev = nullptr;
     hipEvent_t ev = nullptr;
     bool pending = false;
@@ -757,6 +757,8 @@ struct rf_adam8_plan {
     int device = 0;
     int32_t apply = 1;
     int32_t n_leaves = 0;
+    int32_t group_cap = 1;    // group count of a grouped run: 1 + the largest leaf.group at creation
+    size_t group_off = 0;     // byte offset of the group table in a ring slot
     int64_t total_units = 0;
     int64_t n_segs = 0;
     std::vector<PlanGroup> groups;
@@ -800,6 +802,7 @@ rf_status validate_leaf(const rf_adam8_leaf& L, int32_t i, int32_t apply)
         if (!L.mu_scales || !L.nu_scales) return fail(RF_ERR_INVALID, at + "null scales");
     }
     if (L.state_index < 0 || L.param_index < 0) return fail(RF_ERR_INVALID, at + "negative key index");
+    if (L.group < 0) return fail(RF_ERR_INVALID, at + "negative group index");
     return RF_OK;
 }
 
@@ -955,11 +958,14 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     // Every buffer a run needs is allocated here, so runs never allocate
     // (pinned-host and device allocation synchronise the device).
     const size_t table_bytes = sizeof(rf_adam8_leaf) * (size_t)std::max(n_leaves, 1);
+    for (int32_t i = 0; i < n_leaves; ++i) p->group_cap = std::max(p->group_cap, leaves[i].group + 1);
+    p->group_off = (table_bytes + 15) & ~(size_t)15;
+    const size_t slot_bytes = p->group_off + sizeof(rf_adam8_group) * (size_t)p->group_cap;
     hipError_t e = hipMalloc(&p->d_leaves, table_bytes);
     if (e == hipSuccess) e = hipMalloc(&p->d_segs, sizeof(Seg) * segs.size());
     for (RingSlot& slot : p->ring) {
-        if (e == hipSuccess) e = hipHostMalloc((void**)&slot.host, table_bytes, hipHostMallocDefault);
-        if (e == hipSuccess) e = hipMalloc((void**)&slot.dev, table_bytes);
+        if (e == hipSuccess) e = hipHostMalloc((void**)&slot.host, slot_bytes, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipMalloc((void**)&slot.dev, slot_bytes);
         if (e == hipSuccess) e = hipEventCreateWithFlags(&slot.ev, hipEventDisableTiming);
     }
     if (e == hipSuccess) e = hipMalloc(&p->d_nsegs, sizeof(Seg) * nsegs.size());
@@ -992,8 +998,8 @@ rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64
 
 namespace {
 
-rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, const BitsCover& cover,
-                      const rf_adam8_hparams* hp, void* stream)
+rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, const rf_adam8_group* d_groups,
+                      const BitsCover& cover, const rf_adam8_hparams* hp, void* stream)
 {
     if (plan->total_units == 0) return RF_OK;
     const uint32_t f = hp->flags;
@@ -1038,6 +1044,7 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
     }
 
     KHp k{};
+    k.groups = hp->n_groups > 0 ? d_groups : nullptr;
     k.clip = max_norm > 0.0f ? plan->d_clip : nullptr;
     k.gate = skip ? plan->d_clip + 2 : nullptr;
     k.b1 = hp->b1;
@@ -1122,7 +1129,40 @@ bool same_structure(const rf_adam8_leaf& a, const rf_adam8_leaf& b)
 {
     return a.size == b.size && a.block_size == b.block_size && a.param_dtype == b.param_dtype &&
            a.grad_dtype == b.grad_dtype && a.moment_kind == b.moment_kind && a.state_index == b.state_index &&
-           a.param_index == b.param_index && a.flags == b.flags;
+           a.param_index == b.param_index && a.flags == b.flags && a.group == b.group;
+}
+
+rf_status check_groups(const rf_adam8_plan* plan, const rf_adam8_hparams* hp)
+{
+    if (hp->n_groups < 0) return fail(RF_ERR_INVALID, "negative n_groups");
+    if (hp->n_groups == 0) return RF_OK;
+    if (!hp->groups) return fail(RF_ERR_INVALID, "n_groups > 0 with a null group table");
+    // Every leaf's group index is below group_cap (leaf structure is fixed by the plan).
+    if (hp->n_groups != plan->group_cap)
+        return fail(RF_ERR_INVALID, "n_groups must be 0 or the plan's group count (1 + the largest leaf.group at creation)");
+    return RF_OK;
+}
+
+// Stages the leaf table (and the group table) in the next pinned ring slot,
+// copies it to the slot's device twin on `stream` and launches.
+rf_status run_staged(rf_adam8_plan* plan, const rf_adam8_leaf* leaves, int32_t n_leaves, const BitsCover& cover,
+                     const rf_adam8_hparams* hp, void* stream)
+{
+    std::lock_guard<std::mutex> lock(plan->mu);
+    RingSlot& slot = plan->ring[plan->next % RING];
+    plan->next++;
+    const size_t bytes = sizeof(rf_adam8_leaf) * (size_t)n_leaves;
+    const size_t gbytes = sizeof(rf_adam8_group) * (size_t)std::max(hp->n_groups, 0);
+    if (slot.pending) HIP_TRY(hipEventSynchronize(slot.ev));
+    std::memcpy(slot.host, leaves, bytes);
+    if (gbytes) std::memcpy((uint8_t*)slot.host + plan->group_off, hp->groups, gbytes);
+    const size_t span = gbytes ? plan->group_off + gbytes : bytes;
+    HIP_TRY(hipMemcpyAsync(slot.dev, slot.host, span, hipMemcpyHostToDevice, (hipStream_t)stream));
+    const rf_adam8_group* d_groups = (const rf_adam8_group*)((uint8_t*)slot.dev + plan->group_off);
+    rf_status st = plan_launch(plan, slot.dev, d_groups, cover, hp, stream);
+    HIP_TRY(hipEventRecord(slot.ev, (hipStream_t)stream));
+    slot.pending = true;
+    return st;
 }
 
 }  // namespace
@@ -1135,7 +1175,13 @@ rf_status rf_adam8_plan_run(const rf_adam8_plan* plan, const rf_adam8_hparams* h
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     if (dev != plan->device) return fail(RF_ERR_INVALID, "plan was created on another device");
-    return plan_launch(plan, plan->d_leaves, plan->cover, hp, stream);
+    rf_status st = check_groups(plan, hp);
+    if (st != RF_OK) return st;
+    if (hp->n_groups == 0) return plan_launch(plan, plan->d_leaves, nullptr, plan->cover, hp, stream);
+    // The group table travels through the staging ring with the creation-time leaf table.
+    if (plan->total_units == 0) return RF_OK;
+    rf_adam8_plan* mp = const_cast<rf_adam8_plan*>(plan);
+    return run_staged(mp, plan->shape.data(), plan->n_leaves, plan->cover, hp, stream);
 }
 
 rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* leaves, int32_t n_leaves,
@@ -1147,28 +1193,19 @@ rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* lea
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     if (dev != plan->device) return fail(RF_ERR_INVALID, "plan was created on another device");
+    rf_status st = check_groups(plan, hp);
+    if (st != RF_OK) return st;
     for (int32_t i = 0; i < n_leaves; ++i) {
         const rf_adam8_leaf& L = leaves[i];
         if (!same_structure(L, plan->shape[i]))
             return fail(RF_ERR_INVALID, "leaf " + std::to_string(i) + " differs in structure from the plan");
-        rf_status st = validate_leaf(L, i, plan->apply);
+        st = validate_leaf(L, i, plan->apply);
         if (st != RF_OK) return st;
         if (plan->vec[i] && !leaf_vec_ok(L, plan->apply))
             return fail(RF_ERR_INVALID, "leaf " + std::to_string(i) + " lost the 16-byte alignment the plan relies on");
     }
-    const BitsCover cover = bits_cover(leaves, n_leaves);
     if (plan->total_units == 0) return RF_OK;
-    std::lock_guard<std::mutex> lock(plan->mu);
-    RingSlot& slot = plan->ring[plan->next % RING];
-    plan->next++;
-    const size_t bytes = sizeof(rf_adam8_leaf) * (size_t)n_leaves;
-    if (slot.pending) HIP_TRY(hipEventSynchronize(slot.ev));
-    std::memcpy(slot.host, leaves, bytes);
-    HIP_TRY(hipMemcpyAsync(slot.dev, slot.host, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
-    rf_status st = plan_launch(plan, slot.dev, cover, hp, stream);
-    HIP_TRY(hipEventRecord(slot.ev, (hipStream_t)stream));
-    slot.pending = true;
-    return st;
+    return run_staged(plan, leaves, n_leaves, bits_cover(leaves, n_leaves), hp, stream);
 }
 
 rf_status rf_adam8_plan_wait_prepass(const rf_adam8_plan* plan)

@@ -135,7 +135,8 @@ class _ScaleByAdamUpdate:
         return self._step(updates, state, params, apply=False)
 
     def _step(self, updates, state, params, *, apply: bool, skip_nonfinite=False, finite_out=None,
-              finite_host=None):
+              finite_host=None, clip_global_norm=None, clip_stats=None, **fused_only):
+        del fused_only  # param_key, param_sr, random_bits: fused-step arguments
         if apply:
             raise TypeError("scale_by_adam has no learning rate: the fused step needs adamw(...)")
         decays = _has_nonzero_or_scheduled(self.weight_decay)
@@ -159,7 +160,7 @@ class _ScaleByAdamUpdate:
             wd = np.float32(_as_f32(wd))
         return self.engine.run(updates, state, params, apply=False, decay_mask=decay_mask, weight_decay=wd,
                                neg_lr=None, skip_nonfinite=skip_nonfinite, finite_out=finite_out,
-                               finite_host=finite_host)
+                               finite_host=finite_host, clip_global_norm=clip_global_norm, clip_stats=clip_stats)
 
 
 def scale_by_adam(
@@ -248,12 +249,12 @@ def adamw_step(tx, params, grads, state, key=None, stochastic: bool = True, *, r
     replace the in-kernel bits of the bf16 moment storage and the param SR.
     ``clip_global_norm`` / ``clip_stats``: fused global-norm clipping, as for
     ``adamw8_step``."""
-    from ..transforms import _ApplyIfFiniteUpdate
     from .adam8 import adamw8_step
 
-    inner = tx.update.inner.update if isinstance(tx.update, _ApplyIfFiniteUpdate) else tx.update
-    if not isinstance(inner, _Adamw8Update) or not isinstance(inner.engine, _AdamEngine):
-        raise TypeError("adamw_step needs a transformation built by adamw(...) (optionally in apply_if_finite)")
+    if isinstance(tx.update, _ScaleByAdamUpdate) or (isinstance(tx.update, _Adamw8Update)
+                                                     and not isinstance(tx.update.engine, _AdamEngine)):
+        raise TypeError("adamw_step needs a transformation built by adamw(...) or a composition of them "
+                        "(apply_if_finite, chain with clip_by_global_norm, multi_transform)")
     return adamw8_step(tx, params, grads, state, key=key, stochastic=stochastic, random_bits=random_bits,
                        clip_global_norm=clip_global_norm, clip_stats=clip_stats)
 

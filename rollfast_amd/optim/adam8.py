@@ -747,38 +747,13 @@ class _Engine:
         if skip_nonfinite:
             flags |= _lib.RF_SKIP_NONFINITE
 
-        hp = _lib.Adam8Hparams()
-        hp.b1 = _as_f32(cfg.b1)
+        hp = _common_hparams(cfg, count_inc, flags, param_key, clip_global_norm, clip_stats, finite_out,
+                             finite_host)
         hp.one_minus_b1 = self.ema_weight(cfg.b1)
-        hp.nesterov_one_minus_b1 = _one_minus(cfg.b1)
-        hp.b2 = _as_f32(cfg.b2)
-        hp.one_minus_b2 = _one_minus(cfg.b2)
-        hp.bc1 = _bias_correction(cfg.b1, count_inc)
-        hp.bc2 = _bias_correction(cfg.b2, count_inc)
-        hp.bc1_next = _bias_correction(cfg.b1, safe_int32_increment(count_inc))
-        hp.eps = _as_f32(cfg.eps)
-        hp.eps_root = _as_f32(cfg.eps_root)
         hp.weight_decay = _as_f32(weight_decay) if weight_decay is not None else np.float32(0.0)
         hp.neg_lr = neg_lr if neg_lr is not None else np.float32(1.0)
-        hp.flags = flags
         hp.key_mu[0], hp.key_mu[1] = int(key_mu[0]), int(key_mu[1])
         hp.key_nu[0], hp.key_nu[1] = int(key_nu[0]), int(key_nu[1])
-        if param_key is not None:
-            pk = prng.as_key(param_key)
-            hp.key_param[0], hp.key_param[1] = int(pk[0]), int(pk[1])
-        if clip_global_norm is not None:
-            if not (float(clip_global_norm) > 0.0) or not math.isfinite(float(clip_global_norm)):
-                raise ValueError("max_norm must be positive.")
-            hp.clip_max_norm = float(clip_global_norm)
-            if clip_stats is not None:
-                _require_device_tensor(clip_stats, "clip_stats")
-                if clip_stats.dtype != torch.float32 or clip_stats.numel() < 2 or not clip_stats.is_contiguous():
-                    raise ValueError("clip_stats must be a contiguous float32 device tensor of 2 elements")
-                hp.clip_out = clip_stats.data_ptr()
-        if finite_out is not None:
-            hp.finite_out = finite_out.data_ptr()
-        if finite_host is not None:
-            hp.finite_host = finite_host.data_ptr()
 
         if n_rows:
             with torch.cuda.device(device):
@@ -789,6 +764,42 @@ class _Engine:
         new_state = self.new_state(state, count_inc, next_key)
         out_tree = _tree.unflatten(g_td, out_leaves) if not apply else None
         return out_tree, new_state
+
+
+def _common_hparams(cfg: _Config, count_inc: int, flags: int, param_key, clip_global_norm, clip_stats, finite_out,
+                    finite_host):
+    """The launch scalars every leaf shares: betas, bias corrections at
+    ``count_inc`` (adam8.py:336-339), eps, flags, the param-SR key, clipping
+    and the finite flag outputs."""
+    torch = _torch()
+    hp = _lib.Adam8Hparams()
+    hp.b1 = _as_f32(cfg.b1)
+    hp.nesterov_one_minus_b1 = _one_minus(cfg.b1)
+    hp.b2 = _as_f32(cfg.b2)
+    hp.one_minus_b2 = _one_minus(cfg.b2)
+    hp.bc1 = _bias_correction(cfg.b1, count_inc)
+    hp.bc2 = _bias_correction(cfg.b2, count_inc)
+    hp.bc1_next = _bias_correction(cfg.b1, safe_int32_increment(count_inc))
+    hp.eps = _as_f32(cfg.eps)
+    hp.eps_root = _as_f32(cfg.eps_root)
+    hp.flags = flags
+    if param_key is not None:
+        pk = prng.as_key(param_key)
+        hp.key_param[0], hp.key_param[1] = int(pk[0]), int(pk[1])
+    if clip_global_norm is not None:
+        if not (float(clip_global_norm) > 0.0) or not math.isfinite(float(clip_global_norm)):
+            raise ValueError("max_norm must be positive.")
+        hp.clip_max_norm = float(clip_global_norm)
+        if clip_stats is not None:
+            _require_device_tensor(clip_stats, "clip_stats")
+            if clip_stats.dtype != torch.float32 or clip_stats.numel() < 2 or not clip_stats.is_contiguous():
+                raise ValueError("clip_stats must be a contiguous float32 device tensor of 2 elements")
+            hp.clip_out = clip_stats.data_ptr()
+    if finite_out is not None:
+        hp.finite_out = finite_out.data_ptr()
+    if finite_host is not None:
+        hp.finite_host = finite_host.data_ptr()
+    return hp
 
 
 def _validate(block_size, min_size, block_layout, fallback_dtype, scale_dtype):
@@ -812,12 +823,13 @@ class _ScaleByAdam8Update:
         self.engine = engine
 
     def _step(self, updates, state, params, *, apply: bool, skip_nonfinite=False, finite_out=None,
-              finite_host=None):
-        del params
+              finite_host=None, clip_global_norm=None, clip_stats=None, **fused_only):
+        del params, fused_only  # param_key, param_sr, random_bits: fused-step arguments
         if apply:
             raise TypeError("scale_by_adam8 has no learning rate: the fused step needs adamw8(...)")
         return self.engine.run(updates, state, None, apply=False, decay_mask=None, weight_decay=None, neg_lr=None,
-                               skip_nonfinite=skip_nonfinite, finite_out=finite_out, finite_host=finite_host)
+                               skip_nonfinite=skip_nonfinite, finite_out=finite_out, finite_host=finite_host,
+                               clip_global_norm=clip_global_norm, clip_stats=clip_stats)
 
     def __call__(self, updates, state, params=None):
         return self._step(updates, state, params, apply=False)
@@ -998,17 +1010,17 @@ def adamw8_step(tx, params, grads, state, key=None, stochastic: bool = True, *, 
     ``clip_stats``: optional float32 device tensor of 2 elements that receives
     (scale, norm).
 
-    ``tx`` may also be ``apply_if_finite(adamw8(...), n)``: a step whose
-    grads hold an Inf or NaN is then rejected on the device (moments
-    untouched, params given the zero update) and the guard's counters are
-    updated, as ``optax.apply_if_finite`` followed by ``apply_updates`` does.
+    ``tx`` may also be a composition the fine-tune builders use, still one
+    launch: ``apply_if_finite(...)`` (a step whose grads hold an Inf or NaN
+    is rejected on the device: moments untouched, params given the zero
+    update, the guard's counters updated), ``chain(clip_by_global_norm(m),
+    ...)`` and ``multi_transform({label: adamw8(...) or adamw(...)}, labels)``
+    (one grouped launch).
     """
-    from ..transforms import _ApplyIfFiniteUpdate
-
     upd = tx.update
-    inner = upd.inner.update if isinstance(upd, _ApplyIfFiniteUpdate) else upd
-    if not isinstance(inner, _Adamw8Update):
-        raise TypeError("adamw8_step needs a transformation built by adamw8(...) (optionally in apply_if_finite)")
+    if not hasattr(upd, "_step") or isinstance(upd, _ScaleByAdam8Update):
+        raise TypeError("adamw8_step needs a transformation built by adamw8(...), adamw(...) or a composition "
+                        "of them (apply_if_finite, chain with clip_by_global_norm, multi_transform)")
     if stochastic and key is None:
         raise ValueError(
             "apply_updates requires a PRNG `key` when stochastic=True. "
@@ -1036,3 +1048,133 @@ __all__ = (
     "scale_by_adam8",
     "tree_state_nbytes",
 )
+
+
+# --------------------------------------------------- grouped launches -----
+def _group_key(upd) -> tuple:
+    """What a group must share with the others to join one grouped launch:
+    everything but the learning rate, weight decay, EMA-weight convention
+    and keys (those travel per group).  Moment stochastic rounding is
+    compared separately: only groups with quantized moments have it."""
+    cfg = upd.engine.cfg
+    wd = upd.weight_decay if upd.wd_nonzero else 0.0
+    return (_as_f32(cfg.b1).item(), _as_f32(cfg.b2).item(), _as_f32(cfg.eps).item(), _as_f32(cfg.eps_root).item(),
+            bool(cfg.nesterov), bool(cfg.exact), isinstance(wd, (int, float)))
+
+
+def _moment_sr(upd) -> Optional[bool]:
+    """adamw8(stochastic_rounding=...) of a group; None for optim/adam.py's
+    adamw, whose moments are never requantized."""
+    return bool(upd.engine.cfg.stochastic_rounding) if type(upd.engine) is _Engine else None
+
+
+class _GroupedRunner:
+    """One launch over several adamw8 / adamw transforms that each own a
+    disjoint subset of the leaves (optax.multi_transform with masked inner
+    transforms, finetune/builders.py:1529-1621).  Each leaf row carries its
+    group index; the per-group learning rate, weight decay, EMA weight and
+    moment keys travel in the launch's group table, the rest is shared."""
+
+    def __init__(self):
+        self._plans: dict = {}
+
+    @staticmethod
+    def compatible(updates_objs, adam_states) -> bool:
+        if not updates_objs or not all(isinstance(u, _Adamw8Update) for u in updates_objs):
+            return False
+        keys = {_group_key(u) for u in updates_objs}
+        srs = {_moment_sr(u) for u in updates_objs} - {None}
+        counts = {int(np.asarray(s.count)) for s in adam_states}
+        return len(keys) == 1 and len(srs) <= 1 and len(counts) == 1
+
+    def run(self, members, updates, params, *, apply: bool, param_key=None, param_sr=False, random_bits=None,
+            clip_global_norm=None, clip_stats=None, skip_nonfinite=False, finite_out=None, finite_host=None):
+        """``members``: list of (update object, chain state, per-leaf membership
+        list).  Returns (out leaves or None, list of new chain states)."""
+        torch = _torch()
+        g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
+        n = len(g_leaves)
+        p_leaves = _tree.flatten_up_to(g_td, params) if params is not None else None
+        masked = MaskedNode()
+        rows, structure, groups, new_states = [], [], [], []
+        out_leaves = [None] * n
+        device = None
+        for gi, (upd, state, member) in enumerate(members):
+            eng = upd.engine
+            adam_state, lr_state = state[0], state[-1]
+            neg_lr, new_lr_state = upd._lr(lr_state)
+            gm = [g_leaves[i] if member[i] else masked for i in range(n)]
+            pm = None if p_leaves is None else [p_leaves[i] if member[i] else masked for i in range(n)]
+            decay_mask = None
+            if upd.wd_nonzero:
+                if params is None:
+                    raise ValueError(NO_PARAMS_MSG)
+                decay_mask = _decay_mask_leaves(upd.weight_decay_mask, _tree.unflatten(g_td, pm), n)
+            mu_leaves = _tree.flatten_up_to(g_td, adam_state.mu) if n else []
+            nu_leaves = _tree.flatten_up_to(g_td, adam_state.nu) if n else []
+            grows, gstruct, _refs, gouts, gdev = eng._build_rows(gm, mu_leaves, nu_leaves, pm, apply=apply,
+                                                                 decay_mask=decay_mask, random_bits=random_bits)
+            if gdev is not None:
+                if device is not None and gdev != device:
+                    raise ValueError("all leaves must live on the same device")
+                device = gdev
+            for row in grows:
+                row.group = gi
+            rows.extend(grows)
+            structure.extend(s + (gi,) for s in gstruct)
+            for i in range(n):
+                if member[i]:
+                    out_leaves[i] = gouts[i]
+            key_mu, key_nu, next_key = eng.split_keys(adam_state.key)
+            grp = _lib.Adam8Group()
+            grp.neg_lr = neg_lr
+            grp.weight_decay = _as_f32(upd.weight_decay) if upd.wd_nonzero else np.float32(0.0)
+            grp.one_minus_b1 = eng.ema_weight(eng.cfg.b1)
+            grp.key_mu[0], grp.key_mu[1] = int(key_mu[0]), int(key_mu[1])
+            grp.key_nu[0], grp.key_nu[1] = int(key_nu[0]), int(key_nu[1])
+            groups.append(grp)
+            count_inc = safe_int32_increment(int(np.asarray(adam_state.count)))
+            new_states.append((eng.new_state(adam_state, count_inc, next_key),) + tuple(state[1:-1])
+                              + (new_lr_state,))
+        for i in range(n):
+            if out_leaves[i] is None:  # passthrough leaves and leaves of no group keep their update
+                out_leaves[i] = g_leaves[i]
+
+        upd0, state0, _ = members[0]
+        cfg = upd0.engine.cfg
+        flags = _lib.RF_LR
+        if cfg.nesterov:
+            flags |= _lib.RF_NESTEROV
+        if _group_key(upd0)[-1]:
+            flags |= _lib.RF_DECAY_WEAK
+        if any(_moment_sr(m[0]) for m in members):
+            flags |= _lib.RF_MOMENT_SR
+        if apply and param_sr:
+            flags |= _lib.RF_PARAM_SR
+        if cfg.exact:
+            flags |= _lib.RF_EXACT
+        if random_bits is not None:
+            flags |= _lib.RF_FED_BITS
+        if skip_nonfinite:
+            flags |= _lib.RF_SKIP_NONFINITE
+        count_inc = safe_int32_increment(int(np.asarray(state0[0].count)))
+        hp = _common_hparams(cfg, count_inc, flags, param_key, clip_global_norm, clip_stats, finite_out,
+                             finite_host)
+        if rows:
+            table = (_lib.Adam8Leaf * len(rows))(*rows)
+            gtab = (_lib.Adam8Group * len(groups))(*groups)
+            hp.groups = ctypes.cast(gtab, ctypes.c_void_p)
+            hp.n_groups = 1 + max(r.group for r in rows)
+            skey = (bool(apply), device.index, tuple(structure))
+            plan = self._plans.get(skey)
+            if plan is None:
+                with torch.cuda.device(device):
+                    plan = _LeafPlan(table, len(rows), apply)
+                if len(self._plans) > 16:
+                    self._plans.clear()
+                self._plans[skey] = plan
+            with torch.cuda.device(device):
+                plan.run(table, hp, _lib.stream_ptr())
+                if finite_host is not None:
+                    plan.wait_prepass()
+        return (out_leaves if not apply else None), g_td, new_states

@@ -38,26 +38,24 @@ class GlobalNormClipState(NamedTuple):
     count: Any
 
 
-def clip_by_global_norm(max_norm: float, *, axis_name=None, partition_axis_names=None,
-                        replicated_axis_names=None) -> GradientTransformation:
-    """Clip by global norm over the leaves (transforms.py:20-54): scale every
-    leaf by ``min(1, max_norm / (norm + 1e-6))`` in the leaf dtype.  The axis
-    arguments name collective axes of a multi-device reduction, which this
-    single-device build does not perform; they must be None."""
-    import torch
+def _next_clip_state(state) -> GlobalNormClipState:
+    """transforms.py:54: ``GlobalNormClipState(count=state.count + 1)``."""
+    return GlobalNormClipState(count=np.asarray(np.int32(int(np.asarray(state.count)) + 1), dtype=np.int32))
 
-    if max_norm <= 0.0:
-        raise ValueError("max_norm must be positive.")
-    if axis_name is not None or partition_axis_names is not None or replicated_axis_names is not None:
-        raise NotImplementedError("cross-device norm reduction is not part of this single-device build")
 
-    def init_fn(params):
-        del params
-        return GlobalNormClipState(count=np.zeros((), dtype=np.int32))
+class _ClipUpdate:
+    """``clip_by_global_norm(max_norm).update`` (transforms.py:36-54) as one
+    norm pre-pass and one scaling launch.  ``max_norm`` also lets the fused
+    optimizer steps recognise ``chain(clip_by_global_norm(m), tx)``."""
 
-    def update_fn(updates, state, params=None, stats=None):
+    def __init__(self, max_norm: float):
+        self.max_norm = max_norm
+
+    def __call__(self, updates, state, params=None, stats=None):
         """``stats`` (extension): optional float32 device tensor of 2 elements
         receiving (scale, norm)."""
+        import torch
+
         del params
         leaves, td = _tree.flatten(updates, is_leaf=lambda x: x is None)
         rows = []
@@ -92,13 +90,28 @@ def clip_by_global_norm(max_norm: float, *, axis_name=None, partition_axis_names
                     raise ValueError("stats must be a float32 device tensor of 2 elements")
                 stats_ptr = stats.data_ptr()
             with torch.cuda.device(device):
-                _lib.check(_lib.lib().rf_clip_by_global_norm(table, len(rows), ctypes.c_float(float(max_norm)),
+                _lib.check(_lib.lib().rf_clip_by_global_norm(table, len(rows), ctypes.c_float(self.max_norm),
                                                              ctypes.c_void_p(stats_ptr), _lib.stream_ptr()),
                            "clip_by_global_norm")
-        count = np.asarray(np.int32(int(np.asarray(state.count)) + 1), dtype=np.int32)
-        return _tree.unflatten(td, out), GlobalNormClipState(count=count)
+        return _tree.unflatten(td, out), _next_clip_state(state)
 
-    return GradientTransformation(init_fn, update_fn)
+
+def clip_by_global_norm(max_norm: float, *, axis_name=None, partition_axis_names=None,
+                        replicated_axis_names=None) -> GradientTransformation:
+    """Clip by global norm over the leaves (transforms.py:20-54): scale every
+    leaf by ``min(1, max_norm / (norm + 1e-6))`` in the leaf dtype.  The axis
+    arguments name collective axes of a multi-device reduction, which this
+    single-device build does not perform; they must be None."""
+    if max_norm <= 0.0:
+        raise ValueError("max_norm must be positive.")
+    if axis_name is not None or partition_axis_names is not None or replicated_axis_names is not None:
+        raise NotImplementedError("cross-device norm reduction is not part of this single-device build")
+
+    def init_fn(params):
+        del params
+        return GlobalNormClipState(count=np.zeros((), dtype=np.int32))
+
+    return GradientTransformation(init_fn, _ClipUpdate(float(max_norm)))
 
 
 class _ApplyIfFiniteUpdate:

@@ -217,6 +217,37 @@ def test_apply_if_finite_construction_and_state():
     # no CPU fallback behind the guard either
     with pytest.raises(ValueError, match="ROCm device"):
         tx.update({"w": torch.zeros(8)}, st, {"w": torch.zeros(8)})
+    txg = rf.apply_if_finite(rf.scale_by_adam8(), 1)
     with pytest.raises(TypeError, match="adamw8"):
-        rf.adamw8_step(rf.apply_if_finite(rf.scale_by_adam8(), 1), {"w": torch.zeros(8)}, {"w": torch.zeros(8)},
-                       None, stochastic=False)
+        rf.adamw8_step(txg, {"w": torch.zeros(8)}, {"w": torch.zeros(8)}, txg.init({"w": torch.zeros(8)}),
+                       stochastic=False)
+
+
+def test_optax_combinators_state_layout():
+    params = {"a": torch.zeros(8192), "b": torch.zeros(16), "c": torch.zeros(4)}
+    labels = {"a": "q", "b": "f", "c": "f"}
+    tx = rf.multi_transform({"q": rf.adamw8(1e-3), "f": rf.adamw(1e-3)}, labels)
+    st = tx.init(params)
+    assert isinstance(st, rf.MultiTransformState) and list(st.inner_states) == ["q", "f"]
+    q = st.inner_states["q"]
+    assert isinstance(q, rf.MaskedState)
+    assert isinstance(q.inner_state[0].mu["a"], rf.QuantizedBlocks)
+    assert isinstance(q.inner_state[0].mu["b"], rf.MaskedNode) and isinstance(q.inner_state[0].mu["c"], rf.MaskedNode)
+    f = st.inner_states["f"].inner_state[0]
+    assert isinstance(f, rf.ScaleByAdamState) and isinstance(f.mu["a"], rf.MaskedNode) and f.mu["b"].dtype == torch.float32
+    with pytest.raises(ValueError, match="no corresponding transformation"):
+        rf.multi_transform({"q": rf.adamw8(1e-3)}, labels).init(params)
+    # labels may be a callable of the params
+    st2 = rf.multi_transform({"q": rf.adamw8(1e-3), "f": rf.adamw(1e-3)}, lambda p: labels).init(params)
+    assert list(st2.inner_states) == ["q", "f"]
+    ch = rf.chain(rf.clip_by_global_norm(1.0), tx)
+    cst = ch.init(params)
+    assert isinstance(cst, tuple) and len(cst) == 2 and int(cst[0].count) == 0
+    m = rf.masked(rf.adamw8(1e-3), {"a": True, "b": False, "c": False}).init(params)
+    assert isinstance(m, rf.MaskedState) and isinstance(m.inner_state[0].mu["b"], rf.MaskedNode)
+    # no CPU fallback behind the combinators
+    with pytest.raises(ValueError, match="ROCm device"):
+        tx.update(params, st, params)
+    with pytest.raises(ValueError, match="ROCm device"):
+        rf.adamw8_step(rf.apply_if_finite(ch, 1), params, params, rf.apply_if_finite(ch, 1).init(params),
+                       stochastic=False)
