@@ -34,6 +34,7 @@ from .optim.adam8 import (
     tree_state_nbytes,
 )
 from .optim.adam import ScaleByAdamState, adamw, adamw_step, scale_by_adam
+from .optim.convert import adam8_state_from_adam, adam_state_from_adam8, dequantize_state_tree, quantize_state_tree
 from .combine import MultiTransformState, chain, masked, multi_transform
 from .transforms import GlobalNormClipState, apply_if_finite, clip_by_global_norm
 from .utils import apply_updates, apply_updates_prefix
@@ -56,6 +57,8 @@ __all__ = (
     "ScaleByAdam8State",
     "ScaleByAdamState",
     "ScaleByScheduleState",
+    "adam8_state_from_adam",
+    "adam_state_from_adam8",
     "adamw",
     "adamw8",
     "adamw8_step",
@@ -66,11 +69,13 @@ __all__ = (
     "chain",
     "clip_by_global_norm",
     "dequantize_blocks",
+    "dequantize_state_tree",
     "estimate_quantized_moment_bytes",
     "masked",
     "multi_transform",
     "prng",
     "quantize_blocks",
+    "quantize_state_tree",
     "quantized_nbytes",
     "scale_by_adam",
     "scale_by_adam8",

@@ -251,3 +251,13 @@ def test_optax_combinators_state_layout():
     with pytest.raises(ValueError, match="ROCm device"):
         rf.adamw8_step(rf.apply_if_finite(ch, 1), params, params, rf.apply_if_finite(ch, 1).init(params),
                        stochastic=False)
+
+
+def test_state_conversions_refuse_host_tensors():
+    st = rf.adamw8(1e-3).init({"w": torch.zeros(8192), "b": torch.zeros(4)})[0]
+    with pytest.raises(ValueError, match="ROCm device"):
+        rf.dequantize_state_tree(st.mu)
+    with pytest.raises(ValueError, match="PRNG key"):
+        rf.quantize_state_tree({"w": torch.zeros(8192), "b": torch.zeros(4)}, st.mu, stochastic_rounding=True)
+    with pytest.raises(ValueError, match="ROCm device"):
+        rf.quantize_state_tree({"w": torch.zeros(8192), "b": torch.zeros(4)}, st.mu)
