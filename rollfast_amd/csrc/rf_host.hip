@@ -336,6 +336,9 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
 // scale = min(1, max_norm / (norm + 1e-6)) with NaN propagating.
 constexpr int64_t NORM_UNIT = 16384;
 
+// Work units (blocks or chunks) per wave of a step launch (see plan_launch).
+constexpr int64_t STEP_UNITS_PER_WAVE = 16;
+
 __device__ __forceinline__ double wave_sum_f64(double x)
 {
 #pragma unroll
@@ -1089,9 +1092,15 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         int occ = 1;
         st = occupancy((const void*)fn, &occ);
         if (st != RF_OK) return st;
+        // About STEP_UNITS_PER_WAVE units per wave, never fewer workgroups
+        // than fit on the chip at once.  On the Llama-7B tree this measured
+        // 3-5 % faster than one persistent grid (8 to 32 units per wave
+        // within noise of each other); one unit per wave is 26 % slower
+        // (the lookup tables are staged per workgroup).
         const int64_t wg_needed = (g.units + WAVES_PER_WG - 1) / WAVES_PER_WG;
         const int64_t wg_resident = (int64_t)ds->num_cus * occ;
-        const int grid = (int)std::max<int64_t>(1, std::min(wg_needed, wg_resident));
+        const int64_t wg_spread = (wg_needed + STEP_UNITS_PER_WAVE - 1) / STEP_UNITS_PER_WAVE;
+        const int grid = (int)std::max<int64_t>(1, std::max(std::min(wg_needed, wg_resident), wg_spread));
         hipLaunchKernelGGL(fn, dim3(grid), dim3(WG), 0, (hipStream_t)stream, d_leaves, plan->d_segs + g.seg_offset,
                            g.units, k, ds->tables);
         HIP_TRY(hipGetLastError());
@@ -1258,8 +1267,10 @@ rf_status rf_blockwise_quantize(int32_t quantizer, const float* x, int64_t size,
     int occ = 1;
     st = occupancy((const void*)&k_quantize, &occ);
     if (st != RF_OK) return st;
+    // One wave per block, about STEP_UNITS_PER_WAVE blocks per wave (as the step).
     const int64_t wg_needed = (nb + WAVES_PER_WG - 1) / WAVES_PER_WG;
-    const int grid = (int)std::max<int64_t>(1, std::min(wg_needed, (int64_t)ds->num_cus * occ));
+    const int64_t wg_spread = (wg_needed + STEP_UNITS_PER_WAVE - 1) / STEP_UNITS_PER_WAVE;
+    const int grid = (int)std::max<int64_t>(1, std::max(std::min(wg_needed, (int64_t)ds->num_cus * occ), wg_spread));
     const int32_t vec_ok = aligned(x, 16) && aligned(values, 8) && (!bits || aligned(bits, 16));
     hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(WG), 0, (hipStream_t)stream, quantizer, x, size,
                        (int64_t)block_size, nb, sr, key0, key1, bits, (uint8_t*)values, scales, ds->tables, vec_ok);
