@@ -1,7 +1,9 @@
 """GPU parity at the benchmark configurations' real shapes.
 
 * GPT-2-small bf16 tree (74 leaves, LayerNorms on f32 fallback moments),
-  param stochastic rounding with in-kernel Threefry bits, 2 steps.
+  param stochastic rounding with in-kernel Threefry bits, 2 steps; and the
+  configuration's 100 steps, three leaves following their own oracle
+  trajectory bit for bit (IEEE direction).
 * The ragged tree (2256 leaves, most below min_size; Student-t(3) grads with
   log-uniform per-leaf scales and 10 % all-zero blocks), 2 steps.
 * Full-size Llama-7B leaves (embedding 32000x4096 and one decoder layer:
@@ -111,6 +113,64 @@ def _tree_run(kind, grads_kind, steps, psr):
 
 def test_gpt2_small_full_tree_param_sr():
     _tree_run("gpt2", "normal", steps=2, psr=True)
+
+
+def test_gpt2_small_100_steps_param_sr_trajectory():
+    """The GPT-2-small configuration as specified: 100 steps with bf16 param
+    stochastic rounding on (in-kernel Threefry bits), the whole tree on the
+    GPU.  Three leaves (a 768x2304 matrix, a LayerNorm on f32 fallback
+    moments, the final LayerNorm) follow their own oracle trajectory for all
+    100 steps, never resynchronised: with the IEEE direction (``exact``)
+    params, codes and scales stay bit-identical."""
+    import torch
+
+    import rollfast_amd as rf
+
+    shapes = _shapes("gpt2")
+    names = [n for n, _ in shapes]
+    watch = [names.index("h00.qkv"), names.index("h11.ln2"), names.index("ln_f")]
+    flat = sorted(names)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    params = {n: (torch.randn(s, generator=gen, device="cuda") * 0.02).to(torch.bfloat16) for n, s in shapes}
+    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=True)
+    state = tx.init(params)
+    leaves = []
+    for i in watch:
+        n, s = shapes[i]
+        m, v = state[0].mu[n], state[0].nu[n]
+        L = {"pdtype": "bf16", "gdtype": "bf16", "size": int(np.prod(s)), "param": to_host(params[n]).copy()}
+        if isinstance(m, rf.QuantizedBlocks):
+            L.update(kind="quant", block_size=2048, mu=to_host(m.values).copy(), mu_scales=to_host(m.scales).copy(),
+                     nu=to_host(v.values).copy(), nu_scales=to_host(v.scales).copy())
+        else:
+            L.update(kind="f32", mu=to_host(m).copy(), nu=to_host(v).copy())
+        leaves.append(L)
+    assert [L["kind"] for L in leaves] == ["quant", "f32", "f32"]
+    tree = OracleTree(leaves)
+    for step in range(100):
+        grads = {n: (torch.randn(s, generator=gen, device="cuda") * 1e-3).to(torch.bfloat16) for n, s in shapes}
+        key = rf.prng.PRNGKey(5000 + step)
+        kp = orc.split(tuple(int(k) for k in key), len(shapes))
+        # a dict flattens in sorted key order: that position indexes the key split
+        p_bits = [orc.random_bits(tuple(kp[flat.index(names[i])]), leaves[j]["size"]) for j, i in enumerate(watch)]
+        tree.step([to_host(grads[names[i]]) for i in watch], weight_decay=0.01, lr=1e-3, count=step + 1,
+                  param_sr=True, p_bits=p_bits)
+        params, state = rf.adamw8_step(tx, params, grads, state, key=key, stochastic=True)
+    torch.cuda.synchronize()
+    assert int(state[0].count) == 100
+    for j, i in enumerate(watch):
+        n, L = names[i], leaves[j]
+        np.testing.assert_array_equal(to_host(params[n]), L["param"], err_msg=f"{n} params after 100 steps")
+        m, v = state[0].mu[n], state[0].nu[n]
+        if L["kind"] == "quant":
+            np.testing.assert_array_equal(to_host(m.values), L["mu"])
+            np.testing.assert_array_equal(to_host(v.values), L["nu"])
+            np.testing.assert_array_equal(to_host(m.scales).view(np.uint32), L["mu_scales"].view(np.uint32))
+            np.testing.assert_array_equal(to_host(v.scales).view(np.uint32), L["nu_scales"].view(np.uint32))
+        else:
+            np.testing.assert_array_equal(to_host(m).view(np.uint32), L["mu"].view(np.uint32))
+            np.testing.assert_array_equal(to_host(v).view(np.uint32), L["nu"].view(np.uint32))
 
 
 def test_ragged_tree_student_t_zero_blocks():
