@@ -183,6 +183,31 @@ def lib() -> ctypes.CDLL:
     return L
 
 
+_pyhost = None
+
+
+def pyhost():
+    """The native host fast-path module ``_rfhost`` (built with the library
+    by ``rollfast_amd.build``); raises if it is not built."""
+    global _pyhost
+    if _pyhost is not None:
+        return _pyhost
+    import importlib.util
+    import sysconfig
+
+    from ._base import MaskedNode
+
+    path = os.path.join(os.path.dirname(LIB_PATH), "_rfhost" + sysconfig.get_config_var("EXT_SUFFIX"))
+    if not os.path.exists(path):
+        raise LibraryMissing(f"{path} is not built; run `python -m rollfast_amd.build` first")
+    spec = importlib.util.spec_from_file_location("rollfast_amd._lib._rfhost", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    mod.set_masked_node_type(MaskedNode)
+    _pyhost = mod
+    return mod
+
+
 def check(status: int, what: str) -> None:
     """Map an rf_status to the reference's exception types."""
     if status == RF_OK:

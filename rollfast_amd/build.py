@@ -1,7 +1,9 @@
-"""Build recipe for the gfx950 shared library ``rollfast_amd/_lib/librfadam8.so``.
+"""Build recipe for the gfx950 shared library ``rollfast_amd/_lib/librfadam8.so``
+and the host fast-path module ``rollfast_amd/_lib/_rfhost*.so``.
 
-The library is built in-tree with ``hipcc`` (cross-compiles without a GPU)
-so the ``.so`` travels with the source tree to the machine that runs it.
+Both are built in-tree (``hipcc`` cross-compiles without a GPU; the module
+with ``g++`` against torch's headers) so they travel with the source tree to
+the machine that runs them.
 """
 
 from __future__ import annotations
@@ -18,6 +20,9 @@ LIB_NAME = "librfadam8.so"
 LIB_PATH = os.path.join(OUT_DIR, LIB_NAME)
 OBJ_DIR = os.path.join(HERE, "_lib", "obj")
 HOST_SRC = os.path.join(CSRC, "rf_host.hip")
+# The native host fast path of the fused step: a CPython module built against
+# torch's C++ headers (tensor data pointers without a Python call).
+PYHOST_SRC = os.path.join(CSRC, "rf_pyhost.cpp")
 INST_SRC = os.path.join(CSRC, "rf_adam8_inst.hip")
 # One object per (apply, moment SR, exact) instance of the step kernel.
 VARIANTS = [(a, m, e) for a in (0, 1) for m in (0, 1) for e in (0, 1)]
@@ -52,12 +57,37 @@ def _compile_jobs():
     return jobs
 
 
+def pyhost_path() -> str:
+    import sysconfig
+
+    return os.path.join(OUT_DIR, "_rfhost" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _pyhost_job():
+    """g++ command for the host fast-path module (compiled and linked at once)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    inc = [f"-I{d}" for d in cpp_extension.include_paths()] + [f"-I{sysconfig.get_paths()['include']}",
+                                                               f"-I{os.path.join(REPO, 'include')}"]
+    libdirs = cpp_extension.library_paths()
+    libs = [f"-L{d}" for d in libdirs] + [f"-Wl,-rpath,{d}" for d in libdirs]
+    out = pyhost_path() + ".tmp"
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", *inc, PYHOST_SRC, "-o", out, *libs,
+           "-ltorch_python", "-ltorch", "-lc10"]
+    return cmd, out
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> str:
     """Compile the HIP library (objects in parallel, then link); returns
     the path of the built ``.so``."""
     os.makedirs(OBJ_DIR, exist_ok=True)
     max_par = jobs or min(len(VARIANTS) + 1, max(1, os.cpu_count() or 1))
-    pending = _compile_jobs()
+    pending = [_pyhost_job()] + _compile_jobs()
     running = []
     failures = []
     while pending or running:
@@ -73,7 +103,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     if failures:
         for obj, out in failures:
             sys.stderr.write(f"--- {obj}\n{out}\n")
-        raise RuntimeError(f"hipcc failed for {len(failures)} object(s)")
+        raise RuntimeError(f"compilation failed for {len(failures)} object(s)")
+    os.replace(pyhost_path() + ".tmp", pyhost_path())
     tmp = LIB_PATH + ".tmp"
     objs = [obj for _, obj in _compile_jobs()]
     link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]

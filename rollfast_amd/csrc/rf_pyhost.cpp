@@ -1,0 +1,239 @@
+// rf_pyhost.cpp -- native host fast path of the fused step (CPython module
+// rollfast_amd._lib._rfhost).
+//
+// A fused step over a tree whose structure, params and moment objects are
+// those of the previous step only needs new grad pointers in the leaf table.
+// Doing that in Python costs about 1.6 us per leaf (pytree walks, weakref and
+// pointer checks); here it is one joint walk of the four trees and one pass
+// over the cached rows, in C++.
+//
+//   gather(grads, mu, nu, params) -> (g, mu, nu, p) leaf lists, or None
+//       Joint walk in the flattening order of rollfast_amd._tree (dicts by
+//       sorted keys, lists and tuples in order; None and MaskedNode are
+//       leaves of the grads tree).  mu / nu / params are taken as they are
+//       at each grads leaf.  Returns None (the caller falls back to the
+//       Python walk) for any container it does not handle or any mismatch.
+//
+//   refresh(g, mu, nu, p, rows, table_address, device) -> bool
+//       rows[j] = (i, mref, vref, pref, bufrefs, bufptrs, grad_dtype, size, vec)
+//       Checks that leaf i's moment and param objects are the cached ones
+//       (weak references), that their buffers still have the cached device
+//       pointers, and that grad i is a contiguous tensor of the cached dtype,
+//       size and device (16-byte aligned when the row was); then writes its
+//       pointer into row j of the rf_adam8_leaf table at table_address.
+//       Returns False at the first difference (the table may then be partly
+//       rewritten: the caller rebuilds it).
+#include <Python.h>
+
+#include <torch/csrc/autograd/python_variable.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "rfadam8.h"
+
+namespace {
+
+PyObject* g_masked_node_type = nullptr;  // rollfast_amd._base.MaskedNode
+
+bool is_grad_leaf(PyObject* x)
+{
+    return x == Py_None || THPVariable_Check(x) ||
+           (g_masked_node_type && PyObject_TypeCheck(x, (PyTypeObject*)g_masked_node_type));
+}
+
+// Appends the grads leaves and the other trees' subtrees at those positions.
+// Returns 1 on success, 0 for "not handled here" (no Python error set), -1 on
+// a Python error.
+int walk(PyObject* g, PyObject* m, PyObject* v, PyObject* p, PyObject* lg, PyObject* lm, PyObject* lv, PyObject* lp)
+{
+    if (is_grad_leaf(g)) {
+        if (PyList_Append(lg, g) || PyList_Append(lm, m) || PyList_Append(lv, v)) return -1;
+        if (lp && PyList_Append(lp, p)) return -1;
+        return 1;
+    }
+    if (PyDict_CheckExact(g)) {
+        if (!PyDict_CheckExact(m) || !PyDict_CheckExact(v) || (lp && !PyDict_CheckExact(p))) return 0;
+        const Py_ssize_t n = PyDict_Size(g);
+        if (PyDict_Size(m) != n || PyDict_Size(v) != n || (lp && PyDict_Size(p) != n)) return 0;
+        PyObject* keys = PyDict_Keys(g);
+        if (!keys) return -1;
+        if (PyList_Sort(keys) < 0) {  // keys that do not sort: leave it to the Python walk
+            Py_DECREF(keys);
+            PyErr_Clear();
+            return 0;
+        }
+        int rc = 1;
+        for (Py_ssize_t k = 0; k < n && rc == 1; ++k) {
+            PyObject* key = PyList_GET_ITEM(keys, k);
+            PyObject* cg = PyDict_GetItemWithError(g, key);
+            PyObject* cm = cg ? PyDict_GetItemWithError(m, key) : nullptr;
+            PyObject* cv = cm ? PyDict_GetItemWithError(v, key) : nullptr;
+            PyObject* cp = (cv && lp) ? PyDict_GetItemWithError(p, key) : nullptr;
+            if (!cg || !cm || !cv || (lp && !cp)) {
+                rc = PyErr_Occurred() ? -1 : 0;
+                break;
+            }
+            rc = walk(cg, cm, cv, cp, lg, lm, lv, lp);
+        }
+        Py_DECREF(keys);
+        return rc;
+    }
+    const bool is_list = PyList_CheckExact(g), is_tuple = PyTuple_CheckExact(g);
+    if (is_list || is_tuple) {
+        auto same = [&](PyObject* x) { return is_list ? PyList_CheckExact(x) : PyTuple_CheckExact(x); };
+        if (!same(m) || !same(v) || (lp && !same(p))) return 0;
+        const Py_ssize_t n = PySequence_Fast_GET_SIZE(g);
+        if (PySequence_Fast_GET_SIZE(m) != n || PySequence_Fast_GET_SIZE(v) != n ||
+            (lp && PySequence_Fast_GET_SIZE(p) != n))
+            return 0;
+        for (Py_ssize_t k = 0; k < n; ++k) {
+            const int rc = walk(PySequence_Fast_GET_ITEM(g, k), PySequence_Fast_GET_ITEM(m, k),
+                                PySequence_Fast_GET_ITEM(v, k), lp ? PySequence_Fast_GET_ITEM(p, k) : nullptr, lg,
+                                lm, lv, lp);
+            if (rc != 1) return rc;
+        }
+        return 1;
+    }
+    return 0;  // custom nodes, namedtuples, OrderedDicts: the Python walk
+}
+
+PyObject* py_gather(PyObject*, PyObject* args)
+{
+    PyObject *g, *m, *v, *p;
+    if (!PyArg_ParseTuple(args, "OOOO", &g, &m, &v, &p)) return nullptr;
+    const bool has_p = p != Py_None;
+    PyObject* lg = PyList_New(0);
+    PyObject* lm = PyList_New(0);
+    PyObject* lv = PyList_New(0);
+    PyObject* lp = has_p ? PyList_New(0) : nullptr;
+    PyObject* out = nullptr;
+    if (lg && lm && lv && (!has_p || lp)) {
+        const int rc = walk(g, m, v, has_p ? p : nullptr, lg, lm, lv, lp);
+        if (rc == 1) {
+            out = PyTuple_Pack(4, lg, lm, lv, has_p ? lp : Py_None);
+        } else if (rc == 0) {
+            out = Py_None;
+            Py_INCREF(out);
+        }
+    }
+    Py_XDECREF(lg);
+    Py_XDECREF(lm);
+    Py_XDECREF(lv);
+    Py_XDECREF(lp);
+    return out;
+}
+
+// The live object behind a weak reference, or nullptr (borrowed).
+PyObject* deref(PyObject* ref)
+{
+    if (ref == Py_None) return nullptr;
+    PyObject* o = PyWeakref_GetObject(ref);
+    return o == Py_None ? nullptr : o;
+}
+
+bool tensor_ptr(PyObject* o, uintptr_t* out)
+{
+    if (!o || !THPVariable_Check(o)) return false;
+    *out = (uintptr_t)THPVariable_Unpack(o).data_ptr();
+    return true;
+}
+
+PyObject* py_refresh(PyObject*, PyObject* args)
+{
+    PyObject *lg, *lm, *lv, *lp, *rows;
+    unsigned long long table_addr = 0;
+    int device = 0;
+    if (!PyArg_ParseTuple(args, "O!O!O!OO!Ki", &PyList_Type, &lg, &PyList_Type, &lm, &PyList_Type, &lv, &lp,
+                          &PyList_Type, &rows, &table_addr, &device))
+        return nullptr;
+    if (lp != Py_None && !PyList_Check(lp)) {
+        PyErr_SetString(PyExc_TypeError, "params leaves must be a list or None");
+        return nullptr;
+    }
+    const Py_ssize_t n = PyList_GET_SIZE(lg);
+    if (PyList_GET_SIZE(lm) != n || PyList_GET_SIZE(lv) != n || (lp != Py_None && PyList_GET_SIZE(lp) != n))
+        Py_RETURN_FALSE;
+    auto* table = (rf_adam8_leaf*)(uintptr_t)table_addr;
+    const Py_ssize_t nrows = PyList_GET_SIZE(rows);
+    Py_ssize_t live = 0;  // leaves that are neither passthrough in mu nor in the grads
+    for (Py_ssize_t i = 0; i < n; ++i) {
+        PyObject* g = PyList_GET_ITEM(lg, i);
+        PyObject* m = PyList_GET_ITEM(lm, i);
+        const bool pass = g == Py_None || m == Py_None ||
+                          (g_masked_node_type && (PyObject_TypeCheck(g, (PyTypeObject*)g_masked_node_type) ||
+                                                  PyObject_TypeCheck(m, (PyTypeObject*)g_masked_node_type)));
+        live += pass ? 0 : 1;
+    }
+    if (live != nrows) Py_RETURN_FALSE;
+    for (Py_ssize_t j = 0; j < nrows; ++j) {
+        PyObject* row = PyList_GET_ITEM(rows, j);
+        if (!PyTuple_Check(row) || PyTuple_GET_SIZE(row) != 9) {
+            PyErr_SetString(PyExc_TypeError, "bad row record");
+            return nullptr;
+        }
+        const Py_ssize_t i = PyLong_AsSsize_t(PyTuple_GET_ITEM(row, 0));
+        if (i < 0 || i >= n) {
+            if (PyErr_Occurred()) return nullptr;
+            Py_RETURN_FALSE;
+        }
+        PyObject* m = PyList_GET_ITEM(lm, i);
+        PyObject* v = PyList_GET_ITEM(lv, i);
+        if (deref(PyTuple_GET_ITEM(row, 1)) != m || deref(PyTuple_GET_ITEM(row, 2)) != v) Py_RETURN_FALSE;
+        PyObject* pref = PyTuple_GET_ITEM(row, 3);
+        if (pref != Py_None && (lp == Py_None || deref(pref) != PyList_GET_ITEM(lp, i))) Py_RETURN_FALSE;
+        // same objects, same storage (a `.data` swap changes the pointer)
+        PyObject* bufrefs = PyTuple_GET_ITEM(row, 4);
+        PyObject* bufptrs = PyTuple_GET_ITEM(row, 5);
+        const Py_ssize_t nb = PyTuple_GET_SIZE(bufrefs);
+        if (PyTuple_GET_SIZE(bufptrs) != nb) Py_RETURN_FALSE;
+        for (Py_ssize_t b = 0; b < nb; ++b) {
+            uintptr_t ptr = 0;
+            if (!tensor_ptr(deref(PyTuple_GET_ITEM(bufrefs, b)), &ptr)) Py_RETURN_FALSE;
+            if ((unsigned long long)ptr != PyLong_AsUnsignedLongLong(PyTuple_GET_ITEM(bufptrs, b))) {
+                if (PyErr_Occurred()) return nullptr;
+                Py_RETURN_FALSE;
+            }
+        }
+        PyObject* g = PyList_GET_ITEM(lg, i);
+        if (!THPVariable_Check(g)) Py_RETURN_FALSE;
+        const at::Tensor& t = THPVariable_Unpack(g);
+        const long want_dtype = PyLong_AsLong(PyTuple_GET_ITEM(row, 6));
+        const long long want_size = PyLong_AsLongLong(PyTuple_GET_ITEM(row, 7));
+        const int vec = PyObject_IsTrue(PyTuple_GET_ITEM(row, 8));
+        if (PyErr_Occurred()) return nullptr;
+        const at::ScalarType st = t.scalar_type();
+        const bool dtype_ok = (want_dtype == RF_F32 && st == at::kFloat) || (want_dtype == RF_BF16 && st == at::kBFloat16);
+        if (!dtype_ok || !t.is_cuda() || t.get_device() != device || t.numel() != want_size || !t.is_contiguous())
+            Py_RETURN_FALSE;
+        const uintptr_t gp = (uintptr_t)t.data_ptr();
+        if (vec && (gp & 15u)) Py_RETURN_FALSE;
+        table[j].grad = (const void*)gp;
+    }
+    Py_RETURN_TRUE;
+}
+
+PyObject* py_set_masked_node_type(PyObject*, PyObject* t)
+{
+    if (!PyType_Check(t)) {
+        PyErr_SetString(PyExc_TypeError, "expected a type");
+        return nullptr;
+    }
+    Py_XDECREF(g_masked_node_type);
+    Py_INCREF(t);
+    g_masked_node_type = t;
+    Py_RETURN_NONE;
+}
+
+PyMethodDef methods[] = {
+    {"gather", py_gather, METH_VARARGS, "joint walk of (grads, mu, nu, params); None if not handled"},
+    {"refresh", py_refresh, METH_VARARGS, "rewrite the grad pointers of a cached leaf table; False on a mismatch"},
+    {"set_masked_node_type", py_set_masked_node_type, METH_O, "the MaskedNode class (a grads leaf)"},
+    {nullptr, nullptr, 0, nullptr},
+};
+
+PyModuleDef module = {PyModuleDef_HEAD_INIT, "_rfhost", "native host fast path of the fused step", -1, methods};
+
+}  // namespace
+
+PyMODINIT_FUNC PyInit__rfhost(void) { return PyModule_Create(&module); }

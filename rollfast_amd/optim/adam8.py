@@ -461,13 +461,32 @@ def _aligned(t, a: int) -> bool:
     return t is None or t.data_ptr() % a == 0
 
 
+class _AllLeaves:
+    """Decay mask of every leaf (``weight_decay_mask=None``): it needs no
+    per-leaf list, so the steady-state step does not walk the tree for it."""
+
+    def __getitem__(self, i) -> bool:
+        return True
+
+    def __repr__(self) -> str:
+        return "ALL_LEAVES"
+
+
+ALL_LEAVES = _AllLeaves()
+
+
+def _buffers(m, v, p) -> tuple:
+    """A leaf's moment buffers and param tensors."""
+    if isinstance(m, QuantizedBlocks):
+        t = (m.values, m.scales, v.values, v.scales)
+    else:
+        t = (m, v)
+    return t + ((p,) if p is not None else ())
+
+
 def _buffer_ptrs(m, v, p) -> tuple:
     """Device addresses of a leaf's moment buffers and param."""
-    if isinstance(m, QuantizedBlocks):
-        t = (m.values.data_ptr(), m.scales.data_ptr(), v.values.data_ptr(), v.scales.data_ptr())
-    else:
-        t = (m.data_ptr(), v.data_ptr())
-    return t + ((p.data_ptr(),) if p is not None else ())
+    return tuple(t.data_ptr() for t in _buffers(m, v, p))
 
 
 class _Engine:
@@ -513,6 +532,9 @@ class _Engine:
         out_leaves: list = [None] * n
         rows = []
         structure = []
+        # per row: (leaf index, weakrefs of mu, nu, param, weakrefs of the
+        # buffer tensors, their device pointers, grad dtype code, size,
+        # 16-byte aligned) -- the record rf_pyhost.cpp's refresh() reads
         refs = []
         device = None
         for i in range(n):
@@ -616,8 +638,10 @@ class _Engine:
             rows.append(row)
             structure.append((size, row.block_size, row.param_dtype, gdt, row.moment_kind, i, row.flags, align_ok,
                               row.mu_bits is not None or row.nu_bits is not None, row.param_bits is not None))
+            bufs = _buffers(m, v, p)
             refs.append((i, weakref.ref(m), weakref.ref(v), None if p is None else weakref.ref(p),
-                         g.dtype, size, align_ok, _buffer_ptrs(m, v, p)))
+                         tuple(weakref.ref(t) for t in bufs), tuple(t.data_ptr() for t in bufs), gdt, size,
+                         align_ok))
         return rows, structure, refs, out_leaves, device
 
     # -- cached table (same objects as the previous call) -------------------
@@ -636,7 +660,9 @@ class _Engine:
         if len(refs) != sum(1 for i in range(n) if not (_is_passthrough_leaf(mu_leaves[i])
                                                         or _is_passthrough_leaf(g_leaves[i]))):
             return None
-        for j, (i, mref, vref, pref, gdtype, size, align_ok, ptrs) in enumerate(refs):
+        gdtypes = (torch.float32, torch.bfloat16)  # by RF_F32 / RF_BF16
+        for j, (i, mref, vref, pref, _bufrefs, ptrs, gdt, size, align_ok) in enumerate(refs):
+            gdtype = gdtypes[gdt]
             g, m, v = g_leaves[i], mu_leaves[i], nu_leaves[i]
             if mref() is not m or vref() is not v:
                 return None
@@ -667,68 +693,13 @@ class _Engine:
                 out_leaves[i] = m if _is_passthrough_leaf(m) else g
         return out_leaves
 
-    def run(
-        self,
-        updates,
-        state: ScaleByAdam8State,
-        params,
-        *,
-        apply: bool,
-        decay_mask: Optional[list],
-        weight_decay,
-        neg_lr: Optional[np.float32],
-        param_key=None,
-        param_sr: bool = False,
-        random_bits: Optional[dict] = None,
-        clip_global_norm: Optional[float] = None,
-        clip_stats=None,
-        skip_nonfinite: bool = False,
-        finite_out=None,
-        finite_host=None,
-    ):
+    def _launch(self, table, n_rows, device, plan, count_inc, key_mu, key_nu, *, apply, decay_mask,
+                weight_decay, neg_lr, param_key, param_sr, random_bits, clip_global_norm, clip_stats,
+                skip_nonfinite, finite_out, finite_host):
+        """Scalars of the step (adam8.py:322-339 and the optax chain) and the
+        plan launch over ``table``."""
         torch = _torch()
         cfg = self.cfg
-        key_mu, key_nu, next_key = self.split_keys(state.key)
-        count_inc = safe_int32_increment(int(np.asarray(state.count)))
-
-        g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
-        mu_leaves = _tree.flatten_up_to(g_td, state.mu) if g_td.num_leaves else []
-        nu_leaves = _tree.flatten_up_to(g_td, state.nu) if g_td.num_leaves else []
-        p_leaves = None
-        if params is not None:
-            p_leaves = _tree.flatten_up_to(g_td, params)
-
-        mask_key = None if decay_mask is None else tuple(decay_mask)
-        last = self._last
-        out_leaves = None
-        if (last is not None and random_bits is None and last["apply"] == apply and last["mask"] == mask_key
-                and last["td"] == g_td):
-            out_leaves = self._reuse_rows(last, g_leaves, mu_leaves, nu_leaves, p_leaves, apply)
-        if out_leaves is not None:
-            table, n_rows, device, plan = last["table"], last["n"], last["device"], last["plan"]
-        else:
-            self._last = None
-            if len(_tree.leaves(state.mu, is_leaf=_is_state_leaf)) != len(g_leaves):
-                raise ValueError("updates and optimizer state have different tree structures")
-            rows, structure, refs, out_leaves, device = self._build_rows(
-                g_leaves, mu_leaves, nu_leaves, p_leaves, apply=apply, decay_mask=decay_mask,
-                random_bits=random_bits)
-            n_rows = len(rows)
-            table = (_lib.Adam8Leaf * n_rows)(*rows) if rows else None
-            plan = None
-            if rows:
-                skey = (bool(apply), device.index, tuple(structure))
-                plan = self._plans.get(skey)
-                if plan is None:
-                    with torch.cuda.device(device):
-                        plan = _LeafPlan(table, n_rows, apply)
-                    if len(self._plans) > 64:
-                        self._plans.clear()
-                    self._plans[skey] = plan
-                if random_bits is None:
-                    self._last = {"apply": apply, "mask": mask_key, "td": g_td, "refs": refs, "table": table,
-                                  "n": n_rows, "device": device, "plan": plan}
-
         flags = 0
         if cfg.nesterov:
             flags |= _lib.RF_NESTEROV
@@ -760,6 +731,92 @@ class _Engine:
                 plan.run(table, hp, _lib.stream_ptr())
                 if finite_host is not None:
                     plan.wait_prepass()
+
+    def run(
+        self,
+        updates,
+        state: ScaleByAdam8State,
+        params,
+        *,
+        apply: bool,
+        decay_mask: Optional[list],
+        weight_decay,
+        neg_lr: Optional[np.float32],
+        param_key=None,
+        param_sr: bool = False,
+        random_bits: Optional[dict] = None,
+        clip_global_norm: Optional[float] = None,
+        clip_stats=None,
+        skip_nonfinite: bool = False,
+        finite_out=None,
+        finite_host=None,
+    ):
+        torch = _torch()
+        cfg = self.cfg
+        key_mu, key_nu, next_key = self.split_keys(state.key)
+        count_inc = safe_int32_increment(int(np.asarray(state.count)))
+
+        # Steady state of the fused step (same tree, params and moment objects
+        # as the previous call): the native fast path walks the four trees
+        # and rewrites the grad pointers of the cached table.
+        last = self._last
+        if (apply and last is not None and random_bits is None and last["apply"] and last["n"]
+                and last["mask"] == (decay_mask if decay_mask is None or decay_mask is ALL_LEAVES
+                                     else tuple(decay_mask))):
+            host = _lib.pyhost()
+            lists = host.gather(updates, state.mu, state.nu, params)
+            if lists is not None and host.refresh(*lists, last["refs"], ctypes.addressof(last["table"]),
+                                                  last["device"].index):
+                self._launch(last["table"], last["n"], last["device"], last["plan"], count_inc, key_mu, key_nu,
+                             apply=True, decay_mask=decay_mask, weight_decay=weight_decay, neg_lr=neg_lr,
+                             param_key=param_key, param_sr=param_sr, random_bits=None,
+                             clip_global_norm=clip_global_norm, clip_stats=clip_stats,
+                             skip_nonfinite=skip_nonfinite, finite_out=finite_out, finite_host=finite_host)
+                return None, self.new_state(state, count_inc, next_key)
+
+        g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
+        mu_leaves = _tree.flatten_up_to(g_td, state.mu) if g_td.num_leaves else []
+        nu_leaves = _tree.flatten_up_to(g_td, state.nu) if g_td.num_leaves else []
+        p_leaves = None
+        if params is not None:
+            p_leaves = _tree.flatten_up_to(g_td, params)
+
+        mask_key = decay_mask if decay_mask is None or decay_mask is ALL_LEAVES else tuple(decay_mask)
+        last = self._last
+        out_leaves = None
+        if (last is not None and random_bits is None and last["apply"] == apply and last["mask"] == mask_key
+                and last["td"] == g_td):
+            out_leaves = self._reuse_rows(last, g_leaves, mu_leaves, nu_leaves, p_leaves, apply)
+        if out_leaves is not None:
+            table, n_rows, device, plan = last["table"], last["n"], last["device"], last["plan"]
+        else:
+            self._last = None
+            if len(_tree.leaves(state.mu, is_leaf=_is_state_leaf)) != len(g_leaves):
+                raise ValueError("updates and optimizer state have different tree structures")
+            rows, structure, refs, out_leaves, device = self._build_rows(
+                g_leaves, mu_leaves, nu_leaves, p_leaves, apply=apply, decay_mask=decay_mask,
+                random_bits=random_bits)
+            n_rows = len(rows)
+            table = (_lib.Adam8Leaf * n_rows)(*rows) if rows else None
+            plan = None
+            if rows:
+                skey = (bool(apply), device.index, tuple(structure))
+                plan = self._plans.get(skey)
+                if plan is None:
+                    with torch.cuda.device(device):
+                        plan = _LeafPlan(table, n_rows, apply)
+                    if len(self._plans) > 64:
+                        self._plans.clear()
+                    self._plans[skey] = plan
+                if random_bits is None:
+                    self._last = {"apply": apply, "mask": mask_key, "td": g_td, "refs": refs, "table": table,
+                                  "n": n_rows, "device": device, "plan": plan}
+
+        self._launch(table, n_rows, device, plan, count_inc, key_mu, key_nu, apply=apply,
+                     decay_mask=decay_mask, weight_decay=weight_decay, neg_lr=neg_lr, param_key=param_key,
+                     param_sr=param_sr, random_bits=random_bits, clip_global_norm=clip_global_norm,
+                     clip_stats=clip_stats, skip_nonfinite=skip_nonfinite, finite_out=finite_out,
+                     finite_host=finite_host)
 
         new_state = self.new_state(state, count_inc, next_key)
         out_tree = _tree.unflatten(g_td, out_leaves) if not apply else None
@@ -922,8 +979,11 @@ class _Adamw8Update:
         if self.wd_nonzero:
             if params is None:
                 raise ValueError(NO_PARAMS_MSG)
-            n = len(_tree.leaves(updates, is_leaf=_is_passthrough_leaf))
-            decay_mask = _decay_mask_leaves(self.weight_decay_mask, params, n)
+            if self.weight_decay_mask is None:
+                decay_mask = ALL_LEAVES
+            else:
+                n = len(_tree.leaves(updates, is_leaf=_is_passthrough_leaf))
+                decay_mask = _decay_mask_leaves(self.weight_decay_mask, params, n)
         out, new_adam = self.engine.run(
             updates, adam_state, params, apply=apply, decay_mask=decay_mask,
             weight_decay=self.weight_decay if self.wd_nonzero else None, neg_lr=neg_lr,

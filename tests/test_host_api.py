@@ -261,3 +261,33 @@ def test_state_conversions_refuse_host_tensors():
         rf.quantize_state_tree({"w": torch.zeros(8192), "b": torch.zeros(4)}, st.mu, stochastic_rounding=True)
     with pytest.raises(ValueError, match="ROCm device"):
         rf.quantize_state_tree({"w": torch.zeros(8192), "b": torch.zeros(4)}, st.mu)
+
+
+def test_native_host_walk_matches_python_flatten():
+    """The native fast path walks (grads, mu, nu, params) in the order of
+    rollfast_amd._tree: dicts by sorted keys, lists and tuples in order,
+    None and MaskedNode as grads leaves; anything else is left to Python."""
+    from rollfast_amd import _lib
+
+    host = _lib.pyhost()
+    t = [torch.zeros(i + 1) for i in range(6)]
+    g = {"b": [t[0], (t[1], None)], "a": {"y": t[2], "x": rf.MaskedNode()}, "c": t[3]}
+    m = {"b": ["m0", ("m1", "m2")], "a": {"y": "m3", "x": "m4"}, "c": "m5"}
+    v = {"b": ["v0", ("v1", "v2")], "a": {"y": "v3", "x": "v4"}, "c": "v5"}
+    p = {"b": ["p0", ("p1", "p2")], "a": {"y": "p3", "x": "p4"}, "c": "p5"}
+    lg, lm, lv, lp = host.gather(g, m, v, p)
+    want_g, td = _tree.flatten(g, is_leaf=lambda x: x is None or isinstance(x, rf.MaskedNode))
+    assert [id(x) for x in lg] == [id(x) for x in want_g]
+    assert lm == _tree.flatten_up_to(td, m) and lv == _tree.flatten_up_to(td, v) and lp == _tree.flatten_up_to(td, p)
+    assert host.gather(g, m, v, None)[3] is None
+    # structure mismatches and containers left to the Python walk
+    assert host.gather(g, {**m, "d": 1}, v, p) is None
+    assert host.gather({"k": (t[0],)}, {"k": ["x"]}, {"k": ["y"]}, None) is None
+
+    class NT(NamedTuple):
+        a: object
+
+    assert host.gather(NT(t[0]), NT(1), NT(2), None) is None
+    assert host.gather({1: t[0], "a": t[1]}, {1: 0, "a": 0}, {1: 0, "a": 0}, None) is None  # keys do not sort
+    # refresh refuses host tensors (the caller then rebuilds the table)
+    assert host.refresh([t[0]], ["m"], ["v"], None, [], 0, 0) is False
