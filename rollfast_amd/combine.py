@@ -152,17 +152,20 @@ class _MultiTransformUpdate:
         self.param_labels = param_labels
         self._runner = None
 
-    def _labels(self, tree) -> list:
-        labels = self.param_labels(tree) if callable(self.param_labels) else self.param_labels
+    def _labels_obj(self, tree):
+        return self.param_labels(tree) if callable(self.param_labels) else self.param_labels
+
+    def _labels(self, tree, labels_obj=None) -> list:
+        labels = self._labels_obj(tree) if labels_obj is None else labels_obj
         _leaves, td = _tree.flatten(tree, is_leaf=_is_passthrough_leaf)
         return _tree.flatten_up_to(td, labels)
 
-    def _members(self, updates, state):
+    def _members(self, updates, state, labels_obj=None):
         """(group update object, its chain state, membership flags) per label
         whose transformation can join a grouped launch, else None."""
         from .optim.adam8 import _Adamw8Update, _GroupedRunner
 
-        labels = self._labels(updates)
+        labels = self._labels(updates, labels_obj)
         members = []
         for group, tx in self.transforms.items():
             if not isinstance(tx.update, _Adamw8Update):
@@ -198,12 +201,23 @@ class _MultiTransformUpdate:
         return out, MultiTransformState(inner_states=new_inner)
 
     def _step(self, updates, state, params, *, apply: bool, **kwargs):
-        members = self._members(updates, state)
+        from .optim.adam8 import _Adamw8Update
+
+        labels_obj = self._labels_obj(updates)
+        if apply and self._runner is not None:
+            # steady state: the same labels and state objects as the previous call
+            groups_in = [(tx.update, state.inner_states[g].inner_state) for g, tx in self.transforms.items()]
+            if all(isinstance(u, _Adamw8Update) for u, _ in groups_in):
+                new_states = self._runner.run_cached(groups_in, labels_obj, updates, params, **kwargs)
+                if new_states is not None:
+                    return None, MultiTransformState(
+                        inner_states={g: MaskedState(inner_state=s) for g, s in zip(self.transforms, new_states)})
+        members = self._members(updates, state, labels_obj)
         if members is None:
             raise NotImplementedError(
                 "a fused multi_transform step needs adamw8 / adamw groups that share b1, b2, eps, eps_root, "
                 "nesterov, exact, stochastic_rounding and the step count")
-        return self._grouped(updates, state, params, members, apply=apply, **kwargs)
+        return self._grouped(updates, state, params, members, apply=apply, labels_obj=labels_obj, **kwargs)
 
 
 def multi_transform(transforms: Mapping[Hashable, Any], param_labels) -> GradientTransformationExtraArgs:

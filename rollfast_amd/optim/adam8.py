@@ -1137,6 +1137,7 @@ class _GroupedRunner:
 
     def __init__(self):
         self._plans: dict = {}
+        self._last = None  # the previous fused call's table, for run_cached
 
     @staticmethod
     def compatible(updates_objs, adam_states) -> bool:
@@ -1147,44 +1148,15 @@ class _GroupedRunner:
         counts = {int(np.asarray(s.count)) for s in adam_states}
         return len(keys) == 1 and len(srs) <= 1 and len(counts) == 1
 
-    def run(self, members, updates, params, *, apply: bool, param_key=None, param_sr=False, random_bits=None,
-            clip_global_norm=None, clip_stats=None, skip_nonfinite=False, finite_out=None, finite_host=None):
-        """``members``: list of (update object, chain state, per-leaf membership
-        list).  Returns (out leaves or None, list of new chain states)."""
-        torch = _torch()
-        g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
-        n = len(g_leaves)
-        p_leaves = _tree.flatten_up_to(g_td, params) if params is not None else None
-        masked = MaskedNode()
-        rows, structure, groups, new_states = [], [], [], []
-        out_leaves = [None] * n
-        device = None
-        for gi, (upd, state, member) in enumerate(members):
+    @staticmethod
+    def _scalars(groups_in):
+        """Per group (update object, chain state): its group record (-lr,
+        decay, EMA weight, moment keys) and its new chain state."""
+        records, new_states = [], []
+        for upd, state in groups_in:
             eng = upd.engine
             adam_state, lr_state = state[0], state[-1]
             neg_lr, new_lr_state = upd._lr(lr_state)
-            gm = [g_leaves[i] if member[i] else masked for i in range(n)]
-            pm = None if p_leaves is None else [p_leaves[i] if member[i] else masked for i in range(n)]
-            decay_mask = None
-            if upd.wd_nonzero:
-                if params is None:
-                    raise ValueError(NO_PARAMS_MSG)
-                decay_mask = _decay_mask_leaves(upd.weight_decay_mask, _tree.unflatten(g_td, pm), n)
-            mu_leaves = _tree.flatten_up_to(g_td, adam_state.mu) if n else []
-            nu_leaves = _tree.flatten_up_to(g_td, adam_state.nu) if n else []
-            grows, gstruct, _refs, gouts, gdev = eng._build_rows(gm, mu_leaves, nu_leaves, pm, apply=apply,
-                                                                 decay_mask=decay_mask, random_bits=random_bits)
-            if gdev is not None:
-                if device is not None and gdev != device:
-                    raise ValueError("all leaves must live on the same device")
-                device = gdev
-            for row in grows:
-                row.group = gi
-            rows.extend(grows)
-            structure.extend(s + (gi,) for s in gstruct)
-            for i in range(n):
-                if member[i]:
-                    out_leaves[i] = gouts[i]
             key_mu, key_nu, next_key = eng.split_keys(adam_state.key)
             grp = _lib.Adam8Group()
             grp.neg_lr = neg_lr
@@ -1192,22 +1164,25 @@ class _GroupedRunner:
             grp.one_minus_b1 = eng.ema_weight(eng.cfg.b1)
             grp.key_mu[0], grp.key_mu[1] = int(key_mu[0]), int(key_mu[1])
             grp.key_nu[0], grp.key_nu[1] = int(key_nu[0]), int(key_nu[1])
-            groups.append(grp)
+            records.append(grp)
             count_inc = safe_int32_increment(int(np.asarray(adam_state.count)))
             new_states.append((eng.new_state(adam_state, count_inc, next_key),) + tuple(state[1:-1])
                               + (new_lr_state,))
-        for i in range(n):
-            if out_leaves[i] is None:  # passthrough leaves and leaves of no group keep their update
-                out_leaves[i] = g_leaves[i]
+        return records, new_states
 
-        upd0, state0, _ = members[0]
+    @staticmethod
+    def _launch(groups_in, records, table, n_rows, n_groups, device, plan, *, apply, param_key=None, param_sr=False,
+                random_bits=None, clip_global_norm=None, clip_stats=None, skip_nonfinite=False, finite_out=None,
+                finite_host=None):
+        torch = _torch()
+        upd0, state0 = groups_in[0]
         cfg = upd0.engine.cfg
         flags = _lib.RF_LR
         if cfg.nesterov:
             flags |= _lib.RF_NESTEROV
         if _group_key(upd0)[-1]:
             flags |= _lib.RF_DECAY_WEAK
-        if any(_moment_sr(m[0]) for m in members):
+        if any(_moment_sr(u) for u, _ in groups_in):
             flags |= _lib.RF_MOMENT_SR
         if apply and param_sr:
             flags |= _lib.RF_PARAM_SR
@@ -1220,11 +1195,92 @@ class _GroupedRunner:
         count_inc = safe_int32_increment(int(np.asarray(state0[0].count)))
         hp = _common_hparams(cfg, count_inc, flags, param_key, clip_global_norm, clip_stats, finite_out,
                              finite_host)
+        if n_rows:
+            gtab = (_lib.Adam8Group * len(records))(*records)
+            hp.groups = ctypes.cast(gtab, ctypes.c_void_p)
+            hp.n_groups = n_groups
+            with torch.cuda.device(device):
+                plan.run(table, hp, _lib.stream_ptr())
+                if finite_host is not None:
+                    plan.wait_prepass()
+
+    def run_cached(self, groups_in, labels_obj, updates, params, **kw):
+        """Steady state of the fused grouped step: the same labels object and,
+        per group, the same moment and param objects as the previous call.
+        The native fast path rewrites each group's grad pointers in the cached
+        table.  Returns the new chain states, or None (run() then rebuilds)."""
+        last = self._last
+        if (last is None or labels_obj is not last["labels"] or kw.get("random_bits") is not None
+                or len(groups_in) != len(last["groups"])):
+            return None
+        if not self.compatible([u for u, _ in groups_in], [st[0] for _, st in groups_in]):
+            return None
+        host = _lib.pyhost()
+        base = ctypes.addressof(last["table"])
+        size = ctypes.sizeof(_lib.Adam8Leaf)
+        for (upd, state), (first, refs) in zip(groups_in, last["groups"]):
+            if upd.wd_nonzero and upd.weight_decay_mask is not None:
+                return None
+            adam = state[0]
+            lists = host.gather(updates, adam.mu, adam.nu, params)
+            if lists is None or not host.refresh(*lists, refs, base + first * size, last["device"].index):
+                return None
+        records, new_states = self._scalars(groups_in)
+        self._launch(groups_in, records, last["table"], last["n"], last["n_groups"], last["device"], last["plan"],
+                     apply=True, **kw)
+        return new_states
+
+    def run(self, members, updates, params, *, apply: bool, labels_obj=None, param_key=None, param_sr=False,
+            random_bits=None, clip_global_norm=None, clip_stats=None, skip_nonfinite=False, finite_out=None,
+            finite_host=None):
+        """``members``: list of (update object, chain state, per-leaf membership
+        list).  Returns (out leaves or None, the grads treedef, list of new
+        chain states)."""
+        torch = _torch()
+        self._last = None
+        g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
+        n = len(g_leaves)
+        p_leaves = _tree.flatten_up_to(g_td, params) if params is not None else None
+        masked = MaskedNode()
+        rows, structure, group_rows = [], [], []
+        out_leaves = [None] * n
+        device = None
+        for gi, (upd, state, member) in enumerate(members):
+            eng = upd.engine
+            adam_state = state[0]
+            gm = [g_leaves[i] if member[i] else masked for i in range(n)]
+            pm = None if p_leaves is None else [p_leaves[i] if member[i] else masked for i in range(n)]
+            decay_mask = None
+            if upd.wd_nonzero:
+                if params is None:
+                    raise ValueError(NO_PARAMS_MSG)
+                decay_mask = _decay_mask_leaves(upd.weight_decay_mask, _tree.unflatten(g_td, pm), n)
+            mu_leaves = _tree.flatten_up_to(g_td, adam_state.mu) if n else []
+            nu_leaves = _tree.flatten_up_to(g_td, adam_state.nu) if n else []
+            grows, gstruct, grefs, gouts, gdev = eng._build_rows(gm, mu_leaves, nu_leaves, pm, apply=apply,
+                                                                 decay_mask=decay_mask, random_bits=random_bits)
+            if gdev is not None:
+                if device is not None and gdev != device:
+                    raise ValueError("all leaves must live on the same device")
+                device = gdev
+            for row in grows:
+                row.group = gi
+            group_rows.append((len(rows), grefs))
+            rows.extend(grows)
+            structure.extend(s + (gi,) for s in gstruct)
+            for i in range(n):
+                if member[i]:
+                    out_leaves[i] = gouts[i]
+        for i in range(n):
+            if out_leaves[i] is None:  # passthrough leaves and leaves of no group keep their update
+                out_leaves[i] = g_leaves[i]
+        groups_in = [(upd, state) for upd, state, _ in members]
+        records, new_states = self._scalars(groups_in)
+        table = plan = None
+        n_groups = 0
         if rows:
             table = (_lib.Adam8Leaf * len(rows))(*rows)
-            gtab = (_lib.Adam8Group * len(groups))(*groups)
-            hp.groups = ctypes.cast(gtab, ctypes.c_void_p)
-            hp.n_groups = 1 + max(r.group for r in rows)
+            n_groups = 1 + max(r.group for r in rows)
             skey = (bool(apply), device.index, tuple(structure))
             plan = self._plans.get(skey)
             if plan is None:
@@ -1233,8 +1289,11 @@ class _GroupedRunner:
                 if len(self._plans) > 16:
                     self._plans.clear()
                 self._plans[skey] = plan
-            with torch.cuda.device(device):
-                plan.run(table, hp, _lib.stream_ptr())
-                if finite_host is not None:
-                    plan.wait_prepass()
+        self._launch(groups_in, records, table, len(rows), n_groups, device, plan, apply=apply, param_key=param_key,
+                     param_sr=param_sr, random_bits=random_bits, clip_global_norm=clip_global_norm,
+                     clip_stats=clip_stats, skip_nonfinite=skip_nonfinite, finite_out=finite_out,
+                     finite_host=finite_host)
+        if apply and rows and random_bits is None and labels_obj is not None:
+            self._last = {"labels": labels_obj, "groups": group_rows, "table": table, "n": len(rows),
+                          "n_groups": n_groups, "device": device, "plan": plan}
         return (out_leaves if not apply else None), g_td, new_states

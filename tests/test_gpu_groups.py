@@ -277,3 +277,39 @@ def test_group_table_abi_checks():
         assert np.allclose(got[: n // 2], -1e-3, rtol=1e-5) and np.allclose(got[n // 2:], -2e-3, rtol=1e-5)
     finally:
         lib.rf_adam8_plan_destroy(plan)
+
+
+def test_grouped_cached_table_follows_changes():
+    """From the second call the grouped step rewrites only grad pointers of
+    its cached table; a replaced param tensor, a storage swap or new labels
+    must send it back to a full rebuild (results equal to the groups one by
+    one throughout)."""
+    import torch
+
+    import rollfast_amd as rf
+
+    _, pa = _tree(6, 0.02)
+    _, pb = _tree(6, 0.02)
+    labels_a = dict(LABELS)
+    txa = rf.multi_transform(_transforms(rf), lambda _: labels_a)
+    sa = txa.init(pa)
+    singles = _transforms(rf)
+    txb = {lab: rf.masked(tx, {n: LABELS[n] == lab for n in LABELS}) for lab, tx in singles.items()}
+    sb = {lab: tx.init(pb) for lab, tx in txb.items()}
+    for step in range(6):
+        if step == 2:  # a new param tensor object for one leaf, in both trees
+            pa["w1"] = pa["w1"].clone()
+            pb["w1"] = pb["w1"].clone()
+        if step == 3:  # a storage swap behind the same object
+            pa["head"].data = pa["head"].data.clone()
+            pb["head"].data = pb["head"].data.clone()
+        if step == 4:  # an equal labels tree, but a new object
+            labels_a = dict(LABELS)
+        _, g = _tree(600 + step, 1e-2)
+        pa, sa = rf.adamw8_step(txa, pa, g, sa, stochastic=False)
+        for lab, tx in txb.items():
+            pb, sb[lab] = rf.adamw8_step(tx, pb, g, sb[lab], stochastic=False)
+        torch.cuda.synchronize()
+        ga = {lab: s.inner_state for lab, s in sa.inner_states.items()}
+        gb = {lab: s.inner_state for lab, s in sb.items()}
+        _assert_same(pa, pb, ga, gb, f"step {step + 1}")
