@@ -504,7 +504,7 @@ def main(argv=None):
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the step has no cross-GPU "
-              "communication and multi-GPU runs are not part of this build.", file=sys.stderr)
+              "communication and rollfast_amd runs on one GPU.", file=sys.stderr)
         return 2
 
     import torch

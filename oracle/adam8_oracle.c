@@ -1,8 +1,8 @@
 /*
  * adam8_oracle.c -- CPU restatement of rollfast's 8-bit AdamW step.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP library
- * is compared against.  Only tests/, __graft_entry__.smoke() and the
+ * TEST INFRASTRUCTURE ONLY.  The HIP library's results are compared against
+ * this restatement.  Only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py may load it; the product (rollfast_amd/)
  * never links, imports or calls it.
  *

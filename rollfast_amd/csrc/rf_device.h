@@ -14,10 +14,11 @@
 // global access is a fully coalesced 16-byte (params, grads) or 8-byte
 // (codes) vector access, the block absmax is a wave-local reduction (no LDS
 // round trip, no barrier), and the updated moments stay in VGPRs until the
-// scale is known.  Workgroups are persistent (grid = CUs x occupancy) and
-// walk a device-resident work list that covers every leaf of the pytree, so
-// a whole parameter tree is one launch.  The codebooks and the requantization
-// lookup tables (rf_tables.h) are staged into LDS once per workgroup.
+// scale is known.  Waves walk a device-resident work list that covers every
+// leaf of the pytree (unit u goes to wave u mod nwaves, about 16 units per
+// wave), so a whole parameter tree is one launch.  The codebooks and the
+// requantization lookup tables (rf_tables.h) are staged into LDS once per
+// workgroup.
 //
 // Compiled with -ffp-contract=off: the reference rounds every multiply and
 // add separately; FMAs appear only where written explicitly.
@@ -1134,8 +1135,8 @@ __device__ void reject_units(const rf_adam8_leaf* __restrict__ leaves, const Seg
 __device__ __forceinline__ bool gate_rejects(const KHp& h) { return h.gate != nullptr && *h.gate == 0.0f; }
 
 // Full 2048-element blocks of the leaves whose (param, grad) dtypes are
-// (PT, GT) (uint16_t = bf16, float = f32): the hot kernel.  Persistent
-// waves walk the work list with a grid stride of one block per wave.
+// (PT, GT) (uint16_t = bf16, float = f32): the hot kernel.  Waves walk the
+// work list with a grid stride of one block per wave.
 template <typename PT, typename GT, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVES_PER_EU))) void k_adam8(
     const rf_adam8_leaf* __restrict__ leaves, const Seg* __restrict__ segs, int64_t total_units, KHp h,

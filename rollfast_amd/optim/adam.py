@@ -18,7 +18,7 @@ unquantized ("fallback") moment path:
 * ``adamw`` = ``chain(scale_by_adam, add_decayed_weights, scale_by_learning_rate)``
   (adam.py:381-406), fused into the same launch.
 
-Magma (``use_magma=True``) is not part of this build and raises
+Magma (``use_magma=True``) is not implemented in rollfast_amd and raises
 ``NotImplementedError``.
 """
 
@@ -184,7 +184,7 @@ def scale_by_adam(
     ``exact`` (extension): IEEE division and square root in the direction."""
     del magma_p, magma_tau, axis_name
     if use_magma:
-        raise NotImplementedError("Magma is not supported by this build.")
+        raise NotImplementedError("Magma is not supported by rollfast_amd.")
     _has_nonzero_or_scheduled(weight_decay)
     mu = _canonical_mu_dtype(mu_dtype)
     engine = _make_engine(b1, b2, eps, eps_root, mu, nesterov, key, exact)
@@ -219,7 +219,7 @@ def adamw(
     launch.  The state is the chain's tuple ``(ScaleByAdamState,
     add_decayed_weights state?, lr state)``."""
     if use_magma:
-        raise NotImplementedError("Magma is not supported by this build.")
+        raise NotImplementedError("Magma is not supported by rollfast_amd.")
     if callable(weight_decay):
         raise NotImplementedError("weight-decay schedules are not supported by adamw; pass a scalar")
     inner = scale_by_adam(b1=b1, b2=b2, eps=eps, eps_root=eps_root, mu_dtype=mu_dtype, nesterov=nesterov,

@@ -100,12 +100,12 @@ def clip_by_global_norm(max_norm: float, *, axis_name=None, partition_axis_names
                         replicated_axis_names=None) -> GradientTransformation:
     """Clip by global norm over the leaves (transforms.py:20-54): scale every
     leaf by ``min(1, max_norm / (norm + 1e-6))`` in the leaf dtype.  The axis
-    arguments name collective axes of a multi-device reduction, which this
-    single-device build does not perform; they must be None."""
+    arguments name collective axes of a multi-device reduction, which
+    rollfast_amd (one device) does not perform; they must be None."""
     if max_norm <= 0.0:
         raise ValueError("max_norm must be positive.")
     if axis_name is not None or partition_axis_names is not None or replicated_axis_names is not None:
-        raise NotImplementedError("cross-device norm reduction is not part of this single-device build")
+        raise NotImplementedError("cross-device norm reduction is not implemented: rollfast_amd runs on one device")
 
     def init_fn(params):
         del params
