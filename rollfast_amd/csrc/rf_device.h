@@ -120,10 +120,15 @@ __device__ __forceinline__ void threefry2x32(uint32_t k0, uint32_t k1, uint32_t 
 {
     const uint32_t k2 = k0 ^ k1 ^ 0x1BD11BDAu;
     uint32_t x0 = c0 + k0, x1 = c1 + k1;
+// The empty asm pins x0 and x1 to one register each after every round:
+// without it the compiler keeps x0 as a sum of two registers across rounds
+// and spends a second add per round on it (about 89 instead of 69 VALU
+// instructions per Threefry block).
 #define RF_TF_ROUND(r)                  \
     x0 += x1;                           \
     x1 = __builtin_rotateleft32(x1, r); \
-    x1 ^= x0;
+    x1 ^= x0;                           \
+    __asm__("" : "+v"(x0), "+v"(x1));
 #define RF_TF_R0 RF_TF_ROUND(13) RF_TF_ROUND(15) RF_TF_ROUND(26) RF_TF_ROUND(6)
 #define RF_TF_R1 RF_TF_ROUND(17) RF_TF_ROUND(29) RF_TF_ROUND(16) RF_TF_ROUND(24)
     RF_TF_R0 x0 += k1; x1 += k2 + 1u;
