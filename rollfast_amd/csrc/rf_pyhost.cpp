@@ -14,6 +14,9 @@
 //       at each grads leaf.  Returns None (the caller falls back to the
 //       Python walk) for any container it does not handle or any mismatch.
 //
+//   apply_rows(params, updates) -> packed rf_apply_leaf rows and the params
+//       tree for rollfast.apply_updates (see py_apply_rows).
+//
 //   refresh(g, mu, nu, p, rows, table_address, device) -> bool
 //       rows[j] = (i, mref, vref, pref, bufrefs, bufptrs, grad_dtype, size, vec)
 //       Checks that leaf i's moment and param objects are the cached ones
@@ -29,6 +32,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <string>
 
 #include "rfadam8.h"
 
@@ -213,6 +217,121 @@ PyObject* py_refresh(PyObject*, PyObject* args)
     Py_RETURN_TRUE;
 }
 
+// apply_rows(params, updates) -> (rows bytes, n rows, device, new params tree) or None
+//
+// rollfast.apply_updates' walk (utils.py:648-708): the params tree drives,
+// updates are taken at its leaves; None / MaskedNode on either side is left
+// alone.  Every other leaf pair must be a contiguous f32 / bf16 param and a
+// contiguous f32 update of the same size on one device: the row records
+// (rf_apply_leaf) come back packed, with param_index = the leaf's position.
+// The returned params tree has new containers around the same tensors.
+// None means "not handled here" (other containers, dtypes or layouts): the
+// Python walk then does the conversions and raises the errors.
+struct ApplyWalk {
+    std::string rows;
+    int64_t leaf = 0;
+    int device = -1;
+};
+
+bool is_aux(PyObject* x)
+{
+    return x == Py_None || (g_masked_node_type && PyObject_TypeCheck(x, (PyTypeObject*)g_masked_node_type));
+}
+
+// Returns a new reference to the rebuilt subtree; nullptr with no error set
+// for "not handled here", nullptr with an error set on failure.
+PyObject* apply_walk(PyObject* p, PyObject* u, ApplyWalk& w)
+{
+    if (!is_aux(p) && !THPVariable_Check(p) && !PyDict_CheckExact(p) && !PyList_CheckExact(p) && !PyTuple_CheckExact(p))
+        return nullptr;  // other leaves and containers (namedtuples, custom nodes): the Python walk
+    if (is_aux(p) || THPVariable_Check(p)) {
+        const int64_t i = w.leaf++;
+        if (!is_aux(p) && !is_aux(u)) {
+            if (!THPVariable_Check(p) || !THPVariable_Check(u)) return nullptr;
+            const at::Tensor& tp = THPVariable_Unpack(p);
+            const at::Tensor& tu = THPVariable_Unpack(u);
+            const at::ScalarType sp = tp.scalar_type();
+            if ((sp != at::kFloat && sp != at::kBFloat16) || tu.scalar_type() != at::kFloat) return nullptr;
+            if (!tp.is_cuda() || !tu.is_cuda() || tp.get_device() != tu.get_device()) return nullptr;
+            if (w.device < 0) w.device = tp.get_device();
+            if (tp.get_device() != w.device) return nullptr;
+            if (!tp.is_contiguous() || !tu.is_contiguous() || tp.numel() != tu.numel()) return nullptr;
+            if (i > INT32_MAX) return nullptr;
+            rf_apply_leaf row{};
+            row.param = tp.data_ptr();
+            row.updates = (const float*)tu.data_ptr();
+            row.bits = nullptr;
+            row.size = tp.numel();
+            row.param_dtype = sp == at::kBFloat16 ? RF_BF16 : RF_F32;
+            row.param_index = (int32_t)i;
+            w.rows.append((const char*)&row, sizeof(row));
+        }
+        Py_INCREF(p);
+        return p;
+    }
+    if (PyDict_CheckExact(p)) {
+        if (!PyDict_CheckExact(u) || PyDict_Size(u) != PyDict_Size(p)) return nullptr;
+        PyObject* keys = PyDict_Keys(p);
+        if (!keys) return nullptr;
+        if (PyList_Sort(keys) < 0) {
+            Py_DECREF(keys);
+            PyErr_Clear();
+            return nullptr;
+        }
+        PyObject* out = PyDict_New();
+        const Py_ssize_t n = PyList_GET_SIZE(keys);
+        for (Py_ssize_t k = 0; out && k < n; ++k) {
+            PyObject* key = PyList_GET_ITEM(keys, k);
+            PyObject* cp = PyDict_GetItemWithError(p, key);
+            PyObject* cu = cp ? PyDict_GetItemWithError(u, key) : nullptr;
+            PyObject* c = (cp && cu) ? apply_walk(cp, cu, w) : nullptr;
+            if (!c || PyDict_SetItem(out, key, c) < 0) {
+                Py_XDECREF(c);
+                Py_CLEAR(out);
+                break;
+            }
+            Py_DECREF(c);
+        }
+        Py_DECREF(keys);
+        return out;
+    }
+    const bool is_list = PyList_CheckExact(p);
+    if (is_list ? !PyList_CheckExact(u) : !PyTuple_CheckExact(u)) return nullptr;
+    const Py_ssize_t n = PySequence_Fast_GET_SIZE(p);
+    if (PySequence_Fast_GET_SIZE(u) != n) return nullptr;
+    PyObject* out = is_list ? PyList_New(n) : PyTuple_New(n);
+    for (Py_ssize_t k = 0; out && k < n; ++k) {
+        PyObject* c = apply_walk(PySequence_Fast_GET_ITEM(p, k), PySequence_Fast_GET_ITEM(u, k), w);
+        if (!c) {
+            Py_CLEAR(out);
+            break;
+        }
+        if (is_list) PyList_SET_ITEM(out, k, c);
+        else PyTuple_SET_ITEM(out, k, c);
+    }
+    return out;
+}
+
+PyObject* py_apply_rows(PyObject*, PyObject* args)
+{
+    PyObject *p, *u;
+    if (!PyArg_ParseTuple(args, "OO", &p, &u)) return nullptr;
+    ApplyWalk w;
+    PyObject* tree = apply_walk(p, u, w);
+    if (!tree) {
+        if (PyErr_Occurred()) return nullptr;
+        Py_RETURN_NONE;
+    }
+    PyObject* rows = PyBytes_FromStringAndSize(w.rows.data(), (Py_ssize_t)w.rows.size());
+    if (!rows) {
+        Py_DECREF(tree);
+        return nullptr;
+    }
+    PyObject* out = Py_BuildValue("(NnnN)", rows, (Py_ssize_t)(w.rows.size() / sizeof(rf_apply_leaf)),
+                                  (Py_ssize_t)w.device, tree);
+    return out;
+}
+
 PyObject* py_set_masked_node_type(PyObject*, PyObject* t)
 {
     if (!PyType_Check(t)) {
@@ -228,6 +347,7 @@ PyObject* py_set_masked_node_type(PyObject*, PyObject* t)
 PyMethodDef methods[] = {
     {"gather", py_gather, METH_VARARGS, "joint walk of (grads, mu, nu, params); None if not handled"},
     {"refresh", py_refresh, METH_VARARGS, "rewrite the grad pointers of a cached leaf table; False on a mismatch"},
+    {"apply_rows", py_apply_rows, METH_VARARGS, "apply_updates' leaf table and rebuilt params tree; None if not handled"},
     {"set_masked_node_type", py_set_masked_node_type, METH_O, "the MaskedNode class (a grads leaf)"},
     {nullptr, nullptr, 0, nullptr},
 };

@@ -10,6 +10,8 @@ updated in place and returned (JAX donation semantics).
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 
 from . import _lib, _tree, prng
@@ -79,6 +81,19 @@ def _launch_apply(pairs, stochastic: bool, key) -> None:
     del keep
 
 
+def _launch_rows(rows: bytes, n: int, device: int, stochastic: bool, key) -> None:
+    """rf_apply_updates over ``n`` packed rf_apply_leaf records."""
+    torch = _torch()
+    k = prng.as_key(key) if key is not None else np.zeros(2, np.uint32)
+    buf = ctypes.create_string_buffer(rows, len(rows))
+    table = ctypes.cast(buf, ctypes.POINTER(_lib.ApplyLeaf))
+    with torch.cuda.device(device):
+        _lib.check(
+            _lib.lib().rf_apply_updates(table, n, 1 if stochastic else 0, int(k[0]), int(k[1]), _lib.stream_ptr()),
+            "apply_updates",
+        )
+
+
 def apply_updates(params, updates, key=None, stochastic: bool = True):
     """Apply updates with optional stochastic rounding for bf16 params
     (utils.py:648-708): bf16 leaves take ``f32(p) + f32(u)`` then SR (per-leaf
@@ -86,6 +101,14 @@ def apply_updates(params, updates, key=None, stochastic: bool = True):
     take ``p + u``.  None / MaskedNode leaves are left unchanged."""
     if stochastic and key is None:
         raise ValueError(_KEY_MSG)
+    # Native walk (contiguous f32/bf16 params, f32 updates, dict/list/tuple
+    # containers); anything else takes the Python walk below.
+    fast = _lib.pyhost().apply_rows(params, updates)
+    if fast is not None:
+        rows, n, device, tree = fast
+        if n:
+            _launch_rows(rows, n, device, stochastic, key)
+        return tree
     leaves, td = _tree.flatten(params, is_leaf=_is_aux_leaf)
     u_leaves = _tree.flatten_up_to(td, updates)
     pairs = []

@@ -274,3 +274,50 @@ def test_tree_stochastic_cast_keys_and_passthrough():
     assert out["z"].dtype == torch.complex64
     f32 = _tree_stochastic_cast({"a": tree["a"]}, torch.float32, key)["a"]
     assert f32.dtype == torch.float32
+
+
+def test_apply_updates_nested_tree_native_and_python_walks():
+    """apply_updates over a nested dict / list / tuple tree with None and
+    MaskedNode leaves: the native walk (f32 updates) and the Python walk
+    (bf16 updates, converted) give the oracle's result with the per-leaf key
+    of each leaf's flatten position; the returned tree has new containers
+    around the same tensors."""
+    import torch
+
+    rf = _rf()
+    rng = np.random.default_rng(9)
+
+    def tree(seed_shift):
+        r = np.random.default_rng(100 + seed_shift)
+        p = [bf16_bits((r.standard_normal(n) * 0.5).astype(np.float32)) for n in (300, 70, 5000)]
+        pf = (r.standard_normal(64) * 0.5).astype(np.float32)
+        return p, pf
+
+    hp, hpf = tree(0)
+    u = [(rng.standard_normal(n) * 1e-3).astype(np.float32) for n in (300, 70, 5000)]
+    uf = (rng.standard_normal(64) * 1e-3).astype(np.float32)
+    key = rf.prng.PRNGKey(5)
+    results = []
+    for native in (True, False):
+        params = {"a": [to_device(hp[0], "bf16"), (to_device(hp[1], "bf16"), None)],
+                  "b": {"x": to_device(hpf, "f32"), "y": to_device(hp[2], "bf16")}}
+        udt = torch.float32 if native else torch.bfloat16
+        ups = {"a": [torch.from_numpy(u[0]).cuda().to(udt), (torch.from_numpy(u[1]).cuda().to(udt), None)],
+               "b": {"x": torch.from_numpy(uf).cuda().to(udt), "y": rf.MaskedNode()}}
+        out = rf.apply_updates(params, ups, key=key)
+        torch.cuda.synchronize()
+        assert out is not params and out["a"] is not params["a"] and out["a"][0] is params["a"][0]
+        assert out["a"][1][1] is None and out["b"]["y"] is params["b"]["y"]
+        results.append(out)
+    # flatten order: a/0, a/1/0, a/1/1 (None), b/x, b/y -> indices 0, 1, 2, 3, 4
+    keys = orc.split(key, 5)
+    for native, out in zip((True, False), results):
+        uu = [u[0], u[1], uf] if native else [orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(x)) for x in (u[0], u[1], uf)]
+        want0, want1, wantx = hp[0].copy(), hp[1].copy(), hpf.copy()
+        orc.apply_updates(want0, orc.BF16, uu[0], bits=orc.random_bits(keys[0], 300))
+        orc.apply_updates(want1, orc.BF16, uu[1], bits=orc.random_bits(keys[1], 70))
+        orc.apply_updates(wantx, orc.F32, uu[2], bits=orc.random_bits(keys[3], 64))
+        np.testing.assert_array_equal(to_host(out["a"][0]), want0)
+        np.testing.assert_array_equal(to_host(out["a"][1][0]), want1)
+        np.testing.assert_array_equal(to_host(out["b"]["x"]).view(np.uint32), wantx.view(np.uint32))
+        np.testing.assert_array_equal(to_host(out["b"]["y"]), hp[2])
