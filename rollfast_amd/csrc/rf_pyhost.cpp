@@ -14,6 +14,10 @@
 //       at each grads leaf.  Returns None (the caller falls back to the
 //       Python walk) for any container it does not handle or any mismatch.
 //
+//   updates_out(grads, g, mu, rows, table_address) -> updates tree
+//       Update-only mode: the f32 outputs of a refreshed table (one device
+//       buffer, a view per leaf) and the updates tree (see py_updates_out).
+//
 //   apply_rows(params, updates) -> packed rf_apply_leaf rows and the params
 //       tree for rollfast.apply_updates (see py_apply_rows).
 //
@@ -33,12 +37,20 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
+
+#include <ATen/ATen.h>
 
 #include "rfadam8.h"
 
 namespace {
 
 PyObject* g_masked_node_type = nullptr;  // rollfast_amd._base.MaskedNode
+
+bool is_aux(PyObject* x)
+{
+    return x == Py_None || (g_masked_node_type && PyObject_TypeCheck(x, (PyTypeObject*)g_masked_node_type));
+}
 
 bool is_grad_leaf(PyObject* x)
 {
@@ -217,6 +229,101 @@ PyObject* py_refresh(PyObject*, PyObject* args)
     Py_RETURN_TRUE;
 }
 
+// Rebuilds the containers of `g` (the grads tree, walked as in walk()) with
+// leaf k replaced by vals[k].  New reference, or nullptr with an error set.
+PyObject* rebuild(PyObject* g, PyObject* vals, Py_ssize_t& k)
+{
+    if (is_grad_leaf(g)) {
+        PyObject* v = PyList_GET_ITEM(vals, k++);
+        Py_INCREF(v);
+        return v;
+    }
+    if (PyDict_CheckExact(g)) {
+        PyObject* keys = PyDict_Keys(g);
+        if (!keys || PyList_Sort(keys) < 0) {
+            Py_XDECREF(keys);
+            return nullptr;
+        }
+        PyObject* out = PyDict_New();
+        for (Py_ssize_t i = 0; out && i < PyList_GET_SIZE(keys); ++i) {
+            PyObject* key = PyList_GET_ITEM(keys, i);
+            PyObject* c = rebuild(PyDict_GetItem(g, key), vals, k);
+            if (!c || PyDict_SetItem(out, key, c) < 0) Py_CLEAR(out);
+            Py_XDECREF(c);
+        }
+        Py_DECREF(keys);
+        return out;
+    }
+    const bool is_list = PyList_CheckExact(g);
+    const Py_ssize_t n = PySequence_Fast_GET_SIZE(g);
+    PyObject* out = is_list ? PyList_New(n) : PyTuple_New(n);
+    for (Py_ssize_t i = 0; out && i < n; ++i) {
+        PyObject* c = rebuild(PySequence_Fast_GET_ITEM(g, i), vals, k);
+        if (!c) {
+            Py_CLEAR(out);
+            break;
+        }
+        if (is_list) PyList_SET_ITEM(out, i, c);
+        else PyTuple_SET_ITEM(out, i, c);
+    }
+    return out;
+}
+
+// updates_out(grads, lg, lm, rows, table_address) -> updates tree
+//
+// Update-only (Optax) mode after a successful refresh(): one f32 device
+// buffer holds every row's updates (each leaf 16-byte aligned), row j's
+// `updates` pointer is set to its slice and the updates tree is the grads
+// tree with, per leaf, that slice viewed in the grad's shape, or the
+// passthrough leaf (the moment's MaskedNode / None, else the grad's).
+PyObject* py_updates_out(PyObject*, PyObject* args)
+{
+    PyObject *g, *lg, *lm, *rows;
+    unsigned long long table_addr = 0;
+    if (!PyArg_ParseTuple(args, "OO!O!O!K", &g, &PyList_Type, &lg, &PyList_Type, &lm, &PyList_Type, &rows,
+                          &table_addr))
+        return nullptr;
+    const Py_ssize_t n = PyList_GET_SIZE(lg);
+    const Py_ssize_t nrows = PyList_GET_SIZE(rows);
+    auto* table = (rf_adam8_leaf*)(uintptr_t)table_addr;
+    std::vector<int64_t> off((size_t)nrows);
+    int64_t total = 0;
+    for (Py_ssize_t j = 0; j < nrows; ++j) {
+        off[(size_t)j] = total;
+        total += (table[j].size + 3) / 4 * 4;
+    }
+    PyObject* vals = PyList_New(n);
+    if (!vals) return nullptr;
+    for (Py_ssize_t i = 0; i < n; ++i) {  // passthrough leaves (utils of the Python path)
+        PyObject* gi = PyList_GET_ITEM(lg, i);
+        PyObject* mi = PyList_GET_ITEM(lm, i);
+        PyObject* v = is_aux(mi) ? mi : gi;
+        Py_INCREF(v);
+        PyList_SET_ITEM(vals, i, v);
+    }
+    if (nrows > 0) {
+        const at::Tensor& g0 = THPVariable_Unpack(PyList_GET_ITEM(lg, PyLong_AsSsize_t(PyTuple_GET_ITEM(
+                                                                          PyList_GET_ITEM(rows, 0), 0))));
+        at::Tensor flat = at::empty({total}, g0.options().dtype(at::kFloat));
+        for (Py_ssize_t j = 0; j < nrows; ++j) {
+            const Py_ssize_t i = PyLong_AsSsize_t(PyTuple_GET_ITEM(PyList_GET_ITEM(rows, j), 0));
+            const at::Tensor& gi = THPVariable_Unpack(PyList_GET_ITEM(lg, i));
+            at::Tensor view = flat.as_strided(gi.sizes(), gi.strides(), off[(size_t)j]);  // gi is contiguous
+            table[j].updates = view.data_ptr<float>();
+            PyObject* obj = THPVariable_Wrap(std::move(view));
+            if (!obj) {
+                Py_DECREF(vals);
+                return nullptr;
+            }
+            PyList_SetItem(vals, i, obj);  // steals obj, drops the passthrough placeholder
+        }
+    }
+    Py_ssize_t k = 0;
+    PyObject* out = rebuild(g, vals, k);
+    Py_DECREF(vals);
+    return out;
+}
+
 // apply_rows(params, updates) -> (rows bytes, n rows, device, new params tree) or None
 //
 // rollfast.apply_updates' walk (utils.py:648-708): the params tree drives,
@@ -232,11 +339,6 @@ struct ApplyWalk {
     int64_t leaf = 0;
     int device = -1;
 };
-
-bool is_aux(PyObject* x)
-{
-    return x == Py_None || (g_masked_node_type && PyObject_TypeCheck(x, (PyTypeObject*)g_masked_node_type));
-}
 
 // Returns a new reference to the rebuilt subtree; nullptr with no error set
 // for "not handled here", nullptr with an error set on failure.
@@ -347,6 +449,7 @@ PyObject* py_set_masked_node_type(PyObject*, PyObject* t)
 PyMethodDef methods[] = {
     {"gather", py_gather, METH_VARARGS, "joint walk of (grads, mu, nu, params); None if not handled"},
     {"refresh", py_refresh, METH_VARARGS, "rewrite the grad pointers of a cached leaf table; False on a mismatch"},
+    {"updates_out", py_updates_out, METH_VARARGS, "update-only mode: output buffers and the updates tree"},
     {"apply_rows", py_apply_rows, METH_VARARGS, "apply_updates' leaf table and rebuilt params tree; None if not handled"},
     {"set_masked_node_type", py_set_masked_node_type, METH_O, "the MaskedNode class (a grads leaf)"},
     {nullptr, nullptr, 0, nullptr},

@@ -760,19 +760,23 @@ class _Engine:
         # as the previous call): the native fast path walks the four trees
         # and rewrites the grad pointers of the cached table.
         last = self._last
-        if (apply and last is not None and random_bits is None and last["apply"] and last["n"]
+        if (last is not None and random_bits is None and last["apply"] == apply and last["n"]
                 and last["mask"] == (decay_mask if decay_mask is None or decay_mask is ALL_LEAVES
                                      else tuple(decay_mask))):
             host = _lib.pyhost()
             lists = host.gather(updates, state.mu, state.nu, params)
-            if lists is not None and host.refresh(*lists, last["refs"], ctypes.addressof(last["table"]),
-                                                  last["device"].index):
+            addr = ctypes.addressof(last["table"])
+            if lists is not None and host.refresh(*lists, last["refs"], addr, last["device"].index):
+                out_tree = None
+                if not apply:  # f32 outputs: one buffer, a view per leaf
+                    with torch.cuda.device(last["device"]):
+                        out_tree = host.updates_out(updates, lists[0], lists[1], last["refs"], addr)
                 self._launch(last["table"], last["n"], last["device"], last["plan"], count_inc, key_mu, key_nu,
-                             apply=True, decay_mask=decay_mask, weight_decay=weight_decay, neg_lr=neg_lr,
+                             apply=apply, decay_mask=decay_mask, weight_decay=weight_decay, neg_lr=neg_lr,
                              param_key=param_key, param_sr=param_sr, random_bits=None,
                              clip_global_norm=clip_global_norm, clip_stats=clip_stats,
                              skip_nonfinite=skip_nonfinite, finite_out=finite_out, finite_host=finite_host)
-                return None, self.new_state(state, count_inc, next_key)
+                return out_tree, self.new_state(state, count_inc, next_key)
 
         g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
         mu_leaves = _tree.flatten_up_to(g_td, state.mu) if g_td.num_leaves else []
