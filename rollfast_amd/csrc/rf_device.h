@@ -164,11 +164,33 @@ __device__ __forceinline__ float uniform_from_bits(uint32_t bits)
     return __uint_as_float((bits >> 9) | 0x3F800000u) - 1.0f;
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+
+// Wave-wide unsigned max (every lane active), returned wave-uniform: four
+// DPP steps leave each 16-lane row's max in all of its lanes, then the four
+// row maxima are combined in scalar registers.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x)
 {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x = max(x, (uint32_t)__shfl_xor((int)x, o, WAVE));
-    return x;
+    x = max(x, dpp_u32<0xB1>(x));   // quad_perm [1,0,3,2]
+    x = max(x, dpp_u32<0x4E>(x));   // quad_perm [2,3,0,1]
+    x = max(x, dpp_u32<0x141>(x));  // row_half_mirror
+    x = max(x, dpp_u32<0x140>(x));  // row_mirror
+    const uint32_t r0 = __builtin_amdgcn_readlane(x, 0), r1 = __builtin_amdgcn_readlane(x, 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane(x, 32), r3 = __builtin_amdgcn_readlane(x, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
+// Four byte values (each < 256) packed little-endian: two shift-or steps and
+// one byte permute, three instructions.
+__device__ __forceinline__ uint32_t pack4_u8(uint32_t a, uint32_t b, uint32_t c, uint32_t d)
+{
+    const uint32_t lo = a | (b << 8);
+    const uint32_t hi = c | (d << 8);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);  // bytes lo.0, lo.1, hi.0, hi.1
 }
 
 __device__ __forceinline__ uint32_t uniform_u32(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -220,11 +242,18 @@ __device__ __forceinline__ float div_by_scale(float x, float s, float rs)
 
 // Threshold-count candidates of a normalised value: the number of decision
 // thresholds at or below the low end of n's cell (signed: per sign).
-__device__ __forceinline__ uint32_t cand_signed(const uint8_t* lds, float n)
+// Signed candidate-table index of n: the cell of |n| with the sign as bit
+// CANDS_SIGN_SHIFT.
+__device__ __forceinline__ uint32_t signed_cell(float n)
 {
     const uint32_t nb = __float_as_uint(n);
     const uint32_t idx = __builtin_elementwise_sub_sat((nb >> CELL_SHIFT) & 0xFFFFu, CELL_LO);
-    return lds[L_CANDS + __umul24(nb >> 31, NCELL_PAD) + idx];
+    return ((nb >> (31 - CANDS_SIGN_SHIFT)) & CANDS_SIGN_STRIDE) | idx;
+}
+
+__device__ __forceinline__ uint32_t cand_signed(const uint8_t* lds, float n)
+{
+    return lds[L_CANDS + signed_cell(n)];
 }
 
 __device__ __forceinline__ uint32_t cand_unsigned(const uint8_t* lds, float n)
@@ -237,9 +266,7 @@ __device__ __forceinline__ uint32_t cand_unsigned(const uint8_t* lds, float n)
 __device__ __forceinline__ uint32_t code_signed_fast(const uint8_t* lds, float x, float s, float rs)
 {
     const float n = div_by_scale(x, s, rs);
-    const uint32_t nb = __float_as_uint(n);
-    const uint32_t idx = __builtin_elementwise_sub_sat((nb >> CELL_SHIFT) & 0xFFFFu, CELL_LO);
-    const uint32_t cand = lds[L_CANDS + __umul24(nb >> 31, NCELL_PAD) + idx];
+    const uint32_t cand = lds[L_CANDS + signed_cell(n)];
     const float t = *(const float*)(lds + L_TS + cand * 4u);
     return cand + (n >= t ? 1u : 0u);
 }
@@ -326,6 +353,16 @@ __device__ __forceinline__ void decay_and_scale8(const KHp& h, float (&u)[8], co
 __device__ __forceinline__ bool cancels(float sum, float u)
 {
     return fabsf(sum) * 4096.0f < fabsf(u);
+}
+
+// Active lanes where any of 8 sums nearly cancels: each compare's lane mask
+// is OR-ed in scalar registers, with no per-lane flag materialised.
+__device__ __forceinline__ uint64_t cancel_lanes8(const float (&sum)[8], const float (&u)[8])
+{
+    uint64_t r = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) r |= __builtin_amdgcn_ballot_w64(cancels(sum[t], u[t]));
+    return r;
 }
 
 // EMA moment updates (adam8.py:322-335).
@@ -763,10 +800,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                 // value; that moves the rounded param by more than one
                 // bf16 ulp only where p + u nearly cancels.  Such chunks
                 // (rare) are recomputed with IEEE arithmetic.
-                bool risky = false;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) risky |= cancels(sum[t], u[t]);
-                if (__builtin_amdgcn_ballot_w64(risky) != 0) {
+                if (cancel_lanes8(sum, u) != 0) {
 #pragma unroll
                     for (int t = 0; t < 8; ++t) {
                         if (cancels(sum[t], u[t])) {
@@ -843,10 +877,10 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                 cv[t] += nv[t] >= tv[t] ? 1u : 0u;
             }
             uint2 wm, wv;
-            wm.x = cm[0] | (cm[1] << 8) | (cm[2] << 16) | (cm[3] << 24);
-            wm.y = cm[4] | (cm[5] << 8) | (cm[6] << 16) | (cm[7] << 24);
-            wv.x = cv[0] | (cv[1] << 8) | (cv[2] << 16) | (cv[3] << 24);
-            wv.y = cv[4] | (cv[5] << 8) | (cv[6] << 16) | (cv[7] << 24);
+            wm.x = pack4_u8(cm[0], cm[1], cm[2], cm[3]);
+            wm.y = pack4_u8(cm[4], cm[5], cm[6], cm[7]);
+            wv.x = pack4_u8(cv[0], cv[1], cv[2], cv[3]);
+            wv.y = pack4_u8(cv[4], cv[5], cv[6], cv[7]);
             *(RF_GLOBAL uint2*)(mW + eo) = wm;
             *(RF_GLOBAL uint2*)(vW + eo) = wv;
         }
@@ -992,10 +1026,7 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
 #pragma unroll
             for (int t = 0; t < 8; ++t) sum[t] = p[t] + u[t];
             if constexpr (!EXACT) {
-                bool risky = false;
-#pragma unroll
-                for (int t = 0; t < 8; ++t) risky |= cancels(sum[t], u[t]);
-                if (__builtin_amdgcn_ballot_w64(risky) != 0) {
+                if (cancel_lanes8(sum, u) != 0) {
 #pragma unroll
                     for (int t = 0; t < 8; ++t) {
                         if (cancels(sum[t], u[t]))

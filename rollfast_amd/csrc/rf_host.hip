@@ -149,8 +149,8 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const float*
                     for (int t = 0; t < 8; ++t) cc[t] = code_of(xr[j * 8 + t], e0 + t);
                 }
                 uint2 w;
-                w.x = cc[0] | (cc[1] << 8) | (cc[2] << 16) | (cc[3] << 24);
-                w.y = cc[4] | (cc[5] << 8) | (cc[6] << 16) | (cc[7] << 24);
+                w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
+                w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
                 *(uint2*)(values + e0) = w;
             }
             if (next_full) {
@@ -598,7 +598,7 @@ HostTables build_tables()
     std::memcpy(b + L_TS, ts, 1024);
     std::memcpy(b + L_TU, tu, 1024);
     if (!fill_cells(ts, false, b + L_CANDS, ht.error)) return ht;
-    if (!fill_cells(ts, true, b + L_CANDS + NCELL_PAD, ht.error)) return ht;
+    if (!fill_cells(ts, true, b + L_CANDS + CANDS_SIGN_STRIDE, ht.error)) return ht;
     if (!fill_cells(tu, false, b + L_CANDU, ht.error)) return ht;
     return ht;
 }
@@ -627,7 +627,7 @@ uint32_t host_table_code(const uint8_t* tb, int32_t quantizer, float n)
         cand = tb[L_CANDU + idx];
         std::memcpy(&t, tb + L_TU + cand * 4u, 4);
     } else {
-        cand = tb[L_CANDS + (nb >> 31) * NCELL_PAD + idx];
+        cand = tb[L_CANDS + (nb >> 31) * CANDS_SIGN_STRIDE + idx];
         std::memcpy(&t, tb + L_TS + cand * 4u, 4);
     }
     return cand + (n >= t ? 1u : 0u);

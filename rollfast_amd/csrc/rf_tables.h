@@ -20,13 +20,16 @@
 // builder checks this and refuses to produce tables otherwise.  Cells below
 // CELL_LO all map to CELL_LO (no threshold lies below 2^-23 in magnitude).
 //
-// Byte layout (identical in global memory and in LDS):
-//   [L_CBS]      f32 cb_signed[256]
-//   [L_CBU]      f32 cb_unsigned[256]
+// Byte layout (identical in global memory and in LDS).  The two sign halves
+// of the signed candidates sit CANDS_SIGN_STRIDE (a power of two) apart, so
+// a lookup forms its index as ((bits(n) >> 31) << 13) | cell with one
+// shift-and-or; the threshold tables fill the gap between the halves.
+//   [L_CANDS]    u8  signed candidates, n >= 0    [NCELL_PAD]
 //   [L_TS]       f32 signed thresholds T[256]     (value space, +inf padded)
 //   [L_TU]       f32 unsigned thresholds T[256]
-//   [L_CANDS]    u8  signed candidates, n >= 0    [NCELL_PAD]
-//   [L_CANDS + NCELL_PAD]  signed candidates, n < 0
+//   [L_CANDS + CANDS_SIGN_STRIDE]  signed candidates, n < 0
+//   [L_CBS]      f32 cb_signed[256]
+//   [L_CBU]      f32 cb_unsigned[256]
 //   [L_CANDU]    u8  unsigned candidates          [NCELL_PAD]
 #pragma once
 #include <stdint.h>
@@ -39,14 +42,18 @@ constexpr uint32_t CELL_HI = 0x7F00;   // bits(1.0f) >> 15
 constexpr uint32_t NCELL = CELL_HI - CELL_LO + 1;
 constexpr uint32_t NCELL_PAD = (NCELL + 15u) & ~15u;
 
-constexpr uint32_t L_CBS = 0;
-constexpr uint32_t L_CBU = 1024;
-constexpr uint32_t L_TS = 2048;
-constexpr uint32_t L_TU = 3072;
-constexpr uint32_t L_CANDS = 4096;
-constexpr uint32_t L_CANDU = L_CANDS + 2 * NCELL_PAD;
+constexpr uint32_t CANDS_SIGN_SHIFT = 13;
+constexpr uint32_t CANDS_SIGN_STRIDE = 1u << CANDS_SIGN_SHIFT;
+constexpr uint32_t L_CANDS = 0;
+constexpr uint32_t L_TS = L_CANDS + NCELL_PAD;
+constexpr uint32_t L_TU = L_TS + 1024;
+constexpr uint32_t L_CBS = L_CANDS + CANDS_SIGN_STRIDE + NCELL_PAD;
+constexpr uint32_t L_CBU = L_CBS + 1024;
+constexpr uint32_t L_CANDU = L_CBU + 1024;
 constexpr uint32_t TABLE_BYTES = L_CANDU + NCELL_PAD;
-static_assert(TABLE_BYTES % 16 == 0, "tables are copied in 16-byte words");
+static_assert(NCELL_PAD <= CANDS_SIGN_STRIDE, "a cell index fits below the sign bit");
+static_assert(L_TU + 1024 <= L_CANDS + CANDS_SIGN_STRIDE, "thresholds fit between the sign halves");
+static_assert(NCELL_PAD % 16 == 0 && TABLE_BYTES % 16 == 0, "tables are copied in 16-byte words");
 
 // Fast requantization is exact when the block scale s satisfies
 // FAST_SCALE_MIN <= s < inf: the reciprocal-and-correct division
