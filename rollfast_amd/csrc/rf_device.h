@@ -78,13 +78,31 @@ struct Seg {
     int64_t first;  // first block (quantized) or chunk (fallback) index in the leaf
     int32_t leaf;
     int32_t kind;
-    int64_t pad;
+    int32_t nseg;   // the list's sentinel index (its segment count), in every record
+    int32_t reserved;
 };
 static_assert(sizeof(Seg) == 32, "Seg is 32 bytes");
 
 typedef void (*adam_kernel_t)(const rf_adam8_leaf*, const Seg*, int64_t, KHp, const uint4*);
 
 // ============================================================ helpers ====
+// The segment of unit u (segs[s].unit_start <= u < segs[s + 1].unit_start),
+// searched upward from s, which must not lie past it.  A wave's first unit
+// and its strides over many small leaves cost a binary search (about
+// log2(nseg) dependent scalar loads) instead of a walk over every segment
+// in between; a unit in the same segment as the last costs one load.
+__device__ __forceinline__ int32_t seek_seg(const Seg* __restrict__ segs, int32_t nseg, int32_t s, int64_t u)
+{
+    if (segs[s + 1].unit_start > u) return s;
+    int32_t lo = s + 1, hi = nseg;  // segs[lo].unit_start <= u < segs[hi].unit_start (the sentinel's)
+    while (hi - lo > 1) {
+        const int32_t mid = (lo + hi) >> 1;
+        if (segs[mid].unit_start <= u) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 // f32 -> bf16 round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
@@ -1148,8 +1166,9 @@ __device__ void reject_units(const rf_adam8_leaf* __restrict__ leaves, const Seg
 {
     const int lane = threadIdx.x & (WAVE - 1);
     int32_t s = 0;
+    const int32_t nseg = segs[0].nseg;
     for (int64_t u = wave; u < total_units; u += nwaves) {
-        while (segs[s + 1].unit_start <= u) ++s;
+        s = seek_seg(segs, nseg, s, u);
         const Seg sg = segs[s];
         const rf_adam8_leaf& L = leaves[sg.leaf];
         const int64_t span = (sg.kind == KIND_QFAST || sg.kind == KIND_QGEN) ? (int64_t)L.block_size : CHUNK;
@@ -1186,6 +1205,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + wave_in_wg;
     const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
     int32_t s = 0;
+    const int32_t nseg = segs[0].nseg;
     int32_t cur_leaf = -1;
     UnitCtx c;
     c.lds = lds;
@@ -1203,7 +1223,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     ChunkSlots<PT, GT> sl;
     bool have0 = false;  // slot 0 holds chunk 0 of unit u
     for (int64_t u = wave; u < total_units; u += nwaves) {
-        while (segs[s + 1].unit_start <= u) ++s;
+        s = seek_seg(segs, nseg, s, u);
         const Seg sg = segs[s];
         if (sg.leaf != cur_leaf) {
             cur_leaf = sg.leaf;
@@ -1237,6 +1257,7 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
     const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
     const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
     int32_t s = 0;
+    const int32_t nseg = segs[0].nseg;
     int32_t cur_leaf = -1;
     UnitCtx c;
     c.lds = lds;
@@ -1252,7 +1273,7 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
     rf_adam8_leaf L;
     KHp hl = h;  // the current leaf's scalars (its group's, in a grouped launch)
     for (int64_t u = wave; u < total_units; u += nwaves) {
-        while (segs[s + 1].unit_start <= u) ++s;
+        s = seek_seg(segs, nseg, s, u);
         const Seg sg = segs[s];
         if (sg.leaf != cur_leaf) {
             cur_leaf = sg.leaf;

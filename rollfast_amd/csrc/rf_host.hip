@@ -354,8 +354,9 @@ __global__ __launch_bounds__(WG) void k_gnorm_partial(const rf_adam8_leaf* __res
     const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
     const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
     int32_t s = 0;
+    const int32_t nseg = nsegs[0].nseg;
     for (int64_t u = wave; u < nunits; u += nwaves) {
-        while (nsegs[s + 1].unit_start <= u) ++s;
+        s = seek_seg(nsegs, nseg, s, u);
         const Seg sg = nsegs[s];
         const rf_adam8_leaf& L = leaves[sg.leaf];
         const int64_t e_begin = (u - sg.unit_start) * NORM_UNIT;
@@ -809,6 +810,14 @@ rf_status validate_leaf(const rf_adam8_leaf& L, int32_t i, int32_t apply)
     return RF_OK;
 }
 
+// Stores the sentinel's index (the list's last record) in every record of a
+// work list, for the kernels' binary search.
+void mark_list(std::vector<Seg>& list)
+{
+    const int32_t n = (int32_t)list.size() - 1;
+    for (Seg& sg : list) sg.nseg = n;
+}
+
 bool leaf_vec_ok(const rf_adam8_leaf& L, int32_t apply)
 {
     const uintptr_t a = 16;
@@ -909,12 +918,13 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     for (int combo = 4; combo >= 0; --combo) {
         if (gunits[combo] == 0) continue;
         groups.push_back({combo == 4 ? -1 : combo, (int64_t)segs.size(), gunits[combo]});
-        segs.insert(segs.end(), gsegs[combo].begin(), gsegs[combo].end());
         Seg sentinel{};
         sentinel.unit_start = gunits[combo];
         sentinel.leaf = -1;
         sentinel.kind = -1;
-        segs.push_back(sentinel);
+        gsegs[combo].push_back(sentinel);
+        mark_list(gsegs[combo]);
+        segs.insert(segs.end(), gsegs[combo].begin(), gsegs[combo].end());
         units += gunits[combo];
     }
     if (segs.empty()) {
@@ -942,6 +952,7 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
         sentinel.leaf = -1;
         sentinel.kind = -1;
         nsegs.push_back(sentinel);
+        mark_list(nsegs);
     }
 
     int device = 0;
@@ -1359,6 +1370,7 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
     sentinel.leaf = -1;
     sentinel.kind = -1;
     nsegs.push_back(sentinel);
+    mark_list(nsegs);
     DevState* ds = nullptr;
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;

@@ -119,3 +119,33 @@ def test_plan_run_on_creation_table_and_info():
             _compare(b2, h2)
     finally:
         assert lib.rf_adam8_plan_destroy(plan) == _lib.RF_OK
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 2047, 2 * 2048 + 512, 3 * 2048 + 1, 5 * 2048 + 77])
+def test_partial_last_block_ignores_old_padding_codes(n):
+    """A leaf's partial last block: the padding's old codes do not enter the
+    new moments (quantize_blocks pads the new moments with zeros,
+    adam8.py:137-141), so garbage padding codes give the oracle's codes,
+    scales and params bit for bit, and the padding comes back as zero codes.
+    Sizes from one element to several whole blocks plus a tail."""
+    import torch
+
+    from rollfast_amd import _lib
+
+    L, bufs, host = _leaf_and_buffers(n, 11)
+    nb = -(-n // 2048)
+    rng = np.random.default_rng(5)
+    pad = np.arange(n, nb * 2048)
+    for key in ("mc", "vc"):
+        junk = rng.integers(0, 256, pad.size, dtype=np.uint8)
+        host[key][pad] = junk
+        bufs[key][torch.as_tensor(pad, device="cuda")] = torch.as_tensor(junk, device="cuda")
+    table = (_lib.Adam8Leaf * 1)(L)
+    for step in range(1, 4):
+        hp, o = _hparams(step)
+        st = _lib.lib().rf_adam8_step(table, 1, 1, ctypes.byref(hp), _lib.stream_ptr())
+        assert st == _lib.RF_OK, _lib.lib().rf_last_error()
+        torch.cuda.synchronize()
+        _oracle_step(host, o, n)
+        _compare(bufs, host)
+        assert (to_host(bufs["mc"])[pad] == 127).all() and (to_host(bufs["vc"])[pad] == 0).all()
