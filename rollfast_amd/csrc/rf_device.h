@@ -65,6 +65,7 @@ struct KHp {
     float wd, wd16;           // f32(wd) and bf16(wd) as f32 (weak-typed decay of bf16 params)
     float neg_lr;             // f32(-lr), or 1.0 when the chain has no learning-rate scale
     uint32_t flags;
+    int32_t run;              // fast kernel: consecutive units a wave takes before its grid stride (>= 1)
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;
     const float* clip;        // device (scale, norm) of global-norm clipping, or null
     const float* gate;        // device flag: 1 = every grad finite, 0 = reject the step; null = no gate
@@ -1222,24 +1223,30 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     KHp hl = h;  // the current leaf's scalars (its group's, in a grouped launch)
     ChunkSlots<PT, GT> sl;
     bool have0 = false;  // slot 0 holds chunk 0 of unit u
-    for (int64_t u = wave; u < total_units; u += nwaves) {
-        s = seek_seg(segs, nseg, s, u);
-        const Seg sg = segs[s];
-        if (sg.leaf != cur_leaf) {
-            cur_leaf = sg.leaf;
-            L = leaves[cur_leaf];
-            group_hparams(hl, h, L);
-            leaf_context(c, L, hl, MSR, PSR);
+    // Wave w takes runs of h.run consecutive units: run r = w, w + nwaves, ...
+    const int64_t run = h.run;
+    const int64_t nruns = (total_units + run - 1) / run;
+    for (int64_t r = wave; r < nruns; r += nwaves) {
+        const int64_t u_end = min(r * run + run, total_units);
+        for (int64_t u = r * run; u < u_end; ++u) {
+            s = seek_seg(segs, nseg, s, u);
+            const Seg sg = segs[s];
+            if (sg.leaf != cur_leaf) {
+                cur_leaf = sg.leaf;
+                L = leaves[cur_leaf];
+                group_hparams(hl, h, L);
+                leaf_context(c, L, hl, MSR, PSR);
+            }
+            // The next unit of this wave, when it is a block of the same leaf
+            // (this kernel's units are all full blocks; one segment per leaf).
+            const int64_t un = u + 1 < u_end ? u + 1 : (r + nwaves) * run;
+            int64_t next_blk = -1;
+            if (RF_PREFETCH_NEXT && un < total_units && un < segs[s + 1].unit_start)
+                next_blk = sg.first + (un - sg.unit_start);
+            dispatch_qfast<PT, GT, APPLY, MSR, PSR, NEST, EXACT>(c, L, sg.first + (u - sg.unit_start), hl, sl,
+                                                                 have0, next_blk);
+            have0 = next_blk >= 0;
         }
-        // The next unit of this wave, when it is a block of the same leaf
-        // (this kernel's units are all full blocks; one segment per leaf).
-        const int64_t un = u + nwaves;
-        int64_t next_blk = -1;
-        if (RF_PREFETCH_NEXT && un < total_units && un < segs[s + 1].unit_start)
-            next_blk = sg.first + (un - sg.unit_start);
-        dispatch_qfast<PT, GT, APPLY, MSR, PSR, NEST, EXACT>(c, L, sg.first + (u - sg.unit_start), hl, sl, have0,
-                                                             next_blk);
-        have0 = next_blk >= 0;
     }
 }
 
