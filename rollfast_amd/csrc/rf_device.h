@@ -525,13 +525,13 @@ __device__ __forceinline__ uint32_t new_param_bits(float p, float u, uint32_t rb
 
 // One element of the update for the generic (scalar) paths: writes the new
 // param (fused) or the f32 update.
+// `p` is the element's param, already loaded where APPLY or decay needs it
+// (0 otherwise).
 template <bool APPLY, bool PSR, bool NEST, bool EXACT>
 __device__ __forceinline__ void update_one(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e, const KHp& h,
-                                           float mm, float vv, float g)
+                                           float mm, float vv, float g, float p)
 {
     float u = adam_direction<NEST, EXACT>(h, mm, vv, g);
-    const bool need_p = APPLY || c.wd_mode != WD_OFF;
-    const float p = need_p ? load1(L.param, L.param_dtype, e) : 0.0f;
     u = decay_and_scale(h, u, p, c.wd_mode);
     if constexpr (APPLY && !EXACT) {
         if (cancels(p + u, u)) u = decay_and_scale(h, adam_direction<NEST, true>(h, mm, vv, g), p, c.wd_mode);
@@ -549,13 +549,40 @@ __device__ __forceinline__ void update_one(const UnitCtx& c, const rf_adam8_leaf
     }
 }
 
+// Element-wise units take each lane's elements EW_BATCH at a time and issue
+// all of a batch's loads before its arithmetic: one memory round trip per
+// batch instead of one per element.
+constexpr int EW_BATCH = 4;
+
+// Old codes and grads of lane elements j0 + k*WAVE (k < B) of the block at
+// `base`; elements at or past nvalid read as code 0 and grad 0.
+template <int B>
+__device__ __forceinline__ void load_batch(const UnitCtx& c, const rf_adam8_leaf& L, int64_t base, int64_t j0,
+                                           int64_t nvalid, uint32_t (&cm)[B], uint32_t (&cv)[B], float (&g)[B])
+{
+    const uint8_t* mcodes = (const uint8_t*)L.mu;
+    const uint8_t* vcodes = (const uint8_t*)L.nu;
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+        const int64_t j = j0 + k * WAVE;
+        cm[k] = cv[k] = 0u;
+        g[k] = 0.0f;
+        if (j < nvalid) {
+            cm[k] = mcodes[base + j];
+            cv[k] = vcodes[base + j];
+            g[k] = load_grad1(c, L, base + j);
+        }
+    }
+}
+
 // Requantization of one block by the literal search (or moment SR): the new
 // moments are recomputed from the old codes and scales, which are still in
 // place, with the reference's NaN-propagating absmax (adam8.py:142), then
 // every element is coded and the new scales are written.  Used for blocks of
 // any size, blocks whose scale leaves the fast range (zero-free tiny, Inf,
-// NaN) and moment SR.
-template <bool MSR>
+// NaN) and moment SR.  B: elements per lane per batch (1 inside the fast
+// kernel, where this path is rare and registers are scarce).
+template <bool MSR, int B = EW_BATCH>
 __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h)
 {
     const int lane = threadIdx.x & (WAVE - 1);
@@ -569,12 +596,19 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
     uint8_t* mcodes = (uint8_t*)L.mu;
     uint8_t* vcodes = (uint8_t*)L.nu;
     uint32_t am = 0, av = 0;
-    for (int64_t j = lane; j < nvalid; j += WAVE) {
-        const int64_t e = base + j;
-        float mm, vv;
-        ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, load_grad1(c, L, e), mm, vv);
-        am = max(am, __float_as_uint(mm) & 0x7FFFFFFFu);
-        av = max(av, __float_as_uint(vv));
+    for (int64_t j0 = lane; j0 < nvalid; j0 += B * WAVE) {
+        uint32_t cm[B], cv[B];
+        float g[B];
+        load_batch<B>(c, L, base, j0, nvalid, cm, cv, g);
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+            if (j0 + k * WAVE < nvalid) {
+                float mm, vv;
+                ema(h, cbs[cm[k]] * sm_old, cbu[cv[k]] * sv_old, g[k], mm, vv);
+                am = max(am, __float_as_uint(mm) & 0x7FFFFFFFu);
+                av = max(av, __float_as_uint(vv));
+            }
+        }
     }
     am = wave_max_u32(am);
     av = wave_max_u32(av);
@@ -584,27 +618,35 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
     const bool fast_v = !MSR && block_is_fast(av, sv);
     const float rsm = 1.0f / sm;
     const float rsv = 1.0f / sv;
-    for (int64_t j = lane; j < bs; j += WAVE) {
-        const int64_t e = base + j;
-        float mm = 0.0f, vv = 0.0f;
-        if (j < nvalid) ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, load_grad1(c, L, e), mm, vv);
-        uint32_t cm, cv;
-        if (fast_m) {
-            cm = code_signed_fast(c.lds, mm, sm, rsm);
-        } else {
-            uint32_t bits = 0;
-            if constexpr (MSR) bits = c.fed ? L.mu_bits[e] : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
-            cm = code_literal(cbs, mm, sm, MSR, bits);
+    for (int64_t j0 = lane; j0 < bs; j0 += B * WAVE) {
+        uint32_t om[B], ov[B];
+        float g[B];
+        load_batch<B>(c, L, base, j0, nvalid, om, ov, g);
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+            const int64_t j = j0 + k * WAVE;
+            if (j >= bs) continue;
+            const int64_t e = base + j;
+            float mm = 0.0f, vv = 0.0f;  // zero padding past the leaf's end
+            if (j < nvalid) ema(h, cbs[om[k]] * sm_old, cbu[ov[k]] * sv_old, g[k], mm, vv);
+            uint32_t cm, cv;
+            if (fast_m) {
+                cm = code_signed_fast(c.lds, mm, sm, rsm);
+            } else {
+                uint32_t bits = 0;
+                if constexpr (MSR) bits = c.fed ? L.mu_bits[e] : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
+                cm = code_literal(cbs, mm, sm, MSR, bits);
+            }
+            if (fast_v) {
+                cv = code_unsigned_fast(c.lds, vv, sv, rsv);
+            } else {
+                uint32_t bits = 0;
+                if constexpr (MSR) bits = c.fed ? L.nu_bits[e] : jax_bits(c.knu0, c.knu1, (uint64_t)e);
+                cv = code_literal(cbu, vv, sv, MSR, bits);
+            }
+            mcodes[e] = (uint8_t)cm;
+            vcodes[e] = (uint8_t)cv;
         }
-        if (fast_v) {
-            cv = code_unsigned_fast(c.lds, vv, sv, rsv);
-        } else {
-            uint32_t bits = 0;
-            if constexpr (MSR) bits = c.fed ? L.nu_bits[e] : jax_bits(c.knu0, c.knu1, (uint64_t)e);
-            cv = code_literal(cbu, vv, sv, MSR, bits);
-        }
-        mcodes[e] = (uint8_t)cm;
-        vcodes[e] = (uint8_t)cv;
     }
     if (lane == 0) {
         L.mu_scales[blk] = sm;
@@ -908,7 +950,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             L.nu_scales[blk] = sv;
         }
     } else {
-        requant_literal<MSR>(c, L, blk, h);
+        requant_literal<MSR, 1>(c, L, blk, h);
     }
 }
 
@@ -944,15 +986,26 @@ __device__ __forceinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf&
     const float* cbu = (const float*)(c.lds + L_CBU);
     const float sm_old = L.mu_scales[blk];
     const float sv_old = L.nu_scales[blk];
-    const uint8_t* mcodes = (const uint8_t*)L.mu;
-    const uint8_t* vcodes = (const uint8_t*)L.nu;
 
-    for (int64_t j = lane; j < nvalid; j += WAVE) {
-        const int64_t e = base + j;
-        const float g = load_grad1(c, L, e);
-        float mm, vv;
-        ema(h, cbs[mcodes[e]] * sm_old, cbu[vcodes[e]] * sv_old, g, mm, vv);
-        update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g);
+    const bool need_p = APPLY || c.wd_mode != WD_OFF;
+    for (int64_t j0 = lane; j0 < nvalid; j0 += EW_BATCH * WAVE) {
+        uint32_t cm[EW_BATCH], cv[EW_BATCH];
+        float g[EW_BATCH], p[EW_BATCH];
+        load_batch<EW_BATCH>(c, L, base, j0, nvalid, cm, cv, g);
+#pragma unroll
+        for (int k = 0; k < EW_BATCH; ++k) {
+            const int64_t j = j0 + k * WAVE;
+            p[k] = (need_p && j < nvalid) ? load1(L.param, L.param_dtype, base + j) : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < EW_BATCH; ++k) {
+            const int64_t j = j0 + k * WAVE;
+            if (j < nvalid) {
+                float mm, vv;
+                ema(h, cbs[cm[k]] * sm_old, cbu[cv[k]] * sv_old, g[k], mm, vv);
+                update_one<APPLY, PSR, NEST, EXACT>(c, L, base + j, h, mm, vv, g[k], p[k]);
+            }
+        }
     }
     requant_literal<MSR>(c, L, blk, h);
 }
@@ -968,20 +1021,37 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
     const int64_t end = min(base + CHUNK, L.size);
     const int32_t mdt = L.moment_kind == RF_MOMENT_BF16 ? RF_BF16 : RF_F32;
     const bool store_sr = mdt == RF_BF16 && (L.flags & RF_LEAF_STORE_SR);
-    for (int64_t e = base + lane; e < end; e += WAVE) {
-        const float g = load_grad1(c, L, e);
-        float mm, vv;
-        ema(h, load1(L.mu, mdt, e), load1(L.nu, mdt, e), g, mm, vv);
-        update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g);
-        if (store_sr) {
-            // optim/adam.py:219-222: _tree_stochastic_cast(moments, bfloat16, k1 | k2)
-            const uint32_t bm = c.fed ? L.mu_bits[e] : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
-            const uint32_t bv = c.fed ? L.nu_bits[e] : jax_bits(c.knu0, c.knu1, (uint64_t)e);
-            ((uint16_t*)L.mu)[e] = (uint16_t)sr_bf16(mm, bm);
-            ((uint16_t*)L.nu)[e] = (uint16_t)sr_bf16(vv, bv);
-        } else {
-            store1(L.mu, mdt, e, mm);  // adam8.py:688 moment.astype(fallback_dtype)
-            store1(L.nu, mdt, e, vv);
+    const bool need_p = APPLY || c.wd_mode != WD_OFF;
+    for (int64_t e0 = base + lane; e0 < end; e0 += EW_BATCH * WAVE) {
+        float g[EW_BATCH], mo[EW_BATCH], vo[EW_BATCH], p[EW_BATCH];
+#pragma unroll
+        for (int k = 0; k < EW_BATCH; ++k) {
+            const int64_t e = e0 + k * WAVE;
+            g[k] = mo[k] = vo[k] = p[k] = 0.0f;
+            if (e < end) {
+                g[k] = load_grad1(c, L, e);
+                mo[k] = load1(L.mu, mdt, e);
+                vo[k] = load1(L.nu, mdt, e);
+                if (need_p) p[k] = load1(L.param, L.param_dtype, e);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < EW_BATCH; ++k) {
+            const int64_t e = e0 + k * WAVE;
+            if (e >= end) continue;
+            float mm, vv;
+            ema(h, mo[k], vo[k], g[k], mm, vv);
+            update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g[k], p[k]);
+            if (store_sr) {
+                // optim/adam.py:219-222: _tree_stochastic_cast(moments, bfloat16, k1 | k2)
+                const uint32_t bm = c.fed ? L.mu_bits[e] : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
+                const uint32_t bv = c.fed ? L.nu_bits[e] : jax_bits(c.knu0, c.knu1, (uint64_t)e);
+                ((uint16_t*)L.mu)[e] = (uint16_t)sr_bf16(mm, bm);
+                ((uint16_t*)L.nu)[e] = (uint16_t)sr_bf16(vv, bv);
+            } else {
+                store1(L.mu, mdt, e, mm);  // adam8.py:688 moment.astype(fallback_dtype)
+                store1(L.nu, mdt, e, vv);
+            }
         }
     }
 }
