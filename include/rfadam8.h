@@ -258,6 +258,36 @@ typedef struct rf_clip_leaf {
 RF_API rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, float max_norm,
                                         float* stats, void* stream);
 
+/* One leaf of the Magma pass of scale_by_adam(use_magma=True)
+ * (optim/adam.py:127-131, :203-217; optim/magma.py:15-132). */
+typedef struct rf_magma_leaf {
+    const void* grad;   /* [size] grad_dtype: the raw gradient the step receives */
+    const void* mu;     /* [size] mu_dtype: the first moment before this step's EMA */
+    float* updates;     /* [size] f32: the step's update, scaled in place by rf_magma_scale */
+    int64_t size;
+    int32_t grad_dtype; /* RF_F32 | RF_BF16 */
+    int32_t mu_dtype;   /* RF_F32 | RF_BF16 */
+    int32_t key_index;  /* the leaf's position among all leaves of the update tree */
+    int32_t reserved;   /* 0 */
+} rf_magma_leaf;
+
+/* magma.py:98-106 before the step: per leaf i, sums[3i..3i+2] (device f64) =
+ * (sum g*m', sum g*g, sum m'*m') with m' = f32(b1*mu) + f32(one_minus_b1*g),
+ * the step's new first moment (utils.py:327-335, :437-467).  Enqueue it
+ * before the step, which overwrites mu.  Scratch: hipMallocAsync on stream. */
+RF_API rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, float b1, float one_minus_b1,
+                                 double* sums, void* stream);
+
+/* magma.py:106-124 after the step: per leaf, the f32 cosine of the sums
+ * (denominator at least 1e-12, NaN -> 0, clipped to [-1, 1]), the score
+ * s = 0.9 * s_prev + 0.1 * sigmoid(cos / tau) written over scores[i] (device
+ * f32), the Bernoulli mask m = uniform(split(key, n_keys)[key_index]) < p,
+ * and updates = neg_lr * ((m * s) * updates) (neg_lr = 1: no learning-rate
+ * scale, optax scale_by_learning_rate otherwise).  Scratch: hipMallocAsync. */
+RF_API rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const double* sums, float* scores,
+                                float p, float tau, uint32_t key0, uint32_t key1, int32_t n_keys, float neg_lr,
+                                void* stream);
+
 /* Host-side: the 256 f32 values of a dynamic codebook (adam8.py:461-503). */
 RF_API rf_status rf_codebook(int32_t quantizer, float* out256);
 

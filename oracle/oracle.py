@@ -99,6 +99,50 @@ def get_threads() -> int:
     return int(lib().orc_get_threads())
 
 
+# ----------------------------------------------------------------- Magma --
+def uniform01(bits: np.ndarray) -> np.ndarray:
+    """jax.random.uniform(float32) from raw bits (the mantissa fill of
+    [1, 2) minus 1; jax random.py _uniform)."""
+    b = (np.asarray(bits, np.uint32) >> np.uint32(9)) | np.uint32(0x3F800000)
+    return (b.view(np.float32) - np.float32(1.0)).astype(np.float32)
+
+
+def magma_leaf(g, mu_new, s_prev, leaf_key, p: float, tau: float):
+    """rollfast optim/magma.py:98-124 for one real leaf: the f32 cosine of the
+    raw gradient and the step's new first moment, the score
+    s = 0.9 * s_prev + 0.1 * sigmoid(cos / tau) and the Bernoulli keep flag
+    uniform(leaf_key) < p.  The three sums are float64 sums rounded once to
+    f32 (the reference's f32 jnp.vdot adds its own summation rounding);
+    sigmoid is evaluated in float64 and rounded.  Returns (s_new as f32,
+    keep as bool)."""
+    g64 = np.asarray(g, np.float64).reshape(-1)
+    m64 = np.asarray(mu_new, np.float64).reshape(-1)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        dot = np.float32(np.dot(g64, m64))
+        ng = np.float32(np.dot(g64, g64))
+        nm = np.float32(np.dot(m64, m64))
+        prod = np.float32(np.sqrt(ng, dtype=np.float32) * np.sqrt(nm, dtype=np.float32))
+        denom = prod if np.isnan(prod) else np.maximum(prod, np.float32(1e-12))
+        cos = np.float32(dot / denom)
+    cos = np.float32(0.0) if np.isnan(cos) else np.float32(np.clip(cos, -1.0, 1.0))
+    x = np.float32(cos / np.float32(tau))
+    s_tilde = np.float32(1.0 / (1.0 + np.exp(-np.float64(x))))
+    s_new = np.float32(np.float32(np.float32(0.9) * np.float32(s_prev)) + np.float32(np.float32(0.1) * s_tilde))
+    keep = bool(uniform01(random_bits(leaf_key, 1))[0] < np.float32(p))
+    return s_new, keep
+
+
+def magma_apply(delta: np.ndarray, s_new, keep: bool, neg_lr=None) -> np.ndarray:
+    """magma.py:120-122 ``m_mask * s_new * delta`` in f32 (m in {0, 1}), then
+    optax scale_by_learning_rate's ``(-lr) * u`` when ``neg_lr`` is given."""
+    f = np.float32(np.float32(1.0 if keep else 0.0) * np.float32(s_new))
+    with np.errstate(invalid="ignore", over="ignore"):
+        out = (f * np.asarray(delta, np.float32)).astype(np.float32)
+        if neg_lr is not None:
+            out = (np.float32(neg_lr) * out).astype(np.float32)
+    return out
+
+
 # ------------------------------------------------------------------ PRNG --
 def threefry2x32(key, counter):
     y0, y1 = ctypes.c_uint32(), ctypes.c_uint32()

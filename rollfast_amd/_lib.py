@@ -106,6 +106,19 @@ class ClipLeaf(ctypes.Structure):
     ]
 
 
+class MagmaLeaf(ctypes.Structure):
+    _fields_ = [
+        ("grad", _p),
+        ("mu", _p),
+        ("updates", _p),
+        ("size", ctypes.c_int64),
+        ("grad_dtype", ctypes.c_int32),
+        ("mu_dtype", ctypes.c_int32),
+        ("key_index", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
 class ApplyLeaf(ctypes.Structure):
     _fields_ = [
         ("param", _p),
@@ -137,6 +150,8 @@ EXPORTS = (
     "rf_sr_bf16",
     "rf_apply_updates",
     "rf_clip_by_global_norm",
+    "rf_magma_reduce",
+    "rf_magma_scale",
     "rf_codebook",
     "rf_host_table_codes",
     "rf_version",
@@ -174,6 +189,9 @@ def lib() -> ctypes.CDLL:
     L.rf_blockwise_dequantize.argtypes = [i32, _p, _p, i64, i32, i32, _p, _p]
     L.rf_sr_bf16.argtypes = [_p, i64, u32, u32, _p, _p, _p]
     L.rf_apply_updates.argtypes = [ctypes.POINTER(ApplyLeaf), i32, i32, u32, u32, _p]
+    f32 = ctypes.c_float
+    L.rf_magma_reduce.argtypes = [ctypes.POINTER(MagmaLeaf), i32, f32, f32, _p, _p]
+    L.rf_magma_scale.argtypes = [ctypes.POINTER(MagmaLeaf), i32, _p, _p, f32, f32, u32, u32, i32, f32, _p]
     L.rf_codebook.argtypes = [i32, _p]
     L.rf_host_table_codes.argtypes = [i32, u32, i64, _p]
     for name in EXPORTS:

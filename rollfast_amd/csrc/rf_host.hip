@@ -438,6 +438,149 @@ __global__ void k_gnorm_finish(const double* __restrict__ leafsum, int32_t nseg,
     if (finite_out) *finite_out = finite ? 1 : 0;
 }
 
+// ---------------------------------------------------------------- Magma --
+// Momentum-aligned update masking of scale_by_adam(use_magma=True)
+// (optim/magma.py:15-132).  Work units are NORM_UNIT-element ranges of a
+// leaf; every leaf has a segment (empty leaves an empty one), so segment i is
+// leaf i.
+
+// 8 consecutive elements of a bf16 or f32 array as f32 (16-byte aligned).
+__device__ __forceinline__ void load8_dt(const void* base, int32_t dtype, int64_t e0, float (&x)[8])
+{
+    if (dtype == RF_BF16) load8<uint16_t>(base, e0, x);
+    else load8<float>(base, e0, x);
+}
+
+// Per-unit f64 partial sums of g*m', g*g and m'*m', m' = f32(b1*mu) +
+// f32(omb1*g): the step's new first moment (utils.py:437-467).
+__global__ __launch_bounds__(WG) void k_magma_partial(const rf_magma_leaf* __restrict__ leaves,
+                                                      const Seg* __restrict__ segs, int64_t nunits, float b1,
+                                                      float omb1, double* __restrict__ part)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    int32_t s = 0;
+    const int32_t nseg = segs[0].nseg;
+    for (int64_t u = wave; u < nunits; u += nwaves) {
+        s = seek_seg(segs, nseg, s, u);
+        const Seg sg = segs[s];
+        const rf_magma_leaf& L = leaves[sg.leaf];
+        const int64_t e_begin = (u - sg.unit_start) * NORM_UNIT;
+        const int64_t e_end = min(L.size, e_begin + NORM_UNIT);
+        double dot = 0.0, gg = 0.0, mm = 0.0;
+        auto add = [&](float g, float mp) {
+            const float t1 = b1 * mp;
+            const float t2 = omb1 * g;
+            const float m = t1 + t2;
+            dot += (double)g * (double)m;
+            gg += (double)g * (double)g;
+            mm += (double)m * (double)m;
+        };
+        if (e_end - e_begin == NORM_UNIT && ((uintptr_t)L.grad & 15u) == 0 && ((uintptr_t)L.mu & 15u) == 0) {
+            for (int64_t e0 = e_begin + lane * 8; e0 < e_end; e0 += 512) {
+                float g[8], mp[8];
+                load8_dt(L.grad, L.grad_dtype, e0, g);
+                load8_dt(L.mu, L.mu_dtype, e0, mp);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) add(g[t], mp[t]);
+            }
+        } else {
+            for (int64_t e = e_begin + lane; e < e_end; e += WAVE)
+                add(load1(L.grad, L.grad_dtype, e), load1(L.mu, L.mu_dtype, e));
+        }
+        dot = wave_sum_f64(dot);
+        gg = wave_sum_f64(gg);
+        mm = wave_sum_f64(mm);
+        if (lane == 0) {
+            part[3 * u] = dot;
+            part[3 * u + 1] = gg;
+            part[3 * u + 2] = mm;
+        }
+    }
+}
+
+// Leaf i's three sums from its units' partials.
+__global__ __launch_bounds__(WG) void k_magma_leaf(const Seg* __restrict__ segs, int32_t nseg,
+                                                   const double* __restrict__ part, double* __restrict__ sums)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    for (int64_t i = wave; i < nseg; i += nwaves) {
+        double acc[3] = {0.0, 0.0, 0.0};
+        for (int64_t u = segs[i].unit_start + lane; u < segs[i + 1].unit_start; u += WAVE)
+#pragma unroll
+            for (int k = 0; k < 3; ++k) acc[k] += part[3 * u + k];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) acc[k] = wave_sum_f64(acc[k]);
+        if (lane == 0) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) sums[3 * i + k] = acc[k];
+        }
+    }
+}
+
+// Per leaf (one thread each): the f32 cosine, the new score and the masked
+// factor (magma.py:98-122); scores[i] goes from s_prev to s_new.
+__global__ void k_magma_factor(const rf_magma_leaf* __restrict__ leaves, int32_t n, const double* __restrict__ sums,
+                               float* __restrict__ scores, float* __restrict__ factor, float p, float tau,
+                               uint32_t k0, uint32_t k1)
+{
+    const int32_t i = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= n) return;
+    const float dot = (float)sums[3 * i];
+    const float ng = (float)sums[3 * i + 1];
+    const float nm = (float)sums[3 * i + 2];
+    const float prod = sqrtf(ng) * sqrtf(nm);
+    const float denom = prod != prod ? prod : fmaxf(prod, 1e-12f);  // jnp.maximum keeps a NaN
+    float cs = dot / denom;
+    if (cs != cs) cs = 0.0f;                       // jnp.nan_to_num(nan=0.0)
+    cs = cs < -1.0f ? -1.0f : (cs > 1.0f ? 1.0f : cs);  // jnp.clip (an infinity lands on +-1)
+    const float s_tilde = 1.0f / (1.0f + expf(-(cs / tau)));  // jax.nn.sigmoid
+    const float a = 0.9f * scores[i];
+    const float b = 0.1f * s_tilde;
+    const float s_new = a + b;
+    // jax.random.bernoulli(split(key, n_keys)[key_index], p): uniform < p
+    uint32_t b0, b1;
+    jax_split(k0, k1, (uint32_t)leaves[i].key_index, b0, b1);
+    const bool keep = uniform_from_bits(jax_bits(b0, b1, 0)) < p;
+    scores[i] = s_new;
+    factor[i] = (keep ? 1.0f : 0.0f) * s_new;
+}
+
+// updates = neg_lr * (factor[leaf] * updates) over the same units.
+__global__ __launch_bounds__(WG) void k_magma_apply(const rf_magma_leaf* __restrict__ leaves,
+                                                    const Seg* __restrict__ segs, int64_t nunits,
+                                                    const float* __restrict__ factor, float neg_lr)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    int32_t s = 0;
+    const int32_t nseg = segs[0].nseg;
+    for (int64_t u = wave; u < nunits; u += nwaves) {
+        s = seek_seg(segs, nseg, s, u);
+        const Seg sg = segs[s];
+        float* up = leaves[sg.leaf].updates;
+        const float f = factor[sg.leaf];
+        const int64_t e_begin = (u - sg.unit_start) * NORM_UNIT;
+        const int64_t e_end = min(leaves[sg.leaf].size, e_begin + NORM_UNIT);
+        if (e_end - e_begin == NORM_UNIT && ((uintptr_t)up & 15u) == 0) {
+            for (int64_t e0 = e_begin + lane * 4; e0 < e_end; e0 += 256) {
+                float4 v = *(const float4*)(up + e0);
+                v.x = neg_lr * (f * v.x);
+                v.y = neg_lr * (f * v.y);
+                v.z = neg_lr * (f * v.z);
+                v.w = neg_lr * (f * v.w);
+                *(float4*)(up + e0) = v;
+            }
+        } else {
+            for (int64_t e = e_begin + lane; e < e_end; e += WAVE) up[e] = neg_lr * (f * up[e]);
+        }
+    }
+}
+
 // Standalone clip_by_global_norm: out = grad * scale per leaf (blockIdx.y =
 // leaf), with the leaf-dtype semantics of the fused path.
 __global__ __launch_bounds__(WG) void k_clip_scale(const rf_clip_leaf* __restrict__ leaves,
@@ -1448,6 +1591,145 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
     }
     hipError_t ef = hipFreeAsync(scratch, s);
     if (e != hipSuccess) return fail(RF_ERR_HIP, std::string("rf_clip_by_global_norm: ") + hipGetErrorString(e));
+    if (ef != hipSuccess) return fail(RF_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(ef));
+    return RF_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Validates a Magma leaf table and builds its work list (segment i = leaf i).
+rf_status magma_list(const rf_magma_leaf* leaves, int32_t n_leaves, bool need_updates, std::vector<Seg>& segs,
+                     int64_t& nunits)
+{
+    if (n_leaves < 0 || (n_leaves > 0 && !leaves)) return fail(RF_ERR_INVALID, "bad leaf table");
+    nunits = 0;
+    segs.clear();
+    for (int32_t i = 0; i < n_leaves; ++i) {
+        const rf_magma_leaf& L = leaves[i];
+        if (L.size < 0) return fail(RF_ERR_INVALID, "negative size");
+        if ((L.grad_dtype != RF_F32 && L.grad_dtype != RF_BF16) || (L.mu_dtype != RF_F32 && L.mu_dtype != RF_BF16))
+            return fail(RF_ERR_UNSUPPORTED, "grad and moment dtypes must be f32 or bf16");
+        if (L.size > 0 && (!L.grad || !L.mu || (need_updates && !L.updates)))
+            return fail(RF_ERR_INVALID, "null buffer");
+        Seg sg{};
+        sg.unit_start = nunits;
+        sg.leaf = i;
+        segs.push_back(sg);
+        nunits += (L.size + NORM_UNIT - 1) / NORM_UNIT;
+    }
+    Seg sentinel{};
+    sentinel.unit_start = nunits;
+    sentinel.leaf = -1;
+    sentinel.kind = -1;
+    segs.push_back(sentinel);
+    mark_list(segs);
+    return RF_OK;
+}
+
+// Stages the leaf table and the work list in one stream-ordered scratch
+// allocation of `extra` more bytes (returned at `*tail`).
+rf_status magma_stage(const rf_magma_leaf* leaves, int32_t n_leaves, const std::vector<Seg>& segs, size_t extra,
+                      hipStream_t s, uint8_t** scratch, uint8_t** tail)
+{
+    const size_t o_sg = (sizeof(rf_magma_leaf) * (size_t)std::max(n_leaves, 1) + 15) & ~(size_t)15;
+    const size_t o_tail = (o_sg + sizeof(Seg) * segs.size() + 15) & ~(size_t)15;
+    HIP_TRY(hipMallocAsync((void**)scratch, o_tail + std::max<size_t>(extra, 16), s));
+    std::vector<uint8_t> host(o_tail);
+    if (n_leaves > 0) std::memcpy(host.data(), leaves, sizeof(rf_magma_leaf) * (size_t)n_leaves);
+    std::memcpy(host.data() + o_sg, segs.data(), sizeof(Seg) * segs.size());
+    // From pageable memory: returns once the source is consumed.
+    const hipError_t e = hipMemcpyAsync(*scratch, host.data(), o_tail, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) {
+        (void)hipFreeAsync(*scratch, s);
+        return fail(RF_ERR_HIP, std::string("hipMemcpyAsync: ") + hipGetErrorString(e));
+    }
+    *tail = *scratch + o_tail;
+    return RF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, float b1, float one_minus_b1, double* sums,
+                          void* stream)
+{
+    std::vector<Seg> segs;
+    int64_t nunits = 0;
+    rf_status st = magma_list(leaves, n_leaves, false, segs, nunits);
+    if (st != RF_OK) return st;
+    if (n_leaves == 0) return RF_OK;
+    if (!sums) return fail(RF_ERR_INVALID, "null sums");
+    DevState* ds = nullptr;
+    st = device_state(&ds);
+    if (st != RF_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t *scratch = nullptr, *tail = nullptr;
+    st = magma_stage(leaves, n_leaves, segs, sizeof(double) * 3 * (size_t)std::max<int64_t>(nunits, 1), s, &scratch,
+                     &tail);
+    if (st != RF_OK) return st;
+    const rf_magma_leaf* d_leaves = (const rf_magma_leaf*)scratch;
+    const Seg* d_segs = (const Seg*)(scratch + ((sizeof(rf_magma_leaf) * (size_t)n_leaves + 15) & ~(size_t)15));
+    double* d_part = (double*)tail;
+    hipError_t e = hipSuccess;
+    if (nunits > 0) {
+        const int64_t pw = std::max<int64_t>(1, std::min<int64_t>((nunits + WAVES_PER_WG - 1) / WAVES_PER_WG,
+                                                                  (int64_t)ds->num_cus * 8));
+        hipLaunchKernelGGL(k_magma_partial, dim3((unsigned)pw), dim3(WG), 0, s, d_leaves, d_segs, nunits, b1,
+                           one_minus_b1, d_part);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) {
+        const int64_t lw = std::max<int64_t>(1, std::min<int64_t>((n_leaves + WAVES_PER_WG - 1) / WAVES_PER_WG,
+                                                                  (int64_t)ds->num_cus * 8));
+        hipLaunchKernelGGL(k_magma_leaf, dim3((unsigned)lw), dim3(WG), 0, s, d_segs, n_leaves, d_part, sums);
+        e = hipGetLastError();
+    }
+    const hipError_t ef = hipFreeAsync(scratch, s);
+    if (e != hipSuccess) return fail(RF_ERR_HIP, std::string("rf_magma_reduce: ") + hipGetErrorString(e));
+    if (ef != hipSuccess) return fail(RF_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(ef));
+    return RF_OK;
+}
+
+rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const double* sums, float* scores, float p,
+                         float tau, uint32_t key0, uint32_t key1, int32_t n_keys, float neg_lr, void* stream)
+{
+    // magma.py:8-13 validate_magma_args
+    if (!(p >= 0.0f && p <= 1.0f)) return fail(RF_ERR_INVALID, "magma_p must be in [0, 1].");
+    if (!(tau > 0.0f)) return fail(RF_ERR_INVALID, "magma_tau must be positive.");
+    std::vector<Seg> segs;
+    int64_t nunits = 0;
+    rf_status st = magma_list(leaves, n_leaves, true, segs, nunits);
+    if (st != RF_OK) return st;
+    if (n_leaves == 0) return RF_OK;
+    if (!sums || !scores) return fail(RF_ERR_INVALID, "null sums or scores");
+    for (int32_t i = 0; i < n_leaves; ++i)
+        if (leaves[i].key_index < 0 || leaves[i].key_index >= n_keys)
+            return fail(RF_ERR_INVALID, "key_index outside [0, n_keys)");
+    DevState* ds = nullptr;
+    st = device_state(&ds);
+    if (st != RF_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    uint8_t *scratch = nullptr, *tail = nullptr;
+    st = magma_stage(leaves, n_leaves, segs, sizeof(float) * (size_t)n_leaves, s, &scratch, &tail);
+    if (st != RF_OK) return st;
+    const rf_magma_leaf* d_leaves = (const rf_magma_leaf*)scratch;
+    const Seg* d_segs = (const Seg*)(scratch + ((sizeof(rf_magma_leaf) * (size_t)n_leaves + 15) & ~(size_t)15));
+    float* d_factor = (float*)tail;
+    hipLaunchKernelGGL(k_magma_factor, dim3((unsigned)((n_leaves + WG - 1) / WG)), dim3(WG), 0, s, d_leaves,
+                       n_leaves, sums, scores, d_factor, p, tau, key0, key1);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && nunits > 0) {
+        const int64_t aw = std::max<int64_t>(1, std::min<int64_t>((nunits + WAVES_PER_WG - 1) / WAVES_PER_WG,
+                                                                  (int64_t)ds->num_cus * 8));
+        hipLaunchKernelGGL(k_magma_apply, dim3((unsigned)aw), dim3(WG), 0, s, d_leaves, d_segs, nunits, d_factor,
+                           neg_lr);
+        e = hipGetLastError();
+    }
+    const hipError_t ef = hipFreeAsync(scratch, s);
+    if (e != hipSuccess) return fail(RF_ERR_HIP, std::string("rf_magma_scale: ") + hipGetErrorString(e));
     if (ef != hipSuccess) return fail(RF_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(ef));
     return RF_OK;
 }

@@ -18,8 +18,16 @@ unquantized ("fallback") moment path:
 * ``adamw`` = ``chain(scale_by_adam, add_decayed_weights, scale_by_learning_rate)``
   (adam.py:381-406), fused into the same launch.
 
-Magma (``use_magma=True``) is not implemented in rollfast_amd and raises
-``NotImplementedError``.
+Magma (``use_magma=True``, optim/magma.py:15-132 as adam.py:127-131,
+:203-217 call it): before the step, ``rf_magma_reduce`` sums ``g * m'``,
+``g * g`` and ``m' * m'`` per leaf over the step's new first moment ``m'``;
+the step then runs in update-only mode (decay inside, f32 product); after
+it, ``rf_magma_scale`` turns the sums into the leaf's cosine, score and
+Bernoulli mask and scales the update in place (times ``-lr`` for ``adamw``).
+The PRNG key splits three ways (next, SR, Magma).  Magma runs without the
+fused clipping, the non-finite guard and the grouped launch: those raise
+``NotImplementedError`` (a ``chain``/``multi_transform`` around it still
+works, one transform after the other).
 """
 
 from __future__ import annotations
@@ -28,7 +36,7 @@ from typing import Any, Callable, NamedTuple, Optional, Union
 
 import numpy as np
 
-from .. import _tree, prng
+from .. import _lib, _tree, prng
 from .._base import (
     EmptyState,
     GradientTransformation,
@@ -43,6 +51,7 @@ from .adam8 import (
     _Config,
     _decay_mask_leaves,
     _Engine,
+    _require_device_tensor,
     _torch,
     canonicalize_dtype,
 )
@@ -82,6 +91,107 @@ class _AdamEngine(_Engine):
                                 magma_s=state.magma_s, key=next_key)
 
 
+class _MagmaAdamEngine(_AdamEngine):
+    """The adam engine with Magma's three-way key split."""
+
+    @staticmethod
+    def split_keys(state_key):
+        """``next_state_key, sr_key, magma_key = split(key, 3)`` (adam.py:127-128)
+        and ``k1, k2 = split(sr_key)`` for the two moment trees."""
+        next_key, sr_key, _magma_key = prng.split(state_key, 3)
+        k1, k2 = prng.split(sr_key, 2)
+        return k1, k2, next_key
+
+
+def _validate_magma_args(p: float, tau: float) -> None:
+    """magma.py:8-13."""
+    if not 0.0 <= p <= 1.0:
+        raise ValueError(f"magma_p must be in [0, 1], got {p!r}.")
+    if tau <= 0.0:
+        raise ValueError(f"magma_tau must be positive, got {tau!r}.")
+
+
+def _init_magma_state(params):
+    """utils.py:65-70: an f32 scalar 0.5 per array leaf, on the leaf's device."""
+    torch = _torch()
+
+    def leaf(x):
+        if _is_passthrough_leaf(x):
+            return x
+        return torch.full((), 0.5, dtype=torch.float32, device=x.device)
+
+    return _tree.tree_map(leaf, params, is_leaf=_is_passthrough_leaf)
+
+
+def _dtype_code(t) -> int:
+    torch = _torch()
+    if t.dtype == torch.bfloat16:
+        return _lib.RF_BF16
+    if t.dtype == torch.float32:
+        return _lib.RF_F32
+    raise NotImplementedError(f"dtype {t.dtype} is not supported (float32 or bfloat16)")
+
+
+def _magma_step(engine, magma_p, magma_tau, updates, state, params, *, decay_mask, weight_decay, neg_lr):
+    """One scale_by_adam(use_magma=True) update (adam.py:123-235 with
+    magma.py:15-132): the Magma sums before the step (over the old moments,
+    which the step overwrites), the step in update-only mode, then the
+    per-leaf scaling of its f32 updates by ``neg_lr * (mask * score)``."""
+    torch = _torch()
+    g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
+    mu_leaves = _tree.flatten_up_to(g_td, state.mu) if g_leaves else []
+    s_leaves = _tree.flatten_up_to(g_td, state.magma_s) if g_leaves else []
+    picked = [i for i, (g, m) in enumerate(zip(g_leaves, mu_leaves))
+              if not (_is_passthrough_leaf(g) or _is_passthrough_leaf(m))]
+    if not picked:
+        out, new_state = engine.run(updates, state, params, apply=False, decay_mask=decay_mask,
+                                    weight_decay=weight_decay, neg_lr=None)
+        return out, new_state
+    hold = []  # contiguous operands, alive until the launches are enqueued
+    table = (_lib.MagmaLeaf * len(picked))()
+    device = None
+    for k, i in enumerate(picked):
+        g = _require_device_tensor(g_leaves[i], "gradient").contiguous()
+        m = _require_device_tensor(mu_leaves[i], "first moment").contiguous()
+        if device is None:
+            device = g.device
+        if g.device != device or m.device != device:
+            raise ValueError("all leaves of one Magma step must live on one device")
+        if g.numel() != m.numel():
+            raise ValueError("updates and optimizer state have different tree structures")
+        hold += [g, m]
+        r = table[k]
+        r.grad, r.mu, r.size = g.data_ptr(), m.data_ptr(), g.numel()
+        r.grad_dtype, r.mu_dtype, r.key_index = _dtype_code(g), _dtype_code(m), i
+    lib = _lib.lib()
+    magma_key = prng.split(prng.as_key(state.key), 3)[2]
+    b1 = float(_as_f32(engine.cfg.b1))
+    omb1 = float(engine.ema_weight(engine.cfg.b1))
+    with torch.cuda.device(device):
+        stream = _lib.stream_ptr()
+        sums = torch.empty(3 * len(picked), dtype=torch.float64, device=device)
+        _lib.check(lib.rf_magma_reduce(table, len(picked), b1, omb1, sums.data_ptr(), stream), "rf_magma_reduce")
+        out, new_state = engine.run(updates, state, params, apply=False, decay_mask=decay_mask,
+                                    weight_decay=weight_decay, neg_lr=None)
+        out_leaves = _tree.flatten_up_to(g_td, out)
+        for k, i in enumerate(picked):
+            u = out_leaves[i]
+            if not u.is_contiguous():
+                raise RuntimeError("the step's updates are expected contiguous")
+            table[k].updates = u.data_ptr()
+        scores = torch.stack([_require_device_tensor(s_leaves[i], "magma score").reshape(()).to(
+            device=device, dtype=torch.float32) for i in picked])
+        lr = 1.0 if neg_lr is None else float(np.float32(neg_lr))
+        _lib.check(lib.rf_magma_scale(table, len(picked), sums.data_ptr(), scores.data_ptr(), float(magma_p),
+                                      float(magma_tau), int(magma_key[0]), int(magma_key[1]), len(g_leaves), lr,
+                                      stream), "rf_magma_scale")
+    new_s = list(s_leaves)
+    for k, i in enumerate(picked):
+        new_s[i] = scores[k]
+    del hold
+    return out, new_state._replace(magma_s=_tree.unflatten(g_td, new_s))
+
+
 def _has_nonzero_or_scheduled(value) -> bool:
     """utils.py:105-111."""
     if isinstance(value, (int, float)):
@@ -106,11 +216,11 @@ def _zeros_like_tree(params, dtype):
     return _tree.tree_map(zeros, params, is_leaf=_is_passthrough_leaf)
 
 
-def _make_engine(b1, b2, eps, eps_root, mu_dtype, nesterov, key, exact) -> _AdamEngine:
+def _make_engine(b1, b2, eps, eps_root, mu_dtype, nesterov, key, exact, magma: bool = False) -> _AdamEngine:
     torch = _torch()
     cfg = _Config(b1, b2, eps, eps_root, 2048, 1 << 62, torch.float32, mu_dtype, False, "shard_local", False,
                   bool(nesterov), key, bool(exact))
-    eng = _AdamEngine(cfg)
+    eng = (_MagmaAdamEngine if magma else _AdamEngine)(cfg)
     eng.store_sr = mu_dtype == torch.bfloat16
     return eng
 
@@ -123,13 +233,41 @@ def _canonical_mu_dtype(mu_dtype):
     return d
 
 
+def _adam_decay(weight_decay, weight_decay_mask, updates, state, params):
+    """scale_by_adam's own decoupled decay (adam.py:189-202): (leaf mask,
+    f32 decay) or (None, None) when it does not apply."""
+    decays = _has_nonzero_or_scheduled(weight_decay)
+    if decays and params is None:
+        raise ValueError(
+            "`params` must be provided to `scale_by_adam.update` when "
+            "`weight_decay` is nonzero or scheduled."
+        )
+    if params is None or not decays:
+        return None, None
+    n = len(_tree.leaves(updates, is_leaf=_is_passthrough_leaf))
+    decay_mask = _decay_mask_leaves(weight_decay_mask, params, n)
+    # _resolve_scalar(weight_decay, state.count): a schedule sees the count
+    # before the increment (adam.py:196).
+    wd = weight_decay
+    if callable(wd):
+        wd = wd(np.asarray(state.count, dtype=np.int32))
+    # update + wd * param.astype(f32) (utils.py:79-90): f32 product, so the
+    # decay is passed as an array scalar (no weak bf16 typing).
+    return decay_mask, np.float32(_as_f32(wd))
+
+
+_MAGMA_FUSED_MSG = ("Magma is not supported with the fused global-norm clipping, the non-finite guard "
+                    "or the grouped launch")
+
+
 class _ScaleByAdamUpdate:
     """``scale_by_adam(...).update`` (adam.py:123-235)."""
 
-    def __init__(self, engine: _AdamEngine, weight_decay, weight_decay_mask):
+    def __init__(self, engine: _AdamEngine, weight_decay, weight_decay_mask, magma=None):
         self.engine = engine
         self.weight_decay = weight_decay
         self.weight_decay_mask = weight_decay_mask
+        self.magma = magma  # (p, tau) with use_magma=True, else None
 
     def __call__(self, updates, state, params=None):
         return self._step(updates, state, params, apply=False)
@@ -139,28 +277,48 @@ class _ScaleByAdamUpdate:
         del fused_only  # param_key, param_sr, random_bits: fused-step arguments
         if apply:
             raise TypeError("scale_by_adam has no learning rate: the fused step needs adamw(...)")
-        decays = _has_nonzero_or_scheduled(self.weight_decay)
-        if decays and params is None:
-            raise ValueError(
-                "`params` must be provided to `scale_by_adam.update` when "
-                "`weight_decay` is nonzero or scheduled."
-            )
-        decay_mask = None
-        wd = None
-        if params is not None and decays:
-            n = len(_tree.leaves(updates, is_leaf=_is_passthrough_leaf))
-            decay_mask = _decay_mask_leaves(self.weight_decay_mask, params, n)
-            # _resolve_scalar(weight_decay, state.count): a schedule sees the
-            # count before the increment (adam.py:196).
-            wd = self.weight_decay
-            if callable(wd):
-                wd = wd(np.asarray(state.count, dtype=np.int32))
-            # update + wd * param.astype(f32) (utils.py:79-90): f32 product, so
-            # the decay is passed as an array scalar (no weak bf16 typing).
-            wd = np.float32(_as_f32(wd))
+        decay_mask, wd = _adam_decay(self.weight_decay, self.weight_decay_mask, updates, state, params)
+        if self.magma is not None:
+            if skip_nonfinite or finite_out is not None or finite_host is not None or clip_global_norm:
+                raise NotImplementedError(_MAGMA_FUSED_MSG)
+            return _magma_step(self.engine, *self.magma, updates, state, params, decay_mask=decay_mask,
+                               weight_decay=wd, neg_lr=None)
         return self.engine.run(updates, state, params, apply=False, decay_mask=decay_mask, weight_decay=wd,
                                neg_lr=None, skip_nonfinite=skip_nonfinite, finite_out=finite_out,
                                finite_host=finite_host, clip_global_norm=clip_global_norm, clip_stats=clip_stats)
+
+
+class _AdamwMagmaUpdate:
+    """``adamw(..., use_magma=True).update``: the chain scale_by_adam (decay
+    inside, then Magma) -> scale_by_learning_rate (adam.py:380-404); the
+    learning rate multiplies the masked update."""
+
+    def __init__(self, engine: _AdamEngine, learning_rate, weight_decay, weight_decay_mask, magma):
+        self.engine = engine
+        self.learning_rate = learning_rate
+        self.weight_decay = weight_decay
+        self.weight_decay_mask = weight_decay_mask
+        self.magma = magma
+        self._lr = _Adamw8Update(engine, learning_rate, 0.0, None, False)._lr
+
+    def __call__(self, updates, state, params=None, **extra_args):
+        del extra_args
+        return self._step(updates, state, params, apply=False)
+
+    def _step(self, updates, state, params, *, apply: bool, skip_nonfinite=False, finite_out=None,
+              finite_host=None, clip_global_norm=None, clip_stats=None, **fused_only):
+        del clip_stats
+        if apply or fused_only.get("random_bits") is not None:
+            raise NotImplementedError("the fused step with Magma: use adamw_step, which applies tx.update's "
+                                      "updates with apply_updates")
+        if skip_nonfinite or finite_out is not None or finite_host is not None or clip_global_norm:
+            raise NotImplementedError(_MAGMA_FUSED_MSG)
+        adam_state, lr_state = state[0], state[-1]
+        neg_lr, new_lr_state = self._lr(lr_state)
+        decay_mask, wd = _adam_decay(self.weight_decay, self.weight_decay_mask, updates, adam_state, params)
+        out, new_adam = _magma_step(self.engine, *self.magma, updates, adam_state, params, decay_mask=decay_mask,
+                                    weight_decay=wd, neg_lr=neg_lr)
+        return out, (new_adam,) + tuple(state[1:-1]) + (new_lr_state,)
 
 
 def scale_by_adam(
@@ -181,19 +339,23 @@ def scale_by_adam(
     exact: bool = False,
 ) -> GradientTransformation:
     """Rescale updates according to the Adam algorithm (adam.py:38-235).
-    ``exact`` (extension): IEEE division and square root in the direction."""
-    del magma_p, magma_tau, axis_name
+    ``exact`` (extension): IEEE division and square root in the direction.
+    ``axis_name`` names a collective axis of the reference's sharded runs and
+    has no effect on one device."""
+    del axis_name
     if use_magma:
-        raise NotImplementedError("Magma is not supported by rollfast_amd.")
+        _validate_magma_args(magma_p, magma_tau)
     _has_nonzero_or_scheduled(weight_decay)
     mu = _canonical_mu_dtype(mu_dtype)
-    engine = _make_engine(b1, b2, eps, eps_root, mu, nesterov, key, exact)
+    engine = _make_engine(b1, b2, eps, eps_root, mu, nesterov, key, exact, magma=use_magma)
 
     def init_fn(params):
         return ScaleByAdamState(count=np.zeros((), dtype=np.int32), mu=_zeros_like_tree(params, mu),
-                                nu=_zeros_like_tree(params, mu), magma_s=(), key=prng.fresh_key(key))
+                                nu=_zeros_like_tree(params, mu),
+                                magma_s=_init_magma_state(params) if use_magma else (), key=prng.fresh_key(key))
 
-    return GradientTransformation(init_fn, _ScaleByAdamUpdate(engine, weight_decay, weight_decay_mask))
+    magma = (float(magma_p), float(magma_tau)) if use_magma else None
+    return GradientTransformation(init_fn, _ScaleByAdamUpdate(engine, weight_decay, weight_decay_mask, magma))
 
 
 def adamw(
@@ -219,7 +381,20 @@ def adamw(
     launch.  The state is the chain's tuple ``(ScaleByAdamState,
     add_decayed_weights state?, lr state)``."""
     if use_magma:
-        raise NotImplementedError("Magma is not supported by rollfast_amd.")
+        # scale_by_adam(weight_decay, use_magma) -> scale_by_learning_rate
+        inner = scale_by_adam(b1=b1, b2=b2, eps=eps, eps_root=eps_root, mu_dtype=mu_dtype,
+                              weight_decay=weight_decay, weight_decay_mask=weight_decay_mask, nesterov=nesterov,
+                              use_magma=True, magma_p=magma_p, magma_tau=magma_tau, axis_name=axis_name, key=key,
+                              exact=exact)
+
+        def magma_init(params):
+            lr_state = (ScaleByScheduleState(count=np.zeros((), dtype=np.int32)) if callable(learning_rate)
+                        else EmptyState())
+            return (inner.init(params), lr_state)
+
+        return GradientTransformationExtraArgs(
+            magma_init, _AdamwMagmaUpdate(inner.update.engine, learning_rate, weight_decay, weight_decay_mask,
+                                          inner.update.magma))
     if callable(weight_decay):
         raise NotImplementedError("weight-decay schedules are not supported by adamw; pass a scalar")
     inner = scale_by_adam(b1=b1, b2=b2, eps=eps, eps_root=eps_root, mu_dtype=mu_dtype, nesterov=nesterov,
@@ -251,6 +426,15 @@ def adamw_step(tx, params, grads, state, key=None, stochastic: bool = True, *, r
     ``adamw8_step``."""
     from .adam8 import adamw8_step
 
+    if isinstance(tx.update, _AdamwMagmaUpdate):
+        # Magma scales the finished update per leaf: tx.update, then
+        # apply_updates (utils.py:648-708), as the reference runs them.
+        if random_bits is not None or clip_global_norm is not None:
+            raise NotImplementedError(_MAGMA_FUSED_MSG)
+        from ..utils import apply_updates
+
+        updates, new_state = tx.update(grads, state, params)
+        return apply_updates(params, updates, key=key, stochastic=stochastic), new_state
     if isinstance(tx.update, _ScaleByAdamUpdate) or (isinstance(tx.update, _Adamw8Update)
                                                      and not isinstance(tx.update.engine, _AdamEngine)):
         raise TypeError("adamw_step needs a transformation built by adamw(...) or a composition of them "

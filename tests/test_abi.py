@@ -59,6 +59,7 @@ def test_struct_sizes_match_header():
     assert ctypes.sizeof(_lib.Adam8Hparams) == 120
     assert ctypes.sizeof(_lib.Adam8Group) == 32
     assert ctypes.sizeof(_lib.ApplyLeaf) == 40
+    assert ctypes.sizeof(_lib.MagmaLeaf) == 48
 
 
 def test_version_string():

@@ -291,3 +291,33 @@ def test_native_host_walk_matches_python_flatten():
     assert host.gather({1: t[0], "a": t[1]}, {1: 0, "a": 0}, {1: 0, "a": 0}, None) is None  # keys do not sort
     # refresh refuses host tensors (the caller then rebuilds the table)
     assert host.refresh([t[0]], ["m"], ["v"], None, [], 0, 0) is False
+
+
+# ----------------------------------------------------------------- Magma --
+def test_magma_construction_and_state():
+    """scale_by_adam / adamw with use_magma=True (optim/adam.py:95-119,
+    :380-404): argument checks of magma.py:8-13, a 0.5 f32 score per array
+    leaf (utils.py:65-70; None and MaskedNode leaves kept), and adamw's chain
+    state without an add_decayed_weights entry."""
+    with pytest.raises(ValueError, match="magma_p"):
+        rf.scale_by_adam(use_magma=True, magma_p=1.1)
+    with pytest.raises(ValueError, match="magma_tau"):
+        rf.scale_by_adam(use_magma=True, magma_tau=0.0)
+    with pytest.raises(ValueError, match="magma_p"):
+        rf.adamw(1e-3, use_magma=True, magma_p=-0.1)
+    params = {"w": torch.zeros(3, 2), "b": None, "m": rf.MaskedNode()}
+    st = rf.scale_by_adam(use_magma=True).init(params)
+    assert st.magma_s["b"] is None and isinstance(st.magma_s["m"], rf.MaskedNode)
+    s = st.magma_s["w"]
+    assert s.shape == () and s.dtype == torch.float32 and float(s) == 0.5
+    assert rf.scale_by_adam().init(params).magma_s == ()
+    ast = rf.adamw(1e-3, weight_decay=0.1, use_magma=True).init(params)
+    assert len(ast) == 2 and isinstance(ast[0], rf.ScaleByAdamState) and isinstance(ast[1], rf.EmptyState)
+    assert len(rf.adamw(1e-3, weight_decay=0.1).init(params)) == 3
+
+
+def test_magma_refuses_host_tensors():
+    tx = rf.scale_by_adam(use_magma=True)
+    params = {"w": torch.zeros(4)}
+    with pytest.raises((TypeError, ValueError)):
+        tx.update({"w": torch.ones(4)}, tx.init(params), params)

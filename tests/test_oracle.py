@@ -620,3 +620,57 @@ def test_all_finite_and_reject_params():
     want_h[0] = 0
     orc.reject_params(h, orc.BF16)
     np.testing.assert_array_equal(h, want_h)
+
+
+# ----------------------------------------------------------------- Magma --
+def test_uniform01_known_bits():
+    """jax.random.uniform's mantissa fill: bits 0 -> 0, all ones -> 1 - 2^-23,
+    the top 23 bits set the mantissa, the low 9 bits are dropped."""
+    u = orc.uniform01(np.array([0, 0xFFFFFFFF, 1 << 31, 0x1FF], np.uint32))
+    assert u[0] == np.float32(0.0)
+    assert u[1] == np.float32(1.0 - 2.0 ** -23)
+    assert u[2] == np.float32(0.5)
+    assert u[3] == np.float32(0.0)
+
+
+def test_magma_leaf_closed_forms():
+    """magma.py:98-118: a moment parallel to the gradient has cosine 1, an
+    antiparallel one -1, an orthogonal one and an all-zero leaf 0 (the
+    1e-12 floor), a NaN gradient 0 (nan_to_num); the score is
+    0.9 * s_prev + 0.1 * sigmoid(cos / tau), here against float64."""
+    key = orc.split(np.array([0, 7], np.uint32), 1)[0]
+    g = np.array([1.0, -2.0, 3.0], np.float32)
+
+    def want(cos, tau, s_prev):
+        return 0.9 * s_prev + 0.1 / (1.0 + np.exp(-cos / tau))
+
+    for mu, cos in ((3 * g, 1.0), (-0.5 * g, -1.0), (np.array([2.0, 1.0, 0.0], np.float32), 0.0),
+                    (np.zeros(3, np.float32), 0.0)):
+        for tau, s_prev in ((2.0, 0.5), (0.25, 0.9)):
+            s, _keep = orc.magma_leaf(g, mu, s_prev, key, 0.5, tau)
+            assert s.dtype == np.float32 and abs(float(s) - want(cos, tau, s_prev)) < 2e-7, (mu, tau, s)
+    s, _ = orc.magma_leaf(np.array([np.nan, 1.0], np.float32), np.ones(2, np.float32), 0.5, key, 0.5, 2.0)
+    assert abs(float(s) - want(0.0, 2.0, 0.5)) < 2e-7
+
+
+def test_magma_bernoulli_mask():
+    """bernoulli(key, p) = uniform(key) < p: never at p = 0, always at p = 1,
+    and at p = 0.3 the keep frequency over 4,000 keys lies within 4 sigma."""
+    keys = orc.split(np.array([0, 42], np.uint32), 4000)
+    g = np.ones(4, np.float32)
+    for p, rate in ((0.0, 0.0), (1.0, 1.0)):
+        kept = [orc.magma_leaf(g, g, 0.5, k, p, 2.0)[1] for k in keys[:200]]
+        assert np.mean(kept) == rate
+    kept = np.array([orc.magma_leaf(g, g, 0.5, k, 0.3, 2.0)[1] for k in keys])
+    sigma = np.sqrt(0.3 * 0.7 / keys.shape[0])
+    assert abs(kept.mean() - 0.3) < 4 * sigma
+
+
+def test_magma_apply_masks_and_scales():
+    """magma.py:120-122 and scale_by_learning_rate: a dropped leaf's update
+    is exactly zero; a kept one is s * delta, then times -lr."""
+    delta = np.array([1.0, -2.0, 0.5], np.float32)
+    assert (orc.magma_apply(delta, np.float32(0.7), False) == 0.0).all()
+    np.testing.assert_array_equal(orc.magma_apply(delta, np.float32(0.5), True), delta * np.float32(0.5))
+    np.testing.assert_array_equal(orc.magma_apply(delta, np.float32(0.5), True, np.float32(-0.1)),
+                                  np.float32(-0.1) * (delta * np.float32(0.5)))
