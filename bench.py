@@ -30,6 +30,8 @@ Other workloads (one JSON line each, same fields):
   llama7b_adamw_f32   full-precision AdamW (adamw, f32 moments) over the Llama
                    tree: 22 B/param.
   llama7b_adamw_bf16  the same with stochastically rounded bf16 moments.
+  llama7b_adamw_magma full-precision AdamW with Magma (use_magma=True):
+                   tx.update then apply_updates.
   llama7b_apply    apply_updates of f32 updates to the bf16 Llama params with
                    stochastic rounding (in-kernel Threefry bits).
   quantize_2p30    quantize_blocks, dynamic signed, 2^30 f32 elements
@@ -265,7 +267,7 @@ class Workload:
 
 
 def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None, clip=None,
-                   guard=False, groups=False):
+                   guard=False, groups=False, magma=False):
     import numpy as np
     import torch
 
@@ -282,7 +284,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=args.exact)
     else:
         tx = rf.adamw(learning_rate=1e-3, weight_decay=0.01, exact=args.exact,
-                      mu_dtype=torch.bfloat16 if adam_mu == "bf16" else None)
+                      mu_dtype=torch.bfloat16 if adam_mu == "bf16" else None, use_magma=magma)
     chain_clip = None
     if groups:
         # the fine-tune builders' shape: groups with their own lr / decay / key
@@ -331,6 +333,9 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         holder["k"] += 1
         if optax:
             _, holder["state"] = tx.update(g, holder["state"], holder["params"])
+        elif magma:  # tx.update (Magma sums, step, Magma scaling) then apply_updates
+            holder["params"], holder["state"] = rf.adamw_step(tx, holder["params"], g, holder["state"], key=key,
+                                                              stochastic=param_sr)
         else:
             holder["params"], holder["state"] = rf.adamw8_step(tx, holder["params"], g, holder["state"], key=key,
                                                                stochastic=param_sr, clip_global_norm=clip)
@@ -362,6 +367,10 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     if guard:
         config["nonfinite"] = "skip (apply_if_finite, max_consecutive_errors=1; one int32 read back per step)"
         config["launches_per_step"] = 4
+    if magma:
+        config["magma"] = "use_magma=True (p 0.5, tau 2): sums before the step, scaling after, then apply_updates"
+        config["mode"] = "tx.update + apply_updates"
+        config["launches_per_step"] = 7
     if shapes_fn is llama7b_shapes:
         cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr)  # noqa: E731
     else:
@@ -375,6 +384,12 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     else:
         mb = 4 if adam_mu == "f32" else 2
         nbytes = n_params * (2 + 2 + 2 + 2 * 2 * mb)  # p r+w, g r, two moments r+w
+        if magma:
+            # update-only step writes f32 updates (4) instead of params (2);
+            # Magma sums read g and mu (2 + mb); the scaling reads and writes
+            # the updates (8); apply_updates reads them (4) and the params
+            # and writes the params (2 + 2)
+            nbytes = n_params * ((2 + 2 + 2 * 2 * mb + 4) + (2 + mb) + 8 + (4 + 2 + 2))
         cpu = None
     return Workload(workload, n_params, "params/s", nbytes, step, config, cpu, metric)
 
@@ -479,6 +494,8 @@ WORKLOADS = {
                                                   param_sr=False, adam_mu="f32"),
     "llama7b_adamw_bf16": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw_bf16_moments",
                                                    param_sr=False, adam_mu="bf16"),
+    "llama7b_adamw_magma": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw_f32_moments_magma",
+                                                    param_sr=False, adam_mu="f32", magma=True),
     "llama7b_apply": lambda a: _kernel_workload(a, "apply"),
     "quantize_2p30": lambda a: _kernel_workload(a, "quantize"),
     "dequantize_2p30": lambda a: _kernel_workload(a, "dequantize"),
