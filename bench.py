@@ -30,8 +30,8 @@ Other workloads (one JSON line each, same fields):
   llama7b_adamw_f32   full-precision AdamW (adamw, f32 moments) over the Llama
                    tree: 22 B/param.
   llama7b_adamw_bf16  the same with stochastically rounded bf16 moments.
-  llama7b_adamw_magma full-precision AdamW with Magma (use_magma=True):
-                   tx.update then apply_updates.
+  llama7b_adamw_magma full-precision AdamW with Magma (use_magma=True) by
+                   adamw_step: the Magma factor folded into apply_updates.
   llama7b_apply    apply_updates of f32 updates to the bf16 Llama params with
                    stochastic rounding (in-kernel Threefry bits).
   quantize_2p30    quantize_blocks, dynamic signed, 2^30 f32 elements
@@ -368,9 +368,10 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         config["nonfinite"] = "skip (apply_if_finite, max_consecutive_errors=1; one int32 read back per step)"
         config["launches_per_step"] = 4
     if magma:
-        config["magma"] = "use_magma=True (p 0.5, tau 2): sums before the step, scaling after, then apply_updates"
-        config["mode"] = "tx.update + apply_updates"
-        config["launches_per_step"] = 7
+        config["magma"] = ("use_magma=True (p 0.5, tau 2): sums before the step, per-leaf factors after it, "
+                           "folded into apply_updates")
+        config["mode"] = "adamw_step (update-only step, then apply_updates with the Magma factor)"
+        config["launches_per_step"] = 5
     if shapes_fn is llama7b_shapes:
         cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr)  # noqa: E731
     else:
@@ -386,10 +387,10 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         nbytes = n_params * (2 + 2 + 2 + 2 * 2 * mb)  # p r+w, g r, two moments r+w
         if magma:
             # update-only step writes f32 updates (4) instead of params (2);
-            # Magma sums read g and mu (2 + mb); the scaling reads and writes
-            # the updates (8); apply_updates reads them (4) and the params
-            # and writes the params (2 + 2)
-            nbytes = n_params * ((2 + 2 + 2 * 2 * mb + 4) + (2 + mb) + 8 + (4 + 2 + 2))
+            # Magma sums read g and mu (2 + mb); apply_updates with the
+            # per-leaf Magma factor folded in reads the updates (4) and the
+            # params and writes the params (2 + 2)
+            nbytes = n_params * ((2 + 2 + 2 * 2 * mb + 4) + (2 + mb) + (4 + 2 + 2))
         cpu = None
     return Workload(workload, n_params, "params/s", nbytes, step, config, cpu, metric)
 

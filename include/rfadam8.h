@@ -283,10 +283,21 @@ RF_API rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, 
  * s = 0.9 * s_prev + 0.1 * sigmoid(cos / tau) written over scores[i] (device
  * f32), the Bernoulli mask m = uniform(split(key, n_keys)[key_index]) < p,
  * and updates = neg_lr * ((m * s) * updates) (neg_lr = 1: no learning-rate
- * scale, optax scale_by_learning_rate otherwise).  Scratch: hipMallocAsync. */
+ * scale, optax scale_by_learning_rate otherwise).  With factor_out (device
+ * f32[n_leaves], else NULL) the per-leaf factors m * s are written there and
+ * the updates are left for rf_magma_apply_updates (updates may then be
+ * NULL).  Scratch: hipMallocAsync. */
 RF_API rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const double* sums, float* scores,
                                 float p, float tau, uint32_t key0, uint32_t key1, int32_t n_keys, float neg_lr,
-                                void* stream);
+                                float* factor_out, void* stream);
+
+/* rf_apply_updates with Magma's scaling folded in (no reference
+ * counterpart; the fused form of optim/magma.py:120-122, optax
+ * scale_by_learning_rate and utils.py:648-708): row i applies
+ * neg_lr * (factor[i] * updates) (factor: device f32[n_leaves]). */
+RF_API rf_status rf_magma_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, const float* factor,
+                                        float neg_lr, int32_t stochastic, uint32_t key0, uint32_t key1,
+                                        void* stream);
 
 /* Host-side: the 256 f32 values of a dynamic codebook (adam8.py:461-503). */
 RF_API rf_status rf_codebook(int32_t quantizer, float* out256);

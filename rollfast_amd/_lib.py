@@ -152,6 +152,7 @@ EXPORTS = (
     "rf_clip_by_global_norm",
     "rf_magma_reduce",
     "rf_magma_scale",
+    "rf_magma_apply_updates",
     "rf_codebook",
     "rf_host_table_codes",
     "rf_version",
@@ -191,7 +192,8 @@ def lib() -> ctypes.CDLL:
     L.rf_apply_updates.argtypes = [ctypes.POINTER(ApplyLeaf), i32, i32, u32, u32, _p]
     f32 = ctypes.c_float
     L.rf_magma_reduce.argtypes = [ctypes.POINTER(MagmaLeaf), i32, f32, f32, _p, _p]
-    L.rf_magma_scale.argtypes = [ctypes.POINTER(MagmaLeaf), i32, _p, _p, f32, f32, u32, u32, i32, f32, _p]
+    L.rf_magma_scale.argtypes = [ctypes.POINTER(MagmaLeaf), i32, _p, _p, f32, f32, u32, u32, i32, f32, _p, _p]
+    L.rf_magma_apply_updates.argtypes = [ctypes.POINTER(ApplyLeaf), i32, _p, f32, i32, u32, u32, _p]
     L.rf_codebook.argtypes = [i32, _p]
     L.rf_host_table_codes.argtypes = [i32, u32, i64, _p]
     for name in EXPORTS:

@@ -282,10 +282,14 @@ __device__ __forceinline__ uint32_t apply_bf16(float p, float u, bool stochastic
     return sr_bf16(s, bits ? bits[e] : jax_bits(lk0, lk1, (uint64_t)e));
 }
 
+// `factor` (Magma's fused form, or null): each update is first taken as
+// neg_lr * (factor[leaf] * u), the scaling rf_magma_scale would have done.
 __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ leaves, int32_t stochastic,
-                                              uint32_t k0, uint32_t k1)
+                                              uint32_t k0, uint32_t k1, const float* __restrict__ factor,
+                                              float neg_lr)
 {
     const rf_apply_leaf L = leaves[blockIdx.y];
+    const float f = factor ? factor[blockIdx.y] : 1.0f;
     uint32_t lk0 = 0, lk1 = 0;
     if (stochastic) jax_split(k0, k1, (uint32_t)L.param_index, lk0, lk1);
     const int64_t tid = (int64_t)blockIdx.x * WG + threadIdx.x;
@@ -298,6 +302,10 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
         const int64_t e0 = gi * 8;
         float u[8], p[8];
         load8<float>(L.updates, e0, u);
+        if (factor) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) u[t] = neg_lr * (f * u[t]);
+        }
         if (L.param_dtype == RF_BF16) {
             load8<uint16_t>(L.param, e0, p);
             uint32_t h[8];
@@ -319,7 +327,7 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
         }
     }
     for (int64_t e = ngroups * 8 + tid; e < L.size; e += nthreads) {
-        const float u = L.updates[e];
+        const float u = factor ? neg_lr * (f * L.updates[e]) : L.updates[e];
         if (L.param_dtype == RF_BF16) {
             const float p = bf16_bits_to_f32(((const uint16_t*)L.param)[e]);
             ((uint16_t*)L.param)[e] = (uint16_t)apply_bf16(p, u, sr, L.bits, lk0, lk1, e);
@@ -1599,6 +1607,9 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
 
 namespace {
 
+rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic, uint32_t key0,
+                       uint32_t key1, const float* factor, float neg_lr, void* stream);
+
 // Validates a Magma leaf table and builds its work list (segment i = leaf i).
 rf_status magma_list(const rf_magma_leaf* leaves, int32_t n_leaves, bool need_updates, std::vector<Seg>& segs,
                      int64_t& nunits)
@@ -1694,14 +1705,15 @@ rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, float b
 }
 
 rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const double* sums, float* scores, float p,
-                         float tau, uint32_t key0, uint32_t key1, int32_t n_keys, float neg_lr, void* stream)
+                         float tau, uint32_t key0, uint32_t key1, int32_t n_keys, float neg_lr, float* factor_out,
+                         void* stream)
 {
     // magma.py:8-13 validate_magma_args
     if (!(p >= 0.0f && p <= 1.0f)) return fail(RF_ERR_INVALID, "magma_p must be in [0, 1].");
     if (!(tau > 0.0f)) return fail(RF_ERR_INVALID, "magma_tau must be positive.");
     std::vector<Seg> segs;
     int64_t nunits = 0;
-    rf_status st = magma_list(leaves, n_leaves, true, segs, nunits);
+    rf_status st = magma_list(leaves, n_leaves, factor_out == nullptr, segs, nunits);
     if (st != RF_OK) return st;
     if (n_leaves == 0) return RF_OK;
     if (!sums || !scores) return fail(RF_ERR_INVALID, "null sums or scores");
@@ -1717,11 +1729,11 @@ rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const do
     if (st != RF_OK) return st;
     const rf_magma_leaf* d_leaves = (const rf_magma_leaf*)scratch;
     const Seg* d_segs = (const Seg*)(scratch + ((sizeof(rf_magma_leaf) * (size_t)n_leaves + 15) & ~(size_t)15));
-    float* d_factor = (float*)tail;
+    float* d_factor = factor_out ? factor_out : (float*)tail;
     hipLaunchKernelGGL(k_magma_factor, dim3((unsigned)((n_leaves + WG - 1) / WG)), dim3(WG), 0, s, d_leaves,
                        n_leaves, sums, scores, d_factor, p, tau, key0, key1);
     hipError_t e = hipGetLastError();
-    if (e == hipSuccess && nunits > 0) {
+    if (e == hipSuccess && nunits > 0 && !factor_out) {
         const int64_t aw = std::max<int64_t>(1, std::min<int64_t>((nunits + WAVES_PER_WG - 1) / WAVES_PER_WG,
                                                                   (int64_t)ds->num_cus * 8));
         hipLaunchKernelGGL(k_magma_apply, dim3((unsigned)aw), dim3(WG), 0, s, d_leaves, d_segs, nunits, d_factor,
@@ -1736,6 +1748,23 @@ rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const do
 
 rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic, uint32_t key0,
                            uint32_t key1, void* stream)
+{
+    return apply_launch(leaves, n_leaves, stochastic, key0, key1, nullptr, 1.0f, stream);
+}
+
+rf_status rf_magma_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, const float* factor, float neg_lr,
+                                 int32_t stochastic, uint32_t key0, uint32_t key1, void* stream)
+{
+    if (n_leaves > 0 && !factor) return fail(RF_ERR_INVALID, "null factor");
+    return apply_launch(leaves, n_leaves, stochastic, key0, key1, factor, neg_lr, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic, uint32_t key0,
+                       uint32_t key1, const float* factor, float neg_lr, void* stream)
 {
     if (n_leaves < 0 || (n_leaves > 0 && !leaves)) return fail(RF_ERR_INVALID, "bad leaf table");
     if (n_leaves == 0) return RF_OK;
@@ -1759,11 +1788,15 @@ rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_
     HIP_TRY(hipMallocAsync((void**)&d, sizeof(rf_apply_leaf) * (size_t)n_leaves, s));
     HIP_TRY(hipMemcpyAsync(d, leaves, sizeof(rf_apply_leaf) * (size_t)n_leaves, hipMemcpyHostToDevice, s));
     const int gx = (int)std::max<int64_t>(1, std::min<int64_t>((maxsize + WG - 1) / WG, (int64_t)ds->num_cus * 4));
-    hipLaunchKernelGGL(k_apply, dim3(gx, n_leaves), dim3(WG), 0, s, d, stochastic, key0, key1);
+    hipLaunchKernelGGL(k_apply, dim3(gx, n_leaves), dim3(WG), 0, s, d, stochastic, key0, key1, factor, neg_lr);
     hipError_t le = hipGetLastError();
     HIP_TRY(hipFreeAsync(d, s));
     if (le != hipSuccess) return fail(RF_ERR_HIP, std::string("k_apply launch: ") + hipGetErrorString(le));
     return RF_OK;
 }
+
+}  // namespace
+
+extern "C" {
 
 }  // extern "C"

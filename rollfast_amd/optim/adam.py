@@ -132,11 +132,15 @@ def _dtype_code(t) -> int:
     raise NotImplementedError(f"dtype {t.dtype} is not supported (float32 or bfloat16)")
 
 
-def _magma_step(engine, magma_p, magma_tau, updates, state, params, *, decay_mask, weight_decay, neg_lr):
+def _magma_step(engine, magma_p, magma_tau, updates, state, params, *, decay_mask, weight_decay, neg_lr,
+                fuse_apply=None):
     """One scale_by_adam(use_magma=True) update (adam.py:123-235 with
     magma.py:15-132): the Magma sums before the step (over the old moments,
     which the step overwrites), the step in update-only mode, then the
-    per-leaf scaling of its f32 updates by ``neg_lr * (mask * score)``."""
+    per-leaf scaling of its f32 updates by ``neg_lr * (mask * score)``.
+    ``fuse_apply=(params, key, stochastic)``: instead of scaling the
+    updates, apply them to the params with the scaling folded in (the
+    fused step's ``apply_updates``); returns (None, new state)."""
     torch = _torch()
     g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
     mu_leaves = _tree.flatten_up_to(g_td, state.mu) if g_leaves else []
@@ -182,14 +186,43 @@ def _magma_step(engine, magma_p, magma_tau, updates, state, params, *, decay_mas
         scores = torch.stack([_require_device_tensor(s_leaves[i], "magma score").reshape(()).to(
             device=device, dtype=torch.float32) for i in picked])
         lr = 1.0 if neg_lr is None else float(np.float32(neg_lr))
+        factor = torch.empty(len(picked), dtype=torch.float32, device=device) if fuse_apply else None
         _lib.check(lib.rf_magma_scale(table, len(picked), sums.data_ptr(), scores.data_ptr(), float(magma_p),
                                       float(magma_tau), int(magma_key[0]), int(magma_key[1]), len(g_leaves), lr,
-                                      stream), "rf_magma_scale")
+                                      None if factor is None else factor.data_ptr(), stream), "rf_magma_scale")
+        if fuse_apply:
+            _magma_apply(fuse_apply, g_td, picked, out_leaves, factor, lr, stream)
+            out = None
     new_s = list(s_leaves)
     for k, i in enumerate(picked):
         new_s[i] = scores[k]
     del hold
     return out, new_state._replace(magma_s=_tree.unflatten(g_td, new_s))
+
+
+def _magma_apply(fuse_apply, g_td, picked, out_leaves, factor, neg_lr, stream) -> None:
+    """apply_updates (utils.py:648-708) of the unscaled updates with
+    ``neg_lr * (factor[k] * u)`` per leaf (``rf_magma_apply_updates``); the
+    param key of leaf i is split(key)[i], as apply_updates keys it."""
+    params, key, stochastic = fuse_apply
+    if stochastic and key is None:
+        raise ValueError("apply_updates requires a PRNG `key` when stochastic=True. "
+                         "Pass stochastic=False for deterministic rounding.")
+    p_leaves = _tree.flatten_up_to(g_td, params)
+    rows = (_lib.ApplyLeaf * len(picked))()
+    for k, i in enumerate(picked):
+        p = _require_device_tensor(p_leaves[i], "param")
+        if not p.is_contiguous():
+            raise ValueError("params must be contiguous (they are updated in place)")
+        if p.numel() != out_leaves[i].numel():
+            raise ValueError("param and update sizes differ")
+        r = rows[k]
+        r.param, r.updates, r.bits = p.data_ptr(), out_leaves[i].data_ptr(), None
+        r.size, r.param_dtype, r.param_index = p.numel(), _dtype_code(p), i
+    k0, k1 = (prng.as_key(key) if key is not None else np.zeros(2, np.uint32))[:2]
+    _lib.check(_lib.lib().rf_magma_apply_updates(rows, len(picked), factor.data_ptr(), neg_lr,
+                                                 1 if stochastic else 0, int(k0), int(k1), stream),
+               "rf_magma_apply_updates")
 
 
 def _has_nonzero_or_scheduled(value) -> bool:
@@ -306,18 +339,22 @@ class _AdamwMagmaUpdate:
         return self._step(updates, state, params, apply=False)
 
     def _step(self, updates, state, params, *, apply: bool, skip_nonfinite=False, finite_out=None,
-              finite_host=None, clip_global_norm=None, clip_stats=None, **fused_only):
+              finite_host=None, clip_global_norm=None, clip_stats=None, param_key=None, param_sr=False,
+              random_bits=None):
+        """``apply=True``: the step applied to the params in place with the
+        Magma scaling folded into apply_updates (``param_key`` /
+        ``param_sr`` are apply_updates' ``key`` / ``stochastic``)."""
         del clip_stats
-        if apply or fused_only.get("random_bits") is not None:
-            raise NotImplementedError("the fused step with Magma: use adamw_step, which applies tx.update's "
-                                      "updates with apply_updates")
+        if random_bits is not None:
+            raise NotImplementedError("fed random bits are not supported with Magma")
         if skip_nonfinite or finite_out is not None or finite_host is not None or clip_global_norm:
             raise NotImplementedError(_MAGMA_FUSED_MSG)
         adam_state, lr_state = state[0], state[-1]
         neg_lr, new_lr_state = self._lr(lr_state)
         decay_mask, wd = _adam_decay(self.weight_decay, self.weight_decay_mask, updates, adam_state, params)
         out, new_adam = _magma_step(self.engine, *self.magma, updates, adam_state, params, decay_mask=decay_mask,
-                                    weight_decay=wd, neg_lr=neg_lr)
+                                    weight_decay=wd, neg_lr=neg_lr,
+                                    fuse_apply=(params, param_key, param_sr) if apply else None)
         return out, (new_adam,) + tuple(state[1:-1]) + (new_lr_state,)
 
 
@@ -427,14 +464,15 @@ def adamw_step(tx, params, grads, state, key=None, stochastic: bool = True, *, r
     from .adam8 import adamw8_step
 
     if isinstance(tx.update, _AdamwMagmaUpdate):
-        # Magma scales the finished update per leaf: tx.update, then
-        # apply_updates (utils.py:648-708), as the reference runs them.
+        # tx.update then apply_updates (utils.py:648-708), with Magma's
+        # per-leaf scaling folded into the apply pass
         if random_bits is not None or clip_global_norm is not None:
             raise NotImplementedError(_MAGMA_FUSED_MSG)
-        from ..utils import apply_updates
-
-        updates, new_state = tx.update(grads, state, params)
-        return apply_updates(params, updates, key=key, stochastic=stochastic), new_state
+        if stochastic and key is None:
+            raise ValueError("apply_updates requires a PRNG `key` when stochastic=True. "
+                             "Pass stochastic=False for deterministic rounding.")
+        _out, new_state = tx.update._step(grads, state, params, apply=True, param_key=key, param_sr=stochastic)
+        return params, new_state
     if isinstance(tx.update, _ScaleByAdamUpdate) or (isinstance(tx.update, _Adamw8Update)
                                                      and not isinstance(tx.update.engine, _AdamEngine)):
         raise TypeError("adamw_step needs a transformation built by adamw(...) or a composition of them "

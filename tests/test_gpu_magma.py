@@ -232,3 +232,31 @@ def test_magma_in_multi_transform_runs_its_group_separately():
         if labels[k] == "magma":
             np.testing.assert_array_equal(to_host(updates[k]).view(np.uint32),
                                           to_host(solo_updates[k]).view(np.uint32))
+
+
+@pytest.mark.parametrize("stochastic", [False, True])
+def test_adamw_step_magma_fused_apply_equals_update_plus_apply(stochastic):
+    """adamw_step folds Magma's per-leaf scaling into apply_updates: the
+    params, moments and scores equal tx.update + apply_updates bit for bit
+    (same arithmetic: neg_lr * ((m * s) * u), then f32(p) + u rounded)."""
+    import torch
+
+    import rollfast_amd as rf
+
+    _, pa = _tree(7, 0.02)
+    _, pb = _tree(7, 0.02)
+    tx = rf.adamw(learning_rate=1e-3, weight_decay=0.01, use_magma=True, key=rf.prng.PRNGKey(9))
+    sa, sb = tx.init(pa), tx.init(pb)
+    for step in range(3):
+        _, g = _tree(700 + step, 1e-2, as_grads=True)
+        key = rf.prng.PRNGKey(70 + step) if stochastic else None
+        pa, sa = rf.adamw_step(tx, pa, g, sa, key=key, stochastic=stochastic)
+        upd, sb = tx.update(g, sb, pb)
+        pb = rf.apply_updates(pb, upd, key=key, stochastic=stochastic)
+        torch.cuda.synchronize()
+        for i, (_shape, pd, _gd) in enumerate(SPEC):
+            view = np.uint16 if pd == "bf16" else np.uint32
+            np.testing.assert_array_equal(to_host(pa[f"l{i}"]).view(view), to_host(pb[f"l{i}"]).view(view))
+            np.testing.assert_array_equal(to_host(sa[0].mu[f"l{i}"]).view(np.uint32),
+                                          to_host(sb[0].mu[f"l{i}"]).view(np.uint32))
+            assert float(sa[0].magma_s[f"l{i}"].item()) == float(sb[0].magma_s[f"l{i}"].item())
