@@ -333,7 +333,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         holder["k"] += 1
         if optax:
             _, holder["state"] = tx.update(g, holder["state"], holder["params"])
-        elif magma:  # tx.update (Magma sums, step, Magma scaling) then apply_updates
+        elif magma:  # the step (with the Magma sums), the Magma factors, then apply_updates with them
             holder["params"], holder["state"] = rf.adamw_step(tx, holder["params"], g, holder["state"], key=key,
                                                               stochastic=param_sr)
         else:
@@ -368,10 +368,10 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         config["nonfinite"] = "skip (apply_if_finite, max_consecutive_errors=1; one int32 read back per step)"
         config["launches_per_step"] = 4
     if magma:
-        config["magma"] = ("use_magma=True (p 0.5, tau 2): sums before the step, per-leaf factors after it, "
-                           "folded into apply_updates")
+        config["magma"] = ("use_magma=True (p 0.5, tau 2): sums written by the step, per-leaf factors after "
+                           "it, folded into apply_updates")
         config["mode"] = "adamw_step (update-only step, then apply_updates with the Magma factor)"
-        config["launches_per_step"] = 5
+        config["launches_per_step"] = 4
     if shapes_fn is llama7b_shapes:
         cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr)  # noqa: E731
     else:
@@ -386,11 +386,11 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         mb = 4 if adam_mu == "f32" else 2
         nbytes = n_params * (2 + 2 + 2 + 2 * 2 * mb)  # p r+w, g r, two moments r+w
         if magma:
-            # update-only step writes f32 updates (4) instead of params (2);
-            # Magma sums read g and mu (2 + mb); apply_updates with the
-            # per-leaf Magma factor folded in reads the updates (4) and the
-            # params and writes the params (2 + 2)
-            nbytes = n_params * ((2 + 2 + 2 * 2 * mb + 4) + (2 + mb) + (4 + 2 + 2))
+            # update-only step writes f32 updates (4) instead of params (2)
+            # and the Magma sums (24 B per 2048 elements, left out);
+            # apply_updates with the per-leaf Magma factor folded in reads
+            # the updates (4) and the params and writes the params (2 + 2)
+            nbytes = n_params * ((2 + 2 + 2 * 2 * mb + 4) + (4 + 2 + 2))
         cpu = None
     return Workload(workload, n_params, "params/s", nbytes, step, config, cpu, metric)
 

@@ -159,6 +159,14 @@ typedef struct rf_adam8_hparams {
     int32_t n_groups;        /* 0: one group (the fields above); else exactly the plan's group
                                 count, 1 + the largest leaf.group at plan creation */
     int32_t reserved0;       /* 0 */
+    double* magma_sums;      /* optional device f64[3 * n_leaves]: the run also writes, per
+                                leaf of the plan's table, the Magma sums of
+                                optim/magma.py:98-106 -- sum(g*m'), sum(g*g), sum(m'*m') over
+                                the leaf, with g the (clipped) grad and m' the new first
+                                moment before storage -- the sums rf_magma_reduce computes in
+                                a pass of its own.  Plans whose every leaf has unquantized
+                                moments only (RF_ERR_UNSUPPORTED otherwise, and with
+                                RF_SKIP_NONFINITE).  NULL: none */
 } rf_adam8_hparams;
 
 typedef struct rf_adam8_plan rf_adam8_plan;

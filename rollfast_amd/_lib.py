@@ -93,6 +93,7 @@ class Adam8Hparams(ctypes.Structure):
         ("groups", _p),
         ("n_groups", ctypes.c_int32),
         ("reserved0", ctypes.c_int32),
+        ("magma_sums", _p),
     ]
 
 
@@ -131,7 +132,7 @@ class ApplyLeaf(ctypes.Structure):
 
 
 assert ctypes.sizeof(Adam8Leaf) == 120
-assert ctypes.sizeof(Adam8Hparams) == 120
+assert ctypes.sizeof(Adam8Hparams) == 128
 assert ctypes.sizeof(Adam8Group) == 32
 assert ctypes.sizeof(ApplyLeaf) == 40
 assert ctypes.sizeof(ClipLeaf) == 32

@@ -51,6 +51,8 @@ constexpr int64_t CHUNK = 2048;    // elements per fallback (unquantized moment)
 
 enum : int32_t { KIND_QFAST = 0, KIND_QGEN = 1, KIND_FALLBACK = 2, KIND_FALLBACK_VEC = 3 };
 
+struct Seg;
+
 // Kernel-side scalars (derived from rf_adam8_hparams on the host).
 struct KHp {
     float b1, omb1, b2, omb2;
@@ -70,6 +72,11 @@ struct KHp {
     const float* clip;        // device (scale, norm) of global-norm clipping, or null
     const float* gate;        // device flag: 1 = every grad finite, 0 = reject the step; null = no gate
     const rf_adam8_group* groups;  // per-group lr, decay, EMA weight and keys (grouped launch), or null
+    // Magma sums (optim/magma.py:15-132) written by the unquantized-moment
+    // units, or null: f64 triples (g·m', g·g, m'·m') per 2048-element chunk at
+    // mpart[3 * (msegs[leaf].unit_start + chunk)].
+    double* mpart;
+    const Seg* msegs;
 };
 
 // Work list: unit u belongs to the segment s with
@@ -213,6 +220,13 @@ __device__ __forceinline__ uint32_t pack4_u8(uint32_t a, uint32_t b, uint32_t c,
 }
 
 __device__ __forceinline__ uint32_t uniform_u32(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ double wave_sum_f64(double x)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, WAVE);
+    return x;
+}
 
 __device__ __forceinline__ void stage_tables(uint8_t* lds, const uint4* __restrict__ tables)
 {
@@ -463,6 +477,33 @@ struct UnitCtx {
     bool clip;        // grads are scaled by the global-norm clipping factor
     float cs, cs16;   // that factor as f32 and rounded to bf16
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;  // per-leaf keys
+    double* mpart;    // Magma partial sums (KHp::mpart) or null
+    int64_t mbase;    // the current leaf's first chunk slot in mpart
+};
+
+// One lane's share of a unit's Magma sums (optim/magma.py:98-106: vdot of
+// the raw update with the new first moment, and the two squared norms),
+// accumulated in f64 from the f32 values the step computes.
+struct MagmaAcc {
+    double dot = 0.0, gg = 0.0, mm = 0.0;
+    __device__ __forceinline__ void add(float g, float m)
+    {
+        const double gd = g, md = m;
+        dot += gd * md;
+        gg += gd * gd;
+        mm += md * md;
+    }
+    // Wave sums stored as the unit's partial triple (every lane calls it).
+    __device__ __forceinline__ void store(const UnitCtx& c, int64_t chunk)
+    {
+        const double a = wave_sum_f64(dot), b = wave_sum_f64(gg), d = wave_sum_f64(mm);
+        if ((threadIdx.x & (WAVE - 1)) == 0) {
+            double* out = c.mpart + 3 * (c.mbase + chunk);
+            out[0] = a;
+            out[1] = b;
+            out[2] = d;
+        }
+    }
 };
 
 // Global-norm clipping of one gradient element (finetune/transforms.py:79-82,
@@ -1022,6 +1063,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
     const int32_t mdt = L.moment_kind == RF_MOMENT_BF16 ? RF_BF16 : RF_F32;
     const bool store_sr = mdt == RF_BF16 && (L.flags & RF_LEAF_STORE_SR);
     const bool need_p = APPLY || c.wd_mode != WD_OFF;
+    MagmaAcc acc;
     for (int64_t e0 = base + lane; e0 < end; e0 += EW_BATCH * WAVE) {
         float g[EW_BATCH], mo[EW_BATCH], vo[EW_BATCH], p[EW_BATCH];
 #pragma unroll
@@ -1041,6 +1083,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
             if (e >= end) continue;
             float mm, vv;
             ema(h, mo[k], vo[k], g[k], mm, vv);
+            if (c.mpart) acc.add(g[k], mm);
             update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g[k], p[k]);
             if (store_sr) {
                 // optim/adam.py:219-222: _tree_stochastic_cast(moments, bfloat16, k1 | k2)
@@ -1054,6 +1097,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
             }
         }
     }
+    if (c.mpart) acc.store(c, chunk);
 }
 
 // Full 2048-element chunk of a fallback (unquantized-moment) leaf whose
@@ -1072,6 +1116,8 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
     const int32_t wdm = c.wd_mode;
     const bool need_p = APPLY || wdm != WD_OFF;
     const bool store_sr = BF16M && (L.flags & RF_LEAF_STORE_SR);
+    const bool msum = c.mpart != nullptr;
+    MagmaAcc acc;
 
     // Two chunks in flight: chunk j+1's loads are issued before chunk j's
     // arithmetic.
@@ -1106,6 +1152,7 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
         for (int t = 0; t < 8; ++t) {
             float mm, vv;
             ema(h, m[t], v[t], g[t], mm, vv);
+            if (msum) acc.add(g[t], mm);
             m[t] = mm;
             v[t] = vv;
             u[t] = decay_and_scale(h, adam_direction<NEST, EXACT>(h, mm, vv, g[t]), p[t], wdm);
@@ -1177,6 +1224,7 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
             store8_f32(L.nu, e0, v);
         }
     }
+    if (msum) acc.store(c, chunk);
 }
 
 template <bool APPLY, bool PSR, bool NEST, bool EXACT>
@@ -1282,6 +1330,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     c.lds = lds;
     c.wtab = wtab[wave_in_wg];
     c.fed = (h.flags & RF_FED_BITS) != 0;
+    c.mpart = nullptr;
+    c.mbase = 0;
     if (gate_rejects(h)) {
         reject_units<APPLY>(leaves, segs, total_units, wave, nwaves);
         return;
@@ -1340,6 +1390,8 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
     c.lds = lds;
     c.wtab = nullptr;
     c.fed = (h.flags & RF_FED_BITS) != 0;
+    c.mpart = h.mpart;
+    c.mbase = 0;
     if (gate_rejects(h)) {
         reject_units<APPLY>(leaves, segs, total_units, wave, nwaves);
         return;
@@ -1357,6 +1409,7 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
             L = leaves[cur_leaf];
             group_hparams(hl, h, L);
             leaf_context(c, L, hl, MSR, PSR);
+            if (h.mpart) c.mbase = h.msegs[cur_leaf].unit_start;
         }
         const int64_t idx = sg.first + (u - sg.unit_start);
         if (sg.kind == KIND_QGEN) unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, hl);

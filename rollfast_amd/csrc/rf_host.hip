@@ -361,13 +361,6 @@ constexpr int64_t STEP_UNITS_PER_WAVE = 16;
 constexpr int64_t STEP_RUN_UNITS = RF_STEP_RUN_UNITS;
 constexpr bool STEP_GRID_ROUNDS = RF_STEP_GRID_ROUNDS != 0;
 
-__device__ __forceinline__ double wave_sum_f64(double x)
-{
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, WAVE);
-    return x;
-}
-
 __global__ __launch_bounds__(WG) void k_gnorm_partial(const rf_adam8_leaf* __restrict__ leaves,
                                                       const Seg* __restrict__ nsegs, int64_t nunits,
                                                       double* __restrict__ part)
@@ -508,24 +501,50 @@ __global__ __launch_bounds__(WG) void k_magma_partial(const rf_magma_leaf* __res
     }
 }
 
-// Leaf i's three sums from its units' partials.
+// Leaf i's three sums from its units' partials: one workgroup per leaf
+// (grid-strided over leaves), thread t summing units t, t + WG, ... with
+// four in flight, then wave and workgroup sums.  The order depends only on
+// WG, so a leaf's sums are the same on every run.
 __global__ __launch_bounds__(WG) void k_magma_leaf(const Seg* __restrict__ segs, int32_t nseg,
                                                    const double* __restrict__ part, double* __restrict__ sums)
 {
+    __shared__ double red[WAVES_PER_WG][3];
     const int lane = threadIdx.x & (WAVE - 1);
-    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
-    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
-    for (int64_t i = wave; i < nseg; i += nwaves) {
+    const int w = threadIdx.x / WAVE;
+    for (int64_t i = blockIdx.x; i < nseg; i += gridDim.x) {
         double acc[3] = {0.0, 0.0, 0.0};
-        for (int64_t u = segs[i].unit_start + lane; u < segs[i + 1].unit_start; u += WAVE)
+        const int64_t u1 = segs[i + 1].unit_start;
+        int64_t u = segs[i].unit_start + threadIdx.x;
+        for (; u + 3 * WG < u1; u += 4 * WG) {
+            double t[4][3];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int k = 0; k < 3; ++k) t[j][k] = part[3 * (u + j * WG) + k];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int k = 0; k < 3; ++k) acc[k] += t[j][k];
+        }
+        for (; u < u1; u += WG)
 #pragma unroll
             for (int k = 0; k < 3; ++k) acc[k] += part[3 * u + k];
 #pragma unroll
         for (int k = 0; k < 3; ++k) acc[k] = wave_sum_f64(acc[k]);
         if (lane == 0) {
 #pragma unroll
-            for (int k = 0; k < 3; ++k) sums[3 * i + k] = acc[k];
+            for (int k = 0; k < 3; ++k) red[w][k] = acc[k];
         }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                double a = red[0][k];
+                for (int ww = 1; ww < WAVES_PER_WG; ++ww) a += red[ww][k];
+                sums[3 * i + k] = a;
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -942,6 +961,13 @@ struct rf_adam8_plan {
     double* d_npart = nullptr;
     double* d_leafsum = nullptr;
     float* d_clip = nullptr;  // (scale, norm, finite as f32, finite as int32 bits)
+    // Magma sums written by the step (plans whose every leaf has unquantized
+    // moments): one Seg per leaf whose unit_start is the leaf's first
+    // 2048-element chunk slot, and an f64 triple per chunk (24 B per 2048
+    // elements).  n_mchunks < 0: the plan cannot produce them.
+    Seg* d_msegs = nullptr;
+    int64_t n_mchunks = -1;
+    double* d_mpart = nullptr;
     hipEvent_t ev_prepass = nullptr;  // recorded after the finite flag's copy to finite_host
     std::vector<rf_adam8_leaf> shape;   // creation-time table: the structure runs must match
     std::vector<uint8_t> vec;           // leaf has vectorised (16-byte aligned) work units
@@ -1120,9 +1146,33 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
         mark_list(nsegs);
     }
 
+    // Magma chunk slots: leaf i's chunks c (its fallback work units'
+    // indices) sum into slot msegs[i].unit_start + c.
+    std::vector<Seg> msegs;
+    int64_t mchunks = -1;
+    if (n_leaves > 0 && std::all_of(leaves, leaves + n_leaves,
+                                    [](const rf_adam8_leaf& L) { return L.moment_kind != RF_MOMENT_QUANTIZED; })) {
+        mchunks = 0;
+        for (int32_t i = 0; i < n_leaves; ++i) {
+            Seg sg{};
+            sg.unit_start = mchunks;
+            sg.leaf = i;
+            sg.kind = -1;
+            msegs.push_back(sg);
+            mchunks += (leaves[i].size + CHUNK - 1) / CHUNK;
+        }
+        Seg sentinel{};
+        sentinel.unit_start = mchunks;
+        sentinel.leaf = -1;
+        sentinel.kind = -1;
+        msegs.push_back(sentinel);
+        mark_list(msegs);
+    }
+
     int device = 0;
     HIP_TRY(hipGetDevice(&device));
     rf_adam8_plan* p = new rf_adam8_plan();
+    p->n_mchunks = mchunks;
     p->device = device;
     p->n_nsegs = n_nsegs;
     p->n_norm_units = nunits;
@@ -1156,6 +1206,12 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     if (e == hipSuccess && n_leaves > 0)
         e = hipMemcpy(p->d_leaves, leaves, sizeof(rf_adam8_leaf) * (size_t)n_leaves, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(p->d_segs, segs.data(), sizeof(Seg) * segs.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess && mchunks >= 0) {
+        e = hipMalloc(&p->d_msegs, sizeof(Seg) * msegs.size());
+        if (e == hipSuccess) e = hipMalloc(&p->d_mpart, sizeof(double) * 3 * (size_t)std::max<int64_t>(mchunks, 1));
+        if (e == hipSuccess)
+            e = hipMemcpy(p->d_msegs, msegs.data(), sizeof(Seg) * msegs.size(), hipMemcpyHostToDevice);
+    }
     if (e != hipSuccess) {
         release_plan(p);
         return fail(RF_ERR_HIP, std::string("plan allocation: ") + hipGetErrorString(e));
@@ -1177,11 +1233,32 @@ rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64
 
 namespace {
 
+// The Magma sums of a run that asked for them: every leaf's chunk triples
+// summed in a fixed order (a leaf without elements sums to zero).
+rf_status magma_sums_finish(const rf_adam8_plan* plan, const rf_adam8_hparams* hp, void* stream)
+{
+    if (!hp->magma_sums) return RF_OK;
+    DevState* ds = nullptr;
+    const rf_status st = device_state(&ds);
+    if (st != RF_OK) return st;
+    const int64_t lw = std::max<int64_t>(1, std::min<int64_t>(plan->n_leaves, (int64_t)ds->num_cus * 8));
+    hipLaunchKernelGGL(k_magma_leaf, dim3((unsigned)lw), dim3(WG), 0, (hipStream_t)stream, plan->d_msegs,
+                       plan->n_leaves, plan->d_mpart, hp->magma_sums);
+    HIP_TRY(hipGetLastError());
+    return RF_OK;
+}
+
 rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, const rf_adam8_group* d_groups,
                       const BitsCover& cover, const rf_adam8_hparams* hp, void* stream)
 {
-    if (plan->total_units == 0) return RF_OK;
     const uint32_t f = hp->flags;
+    if (hp->magma_sums) {
+        if (plan->n_mchunks < 0)
+            return fail(RF_ERR_UNSUPPORTED, "magma_sums needs a plan whose every leaf has unquantized moments");
+        if (f & RF_SKIP_NONFINITE) return fail(RF_ERR_UNSUPPORTED, "magma_sums with RF_SKIP_NONFINITE");
+    }
+    if (plan->total_units == 0) return magma_sums_finish(plan, hp, stream);
+
     const bool msr = (f & RF_MOMENT_SR) != 0;
     const bool psr = (f & RF_PARAM_SR) != 0 && plan->apply;
     if (f & RF_FED_BITS) {
@@ -1261,6 +1338,8 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
     k.knu1 = hp->key_nu[1];
     k.kp0 = hp->key_param[0];
     k.kp1 = hp->key_param[1];
+    k.mpart = hp->magma_sums ? plan->d_mpart : nullptr;
+    k.msegs = plan->d_msegs;
 
     for (const PlanGroup& g : plan->groups) {
         adam_kernel_t fn =
@@ -1293,7 +1372,7 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         HIP_TRY(hipGetLastError());
     }
     HIP_TRY(hipGetLastError());
-    return RF_OK;
+    return magma_sums_finish(plan, hp, stream);
 }
 
 // Frees everything a plan owns (waiting for runs still in flight) and the
@@ -1311,7 +1390,8 @@ bool release_plan(rf_adam8_plan* plan)
     }
     if (plan->d_leaves) ok &= hipFree(plan->d_leaves) == hipSuccess;
     if (plan->d_segs) ok &= hipFree(plan->d_segs) == hipSuccess;
-    for (void* q : {(void*)plan->d_nsegs, (void*)plan->d_npart, (void*)plan->d_leafsum, (void*)plan->d_clip})
+    for (void* q : {(void*)plan->d_nsegs, (void*)plan->d_npart, (void*)plan->d_leafsum, (void*)plan->d_clip,
+                    (void*)plan->d_msegs, (void*)plan->d_mpart})
         if (q) ok &= hipFree(q) == hipSuccess;
     if (plan->ev_prepass) {
         (void)hipEventSynchronize(plan->ev_prepass);
@@ -1375,7 +1455,7 @@ rf_status rf_adam8_plan_run(const rf_adam8_plan* plan, const rf_adam8_hparams* h
     if (st != RF_OK) return st;
     if (hp->n_groups == 0) return plan_launch(plan, plan->d_leaves, nullptr, plan->cover, hp, stream);
     // The group table travels through the staging ring with the creation-time leaf table.
-    if (plan->total_units == 0) return RF_OK;
+    if (plan->total_units == 0) return plan_launch(plan, plan->d_leaves, nullptr, plan->cover, hp, stream);
     rf_adam8_plan* mp = const_cast<rf_adam8_plan*>(plan);
     return run_staged(mp, plan->shape.data(), plan->n_leaves, plan->cover, hp, stream);
 }
@@ -1400,7 +1480,8 @@ rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_leaf* lea
         if (plan->vec[i] && !leaf_vec_ok(L, plan->apply))
             return fail(RF_ERR_INVALID, "leaf " + std::to_string(i) + " lost the 16-byte alignment the plan relies on");
     }
-    if (plan->total_units == 0) return RF_OK;
+    // No work units: nothing to stage (plan_launch still writes zero Magma sums).
+    if (plan->total_units == 0) return plan_launch(plan, plan->d_leaves, nullptr, plan->cover, hp, stream);
     return run_staged(plan, leaves, n_leaves, bits_cover(leaves, n_leaves), hp, stream);
 }
 
@@ -1693,8 +1774,7 @@ rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, float b
         e = hipGetLastError();
     }
     if (e == hipSuccess) {
-        const int64_t lw = std::max<int64_t>(1, std::min<int64_t>((n_leaves + WAVES_PER_WG - 1) / WAVES_PER_WG,
-                                                                  (int64_t)ds->num_cus * 8));
+        const int64_t lw = std::max<int64_t>(1, std::min<int64_t>(n_leaves, (int64_t)ds->num_cus * 8));
         hipLaunchKernelGGL(k_magma_leaf, dim3((unsigned)lw), dim3(WG), 0, s, d_segs, n_leaves, d_part, sums);
         e = hipGetLastError();
     }

@@ -19,11 +19,12 @@ unquantized ("fallback") moment path:
   (adam.py:381-406), fused into the same launch.
 
 Magma (``use_magma=True``, optim/magma.py:15-132 as adam.py:127-131,
-:203-217 call it): before the step, ``rf_magma_reduce`` sums ``g * m'``,
-``g * g`` and ``m' * m'`` per leaf over the step's new first moment ``m'``;
-the step then runs in update-only mode (decay inside, f32 product); after
-it, ``rf_magma_scale`` turns the sums into the leaf's cosine, score and
-Bernoulli mask and scales the update in place (times ``-lr`` for ``adamw``).
+:203-217 call it): the step runs in update-only mode (decay inside, f32
+product) and also sums ``g * m'``, ``g * g`` and ``m' * m'`` per leaf over
+its new first moment ``m'`` (the plan's ``magma_sums`` output); after it,
+``rf_magma_scale`` turns the sums into the leaf's cosine, score and
+Bernoulli mask and scales the update in place (times ``-lr`` for ``adamw``),
+or ``adamw_step`` folds that factor into ``apply_updates``.
 The PRNG key splits three ways (next, SR, Magma).  Magma runs without the
 fused clipping, the non-finite guard and the grouped launch: those raise
 ``NotImplementedError`` (a ``chain``/``multi_transform`` around it still
@@ -135,8 +136,8 @@ def _dtype_code(t) -> int:
 def _magma_step(engine, magma_p, magma_tau, updates, state, params, *, decay_mask, weight_decay, neg_lr,
                 fuse_apply=None):
     """One scale_by_adam(use_magma=True) update (adam.py:123-235 with
-    magma.py:15-132): the Magma sums before the step (over the old moments,
-    which the step overwrites), the step in update-only mode, then the
+    magma.py:15-132): the step in update-only mode, which also writes each
+    leaf's Magma sums (of the raw update and the new first moment), then the
     per-leaf scaling of its f32 updates by ``neg_lr * (mask * score)``.
     ``fuse_apply=(params, key, stochastic)``: instead of scaling the
     updates, apply them to the params with the scaling folded in (the
@@ -169,14 +170,13 @@ def _magma_step(engine, magma_p, magma_tau, updates, state, params, *, decay_mas
         r.grad_dtype, r.mu_dtype, r.key_index = _dtype_code(g), _dtype_code(m), i
     lib = _lib.lib()
     magma_key = prng.split(prng.as_key(state.key), 3)[2]
-    b1 = float(_as_f32(engine.cfg.b1))
-    omb1 = float(engine.ema_weight(engine.cfg.b1))
     with torch.cuda.device(device):
         stream = _lib.stream_ptr()
+        # The step's rows are the picked leaves, in order (both skip the
+        # leaves whose update or first moment is None / MaskedNode).
         sums = torch.empty(3 * len(picked), dtype=torch.float64, device=device)
-        _lib.check(lib.rf_magma_reduce(table, len(picked), b1, omb1, sums.data_ptr(), stream), "rf_magma_reduce")
         out, new_state = engine.run(updates, state, params, apply=False, decay_mask=decay_mask,
-                                    weight_decay=weight_decay, neg_lr=None)
+                                    weight_decay=weight_decay, neg_lr=None, magma_sums=sums)
         out_leaves = _tree.flatten_up_to(g_td, out)
         for k, i in enumerate(picked):
             u = out_leaves[i]

@@ -695,9 +695,10 @@ class _Engine:
 
     def _launch(self, table, n_rows, device, plan, count_inc, key_mu, key_nu, *, apply, decay_mask,
                 weight_decay, neg_lr, param_key, param_sr, random_bits, clip_global_norm, clip_stats,
-                skip_nonfinite, finite_out, finite_host):
+                skip_nonfinite, finite_out, finite_host, magma_sums=None):
         """Scalars of the step (adam8.py:322-339 and the optax chain) and the
-        plan launch over ``table``."""
+        plan launch over ``table``.  ``magma_sums``: a device f64 tensor of
+        3 per table row that the launch fills with the rows' Magma sums."""
         torch = _torch()
         cfg = self.cfg
         flags = 0
@@ -725,6 +726,8 @@ class _Engine:
         hp.neg_lr = neg_lr if neg_lr is not None else np.float32(1.0)
         hp.key_mu[0], hp.key_mu[1] = int(key_mu[0]), int(key_mu[1])
         hp.key_nu[0], hp.key_nu[1] = int(key_nu[0]), int(key_nu[1])
+        if magma_sums is not None:
+            hp.magma_sums = magma_sums.data_ptr()
 
         if n_rows:
             with torch.cuda.device(device):
@@ -750,6 +753,7 @@ class _Engine:
         skip_nonfinite: bool = False,
         finite_out=None,
         finite_host=None,
+        magma_sums=None,
     ):
         torch = _torch()
         cfg = self.cfg
@@ -775,7 +779,8 @@ class _Engine:
                              apply=apply, decay_mask=decay_mask, weight_decay=weight_decay, neg_lr=neg_lr,
                              param_key=param_key, param_sr=param_sr, random_bits=None,
                              clip_global_norm=clip_global_norm, clip_stats=clip_stats,
-                             skip_nonfinite=skip_nonfinite, finite_out=finite_out, finite_host=finite_host)
+                             skip_nonfinite=skip_nonfinite, finite_out=finite_out, finite_host=finite_host,
+                             magma_sums=magma_sums)
                 return out_tree, self.new_state(state, count_inc, next_key)
 
         g_leaves, g_td = _tree.flatten(updates, is_leaf=_is_passthrough_leaf)
@@ -820,7 +825,7 @@ class _Engine:
                      decay_mask=decay_mask, weight_decay=weight_decay, neg_lr=neg_lr, param_key=param_key,
                      param_sr=param_sr, random_bits=random_bits, clip_global_norm=clip_global_norm,
                      clip_stats=clip_stats, skip_nonfinite=skip_nonfinite, finite_out=finite_out,
-                     finite_host=finite_host)
+                     finite_host=finite_host, magma_sums=magma_sums)
 
         new_state = self.new_state(state, count_inc, next_key)
         out_tree = _tree.unflatten(g_td, out_leaves) if not apply else None

@@ -56,7 +56,7 @@ def test_dynamic_symbols_are_exactly_the_declared_entry_points():
 
 def test_struct_sizes_match_header():
     assert ctypes.sizeof(_lib.Adam8Leaf) == 120
-    assert ctypes.sizeof(_lib.Adam8Hparams) == 120
+    assert ctypes.sizeof(_lib.Adam8Hparams) == 128
     assert ctypes.sizeof(_lib.Adam8Group) == 32
     assert ctypes.sizeof(_lib.ApplyLeaf) == 40
     assert ctypes.sizeof(_lib.MagmaLeaf) == 48

@@ -260,3 +260,76 @@ def test_adamw_step_magma_fused_apply_equals_update_plus_apply(stochastic):
             np.testing.assert_array_equal(to_host(sa[0].mu[f"l{i}"]).view(np.uint32),
                                           to_host(sb[0].mu[f"l{i}"]).view(np.uint32))
             assert float(sa[0].magma_s[f"l{i}"].item()) == float(sb[0].magma_s[f"l{i}"].item())
+
+
+def _float64_sums(g, mu_new):
+    """The three Magma sums of one leaf in float64 and the sums of the
+    terms' magnitudes (the scale of any reordering error)."""
+    g64, m64 = g.astype(np.float64), mu_new.astype(np.float64)
+    terms = (g64 * m64, g64 * g64, m64 * m64)
+    return np.array([t.sum() for t in terms]), np.array([np.abs(t).sum() for t in terms])
+
+
+@pytest.mark.parametrize("mu_dtype", [None, "bf16"])
+def test_step_magma_sums_match_reduce_and_float64(mu_dtype):
+    """The step's own Magma sums (the plan's magma_sums output, which
+    scale_by_adam(use_magma=True) reads) equal rf_magma_reduce's standalone
+    pass and a float64 sum over the oracle's new first moment, to the
+    reordering error of float64 sums (1e-12 of the terms' magnitudes)."""
+    import torch
+
+    import rollfast_amd as rf
+    from rollfast_amd import _lib
+
+    _, params = _tree(3, 0.02)
+    tx = rf.scale_by_adam(mu_dtype=torch.bfloat16 if mu_dtype else None, key=rf.prng.PRNGKey(2))
+    state = tx.init(params)
+    engine = tx.update.engine
+    b1 = np.float32(B1)
+    omb1 = np.float32(engine.ema_weight(B1))
+    for step in range(2):
+        ghost, gdev = _tree(200 + step, 1e-2, as_grads=True)
+        gl = [gdev[f"l{i}"] for i in range(len(SPEC))]
+        ml = [state.mu[f"l{i}"] for i in range(len(SPEC))]
+        mu_old = [to_host(m).copy() for m in ml]
+        table = (_lib.MagmaLeaf * len(SPEC))()
+        for i, (g, m) in enumerate(zip(gl, ml)):
+            r = table[i]
+            r.grad, r.mu, r.size = g.data_ptr(), m.data_ptr(), g.numel()
+            r.grad_dtype = _lib.RF_BF16 if g.dtype == torch.bfloat16 else _lib.RF_F32
+            r.mu_dtype = _lib.RF_BF16 if m.dtype == torch.bfloat16 else _lib.RF_F32
+            r.key_index = i
+        alone = torch.empty(3 * len(SPEC), dtype=torch.float64, device="cuda")
+        _lib.check(_lib.lib().rf_magma_reduce(table, len(SPEC), float(b1), float(omb1), alone.data_ptr(),
+                                              _lib.stream_ptr()), "rf_magma_reduce")
+        fused = torch.empty(3 * len(SPEC), dtype=torch.float64, device="cuda")
+        _, state = engine.run(gdev, state, None, apply=False, decay_mask=None, weight_decay=None, neg_lr=None,
+                              magma_sums=fused)
+        torch.cuda.synchronize()
+        alone_h, fused_h = to_host(alone).reshape(-1, 3), to_host(fused).reshape(-1, 3)
+        for i, (_, _, g_dt) in enumerate(SPEC):
+            mdt = "bf16" if mu_dtype else "f32"
+            g = _f32(ghost[i], g_dt)
+            mu_new = (b1 * _f32(mu_old[i], mdt) + omb1 * g).astype(np.float32)
+            want, scale = _float64_sums(g, mu_new)
+            tol = 1e-12 * scale + 1e-300
+            assert (np.abs(fused_h[i] - want) <= tol).all(), (step, i, fused_h[i], want)
+            assert (np.abs(alone_h[i] - want) <= tol).all(), (step, i, alone_h[i], want)
+
+
+def test_step_magma_sums_refused_for_quantized_moments():
+    """Only plans whose every leaf has unquantized moments produce the Magma
+    sums; an adamw8 plan (quantized moments) refuses them."""
+    import torch
+
+    import rollfast_amd as rf
+
+    params = {"w": torch.zeros(8192, dtype=torch.float32, device="cuda")}
+    tx = rf.adamw8(learning_rate=1e-3)
+    state = tx.init(params)
+    grads = {"w": torch.full((8192,), 1e-3, dtype=torch.float32, device="cuda")}
+    engine = tx.update.engine
+    sums = torch.empty(3, dtype=torch.float64, device="cuda")
+    with pytest.raises(NotImplementedError, match="unquantized moments"):
+        engine.run(grads, state[0], None, apply=False, decay_mask=None, weight_decay=None, neg_lr=None,
+                   magma_sums=sums)
