@@ -164,9 +164,9 @@ typedef struct rf_adam8_hparams {
                                 optim/magma.py:98-106 -- sum(g*m'), sum(g*g), sum(m'*m') over
                                 the leaf, with g the (clipped) grad and m' the new first
                                 moment before storage -- the sums rf_magma_reduce computes in
-                                a pass of its own.  Plans whose every leaf has unquantized
-                                moments only (RF_ERR_UNSUPPORTED otherwise, and with
-                                RF_SKIP_NONFINITE).  NULL: none */
+                                a pass of its own.  Update-only plans whose every leaf has
+                                unquantized moments only (RF_ERR_UNSUPPORTED otherwise, and
+                                with RF_SKIP_NONFINITE).  NULL: none */
 } rf_adam8_hparams;
 
 typedef struct rf_adam8_plan rf_adam8_plan;

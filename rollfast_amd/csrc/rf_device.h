@@ -73,7 +73,7 @@ struct KHp {
     const float* gate;        // device flag: 1 = every grad finite, 0 = reject the step; null = no gate
     const rf_adam8_group* groups;  // per-group lr, decay, EMA weight and keys (grouped launch), or null
     // Magma sums (optim/magma.py:15-132) written by the unquantized-moment
-    // units, or null: f64 triples (g·m', g·g, m'·m') per 2048-element chunk at
+    // units of an update-only launch, or null: f64 triples (g·m', g·g, m'·m') per 2048-element chunk at
     // mpart[3 * (msegs[leaf].unit_start + chunk)].
     double* mpart;
     const Seg* msegs;
@@ -1063,6 +1063,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
     const int32_t mdt = L.moment_kind == RF_MOMENT_BF16 ? RF_BF16 : RF_F32;
     const bool store_sr = mdt == RF_BF16 && (L.flags & RF_LEAF_STORE_SR);
     const bool need_p = APPLY || c.wd_mode != WD_OFF;
+    const bool msum = !APPLY && c.mpart != nullptr;  // Magma sums: update-only launches
     MagmaAcc acc;
     for (int64_t e0 = base + lane; e0 < end; e0 += EW_BATCH * WAVE) {
         float g[EW_BATCH], mo[EW_BATCH], vo[EW_BATCH], p[EW_BATCH];
@@ -1083,7 +1084,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
             if (e >= end) continue;
             float mm, vv;
             ema(h, mo[k], vo[k], g[k], mm, vv);
-            if (c.mpart) acc.add(g[k], mm);
+            if (msum) acc.add(g[k], mm);
             update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g[k], p[k]);
             if (store_sr) {
                 // optim/adam.py:219-222: _tree_stochastic_cast(moments, bfloat16, k1 | k2)
@@ -1097,7 +1098,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
             }
         }
     }
-    if (c.mpart) acc.store(c, chunk);
+    if (msum) acc.store(c, chunk);
 }
 
 // Full 2048-element chunk of a fallback (unquantized-moment) leaf whose
@@ -1116,7 +1117,7 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
     const int32_t wdm = c.wd_mode;
     const bool need_p = APPLY || wdm != WD_OFF;
     const bool store_sr = BF16M && (L.flags & RF_LEAF_STORE_SR);
-    const bool msum = c.mpart != nullptr;
+    const bool msum = !APPLY && c.mpart != nullptr;  // Magma sums: update-only launches
     MagmaAcc acc;
 
     // Two chunks in flight: chunk j+1's loads are issued before chunk j's

@@ -1255,6 +1255,7 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
     if (hp->magma_sums) {
         if (plan->n_mchunks < 0)
             return fail(RF_ERR_UNSUPPORTED, "magma_sums needs a plan whose every leaf has unquantized moments");
+        if (plan->apply) return fail(RF_ERR_UNSUPPORTED, "magma_sums needs an update-only plan (apply = 0)");
         if (f & RF_SKIP_NONFINITE) return fail(RF_ERR_UNSUPPORTED, "magma_sums with RF_SKIP_NONFINITE");
     }
     if (plan->total_units == 0) return magma_sums_finish(plan, hp, stream);

@@ -333,3 +333,20 @@ def test_step_magma_sums_refused_for_quantized_moments():
     with pytest.raises(NotImplementedError, match="unquantized moments"):
         engine.run(grads, state[0], None, apply=False, decay_mask=None, weight_decay=None, neg_lr=None,
                    magma_sums=sums)
+
+
+def test_step_magma_sums_refused_for_fused_plans():
+    """The Magma sums come from update-only launches only: a fused step
+    (params written) refuses them."""
+    import torch
+
+    import rollfast_amd as rf
+
+    params = {"w": torch.zeros(4096, dtype=torch.float32, device="cuda")}
+    tx = rf.adamw(learning_rate=1e-3)
+    state = tx.init(params)
+    grads = {"w": torch.full((4096,), 1e-3, dtype=torch.float32, device="cuda")}
+    sums = torch.empty(3, dtype=torch.float64, device="cuda")
+    with pytest.raises(NotImplementedError, match="update-only"):
+        tx.update.engine.run(grads, state[0], params, apply=True, decay_mask=None, weight_decay=None,
+                             neg_lr=np.float32(-1e-3), magma_sums=sums)
