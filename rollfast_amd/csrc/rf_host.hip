@@ -991,7 +991,10 @@ rf_status validate_leaf(const rf_adam8_leaf& L, int32_t i, int32_t apply)
     if (L.size > 0 && !L.grad) return fail(RF_ERR_INVALID, at + "null grad");
     if (L.size > 0 && !L.param && (apply || (L.flags & RF_LEAF_DECAY))) return fail(RF_ERR_INVALID, at + "null param");
     if (L.size > 0 && !apply && !L.updates) return fail(RF_ERR_INVALID, at + "null updates in update-only mode");
-    if (!L.mu || !L.nu) return fail(RF_ERR_INVALID, at + "null moment buffer");
+    // An empty unquantized-moment leaf has no work units (its buffers are
+    // never read); a quantized one may still own a padded block.
+    if ((L.size > 0 || L.moment_kind == RF_MOMENT_QUANTIZED) && (!L.mu || !L.nu))
+        return fail(RF_ERR_INVALID, at + "null moment buffer");
     if (L.moment_kind == RF_MOMENT_QUANTIZED) {
         if (L.block_size <= 0) return fail(RF_ERR_INVALID, at + "block_size must be positive");
         if (!L.mu_scales || !L.nu_scales) return fail(RF_ERR_INVALID, at + "null scales");

@@ -350,3 +350,29 @@ def test_step_magma_sums_refused_for_fused_plans():
     with pytest.raises(NotImplementedError, match="update-only"):
         tx.update.engine.run(grads, state[0], params, apply=True, decay_mask=None, weight_decay=None,
                              neg_lr=np.float32(-1e-3), magma_sums=sums)
+
+
+@pytest.mark.parametrize("only_empty", [False, True])
+def test_magma_zero_size_leaf(only_empty):
+    """A leaf without elements (the step has no work units for it) sums to
+    zero: cosine 0, score 0.9 * s + 0.1 * sigmoid(0), its Bernoulli draw
+    still taken from its own key; a tree of only such leaves runs no step
+    kernel at all and still gets its sums."""
+    import torch
+
+    import rollfast_amd as rf
+
+    params = {"e": torch.zeros(0, dtype=torch.float32, device="cuda")}
+    if not only_empty:
+        params["w"] = torch.full((3000,), 0.01, dtype=torch.float32, device="cuda")
+    tx = rf.scale_by_adam(use_magma=True, magma_p=0.5, magma_tau=2.0, key=rf.prng.PRNGKey(9))
+    state = tx.init(params)
+    grads = {k: torch.full_like(v, 1e-3) for k, v in params.items()}
+    names = sorted(params)  # the flattening order of a dict tree
+    leaf_keys = orc.split(tuple(orc.split(tuple(int(k) for k in state.key), 3)[2]), len(names))
+    updates, new_state = tx.update(grads, state, params)
+    torch.cuda.synchronize()
+    i = names.index("e")
+    s_want, _ = orc.magma_leaf(np.zeros(0, np.float32), np.zeros(0, np.float32), 0.5, leaf_keys[i], 0.5, 2.0)
+    assert float(new_state.magma_s["e"].item()) == float(s_want)
+    assert updates["e"].numel() == 0
