@@ -214,6 +214,37 @@ RF_API rf_status rf_adam8_step(const rf_adam8_leaf* leaves, int32_t n_leaves, in
                         const rf_adam8_hparams* hp, void* stream);
 
 /*
+ * rf_adam8_step without allocation.  No counterpart in the reference (whose
+ * hot path is Python traced by jax.jit); it is for callers that cannot
+ * allocate device memory inside a step: code under HIP graph capture, an
+ * XLA FFI handler (which must not allocate behind XLA's allocator), tight
+ * serving loops and harnesses that forbid hipMalloc.
+ *
+ * Same arguments and results as rf_adam8_step (fused or update-only, every
+ * flag, clipping, the finite flag and groups), except: it does not wait for
+ * the stream (the work is enqueued on it; a finite_host flag is there once
+ * the stream has passed the pre-pass), and it refuses magma_sums
+ * (RF_ERR_UNSUPPORTED).  Its leaf and group tables, work lists and norm sums
+ * live in one device-scope array of RF_NOALLOC_SCRATCH_BYTES per GPU (held
+ * until the process ends); a tree whose tables need more fails with
+ * RF_ERR_INVALID before any work is enqueued.  The tables take about 184 B
+ * per leaf; with clipping or the finite flag add 8 B per 16,384 elements
+ * (Llama-7B: 54 KB, 3.35 MB with clipping).  The host copies the tables
+ * with one stream-ordered hipMemcpyAsync from pageable memory, so `leaves`
+ * may be reused when the call returns.
+ *
+ * Every call on one GPU uses that GPU's single array: calls that overlap on
+ * one GPU (enqueued on different streams, or from threads that race) race
+ * on it and give wrong results.  Calls on one stream are ordered.  The first
+ * call of the library on a device uploads the lookup tables with a
+ * synchronous copy; a caller that captures graphs makes one call on the
+ * device before capturing.
+ */
+#define RF_NOALLOC_SCRATCH_BYTES (8u << 20)
+RF_API rf_status rf_adam8_step_noalloc(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply,
+                                       const rf_adam8_hparams* hp, void* stream);
+
+/*
  * adam8.py:113-187 quantize_blocks on a device f32 array of `size` elements:
  * values [nblocks*block_size] (uint8 codes, or int8 for the symmetric
  * quantizer; padding included), scales f32 [nblocks].  sr != 0 selects

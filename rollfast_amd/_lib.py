@@ -29,6 +29,7 @@ RF_FED_BITS = 256
 RF_SKIP_NONFINITE = 512
 RF_LEAF_DECAY = 1
 RF_LEAF_STORE_SR = 2
+RF_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 _p = ctypes.c_void_p
 
@@ -146,6 +147,7 @@ EXPORTS = (
     "rf_adam8_plan_info",
     "rf_adam8_plan_destroy",
     "rf_adam8_step",
+    "rf_adam8_step_noalloc",
     "rf_blockwise_quantize",
     "rf_blockwise_dequantize",
     "rf_sr_bf16",
@@ -187,6 +189,7 @@ def lib() -> ctypes.CDLL:
     L.rf_adam8_plan_info.argtypes = [_p, ctypes.POINTER(i64), ctypes.POINTER(i64), ctypes.POINTER(i64)]
     L.rf_adam8_plan_destroy.argtypes = [_p]
     L.rf_adam8_step.argtypes = [ctypes.POINTER(Adam8Leaf), i32, i32, ctypes.POINTER(Adam8Hparams), _p]
+    L.rf_adam8_step_noalloc.argtypes = [ctypes.POINTER(Adam8Leaf), i32, i32, ctypes.POINTER(Adam8Hparams), _p]
     L.rf_blockwise_quantize.argtypes = [i32, _p, i64, i32, i32, u32, u32, _p, _p, _p, _p]
     L.rf_blockwise_dequantize.argtypes = [i32, _p, _p, i64, i32, i32, _p, _p]
     L.rf_sr_bf16.argtypes = [_p, i64, u32, u32, _p, _p, _p]

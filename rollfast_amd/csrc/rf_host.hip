@@ -818,16 +818,35 @@ uint32_t host_table_code(const uint8_t* tb, int32_t quantizer, float n)
     return cand + (n >= t ? 1u : 0u);
 }
 
+}  // namespace
+
+// ---- device-scope arrays (one copy per GPU, held until the process ends) ----
+// The codebooks and requantization lookup tables every step kernel stages.
+static __device__ __align__(256) uint4 lookup_tables[TABLE_BYTES / 16];
+// rf_adam8_step_noalloc's working memory: the leaf and group tables, the work
+// lists and the norm pre-pass's partial sums of one call.  Every call on a
+// GPU shares that GPU's copy and leaves its contents behind; nothing in it
+// needs to start at zero (each kernel writes every slot it later reads).
+// Calls that overlap on one GPU (different streams, or threads racing to
+// enqueue) race on it.
+static __device__ __align__(256) uint8_t scratch[RF_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
 // ---- per-device state ----
 constexpr int MAX_DEV = 64;
 struct DevState {
     bool ready = false;
-    uint4* tables = nullptr;
+    uint4* tables = nullptr;     // this device's lookup_tables
+    uint8_t* scratch_ptr = nullptr;  // this device's scratch
     int num_cus = 0;
 };
 std::mutex g_mu;
 DevState g_dev[MAX_DEV];
 
+// First use of a device: its arrays' addresses (with the device current,
+// since each GPU holds its own copy at its own address) and the table upload
+// (one synchronous copy; no allocation).
 rf_status device_state(DevState** out)
 {
     int dev = 0;
@@ -839,7 +858,9 @@ rf_status device_state(DevState** out)
         const HostTables& ht = host_tables();
         if (!ht.error.empty()) return fail(RF_ERR_INVALID, "table construction failed: " + ht.error);
         HIP_TRY(hipDeviceGetAttribute(&d.num_cus, hipDeviceAttributeMultiprocessorCount, dev));
-        HIP_TRY(hipMalloc(&d.tables, TABLE_BYTES));
+        HIP_TRY(hipGetSymbolAddress((void**)&d.tables, HIP_SYMBOL(lookup_tables)));
+        HIP_TRY(hipGetSymbolAddress((void**)&d.scratch_ptr, HIP_SYMBOL(scratch)));
+        if (!d.tables || !d.scratch_ptr) return fail(RF_ERR_HIP, "hipGetSymbolAddress returned a null address");
         HIP_TRY(hipMemcpy(d.tables, ht.bytes.data(), TABLE_BYTES, hipMemcpyHostToDevice));
         d.ready = true;
     }
@@ -1029,6 +1050,143 @@ bool leaf_vec_ok(const rf_adam8_leaf& L, int32_t apply)
     return true;
 }
 
+// Host-side work lists of a launch over a leaf table (validated here): the
+// step's per-dtype lists, the norm pre-pass's units and Magma's chunk slots.
+struct WorkLists {
+    std::vector<Seg> segs;           // every launch's list, each ending in a sentinel
+    std::vector<PlanGroup> groups;   // one launch per list
+    int64_t units = 0;
+    std::vector<Seg> nsegs;          // norm units (NORM_UNIT elements) of the non-empty leaves
+    int32_t n_nsegs = 0;
+    int64_t nunits = 0;
+    std::vector<Seg> msegs;          // Magma chunk slots (every leaf unquantized), else empty
+    int64_t mchunks = -1;
+    std::vector<uint8_t> vecs;       // leaf has 16-byte aligned (vectorised) units
+    std::vector<Seg> gsegs[5];       // build space: the lists of each dtype combination
+};
+
+rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply, WorkLists& w)
+{
+    rf_status st = RF_OK;
+    std::vector<Seg>* gsegs = w.gsegs;
+    for (int c = 0; c < 5; ++c) gsegs[c].clear();
+    int64_t gunits[5] = {0, 0, 0, 0, 0};
+    auto add = [&](int32_t leaf, int combo, int32_t kind, int64_t first, int64_t count) {
+        if (count <= 0) return;
+        Seg sg{};
+        sg.unit_start = gunits[combo];
+        sg.first = first;
+        sg.leaf = leaf;
+        sg.kind = kind;
+        gsegs[combo].push_back(sg);
+        gunits[combo] += count;
+    };
+    std::vector<uint8_t>& vecs = w.vecs;
+    vecs.clear();
+    for (int32_t i = 0; i < n_leaves; ++i) {
+        const rf_adam8_leaf& L = leaves[i];
+        st = validate_leaf(L, i, apply);
+        if (st != RF_OK) return st;
+        const bool vec = leaf_vec_ok(L, apply);
+        vecs.push_back(vec ? 1 : 0);
+        // Full aligned 2048-blocks go to the fast kernel of their dtype
+        // combination; everything else to the generic kernel (group 4).
+        const int combo = dtype_combo(L);
+        if (L.moment_kind == RF_MOMENT_QUANTIZED) {
+            const int64_t bs = L.block_size;
+            const int64_t nb = nblocks_of(L.size, bs);
+            if (bs == FAST_BS && vec) {
+                const int64_t nfull = L.size / bs;
+                add(i, combo, KIND_QFAST, 0, nfull);
+                add(i, 4, KIND_QGEN, nfull, nb - nfull);
+            } else {
+                add(i, 4, KIND_QGEN, 0, nb);
+            }
+        } else {
+            // Full chunks of aligned leaves take the vectorised unit, the
+            // tail the element-wise one.
+            const int64_t nfull = vec ? L.size / CHUNK : 0;
+            add(i, 4, KIND_FALLBACK_VEC, 0, nfull);
+            add(i, 4, KIND_FALLBACK, nfull, (L.size - nfull * CHUNK + CHUNK - 1) / CHUNK);
+        }
+    }
+    std::vector<Seg>& segs = w.segs;
+    std::vector<PlanGroup>& groups = w.groups;
+    segs.clear();
+    groups.clear();
+    int64_t units = 0;
+    for (int combo = 4; combo >= 0; --combo) {
+        if (gunits[combo] == 0) continue;
+        groups.push_back({combo == 4 ? -1 : combo, (int64_t)segs.size(), gunits[combo]});
+        Seg sentinel{};
+        sentinel.unit_start = gunits[combo];
+        sentinel.leaf = -1;
+        sentinel.kind = -1;
+        gsegs[combo].push_back(sentinel);
+        mark_list(gsegs[combo]);
+        segs.insert(segs.end(), gsegs[combo].begin(), gsegs[combo].end());
+        units += gunits[combo];
+    }
+    if (segs.empty()) {
+        Seg sentinel{};
+        sentinel.leaf = -1;
+        sentinel.kind = -1;
+        segs.push_back(sentinel);
+    }
+
+    // Norm units for global-norm clipping: every non-empty leaf, in order.
+    std::vector<Seg>& nsegs = w.nsegs;
+    nsegs.clear();
+    int64_t nunits = 0;
+    for (int32_t i = 0; i < n_leaves; ++i) {
+        if (leaves[i].size <= 0) continue;
+        Seg sg{};
+        sg.unit_start = nunits;
+        sg.leaf = i;
+        nsegs.push_back(sg);
+        nunits += (leaves[i].size + NORM_UNIT - 1) / NORM_UNIT;
+    }
+    const int32_t n_nsegs = (int32_t)nsegs.size();
+    {
+        Seg sentinel{};
+        sentinel.unit_start = nunits;
+        sentinel.leaf = -1;
+        sentinel.kind = -1;
+        nsegs.push_back(sentinel);
+        mark_list(nsegs);
+    }
+
+    // Magma chunk slots: leaf i's chunks c (its fallback work units'
+    // indices) sum into slot msegs[i].unit_start + c.
+    std::vector<Seg>& msegs = w.msegs;
+    msegs.clear();
+    int64_t mchunks = -1;
+    if (n_leaves > 0 && std::all_of(leaves, leaves + n_leaves,
+                                    [](const rf_adam8_leaf& L) { return L.moment_kind != RF_MOMENT_QUANTIZED; })) {
+        mchunks = 0;
+        for (int32_t i = 0; i < n_leaves; ++i) {
+            Seg sg{};
+            sg.unit_start = mchunks;
+            sg.leaf = i;
+            sg.kind = -1;
+            msegs.push_back(sg);
+            mchunks += (leaves[i].size + CHUNK - 1) / CHUNK;
+        }
+        Seg sentinel{};
+        sentinel.unit_start = mchunks;
+        sentinel.leaf = -1;
+        sentinel.kind = -1;
+        msegs.push_back(sentinel);
+        mark_list(msegs);
+    }
+
+    w.units = units;
+    w.n_nsegs = n_nsegs;
+    w.nunits = nunits;
+    w.mchunks = mchunks;
+    return RF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1066,112 +1224,14 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     DevState* ds = nullptr;
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
-    std::vector<Seg> gsegs[5];
-    int64_t gunits[5] = {0, 0, 0, 0, 0};
-    auto add = [&](int32_t leaf, int combo, int32_t kind, int64_t first, int64_t count) {
-        if (count <= 0) return;
-        Seg sg{};
-        sg.unit_start = gunits[combo];
-        sg.first = first;
-        sg.leaf = leaf;
-        sg.kind = kind;
-        gsegs[combo].push_back(sg);
-        gunits[combo] += count;
-    };
-    std::vector<uint8_t> vecs;
-    for (int32_t i = 0; i < n_leaves; ++i) {
-        const rf_adam8_leaf& L = leaves[i];
-        st = validate_leaf(L, i, apply);
-        if (st != RF_OK) return st;
-        const bool vec = leaf_vec_ok(L, apply);
-        vecs.push_back(vec ? 1 : 0);
-        // Full aligned 2048-blocks go to the fast kernel of their dtype
-        // combination; everything else to the generic kernel (group 4).
-        const int combo = dtype_combo(L);
-        if (L.moment_kind == RF_MOMENT_QUANTIZED) {
-            const int64_t bs = L.block_size;
-            const int64_t nb = nblocks_of(L.size, bs);
-            if (bs == FAST_BS && vec) {
-                const int64_t nfull = L.size / bs;
-                add(i, combo, KIND_QFAST, 0, nfull);
-                add(i, 4, KIND_QGEN, nfull, nb - nfull);
-            } else {
-                add(i, 4, KIND_QGEN, 0, nb);
-            }
-        } else {
-            // Full chunks of aligned leaves take the vectorised unit, the
-            // tail the element-wise one.
-            const int64_t nfull = vec ? L.size / CHUNK : 0;
-            add(i, 4, KIND_FALLBACK_VEC, 0, nfull);
-            add(i, 4, KIND_FALLBACK, nfull, (L.size - nfull * CHUNK + CHUNK - 1) / CHUNK);
-        }
-    }
-    std::vector<Seg> segs;
-    std::vector<PlanGroup> groups;
-    int64_t units = 0;
-    for (int combo = 4; combo >= 0; --combo) {
-        if (gunits[combo] == 0) continue;
-        groups.push_back({combo == 4 ? -1 : combo, (int64_t)segs.size(), gunits[combo]});
-        Seg sentinel{};
-        sentinel.unit_start = gunits[combo];
-        sentinel.leaf = -1;
-        sentinel.kind = -1;
-        gsegs[combo].push_back(sentinel);
-        mark_list(gsegs[combo]);
-        segs.insert(segs.end(), gsegs[combo].begin(), gsegs[combo].end());
-        units += gunits[combo];
-    }
-    if (segs.empty()) {
-        Seg sentinel{};
-        sentinel.leaf = -1;
-        sentinel.kind = -1;
-        segs.push_back(sentinel);
-    }
-
-    // Norm units for global-norm clipping: every non-empty leaf, in order.
-    std::vector<Seg> nsegs;
-    int64_t nunits = 0;
-    for (int32_t i = 0; i < n_leaves; ++i) {
-        if (leaves[i].size <= 0) continue;
-        Seg sg{};
-        sg.unit_start = nunits;
-        sg.leaf = i;
-        nsegs.push_back(sg);
-        nunits += (leaves[i].size + NORM_UNIT - 1) / NORM_UNIT;
-    }
-    const int32_t n_nsegs = (int32_t)nsegs.size();
-    {
-        Seg sentinel{};
-        sentinel.unit_start = nunits;
-        sentinel.leaf = -1;
-        sentinel.kind = -1;
-        nsegs.push_back(sentinel);
-        mark_list(nsegs);
-    }
-
-    // Magma chunk slots: leaf i's chunks c (its fallback work units'
-    // indices) sum into slot msegs[i].unit_start + c.
-    std::vector<Seg> msegs;
-    int64_t mchunks = -1;
-    if (n_leaves > 0 && std::all_of(leaves, leaves + n_leaves,
-                                    [](const rf_adam8_leaf& L) { return L.moment_kind != RF_MOMENT_QUANTIZED; })) {
-        mchunks = 0;
-        for (int32_t i = 0; i < n_leaves; ++i) {
-            Seg sg{};
-            sg.unit_start = mchunks;
-            sg.leaf = i;
-            sg.kind = -1;
-            msegs.push_back(sg);
-            mchunks += (leaves[i].size + CHUNK - 1) / CHUNK;
-        }
-        Seg sentinel{};
-        sentinel.unit_start = mchunks;
-        sentinel.leaf = -1;
-        sentinel.kind = -1;
-        msegs.push_back(sentinel);
-        mark_list(msegs);
-    }
-
+    WorkLists w;
+    st = build_work_lists(leaves, n_leaves, apply, w);
+    if (st != RF_OK) return st;
+    std::vector<Seg>& segs = w.segs;
+    std::vector<Seg>& nsegs = w.nsegs;
+    std::vector<Seg>& msegs = w.msegs;
+    const int64_t units = w.units, nunits = w.nunits, mchunks = w.mchunks;
+    const int32_t n_nsegs = w.n_nsegs;
     int device = 0;
     HIP_TRY(hipGetDevice(&device));
     rf_adam8_plan* p = new rf_adam8_plan();
@@ -1183,10 +1243,10 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     p->n_leaves = n_leaves;
     p->total_units = units;
     p->n_segs = (int64_t)segs.size();
-    p->groups = groups;
+    p->groups = w.groups;
     p->cover = bits_cover(leaves, n_leaves);
     p->shape.assign(leaves, leaves + n_leaves);
-    p->vec = vecs;
+    p->vec = w.vecs;
     // Every buffer a run needs is allocated here, so runs never allocate
     // (pinned-host and device allocation synchronise the device).
     const size_t table_bytes = sizeof(rf_adam8_leaf) * (size_t)std::max(n_leaves, 1);
@@ -1299,7 +1359,7 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         if (hp->finite_host) {
             HIP_TRY(hipMemcpyAsync(hp->finite_host, plan->d_clip + 3, sizeof(int32_t), hipMemcpyDeviceToHost,
                                    (hipStream_t)stream));
-            HIP_TRY(hipEventRecord(plan->ev_prepass, (hipStream_t)stream));
+            if (plan->ev_prepass) HIP_TRY(hipEventRecord(plan->ev_prepass, (hipStream_t)stream));
         }
     }
 
@@ -1524,6 +1584,83 @@ rf_status rf_adam8_step(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t a
     return st != RF_OK ? st : st2;
 }
 
+rf_status rf_adam8_step_noalloc(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply,
+                                const rf_adam8_hparams* hp, void* stream)
+{
+    if (!hp) return fail(RF_ERR_INVALID, "null hparams");
+    if (n_leaves < 0 || (n_leaves > 0 && !leaves)) return fail(RF_ERR_INVALID, "bad leaf table");
+    if (hp->magma_sums) return fail(RF_ERR_UNSUPPORTED, "rf_adam8_step_noalloc does not write Magma sums");
+    int32_t group_cap = 1;
+    for (int32_t i = 0; i < n_leaves; ++i) group_cap = std::max(group_cap, leaves[i].group + 1);
+    if (hp->n_groups < 0) return fail(RF_ERR_INVALID, "negative n_groups");
+    if (hp->n_groups > 0 && !hp->groups) return fail(RF_ERR_INVALID, "n_groups > 0 with a null group table");
+    if (hp->n_groups > 0 && hp->n_groups != group_cap)
+        return fail(RF_ERR_INVALID, "n_groups must be 0 or 1 + the largest leaf.group");
+    DevState* ds = nullptr;
+    rf_status st = device_state(&ds);
+    if (st != RF_OK) return st;
+    // Host-side lists in per-thread buffers that keep their capacity.
+    thread_local WorkLists w;
+    st = build_work_lists(leaves, n_leaves, apply, w);
+    if (st != RF_OK) return st;
+
+    // Scratch layout: what the host stages (leaf table, group table, step and
+    // norm work lists), then what the kernels write (norm partial sums per
+    // unit and per leaf, the clipping scalars).
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t n_groups = (size_t)hp->n_groups;
+    const size_t o_groups = up(sizeof(rf_adam8_leaf) * (size_t)n_leaves);
+    const size_t o_segs = up(o_groups + sizeof(rf_adam8_group) * n_groups);
+    const size_t o_nsegs = up(o_segs + sizeof(Seg) * w.segs.size());
+    // The norm sums exist only when the pre-pass runs (clipping or the finite flag).
+    const bool prepass = hp->clip_max_norm > 0.0f || (hp->flags & RF_SKIP_NONFINITE) || hp->finite_out ||
+                         hp->finite_host;
+    const size_t o_npart = up(o_nsegs + sizeof(Seg) * w.nsegs.size());
+    const size_t o_leafsum = up(o_npart + sizeof(double) * (size_t)(prepass ? std::max<int64_t>(w.nunits, 1) : 1));
+    const size_t o_clip = up(o_leafsum + sizeof(double) * (size_t)(prepass ? std::max(w.n_nsegs, 1) : 1));
+    const size_t need = o_clip + 4 * sizeof(float);
+    if (need > (size_t)RF_NOALLOC_SCRATCH_BYTES)
+        return fail(RF_ERR_INVALID, "rf_adam8_step_noalloc: this tree needs " + std::to_string(need) +
+                                        " bytes of scratch (leaf and group tables, work lists, norm sums); "
+                                        "the maximum is " + std::to_string((size_t)RF_NOALLOC_SCRATCH_BYTES) +
+                                        ": use a plan");
+    thread_local std::vector<uint8_t> host;
+    host.assign(o_npart, 0);
+    if (n_leaves > 0) std::memcpy(host.data(), leaves, sizeof(rf_adam8_leaf) * (size_t)n_leaves);
+    if (n_groups) std::memcpy(host.data() + o_groups, hp->groups, sizeof(rf_adam8_group) * n_groups);
+    std::memcpy(host.data() + o_segs, w.segs.data(), sizeof(Seg) * w.segs.size());
+    std::memcpy(host.data() + o_nsegs, w.nsegs.data(), sizeof(Seg) * w.nsegs.size());
+    uint8_t* const base = ds->scratch_ptr;
+    // Stream-ordered after earlier calls on this stream; from pageable memory
+    // the call returns once the source has been consumed.
+    HIP_TRY(hipMemcpyAsync(base, host.data(), o_npart, hipMemcpyHostToDevice, (hipStream_t)stream));
+
+    // The launch description of plan_launch, over the scratch (owns nothing).
+    rf_adam8_plan plan;
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    plan.device = dev;
+    plan.apply = apply ? 1 : 0;
+    plan.n_leaves = n_leaves;
+    plan.group_cap = group_cap;
+    plan.total_units = w.units;
+    plan.n_segs = (int64_t)w.segs.size();
+    plan.groups.swap(w.groups);  // lent for the launch, then handed back with its capacity
+    plan.d_leaves = (rf_adam8_leaf*)base;
+    plan.d_segs = (Seg*)(base + o_segs);
+    plan.d_nsegs = (Seg*)(base + o_nsegs);
+    plan.n_nsegs = w.n_nsegs;
+    plan.n_norm_units = w.nunits;
+    plan.d_npart = (double*)(base + o_npart);
+    plan.d_leafsum = (double*)(base + o_leafsum);
+    plan.d_clip = (float*)(base + o_clip);
+    plan.n_mchunks = -1;
+    const rf_adam8_group* d_groups = n_groups ? (const rf_adam8_group*)(base + o_groups) : nullptr;
+    st = plan_launch(&plan, plan.d_leaves, d_groups, bits_cover(leaves, n_leaves), hp, stream);
+    w.groups.swap(plan.groups);
+    return st;
+}
+
 rf_status rf_blockwise_quantize(int32_t quantizer, const float* x, int64_t size, int32_t block_size, int32_t sr,
                                 uint32_t key0, uint32_t key1, const uint32_t* bits, void* values, float* scales,
                                 void* stream)
@@ -1636,7 +1773,7 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    // One scratch allocation: leaf tables, segments, partials, leaf sums, (scale, norm, finite, 0).
+    // One stream-ordered allocation: leaf tables, segments, partials, leaf sums, (scale, norm, finite, 0).
     const size_t o_gl = 0;
     const size_t o_cl = o_gl + sizeof(rf_adam8_leaf) * (size_t)std::max(n_leaves, 1);
     const size_t o_sg = (o_cl + sizeof(rf_clip_leaf) * (size_t)std::max(n_leaves, 1) + 15) & ~(size_t)15;
@@ -1644,22 +1781,22 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
     const size_t o_ls = o_pt + sizeof(double) * (size_t)std::max<int64_t>(nunits, 1);
     const size_t o_cp = (o_ls + sizeof(double) * (size_t)std::max(nseg, 1) + 15) & ~(size_t)15;
     const size_t total = o_cp + 4 * sizeof(float);
-    uint8_t* scratch = nullptr;
-    HIP_TRY(hipMallocAsync((void**)&scratch, total, s));
+    uint8_t* buf = nullptr;
+    HIP_TRY(hipMallocAsync((void**)&buf, total, s));
     std::vector<uint8_t> host(o_pt);
     if (n_leaves > 0) {
         std::memcpy(host.data() + o_gl, gl.data(), sizeof(rf_adam8_leaf) * (size_t)n_leaves);
         std::memcpy(host.data() + o_cl, leaves, sizeof(rf_clip_leaf) * (size_t)n_leaves);
     }
     std::memcpy(host.data() + o_sg, nsegs.data(), sizeof(Seg) * nsegs.size());
-    hipError_t e = hipMemcpyAsync(scratch, host.data(), o_pt, hipMemcpyHostToDevice, s);
+    hipError_t e = hipMemcpyAsync(buf, host.data(), o_pt, hipMemcpyHostToDevice, s);
     // hipMemcpyAsync from pageable memory returns once the source is consumed.
-    const rf_adam8_leaf* d_gl = (const rf_adam8_leaf*)(scratch + o_gl);
-    const rf_clip_leaf* d_cl = (const rf_clip_leaf*)(scratch + o_cl);
-    const Seg* d_sg = (const Seg*)(scratch + o_sg);
-    double* d_pt = (double*)(scratch + o_pt);
-    double* d_ls = (double*)(scratch + o_ls);
-    float* d_cp = (float*)(scratch + o_cp);
+    const rf_adam8_leaf* d_gl = (const rf_adam8_leaf*)(buf + o_gl);
+    const rf_clip_leaf* d_cl = (const rf_clip_leaf*)(buf + o_cl);
+    const Seg* d_sg = (const Seg*)(buf + o_sg);
+    double* d_pt = (double*)(buf + o_pt);
+    double* d_ls = (double*)(buf + o_ls);
+    float* d_cp = (float*)(buf + o_cp);
     if (e == hipSuccess && nunits > 0) {
         const int64_t pw = std::max<int64_t>(1, std::min<int64_t>((nunits + WAVES_PER_WG - 1) / WAVES_PER_WG,
                                                                   (int64_t)ds->num_cus * 8));
@@ -1682,7 +1819,7 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
         hipLaunchKernelGGL(k_clip_scale, dim3(gx, n_leaves), dim3(WG), 0, s, d_cl, d_cp);
         e = hipGetLastError();
     }
-    hipError_t ef = hipFreeAsync(scratch, s);
+    hipError_t ef = hipFreeAsync(buf, s);
     if (e != hipSuccess) return fail(RF_ERR_HIP, std::string("rf_clip_by_global_norm: ") + hipGetErrorString(e));
     if (ef != hipSuccess) return fail(RF_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(ef));
     return RF_OK;
@@ -1724,24 +1861,24 @@ rf_status magma_list(const rf_magma_leaf* leaves, int32_t n_leaves, bool need_up
     return RF_OK;
 }
 
-// Stages the leaf table and the work list in one stream-ordered scratch
+// Stages the leaf table and the work list in one stream-ordered
 // allocation of `extra` more bytes (returned at `*tail`).
 rf_status magma_stage(const rf_magma_leaf* leaves, int32_t n_leaves, const std::vector<Seg>& segs, size_t extra,
-                      hipStream_t s, uint8_t** scratch, uint8_t** tail)
+                      hipStream_t s, uint8_t** buf, uint8_t** tail)
 {
     const size_t o_sg = (sizeof(rf_magma_leaf) * (size_t)std::max(n_leaves, 1) + 15) & ~(size_t)15;
     const size_t o_tail = (o_sg + sizeof(Seg) * segs.size() + 15) & ~(size_t)15;
-    HIP_TRY(hipMallocAsync((void**)scratch, o_tail + std::max<size_t>(extra, 16), s));
+    HIP_TRY(hipMallocAsync((void**)buf, o_tail + std::max<size_t>(extra, 16), s));
     std::vector<uint8_t> host(o_tail);
     if (n_leaves > 0) std::memcpy(host.data(), leaves, sizeof(rf_magma_leaf) * (size_t)n_leaves);
     std::memcpy(host.data() + o_sg, segs.data(), sizeof(Seg) * segs.size());
     // From pageable memory: returns once the source is consumed.
-    const hipError_t e = hipMemcpyAsync(*scratch, host.data(), o_tail, hipMemcpyHostToDevice, s);
+    const hipError_t e = hipMemcpyAsync(*buf, host.data(), o_tail, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) {
-        (void)hipFreeAsync(*scratch, s);
+        (void)hipFreeAsync(*buf, s);
         return fail(RF_ERR_HIP, std::string("hipMemcpyAsync: ") + hipGetErrorString(e));
     }
-    *tail = *scratch + o_tail;
+    *tail = *buf + o_tail;
     return RF_OK;
 }
 
@@ -1762,12 +1899,12 @@ rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, float b
     st = device_state(&ds);
     if (st != RF_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    uint8_t *scratch = nullptr, *tail = nullptr;
-    st = magma_stage(leaves, n_leaves, segs, sizeof(double) * 3 * (size_t)std::max<int64_t>(nunits, 1), s, &scratch,
+    uint8_t *buf = nullptr, *tail = nullptr;
+    st = magma_stage(leaves, n_leaves, segs, sizeof(double) * 3 * (size_t)std::max<int64_t>(nunits, 1), s, &buf,
                      &tail);
     if (st != RF_OK) return st;
-    const rf_magma_leaf* d_leaves = (const rf_magma_leaf*)scratch;
-    const Seg* d_segs = (const Seg*)(scratch + ((sizeof(rf_magma_leaf) * (size_t)n_leaves + 15) & ~(size_t)15));
+    const rf_magma_leaf* d_leaves = (const rf_magma_leaf*)buf;
+    const Seg* d_segs = (const Seg*)(buf + ((sizeof(rf_magma_leaf) * (size_t)n_leaves + 15) & ~(size_t)15));
     double* d_part = (double*)tail;
     hipError_t e = hipSuccess;
     if (nunits > 0) {
@@ -1782,7 +1919,7 @@ rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, float b
         hipLaunchKernelGGL(k_magma_leaf, dim3((unsigned)lw), dim3(WG), 0, s, d_segs, n_leaves, d_part, sums);
         e = hipGetLastError();
     }
-    const hipError_t ef = hipFreeAsync(scratch, s);
+    const hipError_t ef = hipFreeAsync(buf, s);
     if (e != hipSuccess) return fail(RF_ERR_HIP, std::string("rf_magma_reduce: ") + hipGetErrorString(e));
     if (ef != hipSuccess) return fail(RF_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(ef));
     return RF_OK;
@@ -1808,11 +1945,11 @@ rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const do
     st = device_state(&ds);
     if (st != RF_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    uint8_t *scratch = nullptr, *tail = nullptr;
-    st = magma_stage(leaves, n_leaves, segs, sizeof(float) * (size_t)n_leaves, s, &scratch, &tail);
+    uint8_t *buf = nullptr, *tail = nullptr;
+    st = magma_stage(leaves, n_leaves, segs, sizeof(float) * (size_t)n_leaves, s, &buf, &tail);
     if (st != RF_OK) return st;
-    const rf_magma_leaf* d_leaves = (const rf_magma_leaf*)scratch;
-    const Seg* d_segs = (const Seg*)(scratch + ((sizeof(rf_magma_leaf) * (size_t)n_leaves + 15) & ~(size_t)15));
+    const rf_magma_leaf* d_leaves = (const rf_magma_leaf*)buf;
+    const Seg* d_segs = (const Seg*)(buf + ((sizeof(rf_magma_leaf) * (size_t)n_leaves + 15) & ~(size_t)15));
     float* d_factor = factor_out ? factor_out : (float*)tail;
     hipLaunchKernelGGL(k_magma_factor, dim3((unsigned)((n_leaves + WG - 1) / WG)), dim3(WG), 0, s, d_leaves,
                        n_leaves, sums, scores, d_factor, p, tau, key0, key1);
@@ -1824,7 +1961,7 @@ rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const do
                            neg_lr);
         e = hipGetLastError();
     }
-    const hipError_t ef = hipFreeAsync(scratch, s);
+    const hipError_t ef = hipFreeAsync(buf, s);
     if (e != hipSuccess) return fail(RF_ERR_HIP, std::string("rf_magma_scale: ") + hipGetErrorString(e));
     if (ef != hipSuccess) return fail(RF_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(ef));
     return RF_OK;
@@ -1880,7 +2017,3 @@ rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t st
 }
 
 }  // namespace
-
-extern "C" {
-
-}  // extern "C"
