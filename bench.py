@@ -13,6 +13,9 @@ drawn before the timed region into a pool of distinct buffers that the steps
 cycle through.
 
 Other workloads (one JSON line each, same fields):
+  llama7b_msr      the default step with moment stochastic rounding
+                   (adamw8(stochastic_rounding=True)): two in-kernel Threefry
+                   draws per element for the requantization of both moments.
   gpt2             GPT-2-small bf16 tree (74 leaves, LayerNorms on f32
                    fallback moments), param stochastic rounding on.
   ragged           2256 leaves, most below min_size (fallback moments),
@@ -162,10 +165,12 @@ def _timed_loop(body, seconds_target):
 
 
 def cpu_baseline(seconds_target=12.0, threads=None, shapes=None, sample_name="the 9 leaves of one Llama-7B layer",
-                 param_sr=False):
+                 param_sr=False, moment_sr=False):
     """The CPU oracle (C, OpenMP over blocks) on a bounded sample of the same
     workload (default: the 9 leaves of one Llama layer), one step per leaf,
-    repeated until about `seconds_target` seconds of CPU work have run."""
+    repeated until about `seconds_target` seconds of CPU work have run.  With
+    stochastic rounding each step also draws its Threefry bits on the CPU
+    (the kernel draws them in-kernel)."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -186,18 +191,23 @@ def cpu_baseline(seconds_target=12.0, threads=None, shapes=None, sample_name="th
             mc=np.full(nb * BS, 127, np.uint8) if quant else np.zeros(n, np.float32),
             ms=np.ones(nb, np.float32) if quant else None,
             vc=np.zeros(nb * BS, np.uint8) if quant else np.zeros(n, np.float32),
-            vs=np.ones(nb, np.float32) if quant else None,
-            bits=orc.random_bits((0, 1), n) if param_sr else None))
+            vs=np.ones(nb, np.float32) if quant else None))
     state = {"step": 0}
 
     def body():
         state["step"] += 1
-        hp = orc.make_hparams(weight_decay=0.01, lr=1e-3, count=state["step"], decay=True, apply=True,
-                              param_sr=param_sr)
+        t = state["step"]
+        hp = orc.make_hparams(weight_decay=0.01, lr=1e-3, count=t, decay=True, apply=True,
+                              param_sr=param_sr, moment_sr=moment_sr)
         done = 0
-        for L in leaves:
+        for i, L in enumerate(leaves):
+            pb = orc.random_bits((t, i), L["n"]) if param_sr else None
+            mb = vb = None
+            if moment_sr and L["quant"]:
+                mb = orc.random_bits((t, 1000 + i), L["mc"].size)
+                vb = orc.random_bits((t, 2000 + i), L["vc"].size)
             orc.adam8_leaf(hp, L["p"], orc.BF16, L["g"], orc.BF16, orc.MOM_QUANT if L["quant"] else orc.MOM_F32,
-                           L["mc"], L["ms"], L["vc"], L["vs"], BS, p_bits=L["bits"])
+                           L["mc"], L["ms"], L["vc"], L["vs"], BS, mu_bits=mb, nu_bits=vb, p_bits=pb)
             done += L["n"]
         return done
 
@@ -267,7 +277,7 @@ class Workload:
 
 
 def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None, clip=None,
-                   guard=False, groups=False, magma=False):
+                   guard=False, groups=False, magma=False, moment_sr=False):
     import numpy as np
     import torch
 
@@ -281,7 +291,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     params = {name: (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 0.02).to(torch.bfloat16)
               for name, s in shapes}
     if adam_mu is None:
-        tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=args.exact)
+        tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=args.exact, stochastic_rounding=moment_sr)
     else:
         tx = rf.adamw(learning_rate=1e-3, weight_decay=0.01, exact=args.exact,
                       mu_dtype=torch.bfloat16 if adam_mu == "bf16" else None, use_magma=magma)
@@ -353,6 +363,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
                     if adam_mu is None else f"{adam_mu} (full-precision AdamW"
                     + (", stochastically rounded storage)" if adam_mu == "bf16" else ")")),
         "param_rounding": "stochastic" if param_sr else "nearest-even",
+        "moment_rounding": "stochastic (in-kernel Threefry bits)" if moment_sr else "nearest",
         "direction": "ieee" if args.exact else "hw rcp/sqrt",
         "mode": "optax update-only (f32 updates)" if optax else "fused step (params written)",
         "launches_per_step": 1 if clip is None else 4,
@@ -373,11 +384,12 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         config["mode"] = "adamw_step (update-only step, then apply_updates with the Magma factor)"
         config["launches_per_step"] = 4
     if shapes_fn is llama7b_shapes:
-        cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr)  # noqa: E731
+        cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr, moment_sr=moment_sr)  # noqa: E731
     else:
         sub = [s for _, s in shapes][:400]
         cpu = lambda: cpu_baseline(args.cpu_seconds, shapes=sub,  # noqa: E731
-                                   sample_name=f"the first {len(sub)} leaves", param_sr=param_sr)
+                                   sample_name=f"the first {len(sub)} leaves", param_sr=param_sr,
+                                   moment_sr=moment_sr)
     metric = METRIC if workload == "llama7b_bf16_adamw8" else f"adam8 params/sec + achieved HBM GB/s, {workload}, 1 GPU"
     if adam_mu is None:
         nbytes = step_bytes(shapes, apply=not optax) + (n_params * 2 if (clip is not None or guard or groups)
@@ -483,6 +495,8 @@ WORKLOADS = {
     "gpt2": lambda a: _tree_workload(a, gpt2_small_shapes, "gpt2_small_bf16_adamw8", param_sr=True),
     "ragged": lambda a: _tree_workload(a, ragged_shapes, "ragged_2256_leaves_bf16_adamw8", param_sr=a.param_sr,
                                        grads="student_t"),
+    "llama7b_msr": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_moment_sr", param_sr=a.param_sr,
+                                            moment_sr=True),
     "llama7b_clip": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_clip_global_norm",
                                              param_sr=False, clip=1.0),
     "llama7b_finetune": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_clip_skip_nonfinite",

@@ -346,6 +346,13 @@ RF_API rf_status rf_codebook(int32_t quantizer, float* out256);
  * (diagnostics of the lookup tables; `out` is host memory). */
 RF_API rf_status rf_host_table_codes(int32_t quantizer, uint32_t first_bits, int64_t count, uint8_t* out);
 
+/* Host-side: the upper candidate ui = clip(searchsorted_left(cb, n), 0, 255),
+ * n clipped to [cb[0], cb[255]] (adam8.py:549-550), that the moment-SR
+ * kernels' table lookup computes for the normalised values whose f32 bit
+ * patterns are first_bits .. first_bits+count-1 (diagnostics of the tables;
+ * `out` is host memory). */
+RF_API rf_status rf_host_search_index(int32_t quantizer, uint32_t first_bits, int64_t count, uint16_t* out);
+
 /* Library version string. */
 RF_API const char* rf_version(void);
 

@@ -308,6 +308,20 @@ ORC_API void orc_nearest_codes_bits(int quantizer, uint32_t first_bits, int64_t 
     }
 }
 
+/* ui = clip(searchsorted_left(cb, clip(n, cb[0], cb[255])), 0, 255)
+ * (adam8.py:549-550), the upper candidate of moment SR, for the normalised
+ * values n given as the consecutive f32 bit patterns first_bits .. +count-1. */
+ORC_API void orc_search_index_bits(int quantizer, uint32_t first_bits, int64_t count, uint16_t* out)
+{
+    float cb[256];
+    orc_codebook(quantizer == ORC_Q_SIGNED, cb);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < count; ++i) {
+        float n = u2f(first_bits + (uint32_t)i);
+        out[i] = (uint16_t)clampi(searchsorted_left(cb, clipf(n, cb[0], cb[255])), 0, 255);
+    }
+}
+
 /* Nearest codes for an arbitrary list of normalised values given as f32
  * bit patterns. */
 ORC_API void orc_nearest_codes_list(int quantizer, const uint32_t* bits, int64_t count, uint8_t* out)

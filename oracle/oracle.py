@@ -75,6 +75,7 @@ def lib() -> ctypes.CDLL:
         _lib.orc_nearest_code.restype = ctypes.c_int
         _lib.orc_nearest_codes_bits.argtypes = [ctypes.c_int, u32, i64, p]
         _lib.orc_nearest_codes_list.argtypes = [ctypes.c_int, p, i64, p]
+        _lib.orc_search_index_bits.argtypes = [ctypes.c_int, u32, i64, p]
         _lib.orc_adam8_leaf.argtypes = [
             ctypes.POINTER(Hparams), ctypes.c_int, p, ctypes.c_int, p, i64,
             ctypes.c_int, p, p, p, p, i64, p, p, p, p,
@@ -177,6 +178,13 @@ def nearest_code(quantizer: int, n: float) -> int:
 def nearest_codes_bits(quantizer: int, first_bits: int, count: int) -> np.ndarray:
     out = np.empty(int(count), dtype=np.uint8)
     lib().orc_nearest_codes_bits(quantizer, int(first_bits), int(count), _ptr(out))
+    return out
+
+
+def search_index_bits(quantizer: int, first_bits: int, count: int) -> np.ndarray:
+    """The reference's ui (adam8.py:549-550) for consecutive f32 patterns."""
+    out = np.empty(int(count), dtype=np.uint16)
+    lib().orc_search_index_bits(quantizer, int(first_bits), int(count), _ptr(out))
     return out
 
 

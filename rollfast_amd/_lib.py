@@ -158,6 +158,7 @@ EXPORTS = (
     "rf_magma_apply_updates",
     "rf_codebook",
     "rf_host_table_codes",
+    "rf_host_search_index",
     "rf_version",
     "rf_last_error",
 )
@@ -200,6 +201,7 @@ def lib() -> ctypes.CDLL:
     L.rf_magma_apply_updates.argtypes = [ctypes.POINTER(ApplyLeaf), i32, _p, f32, i32, u32, u32, _p]
     L.rf_codebook.argtypes = [i32, _p]
     L.rf_host_table_codes.argtypes = [i32, u32, i64, _p]
+    L.rf_host_search_index.argtypes = [i32, u32, i64, _p]
     for name in EXPORTS:
         if name not in ("rf_version", "rf_last_error"):
             getattr(L, name).restype = i32
@@ -260,6 +262,13 @@ def host_table_codes(quantizer: int, first_bits: int, count: int) -> np.ndarray:
     out = np.empty(int(count), dtype=np.uint8)
     check(lib().rf_host_table_codes(quantizer, int(first_bits), int(count), out.ctypes.data_as(_p)),
           "rf_host_table_codes")
+    return out
+
+
+def host_search_index(quantizer: int, first_bits: int, count: int) -> np.ndarray:
+    out = np.empty(int(count), dtype=np.uint16)
+    check(lib().rf_host_search_index(quantizer, int(first_bits), int(count), out.ctypes.data_as(_p)),
+          "rf_host_search_index")
     return out
 
 

@@ -82,12 +82,34 @@ def _pyhost_job():
     return cmd, out
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> str:
+def _sources_of(obj: str) -> list:
+    """The source files an output is built from (headers included)."""
+    inc = [os.path.join(REPO, "include", "rfadam8.h")]
+    dev = [os.path.join(CSRC, "rf_device.h"), os.path.join(CSRC, "rf_tables.h")]
+    if obj.endswith("rf_host.o"):
+        return [HOST_SRC, *dev, *inc]
+    if obj.endswith(".o"):
+        return [INST_SRC, *dev, *inc]
+    return [PYHOST_SRC, *inc, __file__]
+
+
+def _stale(obj: str) -> bool:
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(src) > t for src in _sources_of(obj))
+
+
+def build(verbose: bool = False, jobs: int | None = None, incremental: bool = False) -> str:
     """Compile the HIP library (objects in parallel, then link); returns
-    the path of the built ``.so``."""
+    the path of the built ``.so``.  ``incremental``: recompile only the
+    objects older than their sources."""
     os.makedirs(OBJ_DIR, exist_ok=True)
     max_par = jobs or min(len(VARIANTS) + 1, max(1, os.cpu_count() or 1))
     pending = [_pyhost_job()] + _compile_jobs()
+    if incremental:
+        pending = [(cmd, obj) for cmd, obj in pending
+                   if _stale(pyhost_path() if obj.endswith(".tmp") else obj)]
     running = []
     failures = []
     while pending or running:
@@ -104,7 +126,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
         for obj, out in failures:
             sys.stderr.write(f"--- {obj}\n{out}\n")
         raise RuntimeError(f"compilation failed for {len(failures)} object(s)")
-    os.replace(pyhost_path() + ".tmp", pyhost_path())
+    if os.path.exists(pyhost_path() + ".tmp"):
+        os.replace(pyhost_path() + ".tmp", pyhost_path())
     tmp = LIB_PATH + ".tmp"
     objs = [obj for _, obj in _compile_jobs()]
     link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
@@ -119,4 +142,4 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, incremental="--incremental" in sys.argv))

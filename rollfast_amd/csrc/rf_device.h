@@ -239,7 +239,7 @@ __device__ __forceinline__ void stage_tables(uint8_t* lds, const uint4* __restri
 // Literal restatement of quantize_blocks' element step (adam8.py:167-169,
 // :542-569): n = clip(x / scale, cb[0], cb[255]), searchsorted-left, nearest
 // with ties to the lower index, or Bernoulli SR.  Used for blocks whose scale
-// is outside the fast range and for moment SR.
+// is outside the fast range, and by the generic (partial-block) units.
 __device__ __forceinline__ uint32_t code_literal(const float* cb, float x, float scale, bool sr, uint32_t bits)
 {
     float n = x / scale;      // IEEE division
@@ -292,6 +292,24 @@ __device__ __forceinline__ uint32_t cand_signed(const uint8_t* lds, float n)
 __device__ __forceinline__ uint32_t cand_unsigned(const uint8_t* lds, float n)
 {
     return lds[L_CANDU + __builtin_elementwise_sub_sat(__float_as_uint(n) >> CELL_SHIFT, CELL_LO)];
+}
+
+// Stochastically rounded code of a normalised n (finite, |n| <= 1) from its
+// searchsorted candidate `cand` (the search image's candidate byte of n's
+// cell): _quantize_to_codebook's SR branch (adam8.py:549-564).
+// ui = searchsorted_left(cb, n) = cand + (cb[cand] < n), li = ui - 1 (at
+// least 0), p = (n - cb[li]) / (cb[ui] - cb[li]) in IEEE f32 (0 when the
+// two coincide), upper code iff uniform(bits) < p.  A value below cb[0]
+// counts no entry (ui = li = 0, p = 0), which is the reference's clip.
+__device__ __forceinline__ uint32_t sr_code(const float* cb, uint32_t cand, float n, uint32_t bits)
+{
+    const uint32_t ui = cand + (cb[cand] < n ? 1u : 0u);
+    const uint32_t li = ui > 0u ? ui - 1u : 0u;
+    const float uv = cb[ui], lv = cb[li];
+    const float den = uv - lv;
+    float p = den > 0.0f ? (n - lv) / den : 0.0f;
+    p = p < 0.0f ? 0.0f : (p > 1.0f ? 1.0f : p);
+    return uniform_from_bits(bits) < p ? ui : li;
 }
 
 // Signed dynamic codebook code of x in a block with scale s (fast path;
@@ -620,9 +638,10 @@ __device__ __forceinline__ void load_batch(const UnitCtx& c, const rf_adam8_leaf
 // moments are recomputed from the old codes and scales, which are still in
 // place, with the reference's NaN-propagating absmax (adam8.py:142), then
 // every element is coded and the new scales are written.  Used for blocks of
-// any size, blocks whose scale leaves the fast range (zero-free tiny, Inf,
-// NaN) and moment SR.  B: elements per lane per batch (1 inside the fast
-// kernel, where this path is rare and registers are scarce).
+// any size and blocks whose scale leaves the fast range (zero-free tiny, Inf,
+// NaN), with nearest or stochastic rounding.  B: elements per lane per batch
+// (1 inside the fast kernel, where this path is rare and registers are
+// scarce).
 template <bool MSR, int B = EW_BATCH>
 __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h)
 {
@@ -941,10 +960,10 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     const float sm = scale_from_absmax_bits(am);
     const float sv = scale_from_absmax_bits(av);
     // Non-finite old scales can make m NaN, which fmaxf would drop: those
-    // blocks, tiny or non-finite new scales, and moment SR go the literal way.
+    // blocks and tiny or non-finite new scales go the literal way.
     const bool old_finite = (__float_as_uint(sm_old) & 0x7FFFFFFFu) < 0x7F800000u &&
                             (__float_as_uint(sv_old) & 0x7FFFFFFFu) < 0x7F800000u;
-    if (!MSR && old_finite && block_is_fast(am, sm) && block_is_fast(av, sv)) {
+    if (old_finite && block_is_fast(am, sm) && block_is_fast(av, sv)) {
         const float rsm = 1.0f / sm;
         const float rsv = 1.0f / sv;
         RF_GLOBAL uint8_t* mW = (RF_GLOBAL uint8_t*)L.mu + base;
@@ -952,9 +971,24 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
-            // Three batched phases (normalise + cell, candidate reads,
-            // threshold reads) keep 16 independent LDS reads in flight
+            // Batched phases (normalise + cell, candidate reads, threshold
+            // or codebook reads) keep 16 independent LDS reads in flight
             // instead of 16 dependent read pairs.
+            uint32_t bm[8], bv[8];
+            if constexpr (MSR) {
+                // random bits of the padded [nblocks, bs] moment arrays
+                // (adam8.py:554-564): fed, or jax.random.bits of the leaf keys
+                if (c.fed) {
+                    load8_u32(L.mu_bits, base + eo, bm);
+                    load8_u32(L.nu_bits, base + eo, bv);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        bm[t] = jax_bits(c.kmu0, c.kmu1, (uint64_t)(base + eo + t));
+                        bv[t] = jax_bits(c.knu0, c.knu1, (uint64_t)(base + eo + t));
+                    }
+                }
+            }
             float nm[8], nv[8];
             uint32_t cm[8], cv[8];
 #pragma unroll
@@ -967,16 +1001,28 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                 cm[t] = cand_signed(c.lds, nm[t]);
                 cv[t] = cand_unsigned(c.lds, nv[t]);
             }
-            float tm[8], tv[8];
+            if constexpr (MSR) {
+                // moment SR launches stage the search image: the candidates
+                // are searchsorted counts
+                const float* cbs = (const float*)(c.lds + L_CBS);
+                const float* cbu = (const float*)(c.lds + L_CBU);
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                tm[t] = *(const float*)(c.lds + L_TS + cm[t] * 4u);
-                tv[t] = *(const float*)(c.lds + L_TU + cv[t] * 4u);
-            }
+                for (int t = 0; t < 8; ++t) {
+                    cm[t] = sr_code(cbs, cm[t], nm[t], bm[t]);
+                    cv[t] = sr_code(cbu, cv[t], nv[t], bv[t]);
+                }
+            } else {
+                float tm[8], tv[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                cm[t] += nm[t] >= tm[t] ? 1u : 0u;
-                cv[t] += nv[t] >= tv[t] ? 1u : 0u;
+                for (int t = 0; t < 8; ++t) {
+                    tm[t] = *(const float*)(c.lds + L_TS + cm[t] * 4u);
+                    tv[t] = *(const float*)(c.lds + L_TU + cv[t] * 4u);
+                }
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    cm[t] += nm[t] >= tm[t] ? 1u : 0u;
+                    cv[t] += nv[t] >= tv[t] ? 1u : 0u;
+                }
             }
             uint2 wm, wv;
             wm.x = pack4_u8(cm[0], cm[1], cm[2], cm[3]);

@@ -756,6 +756,35 @@ bool fill_cells(const float* thr, bool negative, uint8_t* cand, std::string& err
     return true;
 }
 
+// Searchsorted candidate of each magnitude cell for one sign: the number of
+// codebook entries below the cell's low end in value space, so that for n in
+// the cell searchsorted_left(cb, n) = cand + (cb[cand] < n).  A cell may hold
+// at most one codebook entry.
+bool fill_search_cells(const float* cb, bool negative, uint8_t* cand, std::string& err)
+{
+    for (uint32_t cell = CELL_LO; cell <= CELL_HI; ++cell) {
+        const float mlo = cell == CELL_LO ? 0.0f : bitsf(cell << CELL_SHIFT);
+        const float mhi = bitsf((cell << CELL_SHIFT) | ((1u << CELL_SHIFT) - 1u));
+        const float lo = negative ? -mhi : mlo;
+        const float hi = negative ? -mlo : mhi;
+        uint32_t below = 0, upto = 0;
+        for (int i = 0; i < 256; ++i) {
+            below += cb[i] < lo ? 1u : 0u;
+            upto += cb[i] <= hi ? 1u : 0u;
+        }
+        if (upto > below + 1u) {
+            err = "search cell " + std::to_string(cell) + " holds more than one codebook entry";
+            return false;
+        }
+        if (below > 255u) {
+            err = "search cell above the codebook";
+            return false;
+        }
+        cand[cell - CELL_LO] = (uint8_t)below;
+    }
+    return true;
+}
+
 HostTables build_tables()
 {
     HostTables ht;
@@ -794,6 +823,48 @@ const HostTables& host_tables()
     return t;
 }
 
+// The image moment-SR launches stage instead: the same layout, with search
+// candidates in the candidate regions (the threshold regions are unused).
+HostTables build_search_tables()
+{
+    HostTables ht = build_tables();
+    if (!ht.error.empty()) return ht;
+    uint8_t* b = ht.bytes.data();
+    const float* cbs = (const float*)(b + L_CBS);
+    const float* cbu = (const float*)(b + L_CBU);
+    std::memset(b + L_TS, 0, 1024);
+    std::memset(b + L_TU, 0, 1024);
+    if (!fill_search_cells(cbs, false, b + L_CANDS, ht.error)) return ht;
+    if (!fill_search_cells(cbs, true, b + L_CANDS + CANDS_SIGN_STRIDE, ht.error)) return ht;
+    if (!fill_search_cells(cbu, false, b + L_CANDU, ht.error)) return ht;
+    return ht;
+}
+
+const HostTables& host_search_tables()
+{
+    static HostTables t = build_search_tables();
+    return t;
+}
+
+// Host emulation of the moment-SR kernels' searchsorted index of a
+// normalised n: the reference's ui = clip(searchsorted_left(cb, n), 0, 255)
+// with n clipped to [cb[0], cb[255]].  The kernels' table path sees only
+// finite n in [-1, 1] (signed) or [0, 1] (unsigned) and needs no clip there,
+// since a value in [-1, cb[0]) counts no entry either; NaN sorts last.
+uint32_t host_search_index(const uint8_t* tb, int32_t quantizer, float n)
+{
+    const bool uns = quantizer == RF_Q_DYNAMIC_UNSIGNED;
+    const float* cb = (const float*)(tb + (uns ? L_CBU : L_CBS));
+    if (n != n) return 255u;
+    n = n < cb[0] ? cb[0] : n;
+    n = n > cb[255] ? cb[255] : n;
+    const uint32_t nb = fbits(n);
+    const uint32_t cell = (nb >> CELL_SHIFT) & 0xFFFFu;
+    const uint32_t idx = cell > CELL_LO ? cell - CELL_LO : 0u;
+    const uint32_t cand = uns ? tb[L_CANDU + idx] : tb[L_CANDS + (nb >> 31) * CANDS_SIGN_STRIDE + idx];
+    return cand + (cb[cand] < n ? 1u : 0u);
+}
+
 // Host emulation of the kernels' table lookup on a normalised n (NaN and the
 // clip to [cb[0], cb[255]] as in the literal path).
 uint32_t host_table_code(const uint8_t* tb, int32_t quantizer, float n)
@@ -823,6 +894,9 @@ uint32_t host_table_code(const uint8_t* tb, int32_t quantizer, float n)
 // ---- device-scope arrays (one copy per GPU, held until the process ends) ----
 // The codebooks and requantization lookup tables every step kernel stages.
 static __device__ __align__(256) uint4 lookup_tables[TABLE_BYTES / 16];
+// The same for moment stochastic rounding: search candidates (searchsorted
+// indices) instead of nearest-code thresholds.
+static __device__ __align__(256) uint4 search_tables[TABLE_BYTES / 16];
 // rf_adam8_step_noalloc's working memory: the leaf and group tables, the work
 // lists and the norm pre-pass's partial sums of one call.  Every call on a
 // GPU shares that GPU's copy and leaves its contents behind; nothing in it
@@ -838,6 +912,7 @@ constexpr int MAX_DEV = 64;
 struct DevState {
     bool ready = false;
     uint4* tables = nullptr;     // this device's lookup_tables
+    uint4* search = nullptr;     // this device's search_tables
     uint8_t* scratch_ptr = nullptr;  // this device's scratch
     int num_cus = 0;
 };
@@ -857,11 +932,16 @@ rf_status device_state(DevState** out)
     if (!d.ready) {
         const HostTables& ht = host_tables();
         if (!ht.error.empty()) return fail(RF_ERR_INVALID, "table construction failed: " + ht.error);
+        const HostTables& hs = host_search_tables();
+        if (!hs.error.empty()) return fail(RF_ERR_INVALID, "search table construction failed: " + hs.error);
         HIP_TRY(hipDeviceGetAttribute(&d.num_cus, hipDeviceAttributeMultiprocessorCount, dev));
         HIP_TRY(hipGetSymbolAddress((void**)&d.tables, HIP_SYMBOL(lookup_tables)));
+        HIP_TRY(hipGetSymbolAddress((void**)&d.search, HIP_SYMBOL(search_tables)));
         HIP_TRY(hipGetSymbolAddress((void**)&d.scratch_ptr, HIP_SYMBOL(scratch)));
-        if (!d.tables || !d.scratch_ptr) return fail(RF_ERR_HIP, "hipGetSymbolAddress returned a null address");
+        if (!d.tables || !d.search || !d.scratch_ptr)
+            return fail(RF_ERR_HIP, "hipGetSymbolAddress returned a null address");
         HIP_TRY(hipMemcpy(d.tables, ht.bytes.data(), TABLE_BYTES, hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpy(d.search, hs.bytes.data(), TABLE_BYTES, hipMemcpyHostToDevice));
         d.ready = true;
     }
     *out = &d;
@@ -1216,6 +1296,18 @@ rf_status rf_host_table_codes(int32_t quantizer, uint32_t first_bits, int64_t co
     return RF_OK;
 }
 
+rf_status rf_host_search_index(int32_t quantizer, uint32_t first_bits, int64_t count, uint16_t* out)
+{
+    if (!out || count < 0) return fail(RF_ERR_INVALID, "bad arguments");
+    if (quantizer != RF_Q_DYNAMIC_SIGNED && quantizer != RF_Q_DYNAMIC_UNSIGNED)
+        return fail(RF_ERR_INVALID, "quantizer must be dynamic signed or unsigned");
+    const HostTables& hs = host_search_tables();
+    if (!hs.error.empty()) return fail(RF_ERR_INVALID, hs.error);
+    for (int64_t i = 0; i < count; ++i)
+        out[i] = (uint16_t)host_search_index(hs.bytes.data(), quantizer, bitsf(first_bits + (uint32_t)i));
+    return RF_OK;
+}
+
 rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply, rf_adam8_plan** out_plan)
 {
     if (!out_plan) return fail(RF_ERR_INVALID, "null plan output");
@@ -1432,7 +1524,7 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
             grid = std::min(wg_needed, rounds * wg_resident);
         }
         hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WG), 0, (hipStream_t)stream, d_leaves,
-                           plan->d_segs + g.seg_offset, g.units, k, ds->tables);
+                           plan->d_segs + g.seg_offset, g.units, k, msr ? ds->search : ds->tables);
         HIP_TRY(hipGetLastError());
     }
     HIP_TRY(hipGetLastError());

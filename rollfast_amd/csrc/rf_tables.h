@@ -20,6 +20,12 @@
 // builder checks this and refuses to produce tables otherwise.  Cells below
 // CELL_LO all map to CELL_LO (no threshold lies below 2^-23 in magnitude).
 //
+// Moment stochastic rounding needs ui = searchsorted_left(cb, n) instead
+// (adam8.py:549-564).  Its launches stage a second image of the same layout
+// whose candidate regions hold, per cell, the number of codebook entries
+// below the cell's low end; a cell holds at most one entry (checked), so
+// ui = cand + (cb[cand] < n).  Its threshold regions are unused.
+//
 // Byte layout (identical in global memory and in LDS).  The two sign halves
 // of the signed candidates sit CANDS_SIGN_STRIDE (a power of two) apart, so
 // a lookup forms its index as ((bits(n) >> 31) << 13) | cell with one

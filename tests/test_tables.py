@@ -73,3 +73,64 @@ def test_table_codes_exhaustive(q, lo, hi):
         bad = np.nonzero(got != want)[0]
         assert bad.size == 0, f"first mismatch at 0x{start + int(bad[0]):08x}"
         start += count
+
+
+
+def _search_want(cb: np.ndarray, first: int, count: int) -> np.ndarray:
+    """numpy's searchsorted (side left) of n clipped to [cb[0], cb[255]] for
+    the f32 patterns first .. first+count-1: the reference's ui
+    (adam8.py:549-550) for finite n."""
+    n = np.arange(first, first + count, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    return np.searchsorted(cb, np.clip(n, cb[0], cb[255]), side="left").astype(np.uint16)
+
+
+@pytest.mark.parametrize("q,signed", [(orc.Q_SIGNED, True), (orc.Q_UNSIGNED, False)])
+def test_search_index_windows(q, signed):
+    """The moment-SR lookup's searchsorted index, and the oracle's, around
+    every codebook entry (where the count steps) and in random windows,
+    against numpy's searchsorted on the oracle's codebook."""
+    cb = orc.codebook(signed)
+    rng = np.random.default_rng(12)
+    spans = _windows(cb, 4096, rng, 64, 0)
+    if signed:
+        spans += _windows(cb, 4096, rng, 64, 0x80000000)
+    for first, count in spans:
+        want = _search_want(cb, first, count)
+        for got in (_lib.host_search_index(q, first, count), orc.search_index_bits(q, first, count)):
+            bad = np.nonzero(got != want)[0]
+            assert bad.size == 0, f"q={q} first=0x{first + int(bad[0]):08x} got {got[bad[0]]} want {want[bad[0]]}"
+
+
+def test_search_index_special_values():
+    """+-0, denormals, +-1 and beyond (clipped), +-Inf; NaN sorts last and
+    clips to 255."""
+    pats = np.array([0x00000000, 0x80000000, 0x00000001, 0x807FFFFF, 0x3F800000, 0xBF800000,
+                     0x3F800001, 0x40000000, 0xC0000000, 0x7F800000, 0xFF800000, 0x7FC00000], np.uint32)
+    for q in (orc.Q_SIGNED, orc.Q_UNSIGNED):
+        got = np.array([_lib.host_search_index(q, int(b), 1)[0] for b in pats])
+        want = np.array([orc.search_index_bits(q, int(b), 1)[0] for b in pats])
+        np.testing.assert_array_equal(got, want)
+    cb = orc.codebook(True)
+    assert orc.search_index_bits(orc.Q_SIGNED, 0x00000000, 1)[0] == 127   # cb[127] = 0 >= +0
+    assert orc.search_index_bits(orc.Q_SIGNED, 0x80000000, 1)[0] == 127   # -0 == +0
+    assert orc.search_index_bits(orc.Q_SIGNED, 0x00000001, 1)[0] == 128   # 0 < denormal <= cb[128]
+    assert orc.search_index_bits(orc.Q_SIGNED, 0xBF800000, 1)[0] == 0     # -1 clips to cb[0]
+    assert orc.search_index_bits(orc.Q_SIGNED, 0x7FC00000, 1)[0] == 255   # NaN
+    assert cb[127] == 0.0
+
+
+@pytest.mark.parametrize("q,lo,hi", [(orc.Q_UNSIGNED, 0x00000000, 0x3F800000),
+                                     (orc.Q_SIGNED, 0x00000000, 0x3F800000),
+                                     (orc.Q_SIGNED, 0x80000000, 0xBF800000)])
+def test_search_index_exhaustive(q, lo, hi):
+    """Every f32 pattern of [-1, 1] (the moment-SR kernels' range of n)
+    against the oracle's searchsorted."""
+    chunk = 1 << 26
+    start = lo
+    while start <= hi:
+        count = min(chunk, hi - start + 1)
+        got = _lib.host_search_index(q, start, count)
+        want = orc.search_index_bits(q, start, count)
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, f"first mismatch at 0x{start + int(bad[0]):08x}: got {got[bad[0]]} want {want[bad[0]]}"
+        start += count
