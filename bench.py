@@ -407,14 +407,23 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     return Workload(workload, n_params, "params/s", nbytes, step, config, cpu, metric)
 
 
-def _c5_input(n):
+def _c5_input(n, seed=5):
+    """|x| log-uniform in [1e-8, 1e2] with a random sign, plus zeros (half of
+    them -0) at every 97th element and f32 denormals with random mantissa and
+    sign at every 89th from element 1."""
     import torch
 
     gen = torch.Generator(device="cuda")
-    gen.manual_seed(5)
+    gen.manual_seed(seed)
     x = torch.empty(n, device="cuda").uniform_(math.log(1e-8), math.log(1e2), generator=gen).exp_()
     sign = torch.rand(n, device="cuda", generator=gen) < 0.5
     x[sign] *= -1.0
+    d = x[1::89]
+    mant = torch.randint(1, 1 << 23, (d.numel(),), device="cuda", generator=gen, dtype=torch.int32)
+    den = mant.view(torch.float32)
+    d.copy_(torch.where(torch.rand(d.numel(), device="cuda", generator=gen) < 0.5, -den, den))
+    z = x[::97]  # after the denormals: where the two strides meet, a zero
+    z.copy_(torch.where(torch.arange(z.numel(), device="cuda") % 2 == 1, -0.0, 0.0))
     return x
 
 
@@ -485,7 +494,8 @@ def _kernel_workload(args, kind):
     name = f"{kind}_2p30_f32"
     return Workload(name, n, "elements/s", nbytes, step,
                     {"workload": name, "elements": n, "block_size": BS, "quantizer": "dynamic_signed",
-                     "input": "log-uniform |x| in [1e-8, 1e2], random sign", "launches_per_step": 1},
+                     "input": "log-uniform |x| in [1e-8, 1e2], random sign, +-0 every 97th and denormals "
+                              "every 89th element", "launches_per_step": 1},
                     lambda: cpu_baseline_kernel(kind, args.cpu_seconds),
                     f"{kind} elements/sec + achieved HBM GB/s, 2^30 f32, 1 GPU")
 

@@ -72,6 +72,13 @@ typedef int32_t rf_status;
 
 /* rf_adam8_leaf.flags */
 #define RF_LEAF_DECAY 1u    /* add_decayed_weights applies to this leaf (mask True) */
+#define RF_LEAF_ZERO_DECAY 4u /* optim/adam.py's own decay term with weight 0 (adamw's
+                               scale_by_adam gets weight_decay=0.0 and the params,
+                               adam.py:185-201, :380-404): the update first becomes
+                               u + 0*p in f32 -- NaN for a non-finite param, +0 for a
+                               -0 update -- before the RF_LEAF_DECAY term.  Needs the
+                               param; unquantized moments only (scale_by_adam8 has no
+                               such term) */
 #define RF_LEAF_STORE_SR 2u /* bf16 fallback moments are stored with stochastic rounding:
                                bits of split(key_mu | key_nu)[state_index], or mu_bits /
                                nu_bits with RF_FED_BITS (optim/adam.py:219-222 with

@@ -348,6 +348,8 @@ enum {
     ORC_APPLY = 64,         /* write params (fused step) instead of updates */
     ORC_STORE_SR = 512,     /* bf16 fallback moments stored with SR from mu_bits / nu_bits
                                (optim/adam.py:219-222, utils.py:374-409) */
+    ORC_ZERO_DECAY = 1024,  /* optim/adam.py's own decay term with weight 0 before the
+                               optax decay (adam.py:185-201 inside adamw, :380-404) */
 };
 
 /* one_minus_b1 weights the gradient in the first-moment EMA; the Nesterov
@@ -391,6 +393,11 @@ static inline float direction_and_apply(const orc_hparams* hp, int pdtype, void*
     float den = sqrtf(vhat + hp->eps_root) + hp->eps;
     float u = mhat / den;
     float p = load_val(pdtype, param, e);
+    if (hp->flags & ORC_ZERO_DECAY) {
+        /* utils.py:79-90 with weight_decay_step = 0.0: update + 0.0 * f32(param) */
+        float zp = 0.0f * p;
+        u = u + zp;
+    }
     if (hp->flags & ORC_DECAY) {
         float wdp;
         if (pdtype == ORC_BF16 && (hp->flags & ORC_DECAY_WEAK)) {

@@ -27,6 +27,7 @@ Q_SIGNED, Q_UNSIGNED, Q_SYMMETRIC = 0, 1, 2
 F32, BF16 = 0, 1
 MOM_QUANT, MOM_F32, MOM_BF16 = 0, 1, 2
 NESTEROV, DECAY, DECAY_WEAK, LR, MOMENT_SR, PARAM_SR, APPLY, STORE_SR = 1, 2, 4, 8, 16, 32, 64, 512
+ZERO_DECAY = 1024
 
 
 class Hparams(ctypes.Structure):
@@ -248,14 +249,17 @@ def sr_bf16(x: np.ndarray, bits: np.ndarray) -> np.ndarray:
 # -------------------------------------------------------------- the step --
 def make_hparams(*, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0, weight_decay=0.0, lr=None,
                  count=1, nesterov=False, decay=False, decay_weak=True, moment_sr=False,
-                 param_sr=False, apply=False, ema_weight_f32=False, store_sr=False) -> Hparams:
+                 param_sr=False, apply=False, ema_weight_f32=False, store_sr=False,
+                 zero_decay=False) -> Hparams:
     """Scalars exactly as the reference derives them from Python floats:
     ``1.0 - b1`` in double then f32 (adam8.py:323), ``1 - b1**t`` in f32
     (adam8.py:338-339, f32 pow: parity unpinned).  ``ema_weight_f32``: the
     first-moment EMA weight is ``1 - f32(b1)`` computed in f32, as
     optim/adam.py does (utils.py:327-335); the Nesterov weight stays the
     double ``1.0 - b1`` (adam.py:146-160).  ``store_sr``: bf16 fallback
-    moments are stored with stochastic rounding (adam.py:219-222)."""
+    moments are stored with stochastic rounding (adam.py:219-222).
+    ``zero_decay``: optim/adam.py's own weight-0 decay term ``u + 0*p``
+    before the optax decay (adam.py:185-201 inside adamw)."""
     f32 = np.float32
     t = f32(count)
     hp = Hparams()
@@ -288,6 +292,8 @@ def make_hparams(*, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0, weight_decay=0.0, 
         flags |= APPLY
     if store_sr:
         flags |= STORE_SR
+    if zero_decay:
+        flags |= ZERO_DECAY
     hp.flags = flags
     return hp
 

@@ -29,6 +29,7 @@ RF_FED_BITS = 256
 RF_SKIP_NONFINITE = 512
 RF_LEAF_DECAY = 1
 RF_LEAF_STORE_SR = 2
+RF_LEAF_ZERO_DECAY = 4
 RF_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 _p = ctypes.c_void_p

@@ -380,9 +380,14 @@ __device__ __forceinline__ float adam_direction(const KHp& h, float m, float v, 
 
 enum : int32_t { WD_OFF = 0, WD_F32 = 1, WD_BF16 = 2 };
 
-// optax add_decayed_weights (u + wd*p) then scale_by_learning_rate ((-lr)*u).
-__device__ __forceinline__ float decay_and_scale(const KHp& h, float u, float p, int32_t wd_mode)
+// optax add_decayed_weights (u + wd*p) then scale_by_learning_rate ((-lr)*u);
+// `zero`: optim/adam.py's own weight-0 term u + 0*p first (RF_LEAF_ZERO_DECAY).
+__device__ __forceinline__ float decay_and_scale(const KHp& h, float u, float p, int32_t wd_mode, bool zero = false)
 {
+    if (zero) {
+        const float zp = 0.0f * p;  // NaN for a non-finite p, signed zero otherwise
+        u = u + zp;
+    }
     if (wd_mode == WD_BF16) {
         u = u + round_to_bf16(h.wd16 * p);  // bf16*bf16 is exact in f32: one rounding
     } else if (wd_mode == WD_F32) {
@@ -492,6 +497,7 @@ struct UnitCtx {
     float* wtab;  // this wave's 512-float LDS region (dequant-and-decay tables)
     int32_t wd_mode;
     bool fed;
+    bool zero;        // RF_LEAF_ZERO_DECAY of the current leaf (unquantized-moment units)
     bool clip;        // grads are scaled by the global-norm clipping factor
     float cs, cs16;   // that factor as f32 and rounded to bf16
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;  // per-leaf keys
@@ -591,9 +597,10 @@ __device__ __forceinline__ void update_one(const UnitCtx& c, const rf_adam8_leaf
                                            float mm, float vv, float g, float p)
 {
     float u = adam_direction<NEST, EXACT>(h, mm, vv, g);
-    u = decay_and_scale(h, u, p, c.wd_mode);
+    u = decay_and_scale(h, u, p, c.wd_mode, c.zero);
     if constexpr (APPLY && !EXACT) {
-        if (cancels(p + u, u)) u = decay_and_scale(h, adam_direction<NEST, true>(h, mm, vv, g), p, c.wd_mode);
+        if (cancels(p + u, u))
+            u = decay_and_scale(h, adam_direction<NEST, true>(h, mm, vv, g), p, c.wd_mode, c.zero);
     }
     if constexpr (APPLY) {
         if (L.param_dtype == RF_BF16) {
@@ -1108,7 +1115,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
     const int64_t end = min(base + CHUNK, L.size);
     const int32_t mdt = L.moment_kind == RF_MOMENT_BF16 ? RF_BF16 : RF_F32;
     const bool store_sr = mdt == RF_BF16 && (L.flags & RF_LEAF_STORE_SR);
-    const bool need_p = APPLY || c.wd_mode != WD_OFF;
+    const bool need_p = APPLY || c.wd_mode != WD_OFF || c.zero;
     const bool msum = !APPLY && c.mpart != nullptr;  // Magma sums: update-only launches
     MagmaAcc acc;
     for (int64_t e0 = base + lane; e0 < end; e0 += EW_BATCH * WAVE) {
@@ -1161,7 +1168,7 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t base = chunk * CHUNK;
     const int32_t wdm = c.wd_mode;
-    const bool need_p = APPLY || wdm != WD_OFF;
+    const bool need_p = APPLY || wdm != WD_OFF || c.zero;
     const bool store_sr = BF16M && (L.flags & RF_LEAF_STORE_SR);
     const bool msum = !APPLY && c.mpart != nullptr;  // Magma sums: update-only launches
     MagmaAcc acc;
@@ -1202,7 +1209,7 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
             if (msum) acc.add(g[t], mm);
             m[t] = mm;
             v[t] = vv;
-            u[t] = decay_and_scale(h, adam_direction<NEST, EXACT>(h, mm, vv, g[t]), p[t], wdm);
+            u[t] = decay_and_scale(h, adam_direction<NEST, EXACT>(h, mm, vv, g[t]), p[t], wdm, c.zero);
         }
         if constexpr (APPLY) {
             float sum[8];
@@ -1214,7 +1221,7 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
                     for (int t = 0; t < 8; ++t) {
                         if (cancels(sum[t], u[t]))
                             sum[t] = p[t] + decay_and_scale(h, adam_direction<NEST, true>(h, m[t], v[t], g[t]), p[t],
-                                                            wdm);
+                                                            wdm, c.zero);
                     }
                 }
             }
@@ -1313,6 +1320,7 @@ __device__ __forceinline__ void leaf_context(UnitCtx& c, const rf_adam8_leaf& L,
 {
     const bool decay = (L.flags & RF_LEAF_DECAY) != 0;
     c.wd_mode = !decay ? WD_OFF : ((L.param_dtype == RF_BF16 && (h.flags & RF_DECAY_WEAK)) ? WD_BF16 : WD_F32);
+    c.zero = (L.flags & RF_LEAF_ZERO_DECAY) != 0;
     if (msr || (L.flags & RF_LEAF_STORE_SR)) {
         jax_split(h.kmu0, h.kmu1, (uint32_t)L.state_index, c.kmu0, c.kmu1);
         jax_split(h.knu0, h.knu1, (uint32_t)L.state_index, c.knu0, c.knu1);
@@ -1377,6 +1385,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     c.lds = lds;
     c.wtab = wtab[wave_in_wg];
     c.fed = (h.flags & RF_FED_BITS) != 0;
+    c.zero = false;  // quantized blocks only: RF_LEAF_ZERO_DECAY is refused for them
     c.mpart = nullptr;
     c.mbase = 0;
     if (gate_rejects(h)) {
@@ -1437,6 +1446,7 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
     c.lds = lds;
     c.wtab = nullptr;
     c.fed = (h.flags & RF_FED_BITS) != 0;
+    c.zero = false;
     c.mpart = h.mpart;
     c.mbase = 0;
     if (gate_rejects(h)) {

@@ -1090,7 +1090,10 @@ rf_status validate_leaf(const rf_adam8_leaf& L, int32_t i, int32_t apply)
     if (L.grad_dtype != RF_F32 && L.grad_dtype != RF_BF16) return fail(RF_ERR_UNSUPPORTED, at + "grad dtype must be f32 or bf16");
     if (L.moment_kind < RF_MOMENT_QUANTIZED || L.moment_kind > RF_MOMENT_BF16) return fail(RF_ERR_INVALID, at + "bad moment kind");
     if (L.size > 0 && !L.grad) return fail(RF_ERR_INVALID, at + "null grad");
-    if (L.size > 0 && !L.param && (apply || (L.flags & RF_LEAF_DECAY))) return fail(RF_ERR_INVALID, at + "null param");
+    if (L.size > 0 && !L.param && (apply || (L.flags & (RF_LEAF_DECAY | RF_LEAF_ZERO_DECAY))))
+        return fail(RF_ERR_INVALID, at + "null param");
+    if ((L.flags & RF_LEAF_ZERO_DECAY) && L.moment_kind == RF_MOMENT_QUANTIZED)
+        return fail(RF_ERR_UNSUPPORTED, at + "RF_LEAF_ZERO_DECAY with quantized moments (scale_by_adam8 has no such term)");
     if (L.size > 0 && !apply && !L.updates) return fail(RF_ERR_INVALID, at + "null updates in update-only mode");
     // An empty unquantized-moment leaf has no work units (its buffers are
     // never read); a quantized one may still own a padded block.

@@ -72,6 +72,9 @@ class _AdamEngine(_Engine):
     """The adam8 engine with optim/adam.py's scalars, keys and state."""
 
     store_sr = False  # set per instance for mu_dtype=bfloat16
+    # scale_by_adam's own decay, update + wd * param, applies whenever params
+    # are given, with weight 0 inside adamw (adam.py:185-201, :380-404)
+    own_zero_decay = True
 
     @staticmethod
     def ema_weight(b1) -> np.float32:
@@ -267,15 +270,17 @@ def _canonical_mu_dtype(mu_dtype):
 
 
 def _adam_decay(weight_decay, weight_decay_mask, updates, state, params):
-    """scale_by_adam's own decoupled decay (adam.py:189-202): (leaf mask,
-    f32 decay) or (None, None) when it does not apply."""
+    """scale_by_adam's own decoupled decay (adam.py:185-202): (leaf mask,
+    f32 decay) whenever params are given -- a zero weight included, since
+    the reference adds ``0 * param`` too (NaN for a non-finite param) -- or
+    (None, None) without params."""
     decays = _has_nonzero_or_scheduled(weight_decay)
     if decays and params is None:
         raise ValueError(
             "`params` must be provided to `scale_by_adam.update` when "
             "`weight_decay` is nonzero or scheduled."
         )
-    if params is None or not decays:
+    if params is None:
         return None, None
     n = len(_tree.leaves(updates, is_leaf=_is_passthrough_leaf))
     decay_mask = _decay_mask_leaves(weight_decay_mask, params, n)

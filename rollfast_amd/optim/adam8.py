@@ -499,6 +499,10 @@ class _Engine:
     rewritten: the per-leaf validation of the first call is not repeated.
     """
 
+    # optim/adam.py's scale_by_adam adds its own decay term (weight 0 inside
+    # adamw) whenever it is given params; scale_by_adam8 has none
+    own_zero_decay = False
+
     def __init__(self, cfg: _Config):
         self.cfg = cfg
         self._plans: dict = {}
@@ -526,7 +530,11 @@ class _Engine:
     store_sr = False
 
     # -- full table build (first call, or anything changed) -----------------
-    def _build_rows(self, g_leaves, mu_leaves, nu_leaves, p_leaves, *, apply, decay_mask, random_bits):
+    def _build_rows(self, g_leaves, mu_leaves, nu_leaves, p_leaves, *, apply, decay_mask, random_bits,
+                    zero_decay=False):
+        """Leaf table rows of one launch.  ``zero_decay``: every row also gets
+        optim/adam.py's weight-0 decay term (``RF_LEAF_ZERO_DECAY``), so every
+        row needs its param."""
         torch = _torch()
         n = len(g_leaves)
         out_leaves: list = [None] * n
@@ -559,9 +567,10 @@ class _Engine:
             row.param_index = i
             decays = bool(decay_mask[i]) if decay_mask is not None else False
             p = p_leaves[i] if p_leaves is not None else None
-            if (apply or decays) and (p is None or _is_passthrough_leaf(p)):
+            needs_p = apply or decays or zero_decay
+            if needs_p and (p is None or _is_passthrough_leaf(p)):
                 raise ValueError(NO_PARAMS_MSG)
-            if apply or decays:
+            if needs_p:
                 _require_device_tensor(p, "param")
                 if p.device != device:
                     raise ValueError("all leaves must live on the same device")
@@ -574,7 +583,7 @@ class _Engine:
             else:
                 p = None
                 row.param_dtype = _lib.RF_F32
-            row.flags = _lib.RF_LEAF_DECAY if decays else 0
+            row.flags = (_lib.RF_LEAF_DECAY if decays else 0) | (_lib.RF_LEAF_ZERO_DECAY if zero_decay else 0)
             if isinstance(m, QuantizedBlocks):
                 if not isinstance(v, QuantizedBlocks):
                     raise ValueError("first and second moment leaves differ in kind")
@@ -754,10 +763,13 @@ class _Engine:
         finite_out=None,
         finite_host=None,
         magma_sums=None,
+        zero_decay: bool = False,
     ):
         torch = _torch()
         cfg = self.cfg
         key_mu, key_nu, next_key = self.split_keys(state.key)
+        mask_key = (decay_mask if decay_mask is None or decay_mask is ALL_LEAVES else tuple(decay_mask),
+                    bool(zero_decay))
         count_inc = safe_int32_increment(int(np.asarray(state.count)))
 
         # Steady state of the fused step (same tree, params and moment objects
@@ -765,8 +777,7 @@ class _Engine:
         # and rewrites the grad pointers of the cached table.
         last = self._last
         if (last is not None and random_bits is None and last["apply"] == apply and last["n"]
-                and last["mask"] == (decay_mask if decay_mask is None or decay_mask is ALL_LEAVES
-                                     else tuple(decay_mask))):
+                and last["mask"] == mask_key):
             host = _lib.pyhost()
             lists = host.gather(updates, state.mu, state.nu, params)
             addr = ctypes.addressof(last["table"])
@@ -790,7 +801,6 @@ class _Engine:
         if params is not None:
             p_leaves = _tree.flatten_up_to(g_td, params)
 
-        mask_key = decay_mask if decay_mask is None or decay_mask is ALL_LEAVES else tuple(decay_mask)
         last = self._last
         out_leaves = None
         if (last is not None and random_bits is None and last["apply"] == apply and last["mask"] == mask_key
@@ -804,7 +814,7 @@ class _Engine:
                 raise ValueError("updates and optimizer state have different tree structures")
             rows, structure, refs, out_leaves, device = self._build_rows(
                 g_leaves, mu_leaves, nu_leaves, p_leaves, apply=apply, decay_mask=decay_mask,
-                random_bits=random_bits)
+                random_bits=random_bits, zero_decay=zero_decay)
             n_rows = len(rows)
             table = (_lib.Adam8Leaf * n_rows)(*rows) if rows else None
             plan = None
@@ -999,6 +1009,7 @@ class _Adamw8Update:
             param_key=param_key, param_sr=param_sr, random_bits=random_bits,
             clip_global_norm=clip_global_norm, clip_stats=clip_stats, skip_nonfinite=skip_nonfinite,
             finite_out=finite_out, finite_host=finite_host,
+            zero_decay=self.engine.own_zero_decay and params is not None,
         )
         new_state = (new_adam,) + tuple(state[1:-1]) + (new_lr_state,)
         return out, new_state
@@ -1266,8 +1277,9 @@ class _GroupedRunner:
                 decay_mask = _decay_mask_leaves(upd.weight_decay_mask, _tree.unflatten(g_td, pm), n)
             mu_leaves = _tree.flatten_up_to(g_td, adam_state.mu) if n else []
             nu_leaves = _tree.flatten_up_to(g_td, adam_state.nu) if n else []
-            grows, gstruct, grefs, gouts, gdev = eng._build_rows(gm, mu_leaves, nu_leaves, pm, apply=apply,
-                                                                 decay_mask=decay_mask, random_bits=random_bits)
+            grows, gstruct, grefs, gouts, gdev = eng._build_rows(
+                gm, mu_leaves, nu_leaves, pm, apply=apply, decay_mask=decay_mask, random_bits=random_bits,
+                zero_decay=eng.own_zero_decay and params is not None)
             if gdev is not None:
                 if device is not None and gdev != device:
                     raise ValueError("all leaves must live on the same device")

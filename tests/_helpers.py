@@ -73,6 +73,27 @@ def f32_within_bf16_ulp(a: np.ndarray, b: np.ndarray, before: np.ndarray | None 
     return np.abs(a - b) <= ulp
 
 
+def f32_ulp(x: np.ndarray) -> np.ndarray:
+    """Spacing of f32 values at |x| (2^-149 in the subnormal range)."""
+    x = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.where(x > 0, x, 1.0)))
+    return np.exp2(np.maximum(e, -126.0) - 23.0)
+
+
+def f32_params_close(got: np.ndarray, want: np.ndarray, before: np.ndarray, steps: int = 1) -> np.ndarray:
+    """f32 params of the default (hardware rcp/sqrt) direction: the update
+    u = want - before carries a few f32 ulps of error and the fused add
+    rounds once more, so |got - want| <= 8 ulp(|want - before|) + ulp(want)
+    per step (where p + u nearly cancels the kernel recomputes in IEEE
+    arithmetic, which is exact).  ``steps``: device params that followed
+    their own trajectory for that many steps of similar updates."""
+    g = got.astype(np.float64)
+    w = want.astype(np.float64)
+    b = before.astype(np.float64)
+    bound = 8.0 * f32_ulp(w - b) + f32_ulp(np.maximum(np.abs(w), np.abs(g)))
+    return np.abs(g - w) <= steps * bound
+
+
 def gaussian(rng: np.random.Generator, shape, std: float) -> np.ndarray:
     return (rng.standard_normal(size=shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
 
@@ -89,14 +110,15 @@ class OracleTree:
     def step(self, grads, *, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0, weight_decay=0.0, lr=1e-3,
              count=1, decay_mask=None, nesterov=False, moment_sr=False, param_sr=False, apply=True,
              mu_bits=None, nu_bits=None, p_bits=None, lr_scale=True, decay_weak=True, ema_weight_f32=False,
-             store_sr=False):
+             store_sr=False, zero_decay=False):
         outs = []
         for i, L in enumerate(self.leaves):
             decays = weight_decay != 0.0 and (decay_mask is None or decay_mask[i])
             hp = orc.make_hparams(b1=b1, b2=b2, eps=eps, eps_root=eps_root, weight_decay=weight_decay,
                                   lr=lr if lr_scale else None, count=count, nesterov=nesterov, decay=decays,
                                   decay_weak=decay_weak, moment_sr=moment_sr, param_sr=param_sr, apply=apply,
-                                  ema_weight_f32=ema_weight_f32, store_sr=store_sr and L["kind"] == "bf16")
+                                  ema_weight_f32=ema_weight_f32, store_sr=store_sr and L["kind"] == "bf16",
+                                  zero_decay=zero_decay)
             pd = orc.BF16 if L["pdtype"] == "bf16" else orc.F32
             gd = orc.BF16 if L["gdtype"] == "bf16" else orc.F32
             mk = {"quant": orc.MOM_QUANT, "f32": orc.MOM_F32, "bf16": orc.MOM_BF16}[L["kind"]]

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as orc
-from tests._helpers import f32_within_bf16_ulp, to_device, to_host
+from tests._helpers import f32_params_close, to_device, to_host
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 BS = 2048
@@ -102,7 +102,7 @@ def test_gpu_step_f32_matches_golden(exact):
             np.testing.assert_array_equal(got_p.view(np.uint32), z[f"p{t}"].view(np.uint32))
         else:
             before = z[f"p{t - 1}"] if t > 1 else z["p0"]
-            assert np.all(f32_within_bf16_ulp(got_p, z[f"p{t}"], before))
+            assert np.all(f32_params_close(got_p, z[f"p{t}"], before, steps=t))
         adam = state[0]
         np.testing.assert_array_equal(to_host(adam.mu["w"].values), z[f"mu{t}"])
         np.testing.assert_array_equal(to_host(adam.nu["w"].values), z[f"nu{t}"])

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as orc
-from tests._helpers import OracleTree, bf16_bits, bf16_ulp_distance, f32_within_bf16_ulp, gaussian, to_device, to_host
+from tests._helpers import OracleTree, bf16_bits, bf16_ulp_distance, f32_params_close, gaussian, to_device, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -65,7 +65,7 @@ def _store_bits(state_key, n_leaves, sizes):
             [orc.random_bits(tuple(s2[i]), sizes[i]) for i in range(n_leaves)])
 
 
-def _compare(spec, tree, params, adam_state, exact, what):
+def _compare(spec, tree, params, adam_state, exact, what, before=None):
     import torch
 
     for i, (shape, pd, _gd) in enumerate(spec):
@@ -90,7 +90,7 @@ def _compare(spec, tree, params, adam_state, exact, what):
         elif pd == "bf16":
             assert bf16_ulp_distance(got, want).max() <= 1, f"{what} leaf {i}"
         else:
-            assert f32_within_bf16_ulp(got, want).all(), f"{what} leaf {i}"
+            assert f32_params_close(got, want, before[i]).all(), f"{what} leaf {i}"
 
 
 def _run_adamw(*, mu_dtype, exact, nesterov=False, psr=False, fed=False, steps=3, wd=0.01):
@@ -115,8 +115,9 @@ def _run_adamw(*, mu_dtype, exact, nesterov=False, psr=False, fed=False, steps=3
         if psr:
             kp = orc.split(tuple(int(k) for k in pkey), len(SPEC))
             pb = [orc.random_bits(tuple(kp[i]), sizes[i]) for i in range(len(SPEC))]
+        before = [L["param"].copy() for L in tree.leaves]
         tree.step(ghost, weight_decay=wd, lr=1e-3, count=step + 1, nesterov=nesterov, param_sr=psr, mu_bits=mb,
-                  nu_bits=vb, p_bits=pb, ema_weight_f32=True, store_sr=store)
+                  nu_bits=vb, p_bits=pb, ema_weight_f32=True, store_sr=store, zero_decay=True)
         bits = None
         if fed:
             bits = {}
@@ -127,7 +128,7 @@ def _run_adamw(*, mu_dtype, exact, nesterov=False, psr=False, fed=False, steps=3
         params, state = rf.adamw_step(tx, params, gdev, state, key=pkey if psr else None, stochastic=psr,
                                       random_bits=bits)
         torch.cuda.synchronize()
-        _compare(SPEC, tree, params, state[0], exact, f"step {step + 1}")
+        _compare(SPEC, tree, params, state[0], exact, f"step {step + 1}", before)
     return state
 
 
@@ -211,3 +212,59 @@ def test_adamw_fused_equals_update_plus_apply():
             np.testing.assert_array_equal(to_host(pa[k]), to_host(pb[k]))
             np.testing.assert_array_equal(to_host(sa[0].mu[k]), to_host(sb[0].mu[k]))
             np.testing.assert_array_equal(to_host(sa[0].nu[k]), to_host(sb[0].nu[k]))
+
+
+def _nan_equal(got, want, what):
+    """Equal values, NaN where the oracle has NaN (payload bits aside)."""
+    gn, wn = np.isnan(got), np.isnan(want)
+    np.testing.assert_array_equal(gn, wn, err_msg=f"{what}: NaN positions")
+    np.testing.assert_array_equal(got[~gn].view(np.uint32), want[~wn].view(np.uint32), err_msg=what)
+
+
+def test_zero_weight_decay_terms_propagate_nonfinite_params():
+    """optim/adam.py's scale_by_adam adds ``update + wd_step * param`` on every
+    leaf its mask covers whenever it is given params, with wd_step = 0.0
+    inside adamw (adam.py:185-201, :380-404); 0 * Inf and 0 * NaN are NaN.
+    So a non-finite param on a leaf outside adamw's add_decayed_weights mask
+    gets a NaN update, and so does every leaf of scale_by_adam(weight_decay=0)
+    given params; finite params keep their updates (exact mode, against the
+    oracle's weight-0 term)."""
+    import torch
+
+    import rollfast_amd as rf
+
+    spec = [((2, 2048), "f32", "f32"), ((1000,), "f32", "f32"), ((3, 2048), "bf16", "bf16")]
+    host, params = _build(spec, 9)
+    host["l1"][[3, 10, 77]] = [np.inf, -np.inf, np.nan]
+    host["l2"][[5]] = bf16_bits(np.float32([np.inf]))
+    params["l1"].copy_(to_device(host["l1"], "f32"))
+    params["l2"].copy_(to_device(host["l2"], "bf16").reshape(3, 2048))
+    mask = {"l0": True, "l1": False, "l2": False}
+    ghost, gdev = _grads(spec, 17)
+    # adamw update-only: the weight-0 term on every leaf, the optax decay on l0
+    tx = rf.adamw(learning_rate=1e-3, weight_decay=0.01, weight_decay_mask=mask, exact=True)
+    state = tx.init(params)
+    tree = _oracle_tree(spec, params, state[0])
+    outs = tree.step(ghost, weight_decay=0.01, decay_mask=[True, False, False], lr=1e-3, count=1, apply=False,
+                     ema_weight_f32=True, zero_decay=True)
+    updates, _ = tx.update(gdev, state, params)
+    torch.cuda.synchronize()
+    for i in range(3):
+        _nan_equal(to_host(updates[f"l{i}"]), outs[i], f"adamw leaf {i}")
+    assert np.isnan(to_host(updates["l1"])[[3, 10, 77]]).all() and np.isnan(to_host(updates["l2"])[5])
+    assert np.isfinite(to_host(updates["l0"])).all()
+    # scale_by_adam(weight_decay=0) given params: the f32 weight-0 term on every leaf
+    tx = rf.scale_by_adam(weight_decay=0.0, exact=True)
+    state = tx.init(params)
+    tree = _oracle_tree(spec, params, state)
+    outs = tree.step(ghost, count=1, apply=False, lr_scale=False, decay_weak=False, ema_weight_f32=True,
+                     zero_decay=True)
+    updates, _ = tx.update(gdev, state, params)
+    torch.cuda.synchronize()
+    for i in range(3):
+        _nan_equal(to_host(updates[f"l{i}"]), outs[i], f"scale_by_adam leaf {i}")
+    assert np.isnan(to_host(updates["l1"])[[3, 10, 77]]).all()
+    # without params there is no such term: finite updates throughout
+    updates, _ = tx.update(gdev, state, None)
+    torch.cuda.synchronize()
+    assert all(np.isfinite(to_host(updates[f"l{i}"])).all() for i in range(3))

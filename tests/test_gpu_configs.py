@@ -9,7 +9,8 @@
 * Full-size Llama-7B leaves (embedding 32000x4096 and one decoder layer:
   q/k/v/o 4096^2, gate/up/down 11008x4096, two RMSNorm vectors), 1 step.
 * 2^30-element quantize / dequantize / bf16 SR (log-uniform magnitudes
-  1e-8..1e2, random sign).
+  1e-8..1e2, random sign, with +-0 and denormals injected); quantize codes
+  and scales, and the dequantized values, bit-exact.
 
 Bar: codes, scales and fallback moments bit-exact; params within one bf16
 ulp (hardware rcp/sqrt direction); SR outputs bitwise for identical bits.
@@ -182,13 +183,12 @@ def test_llama_embedding_and_layer_full_size():
 
 
 def _c5_input(n, seed=5):
-    import torch
+    """The 2^30 configuration's input: |x| log-uniform in [1e-8, 1e2] with a
+    random sign, plus +-0 at every 97th element and f32 denormals (random
+    mantissa and sign) at every 89th from element 1 (bench.py's input)."""
+    import bench
 
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(seed)
-    x = torch.empty(n, device="cuda").uniform_(float(np.log(1e-8)), float(np.log(1e2)), generator=gen).exp_()
-    x[torch.rand(n, device="cuda", generator=gen) < 0.5] *= -1.0
-    return x
+    return bench._c5_input(n, seed)
 
 
 def test_quantize_dequantize_2p30_bitexact_and_error_bound():
@@ -198,19 +198,33 @@ def test_quantize_dequantize_2p30_bitexact_and_error_bound():
 
     n = 1 << 30
     x = _c5_input(n)
+    den = x[1::89]
+    assert bool(x[::97].eq(0).all()) and bool((den.abs() < 2.0 ** -126).all())
+    assert int(den.ne(0).sum()) > 0.98 * den.numel(), "the input carries its denormal elements"
+    assert bool((x[::97].view(torch.int32) < 0).any()), "some zeros are -0"
     qb = rf.quantize_blocks(x, block_size=2048)
     back = rf.dequantize_blocks(qb)
     # size-independent property on the device: the reference's error bound
     err = (back - x).abs().view(-1, 2048).amax(dim=1)
     assert bool(torch.all(err <= qb.scales * 0.01))
-    del back, err
+    del err
     xh = to_host(x)
     del x
     codes, scales = orc.quantize(xh, 2048, orc.Q_SIGNED)
+    del xh
     np.testing.assert_array_equal(to_host(qb.scales).view(np.uint32), scales.view(np.uint32))
     got = to_host(qb.values)
     bad = np.count_nonzero(got != codes.reshape(-1))
     assert bad == 0, f"{bad} codes differ over 2^30 elements"
+    del got
+    # dequantize bit-exact against the oracle, 2^26 elements at a time
+    sl = 1 << 26
+    flat = codes.reshape(-1)
+    for off in range(0, n, sl):
+        want = orc.dequantize(flat[off:off + sl], scales[off // 2048:(off + sl) // 2048], sl, 2048, orc.Q_SIGNED)
+        gotd = to_host(back[off:off + sl])
+        nbad = np.count_nonzero(gotd.view(np.uint32) != want.view(np.uint32))
+        assert nbad == 0, f"dequantize: {nbad} values differ in elements [{off}, {off + sl})"
 
 
 def test_sr_bf16_2p30_threefry_bitexact_and_unbiased():
@@ -237,9 +251,10 @@ def test_sr_bf16_2p30_threefry_bitexact_and_unbiased():
         r = _stochastic_round_bf16(xs, rf.prng.PRNGKey(100 + s)).to(torch.float64)
         acc += (r - xs.to(torch.float64)) / xs.to(torch.float64).abs()
     rel = (acc / 64).cpu().numpy()
-    dec = np.floor(np.log10(np.abs(xh[:m])))
-    for d in np.unique(dec):
-        sel = rel[dec == d]
+    normal = np.abs(xh[:m]) >= np.float32(2.0 ** -126)   # zeros and denormals have no relative bound
+    dec = np.floor(np.log10(np.where(normal, np.abs(xh[:m]), 1.0)))
+    for d in np.unique(dec[normal]):
+        sel = rel[normal & (dec == d)]
         if sel.size < 1000:
             continue
         # per-element relative error is at most 2^-7; its mean over 64 draws has

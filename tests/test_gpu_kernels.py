@@ -321,3 +321,34 @@ def test_apply_updates_nested_tree_native_and_python_walks():
         np.testing.assert_array_equal(to_host(out["a"][1][0]), want1)
         np.testing.assert_array_equal(to_host(out["b"]["x"]).view(np.uint32), wantx.view(np.uint32))
         np.testing.assert_array_equal(to_host(out["b"]["y"]), hp[2])
+
+
+def test_symmetric_int8_exact_ties_and_sr_closed_form():
+    """The kernel's symmetric quantizer on exact ties of jnp.round (half to
+    even, adam8.py:455) and on the floor + Bernoulli rule with fed words
+    placed one step below, at and above p (adam8.py:456-458); both against
+    the closed forms the oracle is pinned to."""
+    from tests.test_oracle import _bits_for_uniform, _symmetric_tie_block
+
+    rf = _rf()
+    x, n = _symmetric_tie_block()
+    qb = rf.quantize_blocks(to_device(x, "f32"), block_size=256, quantizer="symmetric_int8")
+    got = to_host(qb.values).view(np.int8).astype(np.int64)[:n]
+    k = np.arange(-127, 127)
+    np.testing.assert_array_equal(got[:254], np.where(k % 2 == 0, k, k + 1))
+    assert list(got[254:]) == [127, -127]
+    step = 2.0 ** -23
+    s_vals, us, want = [], [], []
+    for s, lo in ((2.25, 2), (-2.25, -3), (0.75, 0), (-0.75, -1), (126.5, 126), (-126.5, -127)):
+        p = s - lo
+        for u, w in ((p - step, lo + 1), (p, lo), (min(p + step, 1 - step), lo), (0.0, lo + 1)):
+            s_vals.append(s)
+            us.append(u)
+            want.append(w)
+    xs = np.concatenate([np.float32(s_vals), np.float32([127.0])])
+    bits = np.zeros(xs.size, np.uint32)
+    bits[:len(us)] = _bits_for_uniform(us)
+    qb = rf.quantize_blocks(to_device(xs, "f32"), block_size=xs.size, quantizer="symmetric_int8",
+                            stochastic_rounding=True, random_bits=to_device(bits, "u32"))
+    got = to_host(qb.values).view(np.int8).astype(np.int64)[:len(want)]
+    np.testing.assert_array_equal(got, want)

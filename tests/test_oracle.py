@@ -674,3 +674,82 @@ def test_magma_apply_masks_and_scales():
     np.testing.assert_array_equal(orc.magma_apply(delta, np.float32(0.5), True), delta * np.float32(0.5))
     np.testing.assert_array_equal(orc.magma_apply(delta, np.float32(0.5), True, np.float32(-0.1)),
                                   np.float32(-0.1) * (delta * np.float32(0.5)))
+
+
+def _symmetric_tie_block():
+    """A block whose absmax is 127, so scale = 127 / 127 = 1 exactly and
+    x / scale = x: every k + 0.5 for k in -127..126 (exact ties of
+    jnp.round), then 127 and -127 themselves (256 values)."""
+    halves = np.arange(-127, 127, dtype=np.float32) + np.float32(0.5)
+    x = np.concatenate([halves, np.float32([127.0, -127.0])])
+    return x, x.size
+
+
+def test_symmetric_round_half_even_exact_ties():
+    """adam8.py:455 jnp.round rounds halves to the even neighbour: 0.5 -> 0,
+    1.5 -> 2, 2.5 -> 2, -0.5 -> 0, -1.5 -> -2, 126.5 -> 126.  Round half
+    away from zero (1, 2, 3, -1, ...) or half up fails here."""
+    x, n = _symmetric_tie_block()
+    codes, scales = orc.quantize(x, 256, orc.Q_SYMMETRIC)
+    assert scales[0] == np.float32(1.0)
+    got = codes.reshape(-1)[:n].astype(np.int64)
+    k = np.arange(-127, 127)
+    even = np.where(k % 2 == 0, k, k + 1)          # the even one of k and k + 1
+    np.testing.assert_array_equal(got[:254], even)
+    assert list(got[254:]) == [127, -127]
+    assert got[127] == 0 and got[128] == 2 and got[129] == 2 and got[126] == 0 and got[125] == -2
+
+
+def _bits_for_uniform(u: np.ndarray) -> np.ndarray:
+    """Raw words whose jax.random.uniform value is exactly u (u a multiple
+    of 2^-23 in [0, 1)): mantissa = u * 2^23 in bits 9..31."""
+    m = np.round(np.asarray(u, np.float64) * (1 << 23)).astype(np.uint64)
+    return (m << np.uint64(9)).astype(np.uint32)
+
+
+def test_symmetric_sr_floor_plus_bernoulli_closed_form():
+    """adam8.py:456-458: r = floor(s) + bernoulli(s - floor(s)), bernoulli =
+    uniform < p.  With scale 1, s = x: for s = 2.25 the draw u < 0.25 gives
+    3, u >= 0.25 gives 2; for s = -2.25, floor is -3 and p = 0.75, so
+    u < 0.75 gives -2 and u >= 0.75 gives -3 (a truncating floor would give
+    -2 there); integers never move.  u sits one step below, at and above p."""
+    step = 2.0 ** -23
+    cases = []   # (s, u, expected)
+    for s, lo in ((2.25, 2), (-2.25, -3), (0.75, 0), (-0.75, -1), (126.5, 126), (-126.5, -127)):
+        p = s - lo
+        cases += [(s, p - step, lo + 1), (s, p, lo), (s, min(p + step, 1 - step), lo), (s, 0.0, lo + 1)]
+    cases += [(3.0, 0.0, 3), (3.0, 1 - step, 3), (-5.0, 0.0, -5), (0.0, 0.0, 0)]
+    s = np.float32([c[0] for c in cases])
+    x = np.concatenate([s, np.float32([127.0])])       # absmax 127: scale 1
+    bits = np.zeros(x.size, np.uint32)
+    bits[:s.size] = _bits_for_uniform([c[1] for c in cases])
+    assert np.all(orc.uniform01(bits[:s.size]) == np.float32([c[1] for c in cases]))
+    codes, scales = orc.quantize(x, x.size, orc.Q_SYMMETRIC, bits=bits)
+    assert scales[0] == np.float32(1.0)
+    np.testing.assert_array_equal(codes.reshape(-1)[:s.size].astype(np.int64), [c[2] for c in cases])
+
+
+def test_zero_weight_decay_term_closed_form():
+    """optim/adam.py's weight-0 decay term (``u + 0 * f32(p)``, utils.py:79-90)
+    in the oracle: for finite params the updates equal those without it
+    except that a -0 update becomes +0 when the param is positive; a
+    non-finite param makes the update NaN."""
+    rng = np.random.default_rng(4)
+    n = 4096
+    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    p[:4] = [np.inf, -np.inf, np.nan, 0.5]
+    g = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+    g[3] = -0.0   # with a -0 first moment: m = b1*(-0) + (1-b1)*(-0) = -0, a -0 direction
+
+    def run(zero):
+        hp = orc.make_hparams(count=1, apply=False, ema_weight_f32=True, zero_decay=zero)
+        m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+        m[3] = -0.0
+        out = np.empty(n, np.float32)
+        orc.adam8_leaf(hp, p.copy(), orc.F32, g, orc.F32, orc.MOM_F32, m, None, v, None, 2048, updates_out=out)
+        return out
+
+    base, zero = run(False), run(True)
+    assert np.isnan(zero[:3]).all() and np.isfinite(base[:3]).all()
+    np.testing.assert_array_equal(zero[4:], base[4:] + np.float32(0.0))
+    assert np.signbit(base[3]) and not np.signbit(zero[3])
