@@ -469,8 +469,8 @@ def _kernel_workload(args, kind):
     scales = torch.empty(nb, dtype=torch.float32, device="cuda")
 
     def quantize():
-        _lib.check(L.rf_blockwise_quantize(0, x.data_ptr(), n, BS, 0, 0, 0, None, codes.data_ptr(),
-                                           scales.data_ptr(), sp()), "quantize")
+        _lib.check(L.rf_blockwise_quantize(0, x.data_ptr(), _lib.RF_F32, n, BS, 0, 0, 0, None, codes.data_ptr(),
+                                           scales.data_ptr(), _lib.RF_F32, sp()), "quantize")
 
     if kind == "quantize":
         step = quantize
@@ -480,8 +480,8 @@ def _kernel_workload(args, kind):
         out = torch.empty(n, dtype=torch.float32, device="cuda")
 
         def step():
-            _lib.check(L.rf_blockwise_dequantize(0, codes.data_ptr(), scales.data_ptr(), n, BS, _lib.RF_F32,
-                                                 out.data_ptr(), sp()), "dequantize")
+            _lib.check(L.rf_blockwise_dequantize(0, codes.data_ptr(), scales.data_ptr(), _lib.RF_F32, n, BS,
+                                                 _lib.RF_F32, out.data_ptr(), sp()), "dequantize")
         nbytes = n + nb * 4 + n * 4
     elif kind == "sr_bf16":
         out = torch.empty(n, dtype=torch.bfloat16, device="cuda")

@@ -37,14 +37,16 @@ typedef int32_t rf_status;
 #define RF_ERR_HIP 2         /* a HIP runtime call failed */
 #define RF_ERR_UNSUPPORTED 3 /* valid for the reference, not implemented here */
 
-/* Element types of params, grads and fallback moments. */
+/* Element types of params, grads, fallback moments and block scales. */
 #define RF_F32 0
 #define RF_BF16 1
+#define RF_F16 2
 
 /* Moment storage of one leaf (adam8.py:605-630 _init_moment_leaf). */
 #define RF_MOMENT_QUANTIZED 0 /* uint8 codes [nblocks*block_size] + f32 scales [nblocks] */
 #define RF_MOMENT_F32 1       /* fallback_dtype float32 */
 #define RF_MOMENT_BF16 2      /* fallback_dtype bfloat16 */
+#define RF_MOMENT_F16 3       /* fallback_dtype float16 */
 
 /* Quantizers (adam8.py:113-187 quantize_blocks `quantizer`). */
 #define RF_Q_DYNAMIC_SIGNED 0   /* "bitsandbytes.dynamic.signed.8bit.v1", zero code 127 */
@@ -72,6 +74,10 @@ typedef int32_t rf_status;
 
 /* rf_adam8_leaf.flags */
 #define RF_LEAF_DECAY 1u    /* add_decayed_weights applies to this leaf (mask True) */
+#define RF_LEAF_SCALE_BF16 8u /* quantized moments: the block scales are stored as bfloat16
+                               (scale_dtype, adam8.py:186): computed and used for the codes
+                               in f32, stored rounded to nearest even, read back as f32 */
+#define RF_LEAF_SCALE_F16 16u /* the same with float16 scales */
 #define RF_LEAF_ZERO_DECAY 4u /* optim/adam.py's own decay term with weight 0 (adamw's
                                scale_by_adam gets weight_decay=0.0 and the params,
                                adam.py:185-201, :380-404): the update first becomes
@@ -89,8 +95,9 @@ typedef struct rf_adam8_leaf {
     void* param;        /* [size] param_dtype; read (decay/apply), written by the fused step */
     const void* grad;   /* [size] grad_dtype */
     float* updates;     /* [size] f32 output of the update-only (Optax) mode, else NULL */
-    void* mu;           /* quantized: uint8 [nblocks*block_size]; fallback: [size] f32/bf16 */
-    float* mu_scales;   /* quantized: f32 [nblocks]; fallback: NULL */
+    void* mu;           /* quantized: uint8 [nblocks*block_size]; fallback: [size] f32/bf16/f16 */
+    float* mu_scales;   /* quantized: [nblocks] block scales, f32 or (RF_LEAF_SCALE_*) 16-bit
+                           patterns; fallback: NULL */
     void* nu;           /* as mu (unsigned codebook) */
     float* nu_scales;
     const uint32_t* mu_bits;    /* RF_FED_BITS + RF_MOMENT_SR: [nblocks*block_size] raw bits */
@@ -98,8 +105,8 @@ typedef struct rf_adam8_leaf {
     const uint32_t* param_bits; /* RF_FED_BITS + RF_PARAM_SR: [size] raw bits */
     int64_t size;               /* elements of the leaf (QuantizedBlocks.size) */
     int32_t block_size;         /* QuantizedBlocks.block_size (quantized leaves) */
-    int32_t param_dtype;        /* RF_F32 | RF_BF16 */
-    int32_t grad_dtype;         /* RF_F32 | RF_BF16 */
+    int32_t param_dtype;        /* RF_F32 | RF_BF16 | RF_F16 */
+    int32_t grad_dtype;         /* RF_F32 | RF_BF16 | RF_F16 */
     int32_t moment_kind;        /* RF_MOMENT_* */
     int32_t state_index;        /* position in the flattened moment template: the per-leaf
                                    moment-SR key is split(key_mu|key_nu)[state_index]
@@ -252,20 +259,26 @@ RF_API rf_status rf_adam8_step_noalloc(const rf_adam8_leaf* leaves, int32_t n_le
                                        const rf_adam8_hparams* hp, void* stream);
 
 /*
- * adam8.py:113-187 quantize_blocks on a device f32 array of `size` elements:
+ * adam8.py:113-187 quantize_blocks on a device array x of `size` elements of
+ * x_dtype (RF_F32|RF_BF16|RF_F16; taken as f32, jnp.asarray(x, float32)):
  * values [nblocks*block_size] (uint8 codes, or int8 for the symmetric
- * quantizer; padding included), scales f32 [nblocks].  sr != 0 selects
- * stochastic rounding with raw bits `bits` [nblocks*block_size] when
- * non-NULL, else in-kernel Threefry-2x32 bits of key (key0, key1).
+ * quantizer; padding included), scales [nblocks] of scale_dtype (computed
+ * and used for the codes in f32, stored rounded to nearest even:
+ * scales.astype(scale_dtype)).  sr != 0 selects stochastic rounding with raw
+ * bits `bits` [nblocks*block_size] when non-NULL, else in-kernel
+ * Threefry-2x32 bits of key (key0, key1).
  */
-RF_API rf_status rf_blockwise_quantize(int32_t quantizer, const float* x, int64_t size,
+RF_API rf_status rf_blockwise_quantize(int32_t quantizer, const void* x, int32_t x_dtype, int64_t size,
                                 int32_t block_size, int32_t sr, uint32_t key0, uint32_t key1,
-                                const uint32_t* bits, void* values, float* scales, void* stream);
+                                const uint32_t* bits, void* values, void* scales, int32_t scale_dtype,
+                                void* stream);
 
-/* adam8.py:190-204 dequantize_blocks: out [size] of out_dtype (RF_F32|RF_BF16). */
-RF_API rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const float* scales,
-                                  int64_t size, int32_t block_size, int32_t out_dtype, void* out,
-                                  void* stream);
+/* adam8.py:190-204 dequantize_blocks: values * f32(scales) (scales of
+ * scale_dtype), out [size] of out_dtype (RF_F32|RF_BF16|RF_F16, rounded to
+ * nearest even). */
+RF_API rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const void* scales,
+                                  int32_t scale_dtype, int64_t size, int32_t block_size, int32_t out_dtype,
+                                  void* out, void* stream);
 
 /* utils.py:342-371 _stochastic_round_bf16: out [size] bf16 bit patterns.  Uses
  * `bits` [size] when non-NULL, else in-kernel Threefry-2x32 bits of key. */
@@ -278,12 +291,13 @@ typedef struct rf_apply_leaf {
     const float* updates;    /* [size] f32 */
     const uint32_t* bits;    /* fed SR bits [size] or NULL */
     int64_t size;
-    int32_t param_dtype;     /* RF_F32 | RF_BF16 */
+    int32_t param_dtype;     /* RF_F32 | RF_BF16 | RF_F16 */
     int32_t param_index;     /* key = split(key)[param_index] */
 } rf_apply_leaf;
 
 /* utils.py:648-708 apply_updates over n leaves: bf16 params take
- * f32(p) + u then SR (stochastic != 0) or RNE; f32 params take p + u. */
+ * f32(p) + u then SR (stochastic != 0) or RNE; f16 params f32(p) + u
+ * rounded to nearest even; f32 params take p + u. */
 RF_API rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic,
                            uint32_t key0, uint32_t key1, void* stream);
 
@@ -292,7 +306,7 @@ typedef struct rf_clip_leaf {
     const void* grad;   /* [size] dtype */
     void* out;          /* [size] dtype: grad * scale (may equal grad: in place) */
     int64_t size;
-    int32_t dtype;      /* RF_F32 | RF_BF16 */
+    int32_t dtype;      /* RF_F32 | RF_BF16 | RF_F16 */
     int32_t reserved;   /* 0 */
 } rf_clip_leaf;
 
@@ -311,8 +325,8 @@ typedef struct rf_magma_leaf {
     const void* mu;     /* [size] mu_dtype: the first moment before this step's EMA */
     float* updates;     /* [size] f32: the step's update, scaled in place by rf_magma_scale */
     int64_t size;
-    int32_t grad_dtype; /* RF_F32 | RF_BF16 */
-    int32_t mu_dtype;   /* RF_F32 | RF_BF16 */
+    int32_t grad_dtype; /* RF_F32 | RF_BF16 | RF_F16 */
+    int32_t mu_dtype;   /* RF_F32 | RF_BF16 | RF_F16 */
     int32_t key_index;  /* the leaf's position among all leaves of the update tree */
     int32_t reserved;   /* 0 */
 } rf_magma_leaf;

@@ -55,6 +55,37 @@ static inline uint16_t f32_to_bf16_rne(float x)
 }
 static inline float bf16_to_f32(uint16_t h) { return u2f(((uint32_t)h) << 16); }
 
+/* f32 -> IEEE binary16 (astype(float16)), round to nearest even: overflow
+ * from 65520 up goes to Inf, magnitudes below 2^-14 become subnormal
+ * multiples of 2^-24 (or zero), NaN stays NaN with its sign and the top
+ * payload bits, quiet. */
+static inline uint16_t f32_to_f16_rne(float x)
+{
+    uint32_t u = f2u(x);
+    uint32_t sign = (u >> 16) & 0x8000u;
+    uint32_t a = u & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((a >> 13) & 0x3FFu));
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);       /* |x| >= 65520 (or Inf) */
+    if (a < 0x38800000u) {                                          /* |x| < 2^-14 */
+        float k = rintf(u2f(a) * 16777216.0f);                      /* |x| / 2^-24, exact scale */
+        return (uint16_t)(sign | (uint32_t)k);                      /* k = 1024 is 2^-14 itself */
+    }
+    a += 0x0FFFu + ((a >> 13) & 1u);                                /* 23 -> 10 mantissa bits */
+    return (uint16_t)(sign | ((a - 0x38000000u) >> 13));            /* exponent bias 127 -> 15 */
+}
+
+static inline float f16_to_f32(uint16_t h)
+{
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    if (e == 0) {
+        float v = (float)m * 5.9604644775390625e-8f;                /* m * 2^-24, exact */
+        return u2f(f2u(v) | sign);
+    }
+    if (e == 31) return u2f(sign | 0x7F800000u | (m << 13));
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
 /* utils.py:342-371 _stochastic_round_bf16: noise = bits & 0xFFFF, zero noise
  * for |x| >= Inf bit pattern, (x + noise) & 0xFFFF0000. */
 static inline uint16_t sr_bf16_from_bits(float x, uint32_t bits)
@@ -166,6 +197,54 @@ ORC_API void orc_codebook(int is_signed, float* out /* [256] */)
     for (int i = 0; i < 256 && i < nd; ++i) out[i] = (float)data[i];
 }
 
+/* ------------------------------------------------- dtypes and flags -- */
+enum { ORC_F32 = 0, ORC_BF16 = 1, ORC_F16 = 2 };
+enum { ORC_MOM_QUANT = 0, ORC_MOM_F32 = 1, ORC_MOM_BF16 = 2, ORC_MOM_F16 = 3 };
+enum {
+    ORC_NESTEROV = 1,       /* adam8.py:341-350 */
+    ORC_DECAY = 2,          /* add_decayed_weights applies to this leaf */
+    ORC_DECAY_WEAK = 4,     /* wd is a Python scalar: wd*p in the param dtype */
+    ORC_LR = 8,             /* scale_by_learning_rate in the chain */
+    ORC_MOMENT_SR = 16,     /* adamw8(stochastic_rounding=True) */
+    ORC_PARAM_SR = 32,      /* apply_updates(stochastic=True) for bf16 params */
+    ORC_APPLY = 64,         /* write params (fused step) instead of updates */
+    ORC_STORE_SR = 512,     /* bf16 fallback moments stored with SR from mu_bits / nu_bits
+                               (optim/adam.py:219-222, utils.py:374-409) */
+    ORC_ZERO_DECAY = 1024,  /* optim/adam.py's own decay term with weight 0 before the
+                               optax decay (adam.py:185-201 inside adamw, :380-404) */
+    ORC_SCALE_BF16 = 2048,  /* quantized moments store scales.astype(bfloat16) (adam8.py:186) */
+    ORC_SCALE_F16 = 4096,   /* ... astype(float16) */
+};
+
+static inline float load_val(int dtype, const void* p, int64_t e)
+{
+    if (dtype == ORC_BF16) return bf16_to_f32(((const uint16_t*)p)[e]);
+    if (dtype == ORC_F16) return f16_to_f32(((const uint16_t*)p)[e]);
+    return ((const float*)p)[e];
+}
+
+/* x rounded to a 16-bit dtype (nearest even) as its bit pattern. */
+static inline uint16_t to_h16(int dtype, float x)
+{
+    return dtype == ORC_F16 ? f32_to_f16_rne(x) : f32_to_bf16_rne(x);
+}
+
+static inline float round_to(int dtype, float x)
+{
+    if (dtype == ORC_BF16) return bf16_to_f32(f32_to_bf16_rne(x));
+    if (dtype == ORC_F16) return f16_to_f32(f32_to_f16_rne(x));
+    return x;
+}
+
+/* A block scale as stored: scales.astype(scale_dtype) read back as f32
+ * (adam8.py:186, :202); the codes use the f32 scale before this. */
+static inline float stored_scale(int32_t flags, float s)
+{
+    if (flags & ORC_SCALE_BF16) return round_to(ORC_BF16, s);
+    if (flags & ORC_SCALE_F16) return round_to(ORC_F16, s);
+    return s;
+}
+
 /* ---------------------------------------------------------- quantizers -- */
 enum { ORC_Q_SIGNED = 0, ORC_Q_UNSIGNED = 1, ORC_Q_SYMMETRIC = 2 };
 
@@ -230,7 +309,7 @@ static inline float block_absmax(const float* x, int64_t len)
  * (nblocks*block_size words, may be NULL when sr == 0) are the raw
  * jax.random.bits that bernoulli consumes, over the padded block array. */
 ORC_API void orc_quantize(int quantizer, const float* x, int64_t size, int64_t block_size,
-                          int sr, const uint32_t* bits, uint8_t* codes, float* scales)
+                          int sr, const uint32_t* bits, uint8_t* codes, float* scales, int scale_flags)
 {
     int64_t nblocks = size > 0 ? (size + block_size - 1) / block_size : 1;
     float cb[256];
@@ -246,7 +325,7 @@ ORC_API void orc_quantize(int quantizer, const float* x, int64_t size, int64_t b
         if (quantizer == ORC_Q_SYMMETRIC) {
             /* adam8.py:143-164 */
             float scale = (amax > 0.0f) ? amax / 127.0f : 1.0f;
-            scales[b] = scale;
+            scales[b] = stored_scale(scale_flags, scale);
             for (int64_t j = 0; j < block_size; ++j) {
                 float s = clipf(blk[j] / scale, -127.0f, 127.0f);
                 float r;
@@ -262,7 +341,7 @@ ORC_API void orc_quantize(int quantizer, const float* x, int64_t size, int64_t b
             }
         } else {
             float scale = (amax > 0.0f) ? amax : 1.0f;  /* adam8.py:167 */
-            scales[b] = scale;
+            scales[b] = stored_scale(scale_flags, scale);
             for (int64_t j = 0; j < block_size; ++j) {
                 float n = clipf(blk[j] / scale, cb[0], cb[255]);   /* adam8.py:168 */
                 uint32_t w = sr ? bits[b * block_size + j] : 0u;
@@ -336,21 +415,6 @@ ORC_API void orc_nearest_codes_list(int quantizer, const uint32_t* bits, int64_t
 }
 
 /* ------------------------------------------------------------ the step -- */
-enum { ORC_F32 = 0, ORC_BF16 = 1 };
-enum { ORC_MOM_QUANT = 0, ORC_MOM_F32 = 1, ORC_MOM_BF16 = 2 };
-enum {
-    ORC_NESTEROV = 1,       /* adam8.py:341-350 */
-    ORC_DECAY = 2,          /* add_decayed_weights applies to this leaf */
-    ORC_DECAY_WEAK = 4,     /* wd is a Python scalar: wd*p in the param dtype */
-    ORC_LR = 8,             /* scale_by_learning_rate in the chain */
-    ORC_MOMENT_SR = 16,     /* adamw8(stochastic_rounding=True) */
-    ORC_PARAM_SR = 32,      /* apply_updates(stochastic=True) for bf16 params */
-    ORC_APPLY = 64,         /* write params (fused step) instead of updates */
-    ORC_STORE_SR = 512,     /* bf16 fallback moments stored with SR from mu_bits / nu_bits
-                               (optim/adam.py:219-222, utils.py:374-409) */
-    ORC_ZERO_DECAY = 1024,  /* optim/adam.py's own decay term with weight 0 before the
-                               optax decay (adam.py:185-201 inside adamw, :380-404) */
-};
 
 /* one_minus_b1 weights the gradient in the first-moment EMA; the Nesterov
  * combination uses nest_one_minus_b1 (adam8.py:322-327 and :341-350 both use
@@ -366,10 +430,6 @@ typedef struct {
     float nest_one_minus_b1;
 } orc_hparams;
 
-static inline float load_val(int dtype, const void* p, int64_t e)
-{
-    return dtype == ORC_BF16 ? bf16_to_f32(((const uint16_t*)p)[e]) : ((const float*)p)[e];
-}
 
 /* Direction, decay, lr and apply for one element.  Follows adam8.py:352-362
  * (bias correction utils.py:318-324), optax add_decayed_weights (u + wd*p),
@@ -400,11 +460,13 @@ static inline float direction_and_apply(const orc_hparams* hp, int pdtype, void*
     }
     if (hp->flags & ORC_DECAY) {
         float wdp;
-        if (pdtype == ORC_BF16 && (hp->flags & ORC_DECAY_WEAK)) {
-            /* Python-scalar wd times a bf16 array stays bf16 (JAX weak
-             * typing): bf16(wd) * p rounded once to bf16. */
-            float wd16 = bf16_to_f32(f32_to_bf16_rne(hp->weight_decay));
-            wdp = bf16_to_f32(f32_to_bf16_rne(wd16 * p));
+        if ((pdtype == ORC_BF16 || pdtype == ORC_F16) && (hp->flags & ORC_DECAY_WEAK)) {
+            /* Python-scalar wd times a bf16 (f16) array stays bf16 (f16),
+             * JAX weak typing: the wd and the product each rounded once to
+             * the param dtype (the product of two 16-bit values is exact in
+             * f32). */
+            float wd16 = round_to(pdtype, hp->weight_decay);
+            wdp = round_to(pdtype, wd16 * p);
         } else {
             wdp = hp->weight_decay * p;
         }
@@ -417,6 +479,8 @@ static inline float direction_and_apply(const orc_hparams* hp, int pdtype, void*
         if (pdtype == ORC_BF16) {
             float s = p + u;
             *pnew_bf16 = (hp->flags & ORC_PARAM_SR) ? sr_bf16_from_bits(s, pbits) : f32_to_bf16_rne(s);
+        } else if (pdtype == ORC_F16) {
+            *pnew_bf16 = f32_to_f16_rne(p + u);   /* (p + u).astype(float16), utils.py:700 */
         } else {
             *pnew_f32 = p + u;
         }
@@ -468,11 +532,11 @@ ORC_API void orc_adam8_leaf(const orc_hparams* hp,
                 mb[j] = m;
                 vb[j] = v;
                 int wrote;
-                float pf; uint16_t ph;
+                float pf = 0.0f; uint16_t ph = 0;
                 uint32_t pbits = (p_bits && (hp->flags & ORC_PARAM_SR)) ? p_bits[e] : 0u;
                 float u = direction_and_apply(hp, pdtype, param, e, m, v, g, pbits, &wrote, &pf, &ph);
                 if (wrote) {
-                    if (pdtype == ORC_BF16) ((uint16_t*)param)[e] = ph;
+                    if (pdtype != ORC_F32) ((uint16_t*)param)[e] = ph;
                     else ((float*)param)[e] = pf;
                 } else if (updates_out) {
                     updates_out[e] = u;
@@ -482,8 +546,8 @@ ORC_API void orc_adam8_leaf(const orc_hparams* hp,
              * moments, padding zero-filled (adam8.py:137-141). */
             float am = block_absmax(mb, block_size), av = block_absmax(vb, block_size);
             float sm = (am > 0.0f) ? am : 1.0f, sv = (av > 0.0f) ? av : 1.0f;
-            mu_scales[b] = sm;
-            nu_scales[b] = sv;
+            mu_scales[b] = stored_scale(hp->flags, sm);
+            nu_scales[b] = stored_scale(hp->flags, sv);
             for (int64_t j = 0; j < block_size; ++j) {
                 int64_t e = b * block_size + j;
                 float nm = clipf(mb[j] / sm, cbs[0], cbs[255]);
@@ -498,19 +562,20 @@ ORC_API void orc_adam8_leaf(const orc_hparams* hp,
 #pragma omp parallel for schedule(static)
         for (int64_t e = 0; e < n; ++e) {
             float g = load_val(gdtype, grad, e);
-            float mp = mkind == ORC_MOM_BF16 ? bf16_to_f32(((uint16_t*)mu)[e]) : ((float*)mu)[e];
-            float vp = mkind == ORC_MOM_BF16 ? bf16_to_f32(((uint16_t*)nu)[e]) : ((float*)nu)[e];
+            int mdt = mkind == ORC_MOM_BF16 ? ORC_BF16 : (mkind == ORC_MOM_F16 ? ORC_F16 : ORC_F32);
+            float mp = load_val(mdt, mu, e);
+            float vp = load_val(mdt, nu, e);
             float t1 = hp->b1 * mp, t2 = hp->one_minus_b1 * g;
             float m = t1 + t2;
             float gg = g * g;
             float t3 = hp->b2 * vp, t4 = hp->one_minus_b2 * gg;
             float v = t3 + t4;
             int wrote;
-            float pf; uint16_t ph;
+            float pf = 0.0f; uint16_t ph = 0;
             uint32_t pbits = (p_bits && (hp->flags & ORC_PARAM_SR)) ? p_bits[e] : 0u;
             float u = direction_and_apply(hp, pdtype, param, e, m, v, g, pbits, &wrote, &pf, &ph);
             if (wrote) {
-                if (pdtype == ORC_BF16) ((uint16_t*)param)[e] = ph;
+                if (pdtype != ORC_F32) ((uint16_t*)param)[e] = ph;
                 else ((float*)param)[e] = pf;
             } else if (updates_out) {
                 updates_out[e] = u;
@@ -520,9 +585,9 @@ ORC_API void orc_adam8_leaf(const orc_hparams* hp,
             if (mkind == ORC_MOM_BF16 && (hp->flags & ORC_STORE_SR)) {
                 ((uint16_t*)mu)[e] = sr_bf16_from_bits(m, mu_bits[e]);
                 ((uint16_t*)nu)[e] = sr_bf16_from_bits(v, nu_bits[e]);
-            } else if (mkind == ORC_MOM_BF16) {
-                ((uint16_t*)mu)[e] = f32_to_bf16_rne(m);
-                ((uint16_t*)nu)[e] = f32_to_bf16_rne(v);
+            } else if (mdt != ORC_F32) {
+                ((uint16_t*)mu)[e] = to_h16(mdt, m);
+                ((uint16_t*)nu)[e] = to_h16(mdt, v);
             } else {
                 ((float*)mu)[e] = m;
                 ((float*)nu)[e] = v;
@@ -541,6 +606,9 @@ ORC_API void orc_apply_updates(int pdtype, void* param, const float* upd, int64_
         if (pdtype == ORC_BF16) {
             float s = bf16_to_f32(((uint16_t*)param)[e]) + upd[e];
             ((uint16_t*)param)[e] = sr ? sr_bf16_from_bits(s, bits[e]) : f32_to_bf16_rne(s);
+        } else if (pdtype == ORC_F16) {
+            float s = f16_to_f32(((uint16_t*)param)[e]) + upd[e];
+            ((uint16_t*)param)[e] = f32_to_f16_rne(s);
         } else {
             ((float*)param)[e] = ((float*)param)[e] + upd[e];
         }
@@ -552,6 +620,17 @@ ORC_API void orc_sr_bf16(const float* x, const uint32_t* bits, int64_t n, uint16
 {
 #pragma omp parallel for schedule(static)
     for (int64_t e = 0; e < n; ++e) out[e] = sr_bf16_from_bits(x[e], bits[e]);
+}
+
+/* f32 -> f16 RNE over an array (astype(float16)) and back. */
+ORC_API void orc_f32_to_f16(const float* x, int64_t n, uint16_t* out)
+{
+    for (int64_t e = 0; e < n; ++e) out[e] = f32_to_f16_rne(x[e]);
+}
+
+ORC_API void orc_f16_to_f32(const uint16_t* h, int64_t n, float* out)
+{
+    for (int64_t e = 0; e < n; ++e) out[e] = f16_to_f32(h[e]);
 }
 
 /* f32 -> bf16 RNE over an array (astype(bfloat16)). */

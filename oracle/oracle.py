@@ -24,10 +24,11 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liborc_adam8.so")
 
 Q_SIGNED, Q_UNSIGNED, Q_SYMMETRIC = 0, 1, 2
-F32, BF16 = 0, 1
-MOM_QUANT, MOM_F32, MOM_BF16 = 0, 1, 2
+F32, BF16, F16 = 0, 1, 2
+MOM_QUANT, MOM_F32, MOM_BF16, MOM_F16 = 0, 1, 2, 3
 NESTEROV, DECAY, DECAY_WEAK, LR, MOMENT_SR, PARAM_SR, APPLY, STORE_SR = 1, 2, 4, 8, 16, 32, 64, 512
 ZERO_DECAY = 1024
+SCALE_BF16, SCALE_F16 = 2048, 4096
 
 
 class Hparams(ctypes.Structure):
@@ -70,7 +71,7 @@ def lib() -> ctypes.CDLL:
         _lib.orc_random_bits.argtypes = [u32, u32, ctypes.c_uint64, i64, p]
         _lib.orc_split.argtypes = [u32, u32, ctypes.c_int32, p]
         _lib.orc_codebook.argtypes = [ctypes.c_int, p]
-        _lib.orc_quantize.argtypes = [ctypes.c_int, p, i64, i64, ctypes.c_int, p, p, p]
+        _lib.orc_quantize.argtypes = [ctypes.c_int, p, i64, i64, ctypes.c_int, p, p, p, ctypes.c_int]
         _lib.orc_dequantize.argtypes = [ctypes.c_int, p, p, i64, i64, p]
         _lib.orc_nearest_code.argtypes = [ctypes.c_int, ctypes.c_float]
         _lib.orc_nearest_code.restype = ctypes.c_int
@@ -84,6 +85,8 @@ def lib() -> ctypes.CDLL:
         _lib.orc_apply_updates.argtypes = [ctypes.c_int, p, p, i64, ctypes.c_int, p]
         _lib.orc_sr_bf16.argtypes = [p, p, i64, p]
         _lib.orc_f32_to_bf16.argtypes = [p, i64, p]
+        _lib.orc_f32_to_f16.argtypes = [p, i64, p]
+        _lib.orc_f16_to_f32.argtypes = [p, i64, p]
         _lib.orc_set_threads.argtypes = [ctypes.c_int]
         _lib.orc_get_threads.restype = ctypes.c_int
     return _lib
@@ -201,7 +204,9 @@ def nblocks_for(size: int, block_size: int) -> int:
     return max(1, -(-int(size) // int(block_size)))
 
 
-def quantize(x: np.ndarray, block_size: int, quantizer: int = Q_SIGNED, bits=None):
+def quantize(x: np.ndarray, block_size: int, quantizer: int = Q_SIGNED, bits=None, scale_dtype: int = F32):
+    """quantize_blocks (adam8.py:113-187) of f32 values; the returned scales
+    are the stored ones, scales.astype(scale_dtype), as f32 values."""
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
     nb = nblocks_for(x.size, block_size)
     codes = np.empty(nb * block_size, dtype=np.uint8)
@@ -210,8 +215,9 @@ def quantize(x: np.ndarray, block_size: int, quantizer: int = Q_SIGNED, bits=Non
     if sr:
         bits = np.ascontiguousarray(bits, dtype=np.uint32).reshape(-1)
         assert bits.size == nb * block_size
+    flags = {F32: 0, BF16: SCALE_BF16, F16: SCALE_F16}[scale_dtype]
     lib().orc_quantize(quantizer, _ptr(x), x.size, block_size, 1 if sr else 0,
-                       _ptr(bits), _ptr(codes), _ptr(scales))
+                       _ptr(bits), _ptr(codes), _ptr(scales), flags)
     if quantizer == Q_SYMMETRIC:
         codes = codes.view(np.int8)
     return codes.reshape(nb, block_size), scales
@@ -238,6 +244,40 @@ def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    """astype(float16) as bit patterns (the oracle's restatement of IEEE
+    binary16 round to nearest even)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size, dtype=np.uint16)
+    lib().orc_f32_to_f16(_ptr(x), x.size, _ptr(out))
+    return out
+
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16).reshape(-1)
+    out = np.empty(h.size, dtype=np.float32)
+    lib().orc_f16_to_f32(_ptr(h), h.size, _ptr(out))
+    return out
+
+
+def to_f32(x: np.ndarray, dtype: int) -> np.ndarray:
+    """f32 values of an array in F32 values or BF16 / F16 bit patterns."""
+    if dtype == BF16:
+        return bf16_bits_to_f32(x)
+    if dtype == F16:
+        return f16_bits_to_f32(x)
+    return np.asarray(x, np.float32)
+
+
+def from_f32(x: np.ndarray, dtype: int) -> np.ndarray:
+    """F32 values or BF16 / F16 bit patterns (round to nearest even)."""
+    if dtype == BF16:
+        return f32_to_bf16_bits(x)
+    if dtype == F16:
+        return f32_to_f16_bits(x)
+    return np.asarray(x, np.float32)
+
+
 def sr_bf16(x: np.ndarray, bits: np.ndarray) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
     bits = np.ascontiguousarray(bits, dtype=np.uint32).reshape(-1)
@@ -250,7 +290,7 @@ def sr_bf16(x: np.ndarray, bits: np.ndarray) -> np.ndarray:
 def make_hparams(*, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0, weight_decay=0.0, lr=None,
                  count=1, nesterov=False, decay=False, decay_weak=True, moment_sr=False,
                  param_sr=False, apply=False, ema_weight_f32=False, store_sr=False,
-                 zero_decay=False) -> Hparams:
+                 zero_decay=False, scale_dtype=F32) -> Hparams:
     """Scalars exactly as the reference derives them from Python floats:
     ``1.0 - b1`` in double then f32 (adam8.py:323), ``1 - b1**t`` in f32
     (adam8.py:338-339, f32 pow: parity unpinned).  ``ema_weight_f32``: the
@@ -259,7 +299,8 @@ def make_hparams(*, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0, weight_decay=0.0, 
     double ``1.0 - b1`` (adam.py:146-160).  ``store_sr``: bf16 fallback
     moments are stored with stochastic rounding (adam.py:219-222).
     ``zero_decay``: optim/adam.py's own weight-0 decay term ``u + 0*p``
-    before the optax decay (adam.py:185-201 inside adamw)."""
+    before the optax decay (adam.py:185-201 inside adamw).  ``scale_dtype``:
+    quantized moments store their block scales as that dtype (adam8.py:186)."""
     f32 = np.float32
     t = f32(count)
     hp = Hparams()
@@ -294,6 +335,7 @@ def make_hparams(*, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0, weight_decay=0.0, 
         flags |= STORE_SR
     if zero_decay:
         flags |= ZERO_DECAY
+    flags |= {F32: 0, BF16: SCALE_BF16, F16: SCALE_F16}[scale_dtype]
     hp.flags = flags
     return hp
 
@@ -303,7 +345,9 @@ def adam8_leaf(hp: Hparams, param: np.ndarray, pdtype: int, grad: np.ndarray, gd
                mu_bits=None, nu_bits=None, p_bits=None, updates_out=None) -> None:
     """Run one leaf of one step in place on NumPy buffers.
 
-    ``param``/``grad`` hold f32 values or bf16 bit patterns (uint16).
+    ``param``/``grad`` hold f32 values or bf16 / f16 bit patterns (uint16);
+    16-bit fallback moments likewise; quantized scales are f32 arrays holding
+    the stored (``scale_dtype``-rounded) values.
     """
     n = grad.size
     lib().orc_adam8_leaf(ctypes.byref(hp), pdtype, _ptr(param), gdtype, _ptr(grad), n, mkind,
@@ -339,14 +383,15 @@ def global_norm_clip_scale(grads, max_norm: float):
 
 def clip_leaf(g: np.ndarray, dtype: int, scale) -> np.ndarray:
     """transforms.py:79-82 ``leaf * scale.astype(leaf.dtype)``: f32 leaves
-    multiply in f32; bf16 leaves (bit patterns) multiply by bf16(scale) with
-    one round-to-nearest-even of the exact product."""
+    multiply in f32; bf16 / f16 leaves (bit patterns) multiply by the scale
+    rounded to their dtype with one round-to-nearest-even of the exact
+    product."""
     if dtype == F32:
         return (np.asarray(g, np.float32) * np.float32(scale)).astype(np.float32)
-    s16 = bf16_bits_to_f32(f32_to_bf16_bits(np.array([scale], np.float32)))[0]
+    s16 = to_f32(from_f32(np.array([scale], np.float32), dtype), dtype)[0]
     with np.errstate(invalid="ignore", over="ignore"):  # Inf * 0 -> NaN, as on the device
-        prod = bf16_bits_to_f32(np.asarray(g, np.uint16)) * np.float32(s16)  # exact: 8 x 8 significant bits
-    return f32_to_bf16_bits(prod)
+        prod = to_f32(np.asarray(g, np.uint16), dtype) * np.float32(s16)  # exact: at most 11 x 11 bits
+    return from_f32(prod, dtype)
 
 
 # ------------------------------------------------ optax.apply_if_finite --
@@ -354,7 +399,7 @@ def all_finite(grads, dtypes) -> bool:
     """optax.apply_if_finite's ``isfinite``: every element of every incoming
     grad leaf is finite (``dtypes``: F32 arrays or BF16 bit patterns)."""
     for g, dt in zip(grads, dtypes):
-        vals = bf16_bits_to_f32(np.asarray(g, np.uint16)) if dt == BF16 else np.asarray(g, np.float32)
+        vals = to_f32(g, dt)
         if not np.isfinite(vals).all():
             return False
     return True

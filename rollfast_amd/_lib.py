@@ -16,8 +16,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_lib", "librfadam8.so")
 
 RF_OK, RF_ERR_INVALID, RF_ERR_HIP, RF_ERR_UNSUPPORTED = 0, 1, 2, 3
-RF_F32, RF_BF16 = 0, 1
-RF_MOMENT_QUANTIZED, RF_MOMENT_F32, RF_MOMENT_BF16 = 0, 1, 2
+RF_F32, RF_BF16, RF_F16 = 0, 1, 2
+RF_MOMENT_QUANTIZED, RF_MOMENT_F32, RF_MOMENT_BF16, RF_MOMENT_F16 = 0, 1, 2, 3
 RF_Q_DYNAMIC_SIGNED, RF_Q_DYNAMIC_UNSIGNED, RF_Q_SYMMETRIC_INT8 = 0, 1, 2
 RF_NESTEROV = 1
 RF_DECAY_WEAK = 4
@@ -30,6 +30,8 @@ RF_SKIP_NONFINITE = 512
 RF_LEAF_DECAY = 1
 RF_LEAF_STORE_SR = 2
 RF_LEAF_ZERO_DECAY = 4
+RF_LEAF_SCALE_BF16 = 8
+RF_LEAF_SCALE_F16 = 16
 RF_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 _p = ctypes.c_void_p
@@ -192,8 +194,8 @@ def lib() -> ctypes.CDLL:
     L.rf_adam8_plan_destroy.argtypes = [_p]
     L.rf_adam8_step.argtypes = [ctypes.POINTER(Adam8Leaf), i32, i32, ctypes.POINTER(Adam8Hparams), _p]
     L.rf_adam8_step_noalloc.argtypes = [ctypes.POINTER(Adam8Leaf), i32, i32, ctypes.POINTER(Adam8Hparams), _p]
-    L.rf_blockwise_quantize.argtypes = [i32, _p, i64, i32, i32, u32, u32, _p, _p, _p, _p]
-    L.rf_blockwise_dequantize.argtypes = [i32, _p, _p, i64, i32, i32, _p, _p]
+    L.rf_blockwise_quantize.argtypes = [i32, _p, i32, i64, i32, i32, u32, u32, _p, _p, _p, i32, _p]
+    L.rf_blockwise_dequantize.argtypes = [i32, _p, _p, i32, i64, i32, i32, _p, _p]
     L.rf_sr_bf16.argtypes = [_p, i64, u32, u32, _p, _p, _p]
     L.rf_apply_updates.argtypes = [ctypes.POINTER(ApplyLeaf), i32, i32, u32, u32, _p]
     f32 = ctypes.c_float

@@ -17,13 +17,14 @@ template <typename PT, typename GT>
 static adam_kernel_t pick(bool psr, bool nest)
 {
     constexpr bool A = RFI_APPLY != 0, M = RFI_MSR != 0, E = RFI_EXACT != 0;
-    if constexpr (A) {
+    if constexpr (A && IS_BF16<PT>) {  // stochastic rounding exists for bf16 params only
         if (psr) return nest ? &k_adam8<PT, GT, A, M, true, true, E> : &k_adam8<PT, GT, A, M, true, false, E>;
     }
     return nest ? &k_adam8<PT, GT, A, M, false, true, E> : &k_adam8<PT, GT, A, M, false, false, E>;
 }
 
-// dtype_combo = 2*(param is bf16) + (grad is bf16); -1 = the generic kernel
+// dtype_combo = 2*(param is bf16) + (grad is bf16) for f32/bf16 params and
+// grads, 4 for f16 params and grads; -1 = the generic kernel
 adam_kernel_t RF_PICK_NAME(RFI_APPLY, RFI_MSR, RFI_EXACT)(int dtype_combo, bool psr, bool nest)
 {
     constexpr bool A = RFI_APPLY != 0, M = RFI_MSR != 0, E = RFI_EXACT != 0;
@@ -34,6 +35,7 @@ adam_kernel_t RF_PICK_NAME(RFI_APPLY, RFI_MSR, RFI_EXACT)(int dtype_combo, bool 
         return nest ? &k_adam8_gen<A, M, false, true, E> : &k_adam8_gen<A, M, false, false, E>;
     }
     switch (dtype_combo) {
+        case 4: return pick<_Float16, _Float16>(psr, nest);
         case 3: return pick<uint16_t, uint16_t>(psr, nest);
         case 2: return pick<uint16_t, float>(psr, nest);
         case 1: return pick<float, uint16_t>(psr, nest);

@@ -64,7 +64,7 @@ struct KHp {
     float nb1, nomb1, rsbc2;  // nesterov: b1/bc1_next, (1-b1)/bc1, 1/sqrt(bc2)
     float nomb1x;             // nesterov: f32(1 - b1) (double), exact path
     float eps, eps_root;
-    float wd, wd16;           // f32(wd) and bf16(wd) as f32 (weak-typed decay of bf16 params)
+    float wd, wd16, wdh;      // f32(wd), bf16(wd) and f16(wd) as f32 (weak-typed decay of 16-bit params)
     float neg_lr;             // f32(-lr), or 1.0 when the chain has no learning-rate scale
     uint32_t flags;
     int32_t run;              // fast kernel: consecutive units a wave takes before its grid stride (>= 1)
@@ -128,6 +128,45 @@ typedef __bf16 rf_bf2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi)
 {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((rf_f2){lo, hi}, rf_bf2));
+}
+
+// f16 (IEEE binary16) conversions: exact widening; narrowing rounds to
+// nearest even with f16 subnormals kept (v_cvt_f32_f16 / v_cvt_f16_f32).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+__device__ __forceinline__ uint32_t f32_to_f16_rne(float x)
+{
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+__device__ __forceinline__ float round_to_f16(float x) { return f16_bits_to_f32(f32_to_f16_rne(x)); }
+
+__device__ __forceinline__ uint32_t pack_f16x2_rne(float lo, float hi)
+{
+    return f32_to_f16_rne(lo) | (f32_to_f16_rne(hi) << 16);
+}
+
+// Element types of the templated units: float = f32, uint16_t = bf16 bit
+// patterns, _Float16 = f16.
+template <typename T>
+constexpr bool IS_BF16 = std::is_same<T, uint16_t>::value;
+template <typename T>
+constexpr bool IS_F16 = std::is_same<T, _Float16>::value;
+
+// Two f32 values rounded to the 16-bit type T (nearest even) and packed.
+template <typename T>
+__device__ __forceinline__ uint32_t pack_h16x2_rne(float lo, float hi)
+{
+    if constexpr (IS_F16<T>) return pack_f16x2_rne(lo, hi);
+    else return pack_bf16x2_rne(lo, hi);
+}
+
+// f32 value of a 16-bit pattern of type T.
+template <typename T>
+__device__ __forceinline__ float h16_to_f32(uint32_t h)
+{
+    if constexpr (IS_F16<T>) return f16_bits_to_f32(h & 0xFFFFu);
+    else return bf16_bits_to_f32(h & 0xFFFFu);
 }
 
 // utils.py:365-371: noise = bits & 0xFFFF; no noise for |x| >= Inf bits;
@@ -378,7 +417,7 @@ __device__ __forceinline__ float adam_direction(const KHp& h, float m, float v, 
     }
 }
 
-enum : int32_t { WD_OFF = 0, WD_F32 = 1, WD_BF16 = 2 };
+enum : int32_t { WD_OFF = 0, WD_F32 = 1, WD_BF16 = 2, WD_F16 = 3 };
 
 // optax add_decayed_weights (u + wd*p) then scale_by_learning_rate ((-lr)*u);
 // `zero`: optim/adam.py's own weight-0 term u + 0*p first (RF_LEAF_ZERO_DECAY).
@@ -390,6 +429,8 @@ __device__ __forceinline__ float decay_and_scale(const KHp& h, float u, float p,
     }
     if (wd_mode == WD_BF16) {
         u = u + round_to_bf16(h.wd16 * p);  // bf16*bf16 is exact in f32: one rounding
+    } else if (wd_mode == WD_F16) {
+        u = u + round_to_f16(h.wdh * p);    // f16*f16 is exact in f32: one rounding
     } else if (wd_mode == WD_F32) {
         const float wdp = h.wd * p;
         u = u + wdp;
@@ -438,13 +479,21 @@ __device__ __forceinline__ void ema(const KHp& h, float mp, float vp, float g, f
 template <typename T>
 __device__ __forceinline__ void load8(const void* base, int64_t e0, float (&x)[8])
 {
-    if constexpr (std::is_same<T, uint16_t>::value) {
+    if constexpr (IS_BF16<T>) {
         const uint4 w = *(const uint4*)((const uint16_t*)base + e0);
         const uint32_t d[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             x[2 * i] = __uint_as_float(d[i] << 16);
             x[2 * i + 1] = __uint_as_float(d[i] & 0xFFFF0000u);
+        }
+    } else if constexpr (IS_F16<T>) {
+        const uint4 w = *(const uint4*)((const uint16_t*)base + e0);
+        const uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = f16_bits_to_f32(d[i] & 0xFFFFu);
+            x[2 * i + 1] = f16_bits_to_f32(d[i] >> 16);
         }
     } else {
         const float4 a = *(const float4*)((const float*)base + e0);
@@ -461,6 +510,7 @@ __device__ __forceinline__ void store8_f32(void* base, int64_t e0, const float (
     p[1] = make_float4(x[4], x[5], x[6], x[7]);
 }
 
+// 8 consecutive 16-bit patterns (bf16 or f16), 16-byte aligned.
 __device__ __forceinline__ void store8_bf16(void* base, int64_t e0, const uint32_t (&h)[8])
 {
     uint4 w;
@@ -482,13 +532,43 @@ __device__ __forceinline__ void load8_u32(const uint32_t* base, int64_t e0, uint
 // Scalar element access with a runtime dtype (generic paths).
 __device__ __forceinline__ float load1(const void* base, int32_t dtype, int64_t e)
 {
-    return dtype == RF_BF16 ? bf16_bits_to_f32(((const uint16_t*)base)[e]) : ((const float*)base)[e];
+    if (dtype == RF_BF16) return bf16_bits_to_f32(((const uint16_t*)base)[e]);
+    if (dtype == RF_F16) return f16_bits_to_f32(((const uint16_t*)base)[e]);
+    return ((const float*)base)[e];
 }
 
+// x rounded to nearest even in a 16-bit dtype, or as is.
 __device__ __forceinline__ void store1(void* base, int32_t dtype, int64_t e, float x)
 {
     if (dtype == RF_BF16) ((uint16_t*)base)[e] = (uint16_t)f32_to_bf16_rne(x);
+    else if (dtype == RF_F16) ((uint16_t*)base)[e] = (uint16_t)f32_to_f16_rne(x);
     else ((float*)base)[e] = x;
+}
+
+// Round x to a param/grad dtype and back (nearest even).
+__device__ __forceinline__ float round_to_dtype(float x, int32_t dtype)
+{
+    if (dtype == RF_BF16) return round_to_bf16(x);
+    if (dtype == RF_F16) return round_to_f16(x);
+    return x;
+}
+
+// Block scales stored as f32, bf16 or f16 (RF_LEAF_SCALE_* flags of the leaf):
+// quantize_blocks computes the scale in f32, codes with it, and stores it as
+// scales.astype(scale_dtype); dequantize_blocks reads f32(stored)
+// (adam8.py:167-186, :202).
+__device__ __forceinline__ float load_scale(const float* scales, uint32_t leaf_flags, int64_t b)
+{
+    if (leaf_flags & RF_LEAF_SCALE_BF16) return bf16_bits_to_f32(((const uint16_t*)scales)[b]);
+    if (leaf_flags & RF_LEAF_SCALE_F16) return f16_bits_to_f32(((const uint16_t*)scales)[b]);
+    return scales[b];
+}
+
+__device__ __forceinline__ void store_scale(float* scales, uint32_t leaf_flags, int64_t b, float s)
+{
+    if (leaf_flags & RF_LEAF_SCALE_BF16) ((uint16_t*)scales)[b] = (uint16_t)f32_to_bf16_rne(s);
+    else if (leaf_flags & RF_LEAF_SCALE_F16) ((uint16_t*)scales)[b] = (uint16_t)f32_to_f16_rne(s);
+    else scales[b] = s;
 }
 
 // Uniform per-unit context.
@@ -499,7 +579,7 @@ struct UnitCtx {
     bool fed;
     bool zero;        // RF_LEAF_ZERO_DECAY of the current leaf (unquantized-moment units)
     bool clip;        // grads are scaled by the global-norm clipping factor
-    float cs, cs16;   // that factor as f32 and rounded to bf16
+    float cs, cs16, csh;  // that factor as f32, rounded to bf16 and rounded to f16
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;  // per-leaf keys
     double* mpart;    // Magma partial sums (KHp::mpart) or null
     int64_t mbase;    // the current leaf's first chunk slot in mpart
@@ -531,24 +611,30 @@ struct MagmaAcc {
 };
 
 // Global-norm clipping of one gradient element (finetune/transforms.py:79-82,
-// leaf * scale.astype(leaf.dtype)): f32 grads multiply in f32; bf16 grads by
-// the bf16-rounded factor, the exact product rounded once to bf16.
-__device__ __forceinline__ float clip1(const UnitCtx& c, float g, bool bf16)
+// leaf * scale.astype(leaf.dtype)): f32 grads multiply in f32; bf16 (f16)
+// grads by the bf16- (f16-) rounded factor, the exact product rounded once
+// to the grad dtype.
+__device__ __forceinline__ float clip1(const UnitCtx& c, float g, int32_t dtype)
 {
-    return bf16 ? round_to_bf16(g * c.cs16) : g * c.cs;
+    if (dtype == RF_BF16) return round_to_bf16(g * c.cs16);
+    if (dtype == RF_F16) return round_to_f16(g * c.csh);
+    return g * c.cs;
 }
 
 template <typename GT>
 __device__ __forceinline__ void clip8(const UnitCtx& c, float (&g)[8])
 {
     if (!c.clip) return;
-    if constexpr (std::is_same<GT, uint16_t>::value) {
+    if constexpr (IS_BF16<GT>) {
 #pragma unroll
         for (int t = 0; t < 8; t += 2) {
             const uint32_t w2 = pack_bf16x2_rne(g[t] * c.cs16, g[t + 1] * c.cs16);
             g[t] = __uint_as_float(w2 << 16);
             g[t + 1] = __uint_as_float(w2 & 0xFFFF0000u);
         }
+    } else if constexpr (IS_F16<GT>) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) g[t] = round_to_f16(g[t] * c.csh);
     } else {
 #pragma unroll
         for (int t = 0; t < 8; ++t) g[t] = g[t] * c.cs;
@@ -559,7 +645,7 @@ __device__ __forceinline__ void clip8(const UnitCtx& c, float (&g)[8])
 __device__ __forceinline__ float load_grad1(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e)
 {
     const float g = load1(L.grad, L.grad_dtype, e);
-    return c.clip ? clip1(c, g, L.grad_dtype == RF_BF16) : g;
+    return c.clip ? clip1(c, g, L.grad_dtype) : g;
 }
 
 // Kernel-start setup of the clipping factor (one scalar load per wave).
@@ -568,9 +654,11 @@ __device__ __forceinline__ void clip_context(UnitCtx& c, const KHp& h)
     c.clip = h.clip != nullptr;
     c.cs = 1.0f;
     c.cs16 = 1.0f;
+    c.csh = 1.0f;
     if (c.clip) {
         c.cs = h.clip[0];
         c.cs16 = round_to_bf16(c.cs);
+        c.csh = round_to_f16(c.cs);
     }
 }
 
@@ -579,9 +667,12 @@ template <bool PSR, typename PT>
 __device__ __forceinline__ uint32_t new_param_bits(float p, float u, uint32_t rbits)
 {
     const float s = p + u;
-    if constexpr (std::is_same<PT, uint16_t>::value) {
+    if constexpr (IS_BF16<PT>) {
         if constexpr (PSR) return sr_bf16(s, rbits);
         else return f32_to_bf16_rne(s);
+    } else if constexpr (IS_F16<PT>) {
+        (void)rbits;  // apply_updates rounds non-bf16 params to nearest (utils.py:700)
+        return f32_to_f16_rne(s);
     } else {
         (void)rbits;
         return __float_as_uint(s);
@@ -607,6 +698,8 @@ __device__ __forceinline__ void update_one(const UnitCtx& c, const rf_adam8_leaf
             uint32_t rb = 0;
             if constexpr (PSR) rb = c.fed ? L.param_bits[e] : jax_bits(c.kp0, c.kp1, (uint64_t)e);
             ((uint16_t*)L.param)[e] = (uint16_t)new_param_bits<PSR, uint16_t>(p, u, rb);
+        } else if (L.param_dtype == RF_F16) {
+            ((uint16_t*)L.param)[e] = (uint16_t)f32_to_f16_rne(p + u);
         } else {
             ((float*)L.param)[e] = p + u;
         }
@@ -658,8 +751,8 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
     const int64_t nvalid = max((int64_t)0, min(bs, L.size - base));
     const float* cbs = (const float*)(c.lds + L_CBS);
     const float* cbu = (const float*)(c.lds + L_CBU);
-    const float sm_old = L.mu_scales[blk];
-    const float sv_old = L.nu_scales[blk];
+    const float sm_old = load_scale(L.mu_scales, L.flags, blk);
+    const float sv_old = load_scale(L.nu_scales, L.flags, blk);
     uint8_t* mcodes = (uint8_t*)L.mu;
     uint8_t* vcodes = (uint8_t*)L.nu;
     uint32_t am = 0, av = 0;
@@ -716,8 +809,8 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
         }
     }
     if (lane == 0) {
-        L.mu_scales[blk] = sm;
-        L.nu_scales[blk] = sv;
+        store_scale(L.mu_scales, L.flags, blk, sm);
+        store_scale(L.nu_scales, L.flags, blk, sv);
     }
 }
 
@@ -759,12 +852,19 @@ __device__ __forceinline__ void raw8_load(Raw8<T>& r, const void* base, int64_t 
 template <typename T>
 __device__ __forceinline__ void raw8_unpack(const Raw8<T>& r, float (&x)[8])
 {
-    if constexpr (sizeof(T) == 2) {
+    if constexpr (IS_BF16<T>) {
         const uint32_t d[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             x[2 * i] = __uint_as_float(d[i] << 16);
             x[2 * i + 1] = __uint_as_float(d[i] & 0xFFFF0000u);
+        }
+    } else if constexpr (IS_F16<T>) {
+        const uint32_t d[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = f16_bits_to_f32(d[i] & 0xFFFFu);
+            x[2 * i + 1] = f16_bits_to_f32(d[i] >> 16);
         }
     } else {
         const uint32_t d[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
@@ -784,6 +884,9 @@ __device__ __forceinline__ void decay_and_scale8(const KHp& h, float (&u)[8], co
             u[t] = u[t] + __uint_as_float(w2 << 16);
             u[t + 1] = u[t + 1] + __uint_as_float(w2 & 0xFFFF0000u);
         }
+    } else if constexpr (WDM == WD_F16) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) u[t] = u[t] + round_to_f16(h.wdh * p[t]);
     } else if constexpr (WDM == WD_F32) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -846,11 +949,11 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
 {
     constexpr int J = FAST_BS / 512;
     constexpr bool NEED_P = APPLY || WDM != WD_OFF;
-    constexpr bool BF16P = std::is_same<PT, uint16_t>::value;
+    constexpr bool H16P = sizeof(PT) == 2;  // bf16 or f16 params
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t base = blk * FAST_BS;
-    const float sm_old = L.mu_scales[blk];
-    const float sv_old = L.nu_scales[blk];
+    const float sm_old = load_scale(L.mu_scales, L.flags, blk);
+    const float sv_old = load_scale(L.nu_scales, L.flags, blk);
     RF_GLOBAL uint8_t* pB = (RF_GLOBAL uint8_t*)L.param + base * (int64_t)sizeof(PT);
 
     // Chunk j+1's loads are issued before chunk j's arithmetic: two chunks
@@ -939,14 +1042,14 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                     }
                 }
             }
-            if constexpr (BF16P) {
+            if constexpr (H16P) {
                 uint32_t w[4];
-                if constexpr (PSR) {
+                if constexpr (PSR && IS_BF16<PT>) {
 #pragma unroll
                     for (int t = 0; t < 8; t += 2) w[t / 2] = sr_bf16(sum[t], rb[t]) | (sr_bf16(sum[t + 1], rb[t + 1]) << 16);
                 } else {
 #pragma unroll
-                    for (int t = 0; t < 8; t += 2) w[t / 2] = pack_bf16x2_rne(sum[t], sum[t + 1]);
+                    for (int t = 0; t < 8; t += 2) w[t / 2] = pack_h16x2_rne<PT>(sum[t], sum[t + 1]);
                 }
                 *(RF_GLOBAL uint4*)(pB + eo * 2) = make_uint4(w[0], w[1], w[2], w[3]);
             } else {
@@ -1040,8 +1143,8 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             *(RF_GLOBAL uint2*)(vW + eo) = wv;
         }
         if (lane == 0) {
-            L.mu_scales[blk] = sm;
-            L.nu_scales[blk] = sv;
+            store_scale(L.mu_scales, L.flags, blk, sm);
+            store_scale(L.nu_scales, L.flags, blk, sv);
         }
     } else {
         requant_literal<MSR, 1>(c, L, blk, h);
@@ -1055,9 +1158,15 @@ __device__ __forceinline__ void dispatch_qfast(const UnitCtx& c, const rf_adam8_
                                                ChunkSlots<PT, GT>& sl, bool have0, int64_t next_blk)
 {
     const int32_t wdm = c.wd_mode;
-    if constexpr (std::is_same<PT, uint16_t>::value) {
+    if constexpr (IS_BF16<PT>) {
         if (wdm == WD_BF16) {
             unit_qfast<PT, GT, WD_BF16, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h, sl, have0, next_blk);
+            return;
+        }
+    }
+    if constexpr (IS_F16<PT>) {
+        if (wdm == WD_F16) {
+            unit_qfast<PT, GT, WD_F16, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h, sl, have0, next_blk);
             return;
         }
     }
@@ -1078,8 +1187,8 @@ __device__ __forceinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf&
     const int64_t nvalid = max((int64_t)0, min(bs, L.size - base));
     const float* cbs = (const float*)(c.lds + L_CBS);
     const float* cbu = (const float*)(c.lds + L_CBU);
-    const float sm_old = L.mu_scales[blk];
-    const float sv_old = L.nu_scales[blk];
+    const float sm_old = load_scale(L.mu_scales, L.flags, blk);
+    const float sv_old = load_scale(L.nu_scales, L.flags, blk);
 
     const bool need_p = APPLY || c.wd_mode != WD_OFF;
     for (int64_t j0 = lane; j0 < nvalid; j0 += EW_BATCH * WAVE) {
@@ -1113,7 +1222,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t base = chunk * CHUNK;
     const int64_t end = min(base + CHUNK, L.size);
-    const int32_t mdt = L.moment_kind == RF_MOMENT_BF16 ? RF_BF16 : RF_F32;
+    const int32_t mdt = L.moment_kind == RF_MOMENT_BF16 ? RF_BF16 : (L.moment_kind == RF_MOMENT_F16 ? RF_F16 : RF_F32);
     const bool store_sr = mdt == RF_BF16 && (L.flags & RF_LEAF_STORE_SR);
     const bool need_p = APPLY || c.wd_mode != WD_OFF || c.zero;
     const bool msum = !APPLY && c.mpart != nullptr;  // Magma sums: update-only launches
@@ -1164,7 +1273,8 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
                                                   const KHp& h)
 {
     constexpr int J = (int)(CHUNK / 512);
-    constexpr bool BF16M = std::is_same<MT, uint16_t>::value;
+    constexpr bool BF16M = IS_BF16<MT>;
+    constexpr bool H16M = sizeof(MT) == 2;  // bf16 or f16 moments
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t base = chunk * CHUNK;
     const int32_t wdm = c.wd_mode;
@@ -1225,9 +1335,9 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
                     }
                 }
             }
-            if constexpr (std::is_same<PT, uint16_t>::value) {
+            if constexpr (sizeof(PT) == 2) {
                 uint32_t hb[8];
-                if constexpr (PSR) {
+                if constexpr (PSR && IS_BF16<PT>) {
 #pragma unroll
                     for (int t = 0; t < 8; ++t) {
                         const uint32_t rb = c.fed ? L.param_bits[e0 + t] : jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
@@ -1236,7 +1346,7 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
                 } else {
 #pragma unroll
                     for (int t = 0; t < 8; t += 2) {
-                        const uint32_t w2 = pack_bf16x2_rne(sum[t], sum[t + 1]);
+                        const uint32_t w2 = pack_h16x2_rne<PT>(sum[t], sum[t + 1]);
                         hb[t] = w2 & 0xFFFFu;
                         hb[t + 1] = w2 >> 16;
                     }
@@ -1249,9 +1359,9 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
             store8_f32(L.updates, e0, u);
         }
         // adam8.py:688 moment.astype(fallback_dtype) / optim/adam.py:219-222 SR storage
-        if constexpr (BF16M) {
+        if constexpr (H16M) {
             uint32_t hm[8], hv[8];
-            if (store_sr) {
+            if (BF16M && store_sr) {
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
                     const uint64_t e = (uint64_t)(e0 + t);
@@ -1263,8 +1373,8 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
             } else {
 #pragma unroll
                 for (int t = 0; t < 8; t += 2) {
-                    const uint32_t wm = pack_bf16x2_rne(m[t], m[t + 1]);
-                    const uint32_t wv = pack_bf16x2_rne(v[t], v[t + 1]);
+                    const uint32_t wm = pack_h16x2_rne<MT>(m[t], m[t + 1]);
+                    const uint32_t wv = pack_h16x2_rne<MT>(v[t], v[t + 1]);
                     hm[t] = wm & 0xFFFFu;
                     hm[t + 1] = wm >> 16;
                     hv[t] = wv & 0xFFFFu;
@@ -1287,13 +1397,25 @@ __device__ __forceinline__ void dispatch_fallback_vec(const UnitCtx& c, const rf
 {
     // Vectorised instances for params and grads of one dtype; other mixes
     // take the element-wise unit (same arithmetic).
-    const int sel = (L.param_dtype == RF_BF16 ? 4 : 0) | (L.grad_dtype == RF_BF16 ? 2 : 0) |
-                    (L.moment_kind == RF_MOMENT_BF16 ? 1 : 0);
+    // (param dtype, grad dtype, moment dtype) in base 4 (RF_F32/RF_BF16/RF_F16; moments by kind)
+    const int32_t mk = L.moment_kind == RF_MOMENT_BF16 ? RF_BF16 : (L.moment_kind == RF_MOMENT_F16 ? RF_F16 : RF_F32);
+    const int sel = L.param_dtype * 16 + L.grad_dtype * 4 + mk;
+    constexpr int F = RF_F32 * 20, B = RF_BF16 * 20, H = RF_F16 * 20;  // params and grads of one dtype
     switch (sel) {
-    case 0: unit_fallback_vec<float, float, float, APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
-    case 1: unit_fallback_vec<float, float, uint16_t, APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
-    case 6: unit_fallback_vec<uint16_t, uint16_t, float, APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
-    case 7: unit_fallback_vec<uint16_t, uint16_t, uint16_t, APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
+    case F + RF_F32: unit_fallback_vec<float, float, float, APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
+    case F + RF_BF16: unit_fallback_vec<float, float, uint16_t, APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
+    case B + RF_F32:
+        unit_fallback_vec<uint16_t, uint16_t, float, APPLY, PSR, NEST, EXACT>(c, L, chunk, h);
+        break;
+    case B + RF_BF16:
+        unit_fallback_vec<uint16_t, uint16_t, uint16_t, APPLY, PSR, NEST, EXACT>(c, L, chunk, h);
+        break;
+    case H + RF_F32:
+        unit_fallback_vec<_Float16, _Float16, float, APPLY, PSR, NEST, EXACT>(c, L, chunk, h);
+        break;
+    case H + RF_F16:
+        unit_fallback_vec<_Float16, _Float16, _Float16, APPLY, PSR, NEST, EXACT>(c, L, chunk, h);
+        break;
     default: unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
     }
 }
@@ -1309,6 +1431,7 @@ __device__ __forceinline__ void group_hparams(KHp& hl, const KHp& h, const rf_ad
     hl.neg_lr = (h.flags & RF_LR) ? G.neg_lr : 1.0f;
     hl.wd = G.weight_decay;
     hl.wd16 = round_to_bf16(G.weight_decay);
+    hl.wdh = round_to_f16(G.weight_decay);
     hl.omb1 = G.one_minus_b1;
     hl.kmu0 = G.key_mu[0];
     hl.kmu1 = G.key_mu[1];
@@ -1319,7 +1442,10 @@ __device__ __forceinline__ void group_hparams(KHp& hl, const KHp& h, const rf_ad
 __device__ __forceinline__ void leaf_context(UnitCtx& c, const rf_adam8_leaf& L, const KHp& h, bool msr, bool psr)
 {
     const bool decay = (L.flags & RF_LEAF_DECAY) != 0;
-    c.wd_mode = !decay ? WD_OFF : ((L.param_dtype == RF_BF16 && (h.flags & RF_DECAY_WEAK)) ? WD_BF16 : WD_F32);
+    const bool weak = (h.flags & RF_DECAY_WEAK) != 0;
+    c.wd_mode = !decay ? WD_OFF
+                       : (weak && L.param_dtype == RF_BF16) ? WD_BF16
+                       : (weak && L.param_dtype == RF_F16) ? WD_F16 : WD_F32;
     c.zero = (L.flags & RF_LEAF_ZERO_DECAY) != 0;
     if (msr || (L.flags & RF_LEAF_STORE_SR)) {
         jax_split(h.kmu0, h.kmu1, (uint32_t)L.state_index, c.kmu0, c.kmu1);
@@ -1350,10 +1476,7 @@ __device__ void reject_units(const rf_adam8_leaf* __restrict__ leaves, const Seg
         const int64_t end = min(base + span, L.size);
         for (int64_t e = base + lane; e < end; e += WAVE) {
             if constexpr (APPLY) {
-                if (L.param_dtype == RF_BF16)
-                    ((uint16_t*)L.param)[e] = (uint16_t)sr_bf16(load1(L.param, RF_BF16, e) + 0.0f, 0u);
-                else
-                    ((float*)L.param)[e] = ((const float*)L.param)[e] + 0.0f;
+                store1(L.param, L.param_dtype, e, load1(L.param, L.param_dtype, e) + 0.0f);
             } else {
                 L.updates[e] = 0.0f;
             }

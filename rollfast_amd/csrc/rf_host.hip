@@ -49,13 +49,22 @@ adam_kernel_t rf_pick_adam8_a1_m1_e1(int dtype_combo, bool psr, bool nest);
 }  // namespace rf
 
 // ====================================================== standalone kernels ==
+// 8 consecutive elements of an f32, bf16 or f16 array as f32 (16-byte aligned).
+__device__ __forceinline__ void load8_dt(const void* base, int32_t dtype, int64_t e0, float (&x)[8])
+{
+    if (dtype == RF_BF16) load8<uint16_t>(base, e0, x);
+    else if (dtype == RF_F16) load8<_Float16>(base, e0, x);
+    else load8<float>(base, e0, x);
+}
+
 // Standalone quantize_blocks (adam8.py:113-187): one wave per block.  Fast
 // path: 2048-element aligned blocks held in registers; otherwise two passes.
-__global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const float* __restrict__ x, int64_t size,
-                                                 int64_t bs, int64_t nblocks, int32_t sr, uint32_t k0,
+__global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const void* __restrict__ x, int32_t x_dtype,
+                                                 int64_t size, int64_t bs, int64_t nblocks, int32_t sr, uint32_t k0,
                                                  uint32_t k1, const uint32_t* __restrict__ bits,
-                                                 uint8_t* __restrict__ values, float* __restrict__ scales,
-                                                 const uint4* __restrict__ tables, int32_t vec_ok)
+                                                 uint8_t* __restrict__ values, void* __restrict__ scales,
+                                                 int32_t scale_dtype, const uint4* __restrict__ tables,
+                                                 int32_t vec_ok)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
     stage_tables(lds, tables);
@@ -68,7 +77,7 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const float*
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             float t8[8];
-            load8<float>(x, b * FAST_BS + j * 512 + lane * 8, t8);
+            load8_dt(x, x_dtype, b * FAST_BS + j * 512 + lane * 8, t8);
 #pragma unroll
             for (int t = 0; t < 8; ++t) r[j * 8 + t] = t8[t];
         }
@@ -87,14 +96,15 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const float*
 #pragma unroll
             for (int i = 0; i < 32; ++i) am = max(am, __float_as_uint(xr[i]) & 0x7FFFFFFFu);
         } else {
-            for (int64_t j = lane; j < nvalid; j += WAVE) am = max(am, __float_as_uint(x[base + j]) & 0x7FFFFFFFu);
+            for (int64_t j = lane; j < nvalid; j += WAVE)
+                am = max(am, __float_as_uint(load1(x, x_dtype, base + j)) & 0x7FFFFFFFu);
         }
         am = wave_max_u32(am);
         const float amax = __uint_as_float(am);
         float scale;
         if (quantizer == RF_Q_SYMMETRIC_INT8) scale = amax > 0.0f ? amax / 127.0f : 1.0f;
         else scale = amax > 0.0f ? amax : 1.0f;
-        if (lane == 0) scales[b] = scale;
+        if (lane == 0) store1(scales, scale_dtype, b, scale);  // scales.astype(scale_dtype) (adam8.py:186)
         const bool fast = !sr && quantizer != RF_Q_SYMMETRIC_INT8 && block_is_fast(am, scale);
         const float rs = 1.0f / scale;
         auto code_of = [&](float xv, int64_t e) -> uint32_t {
@@ -162,7 +172,7 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const float*
             have = false;
             for (int64_t j = lane; j < bs; j += WAVE) {
                 const int64_t e = base + j;
-                const float xv = j < nvalid ? x[e] : 0.0f;
+                const float xv = j < nvalid ? load1(x, x_dtype, e) : 0.0f;
                 values[e] = (uint8_t)code_of(xv, e);
             }
         }
@@ -182,13 +192,19 @@ __device__ __forceinline__ void dq_store4(void* out, int32_t out_dtype, int64_t 
         w.x = f32_to_bf16_rne(o[0]) | (f32_to_bf16_rne(o[1]) << 16);
         w.y = f32_to_bf16_rne(o[2]) | (f32_to_bf16_rne(o[3]) << 16);
         *(uint2*)((uint16_t*)out + e) = w;
+    } else if (out_dtype == RF_F16) {
+        uint2 w;
+        w.x = pack_f16x2_rne(o[0], o[1]);
+        w.y = pack_f16x2_rne(o[2], o[3]);
+        *(uint2*)((uint16_t*)out + e) = w;
     } else {
         *(float4*)((float*)out + e) = make_float4(o[0], o[1], o[2], o[3]);
     }
 }
 
 __global__ __launch_bounds__(WG) void k_dequantize(int32_t quantizer, const uint8_t* __restrict__ values,
-                                                   const float* __restrict__ scales, int64_t size, int64_t bs,
+                                                   const void* __restrict__ scales, int32_t scale_dtype,
+                                                   int64_t size, int64_t bs,
                                                    int32_t bs_log2, int32_t out_dtype, void* __restrict__ out,
                                                    const uint4* __restrict__ tables, int32_t vec_ok)
 {
@@ -212,7 +228,7 @@ __global__ __launch_bounds__(WG) void k_dequantize(int32_t quantizer, const uint
                 const int64_t e = (t0 + u) * 1024 + k * 256 + lane * 4;
                 if (t0 + u < ntiles) {
                     w[u][k] = *(const uint32_t*)(values + e);
-                    s[u][k] = scales[e >> bs_log2];  // the 4 elements share a block (bs >= 4)
+                    s[u][k] = load1(scales, scale_dtype, e >> bs_log2);  // the 4 elements share a block (bs >= 4)
                 }
             }
         }
@@ -238,7 +254,7 @@ __global__ __launch_bounds__(WG) void k_dequantize(int32_t quantizer, const uint
     for (int64_t e = ntiles * 1024 + tid; e < size; e += nthreads) {
         const uint32_t cbyte = values[e];
         const float val = sym ? (float)(int8_t)cbyte : cb[cbyte];
-        store1(out, out_dtype, e, val * scales[e / bs]);
+        store1(out, out_dtype, e, val * load1(scales, scale_dtype, e / bs));
     }
 }
 
@@ -306,7 +322,13 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
 #pragma unroll
             for (int t = 0; t < 8; ++t) u[t] = neg_lr * (f * u[t]);
         }
-        if (L.param_dtype == RF_BF16) {
+        if (L.param_dtype == RF_F16) {
+            load8<_Float16>(L.param, e0, p);
+            uint32_t h[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) h[t] = f32_to_f16_rne(p[t] + u[t]);  // no SR below bf16 (utils.py:700)
+            store8_bf16(L.param, e0, h);
+        } else if (L.param_dtype == RF_BF16) {
             load8<uint16_t>(L.param, e0, p);
             uint32_t h[8];
             if (sr && L.bits) {
@@ -328,7 +350,10 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
     }
     for (int64_t e = ngroups * 8 + tid; e < L.size; e += nthreads) {
         const float u = factor ? neg_lr * (f * L.updates[e]) : L.updates[e];
-        if (L.param_dtype == RF_BF16) {
+        if (L.param_dtype == RF_F16) {
+            const float p = f16_bits_to_f32(((const uint16_t*)L.param)[e]);
+            ((uint16_t*)L.param)[e] = (uint16_t)f32_to_f16_rne(p + u);
+        } else if (L.param_dtype == RF_BF16) {
             const float p = bf16_bits_to_f32(((const uint16_t*)L.param)[e]);
             ((uint16_t*)L.param)[e] = (uint16_t)apply_bf16(p, u, sr, L.bits, lk0, lk1, e);
         } else {
@@ -377,11 +402,11 @@ __global__ __launch_bounds__(WG) void k_gnorm_partial(const rf_adam8_leaf* __res
         const int64_t e_begin = (u - sg.unit_start) * NORM_UNIT;
         const int64_t e_end = min(L.size, e_begin + NORM_UNIT);
         double acc = 0.0;
-        const bool bf16 = L.grad_dtype == RF_BF16;
         if (e_end - e_begin == NORM_UNIT && ((uintptr_t)L.grad & 15u) == 0) {
             for (int64_t e0 = e_begin + lane * 8; e0 < e_end; e0 += 512) {
                 float x[8];
-                if (bf16) load8<uint16_t>(L.grad, e0, x);
+                if (L.grad_dtype == RF_BF16) load8<uint16_t>(L.grad, e0, x);
+                else if (L.grad_dtype == RF_F16) load8<_Float16>(L.grad, e0, x);
                 else load8<float>(L.grad, e0, x);
 #pragma unroll
                 for (int t = 0; t < 8; ++t) acc += (double)x[t] * (double)x[t];
@@ -445,12 +470,6 @@ __global__ void k_gnorm_finish(const double* __restrict__ leafsum, int32_t nseg,
 // leaf; every leaf has a segment (empty leaves an empty one), so segment i is
 // leaf i.
 
-// 8 consecutive elements of a bf16 or f32 array as f32 (16-byte aligned).
-__device__ __forceinline__ void load8_dt(const void* base, int32_t dtype, int64_t e0, float (&x)[8])
-{
-    if (dtype == RF_BF16) load8<uint16_t>(base, e0, x);
-    else load8<float>(base, e0, x);
-}
 
 // Per-unit f64 partial sums of g*m', g*g and m'*m', m' = f32(b1*mu) +
 // f32(omb1*g): the step's new first moment (utils.py:437-467).
@@ -616,6 +635,7 @@ __global__ __launch_bounds__(WG) void k_clip_scale(const rf_clip_leaf* __restric
     const rf_clip_leaf L = leaves[blockIdx.y];
     const float cs = clip[0];
     const float cs16 = round_to_bf16(cs);
+    const float csh = round_to_f16(cs);
     const int64_t tid = (int64_t)blockIdx.x * WG + threadIdx.x;
     const int64_t nthreads = (int64_t)gridDim.x * WG;
     const bool bf16 = L.dtype == RF_BF16;
@@ -624,7 +644,13 @@ __global__ __launch_bounds__(WG) void k_clip_scale(const rf_clip_leaf* __restric
     for (int64_t gi = tid; gi < ngroups; gi += nthreads) {
         const int64_t e0 = gi * 8;
         float x[8];
-        if (bf16) {
+        if (L.dtype == RF_F16) {
+            load8<_Float16>(L.grad, e0, x);
+            uint32_t hb[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) hb[t] = f32_to_f16_rne(x[t] * csh);
+            store8_bf16(L.out, e0, hb);
+        } else if (bf16) {
             load8<uint16_t>(L.grad, e0, x);
             uint32_t hb[8];
 #pragma unroll
@@ -642,7 +668,9 @@ __global__ __launch_bounds__(WG) void k_clip_scale(const rf_clip_leaf* __restric
         }
     }
     for (int64_t e = ngroups * 8 + tid; e < L.size; e += nthreads) {
-        if (bf16) {
+        if (L.dtype == RF_F16) {
+            ((uint16_t*)L.out)[e] = (uint16_t)f32_to_f16_rne(f16_bits_to_f32(((const uint16_t*)L.grad)[e]) * csh);
+        } else if (bf16) {
             ((uint16_t*)L.out)[e] = (uint16_t)f32_to_bf16_rne(bf16_bits_to_f32(((const uint16_t*)L.grad)[e]) * cs16);
         } else {
             ((float*)L.out)[e] = ((const float*)L.grad)[e] * cs;
@@ -950,8 +978,12 @@ rf_status device_state(DevState** out)
 
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+inline bool valid_dtype(int32_t d) { return d == RF_F32 || d == RF_BF16 || d == RF_F16; }
+
 // ---- kernel selection ----
-// dtype_combo = 2*(param is bf16) + (grad is bf16)
+// The fast kernel's instances: dtype_combo = 2*(param is bf16) + (grad is bf16)
+// for f32/bf16 params and grads, COMBO_F16 for f16 params and grads; -1 (the
+// generic kernel) for the other mixes.
 adam_kernel_t pick_adam_kernel(bool apply, bool msr, bool psr, bool nest, bool exact, int combo)
 {
     if (apply) {
@@ -962,8 +994,13 @@ adam_kernel_t pick_adam_kernel(bool apply, bool msr, bool psr, bool nest, bool e
     return exact ? rf_pick_adam8_a0_m0_e1(combo, false, nest) : rf_pick_adam8_a0_m0_e0(combo, false, nest);
 }
 
+constexpr int COMBO_F16 = 4;
+constexpr int GEN_LIST = 5;  // the generic kernel's work list
+
 inline int dtype_combo(const rf_adam8_leaf& L)
 {
+    if (L.param_dtype == RF_F16 || L.grad_dtype == RF_F16)
+        return L.param_dtype == RF_F16 && L.grad_dtype == RF_F16 ? COMBO_F16 : -1;
     return 2 * (L.param_dtype == RF_BF16 ? 1 : 0) + (L.grad_dtype == RF_BF16 ? 1 : 0);
 }
 
@@ -1029,7 +1066,7 @@ static BitsCover bits_cover(const rf_adam8_leaf* leaves, int32_t n)
         const rf_adam8_leaf& L = leaves[i];
         if (L.size == 0) continue;
         const bool mb = L.mu_bits != nullptr && L.nu_bits != nullptr;
-        if (!L.param_bits) c.pb = false;
+        if (!L.param_bits && L.param_dtype == RF_BF16) c.pb = false;  // SR rounds bf16 params only
         if (L.moment_kind == RF_MOMENT_QUANTIZED && !mb) c.mb_quant = false;
         if (L.moment_kind == RF_MOMENT_BF16 && (L.flags & RF_LEAF_STORE_SR) && !mb) c.mb_store = false;
     }
@@ -1086,9 +1123,13 @@ rf_status validate_leaf(const rf_adam8_leaf& L, int32_t i, int32_t apply)
 {
     const std::string at = "leaf " + std::to_string(i) + ": ";
     if (L.size < 0) return fail(RF_ERR_INVALID, at + "negative size");
-    if (L.param_dtype != RF_F32 && L.param_dtype != RF_BF16) return fail(RF_ERR_UNSUPPORTED, at + "param dtype must be f32 or bf16");
-    if (L.grad_dtype != RF_F32 && L.grad_dtype != RF_BF16) return fail(RF_ERR_UNSUPPORTED, at + "grad dtype must be f32 or bf16");
-    if (L.moment_kind < RF_MOMENT_QUANTIZED || L.moment_kind > RF_MOMENT_BF16) return fail(RF_ERR_INVALID, at + "bad moment kind");
+    if (!valid_dtype(L.param_dtype)) return fail(RF_ERR_UNSUPPORTED, at + "param dtype must be f32, bf16 or f16");
+    if (!valid_dtype(L.grad_dtype)) return fail(RF_ERR_UNSUPPORTED, at + "grad dtype must be f32, bf16 or f16");
+    if (L.moment_kind < RF_MOMENT_QUANTIZED || L.moment_kind > RF_MOMENT_F16) return fail(RF_ERR_INVALID, at + "bad moment kind");
+    if ((L.flags & RF_LEAF_SCALE_BF16) && (L.flags & RF_LEAF_SCALE_F16))
+        return fail(RF_ERR_INVALID, at + "RF_LEAF_SCALE_BF16 and RF_LEAF_SCALE_F16 together");
+    if ((L.flags & (RF_LEAF_SCALE_BF16 | RF_LEAF_SCALE_F16)) && L.moment_kind != RF_MOMENT_QUANTIZED)
+        return fail(RF_ERR_INVALID, at + "a scale dtype flag on unquantized moments");
     if (L.size > 0 && !L.grad) return fail(RF_ERR_INVALID, at + "null grad");
     if (L.size > 0 && !L.param && (apply || (L.flags & (RF_LEAF_DECAY | RF_LEAF_ZERO_DECAY))))
         return fail(RF_ERR_INVALID, at + "null param");
@@ -1145,15 +1186,15 @@ struct WorkLists {
     std::vector<Seg> msegs;          // Magma chunk slots (every leaf unquantized), else empty
     int64_t mchunks = -1;
     std::vector<uint8_t> vecs;       // leaf has 16-byte aligned (vectorised) units
-    std::vector<Seg> gsegs[5];       // build space: the lists of each dtype combination
+    std::vector<Seg> gsegs[6];       // build space: the lists of each dtype combination and the generic one
 };
 
 rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply, WorkLists& w)
 {
     rf_status st = RF_OK;
     std::vector<Seg>* gsegs = w.gsegs;
-    for (int c = 0; c < 5; ++c) gsegs[c].clear();
-    int64_t gunits[5] = {0, 0, 0, 0, 0};
+    for (int c = 0; c <= GEN_LIST; ++c) gsegs[c].clear();
+    int64_t gunits[GEN_LIST + 1] = {0, 0, 0, 0, 0, 0};
     auto add = [&](int32_t leaf, int combo, int32_t kind, int64_t first, int64_t count) {
         if (count <= 0) return;
         Seg sg{};
@@ -1173,24 +1214,24 @@ rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_
         const bool vec = leaf_vec_ok(L, apply);
         vecs.push_back(vec ? 1 : 0);
         // Full aligned 2048-blocks go to the fast kernel of their dtype
-        // combination; everything else to the generic kernel (group 4).
+        // combination; everything else to the generic kernel (GEN_LIST).
         const int combo = dtype_combo(L);
         if (L.moment_kind == RF_MOMENT_QUANTIZED) {
             const int64_t bs = L.block_size;
             const int64_t nb = nblocks_of(L.size, bs);
-            if (bs == FAST_BS && vec) {
+            if (bs == FAST_BS && vec && combo >= 0) {
                 const int64_t nfull = L.size / bs;
                 add(i, combo, KIND_QFAST, 0, nfull);
-                add(i, 4, KIND_QGEN, nfull, nb - nfull);
+                add(i, GEN_LIST, KIND_QGEN, nfull, nb - nfull);
             } else {
-                add(i, 4, KIND_QGEN, 0, nb);
+                add(i, GEN_LIST, KIND_QGEN, 0, nb);
             }
         } else {
             // Full chunks of aligned leaves take the vectorised unit, the
             // tail the element-wise one.
             const int64_t nfull = vec ? L.size / CHUNK : 0;
-            add(i, 4, KIND_FALLBACK_VEC, 0, nfull);
-            add(i, 4, KIND_FALLBACK, nfull, (L.size - nfull * CHUNK + CHUNK - 1) / CHUNK);
+            add(i, GEN_LIST, KIND_FALLBACK_VEC, 0, nfull);
+            add(i, GEN_LIST, KIND_FALLBACK, nfull, (L.size - nfull * CHUNK + CHUNK - 1) / CHUNK);
         }
     }
     std::vector<Seg>& segs = w.segs;
@@ -1198,9 +1239,9 @@ rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_
     segs.clear();
     groups.clear();
     int64_t units = 0;
-    for (int combo = 4; combo >= 0; --combo) {
+    for (int combo = GEN_LIST; combo >= 0; --combo) {
         if (gunits[combo] == 0) continue;
-        groups.push_back({combo == 4 ? -1 : combo, (int64_t)segs.size(), gunits[combo]});
+        groups.push_back({combo == GEN_LIST ? -1 : combo, (int64_t)segs.size(), gunits[combo]});
         Seg sentinel{};
         sentinel.unit_start = gunits[combo];
         sentinel.leaf = -1;
@@ -1488,6 +1529,8 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         if (std::isnan(hp->weight_decay)) u = (u & 0x80000000u) | 0x7FC00000u;
         else u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
         k.wd16 = bitsf(u);
+        // f16(wd), round to nearest even: the weak-typed decay of f16 params
+        k.wdh = (float)(_Float16)hp->weight_decay;
     }
     k.neg_lr = (f & RF_LR) ? hp->neg_lr : 1.0f;
     k.flags = f;
@@ -1756,12 +1799,14 @@ rf_status rf_adam8_step_noalloc(const rf_adam8_leaf* leaves, int32_t n_leaves, i
     return st;
 }
 
-rf_status rf_blockwise_quantize(int32_t quantizer, const float* x, int64_t size, int32_t block_size, int32_t sr,
-                                uint32_t key0, uint32_t key1, const uint32_t* bits, void* values, float* scales,
-                                void* stream)
+rf_status rf_blockwise_quantize(int32_t quantizer, const void* x, int32_t x_dtype, int64_t size, int32_t block_size,
+                                int32_t sr, uint32_t key0, uint32_t key1, const uint32_t* bits, void* values,
+                                void* scales, int32_t scale_dtype, void* stream)
 {
     if (quantizer < RF_Q_DYNAMIC_SIGNED || quantizer > RF_Q_SYMMETRIC_INT8) return fail(RF_ERR_INVALID, "unknown quantizer");
     if (block_size <= 0) return fail(RF_ERR_INVALID, "block_size must be positive.");
+    if (!valid_dtype(x_dtype) || !valid_dtype(scale_dtype))
+        return fail(RF_ERR_UNSUPPORTED, "input and scale dtypes must be f32, bf16 or f16");
     if (size < 0) return fail(RF_ERR_INVALID, "negative size");
     if ((size > 0 && !x) || !values || !scales) return fail(RF_ERR_INVALID, "null buffer");
     DevState* ds = nullptr;
@@ -1776,18 +1821,20 @@ rf_status rf_blockwise_quantize(int32_t quantizer, const float* x, int64_t size,
     const int64_t wg_spread = (wg_needed + STEP_UNITS_PER_WAVE - 1) / STEP_UNITS_PER_WAVE;
     const int grid = (int)std::max<int64_t>(1, std::max(std::min(wg_needed, (int64_t)ds->num_cus * occ), wg_spread));
     const int32_t vec_ok = aligned(x, 16) && aligned(values, 8) && (!bits || aligned(bits, 16));
-    hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(WG), 0, (hipStream_t)stream, quantizer, x, size,
-                       (int64_t)block_size, nb, sr, key0, key1, bits, (uint8_t*)values, scales, ds->tables, vec_ok);
+    hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(WG), 0, (hipStream_t)stream, quantizer, x, x_dtype, size,
+                       (int64_t)block_size, nb, sr, key0, key1, bits, (uint8_t*)values, scales, scale_dtype,
+                       ds->tables, vec_ok);
     HIP_TRY(hipGetLastError());
     return RF_OK;
 }
 
-rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const float* scales, int64_t size,
-                                  int32_t block_size, int32_t out_dtype, void* out, void* stream)
+rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const void* scales, int32_t scale_dtype,
+                                  int64_t size, int32_t block_size, int32_t out_dtype, void* out, void* stream)
 {
     if (quantizer < RF_Q_DYNAMIC_SIGNED || quantizer > RF_Q_SYMMETRIC_INT8) return fail(RF_ERR_INVALID, "unknown quantizer");
     if (block_size <= 0) return fail(RF_ERR_INVALID, "block_size must be positive.");
-    if (out_dtype != RF_F32 && out_dtype != RF_BF16) return fail(RF_ERR_UNSUPPORTED, "out dtype must be f32 or bf16");
+    if (!valid_dtype(out_dtype) || !valid_dtype(scale_dtype))
+        return fail(RF_ERR_UNSUPPORTED, "out and scale dtypes must be f32, bf16 or f16");
     if (size < 0) return fail(RF_ERR_INVALID, "negative size");
     if (size == 0) return RF_OK;
     if (!values || !scales || !out) return fail(RF_ERR_INVALID, "null buffer");
@@ -1797,7 +1844,7 @@ rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const f
     const bool pow2 = block_size >= 4 && (block_size & (block_size - 1)) == 0;
     int32_t bs_log2 = 0;
     while (pow2 && (1 << bs_log2) < block_size) ++bs_log2;
-    const int32_t vec_ok = pow2 && aligned(values, 4) && aligned(out, out_dtype == RF_BF16 ? 8 : 16);
+    const int32_t vec_ok = pow2 && aligned(values, 4) && aligned(out, out_dtype == RF_F32 ? 16 : 8);
     // Vector path: one wave per two 1024-element tiles, at most 8 waves' worth
     // of workgroups per CU; the scalar tail needs few threads.
     const int64_t tiles = vec_ok ? size / 1024 : 0;
@@ -1805,8 +1852,8 @@ rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const f
     const int grid = (int)std::min<int64_t>(std::max<int64_t>(wg_needed, vec_ok ? 1 : (size + WG - 1) / WG),
                                             (int64_t)ds->num_cus * 8);
     hipLaunchKernelGGL(k_dequantize, dim3(grid), dim3(WG), 0, (hipStream_t)stream, quantizer,
-                       (const uint8_t*)values, scales, size, (int64_t)block_size, bs_log2, out_dtype, out,
-                       ds->tables, vec_ok);
+                       (const uint8_t*)values, scales, scale_dtype, size, (int64_t)block_size, bs_log2, out_dtype,
+                       out, ds->tables, vec_ok);
     HIP_TRY(hipGetLastError());
     return RF_OK;
 }
@@ -1843,7 +1890,7 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
     for (int32_t i = 0; i < n_leaves; ++i) {
         const rf_clip_leaf& L = leaves[i];
         if (L.size < 0) return fail(RF_ERR_INVALID, "negative size");
-        if (L.dtype != RF_F32 && L.dtype != RF_BF16) return fail(RF_ERR_UNSUPPORTED, "dtype must be f32 or bf16");
+        if (!valid_dtype(L.dtype)) return fail(RF_ERR_UNSUPPORTED, "dtype must be f32, bf16 or f16");
         if (L.size > 0 && (!L.grad || !L.out)) return fail(RF_ERR_INVALID, "null buffer");
         gl[i] = rf_adam8_leaf{};
         gl[i].grad = L.grad;
@@ -1937,8 +1984,8 @@ rf_status magma_list(const rf_magma_leaf* leaves, int32_t n_leaves, bool need_up
     for (int32_t i = 0; i < n_leaves; ++i) {
         const rf_magma_leaf& L = leaves[i];
         if (L.size < 0) return fail(RF_ERR_INVALID, "negative size");
-        if ((L.grad_dtype != RF_F32 && L.grad_dtype != RF_BF16) || (L.mu_dtype != RF_F32 && L.mu_dtype != RF_BF16))
-            return fail(RF_ERR_UNSUPPORTED, "grad and moment dtypes must be f32 or bf16");
+        if (!valid_dtype(L.grad_dtype) || !valid_dtype(L.mu_dtype))
+            return fail(RF_ERR_UNSUPPORTED, "grad and moment dtypes must be f32, bf16 or f16");
         if (L.size > 0 && (!L.grad || !L.mu || (need_updates && !L.updates)))
             return fail(RF_ERR_INVALID, "null buffer");
         Seg sg{};
@@ -2088,8 +2135,7 @@ rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t st
     for (int32_t i = 0; i < n_leaves; ++i) {
         const rf_apply_leaf& L = leaves[i];
         if (L.size < 0) return fail(RF_ERR_INVALID, "negative size");
-        if (L.param_dtype != RF_F32 && L.param_dtype != RF_BF16)
-            return fail(RF_ERR_UNSUPPORTED, "param dtype must be f32 or bf16");
+        if (!valid_dtype(L.param_dtype)) return fail(RF_ERR_UNSUPPORTED, "param dtype must be f32, bf16 or f16");
         if (L.size > 0 && (!L.param || !L.updates)) return fail(RF_ERR_INVALID, "null buffer");
         if (L.param_index < 0) return fail(RF_ERR_INVALID, "negative key index");
         maxsize = std::max(maxsize, L.size);

@@ -219,7 +219,8 @@ PyObject* py_refresh(PyObject*, PyObject* args)
         const int vec = PyObject_IsTrue(PyTuple_GET_ITEM(row, 8));
         if (PyErr_Occurred()) return nullptr;
         const at::ScalarType st = t.scalar_type();
-        const bool dtype_ok = (want_dtype == RF_F32 && st == at::kFloat) || (want_dtype == RF_BF16 && st == at::kBFloat16);
+        const bool dtype_ok = (want_dtype == RF_F32 && st == at::kFloat) || (want_dtype == RF_BF16 && st == at::kBFloat16) ||
+                              (want_dtype == RF_F16 && st == at::kHalf);
         if (!dtype_ok || !t.is_cuda() || t.get_device() != device || t.numel() != want_size || !t.is_contiguous())
             Py_RETURN_FALSE;
         const uintptr_t gp = (uintptr_t)t.data_ptr();
@@ -353,7 +354,8 @@ PyObject* apply_walk(PyObject* p, PyObject* u, ApplyWalk& w)
             const at::Tensor& tp = THPVariable_Unpack(p);
             const at::Tensor& tu = THPVariable_Unpack(u);
             const at::ScalarType sp = tp.scalar_type();
-            if ((sp != at::kFloat && sp != at::kBFloat16) || tu.scalar_type() != at::kFloat) return nullptr;
+            if ((sp != at::kFloat && sp != at::kBFloat16 && sp != at::kHalf) || tu.scalar_type() != at::kFloat)
+                return nullptr;
             if (!tp.is_cuda() || !tu.is_cuda() || tp.get_device() != tu.get_device()) return nullptr;
             if (w.device < 0) w.device = tp.get_device();
             if (tp.get_device() != w.device) return nullptr;
@@ -364,7 +366,7 @@ PyObject* apply_walk(PyObject* p, PyObject* u, ApplyWalk& w)
             row.updates = (const float*)tu.data_ptr();
             row.bits = nullptr;
             row.size = tp.numel();
-            row.param_dtype = sp == at::kBFloat16 ? RF_BF16 : RF_F32;
+            row.param_dtype = sp == at::kBFloat16 ? RF_BF16 : (sp == at::kHalf ? RF_F16 : RF_F32);
             row.param_index = (int32_t)i;
             w.rows.append((const char*)&row, sizeof(row));
         }

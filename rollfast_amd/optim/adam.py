@@ -129,11 +129,10 @@ def _init_magma_state(params):
 
 def _dtype_code(t) -> int:
     torch = _torch()
-    if t.dtype == torch.bfloat16:
-        return _lib.RF_BF16
-    if t.dtype == torch.float32:
-        return _lib.RF_F32
-    raise NotImplementedError(f"dtype {t.dtype} is not supported (float32 or bfloat16)")
+    code = {torch.bfloat16: _lib.RF_BF16, torch.float32: _lib.RF_F32, torch.float16: _lib.RF_F16}.get(t.dtype)
+    if code is None:
+        raise NotImplementedError(f"dtype {t.dtype} is not supported (float32, bfloat16 or float16)")
+    return code
 
 
 def _magma_step(engine, magma_p, magma_tau, updates, state, params, *, decay_mask, weight_decay, neg_lr,
@@ -264,8 +263,8 @@ def _make_engine(b1, b2, eps, eps_root, mu_dtype, nesterov, key, exact, magma: b
 def _canonical_mu_dtype(mu_dtype):
     torch = _torch()
     d = torch.float32 if mu_dtype is None else canonicalize_dtype(mu_dtype)
-    if d not in (torch.float32, torch.bfloat16):
-        raise NotImplementedError("mu_dtype must be float32 or bfloat16")
+    if d not in (torch.float32, torch.bfloat16, torch.float16):
+        raise NotImplementedError("mu_dtype must be float32, bfloat16 or float16")
     return d
 
 

@@ -92,7 +92,26 @@ def _rf_dtype(dtype, what: str) -> int:
         return _lib.RF_F32
     if dtype == torch.bfloat16:
         return _lib.RF_BF16
-    raise NotImplementedError(f"{what} dtype {dtype} is not supported (float32 or bfloat16)")
+    if dtype == torch.float16:
+        return _lib.RF_F16
+    raise NotImplementedError(f"{what} dtype {dtype} is not supported (float32, bfloat16 or float16)")
+
+
+def _scale_flag(dtype) -> int:
+    """RF_LEAF_SCALE_* flag of a block-scale dtype (scale_dtype, adam8.py:186)."""
+    torch = _torch()
+    if dtype == torch.float32:
+        return 0
+    if dtype == torch.bfloat16:
+        return _lib.RF_LEAF_SCALE_BF16
+    if dtype == torch.float16:
+        return _lib.RF_LEAF_SCALE_F16
+    raise NotImplementedError(f"scale dtype {dtype} is not supported (float32, bfloat16 or float16)")
+
+
+def _check_scale_dtype(dtype):
+    _scale_flag(dtype)
+    return dtype
 
 
 # ------------------------------------------------------ QuantizedBlocks ----
@@ -255,19 +274,18 @@ def quantize_blocks(
             "quantizer must be 'dynamic_signed', 'dynamic_unsigned', or "
             "'symmetric_int8'."
         )
-    scale_dtype = torch.float32 if scale_dtype is None else canonicalize_dtype(scale_dtype)
-    if scale_dtype != torch.float32:
-        raise NotImplementedError("only float32 block scales are implemented (scale_dtype=float32)")
+    scale_dtype = _check_scale_dtype(torch.float32 if scale_dtype is None else canonicalize_dtype(scale_dtype))
     if stochastic_rounding and key is None and random_bits is None:
         raise ValueError("stochastic rounding requires a PRNG key.")
     _require_device_tensor(x, "x")
-    x_f32 = x.to(torch.float32).contiguous()
+    # jnp.asarray(x, float32): f32, bf16 and f16 inputs are widened in the kernel
+    x_in = x.contiguous() if x.dtype in (torch.float32, torch.bfloat16, torch.float16) else x.to(torch.float32)
     shape = tuple(x.shape)
     size = int(x.numel())
     blocks_count = max(1, math.ceil(size / block_size))
     vdtype = torch.int8 if quantizer == "symmetric_int8" else torch.uint8
     values = torch.empty((blocks_count, block_size), dtype=vdtype, device=x.device)
-    scales = torch.empty((blocks_count,), dtype=torch.float32, device=x.device)
+    scales = torch.empty((blocks_count,), dtype=scale_dtype, device=x.device)
     k = prng.as_key(key) if key is not None else np.zeros(2, np.uint32)
     bits = None
     if random_bits is not None:
@@ -277,9 +295,9 @@ def quantize_blocks(
     with _device_ctx(x):
         _lib.check(
             _lib.lib().rf_blockwise_quantize(
-                _QUANTIZER_CODE[quantizer], _ptr(x_f32), size, int(block_size),
+                _QUANTIZER_CODE[quantizer], _ptr(x_in), _rf_dtype(x_in.dtype, "input"), size, int(block_size),
                 1 if stochastic_rounding else 0, int(k[0]), int(k[1]), _ptr(bits),
-                values.data_ptr(), scales.data_ptr(), _lib.stream_ptr(),
+                values.data_ptr(), scales.data_ptr(), _rf_dtype(scale_dtype, "scale"), _lib.stream_ptr(),
             ),
             "quantize_blocks",
         )
@@ -303,16 +321,16 @@ def dequantize_blocks(blocks: QuantizedBlocks, *, dtype=None):
     dtype = torch.float32 if dtype is None else canonicalize_dtype(dtype)
     quantizer = _quantizer_from_codebook_id(blocks.codebook_id)
     values = _require_device_tensor(blocks.values, "values").contiguous()
-    scales = blocks.scales
-    if scales.dtype != torch.float32:
-        raise NotImplementedError("only float32 block scales are implemented")
-    out_dtype = dtype if dtype in (torch.float32, torch.bfloat16) else torch.float32
+    scales = _require_device_tensor(blocks.scales, "scales").contiguous()
+    _check_scale_dtype(scales.dtype)  # values * scales.astype(float32) (adam8.py:202)
+    out_dtype = dtype if dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
     out = torch.empty((blocks.size,), dtype=out_dtype, device=values.device)
     with _device_ctx(values):
         _lib.check(
             _lib.lib().rf_blockwise_dequantize(
-                _QUANTIZER_CODE[quantizer], values.data_ptr(), scales.contiguous().data_ptr(), int(blocks.size),
-                int(blocks.block_size), _rf_dtype(out_dtype, "output"), out.data_ptr(), _lib.stream_ptr(),
+                _QUANTIZER_CODE[quantizer], values.data_ptr(), scales.data_ptr(), _rf_dtype(scales.dtype, "scale"),
+                int(blocks.size), int(blocks.block_size), _rf_dtype(out_dtype, "output"), out.data_ptr(),
+                _lib.stream_ptr(),
             ),
             "dequantize_blocks",
         )
@@ -391,7 +409,7 @@ def _init_moment_leaf(param, cfg: _Config, quantizer: str):
         return QuantizedBlocks(
             values=torch.full((blocks_count, cfg.block_size), _zero_code_for_quantizer(quantizer),
                               dtype=torch.uint8, device=param.device),
-            scales=torch.ones((blocks_count,), dtype=torch.float32, device=param.device),
+            scales=torch.ones((blocks_count,), dtype=cfg.scale_dtype, device=param.device),
             shape=tuple(param.shape),
             size=size,
             block_size=cfg.block_size,
@@ -597,8 +615,9 @@ class _Engine:
                         raise ValueError("all leaves must live on the same device")
                     if not t.is_contiguous():
                         raise ValueError("moment buffers must be contiguous (they are updated in place)")
-                if m.scales.dtype != torch.float32 or v.scales.dtype != torch.float32:
-                    raise NotImplementedError("only float32 block scales are implemented")
+                if m.scales.dtype != v.scales.dtype:
+                    raise ValueError("first and second moment scales differ in dtype")
+                row.flags |= _scale_flag(m.scales.dtype)
                 nb = max(1, math.ceil(size / m.block_size))
                 for t, want in ((m.values, nb * m.block_size), (v.values, nb * m.block_size), (m.scales, nb),
                                 (v.scales, nb)):
@@ -620,9 +639,10 @@ class _Engine:
                     raise ValueError("fallback moment leaf does not match its gradient")
                 if not (m.is_contiguous() and v.is_contiguous()):
                     raise ValueError("moment buffers must be contiguous (they are updated in place)")
-                if m.dtype not in (torch.float32, torch.bfloat16):
+                if m.dtype not in (torch.float32, torch.bfloat16, torch.float16):
                     raise NotImplementedError(f"fallback moment dtype {m.dtype} is not supported")
-                row.moment_kind = _lib.RF_MOMENT_BF16 if m.dtype == torch.bfloat16 else _lib.RF_MOMENT_F32
+                row.moment_kind = {torch.bfloat16: _lib.RF_MOMENT_BF16, torch.float16: _lib.RF_MOMENT_F16}.get(
+                    m.dtype, _lib.RF_MOMENT_F32)
                 if self.store_sr and m.dtype == torch.bfloat16:
                     row.flags |= _lib.RF_LEAF_STORE_SR
                 row.mu = m.data_ptr()
@@ -886,10 +906,9 @@ def _validate(block_size, min_size, block_layout, fallback_dtype, scale_dtype):
         raise ValueError("min_size must be non-negative.")
     if block_layout not in {"shard_local", "logical_global"}:
         raise ValueError("block_layout must be 'shard_local' or 'logical_global'.")
-    if scale_dtype != torch.float32:
-        raise NotImplementedError("only float32 block scales are implemented (scale_dtype=float32)")
-    if fallback_dtype not in (torch.float32, torch.bfloat16):
-        raise NotImplementedError("fallback_dtype must be float32 or bfloat16")
+    _check_scale_dtype(scale_dtype)
+    if fallback_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        raise NotImplementedError("fallback_dtype must be float32, bfloat16 or float16")
 
 
 class _ScaleByAdam8Update:

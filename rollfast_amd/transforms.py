@@ -71,15 +71,15 @@ class _ClipUpdate:
                 device = leaf.device
             if leaf.device != device:
                 raise ValueError("all leaves must live on the same device")
-            if leaf.dtype not in (torch.float32, torch.bfloat16):
-                raise NotImplementedError(f"dtype {leaf.dtype} is not supported (float32 or bfloat16)")
+            if leaf.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                raise NotImplementedError(f"dtype {leaf.dtype} is not supported (float32, bfloat16 or float16)")
             src = leaf.contiguous()
             dst = torch.empty_like(src)
             row = _lib.ClipLeaf()
             row.grad = src.data_ptr()
             row.out = dst.data_ptr()
             row.size = int(src.numel())
-            row.dtype = _lib.RF_BF16 if src.dtype == torch.bfloat16 else _lib.RF_F32
+            row.dtype = {torch.bfloat16: _lib.RF_BF16, torch.float16: _lib.RF_F16}.get(src.dtype, _lib.RF_F32)
             rows.append((row, src))
             out.append(dst.view(leaf.shape))
         if rows:

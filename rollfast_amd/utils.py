@@ -51,12 +51,9 @@ def _launch_apply(pairs, stochastic: bool, key) -> None:
             raise ValueError("params must be contiguous (they are updated in place)")
         if p.numel() != u.numel():
             raise ValueError(f"param and update sizes differ ({p.numel()} vs {u.numel()})")
-        if p.dtype == torch.bfloat16:
-            pdt = _lib.RF_BF16
-        elif p.dtype == torch.float32:
-            pdt = _lib.RF_F32
-        else:
-            raise NotImplementedError(f"param dtype {p.dtype} is not supported (float32 or bfloat16)")
+        pdt = {torch.bfloat16: _lib.RF_BF16, torch.float32: _lib.RF_F32, torch.float16: _lib.RF_F16}.get(p.dtype)
+        if pdt is None:
+            raise NotImplementedError(f"param dtype {p.dtype} is not supported (float32, bfloat16 or float16)")
         # The reference adds the update in f32 (utils.py:694-700).
         uf = u if (u.dtype == torch.float32 and u.is_contiguous()) else u.to(torch.float32).contiguous()
         keep.append(uf)

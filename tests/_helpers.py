@@ -18,12 +18,14 @@ def bf16_to_f32(h: np.ndarray) -> np.ndarray:
 
 
 def to_device(arr: np.ndarray, dtype: str, device="cuda"):
-    """NumPy -> torch on device.  dtype 'f32' takes f32 values; 'bf16' takes
-    bf16 bit patterns (uint16)."""
+    """NumPy -> torch on device.  dtype 'f32' takes f32 values; 'bf16' and
+    'f16' take bit patterns (uint16)."""
     import torch
 
     if dtype == "bf16":
         t = torch.from_numpy(np.ascontiguousarray(arr, dtype=np.uint16).view(np.int16)).view(torch.bfloat16)
+    elif dtype == "f16":
+        t = torch.from_numpy(np.ascontiguousarray(arr, dtype=np.uint16).view(np.int16)).view(torch.float16)
     elif dtype == "f32":
         t = torch.from_numpy(np.ascontiguousarray(arr, dtype=np.float32))
     elif dtype == "u8":
@@ -40,7 +42,7 @@ def to_host(t) -> np.ndarray:
     import torch
 
     t = t.detach().contiguous()
-    if t.dtype == torch.bfloat16:
+    if t.dtype in (torch.bfloat16, torch.float16):
         return t.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
     if t.dtype == torch.uint32:
         return t.view(torch.int32).cpu().numpy().view(np.uint32).reshape(-1)
@@ -48,7 +50,7 @@ def to_host(t) -> np.ndarray:
 
 
 def bf16_ulp_distance(a_bits: np.ndarray, b_bits: np.ndarray) -> np.ndarray:
-    """Distance in bf16 ulps between two arrays of bf16 bit patterns
+    """Distance in ulps between two arrays of bf16 (or f16) bit patterns
     (sign-magnitude order)."""
 
     def key(h):
@@ -110,7 +112,7 @@ class OracleTree:
     def step(self, grads, *, b1=0.9, b2=0.999, eps=1e-8, eps_root=0.0, weight_decay=0.0, lr=1e-3,
              count=1, decay_mask=None, nesterov=False, moment_sr=False, param_sr=False, apply=True,
              mu_bits=None, nu_bits=None, p_bits=None, lr_scale=True, decay_weak=True, ema_weight_f32=False,
-             store_sr=False, zero_decay=False):
+             store_sr=False, zero_decay=False, scale_dtype=None):
         outs = []
         for i, L in enumerate(self.leaves):
             decays = weight_decay != 0.0 and (decay_mask is None or decay_mask[i])
@@ -118,10 +120,11 @@ class OracleTree:
                                   lr=lr if lr_scale else None, count=count, nesterov=nesterov, decay=decays,
                                   decay_weak=decay_weak, moment_sr=moment_sr, param_sr=param_sr, apply=apply,
                                   ema_weight_f32=ema_weight_f32, store_sr=store_sr and L["kind"] == "bf16",
-                                  zero_decay=zero_decay)
-            pd = orc.BF16 if L["pdtype"] == "bf16" else orc.F32
-            gd = orc.BF16 if L["gdtype"] == "bf16" else orc.F32
-            mk = {"quant": orc.MOM_QUANT, "f32": orc.MOM_F32, "bf16": orc.MOM_BF16}[L["kind"]]
+                                  zero_decay=zero_decay,
+                                  scale_dtype=orc.F32 if scale_dtype is None else scale_dtype)
+            dt = {"f32": orc.F32, "bf16": orc.BF16, "f16": orc.F16}
+            pd, gd = dt[L["pdtype"]], dt[L["gdtype"]]
+            mk = {"quant": orc.MOM_QUANT, "f32": orc.MOM_F32, "bf16": orc.MOM_BF16, "f16": orc.MOM_F16}[L["kind"]]
             upd = None if apply else np.empty(L["size"], dtype=np.float32)
             orc.adam8_leaf(hp, L["param"], pd, grads[i], gd, mk, L["mu"], L.get("mu_scales"), L["nu"],
                            L.get("nu_scales"), L.get("block_size", 2048),

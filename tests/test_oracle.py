@@ -753,3 +753,117 @@ def test_zero_weight_decay_term_closed_form():
     assert np.isnan(zero[:3]).all() and np.isfinite(base[:3]).all()
     np.testing.assert_array_equal(zero[4:], base[4:] + np.float32(0.0))
     assert np.signbit(base[3]) and not np.signbit(zero[3])
+
+
+def test_f16_widening_all_patterns_against_numpy():
+    """The oracle's binary16 -> f32 over all 65,536 patterns against numpy's
+    float16 (NaN positions and every other value bit for bit)."""
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    got = orc.f16_bits_to_f32(h)
+    want = h.view(np.float16).astype(np.float32)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    np.testing.assert_array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))
+
+
+def _f16_narrowing_cases():
+    """f32 patterns that decide binary16 rounding: a stride-61 sweep of every
+    pattern, and +-3 patterns around every midpoint between adjacent f16
+    values (including 65504 | 65536 and the subnormal steps)."""
+    sweep = np.arange(0, 1 << 32, 61, dtype=np.uint64).astype(np.uint32)
+    pos = np.arange(0, 0x7C01, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float64)
+    pos = np.append(pos, 65536.0)   # the rounding target just above 65504 (Inf in f16)
+    mids = ((pos[:-1] + pos[1:]) / 2).astype(np.float32).view(np.uint32).astype(np.int64)
+    near = (mids[:, None] + np.arange(-3, 4)[None, :]).reshape(-1)
+    near = np.concatenate([near, near | (1 << 31)]).astype(np.uint32)
+    return [sweep[i:i + (1 << 24)] for i in range(0, sweep.size, 1 << 24)] + [near]
+
+
+def test_f16_narrowing_against_numpy():
+    """The oracle's f32 -> binary16 (round to nearest even, overflow to Inf
+    from 65520, subnormals) against numpy's astype(float16)."""
+    for bits in _f16_narrowing_cases():
+        x = bits.view(np.float32)
+        got = orc.f32_to_f16_bits(x)
+        with np.errstate(over="ignore"):
+            want = x.astype(np.float16).view(np.uint16)
+        nan = np.isnan(x)
+        np.testing.assert_array_equal(got[~nan], want[~nan])
+        assert np.all((got[nan] & 0x7C00) == 0x7C00) and np.all((got[nan] & 0x3FF) != 0)
+
+
+@pytest.mark.parametrize("quantizer", [orc.Q_SIGNED, orc.Q_UNSIGNED, orc.Q_SYMMETRIC])
+def test_scale_dtype_changes_only_the_stored_scales(quantizer):
+    """quantize_blocks codes with the f32 scale and stores
+    scales.astype(scale_dtype) (adam8.py:167-186): the codes do not depend on
+    scale_dtype, and the stored scales are the f32 ones rounded (numpy's
+    bfloat16-free check: bf16 rounding through the bit patterns, f16 through
+    numpy's float16)."""
+    rng = np.random.default_rng(8)
+    x = (rng.standard_normal(5 * 256 + 9) * np.exp(rng.uniform(-30, 12, 5 * 256 + 9))).astype(np.float32)
+    if quantizer == orc.Q_UNSIGNED:
+        x = np.abs(x)
+    c32, s32 = orc.quantize(x, 256, quantizer)
+    cb, sb = orc.quantize(x, 256, quantizer, scale_dtype=orc.BF16)
+    ch, sh = orc.quantize(x, 256, quantizer, scale_dtype=orc.F16)
+    np.testing.assert_array_equal(cb, c32)
+    np.testing.assert_array_equal(ch, c32)
+    np.testing.assert_array_equal(sb, orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(s32)))
+    with np.errstate(over="ignore"):
+        np.testing.assert_array_equal(sh, s32.astype(np.float16).astype(np.float32))
+
+
+def test_step_with_16_bit_scales_reads_the_stored_scale():
+    """One adam8 step with bf16 block scales from a state whose scales are
+    bf16 values: the new moments and codes equal the f32-scale step's (same
+    old scales), and only the stored new scales are rounded."""
+    rng = np.random.default_rng(12)
+    n, bs = 4 * 2048, 2048
+    g = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    mc = rng.integers(0, 256, n).astype(np.uint8)
+    vc = rng.integers(0, 256, n).astype(np.uint8)
+    ms = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(rng.uniform(1e-4, 1e-2, 4).astype(np.float32)))
+    vs = orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(rng.uniform(1e-7, 1e-5, 4).astype(np.float32)))
+    outs = []
+    for sd in (orc.F32, orc.BF16):
+        hp = orc.make_hparams(count=3, apply=False, scale_dtype=sd)
+        a = [p.copy(), mc.copy(), ms.copy(), vc.copy(), vs.copy(), np.empty(n, np.float32)]
+        orc.adam8_leaf(hp, a[0], orc.F32, g, orc.F32, orc.MOM_QUANT, a[1], a[2], a[3], a[4], bs, updates_out=a[5])
+        outs.append(a)
+    (f, b) = outs
+    np.testing.assert_array_equal(b[1], f[1])
+    np.testing.assert_array_equal(b[3], f[3])
+    np.testing.assert_array_equal(b[5].view(np.uint32), f[5].view(np.uint32))
+    np.testing.assert_array_equal(b[2], orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(f[2])))
+    np.testing.assert_array_equal(b[4], orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(f[4])))
+
+
+def test_f16_params_round_the_f32_step():
+    """An f16 param leaf: without the weak-typed decay its new params are
+    the f32 step's params (on the same values) rounded to f16 by numpy; with
+    it, the decay term is f16(f16(wd) * p) (numpy float16 arithmetic, exact
+    products)."""
+    rng = np.random.default_rng(13)
+    n = 3000
+    p16 = (rng.standard_normal(n) * 0.5).astype(np.float16)
+    g16 = (rng.standard_normal(n) * 1e-2).astype(np.float16)
+    p32, g32 = p16.astype(np.float32), g16.astype(np.float32)
+    for weak in (False, True):
+        hp = orc.make_hparams(count=1, weight_decay=0.01, lr=1e-3, decay=True, decay_weak=weak, apply=True)
+        a16 = p16.view(np.uint16).copy()
+        orc.adam8_leaf(hp, a16, orc.F16, g16.view(np.uint16).copy(), orc.F16, orc.MOM_F32,
+                       np.zeros(n, np.float32), None, np.zeros(n, np.float32), None)
+        if not weak:
+            a32 = p32.copy()
+            orc.adam8_leaf(hp, a32, orc.F32, g32, orc.F32, orc.MOM_F32, np.zeros(n, np.float32), None,
+                           np.zeros(n, np.float32), None)
+            np.testing.assert_array_equal(a16, a32.astype(np.float16).view(np.uint16))
+        else:
+            hp0 = orc.make_hparams(count=1, apply=False)
+            u = np.empty(n, np.float32)
+            orc.adam8_leaf(hp0, p32.copy(), orc.F32, g32, orc.F32, orc.MOM_F32, np.zeros(n, np.float32), None,
+                           np.zeros(n, np.float32), None, updates_out=u)
+            wdp = (np.float16(0.01) * p16).astype(np.float32)          # f16 product, rounded once
+            want = (p32 + np.float32(-1e-3) * (u + wdp)).astype(np.float16)
+            np.testing.assert_array_equal(a16, want.view(np.uint16))
