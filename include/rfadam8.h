@@ -314,7 +314,8 @@ typedef struct rf_clip_leaf {
  * L2 norm of all leaves, scale = min(1, max_norm / (norm + 1e-6)), out = grad *
  * scale in the leaf dtype (bf16 leaves: times bf16(scale), one rounding).
  * `stats` (device f32[2] or NULL) receives (scale, norm).  Enqueues on
- * `stream`; its scratch comes from hipMallocAsync on that stream. */
+ * `stream`; its tables and scratch go through the library's per-device
+ * staging ring (no allocation once the ring has grown to the tree). */
 RF_API rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, float max_norm,
                                         float* stats, void* stream);
 
@@ -334,7 +335,7 @@ typedef struct rf_magma_leaf {
 /* magma.py:98-106 before the step: per leaf i, sums[3i..3i+2] (device f64) =
  * (sum g*m', sum g*g, sum m'*m') with m' = f32(b1*mu) + f32(one_minus_b1*g),
  * the step's new first moment (utils.py:327-335, :437-467).  Enqueue it
- * before the step, which overwrites mu.  Scratch: hipMallocAsync on stream. */
+ * before the step, which overwrites mu.  Scratch: the staging ring. */
 RF_API rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, float b1, float one_minus_b1,
                                  double* sums, void* stream);
 
@@ -346,7 +347,7 @@ RF_API rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, 
  * scale, optax scale_by_learning_rate otherwise).  With factor_out (device
  * f32[n_leaves], else NULL) the per-leaf factors m * s are written there and
  * the updates are left for rf_magma_apply_updates (updates may then be
- * NULL).  Scratch: hipMallocAsync. */
+ * NULL).  Scratch: the staging ring. */
 RF_API rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const double* sums, float* scores,
                                 float p, float tau, uint32_t key0, uint32_t key1, int32_t n_keys, float neg_lr,
                                 float* factor_out, void* stream);
@@ -358,6 +359,29 @@ RF_API rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, c
 RF_API rf_status rf_magma_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, const float* factor,
                                         float neg_lr, int32_t stochastic, uint32_t key0, uint32_t key1,
                                         void* stream);
+
+/* One leaf of optax.MultiSteps' gradient accumulator (the fine-tune
+ * builders' wrapper, finetune/builders.py:1614-1620; optax is not vendored
+ * in the reference). */
+typedef struct rf_accum_leaf {
+    const void* grad;   /* [size] grad_dtype: this micro-step's gradient (unused by RF_ACC_ZERO) */
+    void* acc;          /* [size] acc_dtype: the accumulator, updated in place */
+    int64_t size;
+    int32_t grad_dtype; /* RF_F32 | RF_BF16 | RF_F16 */
+    int32_t acc_dtype;  /* RF_F32 | RF_BF16 | RF_F16 (accumulator_dtype) */
+} rf_accum_leaf;
+
+#define RF_ACC_SUM 0  /* use_grad_mean=False: acc = grad + acc */
+#define RF_ACC_MEAN 1 /* use_grad_mean=True: acc = acc + (grad - acc) / (n_acc + 1), Welford's running mean */
+#define RF_ACC_ZERO 2 /* acc = 0 * acc: the reset after the k-th micro-step ((1 - emit) * acc; a signed
+                       zero, NaN where the accumulator held Inf or NaN) */
+
+/* One accumulation over n leaves: per element in the promoted dtype of grad
+ * and accumulator (f32, or their common 16-bit type with every operation
+ * rounded to nearest even), stored in acc_dtype.  n_acc is the micro-step
+ * counter before this step (MultiStepsState.mini_step). */
+RF_API rf_status rf_accumulate(const rf_accum_leaf* leaves, int32_t n_leaves, int32_t mode, int32_t n_acc,
+                               void* stream);
 
 /* Host-side: the 256 f32 values of a dynamic codebook (adam8.py:461-503). */
 RF_API rf_status rf_codebook(int32_t quantizer, float* out256);

@@ -615,6 +615,44 @@ ORC_API void orc_apply_updates(int pdtype, void* param, const float* upd, int64_
     }
 }
 
+/* optax.MultiSteps (optax >=0.2.8,<0.3.0, optax/_src/wrappers.py; the
+ * wrapper of finetune/builders.py:1614-1620) for one leaf, in place on acc:
+ *   mode 1 (use_grad_mean): acc + (grad - acc) / (n_acc + 1)  (Welford)
+ *   mode 0 (sum):           grad + acc
+ *   mode 2 (reset after an emitting step): (1 - emit) * acc = 0 * acc
+ * JAX computes each in the promoted dtype of grad and acc: f32 unless both
+ * are the same 16-bit type, whose every operation then rounds to nearest
+ * even; the int32 count n_acc + 1 converts to that dtype.  The result is
+ * stored in acc's dtype (the promoted one for the combinations MultiSteps
+ * accepts). */
+ORC_API void orc_accumulate(int mode, int32_t n_acc, int gdtype, const void* grad, int adtype, void* acc,
+                            int64_t n)
+{
+    const int cdt = gdtype == adtype ? adtype : ORC_F32;
+    const float div = round_to(cdt, (float)n_acc + 1.0f);
+#pragma omp parallel for schedule(static)
+    for (int64_t e = 0; e < n; ++e) {
+        const float a = load_val(adtype, acc, e);
+        float r;
+        if (mode == 2) {
+            r = 0.0f * a;
+        } else {
+            const float g = load_val(gdtype, grad, e);
+            if (mode == 1) {
+                const float d = round_to(cdt, g - a);
+                const float q = round_to(cdt, d / div);
+                r = round_to(cdt, a + q);
+            } else {
+                r = round_to(cdt, g + a);
+            }
+        }
+        if (adtype == ORC_F32)
+            ((float*)acc)[e] = r;
+        else
+            ((uint16_t*)acc)[e] = to_h16(adtype, r);
+    }
+}
+
 /* utils.py:342-371 _stochastic_round_bf16 over an array with fed bits. */
 ORC_API void orc_sr_bf16(const float* x, const uint32_t* bits, int64_t n, uint16_t* out)
 {

@@ -29,6 +29,7 @@ MOM_QUANT, MOM_F32, MOM_BF16, MOM_F16 = 0, 1, 2, 3
 NESTEROV, DECAY, DECAY_WEAK, LR, MOMENT_SR, PARAM_SR, APPLY, STORE_SR = 1, 2, 4, 8, 16, 32, 64, 512
 ZERO_DECAY = 1024
 SCALE_BF16, SCALE_F16 = 2048, 4096
+ACC_SUM, ACC_MEAN, ACC_ZERO = 0, 1, 2
 
 
 class Hparams(ctypes.Structure):
@@ -83,6 +84,7 @@ def lib() -> ctypes.CDLL:
             ctypes.c_int, p, p, p, p, i64, p, p, p, p,
         ]
         _lib.orc_apply_updates.argtypes = [ctypes.c_int, p, p, i64, ctypes.c_int, p]
+        _lib.orc_accumulate.argtypes = [ctypes.c_int, ctypes.c_int32, ctypes.c_int, p, ctypes.c_int, p, i64]
         _lib.orc_sr_bf16.argtypes = [p, p, i64, p]
         _lib.orc_f32_to_bf16.argtypes = [p, i64, p]
         _lib.orc_f32_to_f16.argtypes = [p, i64, p]
@@ -359,6 +361,32 @@ def apply_updates(param: np.ndarray, pdtype: int, upd: np.ndarray, bits=None) ->
     upd = np.ascontiguousarray(upd, dtype=np.float32).reshape(-1)
     lib().orc_apply_updates(pdtype, _ptr(param), _ptr(upd), upd.size, 1 if bits is not None else 0,
                             _ptr(bits))
+
+
+# ------------------------------------------------------ optax.MultiSteps --
+def accumulate(mode: int, n_acc: int, grad, gdtype: int, acc: np.ndarray, adtype: int) -> None:
+    """optax.MultiSteps' accumulator update for one leaf, in place on ``acc``
+    (F32 values or BF16 / F16 bit patterns): ACC_MEAN ``acc + (grad - acc) /
+    (n_acc + 1)``, ACC_SUM ``grad + acc``, ACC_ZERO ``0 * acc`` (the reset
+    after an emitting step), each op in the promoted dtype."""
+    assert acc.flags.c_contiguous
+    g = None
+    if mode != ACC_ZERO:
+        g = np.ascontiguousarray(grad, dtype=np.float32 if gdtype == F32 else np.uint16).reshape(-1)
+        assert g.size == acc.size
+    lib().orc_accumulate(int(mode), int(n_acc), int(gdtype), _ptr(g), int(adtype), _ptr(acc), acc.size)
+
+
+def multisteps_counters(mini_step: int, gradient_step: int, k_steps: int):
+    """optax.MultiSteps.update's counters: ``emit = mini_step == k - 1``,
+    mini_step -> (mini_step + 1) % k (int32-saturating increment first),
+    gradient_step -> incremented on an emitting step.  Returns (emit,
+    mini_step, gradient_step)."""
+    def inc(c):
+        return c + 1 if c < 2**31 - 1 else c
+
+    emit = int(mini_step) == int(k_steps) - 1
+    return emit, inc(int(mini_step)) % int(k_steps), inc(int(gradient_step)) if emit else int(gradient_step)
 
 
 # ------------------------------------------------- global-norm clipping --

@@ -37,6 +37,7 @@ from .optim.adam import ScaleByAdamState, adamw, adamw_step, scale_by_adam
 from .optim.convert import adam8_state_from_adam, adam_state_from_adam8, dequantize_state_tree, quantize_state_tree
 from .combine import MultiTransformState, chain, masked, multi_transform
 from .transforms import GlobalNormClipState, apply_if_finite, clip_by_global_norm
+from .multisteps import MultiSteps, MultiStepsState
 from .utils import apply_updates, apply_updates_prefix
 
 __version__ = "0.1.0"
@@ -52,6 +53,8 @@ __all__ = (
     "GradientTransformationExtraArgs",
     "MaskedNode",
     "MaskedState",
+    "MultiSteps",
+    "MultiStepsState",
     "MultiTransformState",
     "QuantizedBlocks",
     "ScaleByAdam8State",

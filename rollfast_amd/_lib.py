@@ -32,6 +32,7 @@ RF_LEAF_STORE_SR = 2
 RF_LEAF_ZERO_DECAY = 4
 RF_LEAF_SCALE_BF16 = 8
 RF_LEAF_SCALE_F16 = 16
+RF_ACC_SUM, RF_ACC_MEAN, RF_ACC_ZERO = 0, 1, 2
 RF_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 _p = ctypes.c_void_p
@@ -124,6 +125,16 @@ class MagmaLeaf(ctypes.Structure):
     ]
 
 
+class AccumLeaf(ctypes.Structure):
+    _fields_ = [
+        ("grad", _p),
+        ("acc", _p),
+        ("size", ctypes.c_int64),
+        ("grad_dtype", ctypes.c_int32),
+        ("acc_dtype", ctypes.c_int32),
+    ]
+
+
 class ApplyLeaf(ctypes.Structure):
     _fields_ = [
         ("param", _p),
@@ -140,6 +151,7 @@ assert ctypes.sizeof(Adam8Hparams) == 128
 assert ctypes.sizeof(Adam8Group) == 32
 assert ctypes.sizeof(ApplyLeaf) == 40
 assert ctypes.sizeof(ClipLeaf) == 32
+assert ctypes.sizeof(AccumLeaf) == 32
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTS = (
@@ -159,6 +171,7 @@ EXPORTS = (
     "rf_magma_reduce",
     "rf_magma_scale",
     "rf_magma_apply_updates",
+    "rf_accumulate",
     "rf_codebook",
     "rf_host_table_codes",
     "rf_host_search_index",
@@ -202,6 +215,7 @@ def lib() -> ctypes.CDLL:
     L.rf_magma_reduce.argtypes = [ctypes.POINTER(MagmaLeaf), i32, f32, f32, _p, _p]
     L.rf_magma_scale.argtypes = [ctypes.POINTER(MagmaLeaf), i32, _p, _p, f32, f32, u32, u32, i32, f32, _p, _p]
     L.rf_magma_apply_updates.argtypes = [ctypes.POINTER(ApplyLeaf), i32, _p, f32, i32, u32, u32, _p]
+    L.rf_accumulate.argtypes = [ctypes.POINTER(AccumLeaf), i32, i32, i32, _p]
     L.rf_codebook.argtypes = [i32, _p]
     L.rf_host_table_codes.argtypes = [i32, u32, i64, _p]
     L.rf_host_search_index.argtypes = [i32, u32, i64, _p]

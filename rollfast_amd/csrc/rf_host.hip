@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -298,66 +299,160 @@ __device__ __forceinline__ uint32_t apply_bf16(float p, float u, bool stochastic
     return sr_bf16(s, bits ? bits[e] : jax_bits(lk0, lk1, (uint64_t)e));
 }
 
+// Work units of apply_updates: APPLY_UNIT consecutive elements of one leaf
+// per wave (a ragged tree launches no idle workgroups).
+constexpr int64_t APPLY_UNIT = 8192;
+
 // `factor` (Magma's fused form, or null): each update is first taken as
 // neg_lr * (factor[leaf] * u), the scaling rf_magma_scale would have done.
-__global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ leaves, int32_t stochastic,
-                                              uint32_t k0, uint32_t k1, const float* __restrict__ factor,
-                                              float neg_lr)
+// Segment s of `segs` is leaf segs[s].leaf.
+__global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ leaves, const Seg* __restrict__ segs,
+                                              int64_t nunits, int32_t stochastic, uint32_t k0, uint32_t k1,
+                                              const float* __restrict__ factor, float neg_lr)
 {
-    const rf_apply_leaf L = leaves[blockIdx.y];
-    const float f = factor ? factor[blockIdx.y] : 1.0f;
-    uint32_t lk0 = 0, lk1 = 0;
-    if (stochastic) jax_split(k0, k1, (uint32_t)L.param_index, lk0, lk1);
-    const int64_t tid = (int64_t)blockIdx.x * WG + threadIdx.x;
-    const int64_t nthreads = (int64_t)gridDim.x * WG;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
     const bool sr = stochastic != 0;
-    const bool vec = ((uintptr_t)L.param % 16 == 0) && ((uintptr_t)L.updates % 16 == 0) &&
-                     (!L.bits || (uintptr_t)L.bits % 16 == 0);
-    const int64_t ngroups = vec ? L.size / 8 : 0;
-    for (int64_t gi = tid; gi < ngroups; gi += nthreads) {
-        const int64_t e0 = gi * 8;
-        float u[8], p[8];
-        load8<float>(L.updates, e0, u);
-        if (factor) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) u[t] = neg_lr * (f * u[t]);
+    int32_t s = 0, cur = -1;
+    const int32_t nseg = segs[0].nseg;
+    rf_apply_leaf L{};
+    float f = 1.0f;
+    uint32_t lk0 = 0, lk1 = 0;
+    bool vec = false;
+    for (int64_t u_ = wave; u_ < nunits; u_ += nwaves) {
+        s = seek_seg(segs, nseg, s, u_);
+        if (segs[s].leaf != cur) {
+            cur = segs[s].leaf;
+            L = leaves[cur];
+            f = factor ? factor[cur] : 1.0f;
+            if (sr) jax_split(k0, k1, (uint32_t)L.param_index, lk0, lk1);
+            vec = ((uintptr_t)L.param % 16 == 0) && ((uintptr_t)L.updates % 16 == 0) &&
+                  (!L.bits || (uintptr_t)L.bits % 16 == 0);
         }
-        if (L.param_dtype == RF_F16) {
-            load8<_Float16>(L.param, e0, p);
-            uint32_t h[8];
+        const int64_t e_begin = (u_ - segs[s].unit_start) * APPLY_UNIT;
+        const int64_t e_end = min(L.size, e_begin + APPLY_UNIT);
+        // 8 elements per lane and step over the unit's whole groups of 8
+        const int64_t v_end = vec ? e_begin + ((e_end - e_begin) / 8) * 8 : e_begin;
+        for (int64_t e0 = e_begin + lane * 8; e0 < v_end; e0 += WAVE * 8) {
+            float u[8], p[8];
+            load8<float>(L.updates, e0, u);
+            if (factor) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) h[t] = f32_to_f16_rne(p[t] + u[t]);  // no SR below bf16 (utils.py:700)
-            store8_bf16(L.param, e0, h);
-        } else if (L.param_dtype == RF_BF16) {
-            load8<uint16_t>(L.param, e0, p);
-            uint32_t h[8];
-            if (sr && L.bits) {
-                uint32_t rb[8];
-                load8_u32(L.bits, e0, rb);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) h[t] = sr_bf16(p[t] + u[t], rb[t]);
-            } else {
-#pragma unroll
-                for (int t = 0; t < 8; ++t) h[t] = apply_bf16(p[t], u[t], sr, nullptr, lk0, lk1, e0 + t);
+                for (int t = 0; t < 8; ++t) u[t] = neg_lr * (f * u[t]);
             }
-            store8_bf16(L.param, e0, h);
-        } else {
-            load8<float>(L.param, e0, p);
+            if (L.param_dtype == RF_F16) {
+                load8<_Float16>(L.param, e0, p);
+                uint32_t h[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) p[t] = p[t] + u[t];
-            store8_f32(L.param, e0, p);
+                for (int t = 0; t < 8; ++t) h[t] = f32_to_f16_rne(p[t] + u[t]);  // no SR below bf16 (utils.py:700)
+                store8_bf16(L.param, e0, h);
+            } else if (L.param_dtype == RF_BF16) {
+                load8<uint16_t>(L.param, e0, p);
+                uint32_t h[8];
+                if (sr && L.bits) {
+                    uint32_t rb[8];
+                    load8_u32(L.bits, e0, rb);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) h[t] = sr_bf16(p[t] + u[t], rb[t]);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) h[t] = apply_bf16(p[t], u[t], sr, nullptr, lk0, lk1, e0 + t);
+                }
+                store8_bf16(L.param, e0, h);
+            } else {
+                load8<float>(L.param, e0, p);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) p[t] = p[t] + u[t];
+                store8_f32(L.param, e0, p);
+            }
+        }
+        for (int64_t e = v_end + lane; e < e_end; e += WAVE) {
+            const float u = factor ? neg_lr * (f * L.updates[e]) : L.updates[e];
+            if (L.param_dtype == RF_F16) {
+                const float p = f16_bits_to_f32(((const uint16_t*)L.param)[e]);
+                ((uint16_t*)L.param)[e] = (uint16_t)f32_to_f16_rne(p + u);
+            } else if (L.param_dtype == RF_BF16) {
+                const float p = bf16_bits_to_f32(((const uint16_t*)L.param)[e]);
+                ((uint16_t*)L.param)[e] = (uint16_t)apply_bf16(p, u, sr, L.bits, lk0, lk1, e);
+            } else {
+                ((float*)L.param)[e] = ((const float*)L.param)[e] + u;
+            }
         }
     }
-    for (int64_t e = ngroups * 8 + tid; e < L.size; e += nthreads) {
-        const float u = factor ? neg_lr * (f * L.updates[e]) : L.updates[e];
-        if (L.param_dtype == RF_F16) {
-            const float p = f16_bits_to_f32(((const uint16_t*)L.param)[e]);
-            ((uint16_t*)L.param)[e] = (uint16_t)f32_to_f16_rne(p + u);
-        } else if (L.param_dtype == RF_BF16) {
-            const float p = bf16_bits_to_f32(((const uint16_t*)L.param)[e]);
-            ((uint16_t*)L.param)[e] = (uint16_t)apply_bf16(p, u, sr, L.bits, lk0, lk1, e);
-        } else {
-            ((float*)L.param)[e] = ((const float*)L.param)[e] + u;
+}
+
+// optax.MultiSteps' gradient accumulation (finetune/builders.py:1614-1620):
+// per element, in the promoted dtype of the grad and the accumulator (f32
+// unless both are the same 16-bit type, whose every operation then rounds
+// to nearest even), mean: acc + (g - acc) / (n_acc + 1) (Welford's running
+// mean), sum: g + acc, zero: 0 * acc (MultiSteps' (1 - emit) * acc after an
+// emitting step: a signed zero, NaN where acc was not finite); the result is
+// stored in the accumulator's dtype.  Work units as in k_apply.
+__device__ __forceinline__ float acc_op(int32_t mode, int32_t cdt, float g, float a, float div)
+{
+    if (mode == RF_ACC_MEAN) {
+        const float d = round_to_dtype(g - a, cdt);
+        const float q = round_to_dtype(d / div, cdt);
+        return round_to_dtype(a + q, cdt);
+    }
+    return round_to_dtype(g + a, cdt);
+}
+
+__global__ __launch_bounds__(WG) void k_accumulate(const rf_accum_leaf* __restrict__ leaves,
+                                                   const Seg* __restrict__ segs, int64_t nunits, int32_t mode,
+                                                   int32_t n_acc)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    int32_t s = 0, cur = -1;
+    const int32_t nseg = segs[0].nseg;
+    rf_accum_leaf L{};
+    int32_t cdt = RF_F32;
+    float div = 1.0f;
+    bool vec = false;
+    for (int64_t u = wave; u < nunits; u += nwaves) {
+        s = seek_seg(segs, nseg, s, u);
+        if (segs[s].leaf != cur) {
+            cur = segs[s].leaf;
+            L = leaves[cur];
+            cdt = L.grad_dtype == L.acc_dtype ? L.acc_dtype : RF_F32;
+            div = round_to_dtype((float)n_acc + 1.0f, cdt);  // the int32 count promoted to the compute dtype
+            vec = ((uintptr_t)L.grad % 16 == 0) && ((uintptr_t)L.acc % 16 == 0);
+        }
+        const int64_t e_begin = (u - segs[s].unit_start) * APPLY_UNIT;
+        const int64_t e_end = min(L.size, e_begin + APPLY_UNIT);
+        const int64_t v_end = vec ? e_begin + ((e_end - e_begin) / 8) * 8 : e_begin;
+        for (int64_t e0 = e_begin + lane * 8; e0 < v_end; e0 += WAVE * 8) {
+            float g[8], a[8];
+            load8_dt(L.acc, L.acc_dtype, e0, a);
+            if (mode == RF_ACC_ZERO) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) a[t] = 0.0f * a[t];
+            } else {
+                load8_dt(L.grad, L.grad_dtype, e0, g);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) a[t] = acc_op(mode, cdt, g[t], a[t], div);
+            }
+            if (L.acc_dtype == RF_F32) {
+                store8_f32(L.acc, e0, a);
+            } else {
+                uint32_t h[8];
+#pragma unroll
+                for (int t = 0; t < 8; t += 2) {
+                    const uint32_t w2 = L.acc_dtype == RF_F16 ? pack_f16x2_rne(a[t], a[t + 1])
+                                                              : pack_bf16x2_rne(a[t], a[t + 1]);
+                    h[t] = w2 & 0xFFFFu;
+                    h[t + 1] = w2 >> 16;
+                }
+                store8_bf16(L.acc, e0, h);
+            }
+        }
+        for (int64_t e = v_end + lane; e < e_end; e += WAVE) {
+            const float a = load1(L.acc, L.acc_dtype, e);
+            const float r = mode == RF_ACC_ZERO ? 0.0f * a : acc_op(mode, cdt, load1(L.grad, L.grad_dtype, e), a, div);
+            store1(L.acc, L.acc_dtype, e, r);
         }
     }
 }
@@ -936,6 +1031,24 @@ static __device__ __align__(256) uint8_t scratch[RF_NOALLOC_SCRATCH_BYTES];
 namespace {
 
 // ---- per-device state ----
+// Staging of the standalone entry points (clip, Magma, apply, accumulate):
+// a call's leaf table and work list go through a pinned host buffer and a
+// device buffer that also holds its scratch (partial sums).  A ring of
+// STAGE_RING slots per device: a slot grows (allocates) only when a call
+// needs more than any earlier one, otherwise it is reused; the event
+// recorded after the call's last launch guards its next use, and a slot is
+// held by one call at a time.  Steady-state calls allocate nothing.
+constexpr int STAGE_RING = 4;
+struct StageSlot {
+    std::mutex mu;  // held from acquire to release
+    uint8_t* host = nullptr;
+    size_t host_cap = 0;
+    uint8_t* dev = nullptr;
+    size_t dev_cap = 0;
+    hipEvent_t ev = nullptr;
+    bool pending = false;
+};
+
 constexpr int MAX_DEV = 64;
 struct DevState {
     bool ready = false;
@@ -943,9 +1056,78 @@ struct DevState {
     uint4* search = nullptr;     // this device's search_tables
     uint8_t* scratch_ptr = nullptr;  // this device's scratch
     int num_cus = 0;
+    StageSlot stage[STAGE_RING];
+    std::atomic<uint32_t> stage_next{0};
 };
 std::mutex g_mu;
 DevState g_dev[MAX_DEV];
+
+// One call's hold on a staging slot: host() is pinned memory for the
+// tables, dev() their device copy followed by the call's scratch.
+class Staged {
+public:
+    ~Staged() { release(); }
+
+    rf_status acquire(DevState* ds, size_t host_bytes, size_t dev_bytes)
+    {
+        slot_ = &ds->stage[ds->stage_next.fetch_add(1) % STAGE_RING];
+        slot_->mu.lock();
+        locked_ = true;
+        if (slot_->pending) {
+            HIP_TRY(hipEventSynchronize(slot_->ev));
+            slot_->pending = false;
+        }
+        if (!slot_->ev) HIP_TRY(hipEventCreateWithFlags(&slot_->ev, hipEventDisableTiming));
+        host_bytes = std::max<size_t>(host_bytes, 256);
+        dev_bytes = std::max<size_t>(dev_bytes, host_bytes);
+        if (slot_->host_cap < host_bytes) {
+            if (slot_->host) HIP_TRY(hipHostFree(slot_->host));
+            slot_->host = nullptr;
+            slot_->host_cap = 0;
+            HIP_TRY(hipHostMalloc((void**)&slot_->host, host_bytes, hipHostMallocDefault));
+            slot_->host_cap = host_bytes;
+        }
+        if (slot_->dev_cap < dev_bytes) {
+            if (slot_->dev) HIP_TRY(hipFree(slot_->dev));
+            slot_->dev = nullptr;
+            slot_->dev_cap = 0;
+            HIP_TRY(hipMalloc((void**)&slot_->dev, dev_bytes));
+            slot_->dev_cap = dev_bytes;
+        }
+        return RF_OK;
+    }
+
+    uint8_t* host() const { return slot_->host; }
+    uint8_t* dev() const { return slot_->dev; }
+
+    // Copies the first `bytes` of host() to dev() on the stream.
+    rf_status upload(size_t bytes, hipStream_t s)
+    {
+        if (bytes) HIP_TRY(hipMemcpyAsync(slot_->dev, slot_->host, bytes, hipMemcpyHostToDevice, s));
+        return RF_OK;
+    }
+
+    // After the call's last launch: the slot is reusable once the stream
+    // has passed this point.
+    rf_status finish(hipStream_t s)
+    {
+        HIP_TRY(hipEventRecord(slot_->ev, s));
+        slot_->pending = true;
+        release();
+        return RF_OK;
+    }
+
+private:
+    void release()
+    {
+        if (locked_) slot_->mu.unlock();
+        locked_ = false;
+    }
+    StageSlot* slot_ = nullptr;
+    bool locked_ = false;
+};
+
+inline size_t up16(size_t x) { return (x + 15) & ~(size_t)15; }
 
 // First use of a device: its arrays' addresses (with the device current,
 // since each GPU holds its own copy at its own address) and the table upload
@@ -1915,24 +2097,28 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    // One stream-ordered allocation: leaf tables, segments, partials, leaf sums, (scale, norm, finite, 0).
+    // One staging slot: leaf tables and segments (copied), then the partials,
+    // leaf sums and (scale, norm, finite, 0) the kernels write.
     const size_t o_gl = 0;
     const size_t o_cl = o_gl + sizeof(rf_adam8_leaf) * (size_t)std::max(n_leaves, 1);
-    const size_t o_sg = (o_cl + sizeof(rf_clip_leaf) * (size_t)std::max(n_leaves, 1) + 15) & ~(size_t)15;
-    const size_t o_pt = (o_sg + sizeof(Seg) * nsegs.size() + 15) & ~(size_t)15;
+    const size_t o_sg = up16(o_cl + sizeof(rf_clip_leaf) * (size_t)std::max(n_leaves, 1));
+    const size_t o_pt = up16(o_sg + sizeof(Seg) * nsegs.size());
     const size_t o_ls = o_pt + sizeof(double) * (size_t)std::max<int64_t>(nunits, 1);
-    const size_t o_cp = (o_ls + sizeof(double) * (size_t)std::max(nseg, 1) + 15) & ~(size_t)15;
+    const size_t o_cp = up16(o_ls + sizeof(double) * (size_t)std::max(nseg, 1));
     const size_t total = o_cp + 4 * sizeof(float);
-    uint8_t* buf = nullptr;
-    HIP_TRY(hipMallocAsync((void**)&buf, total, s));
-    std::vector<uint8_t> host(o_pt);
+    Staged stg;
+    st = stg.acquire(ds, o_pt, total);
+    if (st != RF_OK) return st;
+    uint8_t* const host = stg.host();
     if (n_leaves > 0) {
-        std::memcpy(host.data() + o_gl, gl.data(), sizeof(rf_adam8_leaf) * (size_t)n_leaves);
-        std::memcpy(host.data() + o_cl, leaves, sizeof(rf_clip_leaf) * (size_t)n_leaves);
+        std::memcpy(host + o_gl, gl.data(), sizeof(rf_adam8_leaf) * (size_t)n_leaves);
+        std::memcpy(host + o_cl, leaves, sizeof(rf_clip_leaf) * (size_t)n_leaves);
     }
-    std::memcpy(host.data() + o_sg, nsegs.data(), sizeof(Seg) * nsegs.size());
-    hipError_t e = hipMemcpyAsync(buf, host.data(), o_pt, hipMemcpyHostToDevice, s);
-    // hipMemcpyAsync from pageable memory returns once the source is consumed.
+    std::memcpy(host + o_sg, nsegs.data(), sizeof(Seg) * nsegs.size());
+    st = stg.upload(o_pt, s);
+    if (st != RF_OK) return st;
+    uint8_t* const buf = stg.dev();
+    hipError_t e = hipSuccess;
     const rf_adam8_leaf* d_gl = (const rf_adam8_leaf*)(buf + o_gl);
     const rf_clip_leaf* d_cl = (const rf_clip_leaf*)(buf + o_cl);
     const Seg* d_sg = (const Seg*)(buf + o_sg);
@@ -1961,10 +2147,9 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
         hipLaunchKernelGGL(k_clip_scale, dim3(gx, n_leaves), dim3(WG), 0, s, d_cl, d_cp);
         e = hipGetLastError();
     }
-    hipError_t ef = hipFreeAsync(buf, s);
+    st = stg.finish(s);
     if (e != hipSuccess) return fail(RF_ERR_HIP, std::string("rf_clip_by_global_norm: ") + hipGetErrorString(e));
-    if (ef != hipSuccess) return fail(RF_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(ef));
-    return RF_OK;
+    return st;
 }
 
 }  // extern "C"
@@ -2003,24 +2188,21 @@ rf_status magma_list(const rf_magma_leaf* leaves, int32_t n_leaves, bool need_up
     return RF_OK;
 }
 
-// Stages the leaf table and the work list in one stream-ordered
-// allocation of `extra` more bytes (returned at `*tail`).
-rf_status magma_stage(const rf_magma_leaf* leaves, int32_t n_leaves, const std::vector<Seg>& segs, size_t extra,
-                      hipStream_t s, uint8_t** buf, uint8_t** tail)
+// Stages the leaf table and the work list in a staging slot with `extra`
+// more device bytes after them (returned at `*tail`).
+rf_status magma_stage(Staged& stg, DevState* ds, const rf_magma_leaf* leaves, int32_t n_leaves,
+                      const std::vector<Seg>& segs, size_t extra, hipStream_t s, uint8_t** buf, uint8_t** tail)
 {
-    const size_t o_sg = (sizeof(rf_magma_leaf) * (size_t)std::max(n_leaves, 1) + 15) & ~(size_t)15;
-    const size_t o_tail = (o_sg + sizeof(Seg) * segs.size() + 15) & ~(size_t)15;
-    HIP_TRY(hipMallocAsync((void**)buf, o_tail + std::max<size_t>(extra, 16), s));
-    std::vector<uint8_t> host(o_tail);
-    if (n_leaves > 0) std::memcpy(host.data(), leaves, sizeof(rf_magma_leaf) * (size_t)n_leaves);
-    std::memcpy(host.data() + o_sg, segs.data(), sizeof(Seg) * segs.size());
-    // From pageable memory: returns once the source is consumed.
-    const hipError_t e = hipMemcpyAsync(*buf, host.data(), o_tail, hipMemcpyHostToDevice, s);
-    if (e != hipSuccess) {
-        (void)hipFreeAsync(*buf, s);
-        return fail(RF_ERR_HIP, std::string("hipMemcpyAsync: ") + hipGetErrorString(e));
-    }
-    *tail = *buf + o_tail;
+    const size_t o_sg = up16(sizeof(rf_magma_leaf) * (size_t)std::max(n_leaves, 1));
+    const size_t o_tail = up16(o_sg + sizeof(Seg) * segs.size());
+    rf_status st = stg.acquire(ds, o_tail, o_tail + std::max<size_t>(extra, 16));
+    if (st != RF_OK) return st;
+    if (n_leaves > 0) std::memcpy(stg.host(), leaves, sizeof(rf_magma_leaf) * (size_t)n_leaves);
+    std::memcpy(stg.host() + o_sg, segs.data(), sizeof(Seg) * segs.size());
+    st = stg.upload(o_tail, s);
+    if (st != RF_OK) return st;
+    *buf = stg.dev();
+    *tail = stg.dev() + o_tail;
     return RF_OK;
 }
 
@@ -2042,8 +2224,9 @@ rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, float b
     if (st != RF_OK) return st;
     hipStream_t s = (hipStream_t)stream;
     uint8_t *buf = nullptr, *tail = nullptr;
-    st = magma_stage(leaves, n_leaves, segs, sizeof(double) * 3 * (size_t)std::max<int64_t>(nunits, 1), s, &buf,
-                     &tail);
+    Staged stg;
+    st = magma_stage(stg, ds, leaves, n_leaves, segs, sizeof(double) * 3 * (size_t)std::max<int64_t>(nunits, 1), s,
+                     &buf, &tail);
     if (st != RF_OK) return st;
     const rf_magma_leaf* d_leaves = (const rf_magma_leaf*)buf;
     const Seg* d_segs = (const Seg*)(buf + ((sizeof(rf_magma_leaf) * (size_t)n_leaves + 15) & ~(size_t)15));
@@ -2061,10 +2244,9 @@ rf_status rf_magma_reduce(const rf_magma_leaf* leaves, int32_t n_leaves, float b
         hipLaunchKernelGGL(k_magma_leaf, dim3((unsigned)lw), dim3(WG), 0, s, d_segs, n_leaves, d_part, sums);
         e = hipGetLastError();
     }
-    const hipError_t ef = hipFreeAsync(buf, s);
+    st = stg.finish(s);
     if (e != hipSuccess) return fail(RF_ERR_HIP, std::string("rf_magma_reduce: ") + hipGetErrorString(e));
-    if (ef != hipSuccess) return fail(RF_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(ef));
-    return RF_OK;
+    return st;
 }
 
 rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const double* sums, float* scores, float p,
@@ -2088,7 +2270,8 @@ rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const do
     if (st != RF_OK) return st;
     hipStream_t s = (hipStream_t)stream;
     uint8_t *buf = nullptr, *tail = nullptr;
-    st = magma_stage(leaves, n_leaves, segs, sizeof(float) * (size_t)n_leaves, s, &buf, &tail);
+    Staged stg;
+    st = magma_stage(stg, ds, leaves, n_leaves, segs, sizeof(float) * (size_t)n_leaves, s, &buf, &tail);
     if (st != RF_OK) return st;
     const rf_magma_leaf* d_leaves = (const rf_magma_leaf*)buf;
     const Seg* d_segs = (const Seg*)(buf + ((sizeof(rf_magma_leaf) * (size_t)n_leaves + 15) & ~(size_t)15));
@@ -2103,10 +2286,9 @@ rf_status rf_magma_scale(const rf_magma_leaf* leaves, int32_t n_leaves, const do
                            neg_lr);
         e = hipGetLastError();
     }
-    const hipError_t ef = hipFreeAsync(buf, s);
+    st = stg.finish(s);
     if (e != hipSuccess) return fail(RF_ERR_HIP, std::string("rf_magma_scale: ") + hipGetErrorString(e));
-    if (ef != hipSuccess) return fail(RF_ERR_HIP, std::string("hipFreeAsync: ") + hipGetErrorString(ef));
-    return RF_OK;
+    return st;
 }
 
 rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic, uint32_t key0,
@@ -2120,6 +2302,57 @@ rf_status rf_magma_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, 
 {
     if (n_leaves > 0 && !factor) return fail(RF_ERR_INVALID, "null factor");
     return apply_launch(leaves, n_leaves, stochastic, key0, key1, factor, neg_lr, stream);
+}
+
+rf_status rf_accumulate(const rf_accum_leaf* leaves, int32_t n_leaves, int32_t mode, int32_t n_acc, void* stream)
+{
+    if (n_leaves < 0 || (n_leaves > 0 && !leaves)) return fail(RF_ERR_INVALID, "bad leaf table");
+    if (mode != RF_ACC_SUM && mode != RF_ACC_MEAN && mode != RF_ACC_ZERO) return fail(RF_ERR_INVALID, "unknown mode");
+    if (n_acc < 0) return fail(RF_ERR_INVALID, "negative n_acc");
+    thread_local std::vector<Seg> segs;
+    segs.clear();
+    int64_t nunits = 0;
+    for (int32_t i = 0; i < n_leaves; ++i) {
+        const rf_accum_leaf& L = leaves[i];
+        if (L.size < 0) return fail(RF_ERR_INVALID, "negative size");
+        if (!valid_dtype(L.grad_dtype) || !valid_dtype(L.acc_dtype))
+            return fail(RF_ERR_UNSUPPORTED, "grad and accumulator dtypes must be f32, bf16 or f16");
+        if (L.size == 0) continue;
+        if (!L.acc || (mode != RF_ACC_ZERO && !L.grad)) return fail(RF_ERR_INVALID, "null buffer");
+        Seg sg{};
+        sg.unit_start = nunits;
+        sg.leaf = i;
+        segs.push_back(sg);
+        nunits += (L.size + APPLY_UNIT - 1) / APPLY_UNIT;
+    }
+    if (nunits == 0) return RF_OK;
+    Seg sentinel{};
+    sentinel.unit_start = nunits;
+    sentinel.leaf = -1;
+    sentinel.kind = -1;
+    segs.push_back(sentinel);
+    mark_list(segs);
+    DevState* ds = nullptr;
+    rf_status st = device_state(&ds);
+    if (st != RF_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    const size_t o_sg = up16(sizeof(rf_accum_leaf) * (size_t)n_leaves);
+    const size_t bytes = o_sg + sizeof(Seg) * segs.size();
+    Staged stg;
+    st = stg.acquire(ds, bytes, bytes);
+    if (st != RF_OK) return st;
+    std::memcpy(stg.host(), leaves, sizeof(rf_accum_leaf) * (size_t)n_leaves);
+    std::memcpy(stg.host() + o_sg, segs.data(), sizeof(Seg) * segs.size());
+    st = stg.upload(bytes, s);
+    if (st != RF_OK) return st;
+    const int64_t aw = std::max<int64_t>(1, std::min<int64_t>((nunits + WAVES_PER_WG - 1) / WAVES_PER_WG,
+                                                              (int64_t)ds->num_cus * 8));
+    hipLaunchKernelGGL(k_accumulate, dim3((unsigned)aw), dim3(WG), 0, s, (const rf_accum_leaf*)stg.dev(),
+                       (const Seg*)(stg.dev() + o_sg), nunits, mode, n_acc);
+    const hipError_t le = hipGetLastError();
+    st = stg.finish(s);
+    if (le != hipSuccess) return fail(RF_ERR_HIP, std::string("k_accumulate launch: ") + hipGetErrorString(le));
+    return st;
 }
 
 }  // extern "C"
@@ -2141,20 +2374,45 @@ rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t st
         maxsize = std::max(maxsize, L.size);
     }
     if (maxsize == 0) return RF_OK;
-    if (n_leaves > 65535) return fail(RF_ERR_UNSUPPORTED, "more than 65535 leaves in one apply call");
     DevState* ds = nullptr;
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
+    // Work list: APPLY_UNIT-element units of every non-empty leaf.
+    thread_local std::vector<Seg> segs;
+    segs.clear();
+    int64_t nunits = 0;
+    for (int32_t i = 0; i < n_leaves; ++i) {
+        if (leaves[i].size == 0) continue;
+        Seg sg{};
+        sg.unit_start = nunits;
+        sg.leaf = i;
+        segs.push_back(sg);
+        nunits += (leaves[i].size + APPLY_UNIT - 1) / APPLY_UNIT;
+    }
+    Seg sentinel{};
+    sentinel.unit_start = nunits;
+    sentinel.leaf = -1;
+    sentinel.kind = -1;
+    segs.push_back(sentinel);
+    mark_list(segs);
     hipStream_t s = (hipStream_t)stream;
-    rf_apply_leaf* d = nullptr;
-    HIP_TRY(hipMallocAsync((void**)&d, sizeof(rf_apply_leaf) * (size_t)n_leaves, s));
-    HIP_TRY(hipMemcpyAsync(d, leaves, sizeof(rf_apply_leaf) * (size_t)n_leaves, hipMemcpyHostToDevice, s));
-    const int gx = (int)std::max<int64_t>(1, std::min<int64_t>((maxsize + WG - 1) / WG, (int64_t)ds->num_cus * 4));
-    hipLaunchKernelGGL(k_apply, dim3(gx, n_leaves), dim3(WG), 0, s, d, stochastic, key0, key1, factor, neg_lr);
-    hipError_t le = hipGetLastError();
-    HIP_TRY(hipFreeAsync(d, s));
+    const size_t o_sg = up16(sizeof(rf_apply_leaf) * (size_t)n_leaves);
+    const size_t bytes = o_sg + sizeof(Seg) * segs.size();
+    Staged stg;
+    st = stg.acquire(ds, bytes, bytes);
+    if (st != RF_OK) return st;
+    std::memcpy(stg.host(), leaves, sizeof(rf_apply_leaf) * (size_t)n_leaves);
+    std::memcpy(stg.host() + o_sg, segs.data(), sizeof(Seg) * segs.size());
+    st = stg.upload(bytes, s);
+    if (st != RF_OK) return st;
+    const int64_t aw = std::max<int64_t>(1, std::min<int64_t>((nunits + WAVES_PER_WG - 1) / WAVES_PER_WG,
+                                                              (int64_t)ds->num_cus * 8));
+    hipLaunchKernelGGL(k_apply, dim3((unsigned)aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
+                       (const Seg*)(stg.dev() + o_sg), nunits, stochastic, key0, key1, factor, neg_lr);
+    const hipError_t le = hipGetLastError();
+    st = stg.finish(s);
     if (le != hipSuccess) return fail(RF_ERR_HIP, std::string("k_apply launch: ") + hipGetErrorString(le));
-    return RF_OK;
+    return st;
 }
 
 }  // namespace

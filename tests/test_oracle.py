@@ -867,3 +867,127 @@ def test_f16_params_round_the_f32_step():
             wdp = (np.float16(0.01) * p16).astype(np.float32)          # f16 product, rounded once
             want = (p32 + np.float32(-1e-3) * (u + wdp)).astype(np.float16)
             np.testing.assert_array_equal(a16, want.view(np.uint16))
+
+
+# ------------------------------------------------------ optax.MultiSteps --
+def _acc_run(mode, grads, gdtype, adtype, acc0=None):
+    """Feeds the grads one micro-step at a time; returns the accumulator's
+    f32 values after each."""
+    n = np.asarray(grads[0]).size
+    acc = np.zeros(n, np.float32) if adtype == orc.F32 else np.zeros(n, np.uint16)
+    if acc0 is not None:
+        acc[:] = acc0
+    out = []
+    for i, g in enumerate(grads):
+        orc.accumulate(mode, i, g, gdtype, acc, adtype)
+        out.append(orc.to_f32(acc.copy(), adtype))
+    return out
+
+
+def test_accumulate_mean_dyadic_sequence_and_sum():
+    """Welford's running mean of 1, 2, 3, 4 is 1, 1.5, 2, 2.5 exactly (every
+    intermediate is dyadic); the sum mode gives 1, 3, 6, 10.  A divisor of
+    n_acc instead of n_acc + 1, or a dropped term, fails both."""
+    seq = [np.full(5, v, np.float32) for v in (1.0, 2.0, 3.0, 4.0)]
+    for got, want in zip(_acc_run(orc.ACC_MEAN, seq, orc.F32, orc.F32), (1.0, 1.5, 2.0, 2.5)):
+        np.testing.assert_array_equal(got, np.full(5, want, np.float32))
+    for got, want in zip(_acc_run(orc.ACC_SUM, seq, orc.F32, orc.F32), (1.0, 3.0, 6.0, 10.0)):
+        np.testing.assert_array_equal(got, np.full(5, want, np.float32))
+
+
+def test_accumulate_mean_of_a_constant_is_the_constant():
+    """(g - g) = 0 after the first micro-step, so the running mean of a
+    constant stream is that constant, bit for bit, in every dtype."""
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal(257).astype(np.float32)
+    for dt in (orc.F32, orc.BF16, orc.F16):
+        g = orc.from_f32(v, dt)
+        for got in _acc_run(orc.ACC_MEAN, [g] * 6, dt, dt):
+            np.testing.assert_array_equal(got, orc.to_f32(g, dt))
+
+
+def test_accumulate_f32_matches_numpy_float32_per_op():
+    """f32 accumulation against numpy's own float32 arithmetic, one
+    correctly rounded operation at a time."""
+    rng = np.random.default_rng(4)
+    grads = [(rng.standard_normal(1000) * 10.0 ** rng.integers(-3, 3, 1000)).astype(np.float32) for _ in range(7)]
+    a = np.zeros(1000, np.float32)
+    s = np.zeros(1000, np.float32)
+    for i, (got_m, got_s, g) in enumerate(zip(_acc_run(orc.ACC_MEAN, grads, orc.F32, orc.F32),
+                                              _acc_run(orc.ACC_SUM, grads, orc.F32, orc.F32), grads)):
+        a = a + (g - a) / np.float32(i + 1)
+        s = g + s
+        np.testing.assert_array_equal(got_m.view(np.uint32), a.view(np.uint32))
+        np.testing.assert_array_equal(got_s.view(np.uint32), s.view(np.uint32))
+
+
+def test_accumulate_f16_rounds_every_operation():
+    """Same-dtype f16 accumulation against numpy float16 arithmetic, which
+    rounds each operation to binary16; rounding once at the end (an f32
+    computation) differs on part of the sample, so the check can fail."""
+    rng = np.random.default_rng(5)
+    grads16 = [rng.standard_normal(4000).astype(np.float16) for _ in range(5)]
+    got = _acc_run(orc.ACC_MEAN, [g.view(np.uint16) for g in grads16], orc.F16, orc.F16)
+    a = np.zeros(4000, np.float16)
+    a32 = np.zeros(4000, np.float16)
+    differs = 0
+    for i, g in enumerate(grads16):
+        once = (a32.astype(np.float32) + (g.astype(np.float32) - a32.astype(np.float32)) / np.float32(i + 1))
+        a32 = a.copy()
+        a = a + (g - a) / np.float16(i + 1)
+        np.testing.assert_array_equal(got[i], a.astype(np.float32))
+        differs += int(np.sum(once.astype(np.float16) != a))
+    assert differs > 0
+    s = np.zeros(4000, np.float16)
+    for i, (g, gs) in enumerate(zip(grads16, _acc_run(orc.ACC_SUM, [g.view(np.uint16) for g in grads16],
+                                                       orc.F16, orc.F16))):
+        s = g + s
+        np.testing.assert_array_equal(gs, s.astype(np.float32))
+
+
+def test_accumulate_bf16_grads_into_f32_widen_exactly():
+    """bf16 grads into an f32 accumulator (the builders' default
+    accumulate_dtype) compute in f32 on the exactly widened grads."""
+    rng = np.random.default_rng(6)
+    v = [rng.standard_normal(333).astype(np.float32) for _ in range(4)]
+    gb = [orc.f32_to_bf16_bits(x) for x in v]
+    wide = [orc.bf16_bits_to_f32(h) for h in gb]
+    for mode in (orc.ACC_MEAN, orc.ACC_SUM):
+        for x, y in zip(_acc_run(mode, gb, orc.BF16, orc.F32), _acc_run(mode, wide, orc.F32, orc.F32)):
+            np.testing.assert_array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+def test_accumulate_reset_is_zero_times_acc():
+    """(1 - emit) * acc on the emitting micro-step: finite values become a
+    zero of their sign, Inf and NaN become NaN, which the next window's
+    running mean keeps (NaN + (g - NaN) / 1)."""
+    vals = np.array([1.5, -2.0, 0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45], np.float32)
+    for dt in (orc.F32, orc.BF16, orc.F16):
+        acc = orc.from_f32(vals, dt).copy()
+        orc.accumulate(orc.ACC_ZERO, 0, None, dt, acc, dt)
+        got = orc.to_f32(acc, dt)
+        finite = np.isfinite(vals)
+        src = orc.to_f32(orc.from_f32(vals, dt), dt)
+        np.testing.assert_array_equal(got[finite], 0.0)
+        np.testing.assert_array_equal(np.signbit(got[finite]), np.signbit(src[finite]))
+        assert np.isnan(got[~finite]).all()
+        orc.accumulate(orc.ACC_MEAN, 0, orc.from_f32(np.full(vals.size, 3.0, np.float32), dt), dt, acc, dt)
+        got = orc.to_f32(acc, dt)
+        np.testing.assert_array_equal(got[finite], 3.0)
+        assert np.isnan(got[~finite]).all()
+
+
+def test_multisteps_counters_known_sequence():
+    """optax.MultiSteps: with k = 3 the third, sixth, ... micro-steps emit;
+    mini_step cycles 0, 1, 2 and gradient_step counts the emits."""
+    mini = grad = 0
+    emits, minis, grads = [], [], []
+    for _ in range(7):
+        e, mini, grad = orc.multisteps_counters(mini, grad, 3)
+        emits.append(int(e))
+        minis.append(mini)
+        grads.append(grad)
+    assert emits == [0, 0, 1, 0, 0, 1, 0]
+    assert minis == [1, 2, 0, 1, 2, 0, 1]
+    assert grads == [0, 0, 1, 1, 1, 2, 2]
+    assert orc.multisteps_counters(0, 5, 1) == (True, 0, 6)
