@@ -28,6 +28,10 @@ Other workloads (one JSON line each, same fields):
   llama7b_finetune_groups  the same around a three-group multi_transform
                    (base / embeddings / norms with their own learning rates,
                    decays and keys), as the fine-tune builders compose it.
+  llama7b_finetune_accum4  that composition inside MultiSteps(every_k=4,
+                   f32 accumulator): a step is one window of four micro-steps
+                   (one accumulate launch each; the fourth then runs the
+                   guarded grouped step on the accumulator and resets it).
   llama7b_optax    update-only (Optax) mode over the Llama tree: f32 updates
                    written, params read for weight decay.
   llama7b_adamw_f32   full-precision AdamW (adamw, f32 moments) over the Llama
@@ -277,7 +281,7 @@ class Workload:
 
 
 def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None, clip=None,
-                   guard=False, groups=False, magma=False, moment_sr=False):
+                   guard=False, groups=False, magma=False, moment_sr=False, accum=1):
     import numpy as np
     import torch
 
@@ -314,6 +318,10 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
             chain_clip, clip = clip, None
     if guard:
         tx = rf.apply_if_finite(tx, 1)
+    if accum > 1:
+        # the builders' accumulation wrapper (AccumulationConfig defaults:
+        # mean of the micro-steps' grads in an f32 accumulator)
+        tx = rf.MultiSteps(tx, every_k_schedule=accum, use_grad_mean=True, accumulator_dtype=torch.float32)
     state = tx.init(params)
     pool = []
     rng = np.random.default_rng(0)
@@ -338,7 +346,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     key = rf.prng.PRNGKey(0)
     holder = {"params": params, "state": state, "k": 0}
 
-    def step():
+    def micro_step():
         g = pool[holder["k"] % len(pool)]
         holder["k"] += 1
         if optax:
@@ -349,6 +357,11 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         else:
             holder["params"], holder["state"] = rf.adamw8_step(tx, holder["params"], g, holder["state"], key=key,
                                                                stochastic=param_sr, clip_global_norm=clip)
+
+    def step():
+        # one optimizer step: with accumulation, a whole window of micro-steps
+        for _ in range(accum):
+            micro_step()
 
     n_quant = sum(1 for _, s in shapes if _numel(s) >= MIN_SIZE) if adam_mu is None else 0
     config = {
@@ -378,6 +391,11 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     if guard:
         config["nonfinite"] = "skip (apply_if_finite, max_consecutive_errors=1; one int32 read back per step)"
         config["launches_per_step"] = 4
+    if accum > 1:
+        config["accumulation"] = (f"MultiSteps(every_k_schedule={accum}, use_grad_mean=True, f32 accumulator) "
+                                  "around the whole transformation; a step is one window: "
+                                  f"{accum} micro-steps, the last running the inner step on the accumulator")
+        config["launches_per_step"] += accum + 1
     if magma:
         config["magma"] = ("use_magma=True (p 0.5, tau 2): sums written by the step, per-leaf factors after "
                            "it, folded into apply_updates")
@@ -390,10 +408,18 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         cpu = lambda: cpu_baseline(args.cpu_seconds, shapes=sub,  # noqa: E731
                                    sample_name=f"the first {len(sub)} leaves", param_sr=param_sr,
                                    moment_sr=moment_sr)
+    if accum > 1:
+        cpu = None  # the oracle baseline times the plain step, not a window
     metric = METRIC if workload == "llama7b_bf16_adamw8" else f"adam8 params/sec + achieved HBM GB/s, {workload}, 1 GPU"
     if adam_mu is None:
-        nbytes = step_bytes(shapes, apply=not optax) + (n_params * 2 if (clip is not None or guard or groups)
-                                                        else 0)
+        g_extra = 2 if (clip is not None or guard or groups) else 0  # the norm pre-pass's grad read
+        if accum > 1:
+            # micro-steps: bf16 grad read, f32 accumulator read and written
+            # (10 B); the inner step reads f32 grads (+2 B over bf16, and its
+            # pre-pass reads 4 B instead of 2); the reset reads and writes
+            # the accumulator (8 B)
+            g_extra = 2 * g_extra + 2 + accum * 10 + 8
+        nbytes = step_bytes(shapes, apply=not optax) + n_params * g_extra
     else:
         mb = 4 if adam_mu == "f32" else 2
         nbytes = n_params * (2 + 2 + 2 + 2 * 2 * mb)  # p r+w, g r, two moments r+w
@@ -513,6 +539,10 @@ WORKLOADS = {
                                                  param_sr=False, clip=1.0, guard=True),
     "llama7b_finetune_groups": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_grouped_finetune",
                                                         param_sr=False, clip=1.0, guard=True, groups=True),
+    "llama7b_finetune_accum4": lambda a: _tree_workload(a, llama7b_shapes,
+                                                        "llama7b_bf16_adamw8_grouped_finetune_multisteps4",
+                                                        param_sr=a.param_sr, clip=1.0, guard=True, groups=True,
+                                                        accum=4),
     "llama7b_optax": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8_optax_update",
                                               param_sr=False, optax=True),
     "llama7b_adamw_f32": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw_f32_moments",

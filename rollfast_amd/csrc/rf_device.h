@@ -188,21 +188,30 @@ __device__ __forceinline__ void threefry2x32(uint32_t k0, uint32_t k1, uint32_t 
 // The empty asm pins x0 and x1 to one register each after every round:
 // without it the compiler keeps x0 as a sum of two registers across rounds
 // and spends a second add per round on it (about 89 instead of 69 VALU
-// instructions per Threefry block).
+// instructions per Threefry block).  The fourth round of each group takes
+// the key injection before its pin: x1's xor and injection add become one
+// v_xad_u32, and x0's injection, left unpinned for one round, joins the next
+// round's add in a v_add3_u32 (64 instructions per block).
 #define RF_TF_ROUND(r)                  \
     x0 += x1;                           \
     x1 = __builtin_rotateleft32(x1, r); \
     x1 ^= x0;                           \
     __asm__("" : "+v"(x0), "+v"(x1));
-#define RF_TF_R0 RF_TF_ROUND(13) RF_TF_ROUND(15) RF_TF_ROUND(26) RF_TF_ROUND(6)
-#define RF_TF_R1 RF_TF_ROUND(17) RF_TF_ROUND(29) RF_TF_ROUND(16) RF_TF_ROUND(24)
-    RF_TF_R0 x0 += k1; x1 += k2 + 1u;
-    RF_TF_R1 x0 += k2; x1 += k0 + 2u;
-    RF_TF_R0 x0 += k0; x1 += k1 + 3u;
-    RF_TF_R1 x0 += k1; x1 += k2 + 4u;
-    RF_TF_R0 x0 += k2; x1 += k0 + 5u;
+#define RF_TF_INJECT(r, ka, kb)                         \
+    x0 += x1;                                           \
+    x1 = (__builtin_rotateleft32(x1, r) ^ x0) + (kb);   \
+    __asm__("" : "+v"(x1));                             \
+    x0 += (ka);
+#define RF_TF_R0(ka, kb) RF_TF_ROUND(13) RF_TF_ROUND(15) RF_TF_ROUND(26) RF_TF_INJECT(6, ka, kb)
+#define RF_TF_R1(ka, kb) RF_TF_ROUND(17) RF_TF_ROUND(29) RF_TF_ROUND(16) RF_TF_INJECT(24, ka, kb)
+    RF_TF_R0(k1, k2 + 1u)
+    RF_TF_R1(k2, k0 + 2u)
+    RF_TF_R0(k0, k1 + 3u)
+    RF_TF_R1(k1, k2 + 4u)
+    RF_TF_R0(k2, k0 + 5u)
 #undef RF_TF_R0
 #undef RF_TF_R1
+#undef RF_TF_INJECT
 #undef RF_TF_ROUND
     y0 = x0;
     y1 = x1;

@@ -74,17 +74,20 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const void* 
     const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
     const float* cb = (const float*)(lds + (quantizer == RF_Q_DYNAMIC_UNSIGNED ? L_CBU : L_CBS));
     auto is_full = [&](int64_t b) { return vec_ok && bs == FAST_BS && b < nblocks && b * bs + bs <= size; };
+    auto load_chunk = [&](int64_t b, int j, float (&r)[32]) {
+        float t8[8];
+        load8_dt(x, x_dtype, b * FAST_BS + j * 512 + lane * 8, t8);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) r[j * 8 + t] = t8[t];
+    };
     auto load_block = [&](int64_t b, float (&r)[32]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float t8[8];
-            load8_dt(x, x_dtype, b * FAST_BS + j * 512 + lane * 8, t8);
-#pragma unroll
-            for (int t = 0; t < 8; ++t) r[j * 8 + t] = t8[t];
-        }
+        for (int j = 0; j < 4; ++j) load_chunk(b, j, r);
     };
-    // Full 2048-blocks are double-buffered: the next block of this wave is
-    // loaded while the current one is coded.
+    // Full 2048-blocks stream through one 32-value ring per lane: once chunk
+    // j of a block is coded, its registers take chunk j of the wave's next
+    // block, so the next block's loads are in flight while the rest of the
+    // current one is coded.
     float xr[32];
     bool have = false;
     for (int64_t b = wave; b < nblocks; b += nwaves) {
@@ -133,8 +136,6 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const void* 
         };
         if (full) {
             const bool next_full = is_full(b + nwaves);
-            float xn[32];
-            if (next_full) load_block(b + nwaves, xn);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int64_t e0 = base + j * 512 + lane * 8;
@@ -163,10 +164,7 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const void* 
                 w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
                 w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
                 *(uint2*)(values + e0) = w;
-            }
-            if (next_full) {
-#pragma unroll
-                for (int i = 0; i < 32; ++i) xr[i] = xn[i];
+                if (next_full) load_chunk(b + nwaves, j, xr);
             }
             have = next_full;
         } else {
@@ -1216,6 +1214,25 @@ rf_status occupancy(const void* fn, int* blocks)
 
 int64_t nblocks_of(int64_t size, int64_t bs) { return size > 0 ? (size + bs - 1) / bs : 1; }
 
+// Grid of a work-list kernel that walks `nunits` units, one per wave at a
+// time: about STEP_UNITS_PER_WAVE units per wave, never fewer workgroups
+// than fit on the chip at once, rounded to whole chip-fulls (the kernel's
+// own occupancy), so that no last, mostly idle round of workgroups runs.
+rf_status worklist_grid(const void* fn, const DevState* ds, int64_t nunits, unsigned* grid)
+{
+    int occ = 1;
+    const rf_status st = occupancy(fn, &occ);
+    if (st != RF_OK) return st;
+    const int64_t wg_needed = std::max<int64_t>(1, (nunits + WAVES_PER_WG - 1) / WAVES_PER_WG);
+    const int64_t resident = (int64_t)ds->num_cus * occ;
+    const int64_t spread = (nunits + (int64_t)WAVES_PER_WG * STEP_UNITS_PER_WAVE - 1) /
+                           ((int64_t)WAVES_PER_WG * STEP_UNITS_PER_WAVE);
+    int64_t g = std::min(wg_needed, std::max(resident, spread));
+    if (g > resident) g = std::min(wg_needed, std::max<int64_t>(1, (g + resident / 2) / resident) * resident);
+    *grid = (unsigned)std::max<int64_t>(1, g);
+    return RF_OK;
+}
+
 }  // namespace
 
 // ---- plan ----
@@ -1995,13 +2012,10 @@ rf_status rf_blockwise_quantize(int32_t quantizer, const void* x, int32_t x_dtyp
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
     const int64_t nb = nblocks_of(size, block_size);
-    int occ = 1;
-    st = occupancy((const void*)&k_quantize, &occ);
+    // One wave per block at a time, about STEP_UNITS_PER_WAVE blocks per wave.
+    unsigned grid = 1;
+    st = worklist_grid((const void*)&k_quantize, ds, nb, &grid);
     if (st != RF_OK) return st;
-    // One wave per block, about STEP_UNITS_PER_WAVE blocks per wave (as the step).
-    const int64_t wg_needed = (nb + WAVES_PER_WG - 1) / WAVES_PER_WG;
-    const int64_t wg_spread = (wg_needed + STEP_UNITS_PER_WAVE - 1) / STEP_UNITS_PER_WAVE;
-    const int grid = (int)std::max<int64_t>(1, std::max(std::min(wg_needed, (int64_t)ds->num_cus * occ), wg_spread));
     const int32_t vec_ok = aligned(x, 16) && aligned(values, 8) && (!bits || aligned(bits, 16));
     hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(WG), 0, (hipStream_t)stream, quantizer, x, x_dtype, size,
                        (int64_t)block_size, nb, sr, key0, key1, bits, (uint8_t*)values, scales, scale_dtype,
@@ -2336,6 +2350,9 @@ rf_status rf_accumulate(const rf_accum_leaf* leaves, int32_t n_leaves, int32_t m
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
     hipStream_t s = (hipStream_t)stream;
+    unsigned aw = 1;  // before the staging slot: an error here leaves nothing in flight
+    st = worklist_grid((const void*)&k_accumulate, ds, nunits, &aw);
+    if (st != RF_OK) return st;
     const size_t o_sg = up16(sizeof(rf_accum_leaf) * (size_t)n_leaves);
     const size_t bytes = o_sg + sizeof(Seg) * segs.size();
     Staged stg;
@@ -2345,9 +2362,7 @@ rf_status rf_accumulate(const rf_accum_leaf* leaves, int32_t n_leaves, int32_t m
     std::memcpy(stg.host() + o_sg, segs.data(), sizeof(Seg) * segs.size());
     st = stg.upload(bytes, s);
     if (st != RF_OK) return st;
-    const int64_t aw = std::max<int64_t>(1, std::min<int64_t>((nunits + WAVES_PER_WG - 1) / WAVES_PER_WG,
-                                                              (int64_t)ds->num_cus * 8));
-    hipLaunchKernelGGL(k_accumulate, dim3((unsigned)aw), dim3(WG), 0, s, (const rf_accum_leaf*)stg.dev(),
+    hipLaunchKernelGGL(k_accumulate, dim3(aw), dim3(WG), 0, s, (const rf_accum_leaf*)stg.dev(),
                        (const Seg*)(stg.dev() + o_sg), nunits, mode, n_acc);
     const hipError_t le = hipGetLastError();
     st = stg.finish(s);
@@ -2396,6 +2411,9 @@ rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t st
     segs.push_back(sentinel);
     mark_list(segs);
     hipStream_t s = (hipStream_t)stream;
+    unsigned aw = 1;  // before the staging slot: an error here leaves nothing in flight
+    st = worklist_grid((const void*)&k_apply, ds, nunits, &aw);
+    if (st != RF_OK) return st;
     const size_t o_sg = up16(sizeof(rf_apply_leaf) * (size_t)n_leaves);
     const size_t bytes = o_sg + sizeof(Seg) * segs.size();
     Staged stg;
@@ -2405,9 +2423,7 @@ rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t st
     std::memcpy(stg.host() + o_sg, segs.data(), sizeof(Seg) * segs.size());
     st = stg.upload(bytes, s);
     if (st != RF_OK) return st;
-    const int64_t aw = std::max<int64_t>(1, std::min<int64_t>((nunits + WAVES_PER_WG - 1) / WAVES_PER_WG,
-                                                              (int64_t)ds->num_cus * 8));
-    hipLaunchKernelGGL(k_apply, dim3((unsigned)aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
+    hipLaunchKernelGGL(k_apply, dim3(aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
                        (const Seg*)(stg.dev() + o_sg), nunits, stochastic, key0, key1, factor, neg_lr);
     const hipError_t le = hipGetLastError();
     st = stg.finish(s);
