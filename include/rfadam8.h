@@ -398,6 +398,12 @@ RF_API rf_status rf_host_table_codes(int32_t quantizer, uint32_t first_bits, int
  * `out` is host memory). */
 RF_API rf_status rf_host_search_index(int32_t quantizer, uint32_t first_bits, int64_t count, uint16_t* out);
 
+/* Host-side: the 256 neighbour records {cb[li], cb[ui] - cb[li], RN(1 / that
+ * gap) or 0, 0} (li = max(ui - 1, 0)) from which the moment-SR kernels form
+ * the Bernoulli probability (n - cb[li]) / (cb[ui] - cb[li]) of
+ * adam8.py:558-560 (diagnostics of the tables; `out1024` is host memory). */
+RF_API rf_status rf_host_sr_records(int32_t quantizer, float* out1024);
+
 /* Library version string. */
 RF_API const char* rf_version(void);
 

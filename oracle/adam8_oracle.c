@@ -653,6 +653,20 @@ ORC_API void orc_accumulate(int mode, int32_t n_acc, int gdtype, const void* gra
     }
 }
 
+/* Check helper, not a restatement: the moment-SR kernels' probability
+ * quotient from a reciprocal y of the gap d, q0 = a*y, r = fma(-d, q0, a),
+ * p = fma(r, y, q0), over an array of a.  The tables test holds it to the
+ * IEEE quotient a / d that adam8.py:558-560 computes. */
+ORC_API void orc_recip_quotient(const float* a, int64_t n, float d, float y, float* out)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        const float q0 = a[i] * y;
+        const float r = fmaf(-d, q0, a[i]);
+        out[i] = fmaf(r, y, q0);
+    }
+}
+
 /* utils.py:342-371 _stochastic_round_bf16 over an array with fed bits. */
 ORC_API void orc_sr_bf16(const float* x, const uint32_t* bits, int64_t n, uint16_t* out)
 {

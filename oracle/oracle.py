@@ -85,6 +85,7 @@ def lib() -> ctypes.CDLL:
         ]
         _lib.orc_apply_updates.argtypes = [ctypes.c_int, p, p, i64, ctypes.c_int, p]
         _lib.orc_accumulate.argtypes = [ctypes.c_int, ctypes.c_int32, ctypes.c_int, p, ctypes.c_int, p, i64]
+        _lib.orc_recip_quotient.argtypes = [p, i64, ctypes.c_float, ctypes.c_float, p]
         _lib.orc_sr_bf16.argtypes = [p, p, i64, p]
         _lib.orc_f32_to_bf16.argtypes = [p, i64, p]
         _lib.orc_f32_to_f16.argtypes = [p, i64, p]
@@ -375,6 +376,15 @@ def accumulate(mode: int, n_acc: int, grad, gdtype: int, acc: np.ndarray, adtype
         g = np.ascontiguousarray(grad, dtype=np.float32 if gdtype == F32 else np.uint16).reshape(-1)
         assert g.size == acc.size
     lib().orc_accumulate(int(mode), int(n_acc), int(gdtype), _ptr(g), int(adtype), _ptr(acc), acc.size)
+
+
+def recip_quotient(a: np.ndarray, d: float, y: float) -> np.ndarray:
+    """Check helper: fma(fma(-d, a*y, a), y, a*y) per element (the
+    moment-SR kernels' probability from the gap's reciprocal y)."""
+    a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    out = np.empty(a.size, dtype=np.float32)
+    lib().orc_recip_quotient(_ptr(a), a.size, ctypes.c_float(d), ctypes.c_float(y), _ptr(out))
+    return out
 
 
 def multisteps_counters(mini_step: int, gradient_step: int, k_steps: int):

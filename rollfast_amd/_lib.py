@@ -175,6 +175,7 @@ EXPORTS = (
     "rf_codebook",
     "rf_host_table_codes",
     "rf_host_search_index",
+    "rf_host_sr_records",
     "rf_version",
     "rf_last_error",
 )
@@ -219,6 +220,7 @@ def lib() -> ctypes.CDLL:
     L.rf_codebook.argtypes = [i32, _p]
     L.rf_host_table_codes.argtypes = [i32, u32, i64, _p]
     L.rf_host_search_index.argtypes = [i32, u32, i64, _p]
+    L.rf_host_sr_records.argtypes = [i32, _p]
     for name in EXPORTS:
         if name not in ("rf_version", "rf_last_error"):
             getattr(L, name).restype = i32
@@ -286,6 +288,14 @@ def host_search_index(quantizer: int, first_bits: int, count: int) -> np.ndarray
     out = np.empty(int(count), dtype=np.uint16)
     check(lib().rf_host_search_index(quantizer, int(first_bits), int(count), out.ctypes.data_as(_p)),
           "rf_host_search_index")
+    return out
+
+
+def host_sr_records(quantizer: int) -> np.ndarray:
+    """The moment-SR neighbour records [256, 4] (cb[li], gap, RN(1/gap) or
+    0, 0) of a dynamic codebook."""
+    out = np.empty((256, 4), dtype=np.float32)
+    check(lib().rf_host_sr_records(quantizer, out.ctypes.data_as(_p)), "rf_host_sr_records")
     return out
 
 

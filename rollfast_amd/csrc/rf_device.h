@@ -276,10 +276,12 @@ __device__ __forceinline__ double wave_sum_f64(double x)
     return x;
 }
 
+// Copies the first BYTES of a table image into the workgroup's LDS.
+template <uint32_t BYTES = TABLE_BYTES>
 __device__ __forceinline__ void stage_tables(uint8_t* lds, const uint4* __restrict__ tables)
 {
     uint4* dst = (uint4*)lds;
-    for (uint32_t i = threadIdx.x; i < TABLE_BYTES / 16; i += WG) dst[i] = tables[i];
+    for (uint32_t i = threadIdx.x; i < BYTES / 16; i += WG) dst[i] = tables[i];
     __syncthreads();
 }
 
@@ -346,17 +348,25 @@ __device__ __forceinline__ uint32_t cand_unsigned(const uint8_t* lds, float n)
 // searchsorted candidate `cand` (the search image's candidate byte of n's
 // cell): _quantize_to_codebook's SR branch (adam8.py:549-564).
 // ui = searchsorted_left(cb, n) = cand + (cb[cand] < n), li = ui - 1 (at
-// least 0), p = (n - cb[li]) / (cb[ui] - cb[li]) in IEEE f32 (0 when the
-// two coincide), upper code iff uniform(bits) < p.  A value below cb[0]
-// counts no entry (ui = li = 0, p = 0), which is the reference's clip.
-__device__ __forceinline__ uint32_t sr_code(const float* cb, uint32_t cand, float n, uint32_t bits)
+// least 0), p = (n - cb[li]) / (cb[ui] - cb[li]) (0 when the two coincide),
+// upper code iff uniform(bits) < p.  `rec` holds per ui {cb[li], gap, y =
+// RN(1/gap) or 0}: p = fma(r, y, q0) with q0 = a*y and r = fma(-gap, q0, a)
+// (a = n - cb[li]) is the IEEE quotient's Bernoulli decision for every
+// uniform value (a reciprocal correctly rounded and one Markstein
+// correction; the tables test checks it against IEEE division over every
+// gap), and 0 for ui = 0.  Since cb[li] < n <= cb[ui], 0 <= p <= 1 needs no
+// clip.  A value below cb[0] counts no entry (ui = li = 0, p = 0), which is
+// the reference's clip.
+__device__ __forceinline__ uint32_t sr_code(const float* cb, const float4* rec, uint32_t cand, float n,
+                                            uint32_t bits)
 {
     const uint32_t ui = cand + (cb[cand] < n ? 1u : 0u);
-    const uint32_t li = ui > 0u ? ui - 1u : 0u;
-    const float uv = cb[ui], lv = cb[li];
-    const float den = uv - lv;
-    float p = den > 0.0f ? (n - lv) / den : 0.0f;
-    p = p < 0.0f ? 0.0f : (p > 1.0f ? 1.0f : p);
+    const float4 nb = rec[ui];
+    const float a = n - nb.x;
+    const float q0 = a * nb.z;
+    const float r = __builtin_fmaf(-nb.y, q0, a);
+    const float p = __builtin_fmaf(r, nb.z, q0);
+    const uint32_t li = __builtin_elementwise_sub_sat(ui, 1u);
     return uniform_from_bits(bits) < p ? ui : li;
 }
 
@@ -1087,51 +1097,83 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
         const float rsv = 1.0f / sv;
         RF_GLOBAL uint8_t* mW = (RF_GLOBAL uint8_t*)L.mu + base;
         RF_GLOBAL uint8_t* vW = (RF_GLOBAL uint8_t*)L.nu + base;
+        if constexpr (MSR) {
+            // Bernoulli rounding between the searchsorted neighbours
+            // (adam8.py:549-564) with the random bits of the padded
+            // [nblocks, bs] moment arrays: fed, or jax.random.bits of the
+            // leaf keys.  The first moment is coded over the whole block
+            // before the second, so that only one moment's bits, quotients
+            // and candidates are live beside the block's values, and the
+            // first moment's registers are free for the second's pass.
+            // Moment-SR launches stage the search image: the candidates are
+            // searchsorted counts.
+            const float* cbs = (const float*)(c.lds + L_CBS);
+            const float* cbu = (const float*)(c.lds + L_CBU);
+            const float4* srs = (const float4*)(c.lds + L_SRS);
+            const float4* sru = (const float4*)(c.lds + L_SRU);
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
-            // Batched phases (normalise + cell, candidate reads, threshold
-            // or codebook reads) keep 16 independent LDS reads in flight
-            // instead of 16 dependent read pairs.
-            uint32_t bm[8], bv[8];
-            if constexpr (MSR) {
-                // random bits of the padded [nblocks, bs] moment arrays
-                // (adam8.py:554-564): fed, or jax.random.bits of the leaf keys
+            for (int j = 0; j < J; ++j) {
+                const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
+                uint32_t b[8], cc[8];
+                float n[8];
                 if (c.fed) {
-                    load8_u32(L.mu_bits, base + eo, bm);
-                    load8_u32(L.nu_bits, base + eo, bv);
+                    load8_u32(L.mu_bits, base + eo, b);
                 } else {
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        bm[t] = jax_bits(c.kmu0, c.kmu1, (uint64_t)(base + eo + t));
-                        bv[t] = jax_bits(c.knu0, c.knu1, (uint64_t)(base + eo + t));
-                    }
+                    for (int t = 0; t < 8; ++t) b[t] = jax_bits(c.kmu0, c.kmu1, (uint64_t)(base + eo + t));
                 }
-            }
-            float nm[8], nv[8];
-            uint32_t cm[8], cv[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                nm[t] = div_by_scale(m[j][t], sm, rsm);
-                nv[t] = div_by_scale(v[j][t], sv, rsv);
+                for (int t = 0; t < 8; ++t) n[t] = div_by_scale(m[j][t], sm, rsm);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) cc[t] = cand_signed(c.lds, n[t]);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) cc[t] = sr_code(cbs, srs, cc[t], n[t], b[t]);
+                uint2 w;
+                w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
+                w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
+                *(RF_GLOBAL uint2*)(mW + eo) = w;
             }
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                cm[t] = cand_signed(c.lds, nm[t]);
-                cv[t] = cand_unsigned(c.lds, nv[t]);
+            for (int j = 0; j < J; ++j) {
+                const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
+                uint32_t b[8], cc[8];
+                float n[8];
+                if (c.fed) {
+                    load8_u32(L.nu_bits, base + eo, b);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) b[t] = jax_bits(c.knu0, c.knu1, (uint64_t)(base + eo + t));
+                }
+#pragma unroll
+                for (int t = 0; t < 8; ++t) n[t] = div_by_scale(v[j][t], sv, rsv);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) cc[t] = cand_unsigned(c.lds, n[t]);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) cc[t] = sr_code(cbu, sru, cc[t], n[t], b[t]);
+                uint2 w;
+                w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
+                w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
+                *(RF_GLOBAL uint2*)(vW + eo) = w;
             }
-            if constexpr (MSR) {
-                // moment SR launches stage the search image: the candidates
-                // are searchsorted counts
-                const float* cbs = (const float*)(c.lds + L_CBS);
-                const float* cbu = (const float*)(c.lds + L_CBU);
+        } else {
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
+                // Batched phases (normalise + cell, candidate reads,
+                // threshold reads) keep 16 independent LDS reads in flight
+                // instead of 16 dependent read pairs.
+                float nm[8], nv[8], tm[8], tv[8];
+                uint32_t cm[8], cv[8];
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
-                    cm[t] = sr_code(cbs, cm[t], nm[t], bm[t]);
-                    cv[t] = sr_code(cbu, cv[t], nv[t], bv[t]);
+                    nm[t] = div_by_scale(m[j][t], sm, rsm);
+                    nv[t] = div_by_scale(v[j][t], sv, rsv);
                 }
-            } else {
-                float tm[8], tv[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    cm[t] = cand_signed(c.lds, nm[t]);
+                    cv[t] = cand_unsigned(c.lds, nv[t]);
+                }
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
                     tm[t] = *(const float*)(c.lds + L_TS + cm[t] * 4u);
@@ -1142,14 +1184,14 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                     cm[t] += nm[t] >= tm[t] ? 1u : 0u;
                     cv[t] += nv[t] >= tv[t] ? 1u : 0u;
                 }
+                uint2 wm, wv;
+                wm.x = pack4_u8(cm[0], cm[1], cm[2], cm[3]);
+                wm.y = pack4_u8(cm[4], cm[5], cm[6], cm[7]);
+                wv.x = pack4_u8(cv[0], cv[1], cv[2], cv[3]);
+                wv.y = pack4_u8(cv[4], cv[5], cv[6], cv[7]);
+                *(RF_GLOBAL uint2*)(mW + eo) = wm;
+                *(RF_GLOBAL uint2*)(vW + eo) = wv;
             }
-            uint2 wm, wv;
-            wm.x = pack4_u8(cm[0], cm[1], cm[2], cm[3]);
-            wm.y = pack4_u8(cm[4], cm[5], cm[6], cm[7]);
-            wv.x = pack4_u8(cv[0], cv[1], cv[2], cv[3]);
-            wv.y = pack4_u8(cv[4], cv[5], cv[6], cv[7]);
-            *(RF_GLOBAL uint2*)(mW + eo) = wm;
-            *(RF_GLOBAL uint2*)(vW + eo) = wv;
         }
         if (lane == 0) {
             store_scale(L.mu_scales, L.flags, blk, sm);
@@ -1503,9 +1545,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     const rf_adam8_leaf* __restrict__ leaves, const Seg* __restrict__ segs, int64_t total_units, KHp h,
     const uint4* __restrict__ tables)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
+    // moment-SR launches stage the search image with its neighbour records
+    constexpr uint32_t LDS_TABLES = MSR ? SEARCH_BYTES : TABLE_BYTES;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_TABLES];
     __shared__ __attribute__((aligned(16))) float wtab[WAVES_PER_WG][512];
-    stage_tables(lds, tables);
+    stage_tables<LDS_TABLES>(lds, tables);
 
     const uint32_t wave_in_wg = uniform_u32(threadIdx.x / WAVE);
     const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + wave_in_wg;

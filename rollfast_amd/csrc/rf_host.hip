@@ -944,12 +944,46 @@ const HostTables& host_tables()
     return t;
 }
 
+// The f32 nearest to 1/d (ties to even) for a positive finite f32 d: y*d is
+// exact in double, so |y*d - 1| = d*|y - 1/d| ranks the candidates exactly.
+float rcp_rn(float d)
+{
+    float best = (float)(1.0 / (double)d);
+    double err = std::fabs((double)best * (double)d - 1.0);
+    const float around[2] = {std::nextafter(best, 0.0f), std::nextafter(best, INFINITY)};
+    for (float c : around) {
+        const double e = std::fabs((double)c * (double)d - 1.0);
+        if (e < err || (e == err && (fbits(c) & 1u) == 0u)) {
+            best = c;
+            err = e;
+        }
+    }
+    return best;
+}
+
+// Neighbour records of the moment-SR code choice for one codebook: per
+// ui, {cb[li], cb[ui] - cb[li] (f32), RN(1 / that gap) or 0, 0} with
+// li = max(ui - 1, 0).
+void fill_sr_records(const float* cb, float* rec)
+{
+    for (int ui = 0; ui < 256; ++ui) {
+        const float lv = cb[ui > 0 ? ui - 1 : 0];
+        const float d = cb[ui] - lv;
+        rec[4 * ui + 0] = lv;
+        rec[4 * ui + 1] = d;
+        rec[4 * ui + 2] = d > 0.0f ? rcp_rn(d) : 0.0f;
+        rec[4 * ui + 3] = 0.0f;
+    }
+}
+
 // The image moment-SR launches stage instead: the same layout, with search
-// candidates in the candidate regions (the threshold regions are unused).
+// candidates in the candidate regions (the threshold regions are unused),
+// followed by the neighbour records.
 HostTables build_search_tables()
 {
     HostTables ht = build_tables();
     if (!ht.error.empty()) return ht;
+    ht.bytes.resize(SEARCH_BYTES, 0);
     uint8_t* b = ht.bytes.data();
     const float* cbs = (const float*)(b + L_CBS);
     const float* cbu = (const float*)(b + L_CBU);
@@ -958,6 +992,8 @@ HostTables build_search_tables()
     if (!fill_search_cells(cbs, false, b + L_CANDS, ht.error)) return ht;
     if (!fill_search_cells(cbs, true, b + L_CANDS + CANDS_SIGN_STRIDE, ht.error)) return ht;
     if (!fill_search_cells(cbu, false, b + L_CANDU, ht.error)) return ht;
+    fill_sr_records(cbs, (float*)(b + L_SRS));
+    fill_sr_records(cbu, (float*)(b + L_SRU));
     return ht;
 }
 
@@ -1017,7 +1053,7 @@ uint32_t host_table_code(const uint8_t* tb, int32_t quantizer, float n)
 static __device__ __align__(256) uint4 lookup_tables[TABLE_BYTES / 16];
 // The same for moment stochastic rounding: search candidates (searchsorted
 // indices) instead of nearest-code thresholds.
-static __device__ __align__(256) uint4 search_tables[TABLE_BYTES / 16];
+static __device__ __align__(256) uint4 search_tables[SEARCH_BYTES / 16];
 // rf_adam8_step_noalloc's working memory: the leaf and group tables, the work
 // lists and the norm pre-pass's partial sums of one call.  Every call on a
 // GPU shares that GPU's copy and leaves its contents behind; nothing in it
@@ -1149,7 +1185,7 @@ rf_status device_state(DevState** out)
         if (!d.tables || !d.search || !d.scratch_ptr)
             return fail(RF_ERR_HIP, "hipGetSymbolAddress returned a null address");
         HIP_TRY(hipMemcpy(d.tables, ht.bytes.data(), TABLE_BYTES, hipMemcpyHostToDevice));
-        HIP_TRY(hipMemcpy(d.search, hs.bytes.data(), TABLE_BYTES, hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpy(d.search, hs.bytes.data(), SEARCH_BYTES, hipMemcpyHostToDevice));
         d.ready = true;
     }
     *out = &d;
@@ -1536,6 +1572,17 @@ rf_status rf_host_table_codes(int32_t quantizer, uint32_t first_bits, int64_t co
     if (!ht.error.empty()) return fail(RF_ERR_INVALID, ht.error);
     for (int64_t i = 0; i < count; ++i)
         out[i] = (uint8_t)host_table_code(ht.bytes.data(), quantizer, bitsf(first_bits + (uint32_t)i));
+    return RF_OK;
+}
+
+rf_status rf_host_sr_records(int32_t quantizer, float* out1024)
+{
+    if (!out1024) return fail(RF_ERR_INVALID, "null output");
+    if (quantizer != RF_Q_DYNAMIC_SIGNED && quantizer != RF_Q_DYNAMIC_UNSIGNED)
+        return fail(RF_ERR_INVALID, "quantizer must be dynamic signed or unsigned");
+    const HostTables& hs = host_search_tables();
+    if (!hs.error.empty()) return fail(RF_ERR_INVALID, hs.error);
+    std::memcpy(out1024, hs.bytes.data() + (quantizer == RF_Q_DYNAMIC_SIGNED ? L_SRS : L_SRU), 4096);
     return RF_OK;
 }
 

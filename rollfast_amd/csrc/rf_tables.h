@@ -24,7 +24,15 @@
 // (adam8.py:549-564).  Its launches stage a second image of the same layout
 // whose candidate regions hold, per cell, the number of codebook entries
 // below the cell's low end; a cell holds at most one entry (checked), so
-// ui = cand + (cb[cand] < n).  Its threshold regions are unused.
+// ui = cand + (cb[cand] < n).  Its threshold regions are unused.  After the
+// shared layout the search image holds, per codebook and per ui, the
+// neighbour record {cb[li], cb[ui] - cb[li], y, 0} with li = max(ui - 1, 0)
+// and y = RN(1 / (cb[ui] - cb[li])) (0 where the two coincide, ui = 0): the
+// probability p = (n - cb[li]) / (cb[ui] - cb[li]) is then formed as
+// q0 = a*y, r = fma(-d, q0, a), p = fma(r, y, q0), which equals the IEEE
+// quotient wherever the Bernoulli draw can tell them apart (the host's
+// tables test holds it to IEEE division over every gap), and is 0 for ui = 0
+// without a branch.
 //
 // Byte layout (identical in global memory and in LDS).  The two sign halves
 // of the signed candidates sit CANDS_SIGN_STRIDE (a power of two) apart, so
@@ -37,6 +45,8 @@
 //   [L_CBS]      f32 cb_signed[256]
 //   [L_CBU]      f32 cb_unsigned[256]
 //   [L_CANDU]    u8  unsigned candidates          [NCELL_PAD]
+//   [L_SRS]      float4 signed neighbour records [256]    (search image only)
+//   [L_SRU]      float4 unsigned neighbour records [256]  (search image only)
 #pragma once
 #include <stdint.h>
 
@@ -60,6 +70,9 @@ constexpr uint32_t TABLE_BYTES = L_CANDU + NCELL_PAD;
 static_assert(NCELL_PAD <= CANDS_SIGN_STRIDE, "a cell index fits below the sign bit");
 static_assert(L_TU + 1024 <= L_CANDS + CANDS_SIGN_STRIDE, "thresholds fit between the sign halves");
 static_assert(NCELL_PAD % 16 == 0 && TABLE_BYTES % 16 == 0, "tables are copied in 16-byte words");
+constexpr uint32_t L_SRS = TABLE_BYTES;
+constexpr uint32_t L_SRU = L_SRS + 256 * 16;
+constexpr uint32_t SEARCH_BYTES = L_SRU + 256 * 16;
 
 // Fast requantization is exact when the block scale s satisfies
 // FAST_SCALE_MIN <= s < inf: the reciprocal-and-correct division

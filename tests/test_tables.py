@@ -134,3 +134,62 @@ def test_search_index_exhaustive(q, lo, hi):
         bad = np.nonzero(got != want)[0]
         assert bad.size == 0, f"first mismatch at 0x{start + int(bad[0]):08x}: got {got[bad[0]]} want {want[bad[0]]}"
         start += count
+
+
+@pytest.mark.parametrize("q,signed", [(orc.Q_SIGNED, True), (orc.Q_UNSIGNED, False)])
+def test_sr_records_and_reciprocal_quotient(q, signed):
+    """The moment-SR neighbour records: cb[li], the f32 gap cb[ui] - cb[li]
+    and the f32 nearest to 1/gap (exact rationals; 0 for an empty gap); and
+    the kernels' quotient fma(fma(-d, a*y, a), y, a*y) against IEEE a / d
+    (numpy float32) over dense samples of a in [0, d] for every gap: the
+    Bernoulli draw (uniform < p, uniform a multiple of 2^-23,
+    adam8.py:558-564) must decide alike for every uniform value."""
+    from fractions import Fraction
+
+    cb = orc.codebook(signed)
+    rec = _lib.host_sr_records(q)
+    rng = np.random.default_rng(21)
+    exact_equal = total = 0
+    for ui in range(256):
+        li = max(ui - 1, 0)
+        d = np.float32(cb[ui]) - np.float32(cb[li])
+        assert rec[ui, 0] == cb[li] and rec[ui, 1] == d and rec[ui, 3] == 0.0, ui
+        y = rec[ui, 2]
+        if d == 0.0:
+            assert ui == 0 and y == 0.0
+            continue
+        inv = 1 / Fraction(float(d))
+        err = abs(Fraction(float(y)) - inv)
+        for c in (np.nextafter(y, np.float32(0)), np.nextafter(y, np.float32(np.inf))):
+            assert abs(Fraction(float(c)) - inv) >= err, ui
+        # a: rounded multiples k * 2^-23 * d (where p crosses the draw's grid)
+        # and their neighbours, random patterns in [0, d], and the ends
+        k = rng.integers(0, 1 << 23, 4000).astype(np.float64)
+        base = (k * 2.0 ** -23 * float(d)).astype(np.float32)
+        near = [base]
+        for step in (1, 2, 3):
+            up, down = base.copy(), base.copy()
+            for _ in range(step):
+                up = np.nextafter(up, np.float32(np.inf))
+                down = np.nextafter(down, np.float32(0))
+            near += [up, down]
+        rand = rng.integers(0, int(np.float32(d).view(np.uint32)) + 1, 8000).astype(np.uint32).view(np.float32)
+        ends = np.array([0.0, 1e-45, 2e-45, 1.2e-38, d, np.nextafter(d, np.float32(0))], np.float32)
+        a = np.concatenate(near + [rand, ends])
+        a = a[(a >= 0) & (a <= d)]
+        got = orc.recip_quotient(a, float(d), float(y)).astype(np.float64)
+        want = (a / d).astype(np.float32).astype(np.float64)
+        grid = 2.0 ** 23
+        bad = np.nonzero(np.ceil(got * grid) != np.ceil(want * grid))[0]
+        assert bad.size == 0, f"ui={ui} a={a[bad[0]]!r} p={got[bad[0]]!r} ieee={want[bad[0]]!r}"
+        assert (got >= 0).all() and (got <= 1).all()
+        assert ((got > 0) == (want > 0)).all(), ui
+        # the quotient is the IEEE one itself wherever p >= 2^-90; below, a
+        # subnormal a makes the correction term inexact (p < 2^-96 there),
+        # which only the sign of p could show to the draw
+        big = want >= 2.0 ** -90
+        diff = np.nonzero(big & (got != want))[0]
+        assert diff.size == 0, f"ui={ui} a={a[diff[0]]!r} p={got[diff[0]]!r} ieee={want[diff[0]]!r}"
+        exact_equal += int(np.sum(got == want))
+        total += a.size
+    assert exact_equal > 0.99 * total, (exact_equal, total)
