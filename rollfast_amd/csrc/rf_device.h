@@ -1015,15 +1015,6 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
 #pragma unroll
             for (int t = 0; t < 8; ++t) p[t] = 0.0f;
         }
-        uint32_t rb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if constexpr (PSR) {
-            if (c.fed) {
-                load8_u32(L.param_bits, e0, rb);
-            } else {
-#pragma unroll
-                for (int t = 0; t < 8; ++t) rb[t] = jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
-            }
-        }
         float u[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -1064,6 +1055,16 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             if constexpr (H16P) {
                 uint32_t w[4];
                 if constexpr (PSR && IS_BF16<PT>) {
+                    // the rounding bits (fed, or jax.random.bits of the
+                    // leaf's param key) drawn after the arithmetic: they are
+                    // not live through it
+                    uint32_t rb[8];
+                    if (c.fed) {
+                        load8_u32(L.param_bits, e0, rb);
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) rb[t] = jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
+                    }
 #pragma unroll
                     for (int t = 0; t < 8; t += 2) w[t / 2] = sr_bf16(sum[t], rb[t]) | (sr_bf16(sum[t + 1], rb[t + 1]) << 16);
                 } else {
