@@ -1335,35 +1335,41 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
     const bool msum = !APPLY && c.mpart != nullptr;  // Magma sums: update-only launches
     MagmaAcc acc;
 
-    // Two chunks in flight: chunk j+1's loads are issued before chunk j's
-    // arithmetic.
-    Raw8<GT> graw[2];
-    Raw8<PT> praw[2];
-    Raw8<MT> mraw[2], vraw[2];
-    auto issue = [&](int j, int slot) {
+    // Two chunks in flight: chunk j+1's loads are issued into `nxt` before
+    // chunk j's arithmetic on `cur`, and move to `cur` after it.  No buffer
+    // is indexed by the chunk: with param SR (three Threefry streams
+    // inlined) the compiler does not unroll this loop, and a slot index
+    // j & 1 would put both buffers in scratch memory and wait for every
+    // load at once.  Unrolled instances rename the moves away.
+    struct Bufs {
+        Raw8<GT> g;
+        Raw8<PT> p;
+        Raw8<MT> m, v;
+    } cur, nxt;
+    auto issue = [&](int j, Bufs& b) {
         const int64_t e0 = base + j * 512 + lane * 8;
-        raw8_load<GT>(graw[slot], L.grad, e0);
-        if (need_p) raw8_load<PT>(praw[slot], L.param, e0);
-        raw8_load<MT>(mraw[slot], L.mu, e0);
-        raw8_load<MT>(vraw[slot], L.nu, e0);
+        raw8_load<GT>(b.g, L.grad, e0);
+        if (need_p) raw8_load<PT>(b.p, L.param, e0);
+        raw8_load<MT>(b.m, L.mu, e0);
+        raw8_load<MT>(b.v, L.nu, e0);
     };
-    issue(0, 0);
+    issue(0, cur);
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int64_t e0 = base + j * 512 + lane * 8;
-        const int slot = j & 1;
-        if (j + 1 < J) issue(j + 1, slot ^ 1);
+        if (j + 1 < J) issue(j + 1, nxt);
         float g[8], p[8], m[8], v[8], u[8];
-        raw8_unpack<GT>(graw[slot], g);
+        raw8_unpack<GT>(cur.g, g);
         clip8<GT>(c, g);
         if (need_p) {
-            raw8_unpack<PT>(praw[slot], p);
+            raw8_unpack<PT>(cur.p, p);
         } else {
 #pragma unroll
             for (int t = 0; t < 8; ++t) p[t] = 0.0f;
         }
-        raw8_unpack<MT>(mraw[slot], m);
-        raw8_unpack<MT>(vraw[slot], v);
+        raw8_unpack<MT>(cur.m, m);
+        raw8_unpack<MT>(cur.v, v);
+        cur = nxt;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             float mm, vv;
