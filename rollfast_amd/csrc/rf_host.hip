@@ -303,15 +303,18 @@ constexpr int64_t APPLY_UNIT = 8192;
 
 // `factor` (Magma's fused form, or null): each update is first taken as
 // neg_lr * (factor[leaf] * u), the scaling rf_magma_scale would have done.
-// Segment s of `segs` is leaf segs[s].leaf.
+// Segment s of `segs` is leaf segs[s].leaf.  SR: stochastic rounding of bf16
+// params (an instance of its own: the Threefry code would cost the
+// nearest-even instance waves per SIMD).
+template <bool SR>
 __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ leaves, const Seg* __restrict__ segs,
-                                              int64_t nunits, int32_t stochastic, uint32_t k0, uint32_t k1,
+                                              int64_t nunits, uint32_t k0, uint32_t k1,
                                               const float* __restrict__ factor, float neg_lr)
 {
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
     const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
-    const bool sr = stochastic != 0;
+    constexpr bool sr = SR;
     int32_t s = 0, cur = -1;
     const int32_t nseg = segs[0].nseg;
     rf_apply_leaf L{};
@@ -2458,8 +2461,9 @@ rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t st
     segs.push_back(sentinel);
     mark_list(segs);
     hipStream_t s = (hipStream_t)stream;
+    const void* fn = stochastic ? (const void*)&k_apply<true> : (const void*)&k_apply<false>;
     unsigned aw = 1;  // before the staging slot: an error here leaves nothing in flight
-    st = worklist_grid((const void*)&k_apply, ds, nunits, &aw);
+    st = worklist_grid(fn, ds, nunits, &aw);
     if (st != RF_OK) return st;
     const size_t o_sg = up16(sizeof(rf_apply_leaf) * (size_t)n_leaves);
     const size_t bytes = o_sg + sizeof(Seg) * segs.size();
@@ -2470,8 +2474,12 @@ rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t st
     std::memcpy(stg.host() + o_sg, segs.data(), sizeof(Seg) * segs.size());
     st = stg.upload(bytes, s);
     if (st != RF_OK) return st;
-    hipLaunchKernelGGL(k_apply, dim3(aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
-                       (const Seg*)(stg.dev() + o_sg), nunits, stochastic, key0, key1, factor, neg_lr);
+    if (stochastic)
+        hipLaunchKernelGGL(k_apply<true>, dim3(aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
+                           (const Seg*)(stg.dev() + o_sg), nunits, key0, key1, factor, neg_lr);
+    else
+        hipLaunchKernelGGL(k_apply<false>, dim3(aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
+                           (const Seg*)(stg.dev() + o_sg), nunits, key0, key1, factor, neg_lr);
     const hipError_t le = hipGetLastError();
     st = stg.finish(s);
     if (le != hipSuccess) return fail(RF_ERR_HIP, std::string("k_apply launch: ") + hipGetErrorString(le));
