@@ -170,12 +170,23 @@ __device__ __forceinline__ float h16_to_f32(uint32_t h)
 }
 
 // utils.py:365-371: noise = bits & 0xFFFF; no noise for |x| >= Inf bits;
-// (x_u32 + noise) & 0xFFFF0000 -> bf16 (exact truncation).
-__device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t bits)
+// (x_u32 + noise) & 0xFFFF0000 -> bf16 (exact truncation).  The word with
+// the rounded bf16 in its high half (the low half is not cleared): the
+// noise is added unconditionally (one add of the low half of the bits) and
+// the sum kept only for finite x (one class compare and one select).
+__device__ __forceinline__ uint32_t sr_bf16_hi(float x, uint32_t bits)
 {
     const uint32_t u = __float_as_uint(x);
-    const uint32_t noise = ((u & 0x7FFFFFFFu) >= 0x7F800000u) ? 0u : (bits & 0xFFFFu);
-    return (u + noise) >> 16;
+    const uint32_t r = u + (bits & 0xFFFFu);
+    return __builtin_isfinite(x) ? r : u;
+}
+
+__device__ __forceinline__ uint32_t sr_bf16(float x, uint32_t bits) { return sr_bf16_hi(x, bits) >> 16; }
+
+// The high halves of two words as one (lo's in bits 0-15): one byte permute.
+__device__ __forceinline__ uint32_t pack_hi16x2(uint32_t lo, uint32_t hi)
+{
+    return __builtin_amdgcn_perm(hi, lo, 0x07060302u);  // bytes lo.2, lo.3, hi.2, hi.3
 }
 
 // Threefry-2x32, 20 rounds (Salmon et al., SC'11): the block cipher under
@@ -530,6 +541,17 @@ __device__ __forceinline__ void store8_f32(void* base, int64_t e0, const float (
 }
 
 // 8 consecutive 16-bit patterns (bf16 or f16), 16-byte aligned.
+// 8 bf16 / f16 values from words holding them in their high halves.
+__device__ __forceinline__ void store8_hi16(void* base, int64_t e0, const uint32_t (&h)[8])
+{
+    uint4 w;
+    w.x = pack_hi16x2(h[0], h[1]);
+    w.y = pack_hi16x2(h[2], h[3]);
+    w.z = pack_hi16x2(h[4], h[5]);
+    w.w = pack_hi16x2(h[6], h[7]);
+    *(uint4*)((uint16_t*)base + e0) = w;
+}
+
 __device__ __forceinline__ void store8_bf16(void* base, int64_t e0, const uint32_t (&h)[8])
 {
     uint4 w;
@@ -1066,7 +1088,8 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                         for (int t = 0; t < 8; ++t) rb[t] = jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
                     }
 #pragma unroll
-                    for (int t = 0; t < 8; t += 2) w[t / 2] = sr_bf16(sum[t], rb[t]) | (sr_bf16(sum[t + 1], rb[t + 1]) << 16);
+                    for (int t = 0; t < 8; t += 2)
+                        w[t / 2] = pack_hi16x2(sr_bf16_hi(sum[t], rb[t]), sr_bf16_hi(sum[t + 1], rb[t + 1]));
                 } else {
 #pragma unroll
                     for (int t = 0; t < 8; t += 2) w[t / 2] = pack_h16x2_rne<PT>(sum[t], sum[t + 1]);
@@ -1399,8 +1422,9 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
 #pragma unroll
                     for (int t = 0; t < 8; ++t) {
                         const uint32_t rb = c.fed ? L.param_bits[e0 + t] : jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
-                        hb[t] = sr_bf16(sum[t], rb);
+                        hb[t] = sr_bf16_hi(sum[t], rb);
                     }
+                    store8_hi16(L.param, e0, hb);
                 } else {
 #pragma unroll
                     for (int t = 0; t < 8; t += 2) {
@@ -1408,8 +1432,8 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
                         hb[t] = w2 & 0xFFFFu;
                         hb[t + 1] = w2 >> 16;
                     }
+                    store8_bf16(L.param, e0, hb);
                 }
-                store8_bf16(L.param, e0, hb);
             } else {
                 store8_f32(L.param, e0, sum);
             }
@@ -1425,9 +1449,11 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
                     const uint64_t e = (uint64_t)(e0 + t);
                     const uint32_t bm = c.fed ? L.mu_bits[e] : jax_bits(c.kmu0, c.kmu1, e);
                     const uint32_t bv = c.fed ? L.nu_bits[e] : jax_bits(c.knu0, c.knu1, e);
-                    hm[t] = sr_bf16(m[t], bm);
-                    hv[t] = sr_bf16(v[t], bv);
+                    hm[t] = sr_bf16_hi(m[t], bm);
+                    hv[t] = sr_bf16_hi(v[t], bv);
                 }
+                store8_hi16(L.mu, e0, hm);
+                store8_hi16(L.nu, e0, hv);
             } else {
 #pragma unroll
                 for (int t = 0; t < 8; t += 2) {
@@ -1438,9 +1464,9 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
                     hv[t] = wv & 0xFFFFu;
                     hv[t + 1] = wv >> 16;
                 }
+                store8_bf16(L.mu, e0, hm);
+                store8_bf16(L.nu, e0, hv);
             }
-            store8_bf16(L.mu, e0, hm);
-            store8_bf16(L.nu, e0, hv);
         } else {
             store8_f32(L.mu, e0, m);
             store8_f32(L.nu, e0, v);
@@ -1497,6 +1523,9 @@ __device__ __forceinline__ void group_hparams(KHp& hl, const KHp& h, const rf_ad
     hl.knu1 = G.key_nu[1];
 }
 
+// UNIFORM_KEYS: move the leaf's keys to scalar registers (the fast kernel;
+// the generic kernel is short of scalar registers and would spill them).
+template <bool UNIFORM_KEYS>
 __device__ __forceinline__ void leaf_context(UnitCtx& c, const rf_adam8_leaf& L, const KHp& h, bool msr, bool psr)
 {
     const bool decay = (L.flags & RF_LEAF_DECAY) != 0;
@@ -1510,6 +1539,18 @@ __device__ __forceinline__ void leaf_context(UnitCtx& c, const rf_adam8_leaf& L,
         jax_split(h.knu0, h.knu1, (uint32_t)L.state_index, c.knu0, c.knu1);
     }
     if (psr) jax_split(h.kp0, h.kp1, (uint32_t)L.param_index, c.kp0, c.kp1);
+    if constexpr (UNIFORM_KEYS) {
+        // A wave's leaf is one leaf: its keys are wave-uniform.  Threefry's
+        // register pins leave them in vector registers; moved to scalar
+        // ones, the key-schedule constants of every later block are scalar
+        // work.
+        c.kmu0 = uniform_u32(c.kmu0);
+        c.kmu1 = uniform_u32(c.kmu1);
+        c.knu0 = uniform_u32(c.knu0);
+        c.knu1 = uniform_u32(c.knu1);
+        c.kp0 = uniform_u32(c.kp0);
+        c.kp1 = uniform_u32(c.kp1);
+    }
 }
 
 // optax.apply_if_finite's reject branch (zero updates, inner state kept),
@@ -1594,7 +1635,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
                 cur_leaf = sg.leaf;
                 L = leaves[cur_leaf];
                 group_hparams(hl, h, L);
-                leaf_context(c, L, hl, MSR, PSR);
+                leaf_context<true>(c, L, hl, MSR, PSR);
             }
             // The next unit of this wave, when it is a block of the same leaf
             // (this kernel's units are all full blocks; one segment per leaf).
@@ -1648,7 +1689,7 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
             cur_leaf = sg.leaf;
             L = leaves[cur_leaf];
             group_hparams(hl, h, L);
-            leaf_context(c, L, hl, MSR, PSR);
+            leaf_context<false>(c, L, hl, MSR, PSR);
             if (h.mpart) c.mbase = h.msegs[cur_leaf].unit_start;
         }
         const int64_t idx = sg.first + (u - sg.unit_start);

@@ -277,8 +277,8 @@ __global__ __launch_bounds__(WG) void k_sr_bf16(const float* __restrict__ x, int
         }
         uint32_t hb[8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t) hb[t] = sr_bf16(xv[t], rb[t]);
-        store8_bf16(out, e0, hb);
+        for (int t = 0; t < 8; ++t) hb[t] = sr_bf16_hi(xv[t], rb[t]);
+        store8_hi16(out, e0, hb);
     }
     for (int64_t e = ngroups * 8 + tid; e < size; e += nthreads) {
         const uint32_t w = bits ? bits[e] : jax_bits(k0, k1, (uint64_t)e);
@@ -286,9 +286,8 @@ __global__ __launch_bounds__(WG) void k_sr_bf16(const float* __restrict__ x, int
     }
 }
 
-// apply_updates over a leaf table (utils.py:648-708): one workgroup-stride
-// loop per leaf (blockIdx.y = leaf); 8 elements per thread and iteration when
-// the leaf's buffers are 16-byte aligned.
+// apply_updates over a leaf table (utils.py:648-708): f32(p) + f32(u), then
+// stochastic rounding or round-to-nearest-even for bf16 params.
 __device__ __forceinline__ uint32_t apply_bf16(float p, float u, bool stochastic, const uint32_t* bits, uint32_t lk0,
                                                uint32_t lk1, int64_t e)
 {
@@ -327,7 +326,11 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
             cur = segs[s].leaf;
             L = leaves[cur];
             f = factor ? factor[cur] : 1.0f;
-            if (sr) jax_split(k0, k1, (uint32_t)L.param_index, lk0, lk1);
+            if (sr) {
+                jax_split(k0, k1, (uint32_t)L.param_index, lk0, lk1);
+                lk0 = uniform_u32(lk0);  // one leaf per unit: wave-uniform keys
+                lk1 = uniform_u32(lk1);
+            }
             vec = ((uintptr_t)L.param % 16 == 0) && ((uintptr_t)L.updates % 16 == 0) &&
                   (!L.bits || (uintptr_t)L.bits % 16 == 0);
         }
@@ -351,16 +354,22 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
             } else if (L.param_dtype == RF_BF16) {
                 load8<uint16_t>(L.param, e0, p);
                 uint32_t h[8];
-                if (sr && L.bits) {
+                if constexpr (SR) {
                     uint32_t rb[8];
-                    load8_u32(L.bits, e0, rb);
+                    if (L.bits) {
+                        load8_u32(L.bits, e0, rb);
+                    } else {
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) h[t] = sr_bf16(p[t] + u[t], rb[t]);
+                        for (int t = 0; t < 8; ++t) rb[t] = jax_bits(lk0, lk1, (uint64_t)(e0 + t));
+                    }
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) h[t] = sr_bf16_hi(p[t] + u[t], rb[t]);
+                    store8_hi16(L.param, e0, h);
                 } else {
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) h[t] = apply_bf16(p[t], u[t], sr, nullptr, lk0, lk1, e0 + t);
+                    for (int t = 0; t < 8; ++t) h[t] = f32_to_bf16_rne(p[t] + u[t]);
+                    store8_bf16(L.param, e0, h);
                 }
-                store8_bf16(L.param, e0, h);
             } else {
                 load8<float>(L.param, e0, p);
 #pragma unroll
