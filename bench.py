@@ -16,6 +16,8 @@ Other workloads (one JSON line each, same fields):
   llama7b_msr      the default step with moment stochastic rounding
                    (adamw8(stochastic_rounding=True)): two in-kernel Threefry
                    draws per element for the requantization of both moments.
+  llama7b_f32      the default step over the same tree with f32 params and
+                   grads (16.0078 B/param).
   gpt2             GPT-2-small bf16 tree (74 leaves, LayerNorms on f32
                    fallback moments), param stochastic rounding on.
   ragged           2256 leaves, most below min_size (fallback moments),
@@ -169,12 +171,13 @@ def _timed_loop(body, seconds_target):
 
 
 def cpu_baseline(seconds_target=12.0, threads=None, shapes=None, sample_name="the 9 leaves of one Llama-7B layer",
-                 param_sr=False, moment_sr=False):
+                 param_sr=False, moment_sr=False, pdtype="bf16"):
     """The CPU oracle (C, OpenMP over blocks) on a bounded sample of the same
     workload (default: the 9 leaves of one Llama layer), one step per leaf,
     repeated until about `seconds_target` seconds of CPU work have run.  With
     stochastic rounding each step also draws its Threefry bits on the CPU
-    (the kernel draws them in-kernel)."""
+    (the kernel draws them in-kernel).  ``pdtype`` "f32": f32 params and
+    grads."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -188,10 +191,12 @@ def cpu_baseline(seconds_target=12.0, threads=None, shapes=None, sample_name="th
         n = _numel(s)
         nb = -(-n // BS)
         quant = n >= MIN_SIZE
+        p = rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)
+        g = rng.standard_normal(n, dtype=np.float32) * np.float32(1e-3)
+        if pdtype != "f32":
+            p, g = orc.f32_to_bf16_bits(p), orc.f32_to_bf16_bits(g)
         leaves.append(dict(
-            n=n, quant=quant,
-            p=orc.f32_to_bf16_bits(rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)),
-            g=orc.f32_to_bf16_bits(rng.standard_normal(n, dtype=np.float32) * np.float32(1e-3)),
+            n=n, quant=quant, p=p, g=g,
             mc=np.full(nb * BS, 127, np.uint8) if quant else np.zeros(n, np.float32),
             ms=np.ones(nb, np.float32) if quant else None,
             vc=np.zeros(nb * BS, np.uint8) if quant else np.zeros(n, np.float32),
@@ -210,7 +215,8 @@ def cpu_baseline(seconds_target=12.0, threads=None, shapes=None, sample_name="th
             if moment_sr and L["quant"]:
                 mb = orc.random_bits((t, 1000 + i), L["mc"].size)
                 vb = orc.random_bits((t, 2000 + i), L["vc"].size)
-            orc.adam8_leaf(hp, L["p"], orc.BF16, L["g"], orc.BF16, orc.MOM_QUANT if L["quant"] else orc.MOM_F32,
+            dt = orc.F32 if pdtype == "f32" else orc.BF16
+            orc.adam8_leaf(hp, L["p"], dt, L["g"], dt, orc.MOM_QUANT if L["quant"] else orc.MOM_F32,
                            L["mc"], L["ms"], L["vc"], L["vs"], BS, mu_bits=mb, nu_bits=vb, p_bits=pb)
             done += L["n"]
         return done
@@ -281,7 +287,7 @@ class Workload:
 
 
 def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None, clip=None,
-                   guard=False, groups=False, magma=False, moment_sr=False, accum=1):
+                   guard=False, groups=False, magma=False, moment_sr=False, accum=1, pdtype="bf16"):
     import numpy as np
     import torch
 
@@ -292,7 +298,8 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     print(f"[bench] {workload}: {n_params} params in {len(shapes)} leaves; allocating", file=sys.stderr, flush=True)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0)
-    params = {name: (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 0.02).to(torch.bfloat16)
+    tdt = torch.float32 if pdtype == "f32" else torch.bfloat16  # params and grads
+    params = {name: (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 0.02).to(tdt)
               for name, s in shapes}
     if adam_mu is None:
         tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=args.exact, stochastic_rounding=moment_sr)
@@ -341,7 +348,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
                     flat[: nb * BS].view(nb, BS)[zero] = 0.0
                 g[name] = t.to(torch.bfloat16)
             else:
-                g[name] = (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 1e-3).to(torch.bfloat16)
+                g[name] = (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 1e-3).to(tdt)
         pool.append(g)
     key = rf.prng.PRNGKey(0)
     holder = {"params": params, "state": state, "k": 0}
@@ -370,12 +377,12 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         "leaves": len(shapes),
         "quantized_leaves": n_quant,
         "block_size": BS,
-        "param_dtype": "bf16",
-        "grad_dtype": "bf16",
+        "param_dtype": pdtype,
+        "grad_dtype": pdtype,
         "moments": ("uint8 codebook codes + f32 block scales (f32 fallback below 4096 elements)"
                     if adam_mu is None else f"{adam_mu} (full-precision AdamW"
                     + (", stochastically rounded storage)" if adam_mu == "bf16" else ")")),
-        "param_rounding": "stochastic" if param_sr else "nearest-even",
+        "param_rounding": ("stochastic" if param_sr else "nearest-even") if pdtype == "bf16" else "f32 add",
         "moment_rounding": "stochastic (in-kernel Threefry bits)" if moment_sr else "nearest",
         "direction": "ieee" if args.exact else "hw rcp/sqrt",
         "mode": "optax update-only (f32 updates)" if optax else "fused step (params written)",
@@ -401,7 +408,9 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
                            "it, folded into apply_updates")
         config["mode"] = "adamw_step (update-only step, then apply_updates with the Magma factor)"
         config["launches_per_step"] = 4
-    if shapes_fn is llama7b_shapes:
+    if shapes_fn is llama7b_shapes and pdtype == "f32":
+        cpu = lambda: cpu_baseline(args.cpu_seconds, pdtype="f32")  # noqa: E731
+    elif shapes_fn is llama7b_shapes:
         cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr, moment_sr=moment_sr)  # noqa: E731
     else:
         sub = [s for _, s in shapes][:400]
@@ -419,7 +428,8 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
             # pre-pass reads 4 B instead of 2); the reset reads and writes
             # the accumulator (8 B)
             g_extra = 2 * g_extra + 2 + accum * 10 + 8
-        nbytes = step_bytes(shapes, apply=not optax) + n_params * g_extra
+        pb = 4 if pdtype == "f32" else 2
+        nbytes = step_bytes(shapes, pbytes=pb, gbytes=pb, apply=not optax) + n_params * g_extra
     else:
         mb = 4 if adam_mu == "f32" else 2
         nbytes = n_params * (2 + 2 + 2 + 2 * 2 * mb)  # p r+w, g r, two moments r+w
@@ -528,6 +538,7 @@ def _kernel_workload(args, kind):
 
 WORKLOADS = {
     "llama7b": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw8", param_sr=a.param_sr),
+    "llama7b_f32": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_f32_adamw8", param_sr=False, pdtype="f32"),
     "gpt2": lambda a: _tree_workload(a, gpt2_small_shapes, "gpt2_small_bf16_adamw8", param_sr=True),
     "ragged": lambda a: _tree_workload(a, ragged_shapes, "ragged_2256_leaves_bf16_adamw8", param_sr=a.param_sr,
                                        grads="student_t"),
