@@ -24,10 +24,23 @@ static adam_kernel_t pick(bool psr, bool nest)
 }
 
 // dtype_combo = 2*(param is bf16) + (grad is bf16) for f32/bf16 params and
-// grads, 4 for f16 params and grads; -1 = the generic kernel
+// grads, 4 for f16 params and grads; -1 = the generic kernel, -2 = its
+// instance for lists of full-chunk fallback units only (moment SR plays no
+// part there: those are asked of the MSR = 0 instances; null otherwise)
 adam_kernel_t RF_PICK_NAME(RFI_APPLY, RFI_MSR, RFI_EXACT)(int dtype_combo, bool psr, bool nest)
 {
     constexpr bool A = RFI_APPLY != 0, M = RFI_MSR != 0, E = RFI_EXACT != 0;
+    if (dtype_combo == -2) {
+        if constexpr (M) {
+            return nullptr;
+        } else {
+            if constexpr (A) {
+                if (psr)
+                    return nest ? &k_adam8_gen<A, M, true, true, E, true> : &k_adam8_gen<A, M, true, false, E, true>;
+            }
+            return nest ? &k_adam8_gen<A, M, false, true, E, true> : &k_adam8_gen<A, M, false, false, E, true>;
+        }
+    }
     if (dtype_combo < 0) {
         if constexpr (A) {
             if (psr) return nest ? &k_adam8_gen<A, M, true, true, E> : &k_adam8_gen<A, M, true, false, E>;

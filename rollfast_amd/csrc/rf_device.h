@@ -95,18 +95,24 @@ typedef void (*adam_kernel_t)(const rf_adam8_leaf*, const Seg*, int64_t, KHp, co
 
 // ============================================================ helpers ====
 // The segment of unit u (segs[s].unit_start <= u < segs[s + 1].unit_start),
-// searched upward from s, which must not lie past it.  A wave's first unit
-// and its strides over many small leaves cost a binary search (about
-// log2(nseg) dependent scalar loads) instead of a walk over every segment
-// in between; a unit in the same segment as the last costs one load.
+// searched upward from s, which must not lie past it.  A unit in the same
+// segment as the last costs one load.  Otherwise the wave's 64 lanes probe
+// 64 evenly spaced segments of the bracket at once and the ballot narrows it
+// 64-fold: one or two dependent loads for up to 4,096 segments, where a
+// binary search paid log2(nseg).  Called by whole waves with uniform
+// arguments; the result is uniform.
 __device__ __forceinline__ int32_t seek_seg(const Seg* __restrict__ segs, int32_t nseg, int32_t s, int64_t u)
 {
     if (segs[s + 1].unit_start > u) return s;
     int32_t lo = s + 1, hi = nseg;  // segs[lo].unit_start <= u < segs[hi].unit_start (the sentinel's)
+    const int32_t lane = (int32_t)(threadIdx.x & (WAVE - 1));
     while (hi - lo > 1) {
-        const int32_t mid = (lo + hi) >> 1;
-        if (segs[mid].unit_start <= u) lo = mid;
-        else hi = mid;
+        const int32_t step = (hi - lo + WAVE - 1) / WAVE;
+        const int32_t i = lo + lane * step;  // lane 0 probes lo, known to be <= u
+        const bool le = i < hi && segs[i].unit_start <= u;
+        const uint64_t m = __builtin_amdgcn_ballot_w64(le);
+        lo += (63 - __builtin_clzll(m)) * step;  // the last probe <= u
+        hi = min(hi, lo + step);                 // the next probe (or hi) is > u
     }
     return lo;
 }
@@ -287,12 +293,22 @@ __device__ __forceinline__ double wave_sum_f64(double x)
     return x;
 }
 
-// Copies the first BYTES of a table image into the workgroup's LDS.
+// Copies the first BYTES of a table image into the workgroup's LDS.  Every
+// load of a thread is issued before its first LDS write, so a workgroup's
+// start waits for one memory latency instead of one per 4 KB of tables.
 template <uint32_t BYTES = TABLE_BYTES>
 __device__ __forceinline__ void stage_tables(uint8_t* lds, const uint4* __restrict__ tables)
 {
+    constexpr uint32_t N = BYTES / 16;
+    constexpr uint32_t FULL = N / WG, REM = N % WG;  // whole rounds of the workgroup, then a partial one
     uint4* dst = (uint4*)lds;
-    for (uint32_t i = threadIdx.x; i < BYTES / 16; i += WG) dst[i] = tables[i];
+    uint4 t[FULL + 1];
+#pragma unroll
+    for (uint32_t k = 0; k < FULL; ++k) t[k] = tables[threadIdx.x + k * WG];
+    if (REM && threadIdx.x < REM) t[FULL] = tables[threadIdx.x + FULL * WG];
+#pragma unroll
+    for (uint32_t k = 0; k < FULL; ++k) dst[threadIdx.x + k * WG] = t[k];
+    if (REM && threadIdx.x < REM) dst[threadIdx.x + FULL * WG] = t[FULL];
     __syncthreads();
 }
 
@@ -504,7 +520,49 @@ __device__ __forceinline__ void ema(const KHp& h, float mp, float vp, float g, f
     v = t3 + t4;
 }
 
+// Global-address-space views of the leaf's buffers.  The leaf table holds
+// generic pointers, and an access through one compiles to a flat
+// instruction, which counts against lgkmcnt as well as vmcnt: every later
+// wait for an LDS read or a scalar load then also waits for the flat loads
+// and stores in flight, and the element paths' batches of loads serialise.
+// Through these views they compile to global_load/global_store, counted
+// only by vmcnt.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define RF_GLOBAL __attribute__((address_space(1)))
+#else
+#define RF_GLOBAL
+#endif
+
+template <typename T>
+__device__ __forceinline__ const RF_GLOBAL T* gload_ptr(const void* p, int64_t byte_off)
+{
+    return (const RF_GLOBAL T*)((const RF_GLOBAL uint8_t*)p + byte_off);
+}
+
+template <typename T>
+__device__ __forceinline__ RF_GLOBAL T* gstore_ptr(void* p, int64_t byte_off)
+{
+    return (RF_GLOBAL T*)((RF_GLOBAL uint8_t*)p + byte_off);
+}
+
+// Element i of a T array, read or written through its global view.
+template <typename T>
+__device__ __forceinline__ T gld(const void* p, int64_t i)
+{
+    return ((const RF_GLOBAL T*)p)[i];
+}
+
+template <typename T>
+__device__ __forceinline__ void gst(void* p, int64_t i, T v)
+{
+    ((RF_GLOBAL T*)p)[i] = v;
+}
+
 // ----------------------------------------------------------- vector I/O --
+// These keep generic pointers: through the global views above the generic
+// kernel's full-chunk fallback unit took 147 VGPRs instead of 128 (3 waves
+// per SIMD instead of 4), and the full-precision AdamW step over the
+// Llama-7B tree ran 2-4 % slower.
 // Load 8 consecutive elements (16-byte aligned) as f32.
 template <typename T>
 __device__ __forceinline__ void load8(const void* base, int64_t e0, float (&x)[8])
@@ -573,17 +631,17 @@ __device__ __forceinline__ void load8_u32(const uint32_t* base, int64_t e0, uint
 // Scalar element access with a runtime dtype (generic paths).
 __device__ __forceinline__ float load1(const void* base, int32_t dtype, int64_t e)
 {
-    if (dtype == RF_BF16) return bf16_bits_to_f32(((const uint16_t*)base)[e]);
-    if (dtype == RF_F16) return f16_bits_to_f32(((const uint16_t*)base)[e]);
-    return ((const float*)base)[e];
+    if (dtype == RF_BF16) return bf16_bits_to_f32(gld<uint16_t>(base, e));
+    if (dtype == RF_F16) return f16_bits_to_f32(gld<uint16_t>(base, e));
+    return gld<float>(base, e);
 }
 
 // x rounded to nearest even in a 16-bit dtype, or as is.
 __device__ __forceinline__ void store1(void* base, int32_t dtype, int64_t e, float x)
 {
-    if (dtype == RF_BF16) ((uint16_t*)base)[e] = (uint16_t)f32_to_bf16_rne(x);
-    else if (dtype == RF_F16) ((uint16_t*)base)[e] = (uint16_t)f32_to_f16_rne(x);
-    else ((float*)base)[e] = x;
+    if (dtype == RF_BF16) gst<uint16_t>(base, e, (uint16_t)f32_to_bf16_rne(x));
+    else if (dtype == RF_F16) gst<uint16_t>(base, e, (uint16_t)f32_to_f16_rne(x));
+    else gst<float>(base, e, x);
 }
 
 // Round x to a param/grad dtype and back (nearest even).
@@ -600,16 +658,16 @@ __device__ __forceinline__ float round_to_dtype(float x, int32_t dtype)
 // (adam8.py:167-186, :202).
 __device__ __forceinline__ float load_scale(const float* scales, uint32_t leaf_flags, int64_t b)
 {
-    if (leaf_flags & RF_LEAF_SCALE_BF16) return bf16_bits_to_f32(((const uint16_t*)scales)[b]);
-    if (leaf_flags & RF_LEAF_SCALE_F16) return f16_bits_to_f32(((const uint16_t*)scales)[b]);
-    return scales[b];
+    if (leaf_flags & RF_LEAF_SCALE_BF16) return bf16_bits_to_f32(gld<uint16_t>(scales, b));
+    if (leaf_flags & RF_LEAF_SCALE_F16) return f16_bits_to_f32(gld<uint16_t>(scales, b));
+    return gld<float>(scales, b);
 }
 
 __device__ __forceinline__ void store_scale(float* scales, uint32_t leaf_flags, int64_t b, float s)
 {
-    if (leaf_flags & RF_LEAF_SCALE_BF16) ((uint16_t*)scales)[b] = (uint16_t)f32_to_bf16_rne(s);
-    else if (leaf_flags & RF_LEAF_SCALE_F16) ((uint16_t*)scales)[b] = (uint16_t)f32_to_f16_rne(s);
-    else scales[b] = s;
+    if (leaf_flags & RF_LEAF_SCALE_BF16) gst<uint16_t>(scales, b, (uint16_t)f32_to_bf16_rne(s));
+    else if (leaf_flags & RF_LEAF_SCALE_F16) gst<uint16_t>(scales, b, (uint16_t)f32_to_f16_rne(s));
+    else gst<float>(scales, b, s);
 }
 
 // Uniform per-unit context.
@@ -697,7 +755,7 @@ __device__ __forceinline__ void clip_context(UnitCtx& c, const KHp& h)
     c.cs16 = 1.0f;
     c.csh = 1.0f;
     if (c.clip) {
-        c.cs = h.clip[0];
+        c.cs = gld<float>(h.clip, 0);
         c.cs16 = round_to_bf16(c.cs);
         c.csh = round_to_f16(c.cs);
     }
@@ -737,15 +795,15 @@ __device__ __forceinline__ void update_one(const UnitCtx& c, const rf_adam8_leaf
     if constexpr (APPLY) {
         if (L.param_dtype == RF_BF16) {
             uint32_t rb = 0;
-            if constexpr (PSR) rb = c.fed ? L.param_bits[e] : jax_bits(c.kp0, c.kp1, (uint64_t)e);
-            ((uint16_t*)L.param)[e] = (uint16_t)new_param_bits<PSR, uint16_t>(p, u, rb);
+            if constexpr (PSR) rb = c.fed ? gld<uint32_t>(L.param_bits, e) : jax_bits(c.kp0, c.kp1, (uint64_t)e);
+            gst<uint16_t>(L.param, e, (uint16_t)new_param_bits<PSR, uint16_t>(p, u, rb));
         } else if (L.param_dtype == RF_F16) {
-            ((uint16_t*)L.param)[e] = (uint16_t)f32_to_f16_rne(p + u);
+            gst<uint16_t>(L.param, e, (uint16_t)f32_to_f16_rne(p + u));
         } else {
-            ((float*)L.param)[e] = p + u;
+            gst<float>(L.param, e, p + u);
         }
     } else {
-        L.updates[e] = u;
+        gst<float>(L.updates, e, u);
     }
 }
 
@@ -760,16 +818,14 @@ template <int B>
 __device__ __forceinline__ void load_batch(const UnitCtx& c, const rf_adam8_leaf& L, int64_t base, int64_t j0,
                                            int64_t nvalid, uint32_t (&cm)[B], uint32_t (&cv)[B], float (&g)[B])
 {
-    const uint8_t* mcodes = (const uint8_t*)L.mu;
-    const uint8_t* vcodes = (const uint8_t*)L.nu;
 #pragma unroll
     for (int k = 0; k < B; ++k) {
         const int64_t j = j0 + k * WAVE;
         cm[k] = cv[k] = 0u;
         g[k] = 0.0f;
         if (j < nvalid) {
-            cm[k] = mcodes[base + j];
-            cv[k] = vcodes[base + j];
+            cm[k] = gld<uint8_t>(L.mu, base + j);
+            cv[k] = gld<uint8_t>(L.nu, base + j);
             g[k] = load_grad1(c, L, base + j);
         }
     }
@@ -794,8 +850,6 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
     const float* cbu = (const float*)(c.lds + L_CBU);
     const float sm_old = load_scale(L.mu_scales, L.flags, blk);
     const float sv_old = load_scale(L.nu_scales, L.flags, blk);
-    uint8_t* mcodes = (uint8_t*)L.mu;
-    uint8_t* vcodes = (uint8_t*)L.nu;
     uint32_t am = 0, av = 0;
     for (int64_t j0 = lane; j0 < nvalid; j0 += B * WAVE) {
         uint32_t cm[B], cv[B];
@@ -835,18 +889,18 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
                 cm = code_signed_fast(c.lds, mm, sm, rsm);
             } else {
                 uint32_t bits = 0;
-                if constexpr (MSR) bits = c.fed ? L.mu_bits[e] : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
+                if constexpr (MSR) bits = c.fed ? gld<uint32_t>(L.mu_bits, e) : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
                 cm = code_literal(cbs, mm, sm, MSR, bits);
             }
             if (fast_v) {
                 cv = code_unsigned_fast(c.lds, vv, sv, rsv);
             } else {
                 uint32_t bits = 0;
-                if constexpr (MSR) bits = c.fed ? L.nu_bits[e] : jax_bits(c.knu0, c.knu1, (uint64_t)e);
+                if constexpr (MSR) bits = c.fed ? gld<uint32_t>(L.nu_bits, e) : jax_bits(c.knu0, c.knu1, (uint64_t)e);
                 cv = code_literal(cbu, vv, sv, MSR, bits);
             }
-            mcodes[e] = (uint8_t)cm;
-            vcodes[e] = (uint8_t)cv;
+            gst<uint8_t>(L.mu, e, (uint8_t)cm);
+            gst<uint8_t>(L.nu, e, (uint8_t)cv);
         }
     }
     if (lane == 0) {
@@ -856,25 +910,6 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
 }
 
 // ================================================ work units: quantized ====
-// Global-address-space views: loads and stores through them compile to
-// global_load/global_store (not flat), so they count only against vmcnt.
-#if defined(__HIP_DEVICE_COMPILE__)
-#define RF_GLOBAL __attribute__((address_space(1)))
-#else
-#define RF_GLOBAL
-#endif
-
-template <typename T>
-__device__ __forceinline__ const RF_GLOBAL T* gload_ptr(const void* p, int64_t byte_off)
-{
-    return (const RF_GLOBAL T*)((const RF_GLOBAL uint8_t*)p + byte_off);
-}
-
-template <typename T>
-__device__ __forceinline__ RF_GLOBAL T* gstore_ptr(void* p, int64_t byte_off)
-{
-    return (RF_GLOBAL T*)((RF_GLOBAL uint8_t*)p + byte_off);
-}
 
 // 8 consecutive elements of a param/grad array in registers (16-byte words).
 template <typename T>
@@ -1325,10 +1360,10 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
             update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g[k], p[k]);
             if (store_sr) {
                 // optim/adam.py:219-222: _tree_stochastic_cast(moments, bfloat16, k1 | k2)
-                const uint32_t bm = c.fed ? L.mu_bits[e] : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
-                const uint32_t bv = c.fed ? L.nu_bits[e] : jax_bits(c.knu0, c.knu1, (uint64_t)e);
-                ((uint16_t*)L.mu)[e] = (uint16_t)sr_bf16(mm, bm);
-                ((uint16_t*)L.nu)[e] = (uint16_t)sr_bf16(vv, bv);
+                const uint32_t bm = c.fed ? gld<uint32_t>(L.mu_bits, e) : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
+                const uint32_t bv = c.fed ? gld<uint32_t>(L.nu_bits, e) : jax_bits(c.knu0, c.knu1, (uint64_t)e);
+                gst<uint16_t>(L.mu, e, (uint16_t)sr_bf16(mm, bm));
+                gst<uint16_t>(L.nu, e, (uint16_t)sr_bf16(vv, bv));
             } else {
                 store1(L.mu, mdt, e, mm);  // adam8.py:688 moment.astype(fallback_dtype)
                 store1(L.nu, mdt, e, vv);
@@ -1421,7 +1456,8 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
                 if constexpr (PSR && IS_BF16<PT>) {
 #pragma unroll
                     for (int t = 0; t < 8; ++t) {
-                        const uint32_t rb = c.fed ? L.param_bits[e0 + t] : jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
+                        const uint32_t rb =
+                            c.fed ? gld<uint32_t>(L.param_bits, e0 + t) : jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
                         hb[t] = sr_bf16_hi(sum[t], rb);
                     }
                     store8_hi16(L.param, e0, hb);
@@ -1447,8 +1483,8 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
                     const uint64_t e = (uint64_t)(e0 + t);
-                    const uint32_t bm = c.fed ? L.mu_bits[e] : jax_bits(c.kmu0, c.kmu1, e);
-                    const uint32_t bv = c.fed ? L.nu_bits[e] : jax_bits(c.knu0, c.knu1, e);
+                    const uint32_t bm = c.fed ? gld<uint32_t>(L.mu_bits, (int64_t)e) : jax_bits(c.kmu0, c.kmu1, e);
+                    const uint32_t bv = c.fed ? gld<uint32_t>(L.nu_bits, (int64_t)e) : jax_bits(c.knu0, c.knu1, e);
                     hm[t] = sr_bf16_hi(m[t], bm);
                     hv[t] = sr_bf16_hi(v[t], bv);
                 }
@@ -1577,13 +1613,13 @@ __device__ void reject_units(const rf_adam8_leaf* __restrict__ leaves, const Seg
             if constexpr (APPLY) {
                 store1(L.param, L.param_dtype, e, load1(L.param, L.param_dtype, e) + 0.0f);
             } else {
-                L.updates[e] = 0.0f;
+                gst<float>(L.updates, e, 0.0f);
             }
         }
     }
 }
 
-__device__ __forceinline__ bool gate_rejects(const KHp& h) { return h.gate != nullptr && *h.gate == 0.0f; }
+__device__ __forceinline__ bool gate_rejects(const KHp& h) { return h.gate != nullptr && gld<float>(h.gate, 0) == 0.0f; }
 
 // Full 2048-element blocks of the leaves whose (param, grad) dtypes are
 // (PT, GT) (uint16_t = bf16, float = f32): the hot kernel.  Waves walk the
@@ -1653,13 +1689,25 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
 // Everything else, one wave per unit: quantized blocks of other sizes,
 // partial or unaligned blocks (two passes, literal requantization) and
 // leaves with unquantized (fallback) moments.  Dtypes are read per leaf.
-template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
-__global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
+// VEC_ONLY: an instance for lists of full-chunk fallback units only (the
+// full-precision AdamW trees).  Without the other unit kinds its plain
+// instances take 126-127 VGPRs (4 waves per SIMD) as the compiler schedules
+// them; with them, 133-135, which the mixed instances are held to 128 from
+// (GEN_WAVES_PER_EU), the moment-SR, param-SR and Nesterov ones aside
+// (138-151 VGPRs, 3 waves, where 4 would spill).  Measured on the Llama-7B
+// tree, the full-precision step ran 8 % slower in the mixed kernel held to
+// 128 VGPRs; the ragged tree's mixed lists 2.5 % faster held than not.
+template <bool MSR, bool PSR, bool NEST, bool VEC_ONLY>
+constexpr int GEN_WAVES_PER_EU = (VEC_ONLY || MSR || PSR || NEST) ? 1 : 4;
+
+template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT, bool VEC_ONLY = false>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(GEN_WAVES_PER_EU<MSR, PSR, NEST, VEC_ONLY>)))
+void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
                                                   const Seg* __restrict__ segs, int64_t total_units, KHp h,
                                                   const uint4* __restrict__ tables)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
-    stage_tables(lds, tables);
+    if (!VEC_ONLY && tables) stage_tables(lds, tables);  // null: the list has no quantized units
 
     const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
     const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
@@ -1693,9 +1741,13 @@ __global__ __launch_bounds__(WG) void k_adam8_gen(const rf_adam8_leaf* __restric
             if (h.mpart) c.mbase = h.msegs[cur_leaf].unit_start;
         }
         const int64_t idx = sg.first + (u - sg.unit_start);
-        if (sg.kind == KIND_QGEN) unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, hl);
-        else if (sg.kind == KIND_FALLBACK_VEC) dispatch_fallback_vec<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
-        else unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
+        if constexpr (VEC_ONLY) {
+            dispatch_fallback_vec<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
+        } else {
+            if (sg.kind == KIND_QGEN) unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, hl);
+            else if (sg.kind == KIND_FALLBACK_VEC) dispatch_fallback_vec<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
+            else unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
+        }
     }
 }
 

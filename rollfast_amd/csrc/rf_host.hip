@@ -293,7 +293,7 @@ __device__ __forceinline__ uint32_t apply_bf16(float p, float u, bool stochastic
 {
     const float s = p + u;
     if (!stochastic) return f32_to_bf16_rne(s);
-    return sr_bf16(s, bits ? bits[e] : jax_bits(lk0, lk1, (uint64_t)e));
+    return sr_bf16(s, bits ? gld<uint32_t>(bits, e) : jax_bits(lk0, lk1, (uint64_t)e));
 }
 
 // Work units of apply_updates: APPLY_UNIT consecutive elements of one leaf
@@ -378,15 +378,16 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
             }
         }
         for (int64_t e = v_end + lane; e < e_end; e += WAVE) {
-            const float u = factor ? neg_lr * (f * L.updates[e]) : L.updates[e];
+            const float ue = gld<float>(L.updates, e);
+            const float u = factor ? neg_lr * (f * ue) : ue;
             if (L.param_dtype == RF_F16) {
-                const float p = f16_bits_to_f32(((const uint16_t*)L.param)[e]);
-                ((uint16_t*)L.param)[e] = (uint16_t)f32_to_f16_rne(p + u);
+                const float p = f16_bits_to_f32(gld<uint16_t>(L.param, e));
+                gst<uint16_t>(L.param, e, (uint16_t)f32_to_f16_rne(p + u));
             } else if (L.param_dtype == RF_BF16) {
-                const float p = bf16_bits_to_f32(((const uint16_t*)L.param)[e]);
-                ((uint16_t*)L.param)[e] = (uint16_t)apply_bf16(p, u, sr, L.bits, lk0, lk1, e);
+                const float p = bf16_bits_to_f32(gld<uint16_t>(L.param, e));
+                gst<uint16_t>(L.param, e, (uint16_t)apply_bf16(p, u, sr, L.bits, lk0, lk1, e));
             } else {
-                ((float*)L.param)[e] = ((const float*)L.param)[e] + u;
+                gst<float>(L.param, e, gld<float>(L.param, e) + u);
             }
         }
     }
@@ -713,18 +714,18 @@ __global__ __launch_bounds__(WG) void k_magma_apply(const rf_magma_leaf* __restr
     for (int64_t u = wave; u < nunits; u += nwaves) {
         s = seek_seg(segs, nseg, s, u);
         const Seg sg = segs[s];
-        float* up = leaves[sg.leaf].updates;
+        RF_GLOBAL float* up = gstore_ptr<float>(leaves[sg.leaf].updates, 0);
         const float f = factor[sg.leaf];
         const int64_t e_begin = (u - sg.unit_start) * NORM_UNIT;
         const int64_t e_end = min(leaves[sg.leaf].size, e_begin + NORM_UNIT);
         if (e_end - e_begin == NORM_UNIT && ((uintptr_t)up & 15u) == 0) {
             for (int64_t e0 = e_begin + lane * 4; e0 < e_end; e0 += 256) {
-                float4 v = *(const float4*)(up + e0);
+                float4 v = *(const RF_GLOBAL float4*)(up + e0);
                 v.x = neg_lr * (f * v.x);
                 v.y = neg_lr * (f * v.y);
                 v.z = neg_lr * (f * v.z);
                 v.w = neg_lr * (f * v.w);
-                *(float4*)(up + e0) = v;
+                *(RF_GLOBAL float4*)(up + e0) = v;
             }
         } else {
             for (int64_t e = e_begin + lane; e < e_end; e += WAVE) up[e] = neg_lr * (f * up[e]);
@@ -774,11 +775,11 @@ __global__ __launch_bounds__(WG) void k_clip_scale(const rf_clip_leaf* __restric
     }
     for (int64_t e = ngroups * 8 + tid; e < L.size; e += nthreads) {
         if (L.dtype == RF_F16) {
-            ((uint16_t*)L.out)[e] = (uint16_t)f32_to_f16_rne(f16_bits_to_f32(((const uint16_t*)L.grad)[e]) * csh);
+            gst<uint16_t>(L.out, e, (uint16_t)f32_to_f16_rne(f16_bits_to_f32(gld<uint16_t>(L.grad, e)) * csh));
         } else if (bf16) {
-            ((uint16_t*)L.out)[e] = (uint16_t)f32_to_bf16_rne(bf16_bits_to_f32(((const uint16_t*)L.grad)[e]) * cs16);
+            gst<uint16_t>(L.out, e, (uint16_t)f32_to_bf16_rne(bf16_bits_to_f32(gld<uint16_t>(L.grad, e)) * cs16));
         } else {
-            ((float*)L.out)[e] = ((const float*)L.grad)[e] * cs;
+            gst<float>(L.out, e, gld<float>(L.grad, e) * cs);
         }
     }
 }
@@ -1211,9 +1212,16 @@ inline bool valid_dtype(int32_t d) { return d == RF_F32 || d == RF_BF16 || d == 
 // ---- kernel selection ----
 // The fast kernel's instances: dtype_combo = 2*(param is bf16) + (grad is bf16)
 // for f32/bf16 params and grads, COMBO_F16 for f16 params and grads; -1 (the
-// generic kernel) for the other mixes.
+// generic kernel) for the other mixes, VEC_COMBO (its instance without the
+// element-wise and quantized unit code) for a generic list that holds
+// full-chunk fallback units only.
+constexpr int COMBO_F16 = 4;
+constexpr int GEN_LIST = 5;    // the generic kernel's work list
+constexpr int VEC_COMBO = -2;  // a generic list of full-chunk fallback units only
+
 adam_kernel_t pick_adam_kernel(bool apply, bool msr, bool psr, bool nest, bool exact, int combo)
 {
+    if (combo == VEC_COMBO) msr = false;  // fallback units have no codes to round
     if (apply) {
         if (msr) return exact ? rf_pick_adam8_a1_m1_e1(combo, psr, nest) : rf_pick_adam8_a1_m1_e0(combo, psr, nest);
         return exact ? rf_pick_adam8_a1_m0_e1(combo, psr, nest) : rf_pick_adam8_a1_m0_e0(combo, psr, nest);
@@ -1222,8 +1230,6 @@ adam_kernel_t pick_adam_kernel(bool apply, bool msr, bool psr, bool nest, bool e
     return exact ? rf_pick_adam8_a0_m0_e1(combo, false, nest) : rf_pick_adam8_a0_m0_e0(combo, false, nest);
 }
 
-constexpr int COMBO_F16 = 4;
-constexpr int GEN_LIST = 5;  // the generic kernel's work list
 
 inline int dtype_combo(const rf_adam8_leaf& L)
 {
@@ -1324,6 +1330,7 @@ struct PlanGroup {
     int combo;
     int64_t seg_offset;
     int64_t units;
+    bool tables;  // the list holds quantized units (the kernel stages the LDS tables)
 };
 
 struct rf_adam8_plan {
@@ -1488,7 +1495,13 @@ rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_
     int64_t units = 0;
     for (int combo = GEN_LIST; combo >= 0; --combo) {
         if (gunits[combo] == 0) continue;
-        groups.push_back({combo == GEN_LIST ? -1 : combo, (int64_t)segs.size(), gunits[combo]});
+        bool quant = combo != GEN_LIST, vec_only = combo == GEN_LIST;
+        for (const Seg& sg : gsegs[combo]) {
+            quant |= sg.kind == KIND_QGEN;
+            vec_only &= sg.kind == KIND_FALLBACK_VEC;
+        }
+        const int kc = combo != GEN_LIST ? combo : (vec_only ? VEC_COMBO : -1);
+        groups.push_back({kc, (int64_t)segs.size(), gunits[combo], quant});
         Seg sentinel{};
         sentinel.unit_start = gunits[combo];
         sentinel.leaf = -1;
@@ -1804,6 +1817,7 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
     for (const PlanGroup& g : plan->groups) {
         adam_kernel_t fn =
             pick_adam_kernel(plan->apply != 0, msr, psr, (f & RF_NESTEROV) != 0, (f & RF_EXACT) != 0, g.combo);
+        if (!fn) return fail(RF_ERR_HIP, "no step kernel instance for this launch");
         int occ = 1;
         st = occupancy((const void*)fn, &occ);
         if (st != RF_OK) return st;
@@ -1828,7 +1842,8 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
             grid = std::min(wg_needed, rounds * wg_resident);
         }
         hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WG), 0, (hipStream_t)stream, d_leaves,
-                           plan->d_segs + g.seg_offset, g.units, k, msr ? ds->search : ds->tables);
+                           plan->d_segs + g.seg_offset, g.units, k,
+                           !g.tables ? nullptr : (msr ? ds->search : ds->tables));
         HIP_TRY(hipGetLastError());
     }
     HIP_TRY(hipGetLastError());

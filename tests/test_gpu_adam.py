@@ -18,6 +18,10 @@ from tests._helpers import OracleTree, bf16_bits, bf16_ulp_distance, f32_params_
 pytestmark = pytest.mark.gpu
 
 SPEC = [((8, 2048), "bf16", "bf16"), ((3, 1000), "f32", "f32"), ((700,), "bf16", "f32"), ((5,), "f32", "bf16")]
+# Every leaf a whole number of 2048-element chunks: the launch's generic list
+# holds full-chunk fallback units only and takes the kernel instance built
+# for that case alone.
+VEC_SPEC = [((8, 2048), "bf16", "bf16"), ((2, 4096), "f32", "f32"), ((2048,), "bf16", "f32"), ((3, 2048), "f32", "bf16")]
 
 
 def _build(spec, seed):
@@ -93,11 +97,12 @@ def _compare(spec, tree, params, adam_state, exact, what, before=None):
             assert f32_params_close(got, want, before[i]).all(), f"{what} leaf {i}"
 
 
-def _run_adamw(*, mu_dtype, exact, nesterov=False, psr=False, fed=False, steps=3, wd=0.01):
+def _run_adamw(*, mu_dtype, exact, nesterov=False, psr=False, fed=False, steps=3, wd=0.01, spec=SPEC):
     import torch
 
     import rollfast_amd as rf
 
+    SPEC = spec
     host, params = _build(SPEC, 1)
     tx = rf.adamw(learning_rate=1e-3, weight_decay=wd, mu_dtype=mu_dtype, nesterov=nesterov, exact=exact,
                   key=rf.prng.PRNGKey(3))
@@ -160,8 +165,23 @@ def test_adamw_param_sr_in_kernel_bits():
     _run_adamw(mu_dtype=None, exact=True, psr=True)
 
 
+@pytest.mark.parametrize("case", ["f32", "f32_fast", "bf16_sr", "bf16_fed_psr", "nesterov", "psr"])
+def test_adamw_tree_of_whole_chunks(case):
+    """The instance for lists of full-chunk fallback units only, against the
+    oracle at the same bars as the mixed tree."""
+    import torch
+
+    kw = {"f32": dict(mu_dtype=None, exact=True), "f32_fast": dict(mu_dtype=None, exact=False),
+          "bf16_sr": dict(mu_dtype=torch.bfloat16, exact=False),
+          "bf16_fed_psr": dict(mu_dtype=torch.bfloat16, exact=True, psr=True, fed=True),
+          "nesterov": dict(mu_dtype=None, exact=True, nesterov=True),
+          "psr": dict(mu_dtype=None, exact=True, psr=True)}[case]
+    _run_adamw(spec=VEC_SPEC, **kw)
+
+
 @pytest.mark.parametrize("exact", [True, False])
-def test_scale_by_adam_update_only_with_masked_weight_decay(exact):
+@pytest.mark.parametrize("tree", ["mixed", "whole_chunks"])
+def test_scale_by_adam_update_only_with_masked_weight_decay(exact, tree):
     """scale_by_adam(weight_decay=..., weight_decay_mask=...) adds
     wd * f32(param) to the direction (utils.py:79-90: an f32 product, not the
     weak bf16 one of optax add_decayed_weights) and returns f32 updates."""
@@ -169,6 +189,7 @@ def test_scale_by_adam_update_only_with_masked_weight_decay(exact):
 
     import rollfast_amd as rf
 
+    SPEC = VEC_SPEC if tree == "whole_chunks" else globals()["SPEC"]
     host, params = _build(SPEC, 2)
     mask = {f"l{i}": (i % 2 == 0) for i in range(len(SPEC))}
     tx = rf.scale_by_adam(weight_decay=0.05, weight_decay_mask=mask, exact=exact)
