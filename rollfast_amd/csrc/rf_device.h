@@ -831,14 +831,83 @@ __device__ __forceinline__ void load_batch(const UnitCtx& c, const rf_adam8_leaf
     }
 }
 
+// A batch of B lane elements of a quantized block: old codes, grads and (the
+// update pass) params.
+template <int B>
+struct QBatch {
+    uint32_t cm[B], cv[B];
+    float g[B], p[B];
+};
+
+// The coding pass of a partial or odd-sized block (the generic kernel): with
+// the block's new absmax bits (am, av), every element of the block, the
+// padding past the leaf's end as zero (adam8.py:137-141), is coded from its
+// moments, recomputed from the old codes and scales, which are still in
+// place; then the new scales are written.  The next batch's loads are issued
+// before this batch's arithmetic and stores, so a batch does not wait for
+// the previous batch's stores.
+template <bool MSR, int B>
+__device__ __forceinline__ void literal_code(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
+                                             float sm_old, float sv_old, uint32_t am, uint32_t av)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t bs = L.block_size;
+    const int64_t base = blk * bs;
+    const int64_t nvalid = max((int64_t)0, min(bs, L.size - base));
+    const float* cbs = (const float*)(c.lds + L_CBS);
+    const float* cbu = (const float*)(c.lds + L_CBU);
+    const float sm = scale_from_absmax_bits(am);
+    const float sv = scale_from_absmax_bits(av);
+    const bool fast_m = !MSR && block_is_fast(am, sm);
+    const bool fast_v = !MSR && block_is_fast(av, sv);
+    const float rsm = 1.0f / sm;
+    const float rsv = 1.0f / sv;
+    const int64_t nb = (bs + B * WAVE - 1) / (B * WAVE);
+    QBatch<B> cur{}, nxt{};
+    load_batch<B>(c, L, base, lane, nvalid, cur.cm, cur.cv, cur.g);
+    for (int64_t i = 0; i < nb; ++i) {
+        const int64_t j0 = lane + i * (B * WAVE);
+        if (i + 1 < nb) load_batch<B>(c, L, base, j0 + B * WAVE, nvalid, nxt.cm, nxt.cv, nxt.g);
+#pragma unroll
+        for (int k = 0; k < B; ++k) {
+            const int64_t j = j0 + k * WAVE;
+            if (j >= bs) continue;
+            const int64_t e = base + j;
+            float mm = 0.0f, vv = 0.0f;  // zero padding past the leaf's end
+            if (j < nvalid) ema(h, cbs[cur.cm[k]] * sm_old, cbu[cur.cv[k]] * sv_old, cur.g[k], mm, vv);
+            uint32_t cm, cv;
+            if (fast_m) {
+                cm = code_signed_fast(c.lds, mm, sm, rsm);
+            } else {
+                uint32_t bits = 0;
+                if constexpr (MSR) bits = c.fed ? gld<uint32_t>(L.mu_bits, e) : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
+                cm = code_literal(cbs, mm, sm, MSR, bits);
+            }
+            if (fast_v) {
+                cv = code_unsigned_fast(c.lds, vv, sv, rsv);
+            } else {
+                uint32_t bits = 0;
+                if constexpr (MSR) bits = c.fed ? gld<uint32_t>(L.nu_bits, e) : jax_bits(c.knu0, c.knu1, (uint64_t)e);
+                cv = code_literal(cbu, vv, sv, MSR, bits);
+            }
+            gst<uint8_t>(L.mu, e, (uint8_t)cm);
+            gst<uint8_t>(L.nu, e, (uint8_t)cv);
+        }
+        cur = nxt;
+    }
+    if (lane == 0) {
+        store_scale(L.mu_scales, L.flags, blk, sm);
+        store_scale(L.nu_scales, L.flags, blk, sv);
+    }
+}
+
 // Requantization of one block by the literal search (or moment SR): the new
 // moments are recomputed from the old codes and scales, which are still in
 // place, with the reference's NaN-propagating absmax (adam8.py:142), then
-// every element is coded and the new scales are written.  Used for blocks of
-// any size and blocks whose scale leaves the fast range (zero-free tiny, Inf,
-// NaN), with nearest or stochastic rounding.  B: elements per lane per batch
-// (1 inside the fast kernel, where this path is rare and registers are
-// scarce).
+// every element is coded and the new scales are written.  Used inside the
+// fast kernel for blocks whose scale leaves the fast range (zero-free tiny,
+// Inf, NaN), with nearest or stochastic rounding.  B: elements per lane per
+// batch (1 there, where this path is rare and registers are scarce).
 template <bool MSR, int B = EW_BATCH>
 __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h)
 {
@@ -1300,27 +1369,42 @@ __device__ __forceinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf&
     const float sm_old = load_scale(L.mu_scales, L.flags, blk);
     const float sv_old = load_scale(L.nu_scales, L.flags, blk);
 
+    // One pass updates the params and takes the new moments' absmax (the
+    // NaN-propagating max of adam8.py:142 over the valid elements), the
+    // next batch's loads in flight behind each batch; then the coding pass.
     const bool need_p = APPLY || c.wd_mode != WD_OFF;
-    for (int64_t j0 = lane; j0 < nvalid; j0 += EW_BATCH * WAVE) {
-        uint32_t cm[EW_BATCH], cv[EW_BATCH];
-        float g[EW_BATCH], p[EW_BATCH];
-        load_batch<EW_BATCH>(c, L, base, j0, nvalid, cm, cv, g);
+    constexpr int B = EW_BATCH;
+    const int64_t nb = (nvalid + B * WAVE - 1) / (B * WAVE);
+    auto load = [&](int64_t j0, QBatch<B>& q) {
+        load_batch<B>(c, L, base, j0, nvalid, q.cm, q.cv, q.g);
 #pragma unroll
-        for (int k = 0; k < EW_BATCH; ++k) {
+        for (int k = 0; k < B; ++k) {
             const int64_t j = j0 + k * WAVE;
-            p[k] = (need_p && j < nvalid) ? load1(L.param, L.param_dtype, base + j) : 0.0f;
+            q.p[k] = (need_p && j < nvalid) ? load1(L.param, L.param_dtype, base + j) : 0.0f;
         }
+    };
+    uint32_t am = 0, av = 0;
+    QBatch<B> cur{}, nxt{};
+    if (nb > 0) load(lane, cur);
+    for (int64_t i = 0; i < nb; ++i) {
+        const int64_t j0 = lane + i * (B * WAVE);
+        if (i + 1 < nb) load(j0 + B * WAVE, nxt);
 #pragma unroll
-        for (int k = 0; k < EW_BATCH; ++k) {
+        for (int k = 0; k < B; ++k) {
             const int64_t j = j0 + k * WAVE;
             if (j < nvalid) {
                 float mm, vv;
-                ema(h, cbs[cm[k]] * sm_old, cbu[cv[k]] * sv_old, g[k], mm, vv);
-                update_one<APPLY, PSR, NEST, EXACT>(c, L, base + j, h, mm, vv, g[k], p[k]);
+                ema(h, cbs[cur.cm[k]] * sm_old, cbu[cur.cv[k]] * sv_old, cur.g[k], mm, vv);
+                am = max(am, __float_as_uint(mm) & 0x7FFFFFFFu);
+                av = max(av, __float_as_uint(vv));
+                update_one<APPLY, PSR, NEST, EXACT>(c, L, base + j, h, mm, vv, cur.g[k], cur.p[k]);
             }
         }
+        cur = nxt;
     }
-    requant_literal<MSR>(c, L, blk, h);
+    am = wave_max_u32(am);
+    av = wave_max_u32(av);
+    literal_code<MSR, B>(c, L, blk, h, sm_old, sv_old, am, av);
 }
 
 // ============================================= work units: fallback ====
@@ -1337,19 +1421,34 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
     const bool need_p = APPLY || c.wd_mode != WD_OFF || c.zero;
     const bool msum = !APPLY && c.mpart != nullptr;  // Magma sums: update-only launches
     MagmaAcc acc;
-    for (int64_t e0 = base + lane; e0 < end; e0 += EW_BATCH * WAVE) {
+    // Batches of EW_BATCH elements per lane, the next batch's loads in flight
+    // behind each batch's arithmetic and stores.
+    struct Batch {
         float g[EW_BATCH], mo[EW_BATCH], vo[EW_BATCH], p[EW_BATCH];
+    };
+    auto load = [&](int64_t e0, Batch& b) {
 #pragma unroll
         for (int k = 0; k < EW_BATCH; ++k) {
             const int64_t e = e0 + k * WAVE;
-            g[k] = mo[k] = vo[k] = p[k] = 0.0f;
+            b.g[k] = b.mo[k] = b.vo[k] = b.p[k] = 0.0f;
             if (e < end) {
-                g[k] = load_grad1(c, L, e);
-                mo[k] = load1(L.mu, mdt, e);
-                vo[k] = load1(L.nu, mdt, e);
-                if (need_p) p[k] = load1(L.param, L.param_dtype, e);
+                b.g[k] = load_grad1(c, L, e);
+                b.mo[k] = load1(L.mu, mdt, e);
+                b.vo[k] = load1(L.nu, mdt, e);
+                if (need_p) b.p[k] = load1(L.param, L.param_dtype, e);
             }
         }
+    };
+    const int64_t nb = (end - base + EW_BATCH * WAVE - 1) / (EW_BATCH * WAVE);
+    Batch cur{}, nxt{};
+    if (nb > 0) load(base + lane, cur);
+    for (int64_t i = 0; i < nb; ++i) {
+        const int64_t e0 = base + lane + i * (EW_BATCH * WAVE);
+        if (i + 1 < nb) load(e0 + EW_BATCH * WAVE, nxt);
+        const float(&g)[EW_BATCH] = cur.g;
+        const float(&mo)[EW_BATCH] = cur.mo;
+        const float(&vo)[EW_BATCH] = cur.vo;
+        const float(&p)[EW_BATCH] = cur.p;
 #pragma unroll
         for (int k = 0; k < EW_BATCH; ++k) {
             const int64_t e = e0 + k * WAVE;
@@ -1369,6 +1468,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
                 store1(L.nu, mdt, e, vv);
             }
         }
+        cur = nxt;
     }
     if (msum) acc.store(c, chunk);
 }
