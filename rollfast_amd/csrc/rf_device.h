@@ -39,6 +39,13 @@ constexpr int WG = 256;  // four waves per workgroup
 constexpr int WAVES_PER_WG = WG / WAVE;
 constexpr int64_t FAST_BS = 2048;  // block size of the vectorised path
 constexpr int64_t CHUNK = 2048;    // elements per fallback (unquantized moment) work unit
+// Element-wise fallback units (leaves' tails that are not whole aligned
+// chunks): in fused launches 256 elements, one batch per lane, so a small
+// leaf spreads over several waves; update-only launches keep whole chunks,
+// the slots of Magma's partial sums.
+constexpr int64_t EW_UNIT_FUSED = 256;
+template <bool APPLY>
+constexpr int64_t EW_UNIT = APPLY ? EW_UNIT_FUSED : CHUNK;
 
 // Waves per SIMD the step kernel is register-allocated for (<= 512 / N VGPRs).
 #ifndef RF_STEP_WAVES_PER_EU
@@ -1409,13 +1416,14 @@ __device__ __forceinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf&
 
 // ============================================= work units: fallback ====
 // Moments stored unquantized (adam8.py:620-630: size < min_size, a
-// non-inexact dtype or quantize=False): elementwise update of a chunk.
+// non-inexact dtype or quantize=False): elementwise update of elements
+// [base, end).  Magma's partial sums (update-only launches, whose units are
+// whole chunks) go to the slot of chunk base / CHUNK.
 template <bool APPLY, bool PSR, bool NEST, bool EXACT>
-__device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_leaf& L, int64_t chunk, const KHp& h)
+__device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_leaf& L, int64_t base, int64_t end,
+                                              const KHp& h)
 {
     const int lane = threadIdx.x & (WAVE - 1);
-    const int64_t base = chunk * CHUNK;
-    const int64_t end = min(base + CHUNK, L.size);
     const int32_t mdt = L.moment_kind == RF_MOMENT_BF16 ? RF_BF16 : (L.moment_kind == RF_MOMENT_F16 ? RF_F16 : RF_F32);
     const bool store_sr = mdt == RF_BF16 && (L.flags & RF_LEAF_STORE_SR);
     const bool need_p = APPLY || c.wd_mode != WD_OFF || c.zero;
@@ -1470,7 +1478,7 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
         }
         cur = nxt;
     }
-    if (msum) acc.store(c, chunk);
+    if (msum) acc.store(c, base / CHUNK);
 }
 
 // Full 2048-element chunk of a fallback (unquantized-moment) leaf whose
@@ -1636,7 +1644,9 @@ __device__ __forceinline__ void dispatch_fallback_vec(const UnitCtx& c, const rf
     case H + RF_F16:
         unit_fallback_vec<_Float16, _Float16, _Float16, APPLY, PSR, NEST, EXACT>(c, L, chunk, h);
         break;
-    default: unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, chunk, h); break;
+    default:
+        unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, chunk * CHUNK, min(chunk * CHUNK + CHUNK, L.size), h);
+        break;
     }
 }
 
@@ -1706,7 +1716,9 @@ __device__ void reject_units(const rf_adam8_leaf* __restrict__ leaves, const Seg
         s = seek_seg(segs, nseg, s, u);
         const Seg sg = segs[s];
         const rf_adam8_leaf& L = leaves[sg.leaf];
-        const int64_t span = (sg.kind == KIND_QFAST || sg.kind == KIND_QGEN) ? (int64_t)L.block_size : CHUNK;
+        const int64_t span = (sg.kind == KIND_QFAST || sg.kind == KIND_QGEN) ? (int64_t)L.block_size
+                             : sg.kind == KIND_FALLBACK                    ? EW_UNIT<APPLY>
+                                                                           : CHUNK;
         const int64_t base = (sg.first + (u - sg.unit_start)) * span;
         const int64_t end = min(base + span, L.size);
         for (int64_t e = base + lane; e < end; e += WAVE) {
@@ -1846,7 +1858,8 @@ void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
         } else {
             if (sg.kind == KIND_QGEN) unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, hl);
             else if (sg.kind == KIND_FALLBACK_VEC) dispatch_fallback_vec<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
-            else unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
+            else unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, idx * EW_UNIT<APPLY>,
+                                                         min(idx * EW_UNIT<APPLY> + EW_UNIT<APPLY>, L.size), hl);
         }
     }
 }

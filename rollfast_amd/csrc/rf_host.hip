@@ -1217,6 +1217,8 @@ inline bool valid_dtype(int32_t d) { return d == RF_F32 || d == RF_BF16 || d == 
 // full-chunk fallback units only.
 constexpr int COMBO_F16 = 4;
 constexpr int GEN_LIST = 5;    // the generic kernel's work list
+constexpr int GEN_TAIL = 6;    // build space: its fallback units, appended after its quantized ones
+constexpr int64_t GEN_WAVE_PER_UNIT_MAX_ROUNDS = 8;  // mixed generic lists up to 8 chip-fulls: one unit per wave
 constexpr int VEC_COMBO = -2;  // a generic list of full-chunk fallback units only
 
 adam_kernel_t pick_adam_kernel(bool apply, bool msr, bool psr, bool nest, bool exact, int combo)
@@ -1440,15 +1442,15 @@ struct WorkLists {
     std::vector<Seg> msegs;          // Magma chunk slots (every leaf unquantized), else empty
     int64_t mchunks = -1;
     std::vector<uint8_t> vecs;       // leaf has 16-byte aligned (vectorised) units
-    std::vector<Seg> gsegs[6];       // build space: the lists of each dtype combination and the generic one
+    std::vector<Seg> gsegs[7];       // build space: the lists of each dtype combination, the generic one and its tail
 };
 
 rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply, WorkLists& w)
 {
     rf_status st = RF_OK;
     std::vector<Seg>* gsegs = w.gsegs;
-    for (int c = 0; c <= GEN_LIST; ++c) gsegs[c].clear();
-    int64_t gunits[GEN_LIST + 1] = {0, 0, 0, 0, 0, 0};
+    for (int c = 0; c <= GEN_TAIL; ++c) gsegs[c].clear();
+    int64_t gunits[GEN_TAIL + 1] = {0, 0, 0, 0, 0, 0, 0};
     auto add = [&](int32_t leaf, int combo, int32_t kind, int64_t first, int64_t count) {
         if (count <= 0) return;
         Seg sg{};
@@ -1482,12 +1484,21 @@ rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_
             }
         } else {
             // Full chunks of aligned leaves take the vectorised unit, the
-            // tail the element-wise one.
+            // tail element-wise units of EW_UNIT<apply> elements.
             const int64_t nfull = vec ? L.size / CHUNK : 0;
-            add(i, GEN_LIST, KIND_FALLBACK_VEC, 0, nfull);
-            add(i, GEN_LIST, KIND_FALLBACK, nfull, (L.size - nfull * CHUNK + CHUNK - 1) / CHUNK);
+            const int64_t ew = apply ? EW_UNIT<true> : EW_UNIT<false>;
+            add(i, GEN_TAIL, KIND_FALLBACK_VEC, 0, nfull);
+            add(i, GEN_TAIL, KIND_FALLBACK, nfull * CHUNK / ew, (L.size - nfull * CHUNK + ew - 1) / ew);
         }
     }
+    // The generic list holds the quantized units (the long ones: two passes
+    // over a block) first, so that they start in the launch's first
+    // workgroups, then the fallback units.
+    for (Seg sg : gsegs[GEN_TAIL]) {
+        sg.unit_start += gunits[GEN_LIST];
+        gsegs[GEN_LIST].push_back(sg);
+    }
+    gunits[GEN_LIST] += gunits[GEN_TAIL];
     std::vector<Seg>& segs = w.segs;
     std::vector<PlanGroup>& groups = w.groups;
     segs.clear();
@@ -1836,7 +1847,14 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         const int64_t wg_spread = std::min(
             wg_needed, (g.units + (int64_t)WAVES_PER_WG * STEP_UNITS_PER_WAVE - 1) / (WAVES_PER_WG * STEP_UNITS_PER_WAVE));
         int64_t grid = std::max<int64_t>(1, std::max(std::min(wg_needed, wg_resident), wg_spread));
-        if (STEP_GRID_ROUNDS && grid > wg_resident) {
+        if (g.combo == -1 && wg_needed <= GEN_WAVE_PER_UNIT_MAX_ROUNDS * wg_resident) {
+            // Mixed generic lists: one unit per wave.  Their units are short
+            // and latency-bound (a partial block, a leaf's tail), so the
+            // workgroups beyond a chip-full queue behind the first ones'
+            // quick element-wise units instead of stacking a second unit
+            // behind a wave's partial block.
+            grid = wg_needed;
+        } else if (STEP_GRID_ROUNDS && grid > wg_resident) {
             // a whole number of chip-fulls of workgroups: no last partial round
             const int64_t rounds = std::max<int64_t>(1, (grid + wg_resident / 2) / wg_resident);
             grid = std::min(wg_needed, rounds * wg_resident);
