@@ -94,7 +94,7 @@ struct Seg {
     int32_t leaf;
     int32_t kind;
     int32_t nseg;   // the list's sentinel index (its segment count), in every record
-    int32_t reserved;
+    int32_t lead;   // generic list: its leading quantized units, taken a workgroup each (in every record)
 };
 static_assert(sizeof(Seg) == 32, "Seg is 32 bytes");
 
@@ -846,16 +846,18 @@ struct QBatch {
     float g[B], p[B];
 };
 
-// The coding pass of a partial or odd-sized block (the generic kernel): with
-// the block's new absmax bits (am, av), every element of the block, the
-// padding past the leaf's end as zero (adam8.py:137-141), is coded from its
-// moments, recomputed from the old codes and scales, which are still in
-// place; then the new scales are written.  The next batch's loads are issued
-// before this batch's arithmetic and stores, so a batch does not wait for
-// the previous batch's stores.
+// The coding pass of a partial or odd-sized block (the generic kernel), over
+// the wave's elements [lo, hi) of the block: with the block's new absmax
+// bits (am, av), every element, the padding past the leaf's end as zero
+// (adam8.py:137-141), is coded from its moments, recomputed from the old
+// codes and scales, which are still in place; the new scales are written
+// where `scales` is set (one wave of the block).  The next batch's loads are
+// issued before this batch's arithmetic and stores, so a batch does not wait
+// for the previous batch's stores.
 template <bool MSR, int B>
 __device__ __forceinline__ void literal_code(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
-                                             float sm_old, float sv_old, uint32_t am, uint32_t av)
+                                             float sm_old, float sv_old, uint32_t am, uint32_t av, int64_t lo,
+                                             int64_t hi, bool scales)
 {
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t bs = L.block_size;
@@ -869,16 +871,16 @@ __device__ __forceinline__ void literal_code(const UnitCtx& c, const rf_adam8_le
     const bool fast_v = !MSR && block_is_fast(av, sv);
     const float rsm = 1.0f / sm;
     const float rsv = 1.0f / sv;
-    const int64_t nb = (bs + B * WAVE - 1) / (B * WAVE);
+    const int64_t nb = (hi - lo + B * WAVE - 1) / (B * WAVE);
     QBatch<B> cur{}, nxt{};
-    load_batch<B>(c, L, base, lane, nvalid, cur.cm, cur.cv, cur.g);
+    if (nb > 0) load_batch<B>(c, L, base, lo + lane, nvalid, cur.cm, cur.cv, cur.g);
     for (int64_t i = 0; i < nb; ++i) {
-        const int64_t j0 = lane + i * (B * WAVE);
+        const int64_t j0 = lo + lane + i * (B * WAVE);
         if (i + 1 < nb) load_batch<B>(c, L, base, j0 + B * WAVE, nvalid, nxt.cm, nxt.cv, nxt.g);
 #pragma unroll
         for (int k = 0; k < B; ++k) {
             const int64_t j = j0 + k * WAVE;
-            if (j >= bs) continue;
+            if (j >= hi) continue;
             const int64_t e = base + j;
             float mm = 0.0f, vv = 0.0f;  // zero padding past the leaf's end
             if (j < nvalid) ema(h, cbs[cur.cm[k]] * sm_old, cbu[cur.cv[k]] * sv_old, cur.g[k], mm, vv);
@@ -902,7 +904,7 @@ __device__ __forceinline__ void literal_code(const UnitCtx& c, const rf_adam8_le
         }
         cur = nxt;
     }
-    if (lane == 0) {
+    if (scales && lane == 0) {
         store_scale(L.mu_scales, L.flags, blk, sm);
         store_scale(L.nu_scales, L.flags, blk, sv);
     }
@@ -1364,42 +1366,41 @@ __device__ __forceinline__ void dispatch_qfast(const UnitCtx& c, const rf_adam8_
 // finds the new absmax, the second recomputes the moments and writes the
 // params/updates, then the codes are requantized from the old codes (still
 // in place).  Elements past `size` are the reference's zero padding.
-template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
-__device__ __forceinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h)
+// The update pass of a partial or odd-sized block over the wave's valid
+// elements [lo, hi): params updated, and the absmax bits of the new moments
+// (the NaN-propagating max of adam8.py:142) reduced over the wave.  The next
+// batch's loads are in flight behind each batch.
+template <bool APPLY, bool PSR, bool NEST, bool EXACT>
+__device__ __forceinline__ void qgen_update(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
+                                            float sm_old, float sv_old, int64_t lo, int64_t hi, uint32_t& am,
+                                            uint32_t& av)
 {
     const int lane = threadIdx.x & (WAVE - 1);
-    const int64_t bs = L.block_size;
-    const int64_t base = blk * bs;
-    const int64_t nvalid = max((int64_t)0, min(bs, L.size - base));
+    const int64_t base = blk * (int64_t)L.block_size;
     const float* cbs = (const float*)(c.lds + L_CBS);
     const float* cbu = (const float*)(c.lds + L_CBU);
-    const float sm_old = load_scale(L.mu_scales, L.flags, blk);
-    const float sv_old = load_scale(L.nu_scales, L.flags, blk);
-
-    // One pass updates the params and takes the new moments' absmax (the
-    // NaN-propagating max of adam8.py:142 over the valid elements), the
-    // next batch's loads in flight behind each batch; then the coding pass.
     const bool need_p = APPLY || c.wd_mode != WD_OFF;
     constexpr int B = EW_BATCH;
-    const int64_t nb = (nvalid + B * WAVE - 1) / (B * WAVE);
+    const int64_t nb = (hi - lo + B * WAVE - 1) / (B * WAVE);
     auto load = [&](int64_t j0, QBatch<B>& q) {
-        load_batch<B>(c, L, base, j0, nvalid, q.cm, q.cv, q.g);
+        load_batch<B>(c, L, base, j0, hi, q.cm, q.cv, q.g);
 #pragma unroll
         for (int k = 0; k < B; ++k) {
             const int64_t j = j0 + k * WAVE;
-            q.p[k] = (need_p && j < nvalid) ? load1(L.param, L.param_dtype, base + j) : 0.0f;
+            q.p[k] = (need_p && j < hi) ? load1(L.param, L.param_dtype, base + j) : 0.0f;
         }
     };
-    uint32_t am = 0, av = 0;
+    am = 0;
+    av = 0;
     QBatch<B> cur{}, nxt{};
-    if (nb > 0) load(lane, cur);
+    if (nb > 0) load(lo + lane, cur);
     for (int64_t i = 0; i < nb; ++i) {
-        const int64_t j0 = lane + i * (B * WAVE);
+        const int64_t j0 = lo + lane + i * (B * WAVE);
         if (i + 1 < nb) load(j0 + B * WAVE, nxt);
 #pragma unroll
         for (int k = 0; k < B; ++k) {
             const int64_t j = j0 + k * WAVE;
-            if (j < nvalid) {
+            if (j < hi) {
                 float mm, vv;
                 ema(h, cbs[cur.cm[k]] * sm_old, cbu[cur.cv[k]] * sv_old, cur.g[k], mm, vv);
                 am = max(am, __float_as_uint(mm) & 0x7FFFFFFFu);
@@ -1411,7 +1412,40 @@ __device__ __forceinline__ void unit_qgen(const UnitCtx& c, const rf_adam8_leaf&
     }
     am = wave_max_u32(am);
     av = wave_max_u32(av);
-    literal_code<MSR, B>(c, L, blk, h, sm_old, sv_old, am, av);
+}
+
+// A partial or odd-sized block (KIND_QGEN) by the workgroup's waves
+// together: the update pass, which also takes the new moments' absmax, then
+// the coding pass; wave w updates and codes its quarter of the block
+// (rounded up to whole batches), the four waves' absmax bits meet in LDS.  Called by every wave of the workgroup
+// (it holds two barriers); `red` is 8 words of LDS.
+template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
+__device__ __forceinline__ void unit_qgen_wg(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
+                                             uint32_t* red)
+{
+    constexpr int64_t BW = EW_BATCH * WAVE;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int w = (int)uniform_u32(threadIdx.x / WAVE);
+    const int64_t bs = L.block_size;
+    const int64_t nvalid = max((int64_t)0, min(bs, L.size - blk * bs));
+    const int64_t quarter = ((bs + WAVES_PER_WG - 1) / WAVES_PER_WG + BW - 1) / BW * BW;
+    const int64_t lo = min(bs, w * quarter), hi = min(bs, lo + quarter);
+    const float sm_old = load_scale(L.mu_scales, L.flags, blk);
+    const float sv_old = load_scale(L.nu_scales, L.flags, blk);
+    uint32_t am, av;
+    qgen_update<APPLY, PSR, NEST, EXACT>(c, L, blk, h, sm_old, sv_old, lo, min(hi, nvalid), am, av);
+    if (lane == 0) {
+        red[2 * w] = am;
+        red[2 * w + 1] = av;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < WAVES_PER_WG; ++k) {
+        am = max(am, red[2 * k]);
+        av = max(av, red[2 * k + 1]);
+    }
+    __syncthreads();  // red is free for the workgroup's next block
+    literal_code<MSR, EW_BATCH>(c, L, blk, h, sm_old, sv_old, am, av, lo, hi, w == 0);
 }
 
 // ============================================= work units: fallback ====
@@ -1819,6 +1853,7 @@ void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
                                                   const uint4* __restrict__ tables)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
+    __shared__ uint32_t red[2 * WAVES_PER_WG];  // absmax bits of a workgroup's block, per wave
     if (!VEC_ONLY && tables) stage_tables(lds, tables);  // null: the list has no quantized units
 
     const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
@@ -1842,7 +1877,24 @@ void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
     c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;
     rf_adam8_leaf L;
     KHp hl = h;  // the current leaf's scalars (its group's, in a grouped launch)
-    for (int64_t u = wave; u < total_units; u += nwaves) {
+    // The list's leading quantized units (partial and odd-sized blocks, the
+    // long ones), a workgroup each; then the rest a wave each, handed out
+    // from the grid's last waves down so that the workgroups of the first
+    // phase take none when the grid covers every unit.
+    const int64_t nlead = VEC_ONLY ? 0 : segs[0].lead;
+    for (int64_t q = blockIdx.x; q < nlead; q += gridDim.x) {
+        s = seek_seg(segs, nseg, s, q);
+        const Seg sg = segs[s];
+        if (sg.leaf != cur_leaf) {
+            cur_leaf = sg.leaf;
+            L = leaves[cur_leaf];
+            group_hparams(hl, h, L);
+            leaf_context<false>(c, L, hl, MSR, PSR);
+            if (h.mpart) c.mbase = h.msegs[cur_leaf].unit_start;
+        }
+        unit_qgen_wg<APPLY, MSR, PSR, NEST, EXACT>(c, L, sg.first + (q - sg.unit_start), hl, red);
+    }
+    for (int64_t u = nlead + (nwaves - 1 - wave); u < total_units; u += nwaves) {
         s = seek_seg(segs, nseg, s, u);
         const Seg sg = segs[s];
         if (sg.leaf != cur_leaf) {
@@ -1856,8 +1908,8 @@ void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
         if constexpr (VEC_ONLY) {
             dispatch_fallback_vec<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
         } else {
-            if (sg.kind == KIND_QGEN) unit_qgen<APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, hl);
-            else if (sg.kind == KIND_FALLBACK_VEC) dispatch_fallback_vec<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
+            // (the list's quantized units are all among the leading ones)
+            if (sg.kind == KIND_FALLBACK_VEC) dispatch_fallback_vec<APPLY, PSR, NEST, EXACT>(c, L, idx, hl);
             else unit_fallback<APPLY, PSR, NEST, EXACT>(c, L, idx * EW_UNIT<APPLY>,
                                                          min(idx * EW_UNIT<APPLY> + EW_UNIT<APPLY>, L.size), hl);
         }

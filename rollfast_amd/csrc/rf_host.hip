@@ -1332,7 +1332,8 @@ struct PlanGroup {
     int combo;
     int64_t seg_offset;
     int64_t units;
-    bool tables;  // the list holds quantized units (the kernel stages the LDS tables)
+    bool tables;   // the list holds quantized units (the kernel stages the LDS tables)
+    int64_t lead;  // generic list: leading quantized units, a workgroup each
 };
 
 struct rf_adam8_plan {
@@ -1406,11 +1407,15 @@ rf_status validate_leaf(const rf_adam8_leaf& L, int32_t i, int32_t apply)
 }
 
 // Stores the sentinel's index (the list's last record) in every record of a
-// work list, for the kernels' binary search.
-void mark_list(std::vector<Seg>& list)
+// work list, for the kernels' segment search, and the generic list's count
+// of leading quantized units (0 for the other lists).
+void mark_list(std::vector<Seg>& list, int32_t lead = 0)
 {
     const int32_t n = (int32_t)list.size() - 1;
-    for (Seg& sg : list) sg.nseg = n;
+    for (Seg& sg : list) {
+        sg.nseg = n;
+        sg.lead = lead;
+    }
 }
 
 bool leaf_vec_ok(const rf_adam8_leaf& L, int32_t apply)
@@ -1492,8 +1497,11 @@ rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_
         }
     }
     // The generic list holds the quantized units (the long ones: two passes
-    // over a block) first, so that they start in the launch's first
-    // workgroups, then the fallback units.
+    // over a block) first, a workgroup each, then the fallback units, a wave
+    // each.
+    if (gunits[GEN_LIST] > INT32_MAX)
+        return fail(RF_ERR_UNSUPPORTED, "more than 2^31 - 1 partial or odd-sized quantized blocks in one launch");
+    const int64_t gen_lead = gunits[GEN_LIST];
     for (Seg sg : gsegs[GEN_TAIL]) {
         sg.unit_start += gunits[GEN_LIST];
         gsegs[GEN_LIST].push_back(sg);
@@ -1512,13 +1520,14 @@ rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_
             vec_only &= sg.kind == KIND_FALLBACK_VEC;
         }
         const int kc = combo != GEN_LIST ? combo : (vec_only ? VEC_COMBO : -1);
-        groups.push_back({kc, (int64_t)segs.size(), gunits[combo], quant});
+        const int64_t lead = kc == -1 ? gen_lead : 0;
+        groups.push_back({kc, (int64_t)segs.size(), gunits[combo], quant, lead});
         Seg sentinel{};
         sentinel.unit_start = gunits[combo];
         sentinel.leaf = -1;
         sentinel.kind = -1;
         gsegs[combo].push_back(sentinel);
-        mark_list(gsegs[combo]);
+        mark_list(gsegs[combo], (int32_t)lead);
         segs.insert(segs.end(), gsegs[combo].begin(), gsegs[combo].end());
         units += gunits[combo];
     }
@@ -1847,13 +1856,14 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         const int64_t wg_spread = std::min(
             wg_needed, (g.units + (int64_t)WAVES_PER_WG * STEP_UNITS_PER_WAVE - 1) / (WAVES_PER_WG * STEP_UNITS_PER_WAVE));
         int64_t grid = std::max<int64_t>(1, std::max(std::min(wg_needed, wg_resident), wg_spread));
-        if (g.combo == -1 && wg_needed <= GEN_WAVE_PER_UNIT_MAX_ROUNDS * wg_resident) {
-            // Mixed generic lists: one unit per wave.  Their units are short
-            // and latency-bound (a partial block, a leaf's tail), so the
-            // workgroups beyond a chip-full queue behind the first ones'
-            // quick element-wise units instead of stacking a second unit
-            // behind a wave's partial block.
-            grid = wg_needed;
+        const int64_t wg_each = g.lead + (g.units - g.lead + WAVES_PER_WG - 1) / WAVES_PER_WG;
+        if (g.combo == -1 && wg_each <= GEN_WAVE_PER_UNIT_MAX_ROUNDS * wg_resident) {
+            // Mixed generic lists: a workgroup per leading quantized unit,
+            // then a wave per unit.  These units are latency-bound (a
+            // partial block, a leaf's tail), so the workgroups beyond a
+            // chip-full queue behind the first ones' short units instead of
+            // stacking a second unit behind a wave's partial block.
+            grid = wg_each;
         } else if (STEP_GRID_ROUNDS && grid > wg_resident) {
             // a whole number of chip-fulls of workgroups: no last partial round
             const int64_t rounds = std::max<int64_t>(1, (grid + wg_resident / 2) / wg_resident);

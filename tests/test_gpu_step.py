@@ -201,6 +201,16 @@ def test_generic_block_size_256_and_nesterov():
     _run(spec, steps=2, block_size=256, min_size=16, nesterov=True, exact=True)
 
 
+@pytest.mark.parametrize("msr,psr", [(False, False), (True, True)])
+def test_block_size_4096_partial_blocks_by_workgroup(msr, psr):
+    """Blocks of 4096 (every block a generic unit, taken by a workgroup's
+    four waves, 1024 elements each): whole blocks and partial last ones
+    (15000 = 3 x 4096 + 2712, 9000 = 2 x 4096 + 808), with moment and param
+    stochastic rounding."""
+    spec = [((3, 5000), "bf16", "bf16"), ((9000,), "bf16", "f32")]
+    _run(spec, steps=2, block_size=4096, min_size=4096, msr=msr, psr=psr, exact=True)
+
+
 def test_odd_block_size_and_eps_root():
     spec = [((10, 300), "bf16", "bf16"), ((7000,), "f32", "bf16")]
     _run(spec, steps=2, block_size=1000, min_size=100, eps_root=1e-12, exact=True)
