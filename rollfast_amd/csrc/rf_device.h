@@ -552,6 +552,11 @@ __device__ __forceinline__ RF_GLOBAL T* gstore_ptr(void* p, int64_t byte_off)
     return (RF_GLOBAL T*)((RF_GLOBAL uint8_t*)p + byte_off);
 }
 
+// Native vectors for __builtin_nontemporal_store (HIP's uint2 / float4 are
+// structs, which the builtin does not take).
+typedef uint32_t nt_u32x2 __attribute__((ext_vector_type(2)));
+typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
+
 // Element i of a T array, read or written through its global view.
 template <typename T>
 __device__ __forceinline__ T gld(const void* p, int64_t i)

@@ -163,7 +163,8 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const void* 
                 uint2 w;
                 w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
                 w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
-                *(uint2*)(values + e0) = w;
+                // nontemporal: the codes are not read again by this launch
+                __builtin_nontemporal_store((nt_u32x2){w.x, w.y}, (nt_u32x2*)(values + e0));
                 if (next_full) load_chunk(b + nwaves, j, xr);
             }
             have = next_full;
@@ -186,18 +187,16 @@ __global__ __launch_bounds__(WG) void k_quantize(int32_t quantizer, const void* 
 // codes / 16-byte (f32) or 8-byte (bf16) aligned output.
 __device__ __forceinline__ void dq_store4(void* out, int32_t out_dtype, int64_t e, const float (&o)[4])
 {
+    // nontemporal: the launch does not read its output back
     if (out_dtype == RF_BF16) {
-        uint2 w;
-        w.x = f32_to_bf16_rne(o[0]) | (f32_to_bf16_rne(o[1]) << 16);
-        w.y = f32_to_bf16_rne(o[2]) | (f32_to_bf16_rne(o[3]) << 16);
-        *(uint2*)((uint16_t*)out + e) = w;
+        const nt_u32x2 w = {f32_to_bf16_rne(o[0]) | (f32_to_bf16_rne(o[1]) << 16),
+                            f32_to_bf16_rne(o[2]) | (f32_to_bf16_rne(o[3]) << 16)};
+        __builtin_nontemporal_store(w, (nt_u32x2*)((uint16_t*)out + e));
     } else if (out_dtype == RF_F16) {
-        uint2 w;
-        w.x = pack_f16x2_rne(o[0], o[1]);
-        w.y = pack_f16x2_rne(o[2], o[3]);
-        *(uint2*)((uint16_t*)out + e) = w;
+        const nt_u32x2 w = {pack_f16x2_rne(o[0], o[1]), pack_f16x2_rne(o[2], o[3])};
+        __builtin_nontemporal_store(w, (nt_u32x2*)((uint16_t*)out + e));
     } else {
-        *(float4*)((float*)out + e) = make_float4(o[0], o[1], o[2], o[3]);
+        __builtin_nontemporal_store((nt_f32x4){o[0], o[1], o[2], o[3]}, (nt_f32x4*)((float*)out + e));
     }
 }
 
@@ -1271,18 +1270,18 @@ rf_status occupancy(const void* fn, int* blocks)
 int64_t nblocks_of(int64_t size, int64_t bs) { return size > 0 ? (size + bs - 1) / bs : 1; }
 
 // Grid of a work-list kernel that walks `nunits` units, one per wave at a
-// time: about STEP_UNITS_PER_WAVE units per wave, never fewer workgroups
+// time: about `per_wave` units per wave, never fewer workgroups
 // than fit on the chip at once, rounded to whole chip-fulls (the kernel's
 // own occupancy), so that no last, mostly idle round of workgroups runs.
-rf_status worklist_grid(const void* fn, const DevState* ds, int64_t nunits, unsigned* grid)
+rf_status worklist_grid(const void* fn, const DevState* ds, int64_t nunits, unsigned* grid,
+                        int64_t per_wave = STEP_UNITS_PER_WAVE)
 {
     int occ = 1;
     const rf_status st = occupancy(fn, &occ);
     if (st != RF_OK) return st;
     const int64_t wg_needed = std::max<int64_t>(1, (nunits + WAVES_PER_WG - 1) / WAVES_PER_WG);
     const int64_t resident = (int64_t)ds->num_cus * occ;
-    const int64_t spread = (nunits + (int64_t)WAVES_PER_WG * STEP_UNITS_PER_WAVE - 1) /
-                           ((int64_t)WAVES_PER_WG * STEP_UNITS_PER_WAVE);
+    const int64_t spread = (nunits + (int64_t)WAVES_PER_WG * per_wave - 1) / ((int64_t)WAVES_PER_WG * per_wave);
     int64_t g = std::min(wg_needed, std::max(resident, spread));
     if (g > resident) g = std::min(wg_needed, std::max<int64_t>(1, (g + resident / 2) / resident) * resident);
     *grid = (unsigned)std::max<int64_t>(1, g);
@@ -2114,9 +2113,12 @@ rf_status rf_blockwise_quantize(int32_t quantizer, const void* x, int32_t x_dtyp
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
     const int64_t nb = nblocks_of(size, block_size);
-    // One wave per block at a time, about STEP_UNITS_PER_WAVE blocks per wave.
+    // One wave per block at a time, about 4 blocks per wave: on 2^30 f32
+    // elements 0.968 ms, against 1.047 ms at 16 blocks per wave with ordinary
+    // code stores and 1.023-1.027 ms with nontemporal ones; 2 per wave 0.971,
+    // 1 per wave 0.986 (each workgroup stages its tables once).
     unsigned grid = 1;
-    st = worklist_grid((const void*)&k_quantize, ds, nb, &grid);
+    st = worklist_grid((const void*)&k_quantize, ds, nb, &grid, 4);
     if (st != RF_OK) return st;
     const int32_t vec_ok = aligned(x, 16) && aligned(values, 8) && (!bits || aligned(bits, 16));
     hipLaunchKernelGGL(k_quantize, dim3(grid), dim3(WG), 0, (hipStream_t)stream, quantizer, x, x_dtype, size,
@@ -2143,12 +2145,15 @@ rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const v
     int32_t bs_log2 = 0;
     while (pow2 && (1 << bs_log2) < block_size) ++bs_log2;
     const int32_t vec_ok = pow2 && aligned(values, 4) && aligned(out, out_dtype == RF_F32 ? 16 : 8);
-    // Vector path: one wave per two 1024-element tiles, at most 8 waves' worth
-    // of workgroups per CU; the scalar tail needs few threads.
+    // Vector path: one wave per two 1024-element tiles, every pair its own
+    // wave (the workgroup stages only the 1 KB codebook): on 2^30 elements
+    // 0.963 ms against 1.056 ms for a grid of 8 workgroups per CU walking the
+    // tiles, 0.934 ms with nontemporal stores.  The scalar tail needs few
+    // threads.
     const int64_t tiles = vec_ok ? size / 1024 : 0;
     const int64_t wg_needed = std::max<int64_t>(1, (tiles + 2 * WAVES_PER_WG - 1) / (2 * WAVES_PER_WG));
     const int grid = (int)std::min<int64_t>(std::max<int64_t>(wg_needed, vec_ok ? 1 : (size + WG - 1) / WG),
-                                            (int64_t)ds->num_cus * 8);
+                                            (int64_t)1 << 30);
     hipLaunchKernelGGL(k_dequantize, dim3(grid), dim3(WG), 0, (hipStream_t)stream, quantizer,
                        (const uint8_t*)values, scales, scale_dtype, size, (int64_t)block_size, bs_log2, out_dtype,
                        out, ds->tables, vec_ok);
