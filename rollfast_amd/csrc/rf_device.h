@@ -1367,10 +1367,11 @@ __device__ __forceinline__ void dispatch_qfast(const UnitCtx& c, const rf_adam8_
     else unit_qfast<PT, GT, WD_OFF, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h, sl, have0, next_blk);
 }
 
-// Any block size, partial or unaligned blocks (KIND_QGEN).  The first pass
-// finds the new absmax, the second recomputes the moments and writes the
-// params/updates, then the codes are requantized from the old codes (still
-// in place).  Elements past `size` are the reference's zero padding.
+// Any block size, partial or unaligned blocks (KIND_QGEN): an update pass
+// writes the params/updates and takes the new moments' absmax, then the
+// coding pass recomputes the moments from the old codes (still in place) and
+// requantizes them.  Elements past `size` are the reference's zero padding.
+//
 // The update pass of a partial or odd-sized block over the wave's valid
 // elements [lo, hi): params updated, and the absmax bits of the new moments
 // (the NaN-propagating max of adam8.py:142) reduced over the wave.  The next
@@ -1837,9 +1838,10 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     }
 }
 
-// Everything else, one wave per unit: quantized blocks of other sizes,
-// partial or unaligned blocks (two passes, literal requantization) and
-// leaves with unquantized (fallback) moments.  Dtypes are read per leaf.
+// Everything else: quantized blocks of other sizes and partial or unaligned
+// blocks (a workgroup each; two passes, literal requantization), then the
+// leaves with unquantized (fallback) moments (a wave per unit).  Dtypes are
+// read per leaf.
 // VEC_ONLY: an instance for lists of full-chunk fallback units only (the
 // full-precision AdamW trees).  Without the other unit kinds its plain
 // instances take 126-127 VGPRs (4 waves per SIMD) as the compiler schedules
