@@ -440,7 +440,9 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
             # the updates (4) and the params and writes the params (2 + 2)
             nbytes = n_params * ((2 + 2 + 2 * 2 * mb + 4) + (4 + 2 + 2))
         cpu = None
-    return Workload(workload, n_params, "params/s", nbytes, step, config, cpu, metric)
+    wl = Workload(workload, n_params, "params/s", nbytes, step, config, cpu, metric)
+    wl.holder = holder  # params and optimizer state, for the placement study's cross pairs
+    return wl
 
 
 def _c5_input(n, seed=5):
@@ -569,6 +571,92 @@ WORKLOADS = {
 }
 
 
+def placement_study(args):
+    """Times args.copies independent copies of one workload in one process.
+
+    The copies run the same kernels on the same shapes and differ only in
+    where their buffers landed in device memory.  Each round steps every
+    copy once, in ascending order on even rounds and descending on odd ones,
+    each step bracketed by HIP events and a synchronize.  The JSON line lists
+    the copies in step order (warmup steps included) so that a profiler's
+    dispatches can be matched to their copy."""
+    import statistics
+
+    import torch
+
+    wls = []
+    for c in range(args.copies):
+        wls.append(WORKLOADS[args.workload](args))
+        torch.cuda.synchronize()
+        print(f"[bench] copy {c} built; {torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated",
+              file=sys.stderr, flush=True)
+    order = []
+    for c, wl in enumerate(wls):
+        for _ in range(args.warmup):
+            wl.step()
+            order.append(c)
+    torch.cuda.synchronize()
+    times = [[] for _ in wls]
+    for r in range(args.steps):
+        for c in (range(len(wls)) if r % 2 == 0 else reversed(range(len(wls)))):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            wls[c].step()
+            e1.record()
+            torch.cuda.synchronize()
+            times[c].append(e0.elapsed_time(e1))
+            order.append(c)
+    for c, t in enumerate(times):
+        print(f"[bench] copy {c}: median {statistics.median(t):.3f} ms, min {min(t):.3f}, max {max(t):.3f}",
+              file=sys.stderr, flush=True)
+    cross = None
+    if args.cross:
+        # copy a's params and grads stepped with copy b's optimizer state:
+        # three steps per pair, the best of the last two, two rounds in
+        # opposite pair order
+        holders = [getattr(wl, "holder", None) for wl in wls]
+        if any(h is None for h in holders):
+            raise SystemExit(f"--cross needs an optimizer-step workload, not {args.workload}")
+        n = len(wls)
+        best = [[float("inf")] * n for _ in range(n)]
+        pairs = [(a, b) for a in range(n) for b in range(n)]
+        for r in range(2):
+            for a, b in (pairs if r == 0 else pairs[::-1]):
+                own = holders[a]["state"]
+                holders[a]["state"] = holders[b]["state"]
+                t = []
+                for _ in range(3):
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    wls[a].step()
+                    e1.record()
+                    torch.cuda.synchronize()
+                    t.append(e0.elapsed_time(e1))
+                holders[b]["state"] = holders[a]["state"]  # the stepped state stays copy b's
+                if a != b:
+                    holders[a]["state"] = own
+                best[a][b] = min(best[a][b], min(t[1:]))
+        cross = best
+        for a in range(n):
+            print("[bench] params/grads of copy %d with the state of copies 0..%d: %s"
+                  % (a, n - 1, " ".join(f"{x:.3f}" for x in best[a])), file=sys.stderr, flush=True)
+    print(json.dumps({
+        "study": "placement",
+        "config": wls[0].config,
+        "copies": args.copies,
+        "steps_per_copy": args.steps,
+        "warmup_per_copy": args.warmup,
+        "ms_median": [statistics.median(t) for t in times],
+        "ms_min": [min(t) for t in times],
+        "ms_max": [max(t) for t in times],
+        "step_order": order,
+        "cross_ms": cross,
+    }), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -580,6 +668,11 @@ def main(argv=None):
     ap.add_argument("--param-sr", action="store_true", help="stochastic rounding of bf16 params")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copies", type=int, default=1,
+                    help="placement study: build this many independent copies of the workload, time their "
+                         "steps in alternating order and print each copy's times instead of the benchmark line")
+    ap.add_argument("--cross", action="store_true",
+                    help="with --copies: also time every pair (params and grads of copy a, optimizer state of copy b)")
     ap.add_argument("--calibrate-copy-gib", type=float, default=0.0,
                     help="after the timed steps, run three device copies of this many GiB "
                          "(reference kernel of known traffic for profiler byte counters)")
@@ -593,6 +686,8 @@ def main(argv=None):
     import torch
 
     torch.cuda.set_device(0)
+    if args.copies > 1:
+        return placement_study(args)
     wl = WORKLOADS[args.workload](args)
     torch.cuda.synchronize()
     print(f"[bench] warmup {args.warmup} steps", file=sys.stderr, flush=True)
