@@ -256,19 +256,19 @@ def cpu_baseline_kernel(kind, seconds_target=12.0, threads=None, n=1 << 22):
         def body():
             orc.sr_bf16(x, orc.random_bits((0, 1), n))
             return n
-    elif kind == "apply":
+    elif kind in ("apply", "apply_rne"):
         p = orc.f32_to_bf16_bits(x * np.float32(1e-3))
         u = (x * np.float32(1e-6)).astype(np.float32)
 
         def body():
-            orc.apply_updates(p, orc.BF16, u, bits=orc.random_bits((0, 1), n))
+            orc.apply_updates(p, orc.BF16, u, bits=orc.random_bits((0, 1), n) if kind == "apply" else None)
             return n
     else:
         raise ValueError(kind)
     done, reps, el = _timed_loop(body, seconds_target)
     return {
         "value": done / el,
-        "unit": "params/s" if kind == "apply" else "elements/s",
+        "unit": "params/s" if kind in ("apply", "apply_rne") else "elements/s",
         "cores": nthreads,
         "kind": "port",
         "sample": f"CPU oracle ({kind}, C, OpenMP, {nthreads} threads; Threefry bits generated on the CPU where "
@@ -472,10 +472,11 @@ def _kernel_workload(args, kind):
 
     L = _lib.lib()
     sp = _lib.stream_ptr
-    if kind == "apply":
+    if kind in ("apply", "apply_rne"):
+        sr = kind == "apply"
         shapes = llama7b_shapes()
         n = sum(_numel(s) for _, s in shapes)
-        print(f"[bench] llama7b_apply: {n} params; allocating", file=sys.stderr, flush=True)
+        print(f"[bench] llama7b_{kind}: {n} params; allocating", file=sys.stderr, flush=True)
         gen = torch.Generator(device="cuda")
         gen.manual_seed(0)
         params = [(torch.randn(s, generator=gen, device="cuda") * 0.02).to(torch.bfloat16) for _, s in shapes]
@@ -490,15 +491,17 @@ def _kernel_workload(args, kind):
             rows[i].param_index = i
 
         def step():
-            _lib.check(L.rf_apply_updates(rows, len(shapes), 1, 0, 42, sp()), "apply")
+            _lib.check(L.rf_apply_updates(rows, len(shapes), 1 if sr else 0, 0, 42, sp()), "apply")
 
-        name = "llama7b_bf16_apply_updates_sr"
+        name = "llama7b_bf16_apply_updates_" + ("sr" if sr else "rne")
         return Workload(name, n, "params/s", n * (2 + 4 + 2), step,
                         {"workload": name, "params": n, "leaves": len(shapes), "param_dtype": "bf16",
-                         "update_dtype": "f32", "rounding": "stochastic (in-kernel Threefry)",
+                         "update_dtype": "f32",
+                         "rounding": "stochastic (in-kernel Threefry)" if sr else "nearest-even",
                          "launches_per_step": 1},
-                        lambda: cpu_baseline_kernel("apply", args.cpu_seconds),
-                        "apply_updates params/sec + achieved HBM GB/s, 7B Llama pytree bf16 SR, 1 GPU")
+                        lambda: cpu_baseline_kernel(kind, args.cpu_seconds),
+                        "apply_updates params/sec + achieved HBM GB/s, 7B Llama pytree bf16 "
+                        + ("SR" if sr else "nearest-even") + ", 1 GPU")
     n = 1 << 30
     nb = n // BS
     print(f"[bench] {kind}: 2^30 elements; allocating", file=sys.stderr, flush=True)
@@ -565,6 +568,7 @@ WORKLOADS = {
     "llama7b_adamw_magma": lambda a: _tree_workload(a, llama7b_shapes, "llama7b_bf16_adamw_f32_moments_magma",
                                                     param_sr=False, adam_mu="f32", magma=True),
     "llama7b_apply": lambda a: _kernel_workload(a, "apply"),
+    "llama7b_apply_rne": lambda a: _kernel_workload(a, "apply_rne"),
     "quantize_2p30": lambda a: _kernel_workload(a, "quantize"),
     "dequantize_2p30": lambda a: _kernel_workload(a, "dequantize"),
     "sr_bf16_2p30": lambda a: _kernel_workload(a, "sr_bf16"),
