@@ -13,6 +13,9 @@ bits drawn with ``orc.random_bits(key, n, offset=block * 2048)`` from the
 leaf's keys (adam8.py:306 for the moment keys, utils.py:648-708 for the
 param key).  Bar: codes and scales bit-exact; params within one bf16 ulp
 (default hardware rcp/sqrt direction).
+
+The second test takes the standalone kernels (stochastic rounding to bf16,
+apply_updates, quantize and dequantize) past 2^32 elements the same way.
 """
 
 from __future__ import annotations
@@ -44,14 +47,20 @@ def _block(t, b, n):
 
 
 def _fill_normal(t, std, gen):
-    """t (flat bf16, device) <- N(0, std^2), 2^28 elements at a time."""
+    """t (flat bf16 or f32, device) <- N(0, std^2), 2^28 elements at a time."""
     import torch
 
     flat = t.reshape(-1)
     step = 1 << 28
     for lo in range(0, flat.numel(), step):
         hi = min(lo + step, flat.numel())
-        flat[lo:hi] = (torch.randn(hi - lo, generator=gen, device="cuda") * std).to(torch.bfloat16)
+        flat[lo:hi] = (torch.randn(hi - lo, generator=gen, device="cuda") * std).to(t.dtype)
+
+
+def _windows(n):
+    """2048-element windows on both sides of 2^31 and 2^32 elements and at
+    the end of an n-element array: (start, length)."""
+    return [(0, BS), ((1 << 31) - BS // 2, BS), ((1 << 32) - BS // 2, BS), (n - 1500, 1500)]
 
 
 def test_leaf_beyond_2p32_elements_sr_in_kernel_bits():
@@ -106,4 +115,72 @@ def test_leaf_beyond_2p32_elements_sr_in_kernel_bits():
             worst = max(worst, int(bf16_ulp_distance(_block(params["w"], b, N), p).max()))
         assert worst <= 1, f"step {step + 1}: params differ by {worst} bf16 ulp"
     del params, grads, state
+    torch.cuda.empty_cache()
+
+
+def test_standalone_kernels_beyond_2p32_elements():
+    """_stochastic_round_bf16 (utils.py:342-371) and apply_updates with
+    stochastic rounding (utils.py:648-708) of 2^32 + 777 elements with bits
+    drawn in the kernel, and quantize_blocks with stochastic rounding plus
+    dequantize_blocks (adam8.py:113-204) of the same count: windows across
+    2^31 and 2^32 elements and at the end against the oracle (bit-exact)."""
+    import torch
+
+    import rollfast_amd as rf
+    from rollfast_amd import prng
+    from rollfast_amd.utils import _stochastic_round_bf16
+
+    n = (1 << 32) + 777
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(33)
+    key = rf.prng.PRNGKey(9)
+    k = prng.as_key(key)
+
+    print(f"[bigleaf] sr_bf16 of {n} f32 elements", flush=True)
+    x = torch.empty(n, dtype=torch.float32, device="cuda")
+    _fill_normal(x, 1.0, gen)
+    out = _stochastic_round_bf16(x, key)
+    torch.cuda.synchronize()
+    for lo, ln in _windows(n):
+        want = orc.sr_bf16(x[lo:lo + ln].cpu().numpy(), orc.random_bits(k, ln, offset=lo))
+        got = out[lo:lo + ln].view(torch.int16).cpu().numpy().view(np.uint16)
+        np.testing.assert_array_equal(got, want, err_msg=f"sr_bf16 elements {lo}..{lo + ln}")
+    del out
+
+    print("[bigleaf] apply_updates with stochastic rounding", flush=True)
+    p = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    _fill_normal(p, 0.02, gen)
+    x.mul_(1e-4)  # the updates
+    before = {lo: p[lo:lo + ln].view(torch.int16).cpu().numpy().view(np.uint16).copy() for lo, ln in _windows(n)}
+    new = rf.apply_updates({"w": p}, {"w": x}, key=key, stochastic=True)
+    torch.cuda.synchronize()
+    kp = orc.split(k, 1)[0]  # the leaf's key: split(key, n_leaves)[leaf index]
+    for lo, ln in _windows(n):
+        want = before[lo].copy()
+        orc.apply_updates(want, orc.BF16, x[lo:lo + ln].cpu().numpy(), bits=orc.random_bits(kp, ln, offset=lo))
+        got = new["w"][lo:lo + ln].view(torch.int16).cpu().numpy().view(np.uint16)
+        np.testing.assert_array_equal(got, want, err_msg=f"apply_updates elements {lo}..{lo + ln}")
+    del p, new
+
+    print("[bigleaf] quantize_blocks (stochastic rounding) and dequantize_blocks", flush=True)
+    _fill_normal(x, 1.0, gen)
+    q = rf.quantize_blocks(x, stochastic_rounding=True, key=key)
+    nb = (n + BS - 1) // BS
+    assert tuple(q.values.shape) == (nb, BS)
+    blocks = sorted({0, (1 << 31) // BS - 1, (1 << 31) // BS, (1 << 32) // BS - 1, (1 << 32) // BS, nb - 1})
+    for b in blocks:
+        lo, hi = b * BS, min((b + 1) * BS, n)
+        codes, scales = orc.quantize(x[lo:hi].cpu().numpy(), BS, orc.Q_SIGNED,
+                                     bits=orc.random_bits(k, BS, offset=lo))
+        np.testing.assert_array_equal(q.values[b].cpu().numpy(), codes[0], err_msg=f"quantize block {b}")
+        assert q.scales[b:b + 1].cpu().numpy().view(np.uint32)[0] == scales.view(np.uint32)[0], f"scale {b}"
+    del x
+    y = rf.dequantize_blocks(q)
+    torch.cuda.synchronize()
+    for b in blocks:
+        lo, hi = b * BS, min((b + 1) * BS, n)
+        want = orc.dequantize(q.values[b].cpu().numpy(), q.scales[b:b + 1].cpu().numpy(), hi - lo, BS)
+        np.testing.assert_array_equal(y[lo:hi].cpu().numpy().view(np.uint32), want.view(np.uint32),
+                                      err_msg=f"dequantize block {b}")
+    del q, y
     torch.cuda.empty_cache()
