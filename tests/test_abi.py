@@ -62,6 +62,33 @@ def test_struct_sizes_match_header():
     assert ctypes.sizeof(_lib.MagmaLeaf) == 48
 
 
+def test_header_compiles_as_c_with_the_same_struct_sizes(tmp_path):
+    """A C host (cgo, JNI or N-API glue) includes the header as C99; the
+    struct sizes it sees are the ones the library and the binding use."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "h.c"
+    src.write_text(
+        '#include "rfadam8.h"\n'
+        "typedef char leaf_120[sizeof(rf_adam8_leaf) == 120 ? 1 : -1];\n"
+        "typedef char hparams_128[sizeof(rf_adam8_hparams) == 128 ? 1 : -1];\n"
+        "typedef char group_32[sizeof(rf_adam8_group) == 32 ? 1 : -1];\n"
+        "typedef char apply_40[sizeof(rf_apply_leaf) == 40 ? 1 : -1];\n"
+        "typedef char magma_48[sizeof(rf_magma_leaf) == 48 ? 1 : -1];\n"
+        "typedef char accum_32[sizeof(rf_accum_leaf) == 32 ? 1 : -1];\n"
+        "typedef char clip_%d[sizeof(rf_clip_leaf) == %d ? 1 : -1];\n"
+        % (ctypes.sizeof(_lib.ClipLeaf), ctypes.sizeof(_lib.ClipLeaf))
+        + "int main(void) { return 0; }\n"
+    )
+    r = subprocess.run([cc, "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", os.path.dirname(HEADER),
+                        "-fsyntax-only", str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
 def test_version_string():
     v = _lib.version()
     assert v.startswith("rfadam8 ")
