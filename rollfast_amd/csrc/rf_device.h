@@ -505,6 +505,34 @@ __device__ __forceinline__ bool cancels(float sum, float u)
     return fabsf(sum) * 4096.0f < fabsf(u);
 }
 
+// Exact-mode bf16 params from the hardware direction: true when s = p + upd
+// (upd = lr * (a + w), a the hardware rcp/sqrt direction, w the weight
+// decay term) rounds to the same bf16 (nearest even) as the IEEE
+// computation would.  The hardware direction (f32 k1, k2, er2, v + er2,
+// v_sqrt and v_rcp within 1 ulp, one FMA, one product) is within 4 * 2^-23
+// relative of the exact quotient, the IEEE sequence (m / bc1, v / bc2,
+// + eps_root, sqrt, + eps, the quotient) within 2.5 * 2^-23, so the two
+// directions differ by at most about 2^-20.3 |a| (no cancellation inside
+// the non-Nesterov direction; Nesterov's two-term numerator can cancel and
+// is not taken here).  With the roundings of a + w, of the lr product and of
+// both sums, and |lr a| <= |upd| (1 + 2^-22) + |lr w|, |w| <= |wd p| (1 +
+// 2^-8), the two sums differ by less than
+//   B = 2^-17 |upd| + c_w |p| + 2^-22 |s| + 2^-126,  c_w = 2^-17 |lr wd|
+// (each term with a margin of 2x or more).  The rounding is settled when s
+// is farther than B from the bf16 midpoint of its binade (s - mid is exact),
+// B is below |s| 2^-10 (below 0x4000 ulps of s: neither the midpoint of the
+// binade below nor a sign change is within reach) and |upd| < c_g = 2^100
+// |lr| (the direction far from f32 overflow, where one of the two could be
+// infinite; lr = 0 settles nothing).  NaN and Inf fail the tests.  Unsettled
+// lanes are recomputed with IEEE arithmetic.
+__device__ __forceinline__ bool rne_bf16_settled(float s, float upd, float p, float c_w, float c_g)
+{
+    const float b = __builtin_fmaf(0x1p-17f, fabsf(upd),
+                                   __builtin_fmaf(c_w, fabsf(p), __builtin_fmaf(0x1p-22f, fabsf(s), 0x1p-126f)));
+    const float mid = __uint_as_float((__float_as_uint(s) & 0xFFFF0000u) | 0x8000u);
+    return fabsf(s - mid) > b && b < fabsf(s) * 0x1p-10f && fabsf(upd) < c_g;
+}
+
 // Active lanes where any of 8 sums nearly cancels: each compare's lane mask
 // is OR-ed in scalar registers, with no per-lane flag materialised.
 __device__ __forceinline__ uint64_t cancel_lanes8(const float (&sum)[8], const float (&u)[8])
@@ -1109,6 +1137,11 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     constexpr int J = FAST_BS / 512;
     constexpr bool NEED_P = APPLY || WDM != WD_OFF;
     constexpr bool H16P = sizeof(PT) == 2;  // bf16 or f16 params
+    // Exact mode, fused, bf16 params rounded to nearest even, no Nesterov:
+    // the hardware direction, with the IEEE one only where it could change
+    // the rounded param (rne_bf16_settled).
+    constexpr bool SETTLE = EXACT && APPLY && IS_BF16<PT> && !PSR && !NEST;
+    constexpr bool IEEE_DIR = EXACT && !SETTLE;
     const int lane = threadIdx.x & (WAVE - 1);
     const int64_t base = blk * FAST_BS;
     const float sm_old = load_scale(L.mu_scales, L.flags, blk);
@@ -1169,13 +1202,31 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             v[j][t] = vv;
             amf = fmaxf(amf, fabsf(mm));
             av = max(av, __float_as_uint(vv));
-            u[t] = adam_direction<NEST, EXACT>(h, mm, vv, g[t]);
+            u[t] = adam_direction<NEST, IEEE_DIR>(h, mm, vv, g[t]);
         }
         decay_and_scale8<WDM>(h, u, p);
         if constexpr (APPLY) {
             float sum[8];
 #pragma unroll
             for (int t = 0; t < 8; ++t) sum[t] = p[t] + u[t];
+            if constexpr (SETTLE) {
+                const float wd_eff = WDM == WD_BF16 ? h.wd16 : (WDM == WD_F32 ? h.wd : (WDM == WD_F16 ? h.wdh : 0.0f));
+                const float c_w = fabsf(h.neg_lr * wd_eff) * 0x1p-17f;
+                const float c_g = fabsf(h.neg_lr) * 0x1p100f;
+                uint32_t open = 0;  // bit t: element t's rounding is not settled
+#pragma unroll
+                for (int t = 0; t < 8; ++t) open |= rne_bf16_settled(sum[t], u[t], p[t], c_w, c_g) ? 0u : 1u << t;
+                if (__builtin_amdgcn_ballot_w64(open != 0) != 0) {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        if (open & (1u << t)) {
+                            float ue = adam_direction<NEST, true>(h, m[j][t], v[j][t], g[t]);
+                            ue = decay_and_scale(h, ue, p[t], WDM);
+                            sum[t] = p[t] + ue;
+                        }
+                    }
+                }
+            }
             if constexpr (!EXACT) {
                 // Hardware rcp/sqrt leave u a few f32 ulps from the IEEE
                 // value; that moves the rounded param by more than one
