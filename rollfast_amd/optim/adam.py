@@ -55,6 +55,7 @@ from .adam8 import (
     _require_device_tensor,
     _torch,
     canonicalize_dtype,
+    decay_link_state,
 )
 
 
@@ -436,8 +437,6 @@ def adamw(
         return GradientTransformationExtraArgs(
             magma_init, _AdamwMagmaUpdate(inner.update.engine, learning_rate, weight_decay, weight_decay_mask,
                                           inner.update.magma))
-    if callable(weight_decay):
-        raise NotImplementedError("weight-decay schedules are not supported by adamw; pass a scalar")
     inner = scale_by_adam(b1=b1, b2=b2, eps=eps, eps_root=eps_root, mu_dtype=mu_dtype, nesterov=nesterov,
                           axis_name=axis_name, key=key, exact=exact, magma_p=magma_p, magma_tau=magma_tau)
     wd_nonzero = _has_nonzero_or_scheduled(weight_decay)
@@ -446,7 +445,7 @@ def adamw(
     def init_fn(params):
         states = [inner.init(params)]
         if wd_nonzero:
-            states.append(MaskedState(EmptyState()) if weight_decay_mask is not None else EmptyState())
+            states.append(decay_link_state(weight_decay, weight_decay_mask))
         if callable(learning_rate):
             states.append(ScaleByScheduleState(count=np.zeros((), dtype=np.int32)))
         else:

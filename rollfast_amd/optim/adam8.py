@@ -987,6 +987,14 @@ def _decay_mask_leaves(mask, params, n_leaves: int) -> list:
     return out
 
 
+def decay_link_state(weight_decay, weight_decay_mask):
+    """Initial state of the chain's add_decayed_weights link: empty for a
+    scalar decay, the schedule's step count (0) for a schedule; wrapped by
+    optax.masked's state when a mask is given."""
+    inner = ScaleByScheduleState(count=np.zeros((), dtype=np.int32)) if callable(weight_decay) else EmptyState()
+    return MaskedState(inner) if weight_decay_mask is not None else inner
+
+
 class _Adamw8Update:
     """``adamw8(...).update``: the optax chain scale_by_adam8 ->
     add_decayed_weights -> scale_by_learning_rate in one launch."""
@@ -1008,11 +1016,42 @@ class _Adamw8Update:
                 count=np.asarray(safe_int32_increment(count), dtype=np.int32))
         return np.float32(-_as_f32(lr)) if not isinstance(lr, (int, float)) else np.float32(-lr), lr_state
 
+    def _wd(self, state):
+        """(decay for the launch, new add_decayed_weights state) of the
+        chain's decay link (adam8.py:433-443).  A Python scalar stays a
+        Python scalar: wd * p is then weak-typed (kept in the dtype of bf16
+        and f16 params).  A schedule (weight_decay is ScalarOrSchedule,
+        adam8.py:400) is evaluated at the link's own step count, which starts
+        at 0 and advances with a saturating increment, as optax's schedules
+        are (scale_by_learning_rate; the reference's own decay,
+        optim/adam.py:186, likewise reads the count before the step).  Its
+        value is an f32 array scalar, so wd * p is an f32 product for every
+        param dtype.  ``state``: the whole chain state."""
+        wd = self.weight_decay
+        if not self.wd_nonzero:
+            return None, None
+        link = state[1]
+        if not callable(wd):
+            return wd, link
+        inner = link.inner_state if isinstance(link, MaskedState) else link
+        count = int(np.asarray(inner.count))
+        value = np.float32(_as_f32(wd(np.asarray(count, dtype=np.int32))))
+        new_inner = ScaleByScheduleState(count=np.asarray(safe_int32_increment(count), dtype=np.int32))
+        return value, (MaskedState(new_inner) if isinstance(link, MaskedState) else new_inner)
+
+    def new_chain_state(self, state, new_adam, new_decay, new_lr_state):
+        """The chain's state tuple after a step."""
+        mid = tuple(state[1:-1])
+        if self.wd_nonzero:
+            mid = (new_decay,) + mid[1:]
+        return (new_adam,) + mid + (new_lr_state,)
+
     def _step(self, updates, state, params, *, apply: bool, param_key=None, param_sr=False, random_bits=None,
               clip_global_norm=None, clip_stats=None, skip_nonfinite=False, finite_out=None, finite_host=None):
         adam_state = state[0]
         lr_state = state[-1]
         neg_lr, new_lr_state = self._lr(lr_state)
+        wd, new_decay = self._wd(state)
         decay_mask = None
         if self.wd_nonzero:
             if params is None:
@@ -1023,15 +1062,13 @@ class _Adamw8Update:
                 n = len(_tree.leaves(updates, is_leaf=_is_passthrough_leaf))
                 decay_mask = _decay_mask_leaves(self.weight_decay_mask, params, n)
         out, new_adam = self.engine.run(
-            updates, adam_state, params, apply=apply, decay_mask=decay_mask,
-            weight_decay=self.weight_decay if self.wd_nonzero else None, neg_lr=neg_lr,
+            updates, adam_state, params, apply=apply, decay_mask=decay_mask, weight_decay=wd, neg_lr=neg_lr,
             param_key=param_key, param_sr=param_sr, random_bits=random_bits,
             clip_global_norm=clip_global_norm, clip_stats=clip_stats, skip_nonfinite=skip_nonfinite,
             finite_out=finite_out, finite_host=finite_host,
             zero_decay=self.engine.own_zero_decay and params is not None,
         )
-        new_state = (new_adam,) + tuple(state[1:-1]) + (new_lr_state,)
-        return out, new_state
+        return out, self.new_chain_state(state, new_adam, new_decay, new_lr_state)
 
     def __call__(self, updates, state, params=None, **extra_args):
         del extra_args
@@ -1064,8 +1101,6 @@ def adamw8(
     ``(ScaleByAdam8State, add_decayed_weights state?, lr state)``."""
     if use_magma:
         raise NotImplementedError("Magma is not supported by adamw8 yet.")
-    if callable(weight_decay):
-        raise NotImplementedError("weight-decay schedules are not supported; pass a scalar")
     inner = scale_by_adam8(
         b1=b1, b2=b2, eps=eps, eps_root=eps_root, block_size=block_size, min_size=min_size,
         scale_dtype=scale_dtype, fallback_dtype=fallback_dtype, stochastic_rounding=stochastic_rounding,
@@ -1077,7 +1112,7 @@ def adamw8(
     def init_fn(params):
         states = [inner.init(params)]
         if weight_decay_is_nonzero:
-            states.append(MaskedState(EmptyState()) if weight_decay_mask is not None else EmptyState())
+            states.append(decay_link_state(weight_decay, weight_decay_mask))
         if callable(learning_rate):
             states.append(ScaleByScheduleState(count=np.zeros((), dtype=np.int32)))
         else:
@@ -1196,17 +1231,18 @@ class _GroupedRunner:
             eng = upd.engine
             adam_state, lr_state = state[0], state[-1]
             neg_lr, new_lr_state = upd._lr(lr_state)
+            wd, new_decay = upd._wd(state)
             key_mu, key_nu, next_key = eng.split_keys(adam_state.key)
             grp = _lib.Adam8Group()
             grp.neg_lr = neg_lr
-            grp.weight_decay = _as_f32(upd.weight_decay) if upd.wd_nonzero else np.float32(0.0)
+            grp.weight_decay = _as_f32(wd) if upd.wd_nonzero else np.float32(0.0)
             grp.one_minus_b1 = eng.ema_weight(eng.cfg.b1)
             grp.key_mu[0], grp.key_mu[1] = int(key_mu[0]), int(key_mu[1])
             grp.key_nu[0], grp.key_nu[1] = int(key_nu[0]), int(key_nu[1])
             records.append(grp)
             count_inc = safe_int32_increment(int(np.asarray(adam_state.count)))
-            new_states.append((eng.new_state(adam_state, count_inc, next_key),) + tuple(state[1:-1])
-                              + (new_lr_state,))
+            new_states.append(upd.new_chain_state(state, eng.new_state(adam_state, count_inc, next_key), new_decay,
+                                                  new_lr_state))
         return records, new_states
 
     @staticmethod

@@ -72,6 +72,25 @@ def split(key, num: int = 2) -> np.ndarray:
     return np.stack([y0, y1], axis=1).astype(np.uint32)
 
 
+def fold_in(key, data: int) -> np.ndarray:
+    """``jax.random.fold_in(key, data)`` -> ``uint32[2]``.
+
+    JAX converts ``data`` to uint32 (out-of-range Python ints raise
+    OverflowError), makes it a seed pair ``[data >> 32, data & 0xFFFFFFFF]``
+    = ``[0, data]`` and hashes that pair as one Threefry counter:
+    ``threefry2x32(key, (0, data))``.  The fine-tune builders key each
+    adamw8 group with ``fold_in(root_key, group_index)``
+    (``src/rollfast/finetune/builders.py:1582``, ``:1123``, ``:1280``).  In
+    the partitionable layout this is row ``data`` of ``split(key, n)`` for
+    any ``n > data``."""
+    k = as_key(key)
+    d = int(data)
+    if not 0 <= d < (1 << 32):
+        raise OverflowError(f"Python int {d} too large to convert to uint32")
+    y0, y1 = threefry2x32(k, np.zeros(1, np.uint32), np.array([d], np.uint32))
+    return np.array([y0[0], y1[0]], dtype=np.uint32)
+
+
 def bits(key, n: int, offset: int = 0) -> np.ndarray:
     """``jax.random.bits(key, (n,), uint32)`` over flat indices
     ``offset .. offset+n-1``."""

@@ -163,8 +163,12 @@ def _run(spec, *, steps=3, exact=False, block_size=2048, min_size=4096, wd=0.01,
         if psr:
             kp = orc.split(pkey, n)
             p_bits = [orc.random_bits(kp[i], L["size"]) for i, L in enumerate(tree.leaves)]
-        tree.step(ghost, weight_decay=wd, lr=lr, count=count_inc, nesterov=nesterov, moment_sr=msr,
-                  param_sr=psr, mu_bits=mu_bits, nu_bits=nu_bits, p_bits=p_bits, eps_root=eps_root)
+        # a decay schedule is read at the link's count (0, 1, ...) and is an
+        # f32 array scalar: the f32 product, not the weak-typed one
+        wd_step = float(np.float32(wd(np.int32(step)))) if callable(wd) else wd
+        tree.step(ghost, weight_decay=wd_step, lr=lr, count=count_inc, nesterov=nesterov, moment_sr=msr,
+                  param_sr=psr, mu_bits=mu_bits, nu_bits=nu_bits, p_bits=p_bits, eps_root=eps_root,
+                  decay_weak=not callable(wd))
         params, state = rf.adamw8_step(tx, params, gdev, state, key=pkey if psr else None, stochastic=psr)
         torch.cuda.synchronize()
         _compare_state(spec, tree, state[0], f"step {step + 1}")
@@ -231,6 +235,14 @@ def test_moment_stochastic_rounding_matches_threefry_bits():
 def test_param_stochastic_rounding_matches_threefry_bits():
     spec = [((64, 2048), "bf16", "bf16"), ((3, 3000), "bf16", "f32"), ((768,), "bf16", "bf16")]
     _run(spec, steps=2, psr=True, exact=True)
+
+
+def test_weight_decay_schedule():
+    """adamw8(weight_decay=schedule) (adam8.py:400, :435-440): the decay link
+    evaluates the schedule at its own count, 0 on the first step, and the f32
+    value multiplies the params in f32 (bf16 params included)."""
+    sched = lambda c: 0.05 / (1.0 + np.float32(c))  # noqa: E731
+    _run(MIXED, steps=3, wd=sched, exact=True)
 
 
 def test_fast_direction_over_twenty_steps():

@@ -63,6 +63,31 @@ def test_prng_key_and_streams_match_oracle():
     y = prng.threefry2x32(np.array([0, 0], np.uint32), np.uint32(0), np.uint32(0))
     assert (int(y[0]), int(y[1])) == (0x6B200159, 0x99BA4EFE)
     assert prng.fresh_key(None).tolist() == [0, 42]
+    # JAX's printed split(PRNGKey(0)) in the partitionable layout
+    assert prng.split(prng.PRNGKey(0), 2).tolist() == [[1797259609, 2579123966], [928981903, 3453687069]]
+
+
+def test_fold_in_group_keys():
+    """jax.random.fold_in (the fine-tune builders' per-group adamw8 keys,
+    finetune/builders.py:1582): the seed pair [0, data] hashed as one
+    Threefry counter.  fold_in(PRNGKey(0), 0) is therefore the Random123 zero
+    vector, and fold_in(k, i) is row i of the partitionable split(k, n) (the
+    published split(PRNGKey(0)) rows for i = 0, 1).  A seed pair in the other
+    order ([data, 0]) or the legacy split layout fails these."""
+    assert prng.fold_in(prng.PRNGKey(0), 0).tolist() == [0x6B200159, 0x99BA4EFE]
+    assert prng.fold_in(prng.PRNGKey(0), 1).tolist() == [928981903, 3453687069]
+    key = np.array([0x13198A2E, 0x03707344], np.uint32)
+    rows = orc.split(tuple(key), 40)
+    for i in (0, 1, 7, 39):
+        assert prng.fold_in(key, i).tolist() == rows[i].tolist()
+    big = (1 << 32) - 1
+    assert prng.fold_in(key, big).tolist() == list(orc.threefry2x32(tuple(int(k) for k in key), (0, big)))
+    for bad in (-1, 1 << 32):
+        with pytest.raises(OverflowError):
+            prng.fold_in(key, bad)
+    # a group key feeds adamw8(key=...) like any other key
+    tx = rf.adamw8(learning_rate=1e-3, key=prng.fold_in(prng.PRNGKey(7), 2))
+    assert tx is not None
 
 
 # ------------------------------------------------------- state / metadata --
@@ -110,6 +135,21 @@ def test_min_size_and_fallback_dtype():
     assert isinstance(st.mu["big"], rf.QuantizedBlocks)
     st = rf.scale_by_adam8(quantize=False).init({"big": torch.zeros(8192)})
     assert st.mu["big"].dtype == torch.float32
+
+
+def test_weight_decay_schedule_state():
+    """A weight-decay schedule gives the chain's decay link a step count
+    (0 at init, masked when a mask is given); a scalar keeps it empty."""
+    sched = lambda c: 0.01 * (c + 1)  # noqa: E731
+    p = _cpu_params()
+    st = rf.adamw8(learning_rate=1e-3, weight_decay=sched).init(p)
+    assert len(st) == 3 and int(st[1].count) == 0 and type(st[1]).__name__ == "ScaleByScheduleState"
+    st = rf.adamw8(learning_rate=1e-3, weight_decay=sched, weight_decay_mask={k: True for k in p}).init(p)
+    assert type(st[1]).__name__ == "MaskedState" and int(st[1].inner_state.count) == 0
+    st = rf.adamw(learning_rate=1e-3, weight_decay=sched).init({"w": torch.zeros(8, 8)})
+    assert int(st[1].count) == 0
+    st = rf.adamw8(learning_rate=1e-3, weight_decay=0.01).init(p)
+    assert type(st[1]).__name__ == "EmptyState"
 
 
 def test_adamw8_state_tuple_layout():

@@ -50,6 +50,48 @@ def test_random_bits_and_split_layout():
         assert tuple(int(v) for v in sub[i]) == orc.threefry2x32(key, (0, i))
 
 
+# jax.random.split(jax.random.PRNGKey(0)) as JAX prints it (uint32[2, 2]):
+# under the default jax_threefry_partitionable layout (JAX >= 0.5, the
+# reference's jax>=0.6.2), and under the legacy layout JAX used before.
+SPLIT_KEY0_PARTITIONABLE = [[1797259609, 2579123966], [928981903, 3453687069]]
+SPLIT_KEY0_LEGACY = [[4146024105, 967050713], [2718843009, 1272950319]]
+
+
+def test_split_of_prngkey0_is_jax_partitionable_value():
+    """The oracle's split (adam8.py:274, :306, :645; utils.py:682) gives JAX's
+    published split(PRNGKey(0)).  Counters (i, 0) instead of (0, i), or the
+    legacy iota layout, give other words and fail here."""
+    assert orc.split((0, 0), 2).tolist() == SPLIT_KEY0_PARTITIONABLE
+    swapped = [list(orc.threefry2x32((0, 0), (i, 0))) for i in range(2)]
+    assert swapped != SPLIT_KEY0_PARTITIONABLE
+    assert SPLIT_KEY0_LEGACY != SPLIT_KEY0_PARTITIONABLE
+
+
+def test_legacy_split_layout_cross_checks_the_block_function():
+    """The legacy layout of split(key, n): counters iota(2n) cut in halves
+    (x0 = 0..n-1, x1 = n..2n-1), the cipher's y0 words then its y1 words,
+    reshaped to [n, 2].  Built from the oracle's block function it gives
+    JAX's published legacy split(PRNGKey(0)): a second published vector
+    through the same cipher, with other counters than the Random123 ones."""
+    n = 2
+    ys = [orc.threefry2x32((0, 0), (i, n + i)) for i in range(n)]
+    flat = [y[0] for y in ys] + [y[1] for y in ys]
+    assert [flat[0:2], flat[2:4]] == SPLIT_KEY0_LEGACY
+
+
+def test_uniform_of_prngkey0_legacy_value():
+    """jax.random.uniform(PRNGKey(0)) of the legacy layout is 0.41845703
+    (JAX's printed value): the scalar's bits are y0 of threefry(key, (0, 0)),
+    the Random123 zero vector's 0x6B200159, and uniform's mantissa fill
+    (bits >> 9 | 0x3F800000) - 1 (the Bernoulli draw of adam8.py:458, :564)
+    maps it to 3510272 / 2^23 exactly."""
+    y0, _ = orc.threefry2x32((0, 0), (0, 0))
+    assert y0 == 0x6B200159
+    u = orc.uniform01(np.array([y0], np.uint32))[0]
+    assert u == np.float32(3510272 / 2 ** 23)
+    assert abs(float(u) - 0.41845703) < 5e-9
+
+
 # ------------------------------------------------------------ codebooks ---
 def _exact_codebook(signed: bool) -> np.ndarray:
     """The dynamic codebook of rollfast optim/adam8.py:465-503 in exact
@@ -867,6 +909,70 @@ def test_f16_params_round_the_f32_step():
             wdp = (np.float16(0.01) * p16).astype(np.float32)          # f16 product, rounded once
             want = (p32 + np.float32(-1e-3) * (u + wdp)).astype(np.float16)
             np.testing.assert_array_equal(a16, want.view(np.uint16))
+
+
+def _rn_bf16(q: Fraction) -> Fraction:
+    """An exact rational rounded to the nearest bfloat16 (8 significant bits,
+    ties to even; subnormal spacing 2^-133), as an exact rational."""
+    if q == 0:
+        return Fraction(0)
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1                      # now 2^e <= a < 2^(e+1)
+    ulp = Fraction(2) ** max(e - 7, -133)
+    k, rem = divmod(a, ulp)
+    k = int(k)
+    if rem * 2 > ulp or (rem * 2 == ulp and k % 2 == 1):
+        k += 1
+    return sign * k * ulp
+
+
+def test_rn_bf16_helper_against_the_bit_rounding():
+    """The rational rounding above against the oracle's f32 -> bf16
+    (round-to-nearest-even on the bit pattern) for f32 inputs."""
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(5000) * np.exp(rng.uniform(-20, 20, 5000))).astype(np.float32)
+    got = np.array([float(_rn_bf16(Fraction(float(v)))) for v in x], np.float32)
+    np.testing.assert_array_equal(got, orc.bf16_bits_to_f32(orc.f32_to_bf16_bits(x)))
+
+
+def test_weak_typed_bf16_decay_term_closed_form():
+    """optax add_decayed_weights ``u + wd * p`` with a Python-scalar wd and
+    bf16 params (adam8.py:433-443; H5): JAX's weak typing keeps ``wd * p`` in
+    bf16, so the decay term is RN_bf16(RN_bf16(wd) * p), the exact product
+    rounded once, added to the f32 update in f32.  Computed here in exact
+    rationals and checked bit for bit against the oracle's update-only output
+    on inputs where the f32 product (a non-weak oracle) gives another sum for
+    most elements."""
+    rng = np.random.default_rng(17)
+    n = 4096
+    wd = 0.0123
+    p32 = (rng.standard_normal(n) * 0.7).astype(np.float32)
+    pbits = orc.f32_to_bf16_bits(p32)
+    p = orc.bf16_bits_to_f32(pbits)
+    g = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+
+    def update(**kw):
+        hp = orc.make_hparams(count=1, apply=False, **kw)
+        u = np.empty(n, np.float32)
+        orc.adam8_leaf(hp, pbits.copy(), orc.BF16, g.copy(), orc.F32, orc.MOM_F32, np.zeros(n, np.float32), None,
+                       np.zeros(n, np.float32), None, updates_out=u)
+        return u
+
+    u0 = update()                                                   # no decay link
+    u_weak = update(weight_decay=wd, decay=True, decay_weak=True)
+    u_strong = update(weight_decay=wd, decay=True, decay_weak=False)
+    wd16 = _rn_bf16(Fraction(float(np.float32(wd))))               # the Python float is first an f32 weak scalar
+    assert wd16 == _rn_bf16(Fraction(wd))                           # (the same bf16 either way for this wd)
+    term = np.array([float(_rn_bf16(wd16 * Fraction(float(v)))) for v in p], np.float32)
+    want = (u0 + term).astype(np.float32)
+    np.testing.assert_array_equal(u_weak.view(np.uint32), want.view(np.uint32))
+    f32_term = (np.float32(wd) * p).astype(np.float32)
+    want_strong = (u0 + f32_term).astype(np.float32)
+    np.testing.assert_array_equal(u_strong.view(np.uint32), want_strong.view(np.uint32))
+    assert np.count_nonzero(want != want_strong) > n // 2
 
 
 # ------------------------------------------------------ optax.MultiSteps --
