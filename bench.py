@@ -171,13 +171,13 @@ def _timed_loop(body, seconds_target):
 
 
 def cpu_baseline(seconds_target=12.0, threads=None, shapes=None, sample_name="the 9 leaves of one Llama-7B layer",
-                 param_sr=False, moment_sr=False, pdtype="bf16"):
+                 param_sr=False, moment_sr=False, pdtype="bf16", packed=False):
     """The CPU oracle (C, OpenMP over blocks) on a bounded sample of the same
     workload (default: the 9 leaves of one Llama layer), one step per leaf,
     repeated until about `seconds_target` seconds of CPU work have run.  With
     stochastic rounding each step also draws its Threefry bits on the CPU
-    (the kernel draws them in-kernel).  ``pdtype`` "f32": f32 params and
-    grads."""
+    (the kernel draws them in-kernel), from the packed stream with
+    ``packed``.  ``pdtype`` "f32": f32 params and grads."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -210,11 +210,16 @@ def cpu_baseline(seconds_target=12.0, threads=None, shapes=None, sample_name="th
                               param_sr=param_sr, moment_sr=moment_sr)
         done = 0
         for i, L in enumerate(leaves):
-            pb = orc.random_bits((t, i), L["n"]) if param_sr else None
+            pb = None
+            if param_sr:
+                pb = orc.packed_param_bits((t, i), L["n"]) if packed else orc.random_bits((t, i), L["n"])
             mb = vb = None
             if moment_sr and L["quant"]:
-                mb = orc.random_bits((t, 1000 + i), L["mc"].size)
-                vb = orc.random_bits((t, 2000 + i), L["vc"].size)
+                if packed:
+                    mb, vb = orc.packed_moment_bits((t, 1000 + i), L["mc"].size)
+                else:
+                    mb = orc.random_bits((t, 1000 + i), L["mc"].size)
+                    vb = orc.random_bits((t, 2000 + i), L["vc"].size)
             dt = orc.F32 if pdtype == "f32" else orc.BF16
             orc.adam8_leaf(hp, L["p"], dt, L["g"], dt, orc.MOM_QUANT if L["quant"] else orc.MOM_F32,
                            L["mc"], L["ms"], L["vc"], L["vs"], BS, mu_bits=mb, nu_bits=vb, p_bits=pb)
@@ -232,9 +237,10 @@ def cpu_baseline(seconds_target=12.0, threads=None, shapes=None, sample_name="th
     }
 
 
-def cpu_baseline_kernel(kind, seconds_target=12.0, threads=None, n=1 << 22):
+def cpu_baseline_kernel(kind, seconds_target=12.0, threads=None, n=1 << 22, packed=False):
     """The CPU oracle's standalone quantize / dequantize / SR / apply over a
-    2^22-element sample of the same input distribution."""
+    2^22-element sample of the same input distribution (SR bits from the
+    packed stream with ``packed``)."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -254,14 +260,17 @@ def cpu_baseline_kernel(kind, seconds_target=12.0, threads=None, n=1 << 22):
             return n
     elif kind == "sr_bf16":
         def body():
-            orc.sr_bf16(x, orc.random_bits((0, 1), n))
+            orc.sr_bf16(x, orc.packed_param_bits((0, 1), n) if packed else orc.random_bits((0, 1), n))
             return n
     elif kind in ("apply", "apply_rne"):
         p = orc.f32_to_bf16_bits(x * np.float32(1e-3))
         u = (x * np.float32(1e-6)).astype(np.float32)
 
         def body():
-            orc.apply_updates(p, orc.BF16, u, bits=orc.random_bits((0, 1), n) if kind == "apply" else None)
+            bits = None
+            if kind == "apply":
+                bits = orc.packed_param_bits((0, 1), n) if packed else orc.random_bits((0, 1), n)
+            orc.apply_updates(p, orc.BF16, u, bits=bits)
             return n
     else:
         raise ValueError(kind)
@@ -301,11 +310,14 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     tdt = torch.float32 if pdtype == "f32" else torch.bfloat16  # params and grads
     params = {name: (torch.randn(s, generator=gen, device="cuda", dtype=torch.float32) * 0.02).to(tdt)
               for name, s in shapes}
+    packed = args.sr_bits == "packed"
     if adam_mu is None:
-        tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=args.exact, stochastic_rounding=moment_sr)
+        tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, exact=args.exact, stochastic_rounding=moment_sr,
+                       sr_bits=args.sr_bits)
     else:
         tx = rf.adamw(learning_rate=1e-3, weight_decay=0.01, exact=args.exact,
-                      mu_dtype=torch.bfloat16 if adam_mu == "bf16" else None, use_magma=magma)
+                      mu_dtype=torch.bfloat16 if adam_mu == "bf16" else None, use_magma=magma,
+                      sr_bits="jax" if magma else args.sr_bits)
     chain_clip = None
     if groups:
         # the fine-tune builders' shape: groups with their own lr / decay / key
@@ -382,8 +394,10 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         "moments": ("uint8 codebook codes + f32 block scales (f32 fallback below 4096 elements)"
                     if adam_mu is None else f"{adam_mu} (full-precision AdamW"
                     + (", stochastically rounded storage)" if adam_mu == "bf16" else ")")),
-        "param_rounding": ("stochastic" if param_sr else "nearest-even") if pdtype == "bf16" else "f32 add",
-        "moment_rounding": "stochastic (in-kernel Threefry bits)" if moment_sr else "nearest",
+        "param_rounding": (("stochastic" + (" (packed bits: a Threefry block per 4 elements)" if packed else ""))
+                           if param_sr else "nearest-even") if pdtype == "bf16" else "f32 add",
+        "moment_rounding": (("stochastic (packed bits: a Threefry block per element for both moments)" if packed
+                             else "stochastic (in-kernel Threefry bits)") if moment_sr else "nearest"),
         "direction": "ieee" if args.exact else "hw rcp/sqrt",
         "mode": "optax update-only (f32 updates)" if optax else "fused step (params written)",
         "launches_per_step": 1 if clip is None else 4,
@@ -411,12 +425,13 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
     if shapes_fn is llama7b_shapes and pdtype == "f32":
         cpu = lambda: cpu_baseline(args.cpu_seconds, pdtype="f32")  # noqa: E731
     elif shapes_fn is llama7b_shapes:
-        cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr, moment_sr=moment_sr)  # noqa: E731
+        cpu = lambda: cpu_baseline(args.cpu_seconds, param_sr=param_sr, moment_sr=moment_sr,  # noqa: E731
+                                   packed=packed)
     else:
         sub = [s for _, s in shapes][:400]
         cpu = lambda: cpu_baseline(args.cpu_seconds, shapes=sub,  # noqa: E731
                                    sample_name=f"the first {len(sub)} leaves", param_sr=param_sr,
-                                   moment_sr=moment_sr)
+                                   moment_sr=moment_sr, packed=packed)
     if accum > 1:
         cpu = None  # the oracle baseline times the plain step, not a window
     metric = METRIC if workload == "llama7b_bf16_adamw8" else f"adam8 params/sec + achieved HBM GB/s, {workload}, 1 GPU"
@@ -472,6 +487,7 @@ def _kernel_workload(args, kind):
 
     L = _lib.lib()
     sp = _lib.stream_ptr
+    packed = args.sr_bits == "packed"
     if kind in ("apply", "apply_rne"):
         sr = kind == "apply"
         shapes = llama7b_shapes()
@@ -491,15 +507,19 @@ def _kernel_workload(args, kind):
             rows[i].param_index = i
 
         def step():
-            _lib.check(L.rf_apply_updates(rows, len(shapes), 1 if sr else 0, 0, 42, sp()), "apply")
+            if sr and packed:
+                _lib.check(L.rf_apply_updates_packed(rows, len(shapes), 0, 42, sp()), "apply")
+            else:
+                _lib.check(L.rf_apply_updates(rows, len(shapes), 1 if sr else 0, 0, 42, sp()), "apply")
 
-        name = "llama7b_bf16_apply_updates_" + ("sr" if sr else "rne")
+        name = "llama7b_bf16_apply_updates_" + ("sr" if sr else "rne") + ("_packed_bits" if sr and packed else "")
         return Workload(name, n, "params/s", n * (2 + 4 + 2), step,
                         {"workload": name, "params": n, "leaves": len(shapes), "param_dtype": "bf16",
                          "update_dtype": "f32",
-                         "rounding": "stochastic (in-kernel Threefry)" if sr else "nearest-even",
+                         "rounding": ("stochastic (packed bits: a Threefry block per 4 elements)" if packed
+                                      else "stochastic (in-kernel Threefry)") if sr else "nearest-even",
                          "launches_per_step": 1},
-                        lambda: cpu_baseline_kernel(kind, args.cpu_seconds),
+                        lambda: cpu_baseline_kernel(kind, args.cpu_seconds, packed=packed),
                         "apply_updates params/sec + achieved HBM GB/s, 7B Llama pytree bf16 "
                         + ("SR" if sr else "nearest-even") + ", 1 GPU")
     n = 1 << 30
@@ -528,16 +548,19 @@ def _kernel_workload(args, kind):
         out = torch.empty(n, dtype=torch.bfloat16, device="cuda")
 
         def step():
-            _lib.check(L.rf_sr_bf16(x.data_ptr(), n, 0, 42, None, out.data_ptr(), sp()), "sr_bf16")
+            if packed:
+                _lib.check(L.rf_sr_bf16_packed(x.data_ptr(), n, 0, 42, out.data_ptr(), sp()), "sr_bf16")
+            else:
+                _lib.check(L.rf_sr_bf16(x.data_ptr(), n, 0, 42, None, out.data_ptr(), sp()), "sr_bf16")
         nbytes = n * 4 + n * 2
     else:
         raise ValueError(kind)
-    name = f"{kind}_2p30_f32"
+    name = f"{kind}_2p30_f32" + ("_packed_bits" if kind == "sr_bf16" and packed else "")
     return Workload(name, n, "elements/s", nbytes, step,
                     {"workload": name, "elements": n, "block_size": BS, "quantizer": "dynamic_signed",
                      "input": "log-uniform |x| in [1e-8, 1e2], random sign, +-0 every 97th and denormals "
                               "every 89th element", "launches_per_step": 1},
-                    lambda: cpu_baseline_kernel(kind, args.cpu_seconds),
+                    lambda: cpu_baseline_kernel(kind, args.cpu_seconds, packed=packed),
                     f"{kind} elements/sec + achieved HBM GB/s, 2^30 f32, 1 GPU")
 
 
@@ -670,6 +693,10 @@ def main(argv=None):
     ap.add_argument("--grad-pool", type=int, default=2, help="distinct gradient buffers cycled by the steps")
     ap.add_argument("--exact", action="store_true", help="IEEE div/sqrt in the update direction")
     ap.add_argument("--param-sr", action="store_true", help="stochastic rounding of bf16 params")
+    ap.add_argument("--sr-bits", choices=("jax", "packed"), default="jax",
+                    help="bit source of the stochastic roundings: jax.random.bits' stream (one Threefry block per "
+                         "32-bit word) or the packed one (a block per four param roundings, or per element for "
+                         "both moments)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copies", type=int, default=1,

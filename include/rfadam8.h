@@ -64,6 +64,16 @@ typedef int32_t rf_status;
                             default uses hardware rcp/sqrt (params within 1 bf16 ulp) */
 #define RF_FED_BITS 256u /* SR consumes the leaves' *_bits arrays instead of in-kernel
                             Threefry-2x32 */
+#define RF_PACKED_BITS 1024u /* no reference counterpart (opt-in): in-kernel SR bits from the
+                            packed stream instead of jax.random.bits' one Threefry-2x32-20
+                            block per 32-bit word.  Param SR of element e takes the 16-bit
+                            half (e & 1) of word (e & 2 ? y1 : y0) of threefry(param key,
+                            (hi32(e >> 2), lo32(e >> 2))): a block per four elements.
+                            Moment SR (and RF_LEAF_STORE_SR) of element e takes y0 for the
+                            first moment and y1 for the second of threefry(first-moment
+                            key, (hi32(e), lo32(e))): a block per element for both.  Keys
+                            are the per-leaf keys of the default stream.  Exclusive with
+                            RF_FED_BITS */
 #define RF_SKIP_NONFINITE 512u /* optax.apply_if_finite reject branch (the wrapper of the
                             fine-tune chain, finetune/builders.py:1605-1609): when any
                             grad of the run is Inf or NaN, the launch leaves the moments
@@ -230,29 +240,34 @@ RF_API rf_status rf_adam8_step(const rf_adam8_leaf* leaves, int32_t n_leaves, in
 /*
  * rf_adam8_step without allocation.  No counterpart in the reference (whose
  * hot path is Python traced by jax.jit); it is for callers that cannot
- * allocate device memory inside a step: code under HIP graph capture, an
- * XLA FFI handler (which must not allocate behind XLA's allocator), tight
- * serving loops and harnesses that forbid hipMalloc.
+ * allocate device memory inside a step: an XLA FFI handler (which must not
+ * allocate behind XLA's allocator), tight serving loops and harnesses that
+ * forbid hipMalloc.  It cannot be captured into a HIP graph: on a capturing
+ * stream it returns RF_ERR_UNSUPPORTED and enqueues nothing.
  *
  * Same arguments and results as rf_adam8_step (fused or update-only, every
- * flag, clipping, the finite flag and groups), except: it does not wait for
- * the stream (the work is enqueued on it; a finite_host flag is there once
- * the stream has passed the pre-pass), and it refuses magma_sums
- * (RF_ERR_UNSUPPORTED).  Its leaf and group tables, work lists and norm sums
- * live in one device-scope array of RF_NOALLOC_SCRATCH_BYTES per GPU (held
- * until the process ends); a tree whose tables need more fails with
- * RF_ERR_INVALID before any work is enqueued.  The tables take about 184 B
- * per leaf; with clipping or the finite flag add 8 B per 16,384 elements
- * (Llama-7B: 54 KB, 3.35 MB with clipping).  The host copies the tables
- * with one stream-ordered hipMemcpyAsync from pageable memory, so `leaves`
- * may be reused when the call returns.
+ * flag, clipping, the finite flag and groups), except: it does not
+ * synchronise the stream at the end (the work is enqueued on it; a
+ * finite_host flag is there once the stream has passed the pre-pass), and
+ * it refuses magma_sums (RF_ERR_UNSUPPORTED).  Its leaf and group tables,
+ * work lists and norm sums live in one device-scope array of
+ * RF_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends); a tree
+ * whose tables need more fails with RF_ERR_INVALID before any work is
+ * enqueued.  The tables take about 184 B per leaf; with clipping or the
+ * finite flag add 8 B per 16,384 elements (Llama-7B: 54 KB, 3.35 MB with
+ * clipping).  The host copies the tables with one stream-ordered
+ * hipMemcpyAsync from pageable memory, so `leaves` may be reused when the
+ * call returns.  The call does not wait for work already on the stream:
+ * measured on MI355X (ROCm 7.2), it returned in 0.11 ms with 11.7 ms of
+ * work ahead of it on the stream (tests/test_zz_no_alloc.py prints the
+ * figure), so a host can enqueue steps ahead through it.
  *
- * Every call on one GPU uses that GPU's single array: calls that overlap on
- * one GPU (enqueued on different streams, or from threads that race) race
- * on it and give wrong results.  Calls on one stream are ordered.  The first
- * call of the library on a device uploads the lookup tables with a
- * synchronous copy; a caller that captures graphs makes one call on the
- * device before capturing.
+ * Every call on one GPU uses that GPU's single array.  Calls are ordered
+ * per GPU: each call's stream first waits for the previous call's launches
+ * (an event the library records after them, whatever stream they were on),
+ * and concurrent calls from several threads enqueue one after another.  The
+ * first call of the library on a device uploads the lookup tables with a
+ * synchronous copy.
  */
 #define RF_NOALLOC_SCRATCH_BYTES (8u << 20)
 RF_API rf_status rf_adam8_step_noalloc(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_t apply,
@@ -285,6 +300,12 @@ RF_API rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, 
 RF_API rf_status rf_sr_bf16(const float* x, int64_t size, uint32_t key0, uint32_t key1,
                      const uint32_t* bits, uint16_t* out, void* stream);
 
+/* rf_sr_bf16 with the packed bit source (no reference counterpart; see
+ * RF_PACKED_BITS): element e's noise is the 16-bit half (e & 1) of word
+ * (e & 2 ? y1 : y0) of threefry(key, (hi32(e >> 2), lo32(e >> 2))). */
+RF_API rf_status rf_sr_bf16_packed(const float* x, int64_t size, uint32_t key0, uint32_t key1, uint16_t* out,
+                                   void* stream);
+
 /* One leaf of rollfast.apply_updates (utils.py:648-708). */
 typedef struct rf_apply_leaf {
     void* param;             /* [size] param_dtype, updated in place */
@@ -300,6 +321,13 @@ typedef struct rf_apply_leaf {
  * rounded to nearest even; f32 params take p + u. */
 RF_API rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic,
                            uint32_t key0, uint32_t key1, void* stream);
+
+/* rf_apply_updates with stochastic rounding from the packed bit source (no
+ * reference counterpart; see RF_PACKED_BITS): leaf i's key is
+ * split(key)[param_index] as in rf_apply_updates; every leaf's bits must be
+ * NULL. */
+RF_API rf_status rf_apply_updates_packed(const rf_apply_leaf* leaves, int32_t n_leaves, uint32_t key0,
+                                         uint32_t key1, void* stream);
 
 /* One leaf of rf_clip_by_global_norm. */
 typedef struct rf_clip_leaf {
@@ -406,6 +434,15 @@ RF_API rf_status rf_host_sr_records(int32_t quantizer, float* out1024);
 
 /* Library version string. */
 RF_API const char* rf_version(void);
+
+/* ABI revision of this header: 2 since rf_blockwise_quantize and
+ * rf_blockwise_dequantize take x_dtype / scale_dtype (revision 1 had no
+ * dtype arguments).  The shared object's soname carries it
+ * (librfadam8.so.2), so a program linked against another revision does not
+ * load this library; a dlopen/ctypes binding compares rf_abi_version() with
+ * the RF_ABI_VERSION it was written for. */
+#define RF_ABI_VERSION 2
+RF_API int32_t rf_abi_version(void);
 
 /* Thread-local message of the last failed call ("" if none). */
 RF_API const char* rf_last_error(void);

@@ -135,6 +135,19 @@ ORC_API void orc_random_bits(uint32_t k0, uint32_t k1, uint64_t offset, int64_t 
     }
 }
 
+/* Both words of threefry2x32(key, (hi32(c), lo32(c))) for the counters
+ * c = offset .. offset+n-1.  The block stream of the library's packed bit
+ * source (its opt-in RF_PACKED_BITS, which has no reference counterpart):
+ * the Python wrapper picks the words and halves each element takes. */
+ORC_API void orc_threefry_blocks(uint32_t k0, uint32_t k1, uint64_t offset, int64_t n, uint32_t* y0, uint32_t* y1)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        uint64_t c = offset + (uint64_t)i;
+        orc_threefry2x32(k0, k1, (uint32_t)(c >> 32), (uint32_t)c, &y0[i], &y1[i]);
+    }
+}
+
 /* jax.random.split(key, num) under jax_threefry_partitionable: subkey i is
  * threefry2x32(key, (0, i)) as the pair (y0, y1). */
 ORC_API void orc_split(uint32_t k0, uint32_t k1, int32_t num, uint32_t* out /* [num][2] */)

@@ -71,6 +71,7 @@ def lib() -> ctypes.CDLL:
         _lib.orc_threefry2x32.argtypes = [u32, u32, u32, u32, ctypes.POINTER(u32), ctypes.POINTER(u32)]
         _lib.orc_random_bits.argtypes = [u32, u32, ctypes.c_uint64, i64, p]
         _lib.orc_split.argtypes = [u32, u32, ctypes.c_int32, p]
+        _lib.orc_threefry_blocks.argtypes = [u32, u32, ctypes.c_uint64, i64, p, p]
         _lib.orc_codebook.argtypes = [ctypes.c_int, p]
         _lib.orc_quantize.argtypes = [ctypes.c_int, p, i64, i64, ctypes.c_int, p, p, p, ctypes.c_int]
         _lib.orc_dequantize.argtypes = [ctypes.c_int, p, p, i64, i64, p]
@@ -163,6 +164,38 @@ def random_bits(key, n: int, offset: int = 0) -> np.ndarray:
     out = np.empty(int(n), dtype=np.uint32)
     lib().orc_random_bits(int(key[0]), int(key[1]), int(offset), int(n), _ptr(out))
     return out
+
+
+def threefry_blocks(key, n: int, offset: int = 0):
+    """(y0, y1) of threefry2x32(key, (hi32(c), lo32(c))) for c = offset ..
+    offset + n - 1."""
+    y0 = np.empty(int(n), dtype=np.uint32)
+    y1 = np.empty(int(n), dtype=np.uint32)
+    lib().orc_threefry_blocks(int(key[0]), int(key[1]), int(offset), int(n), _ptr(y0), _ptr(y1))
+    return y0, y1
+
+
+def packed_param_bits(key, n: int, offset: int = 0) -> np.ndarray:
+    """The packed source's param-rounding bits of elements offset .. offset
+    + n - 1 (no reference counterpart): element e takes the 16-bit half
+    (e & 1) of word (e & 2 ? y1 : y0) of the block at counter e >> 2, in the
+    low 16 bits of the returned word (the part sr_bf16 adds)."""
+    n = int(n)
+    if n == 0:
+        return np.empty(0, np.uint32)
+    e = np.arange(int(offset), int(offset) + n, dtype=np.uint64)
+    q0 = int(offset) >> 2
+    y0, y1 = threefry_blocks(key, ((int(offset) + n - 1) >> 2) - q0 + 1, q0)
+    q = (e >> np.uint64(2)).astype(np.int64) - q0
+    w = np.where((e & np.uint64(2)) != 0, y1[q], y0[q])
+    return np.where((e & np.uint64(1)) != 0, w >> np.uint32(16), w & np.uint32(0xFFFF)).astype(np.uint32)
+
+
+def packed_moment_bits(key, n: int, offset: int = 0):
+    """The packed source's moment draws of elements offset .. offset + n - 1
+    (no reference counterpart): (first-moment words, second-moment words) =
+    (y0, y1) of the block at counter e under the first-moment key."""
+    return threefry_blocks(key, n, offset)
 
 
 def split(key, num: int) -> np.ndarray:

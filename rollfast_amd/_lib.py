@@ -27,6 +27,8 @@ RF_PARAM_SR = 32
 RF_EXACT = 128
 RF_FED_BITS = 256
 RF_SKIP_NONFINITE = 512
+RF_PACKED_BITS = 1024
+RF_ABI_VERSION = 2
 RF_LEAF_DECAY = 1
 RF_LEAF_STORE_SR = 2
 RF_LEAF_ZERO_DECAY = 4
@@ -166,7 +168,9 @@ EXPORTS = (
     "rf_blockwise_quantize",
     "rf_blockwise_dequantize",
     "rf_sr_bf16",
+    "rf_sr_bf16_packed",
     "rf_apply_updates",
+    "rf_apply_updates_packed",
     "rf_clip_by_global_norm",
     "rf_magma_reduce",
     "rf_magma_scale",
@@ -177,6 +181,7 @@ EXPORTS = (
     "rf_host_search_index",
     "rf_host_sr_records",
     "rf_version",
+    "rf_abi_version",
     "rf_last_error",
 )
 
@@ -212,6 +217,8 @@ def lib() -> ctypes.CDLL:
     L.rf_blockwise_dequantize.argtypes = [i32, _p, _p, i32, i64, i32, i32, _p, _p]
     L.rf_sr_bf16.argtypes = [_p, i64, u32, u32, _p, _p, _p]
     L.rf_apply_updates.argtypes = [ctypes.POINTER(ApplyLeaf), i32, i32, u32, u32, _p]
+    L.rf_sr_bf16_packed.argtypes = [_p, i64, u32, u32, _p, _p]
+    L.rf_apply_updates_packed.argtypes = [ctypes.POINTER(ApplyLeaf), i32, u32, u32, _p]
     f32 = ctypes.c_float
     L.rf_magma_reduce.argtypes = [ctypes.POINTER(MagmaLeaf), i32, f32, f32, _p, _p]
     L.rf_magma_scale.argtypes = [ctypes.POINTER(MagmaLeaf), i32, _p, _p, f32, f32, u32, u32, i32, f32, _p, _p]
@@ -224,6 +231,9 @@ def lib() -> ctypes.CDLL:
     for name in EXPORTS:
         if name not in ("rf_version", "rf_last_error"):
             getattr(L, name).restype = i32
+    if L.rf_abi_version() != RF_ABI_VERSION:
+        raise LibraryMissing(f"{LIB_PATH} has ABI revision {L.rf_abi_version()}, this binding is written for "
+                             f"{RF_ABI_VERSION}; rebuild with `python -m rollfast_amd.build`")
     _lib = L
     return L
 

@@ -18,6 +18,10 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_lib")
 LIB_NAME = "librfadam8.so"
 LIB_PATH = os.path.join(OUT_DIR, LIB_NAME)
+# The soname carries the ABI revision of include/rfadam8.h (RF_ABI_VERSION):
+# a program linked against another revision does not load this library.
+ABI_VERSION = 2
+SONAME = f"{LIB_NAME}.{ABI_VERSION}"
 OBJ_DIR = os.path.join(HERE, "_lib", "obj")
 HOST_SRC = os.path.join(CSRC, "rf_host.hip")
 # The native host fast path of the fused step: a CPython module built against
@@ -130,7 +134,7 @@ def build(verbose: bool = False, jobs: int | None = None, incremental: bool = Fa
         os.replace(pyhost_path() + ".tmp", pyhost_path())
     tmp = LIB_PATH + ".tmp"
     objs = [obj for _, obj in _compile_jobs()]
-    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,-soname,{SONAME}", "-o", tmp, *objs]
     if verbose:
         print(" ".join(link), flush=True)
     proc = subprocess.run(link, capture_output=True, text=True)
@@ -138,6 +142,11 @@ def build(verbose: bool = False, jobs: int | None = None, incremental: bool = Fa
         sys.stderr.write(proc.stdout + proc.stderr)
         raise RuntimeError(f"link failed with exit code {proc.returncode}")
     os.replace(tmp, LIB_PATH)
+    # programs linked with -lrfadam8 ask the loader for the soname
+    link_name = os.path.join(OUT_DIR, SONAME)
+    if os.path.lexists(link_name):
+        os.remove(link_name)
+    os.symlink(LIB_NAME, link_name)
     return LIB_PATH
 
 

@@ -256,6 +256,35 @@ __device__ __forceinline__ void jax_split(uint32_t k0, uint32_t k1, uint32_t i, 
     threefry2x32(k0, k1, 0u, i, o0, o1);
 }
 
+// Packed bit source (RF_PACKED_BITS; no reference counterpart, opt-in): the
+// stochastic roundings draw from whole Threefry-2x32-20 blocks instead of
+// one block per 32-bit word.  Param rounding needs 16 bits per element, so
+// element e of a leaf takes the 16-bit half (e & 1) of word (e & 2 ? y1 :
+// y0) of the block at counter (hi32(e >> 2), lo32(e >> 2)) under the leaf's
+// param key: a block per four elements.  The moments' Bernoulli draws take
+// y0 (first moment) and y1 (second moment) of the block at counter
+// (hi32(e), lo32(e)) under the leaf's first-moment key: a block per element
+// for both.  The rounding reads the noise from the low 16 bits of the word.
+__device__ __forceinline__ void packed_param_bits4(uint32_t k0, uint32_t k1, uint64_t e0, uint32_t* rb)
+{
+    uint32_t y0, y1;
+    const uint64_t q = e0 >> 2;  // e0 is a multiple of 4
+    threefry2x32(k0, k1, (uint32_t)(q >> 32), (uint32_t)q, y0, y1);
+    rb[0] = y0;
+    rb[1] = y0 >> 16;
+    rb[2] = y1;
+    rb[3] = y1 >> 16;
+}
+
+__device__ __forceinline__ uint32_t packed_param_bits1(uint32_t k0, uint32_t k1, uint64_t e)
+{
+    uint32_t y0, y1;
+    const uint64_t q = e >> 2;
+    threefry2x32(k0, k1, (uint32_t)(q >> 32), (uint32_t)q, y0, y1);
+    const uint32_t w = (e & 2) ? y1 : y0;
+    return (e & 1) ? (w >> 16) : w;
+}
+
 // jax.random.uniform(float32) from raw bits: mantissa fill of [1, 2) minus 1.
 __device__ __forceinline__ float uniform_from_bits(uint32_t bits)
 {
@@ -716,6 +745,7 @@ struct UnitCtx {
     float* wtab;  // this wave's 512-float LDS region (dequant-and-decay tables)
     int32_t wd_mode;
     bool fed;
+    bool packed;      // RF_PACKED_BITS without fed bits
     bool zero;        // RF_LEAF_ZERO_DECAY of the current leaf (unquantized-moment units)
     bool clip;        // grads are scaled by the global-norm clipping factor
     float cs, cs16, csh;  // that factor as f32, rounded to bf16 and rounded to f16
@@ -801,6 +831,67 @@ __device__ __forceinline__ void clip_context(UnitCtx& c, const KHp& h)
     }
 }
 
+// Random bits of the stochastic roundings, from the launch's source: fed
+// arrays, the packed stream, or jax.random.bits of the leaf keys.
+__device__ __forceinline__ uint32_t param_bits1(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e)
+{
+    if (c.fed) return gld<uint32_t>(L.param_bits, e);
+    if (c.packed) return packed_param_bits1(c.kp0, c.kp1, (uint64_t)e);
+    return jax_bits(c.kp0, c.kp1, (uint64_t)e);
+}
+
+// Eight consecutive param elements from e0, a multiple of 4.
+__device__ __forceinline__ void param_bits8(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e0, uint32_t (&rb)[8])
+{
+    if (c.fed) {
+        load8_u32(L.param_bits, e0, rb);
+    } else if (c.packed) {
+        packed_param_bits4(c.kp0, c.kp1, (uint64_t)e0, rb);
+        packed_param_bits4(c.kp0, c.kp1, (uint64_t)e0 + 4, rb + 4);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) rb[t] = jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
+    }
+}
+
+// Both moments' bits of element e (quantized: of the padded code arrays).
+__device__ __forceinline__ void moment_bits1(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e, uint32_t& bm,
+                                             uint32_t& bv)
+{
+    if (c.fed) {
+        bm = gld<uint32_t>(L.mu_bits, e);
+        bv = gld<uint32_t>(L.nu_bits, e);
+    } else if (c.packed) {
+        threefry2x32(c.kmu0, c.kmu1, (uint32_t)((uint64_t)e >> 32), (uint32_t)e, bm, bv);
+    } else {
+        bm = jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
+        bv = jax_bits(c.knu0, c.knu1, (uint64_t)e);
+    }
+}
+
+// One moment's bits of element e (the literal paths code the moments apart).
+__device__ __forceinline__ uint32_t mu_bits1(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e)
+{
+    if (c.fed) return gld<uint32_t>(L.mu_bits, e);
+    if (c.packed) {
+        uint32_t y0, y1;
+        threefry2x32(c.kmu0, c.kmu1, (uint32_t)((uint64_t)e >> 32), (uint32_t)e, y0, y1);
+        return y0;
+    }
+    return jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
+}
+
+__device__ __forceinline__ uint32_t nu_bits1(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e)
+{
+    if (c.fed) return gld<uint32_t>(L.nu_bits, e);
+    if (c.packed) {
+        uint32_t y0, y1;
+        threefry2x32(c.kmu0, c.kmu1, (uint32_t)((uint64_t)e >> 32), (uint32_t)e, y0, y1);
+        return y1;
+    }
+    return jax_bits(c.knu0, c.knu1, (uint64_t)e);
+}
+
 // The param after the update (fused) for one element.
 template <bool PSR, typename PT>
 __device__ __forceinline__ uint32_t new_param_bits(float p, float u, uint32_t rbits)
@@ -835,7 +926,7 @@ __device__ __forceinline__ void update_one(const UnitCtx& c, const rf_adam8_leaf
     if constexpr (APPLY) {
         if (L.param_dtype == RF_BF16) {
             uint32_t rb = 0;
-            if constexpr (PSR) rb = c.fed ? gld<uint32_t>(L.param_bits, e) : jax_bits(c.kp0, c.kp1, (uint64_t)e);
+            if constexpr (PSR) rb = param_bits1(c, L, e);
             gst<uint16_t>(L.param, e, (uint16_t)new_param_bits<PSR, uint16_t>(p, u, rb));
         } else if (L.param_dtype == RF_F16) {
             gst<uint16_t>(L.param, e, (uint16_t)f32_to_f16_rne(p + u));
@@ -922,14 +1013,14 @@ __device__ __forceinline__ void literal_code(const UnitCtx& c, const rf_adam8_le
                 cm = code_signed_fast(c.lds, mm, sm, rsm);
             } else {
                 uint32_t bits = 0;
-                if constexpr (MSR) bits = c.fed ? gld<uint32_t>(L.mu_bits, e) : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
+                if constexpr (MSR) bits = mu_bits1(c, L, e);
                 cm = code_literal(cbs, mm, sm, MSR, bits);
             }
             if (fast_v) {
                 cv = code_unsigned_fast(c.lds, vv, sv, rsv);
             } else {
                 uint32_t bits = 0;
-                if constexpr (MSR) bits = c.fed ? gld<uint32_t>(L.nu_bits, e) : jax_bits(c.knu0, c.knu1, (uint64_t)e);
+                if constexpr (MSR) bits = nu_bits1(c, L, e);
                 cv = code_literal(cbu, vv, sv, MSR, bits);
             }
             gst<uint8_t>(L.mu, e, (uint8_t)cm);
@@ -1000,14 +1091,14 @@ __device__ __forceinline__ void requant_literal(const UnitCtx& c, const rf_adam8
                 cm = code_signed_fast(c.lds, mm, sm, rsm);
             } else {
                 uint32_t bits = 0;
-                if constexpr (MSR) bits = c.fed ? gld<uint32_t>(L.mu_bits, e) : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
+                if constexpr (MSR) bits = mu_bits1(c, L, e);
                 cm = code_literal(cbs, mm, sm, MSR, bits);
             }
             if (fast_v) {
                 cv = code_unsigned_fast(c.lds, vv, sv, rsv);
             } else {
                 uint32_t bits = 0;
-                if constexpr (MSR) bits = c.fed ? gld<uint32_t>(L.nu_bits, e) : jax_bits(c.knu0, c.knu1, (uint64_t)e);
+                if constexpr (MSR) bits = nu_bits1(c, L, e);
                 cv = code_literal(cbu, vv, sv, MSR, bits);
             }
             gst<uint8_t>(L.mu, e, (uint8_t)cm);
@@ -1250,12 +1341,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                     // leaf's param key) drawn after the arithmetic: they are
                     // not live through it
                     uint32_t rb[8];
-                    if (c.fed) {
-                        load8_u32(L.param_bits, e0, rb);
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < 8; ++t) rb[t] = jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
-                    }
+                    param_bits8(c, L, e0, rb);
 #pragma unroll
                     for (int t = 0; t < 8; t += 2)
                         w[t / 2] = pack_hi16x2(sr_bf16_hi(sum[t], rb[t]), sr_bf16_hi(sum[t + 1], rb[t + 1]));
@@ -1293,8 +1379,9 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
         if constexpr (MSR) {
             // Bernoulli rounding between the searchsorted neighbours
             // (adam8.py:549-564) with the random bits of the padded
-            // [nblocks, bs] moment arrays: fed, or jax.random.bits of the
-            // leaf keys.  The first moment is coded over the whole block
+            // [nblocks, bs] moment arrays: fed, the packed stream, or
+            // jax.random.bits of the leaf keys.  With one stream per
+            // moment, the first moment is coded over the whole block
             // before the second, so that only one moment's bits, quotients
             // and candidates are live beside the block's values, and the
             // first moment's registers are free for the second's pass.
@@ -1304,49 +1391,83 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             const float* cbu = (const float*)(c.lds + L_CBU);
             const float4* srs = (const float4*)(c.lds + L_SRS);
             const float4* sru = (const float4*)(c.lds + L_SRU);
+            if (c.packed) {
+                // One block per element feeds both moments: each chunk is
+                // coded for both at once, from the same eight blocks.
 #pragma unroll
-            for (int j = 0; j < J; ++j) {
-                const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
-                uint32_t b[8], cc[8];
-                float n[8];
-                if (c.fed) {
-                    load8_u32(L.mu_bits, base + eo, b);
-                } else {
+                for (int j = 0; j < J; ++j) {
+                    const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
+                    const uint64_t e0 = (uint64_t)(base + eo);
+                    uint32_t bm[8], bv[8], cc[8];
+                    float n[8];
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) b[t] = jax_bits(c.kmu0, c.kmu1, (uint64_t)(base + eo + t));
+                    for (int t = 0; t < 8; ++t)
+                        threefry2x32(c.kmu0, c.kmu1, (uint32_t)((e0 + t) >> 32), (uint32_t)(e0 + t), bm[t], bv[t]);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) n[t] = div_by_scale(m[j][t], sm, rsm);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) cc[t] = cand_signed(c.lds, n[t]);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) cc[t] = sr_code(cbs, srs, cc[t], n[t], bm[t]);
+                    uint2 w;
+                    w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
+                    w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
+                    *(RF_GLOBAL uint2*)(mW + eo) = w;
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) n[t] = div_by_scale(v[j][t], sv, rsv);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) cc[t] = cand_unsigned(c.lds, n[t]);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) cc[t] = sr_code(cbu, sru, cc[t], n[t], bv[t]);
+                    w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
+                    w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
+                    *(RF_GLOBAL uint2*)(vW + eo) = w;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
+                    uint32_t b[8], cc[8];
+                    float n[8];
+                    if (c.fed) {
+                        load8_u32(L.mu_bits, base + eo, b);
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) b[t] = jax_bits(c.kmu0, c.kmu1, (uint64_t)(base + eo + t));
+                    }
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) n[t] = div_by_scale(m[j][t], sm, rsm);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) cc[t] = cand_signed(c.lds, n[t]);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) cc[t] = sr_code(cbs, srs, cc[t], n[t], b[t]);
+                    uint2 w;
+                    w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
+                    w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
+                    *(RF_GLOBAL uint2*)(mW + eo) = w;
                 }
 #pragma unroll
-                for (int t = 0; t < 8; ++t) n[t] = div_by_scale(m[j][t], sm, rsm);
+                for (int j = 0; j < J; ++j) {
+                    const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
+                    uint32_t b[8], cc[8];
+                    float n[8];
+                    if (c.fed) {
+                        load8_u32(L.nu_bits, base + eo, b);
+                    } else {
 #pragma unroll
-                for (int t = 0; t < 8; ++t) cc[t] = cand_signed(c.lds, n[t]);
+                        for (int t = 0; t < 8; ++t) b[t] = jax_bits(c.knu0, c.knu1, (uint64_t)(base + eo + t));
+                    }
 #pragma unroll
-                for (int t = 0; t < 8; ++t) cc[t] = sr_code(cbs, srs, cc[t], n[t], b[t]);
-                uint2 w;
-                w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
-                w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
-                *(RF_GLOBAL uint2*)(mW + eo) = w;
-            }
+                    for (int t = 0; t < 8; ++t) n[t] = div_by_scale(v[j][t], sv, rsv);
 #pragma unroll
-            for (int j = 0; j < J; ++j) {
-                const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
-                uint32_t b[8], cc[8];
-                float n[8];
-                if (c.fed) {
-                    load8_u32(L.nu_bits, base + eo, b);
-                } else {
+                    for (int t = 0; t < 8; ++t) cc[t] = cand_unsigned(c.lds, n[t]);
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) b[t] = jax_bits(c.knu0, c.knu1, (uint64_t)(base + eo + t));
+                    for (int t = 0; t < 8; ++t) cc[t] = sr_code(cbu, sru, cc[t], n[t], b[t]);
+                    uint2 w;
+                    w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
+                    w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
+                    *(RF_GLOBAL uint2*)(vW + eo) = w;
                 }
-#pragma unroll
-                for (int t = 0; t < 8; ++t) n[t] = div_by_scale(v[j][t], sv, rsv);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) cc[t] = cand_unsigned(c.lds, n[t]);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) cc[t] = sr_code(cbu, sru, cc[t], n[t], b[t]);
-                uint2 w;
-                w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
-                w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
-                *(RF_GLOBAL uint2*)(vW + eo) = w;
             }
         } else {
 #pragma unroll
@@ -1558,8 +1679,8 @@ __device__ __forceinline__ void unit_fallback(const UnitCtx& c, const rf_adam8_l
             update_one<APPLY, PSR, NEST, EXACT>(c, L, e, h, mm, vv, g[k], p[k]);
             if (store_sr) {
                 // optim/adam.py:219-222: _tree_stochastic_cast(moments, bfloat16, k1 | k2)
-                const uint32_t bm = c.fed ? gld<uint32_t>(L.mu_bits, e) : jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
-                const uint32_t bv = c.fed ? gld<uint32_t>(L.nu_bits, e) : jax_bits(c.knu0, c.knu1, (uint64_t)e);
+                uint32_t bm, bv;
+                moment_bits1(c, L, e, bm, bv);
                 gst<uint16_t>(L.mu, e, (uint16_t)sr_bf16(mm, bm));
                 gst<uint16_t>(L.nu, e, (uint16_t)sr_bf16(vv, bv));
             } else {
@@ -1653,12 +1774,10 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
             if constexpr (sizeof(PT) == 2) {
                 uint32_t hb[8];
                 if constexpr (PSR && IS_BF16<PT>) {
+                    uint32_t rb[8];
+                    param_bits8(c, L, e0, rb);
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        const uint32_t rb =
-                            c.fed ? gld<uint32_t>(L.param_bits, e0 + t) : jax_bits(c.kp0, c.kp1, (uint64_t)(e0 + t));
-                        hb[t] = sr_bf16_hi(sum[t], rb);
-                    }
+                    for (int t = 0; t < 8; ++t) hb[t] = sr_bf16_hi(sum[t], rb[t]);
                     store8_hi16(L.param, e0, hb);
                 } else {
 #pragma unroll
@@ -1681,9 +1800,8 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
             if (BF16M && store_sr) {
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
-                    const uint64_t e = (uint64_t)(e0 + t);
-                    const uint32_t bm = c.fed ? gld<uint32_t>(L.mu_bits, (int64_t)e) : jax_bits(c.kmu0, c.kmu1, e);
-                    const uint32_t bv = c.fed ? gld<uint32_t>(L.nu_bits, (int64_t)e) : jax_bits(c.knu0, c.knu1, e);
+                    uint32_t bm, bv;
+                    moment_bits1(c, L, e0 + t, bm, bv);
                     hm[t] = sr_bf16_hi(m[t], bm);
                     hv[t] = sr_bf16_hi(v[t], bv);
                 }
@@ -1848,6 +1966,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     c.lds = lds;
     c.wtab = wtab[wave_in_wg];
     c.fed = (h.flags & RF_FED_BITS) != 0;
+    c.packed = !c.fed && (h.flags & RF_PACKED_BITS) != 0;
     c.zero = false;  // quantized blocks only: RF_LEAF_ZERO_DECAY is refused for them
     c.mpart = nullptr;
     c.mbase = 0;
@@ -1923,6 +2042,7 @@ void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
     c.lds = lds;
     c.wtab = nullptr;
     c.fed = (h.flags & RF_FED_BITS) != 0;
+    c.packed = !c.fed && (h.flags & RF_PACKED_BITS) != 0;
     c.zero = false;
     c.mpart = h.mpart;
     c.mbase = 0;

@@ -17,7 +17,7 @@
 
 using namespace rf;
 
-#define RF_VERSION "rfadam8 0.1.0 gfx950"
+#define RF_VERSION "rfadam8 0.2.0 gfx950"
 
 // ------------------------------------------------------------------ errors --
 namespace {
@@ -256,7 +256,10 @@ __global__ __launch_bounds__(WG) void k_dequantize(int32_t quantizer, const uint
     }
 }
 
-// Standalone _stochastic_round_bf16 (utils.py:342-371).
+// Standalone _stochastic_round_bf16 (utils.py:342-371).  PACKED: the packed
+// bit source (a Threefry block per four elements) instead of
+// jax.random.bits.
+template <bool PACKED>
 __global__ __launch_bounds__(WG) void k_sr_bf16(const float* __restrict__ x, int64_t size, uint32_t k0,
                                                 uint32_t k1, const uint32_t* __restrict__ bits,
                                                 uint16_t* __restrict__ out, int32_t vec_ok)
@@ -269,8 +272,12 @@ __global__ __launch_bounds__(WG) void k_sr_bf16(const float* __restrict__ x, int
         float xv[8];
         load8<float>(x, e0, xv);
         uint32_t rb[8];
-        if (bits) load8_u32(bits, e0, rb);
-        else {
+        if (bits) {
+            load8_u32(bits, e0, rb);
+        } else if constexpr (PACKED) {
+            packed_param_bits4(k0, k1, (uint64_t)e0, rb);
+            packed_param_bits4(k0, k1, (uint64_t)e0 + 4, rb + 4);
+        } else {
 #pragma unroll
             for (int t = 0; t < 8; ++t) rb[t] = jax_bits(k0, k1, (uint64_t)(e0 + t));
         }
@@ -280,19 +287,23 @@ __global__ __launch_bounds__(WG) void k_sr_bf16(const float* __restrict__ x, int
         store8_hi16(out, e0, hb);
     }
     for (int64_t e = ngroups * 8 + tid; e < size; e += nthreads) {
-        const uint32_t w = bits ? bits[e] : jax_bits(k0, k1, (uint64_t)e);
+        const uint32_t w = bits ? bits[e] : PACKED ? packed_param_bits1(k0, k1, (uint64_t)e) : jax_bits(k0, k1, (uint64_t)e);
         out[e] = (uint16_t)sr_bf16(x[e], w);
     }
 }
 
 // apply_updates over a leaf table (utils.py:648-708): f32(p) + f32(u), then
 // stochastic rounding or round-to-nearest-even for bf16 params.
+template <bool PACKED>
 __device__ __forceinline__ uint32_t apply_bf16(float p, float u, bool stochastic, const uint32_t* bits, uint32_t lk0,
                                                uint32_t lk1, int64_t e)
 {
     const float s = p + u;
     if (!stochastic) return f32_to_bf16_rne(s);
-    return sr_bf16(s, bits ? gld<uint32_t>(bits, e) : jax_bits(lk0, lk1, (uint64_t)e));
+    const uint32_t w = bits      ? gld<uint32_t>(bits, e)
+                       : PACKED ? packed_param_bits1(lk0, lk1, (uint64_t)e)
+                                : jax_bits(lk0, lk1, (uint64_t)e);
+    return sr_bf16(s, w);
 }
 
 // Work units of apply_updates: APPLY_UNIT consecutive elements of one leaf
@@ -303,8 +314,9 @@ constexpr int64_t APPLY_UNIT = 8192;
 // neg_lr * (factor[leaf] * u), the scaling rf_magma_scale would have done.
 // Segment s of `segs` is leaf segs[s].leaf.  SR: stochastic rounding of bf16
 // params (an instance of its own: the Threefry code would cost the
-// nearest-even instance waves per SIMD).
-template <bool SR>
+// nearest-even instance waves per SIMD); PACKED: its bits from the packed
+// source.
+template <bool SR, bool PACKED>
 __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ leaves, const Seg* __restrict__ segs,
                                               int64_t nunits, uint32_t k0, uint32_t k1,
                                               const float* __restrict__ factor, float neg_lr)
@@ -357,6 +369,9 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
                     uint32_t rb[8];
                     if (L.bits) {
                         load8_u32(L.bits, e0, rb);
+                    } else if constexpr (PACKED) {
+                        packed_param_bits4(lk0, lk1, (uint64_t)e0, rb);  // e0: a multiple of 8
+                        packed_param_bits4(lk0, lk1, (uint64_t)e0 + 4, rb + 4);
                     } else {
 #pragma unroll
                         for (int t = 0; t < 8; ++t) rb[t] = jax_bits(lk0, lk1, (uint64_t)(e0 + t));
@@ -384,7 +399,7 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
                 gst<uint16_t>(L.param, e, (uint16_t)f32_to_f16_rne(p + u));
             } else if (L.param_dtype == RF_BF16) {
                 const float p = bf16_bits_to_f32(gld<uint16_t>(L.param, e));
-                gst<uint16_t>(L.param, e, (uint16_t)apply_bf16(p, u, sr, L.bits, lk0, lk1, e));
+                gst<uint16_t>(L.param, e, (uint16_t)apply_bf16<PACKED>(p, u, sr, L.bits, lk0, lk1, e));
             } else {
                 gst<float>(L.param, e, gld<float>(L.param, e) + u);
             }
@@ -1101,6 +1116,12 @@ struct DevState {
     uint4* tables = nullptr;     // this device's lookup_tables
     uint4* search = nullptr;     // this device's search_tables
     uint8_t* scratch_ptr = nullptr;  // this device's scratch
+    // rf_adam8_step_noalloc's ordering of calls on this device: each call
+    // makes its stream wait for the previous call's last launch (recorded
+    // here) before it overwrites the scratch, under noalloc_mu so that the
+    // wait-copy-launch-record sequences of racing threads do not interleave.
+    hipEvent_t noalloc_ev = nullptr;
+    std::mutex noalloc_mu;
     int num_cus = 0;
     StageSlot stage[STAGE_RING];
     std::atomic<uint32_t> stage_next{0};
@@ -1196,6 +1217,7 @@ rf_status device_state(DevState** out)
         HIP_TRY(hipGetSymbolAddress((void**)&d.scratch_ptr, HIP_SYMBOL(scratch)));
         if (!d.tables || !d.search || !d.scratch_ptr)
             return fail(RF_ERR_HIP, "hipGetSymbolAddress returned a null address");
+        HIP_TRY(hipEventCreateWithFlags(&d.noalloc_ev, hipEventDisableTiming));
         HIP_TRY(hipMemcpy(d.tables, ht.bytes.data(), TABLE_BYTES, hipMemcpyHostToDevice));
         HIP_TRY(hipMemcpy(d.search, hs.bytes.data(), SEARCH_BYTES, hipMemcpyHostToDevice));
         d.ready = true;
@@ -1596,6 +1618,8 @@ extern "C" {
 
 const char* rf_version(void) { return RF_VERSION; }
 
+int32_t rf_abi_version(void) { return RF_ABI_VERSION; }
+
 const char* rf_last_error(void) { return g_err.c_str(); }
 
 rf_status rf_codebook(int32_t quantizer, float* out256)
@@ -1751,6 +1775,8 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
 
     const bool msr = (f & RF_MOMENT_SR) != 0;
     const bool psr = (f & RF_PARAM_SR) != 0 && plan->apply;
+    if ((f & RF_FED_BITS) && (f & RF_PACKED_BITS))
+        return fail(RF_ERR_INVALID, "RF_FED_BITS and RF_PACKED_BITS are exclusive bit sources");
     if (f & RF_FED_BITS) {
         if (psr && !cover.pb) return fail(RF_ERR_INVALID, "RF_FED_BITS with param SR: a leaf has no param_bits");
         if (msr && !cover.mb_quant)
@@ -2034,9 +2060,19 @@ rf_status rf_adam8_step_noalloc(const rf_adam8_leaf* leaves, int32_t n_leaves, i
     if (hp->n_groups > 0 && !hp->groups) return fail(RF_ERR_INVALID, "n_groups > 0 with a null group table");
     if (hp->n_groups > 0 && hp->n_groups != group_cap)
         return fail(RF_ERR_INVALID, "n_groups must be 0 or 1 + the largest leaf.group");
+    // Under stream capture the table copy below would either fail to be
+    // captured or be recorded with a host source that a later call
+    // overwrites before the graph replays; refused before anything is
+    // enqueued.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing((hipStream_t)stream, &capture));
+    if (capture != hipStreamCaptureStatusNone)
+        return fail(RF_ERR_UNSUPPORTED, "rf_adam8_step_noalloc cannot be captured into a graph (its leaf tables "
+                                        "are copied from host memory at each call)");
     DevState* ds = nullptr;
     rf_status st = device_state(&ds);
     if (st != RF_OK) return st;
+    std::lock_guard<std::mutex> order(ds->noalloc_mu);
     // Host-side lists in per-thread buffers that keep their capacity.
     thread_local WorkLists w;
     st = build_work_lists(leaves, n_leaves, apply, w);
@@ -2069,8 +2105,9 @@ rf_status rf_adam8_step_noalloc(const rf_adam8_leaf* leaves, int32_t n_leaves, i
     std::memcpy(host.data() + o_segs, w.segs.data(), sizeof(Seg) * w.segs.size());
     std::memcpy(host.data() + o_nsegs, w.nsegs.data(), sizeof(Seg) * w.nsegs.size());
     uint8_t* const base = ds->scratch_ptr;
-    // Stream-ordered after earlier calls on this stream; from pageable memory
-    // the call returns once the source has been consumed.
+    // After the previous call's launches on this device, whatever its stream;
+    // from pageable memory the copy returns once its source is consumed.
+    HIP_TRY(hipStreamWaitEvent((hipStream_t)stream, ds->noalloc_ev, 0));
     HIP_TRY(hipMemcpyAsync(base, host.data(), o_npart, hipMemcpyHostToDevice, (hipStream_t)stream));
 
     // The launch description of plan_launch, over the scratch (owns nothing).
@@ -2096,6 +2133,10 @@ rf_status rf_adam8_step_noalloc(const rf_adam8_leaf* leaves, int32_t n_leaves, i
     const rf_adam8_group* d_groups = n_groups ? (const rf_adam8_group*)(base + o_groups) : nullptr;
     st = plan_launch(&plan, plan.d_leaves, d_groups, bits_cover(leaves, n_leaves), hp, stream);
     w.groups.swap(plan.groups);
+    // The next call (any stream) waits for these launches; recorded even
+    // after a failed launch, so that whatever was enqueued is covered.
+    const hipError_t rec = hipEventRecord(ds->noalloc_ev, (hipStream_t)stream);
+    if (st == RF_OK && rec != hipSuccess) return fail(RF_ERR_HIP, std::string("hipEventRecord: ") + hipGetErrorString(rec));
     return st;
 }
 
@@ -2161,8 +2202,12 @@ rf_status rf_blockwise_dequantize(int32_t quantizer, const void* values, const v
     return RF_OK;
 }
 
-rf_status rf_sr_bf16(const float* x, int64_t size, uint32_t key0, uint32_t key1, const uint32_t* bits, uint16_t* out,
-                     void* stream)
+}  // extern "C"
+
+namespace {
+
+rf_status sr_bf16_launch(const float* x, int64_t size, uint32_t key0, uint32_t key1, const uint32_t* bits,
+                         uint16_t* out, bool packed, void* stream)
 {
     if (size < 0) return fail(RF_ERR_INVALID, "negative size");
     if (size == 0) return RF_OK;
@@ -2173,10 +2218,29 @@ rf_status rf_sr_bf16(const float* x, int64_t size, uint32_t key0, uint32_t key1,
     const int32_t vec_ok = aligned(x, 16) && aligned(out, 16) && (!bits || aligned(bits, 16));
     const int64_t work = vec_ok ? (size + 7) / 8 : size;
     const int grid = (int)std::max<int64_t>(1, std::min<int64_t>((work + WG - 1) / WG, (int64_t)ds->num_cus * 8));
-    hipLaunchKernelGGL(k_sr_bf16, dim3(grid), dim3(WG), 0, (hipStream_t)stream, x, size, key0, key1, bits, out,
-                       vec_ok);
+    if (packed)
+        hipLaunchKernelGGL(k_sr_bf16<true>, dim3(grid), dim3(WG), 0, (hipStream_t)stream, x, size, key0, key1,
+                           nullptr, out, vec_ok);
+    else
+        hipLaunchKernelGGL(k_sr_bf16<false>, dim3(grid), dim3(WG), 0, (hipStream_t)stream, x, size, key0, key1,
+                           bits, out, vec_ok);
     HIP_TRY(hipGetLastError());
     return RF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+rf_status rf_sr_bf16(const float* x, int64_t size, uint32_t key0, uint32_t key1, const uint32_t* bits, uint16_t* out,
+                     void* stream)
+{
+    return sr_bf16_launch(x, size, key0, key1, bits, out, false, stream);
+}
+
+rf_status rf_sr_bf16_packed(const float* x, int64_t size, uint32_t key0, uint32_t key1, uint16_t* out, void* stream)
+{
+    return sr_bf16_launch(x, size, key0, key1, nullptr, out, true, stream);
 }
 
 rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, float max_norm, float* stats,
@@ -2278,7 +2342,7 @@ rf_status rf_clip_by_global_norm(const rf_clip_leaf* leaves, int32_t n_leaves, f
 namespace {
 
 rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic, uint32_t key0,
-                       uint32_t key1, const float* factor, float neg_lr, void* stream);
+                       uint32_t key1, const float* factor, float neg_lr, void* stream, bool packed = false);
 
 // Validates a Magma leaf table and builds its work list (segment i = leaf i).
 rf_status magma_list(const rf_magma_leaf* leaves, int32_t n_leaves, bool need_updates, std::vector<Seg>& segs,
@@ -2418,6 +2482,14 @@ rf_status rf_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, int32_
     return apply_launch(leaves, n_leaves, stochastic, key0, key1, nullptr, 1.0f, stream);
 }
 
+rf_status rf_apply_updates_packed(const rf_apply_leaf* leaves, int32_t n_leaves, uint32_t key0, uint32_t key1,
+                                  void* stream)
+{
+    for (int32_t i = 0; leaves && i < n_leaves; ++i)
+        if (leaves[i].bits) return fail(RF_ERR_INVALID, "rf_apply_updates_packed draws its own bits: leaf bits must be NULL");
+    return apply_launch(leaves, n_leaves, 1, key0, key1, nullptr, 1.0f, stream, true);
+}
+
 rf_status rf_magma_apply_updates(const rf_apply_leaf* leaves, int32_t n_leaves, const float* factor, float neg_lr,
                                  int32_t stochastic, uint32_t key0, uint32_t key1, void* stream)
 {
@@ -2482,7 +2554,7 @@ rf_status rf_accumulate(const rf_accum_leaf* leaves, int32_t n_leaves, int32_t m
 namespace {
 
 rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t stochastic, uint32_t key0,
-                       uint32_t key1, const float* factor, float neg_lr, void* stream)
+                       uint32_t key1, const float* factor, float neg_lr, void* stream, bool packed)
 {
     if (n_leaves < 0 || (n_leaves > 0 && !leaves)) return fail(RF_ERR_INVALID, "bad leaf table");
     if (n_leaves == 0) return RF_OK;
@@ -2518,7 +2590,9 @@ rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t st
     segs.push_back(sentinel);
     mark_list(segs);
     hipStream_t s = (hipStream_t)stream;
-    const void* fn = stochastic ? (const void*)&k_apply<true> : (const void*)&k_apply<false>;
+    const void* fn = !stochastic ? (const void*)&k_apply<false, false>
+                     : packed    ? (const void*)&k_apply<true, true>
+                                 : (const void*)&k_apply<true, false>;
     unsigned aw = 1;  // before the staging slot: an error here leaves nothing in flight
     st = worklist_grid(fn, ds, nunits, &aw);
     if (st != RF_OK) return st;
@@ -2531,11 +2605,14 @@ rf_status apply_launch(const rf_apply_leaf* leaves, int32_t n_leaves, int32_t st
     std::memcpy(stg.host() + o_sg, segs.data(), sizeof(Seg) * segs.size());
     st = stg.upload(bytes, s);
     if (st != RF_OK) return st;
-    if (stochastic)
-        hipLaunchKernelGGL(k_apply<true>, dim3(aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
+    if (stochastic && packed)
+        hipLaunchKernelGGL((k_apply<true, true>), dim3(aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
+                           (const Seg*)(stg.dev() + o_sg), nunits, key0, key1, factor, neg_lr);
+    else if (stochastic)
+        hipLaunchKernelGGL((k_apply<true, false>), dim3(aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
                            (const Seg*)(stg.dev() + o_sg), nunits, key0, key1, factor, neg_lr);
     else
-        hipLaunchKernelGGL(k_apply<false>, dim3(aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
+        hipLaunchKernelGGL((k_apply<false, false>), dim3(aw), dim3(WG), 0, s, (const rf_apply_leaf*)stg.dev(),
                            (const Seg*)(stg.dev() + o_sg), nunits, key0, key1, factor, neg_lr);
     const hipError_t le = hipGetLastError();
     st = stg.finish(s);

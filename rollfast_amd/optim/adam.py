@@ -54,6 +54,7 @@ from .adam8 import (
     _Engine,
     _require_device_tensor,
     _torch,
+    _check_sr_bits,
     canonicalize_dtype,
     decay_link_state,
 )
@@ -252,10 +253,11 @@ def _zeros_like_tree(params, dtype):
     return _tree.tree_map(zeros, params, is_leaf=_is_passthrough_leaf)
 
 
-def _make_engine(b1, b2, eps, eps_root, mu_dtype, nesterov, key, exact, magma: bool = False) -> _AdamEngine:
+def _make_engine(b1, b2, eps, eps_root, mu_dtype, nesterov, key, exact, magma: bool = False,
+                 sr_bits: str = "jax") -> _AdamEngine:
     torch = _torch()
     cfg = _Config(b1, b2, eps, eps_root, 2048, 1 << 62, torch.float32, mu_dtype, False, "shard_local", False,
-                  bool(nesterov), key, bool(exact))
+                  bool(nesterov), key, bool(exact), _check_sr_bits(sr_bits))
     eng = (_MagmaAdamEngine if magma else _AdamEngine)(cfg)
     eng.store_sr = mu_dtype == torch.bfloat16
     return eng
@@ -379,17 +381,22 @@ def scale_by_adam(
     axis_name: Optional[str] = None,
     key=None,
     exact: bool = False,
+    sr_bits: str = "jax",
 ) -> GradientTransformation:
     """Rescale updates according to the Adam algorithm (adam.py:38-235).
     ``exact`` (extension): IEEE division and square root in the direction.
-    ``axis_name`` names a collective axis of the reference's sharded runs and
-    has no effect on one device."""
+    ``sr_bits`` (extension): the bit source of bf16 moment storage and of
+    the fused step's param rounding, "jax" or "packed" (as for
+    scale_by_adam8); Magma keeps "jax".  ``axis_name`` names a collective
+    axis of the reference's sharded runs and has no effect on one device."""
     del axis_name
     if use_magma:
         _validate_magma_args(magma_p, magma_tau)
+        if _check_sr_bits(sr_bits) != "jax":
+            raise NotImplementedError("Magma draws its stochastic rounding from the jax stream only")
     _has_nonzero_or_scheduled(weight_decay)
     mu = _canonical_mu_dtype(mu_dtype)
-    engine = _make_engine(b1, b2, eps, eps_root, mu, nesterov, key, exact, magma=use_magma)
+    engine = _make_engine(b1, b2, eps, eps_root, mu, nesterov, key, exact, magma=use_magma, sr_bits=sr_bits)
 
     def init_fn(params):
         return ScaleByAdamState(count=np.zeros((), dtype=np.int32), mu=_zeros_like_tree(params, mu),
@@ -417,6 +424,7 @@ def adamw(
     axis_name: Optional[str] = None,
     key=None,
     exact: bool = False,
+    sr_bits: str = "jax",
 ) -> GradientTransformationExtraArgs:
     """Adam with decoupled weight decay (adam.py:238-406): the optax chain
     ``scale_by_adam -> add_decayed_weights -> scale_by_learning_rate`` in one
@@ -427,7 +435,7 @@ def adamw(
         inner = scale_by_adam(b1=b1, b2=b2, eps=eps, eps_root=eps_root, mu_dtype=mu_dtype,
                               weight_decay=weight_decay, weight_decay_mask=weight_decay_mask, nesterov=nesterov,
                               use_magma=True, magma_p=magma_p, magma_tau=magma_tau, axis_name=axis_name, key=key,
-                              exact=exact)
+                              exact=exact, sr_bits=sr_bits)
 
         def magma_init(params):
             lr_state = (ScaleByScheduleState(count=np.zeros((), dtype=np.int32)) if callable(learning_rate)
@@ -438,7 +446,8 @@ def adamw(
             magma_init, _AdamwMagmaUpdate(inner.update.engine, learning_rate, weight_decay, weight_decay_mask,
                                           inner.update.magma))
     inner = scale_by_adam(b1=b1, b2=b2, eps=eps, eps_root=eps_root, mu_dtype=mu_dtype, nesterov=nesterov,
-                          axis_name=axis_name, key=key, exact=exact, magma_p=magma_p, magma_tau=magma_tau)
+                          axis_name=axis_name, key=key, exact=exact, magma_p=magma_p, magma_tau=magma_tau,
+                          sr_bits=sr_bits)
     wd_nonzero = _has_nonzero_or_scheduled(weight_decay)
     engine = inner.update.engine
 

@@ -393,6 +393,21 @@ class _Config:
     nesterov: bool
     key: Any
     exact: bool
+    sr_bits: str = "jax"
+
+
+SR_BITS = ("jax", "packed")
+
+
+def _check_sr_bits(sr_bits) -> str:
+    """The bit source of the in-kernel stochastic roundings: "jax" (the
+    default) draws jax.random.bits' stream, one Threefry-2x32-20 block per
+    32-bit word (bitwise the reference's layout); "packed" (no reference
+    counterpart) spends one block on four param roundings, or on both
+    moments' draws of an element, from the same per-leaf keys."""
+    if sr_bits not in SR_BITS:
+        raise ValueError(f"sr_bits must be one of {SR_BITS}, got {sr_bits!r}")
+    return sr_bits
 
 
 def _init_moment_leaf(param, cfg: _Config, quantizer: str):
@@ -745,6 +760,8 @@ class _Engine:
             flags |= _lib.RF_EXACT
         if random_bits is not None:
             flags |= _lib.RF_FED_BITS
+        elif cfg.sr_bits == "packed":
+            flags |= _lib.RF_PACKED_BITS
         if skip_nonfinite:
             flags |= _lib.RF_SKIP_NONFINITE
 
@@ -946,18 +963,23 @@ def scale_by_adam8(
     nesterov: bool = False,
     key=None,
     exact: bool = False,
+    sr_bits: str = "jax",
 ) -> GradientTransformation:
     """Rescale gradients by Adam while storing eligible moments as 8-bit
     blocks (adam8.py:243-391).  ``exact`` (extension): IEEE division and
     square root in the update direction instead of the hardware
     reciprocal/square-root (moments, codes and scales are bit-exact either
-    way)."""
+    way).  ``sr_bits`` (extension): the random-bit source of the moments'
+    stochastic rounding and of the fused step's param rounding, "jax"
+    (jax.random.bits' layout) or "packed" (one Threefry block per element
+    for both moments, per four elements for params)."""
     torch = _torch()
     scale_dtype = torch.float32 if scale_dtype is None else canonicalize_dtype(scale_dtype)
     fallback_dtype = torch.float32 if fallback_dtype is None else canonicalize_dtype(fallback_dtype)
     _validate(block_size, min_size, block_layout, fallback_dtype, scale_dtype)
     cfg = _Config(b1, b2, eps, eps_root, int(block_size), int(min_size), scale_dtype, fallback_dtype,
-                  bool(stochastic_rounding), block_layout, bool(quantize), bool(nesterov), key, bool(exact))
+                  bool(stochastic_rounding), block_layout, bool(quantize), bool(nesterov), key, bool(exact),
+                  _check_sr_bits(sr_bits))
     engine = _Engine(cfg)
 
     def init_fn(params):
@@ -1095,16 +1117,17 @@ def adamw8(
     use_magma: bool = False,
     key=None,
     exact: bool = False,
+    sr_bits: str = "jax",
 ) -> GradientTransformationExtraArgs:
     """AdamW whose eligible moment leaves use blockwise 8-bit codebook state
-    (adam8.py:394-443).  The state is the chain's tuple
+    (adam8.py:394-443).  ``exact`` and ``sr_bits``: as for scale_by_adam8.  The state is the chain's tuple
     ``(ScaleByAdam8State, add_decayed_weights state?, lr state)``."""
     if use_magma:
         raise NotImplementedError("Magma is not supported by adamw8 yet.")
     inner = scale_by_adam8(
         b1=b1, b2=b2, eps=eps, eps_root=eps_root, block_size=block_size, min_size=min_size,
         scale_dtype=scale_dtype, fallback_dtype=fallback_dtype, stochastic_rounding=stochastic_rounding,
-        block_layout=block_layout, quantize=quantize, nesterov=nesterov, key=key, exact=exact,
+        block_layout=block_layout, quantize=quantize, nesterov=nesterov, key=key, exact=exact, sr_bits=sr_bits,
     )
     weight_decay_is_nonzero = weight_decay > 0.0 if isinstance(weight_decay, (int, float)) else True
     engine = inner.update.engine
@@ -1193,7 +1216,7 @@ def _group_key(upd) -> tuple:
     cfg = upd.engine.cfg
     wd = upd.weight_decay if upd.wd_nonzero else 0.0
     return (_as_f32(cfg.b1).item(), _as_f32(cfg.b2).item(), _as_f32(cfg.eps).item(), _as_f32(cfg.eps_root).item(),
-            bool(cfg.nesterov), bool(cfg.exact), isinstance(wd, (int, float)))
+            bool(cfg.nesterov), bool(cfg.exact), cfg.sr_bits, isinstance(wd, (int, float)))
 
 
 def _moment_sr(upd) -> Optional[bool]:
@@ -1265,6 +1288,8 @@ class _GroupedRunner:
             flags |= _lib.RF_EXACT
         if random_bits is not None:
             flags |= _lib.RF_FED_BITS
+        elif cfg.sr_bits == "packed":
+            flags |= _lib.RF_PACKED_BITS
         if skip_nonfinite:
             flags |= _lib.RF_SKIP_NONFINITE
         count_inc = safe_int32_increment(int(np.asarray(state0[0].count)))

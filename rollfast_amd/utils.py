@@ -34,7 +34,29 @@ def _torch():
     return torch
 
 
-def _launch_apply(pairs, stochastic: bool, key) -> None:
+_SR_BITS = ("jax", "packed")
+
+
+def _check_sr_bits(sr_bits) -> bool:
+    """True for the packed bit source (no reference counterpart: one
+    Threefry-2x32-20 block per four roundings, element e taking the 16-bit
+    half (e & 1) of word (e & 2 ? y1 : y0) of the block at counter e >> 2
+    under the leaf's key); False for jax.random.bits' stream."""
+    if sr_bits not in _SR_BITS:
+        raise ValueError(f"sr_bits must be one of {_SR_BITS}, got {sr_bits!r}")
+    return sr_bits == "packed"
+
+
+def _apply_call(table, n: int, stochastic: bool, k, packed: bool) -> None:
+    lib = _lib.lib()
+    if stochastic and packed:
+        _lib.check(lib.rf_apply_updates_packed(table, n, int(k[0]), int(k[1]), _lib.stream_ptr()), "apply_updates")
+    else:
+        _lib.check(lib.rf_apply_updates(table, n, 1 if stochastic else 0, int(k[0]), int(k[1]), _lib.stream_ptr()),
+                   "apply_updates")
+
+
+def _launch_apply(pairs, stochastic: bool, key, packed: bool = False) -> None:
     """pairs: [(param_tensor, update_tensor, param_index)]."""
     torch = _torch()
     if not pairs:
@@ -68,34 +90,29 @@ def _launch_apply(pairs, stochastic: bool, key) -> None:
     k = prng.as_key(key) if key is not None else np.zeros(2, np.uint32)
     table = (_lib.ApplyLeaf * len(rows))(*rows)
     with torch.cuda.device(device):
-        _lib.check(
-            _lib.lib().rf_apply_updates(table, len(rows), 1 if stochastic else 0, int(k[0]), int(k[1]),
-                                        _lib.stream_ptr()),
-            "apply_updates",
-        )
+        _apply_call(table, len(rows), stochastic, k, packed)
     # The kernel is stream-ordered after any producer of `keep`; dropping the
     # references here is safe with torch's stream-ordered caching allocator.
     del keep
 
 
-def _launch_rows(rows: bytes, n: int, device: int, stochastic: bool, key) -> None:
-    """rf_apply_updates over ``n`` packed rf_apply_leaf records."""
+def _launch_rows(rows: bytes, n: int, device: int, stochastic: bool, key, packed: bool = False) -> None:
+    """rf_apply_updates over ``n`` rf_apply_leaf records laid out in ``rows``."""
     torch = _torch()
     k = prng.as_key(key) if key is not None else np.zeros(2, np.uint32)
     buf = ctypes.create_string_buffer(rows, len(rows))
     table = ctypes.cast(buf, ctypes.POINTER(_lib.ApplyLeaf))
     with torch.cuda.device(device):
-        _lib.check(
-            _lib.lib().rf_apply_updates(table, n, 1 if stochastic else 0, int(k[0]), int(k[1]), _lib.stream_ptr()),
-            "apply_updates",
-        )
+        _apply_call(table, n, stochastic, k, packed)
 
 
-def apply_updates(params, updates, key=None, stochastic: bool = True):
+def apply_updates(params, updates, key=None, stochastic: bool = True, *, sr_bits: str = "jax"):
     """Apply updates with optional stochastic rounding for bf16 params
     (utils.py:648-708): bf16 leaves take ``f32(p) + f32(u)`` then SR (per-leaf
     key ``split(key, n_leaves)[i]``) or round-to-nearest-even; f32 leaves
-    take ``p + u``.  None / MaskedNode leaves are left unchanged."""
+    take ``p + u``.  None / MaskedNode leaves are left unchanged.
+    ``sr_bits`` (extension): "jax" (jax.random.bits' stream) or "packed"."""
+    packed = _check_sr_bits(sr_bits)
     if stochastic and key is None:
         raise ValueError(_KEY_MSG)
     # Native walk (contiguous f32/bf16 params, f32 updates, dict/list/tuple
@@ -104,7 +121,7 @@ def apply_updates(params, updates, key=None, stochastic: bool = True):
     if fast is not None:
         rows, n, device, tree = fast
         if n:
-            _launch_rows(rows, n, device, stochastic, key)
+            _launch_rows(rows, n, device, stochastic, key, packed)
         return tree
     leaves, td = _tree.flatten(params, is_leaf=_is_aux_leaf)
     u_leaves = _tree.flatten_up_to(td, updates)
@@ -113,14 +130,15 @@ def apply_updates(params, updates, key=None, stochastic: bool = True):
         if _is_aux_leaf(p) or _is_aux_leaf(u):
             continue
         pairs.append((p, u, i))
-    _launch_apply(pairs, stochastic, key)
+    _launch_apply(pairs, stochastic, key, packed)
     return _tree.unflatten(td, leaves)
 
 
-def apply_updates_prefix(model, updates, key=None, stochastic: bool = True):
+def apply_updates_prefix(model, updates, key=None, stochastic: bool = True, *, sr_bits: str = "jax"):
     """Equinox-compatible apply_updates where ``updates`` may be a prefix of
     ``model`` (utils.py:711-769): a None / MaskedNode update leaves the whole
     model subtree unchanged; keys are split over the update leaves."""
+    packed = _check_sr_bits(sr_bits)
     if stochastic and key is None:
         raise ValueError(_KEY_MSG)
     u_leaves, u_td = _tree.flatten(updates, is_leaf=_is_aux_leaf)
@@ -130,15 +148,17 @@ def apply_updates_prefix(model, updates, key=None, stochastic: bool = True):
         if _is_aux_leaf(u) or _is_aux_leaf(p):
             continue
         pairs.append((p, u, i))
-    _launch_apply(pairs, stochastic, key)
+    _launch_apply(pairs, stochastic, key, packed)
     return _tree.unflatten(u_td, m_sub)
 
 
-def _stochastic_round_bf16(x, key, random_bits=None):
+def _stochastic_round_bf16(x, key, random_bits=None, *, sr_bits: str = "jax"):
     """FP32 -> BF16 stochastic rounding by integer bit-add (utils.py:342-371).
     ``random_bits`` (testing): raw uint32 words replacing the in-kernel
-    ``jax.random.bits(key, x.shape)``."""
+    ``jax.random.bits(key, x.shape)``.  ``sr_bits`` (extension): "jax" or
+    "packed" (a Threefry block per four elements)."""
     torch = _torch()
+    packed = _check_sr_bits(sr_bits)
     if x.dtype == torch.bfloat16:
         return x
     if not isinstance(x, torch.Tensor) or not x.is_cuda:
@@ -151,21 +171,26 @@ def _stochastic_round_bf16(x, key, random_bits=None):
         bits = random_bits.contiguous()
         if bits.dtype != torch.uint32 or bits.numel() != xf.numel():
             raise ValueError("random_bits must be uint32 with one word per element")
+        if packed:
+            raise ValueError("random_bits replace the in-kernel bits: sr_bits must stay 'jax'")
     elif key is None:
         raise ValueError("stochastic rounding requires a PRNG key.")
     with torch.cuda.device(x.device):
-        _lib.check(
-            _lib.lib().rf_sr_bf16(xf.data_ptr(), int(xf.numel()), int(k[0]), int(k[1]),
-                                  None if bits is None else bits.data_ptr(), out.data_ptr(), _lib.stream_ptr()),
-            "_stochastic_round_bf16",
-        )
+        if packed:
+            st = _lib.lib().rf_sr_bf16_packed(xf.data_ptr(), int(xf.numel()), int(k[0]), int(k[1]), out.data_ptr(),
+                                              _lib.stream_ptr())
+        else:
+            st = _lib.lib().rf_sr_bf16(xf.data_ptr(), int(xf.numel()), int(k[0]), int(k[1]),
+                                       None if bits is None else bits.data_ptr(), out.data_ptr(), _lib.stream_ptr())
+        _lib.check(st, "_stochastic_round_bf16")
     return out
 
 
-def _tree_stochastic_cast(tree, target_dtype, key):
+def _tree_stochastic_cast(tree, target_dtype, key, *, sr_bits: str = "jax"):
     """Cast a pytree, stochastically rounding to bf16 (utils.py:374-409):
     per-leaf keys ``split(key, n_leaves)``; MaskedNode / None / non-array
-    leaves pass through."""
+    leaves pass through.  ``sr_bits``: as for _stochastic_round_bf16."""
+    _check_sr_bits(sr_bits)
     torch = _torch()
     leaves, td = _tree.flatten(tree, is_leaf=_is_aux_leaf)
     keys = prng.split(key, len(leaves))
@@ -176,7 +201,7 @@ def _tree_stochastic_cast(tree, target_dtype, key):
         elif leaf.dtype.is_complex and not target_dtype.is_complex:
             out.append(leaf.to(torch.complex64))
         elif target_dtype == torch.bfloat16:
-            out.append(_stochastic_round_bf16(leaf, k))
+            out.append(_stochastic_round_bf16(leaf, k, sr_bits=sr_bits))
         else:
             out.append(leaf.to(target_dtype))
     return _tree.unflatten(td, out)

@@ -11,11 +11,15 @@ block alone.  The oracle keeps its own codes and scales across the steps
 (bar: bit-exact) and takes the device's params before each step (bar: within
 one bf16 ulp after it).
 
-The second test turns on param and moment stochastic rounding with fed
-random bits (arbitrary uint32 words on the device, the same words given to
-the oracle): the moment codes stay bit-exact and the params within one bf16
-ulp (the direction's hardware rcp/sqrt can move the f32 sum by a few ulps
-before it is rounded).
+The other tests turn on param and moment stochastic rounding with three bit
+sources: fed random bits (arbitrary uint32 words on the device, the same
+words given to the oracle), the in-kernel jax.random.bits stream of the
+per-leaf keys (291 leaves' key derivation; the oracle gets
+``orc.random_bits`` of the same keys at each sampled block's offset) and the
+packed source (``orc.packed_param_bits`` / ``packed_moment_bits`` at the
+block's offset).  The moment codes stay bit-exact and the params within one
+bf16 ulp (the direction's hardware rcp/sqrt can move the f32 sum by a few
+ulps before it is rounded).
 """
 
 from __future__ import annotations
@@ -51,7 +55,13 @@ def _random_words(n, gen):
     return torch.randint(0, 256, (4 * n,), dtype=torch.uint8, device="cuda", generator=gen).view(torch.uint32)
 
 
-def _llama_tree_run(sr: bool, steps: int):
+def _key(k):
+    return tuple(int(v) for v in k)
+
+
+def _llama_tree_run(sr: bool, steps: int, source: str = "fed"):
+    """``source``: the SR bits -- "fed", "jax" (in-kernel jax.random.bits)
+    or "packed" (in-kernel packed source)."""
     import torch
 
     import bench
@@ -66,7 +76,8 @@ def _llama_tree_run(sr: bool, steps: int):
     print(f"[llama7b] sr={sr}: allocating params", flush=True)
     params = {nm: (torch.randn(s, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
               for nm, s in zip(names, shapes)}
-    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, stochastic_rounding=sr)
+    tx = rf.adamw8(learning_rate=1e-3, weight_decay=0.01, stochastic_rounding=sr,
+                   sr_bits="packed" if source == "packed" else "jax")
     state = tx.init(params)
     rng = np.random.default_rng(3)
     picks = []
@@ -85,14 +96,34 @@ def _llama_tree_run(sr: bool, steps: int):
         print(f"[llama7b] sr={sr}: step {step + 1}", flush=True)
         grads = {nm: (torch.randn(s, generator=gen, device="cuda") * 1e-3).to(torch.bfloat16)
                  for nm, s in zip(names, shapes)}
-        bits = None
-        if sr:
+        bits = fed = None
+        pkey = rf.prng.PRNGKey(100 + step)
+        if sr and source == "fed":
             bits = {i: (_random_words(sizes[i], gen), _random_words(sizes[i], gen), _random_words(sizes[i], gen))
                     for i in range(len(names))}
+            fed = [tuple(_rows(b, idx) for b in bits[i]) for i, idx in enumerate(picks)]
+        elif sr:
+            # the words the in-kernel source draws for each sampled block:
+            # leaf i's keys are split(key_mu | key_nu | param key, 291)[i]
+            key_mu, key_nu, _ = orc.split(_key(state[0].key), 3)
+            kmu, knu = orc.split(tuple(key_mu), len(names)), orc.split(tuple(key_nu), len(names))
+            kp = orc.split(_key(pkey), len(names))
+            fed = []
+            for i, idx in enumerate(picks):
+                rows = ([], [], [])
+                for b in idx:
+                    off = int(b) * BS
+                    if source == "packed":
+                        bm, bv = orc.packed_moment_bits(kmu[i], BS, off)
+                        bp = orc.packed_param_bits(kp[i], BS, off)
+                    else:
+                        bm, bv = orc.random_bits(kmu[i], BS, off), orc.random_bits(knu[i], BS, off)
+                        bp = orc.random_bits(kp[i], BS, off)
+                    for lst, w in zip(rows, (bm, bv, bp)):
+                        lst.append(w)
+                fed.append(tuple(np.stack(r) for r in rows))
         before = [(_rows(params[nm], idx), _rows(grads[nm], idx)) for nm, idx in zip(names, picks)]
-        fed = ([tuple(_rows(b, idx) for b in bits[i]) for i, idx in enumerate(picks)] if sr else None)
-        params, state = rf.adamw8_step(tx, params, grads, state, key=rf.prng.PRNGKey(100 + step), stochastic=sr,
-                                       random_bits=bits)
+        params, state = rf.adamw8_step(tx, params, grads, state, key=pkey, stochastic=sr, random_bits=bits)
         torch.cuda.synchronize()
         del grads, bits
         hp = orc.make_hparams(weight_decay=0.01, lr=1e-3, count=step + 1, decay=True, apply=True,
@@ -134,3 +165,11 @@ def test_llama7b_whole_tree_three_steps_default_mode():
 
 def test_llama7b_whole_tree_param_and_moment_sr_fed_bits():
     _llama_tree_run(sr=True, steps=2)
+
+
+def test_llama7b_whole_tree_param_and_moment_sr_jax_stream():
+    _llama_tree_run(sr=True, steps=2, source="jax")
+
+
+def test_llama7b_whole_tree_param_and_moment_sr_packed():
+    _llama_tree_run(sr=True, steps=2, source="packed")

@@ -1097,3 +1097,31 @@ def test_multisteps_counters_known_sequence():
     assert minis == [1, 2, 0, 1, 2, 0, 1]
     assert grads == [0, 0, 1, 1, 1, 2, 2]
     assert orc.multisteps_counters(0, 5, 1) == (True, 0, 6)
+
+
+# ------------------------------------------------------ packed bit source --
+def test_packed_param_bits_definition():
+    """The packed source's param bits (no reference counterpart), element by
+    element from the KAT-pinned block function: element e takes half (e & 1)
+    of word (e & 2 ? y1 : y0) of the block at counter e >> 2, including
+    offsets whose block counter crosses 2^32 and unaligned offsets."""
+    key = (0x13198A2E, 0x03707344)
+    for offset in (0, 3, (1 << 34) - 6):
+        got = orc.packed_param_bits(key, 13, offset)
+        for i, b in enumerate(got):
+            e = offset + i
+            q = e >> 2
+            y = orc.threefry2x32(key, (q >> 32, q & 0xFFFFFFFF))
+            w = y[1] if e & 2 else y[0]
+            assert int(b) == ((w >> 16) if e & 1 else (w & 0xFFFF))
+    # four consecutive elements use the four halves of one block, once each
+    y0, y1 = orc.threefry2x32(key, (0, 5))
+    assert orc.packed_param_bits(key, 4, 20).tolist() == [y0 & 0xFFFF, y0 >> 16, y1 & 0xFFFF, y1 >> 16]
+
+
+def test_packed_moment_bits_definition():
+    key = (7, 11)
+    m, v = orc.packed_moment_bits(key, 6, (1 << 32) - 3)
+    for i in range(6):
+        c = (1 << 32) - 3 + i
+        assert (int(m[i]), int(v[i])) == orc.threefry2x32(key, (c >> 32, c & 0xFFFFFFFF))

@@ -175,3 +175,114 @@ def test_noalloc_refuses_a_tree_beyond_its_scratch():
     assert b"maximum" in lib.rf_last_error()
     torch.cuda.synchronize()
     assert torch.equal(p, before)
+
+
+def _hip():
+    """The HIP runtime (stream capture calls the tests make directly)."""
+    lib = ctypes.CDLL("libamdhip64.so")
+    lib.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    lib.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    lib.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+    return lib
+
+
+def test_noalloc_refuses_stream_capture():
+    """On a capturing stream the call returns RF_ERR_UNSUPPORTED and
+    enqueues nothing: the capture ends with an empty graph and the tree's
+    params are unchanged."""
+    import torch
+
+    from rollfast_amd import _lib
+
+    lib = _lib.lib()
+    hip = _hip()
+    leaves = _leaf_set([(2 * BS, "bf16", "bf16", "q")], 5)
+    before = leaves[0]["p"].clone()
+    table = _table(leaves)
+    hp = _hparams(1, _lib.RF_LR, 0.0)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    print("[no_alloc] capture refusal", flush=True)
+    assert hip.hipStreamBeginCapture(ctypes.c_void_p(s.cuda_stream), 2) == 0  # hipStreamCaptureModeRelaxed
+    st = lib.rf_adam8_step_noalloc(table, 1, 1, ctypes.byref(hp), ctypes.c_void_p(s.cuda_stream))
+    msg = lib.rf_last_error()
+    graph = ctypes.c_void_p()
+    assert hip.hipStreamEndCapture(ctypes.c_void_p(s.cuda_stream), ctypes.byref(graph)) == 0
+    if graph.value:
+        hip.hipGraphDestroy(graph)
+    assert st == _lib.RF_ERR_UNSUPPORTED and b"graph" in msg
+    torch.cuda.synchronize()
+    assert torch.equal(leaves[0]["p"], before)
+
+
+def test_noalloc_calls_on_two_streams_are_ordered():
+    """A call on stream A behind pending work, then at once a call on stream
+    B over another tree: B's table copy waits for A's launches (the
+    library's per-device event), so both trees equal rf_adam8_step's."""
+    import torch
+
+    from rollfast_amd import _lib
+
+    lib = _lib.lib()
+    specs_a = [(64 * BS, "bf16", "bf16", "q"), (3 * BS + 11, "f32", "bf16", "q"), (900, "bf16", "bf16", "f32")]
+    specs_b = [(5 * BS, "bf16", "f32", "q"), (2 * BS, "f32", "f32", "q")]
+    a, b = _leaf_set(specs_a, 7), _leaf_set(specs_b, 8)
+    ra, rb = _clone(a), _clone(b)
+    flags = _lib.RF_LR | _lib.RF_DECAY_WEAK
+    for ref, specs in ((ra, specs_a), (rb, specs_b)):
+        hp = _hparams(1, flags, 0.0)
+        assert lib.rf_adam8_step(_table(ref), len(specs), 1, ctypes.byref(hp), _lib.stream_ptr()) == _lib.RF_OK
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    x = torch.ones(1 << 28, device="cuda")
+    ta, tb = _table(a), _table(b)
+    hpa, hpb = _hparams(1, flags, 0.0), _hparams(1, flags, 0.0)
+    print("[no_alloc] two streams", flush=True)
+    with torch.cuda.stream(sa):
+        for _ in range(8):
+            x.mul_(1.0)   # pending work ahead of A's call
+        st = lib.rf_adam8_step_noalloc(ta, len(specs_a), 1, ctypes.byref(hpa), ctypes.c_void_p(sa.cuda_stream))
+        assert st == _lib.RF_OK, lib.rf_last_error()
+    st = lib.rf_adam8_step_noalloc(tb, len(specs_b), 1, ctypes.byref(hpb), ctypes.c_void_p(sb.cuda_stream))
+    assert st == _lib.RF_OK, lib.rf_last_error()
+    torch.cuda.synchronize()
+    _same(ra, a, "stream A")
+    _same(rb, b, "stream B")
+
+
+def test_noalloc_return_time_behind_pending_work():
+    """How long the call holds the host when the stream still has work ahead
+    of it (the table copy is from pageable memory).  Measured and printed;
+    the call's results are checked as in the other tests."""
+    import time
+
+    import torch
+
+    from rollfast_amd import _lib
+
+    lib = _lib.lib()
+    specs = [(4 * BS, "bf16", "bf16", "q")]
+    a = _leaf_set(specs, 9)
+    r = _clone(a)
+    hp = _hparams(1, _lib.RF_LR, 0.0)
+    assert lib.rf_adam8_step(_table(r), 1, 1, ctypes.byref(hp), _lib.stream_ptr()) == _lib.RF_OK
+    x = torch.ones(1 << 30, device="cuda")
+    t = _table(a)
+    # warm: the first call on a stream may set up runtime state
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(8):
+        x.mul_(1.0)
+    e1.record()
+    t0 = time.perf_counter()
+    st = lib.rf_adam8_step_noalloc(t, 1, 1, ctypes.byref(_hparams(1, _lib.RF_LR, 0.0)), _lib.stream_ptr())
+    held = (time.perf_counter() - t0) * 1e3
+    t_enq = time.perf_counter()
+    torch.cuda.synchronize()
+    rest = (time.perf_counter() - t_enq) * 1e3
+    assert st == _lib.RF_OK, lib.rf_last_error()
+    pending = e0.elapsed_time(e1)
+    print(f"[no_alloc] call returned after {held:.3f} ms with {pending:.3f} ms of work ahead on the stream; "
+          f"the stream finished {rest:.3f} ms after the return", flush=True)
+    _same(r, a, "behind pending work")
