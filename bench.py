@@ -293,6 +293,7 @@ class Workload:
     def __init__(self, name, units, unit, nbytes, step, config, cpu, metric):
         self.name, self.units, self.unit, self.nbytes = name, units, unit, nbytes
         self.step, self.config, self.cpu, self.metric = step, config, cpu, metric
+        self.probe = None  # the memory ceiling of the step's byte mix, where the library can measure it
 
 
 def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax=False, adam_mu=None, clip=None,
@@ -457,6 +458,19 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
         cpu = None
     wl = Workload(workload, n_params, "params/s", nbytes, step, config, cpu, metric)
     wl.holder = holder  # params and optimizer state, for the placement study's cross pairs
+    if (shapes_fn is llama7b_shapes and adam_mu is None and not (optax or groups or guard or accum > 1)
+            and clip is None):
+        # every leaf is whole 2048-blocks: the stream probe moves the step's bytes
+        pb = 4 if pdtype == "f32" else 2
+        block_bytes = BS * (2 * pb + pb + 4) + 16
+
+        def probe():
+            from rollfast_amd import _lib
+
+            plan = tx.update.engine._last["plan"]
+            return plan.stream_probe(_lib.stream_ptr()) * block_bytes
+
+        wl.probe = probe
     return wl
 
 
@@ -745,6 +759,25 @@ def main(argv=None):
     print(f"[bench] {ms_per_step:.3f} ms/step wall, {kernel_ms_avg:.3f} ms/step events, "
           f"{achieved / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
 
+    ceiling = None
+    if wl.probe is not None:
+        # The same bytes in the same buffers, layout and grid, without the
+        # step's arithmetic: what this memory placement gives the byte mix.
+        for _ in range(2):
+            wl.probe()
+        pstart = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+        pend = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        pbytes = 0
+        for k in range(args.steps):
+            pstart[k].record()
+            pbytes = wl.probe()
+            pend[k].record()
+        torch.cuda.synchronize()
+        probe_ms = sum(s.elapsed_time(e) for s, e in zip(pstart, pend)) / args.steps
+        ceiling = pbytes / (probe_ms * 1e-3)
+        print(f"[bench] stream probe: {probe_ms:.3f} ms, {ceiling / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
+
     if args.calibrate_copy_gib > 0:
         nbytes = int(args.calibrate_copy_gib * (1 << 30))
         src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
@@ -788,6 +821,12 @@ def main(argv=None):
         },
         "cpu_baseline": cpu,
     }
+    if ceiling is not None:
+        line["roofline"]["ceiling"] = ceiling / 1e9
+        line["roofline"]["ceiling_frac"] = achieved / ceiling
+        line["roofline"]["ceiling_source"] = (
+            "rf_adam8_plan_stream_probe timed after the steps: the step's bytes, lane layout and grid over the "
+            "same buffers, no arithmetic")
     print(json.dumps(line), flush=True)
     return 0
 

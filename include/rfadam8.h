@@ -229,6 +229,18 @@ RF_API rf_status rf_adam8_plan_wait_prepass(const rf_adam8_plan* plan);
 RF_API rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64_t* leaves,
                              int64_t* units);
 
+/* Diagnostics, no reference counterpart: the memory ceiling of the plan's
+ * fused step.  Enqueues, over the plan's full-block (vectorised) work lists
+ * with the step's launch shape and lane layout and the pointers given at
+ * creation, a kernel that moves exactly the step's bytes -- reads params,
+ * grads, both code arrays and both block scales; writes the params, codes
+ * and scales back unchanged -- with no arithmetic.  Timing it beside the
+ * step gives the bandwidth the step's byte mix reaches in the same memory
+ * placement.  `blocks_out` (host, may be NULL) receives the number of
+ * 2048-element blocks moved.  Fused plans (apply != 0) only; it must not
+ * overlap a step on the same buffers. */
+RF_API rf_status rf_adam8_plan_stream_probe(const rf_adam8_plan* plan, void* stream, int64_t* blocks_out);
+
 /* Free a plan (waits for the device to be idle with respect to its tables). */
 RF_API rf_status rf_adam8_plan_destroy(rf_adam8_plan* plan);
 

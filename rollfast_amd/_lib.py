@@ -162,6 +162,7 @@ EXPORTS = (
     "rf_adam8_plan_run_leaves",
     "rf_adam8_plan_wait_prepass",
     "rf_adam8_plan_info",
+    "rf_adam8_plan_stream_probe",
     "rf_adam8_plan_destroy",
     "rf_adam8_step",
     "rf_adam8_step_noalloc",
@@ -210,6 +211,7 @@ def lib() -> ctypes.CDLL:
     L.rf_adam8_plan_run.argtypes = [_p, ctypes.POINTER(Adam8Hparams), _p]
     L.rf_adam8_plan_run_leaves.argtypes = [_p, ctypes.POINTER(Adam8Leaf), i32, ctypes.POINTER(Adam8Hparams), _p]
     L.rf_adam8_plan_info.argtypes = [_p, ctypes.POINTER(i64), ctypes.POINTER(i64), ctypes.POINTER(i64)]
+    L.rf_adam8_plan_stream_probe.argtypes = [_p, _p, ctypes.POINTER(i64)]
     L.rf_adam8_plan_destroy.argtypes = [_p]
     L.rf_adam8_step.argtypes = [ctypes.POINTER(Adam8Leaf), i32, i32, ctypes.POINTER(Adam8Hparams), _p]
     L.rf_adam8_step_noalloc.argtypes = [ctypes.POINTER(Adam8Leaf), i32, i32, ctypes.POINTER(Adam8Hparams), _p]

@@ -471,7 +471,9 @@ __device__ __forceinline__ float scale_from_absmax_bits(uint32_t amax)
 
 // ------------------------------------------------------ per-element step --
 // Bias-corrected Adam direction (adam8.py:336-362, utils.py:318-324).
-template <bool NEST, bool EXACT>
+// ER = false: eps_root is zero and its term is left out of the hardware
+// direction (v + 0 is v for every v the step forms: v >= +0 or NaN).
+template <bool NEST, bool EXACT, bool ER = true>
 __device__ __forceinline__ float adam_direction(const KHp& h, float m, float v, float g)
 {
     if constexpr (EXACT) {
@@ -489,7 +491,7 @@ __device__ __forceinline__ float adam_direction(const KHp& h, float m, float v, 
         const float den = sqrtf(vhat + h.eps_root) + h.eps;
         return mhat / den;
     } else {
-        const float sv = __builtin_amdgcn_sqrtf(v + h.er2);
+        const float sv = __builtin_amdgcn_sqrtf(ER ? v + h.er2 : v);
         if constexpr (NEST) {
             const float mhat = h.nb1 * m + h.nomb1 * g;
             return mhat * __builtin_amdgcn_rcpf(__builtin_fmaf(sv, h.rsbc2, h.eps));
@@ -1156,12 +1158,10 @@ template <int WDM>
 __device__ __forceinline__ void decay_and_scale8(const KHp& h, float (&u)[8], const float (&p)[8])
 {
     if constexpr (WDM == WD_BF16) {
+        // bf16(wd*p) as an f32 in one conversion: the pair (0, wd*p) packed
+        // puts bf16(0) = 0 in the low half
 #pragma unroll
-        for (int t = 0; t < 8; t += 2) {
-            const uint32_t w2 = pack_bf16x2_rne(h.wd16 * p[t], h.wd16 * p[t + 1]);
-            u[t] = u[t] + __uint_as_float(w2 << 16);
-            u[t + 1] = u[t + 1] + __uint_as_float(w2 & 0xFFFF0000u);
-        }
+        for (int t = 0; t < 8; ++t) u[t] = u[t] + __uint_as_float(pack_bf16x2_rne(0.0f, h.wd16 * p[t]));
     } else if constexpr (WDM == WD_F16) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) u[t] = u[t] + round_to_f16(h.wdh * p[t]);
@@ -1221,7 +1221,7 @@ __device__ __forceinline__ void issue_chunk(ChunkSlots<PT, GT>& sl, const rf_ada
 // the same leaf; its chunk 0 is loaded into slot 0 while this block is
 // requantized, so the wave keeps memory traffic in flight through the
 // arithmetic-only requantization phase.
-template <typename PT, typename GT, int WDM, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
+template <typename PT, typename GT, int WDM, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT, bool ER>
 __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
                                            ChunkSlots<PT, GT>& sl, bool have0, int64_t next_blk)
 {
@@ -1293,7 +1293,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             v[j][t] = vv;
             amf = fmaxf(amf, fabsf(mm));
             av = max(av, __float_as_uint(vv));
-            u[t] = adam_direction<NEST, IEEE_DIR>(h, mm, vv, g[t]);
+            u[t] = adam_direction<NEST, IEEE_DIR, ER>(h, mm, vv, g[t]);
         }
         decay_and_scale8<WDM>(h, u, p);
         if constexpr (APPLY) {
@@ -1393,35 +1393,42 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             const float4* sru = (const float4*)(c.lds + L_SRU);
             if (c.packed) {
                 // One block per element feeds both moments: each chunk is
-                // coded for both at once, from the same eight blocks.
+                // coded for both at once, four elements (four blocks) at a
+                // time so that few blocks' words are live.
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
                     const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
                     const uint64_t e0 = (uint64_t)(base + eo);
-                    uint32_t bm[8], bv[8], cc[8];
-                    float n[8];
+                    uint32_t wm[2], wv[2];
 #pragma unroll
-                    for (int t = 0; t < 8; ++t)
-                        threefry2x32(c.kmu0, c.kmu1, (uint32_t)((e0 + t) >> 32), (uint32_t)(e0 + t), bm[t], bv[t]);
+                    for (int hh = 0; hh < 2; ++hh) {
+                        uint32_t bm[4], bv[4], cm[4], cv[4];
+                        float nm[4], nv[4];
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) n[t] = div_by_scale(m[j][t], sm, rsm);
+                        for (int t = 0; t < 4; ++t) {
+                            const uint64_t e = e0 + 4 * hh + t;
+                            threefry2x32(c.kmu0, c.kmu1, (uint32_t)(e >> 32), (uint32_t)e, bm[t], bv[t]);
+                        }
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) cc[t] = cand_signed(c.lds, n[t]);
+                        for (int t = 0; t < 4; ++t) {
+                            nm[t] = div_by_scale(m[j][4 * hh + t], sm, rsm);
+                            nv[t] = div_by_scale(v[j][4 * hh + t], sv, rsv);
+                        }
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) cc[t] = sr_code(cbs, srs, cc[t], n[t], bm[t]);
-                    uint2 w;
-                    w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
-                    w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
-                    *(RF_GLOBAL uint2*)(mW + eo) = w;
+                        for (int t = 0; t < 4; ++t) {
+                            cm[t] = cand_signed(c.lds, nm[t]);
+                            cv[t] = cand_unsigned(c.lds, nv[t]);
+                        }
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) n[t] = div_by_scale(v[j][t], sv, rsv);
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) cc[t] = cand_unsigned(c.lds, n[t]);
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) cc[t] = sr_code(cbu, sru, cc[t], n[t], bv[t]);
-                    w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
-                    w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
-                    *(RF_GLOBAL uint2*)(vW + eo) = w;
+                        for (int t = 0; t < 4; ++t) {
+                            cm[t] = sr_code(cbs, srs, cm[t], nm[t], bm[t]);
+                            cv[t] = sr_code(cbu, sru, cv[t], nv[t], bv[t]);
+                        }
+                        wm[hh] = pack4_u8(cm[0], cm[1], cm[2], cm[3]);
+                        wv[hh] = pack4_u8(cv[0], cv[1], cv[2], cv[3]);
+                    }
+                    *(RF_GLOBAL uint2*)(mW + eo) = make_uint2(wm[0], wm[1]);
+                    *(RF_GLOBAL uint2*)(vW + eo) = make_uint2(wv[0], wv[1]);
                 }
             } else {
 #pragma unroll
@@ -1516,27 +1523,41 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
     }
 }
 
-// The vectorised block: the weight-decay mode is resolved once per unit into
-// a branch-free instance.
-template <typename PT, typename GT, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
-__device__ __forceinline__ void dispatch_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t idx, const KHp& h,
-                                               ChunkSlots<PT, GT>& sl, bool have0, int64_t next_blk)
+// The vectorised block: the weight-decay mode (and, for the hardware
+// direction, whether eps_root is zero) is resolved once per unit into a
+// branch-free instance.
+template <typename PT, typename GT, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT, bool ER>
+__device__ __forceinline__ void dispatch_qfast_wd(const UnitCtx& c, const rf_adam8_leaf& L, int64_t idx, const KHp& h,
+                                                  ChunkSlots<PT, GT>& sl, bool have0, int64_t next_blk)
 {
     const int32_t wdm = c.wd_mode;
     if constexpr (IS_BF16<PT>) {
         if (wdm == WD_BF16) {
-            unit_qfast<PT, GT, WD_BF16, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h, sl, have0, next_blk);
+            unit_qfast<PT, GT, WD_BF16, APPLY, MSR, PSR, NEST, EXACT, ER>(c, L, idx, h, sl, have0, next_blk);
             return;
         }
     }
     if constexpr (IS_F16<PT>) {
         if (wdm == WD_F16) {
-            unit_qfast<PT, GT, WD_F16, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h, sl, have0, next_blk);
+            unit_qfast<PT, GT, WD_F16, APPLY, MSR, PSR, NEST, EXACT, ER>(c, L, idx, h, sl, have0, next_blk);
             return;
         }
     }
-    if (wdm != WD_OFF) unit_qfast<PT, GT, WD_F32, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h, sl, have0, next_blk);
-    else unit_qfast<PT, GT, WD_OFF, APPLY, MSR, PSR, NEST, EXACT>(c, L, idx, h, sl, have0, next_blk);
+    if (wdm != WD_OFF) unit_qfast<PT, GT, WD_F32, APPLY, MSR, PSR, NEST, EXACT, ER>(c, L, idx, h, sl, have0, next_blk);
+    else unit_qfast<PT, GT, WD_OFF, APPLY, MSR, PSR, NEST, EXACT, ER>(c, L, idx, h, sl, have0, next_blk);
+}
+
+template <typename PT, typename GT, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
+__device__ __forceinline__ void dispatch_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t idx, const KHp& h,
+                                               ChunkSlots<PT, GT>& sl, bool have0, int64_t next_blk)
+{
+    if constexpr (!EXACT) {
+        if (h.er2 == 0.0f) {
+            dispatch_qfast_wd<PT, GT, APPLY, MSR, PSR, NEST, EXACT, false>(c, L, idx, h, sl, have0, next_blk);
+            return;
+        }
+    }
+    dispatch_qfast_wd<PT, GT, APPLY, MSR, PSR, NEST, EXACT, true>(c, L, idx, h, sl, have0, next_blk);
 }
 
 // Any block size, partial or unaligned blocks (KIND_QGEN): an update pass
@@ -2004,6 +2025,90 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
             dispatch_qfast<PT, GT, APPLY, MSR, PSR, NEST, EXACT>(c, L, sg.first + (u - sg.unit_start), hl, sl,
                                                                  have0, next_blk);
             have0 = next_blk >= 0;
+        }
+    }
+}
+
+// The memory ceiling of the fused step (diagnostics; no reference
+// counterpart): the fast kernel's work list, launch shape and lane layout,
+// every byte the step moves per 2048-element block -- params, grads, both
+// code arrays and both scales read; params, codes and scales written back
+// unchanged -- and no arithmetic.  Two chunks in flight per wave, as in the
+// step.  The empty asm statements make the loaded values opaque, so the
+// compiler neither drops the grad loads nor folds a store of a loaded
+// value into nothing.
+__device__ __forceinline__ void opaque(uint32_t& x) { __asm__ volatile("" : "+v"(x)); }
+__device__ __forceinline__ void opaque(uint2& x) { opaque(x.x); opaque(x.y); }
+__device__ __forceinline__ void opaque(uint4& x) { opaque(x.x); opaque(x.y); opaque(x.z); opaque(x.w); }
+
+template <typename PT, typename GT>
+__device__ __forceinline__ void probe_block(const rf_adam8_leaf& L, int64_t blk)
+{
+    constexpr int J = FAST_BS / 512;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int64_t base = blk * FAST_BS;
+    // (16-bit stored scales read back and stored again exactly)
+    float sm = load_scale(L.mu_scales, L.flags, blk);
+    float sv = load_scale(L.nu_scales, L.flags, blk);
+    RF_GLOBAL uint8_t* pB = (RF_GLOBAL uint8_t*)L.param + base * (int64_t)sizeof(PT);
+    RF_GLOBAL uint8_t* mW = (RF_GLOBAL uint8_t*)L.mu + base;
+    RF_GLOBAL uint8_t* vW = (RF_GLOBAL uint8_t*)L.nu + base;
+    ChunkSlots<PT, GT> sl;
+    issue_chunk<PT, GT, true>(sl, L, blk, 0, 0);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int slot = j & 1;
+        const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
+        if (j + 1 < J) issue_chunk<PT, GT, true>(sl, L, blk, j + 1, slot ^ 1);
+        uint2 mc = sl.mc[slot], vc = sl.vc[slot];
+        uint4 p0 = sl.praw[slot].w[0];
+        opaque(mc);
+        opaque(vc);
+        opaque(p0);
+        opaque(sl.graw[slot].w[0]);
+        if constexpr (sizeof(GT) == 4) opaque(sl.graw[slot].w[1]);
+        *(RF_GLOBAL uint4*)(pB + eo * sizeof(PT)) = p0;
+        if constexpr (sizeof(PT) == 4) {
+            uint4 p1 = sl.praw[slot].w[1];
+            opaque(p1);
+            *(RF_GLOBAL uint4*)(pB + eo * 4 + 16) = p1;
+        }
+        *(RF_GLOBAL uint2*)(mW + eo) = mc;
+        *(RF_GLOBAL uint2*)(vW + eo) = vc;
+    }
+    uint32_t smb = __float_as_uint(sm), svb = __float_as_uint(sv);
+    opaque(smb);
+    opaque(svb);
+    sm = __uint_as_float(smb);
+    sv = __uint_as_float(svb);
+    if (lane == 0) {
+        store_scale(L.mu_scales, L.flags, blk, sm);
+        store_scale(L.nu_scales, L.flags, blk, sv);
+    }
+}
+
+template <typename PT, typename GT>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVES_PER_EU))) void k_stream_probe(
+    const rf_adam8_leaf* __restrict__ leaves, const Seg* __restrict__ segs, int64_t total_units, int32_t run)
+{
+    const uint32_t wave_in_wg = uniform_u32(threadIdx.x / WAVE);
+    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + wave_in_wg;
+    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    int32_t s = 0;
+    const int32_t nseg = segs[0].nseg;
+    int32_t cur_leaf = -1;
+    rf_adam8_leaf L;
+    const int64_t nruns = (total_units + run - 1) / run;
+    for (int64_t r = wave; r < nruns; r += nwaves) {
+        const int64_t u_end = min(r * run + run, total_units);
+        for (int64_t u = r * run; u < u_end; ++u) {
+            s = seek_seg(segs, nseg, s, u);
+            const Seg sg = segs[s];
+            if (sg.leaf != cur_leaf) {
+                cur_leaf = sg.leaf;
+                L = leaves[cur_leaf];
+            }
+            probe_block<PT, GT>(L, sg.first + (u - sg.unit_start));
         }
     }
 }

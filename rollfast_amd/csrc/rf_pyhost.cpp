@@ -14,9 +14,11 @@
 //       at each grads leaf.  Returns None (the caller falls back to the
 //       Python walk) for any container it does not handle or any mismatch.
 //
-//   updates_out(grads, g, mu, rows, table_address) -> updates tree
+//   updates_out(grads, g, mu, rows, table_address[, cache]) -> updates tree
 //       Update-only mode: the f32 outputs of a refreshed table (one device
-//       buffer, a view per leaf) and the updates tree (see py_updates_out).
+//       buffer, a view per leaf) and the updates tree (see py_updates_out);
+//       with `cache`, the buffers of earlier calls that nothing else still
+//       references are written again instead of allocated.
 //
 //   apply_rows(params, updates) -> packed rf_apply_leaf rows and the params
 //       tree for rollfast.apply_updates (see py_apply_rows).
@@ -270,19 +272,49 @@ PyObject* rebuild(PyObject* g, PyObject* vals, Py_ssize_t& k)
     return out;
 }
 
-// updates_out(grads, lg, lm, rows, table_address) -> updates tree
+// An earlier call's output (cache entry [flat, views]) that may be written
+// again: no Python reference to its views but the entry's own, no tensor but
+// the buffer and its views on the buffer's storage (so no alias survives
+// from a tree the caller still holds), and views of the grads' shapes.
+bool reusable(PyObject* entry, PyObject* lg, PyObject* rows)
+{
+    PyObject* flat_obj = PyList_GET_ITEM(entry, 0);
+    PyObject* views = PyList_GET_ITEM(entry, 1);
+    const Py_ssize_t nrows = PyList_GET_SIZE(rows);
+    if (PyList_GET_SIZE(views) != nrows) return false;  // (the buffer object itself is never handed out)
+    const at::Tensor& flat = THPVariable_Unpack(flat_obj);
+    if (flat.storage().use_count() != 1 + nrows) return false;
+    for (Py_ssize_t j = 0; j < nrows; ++j) {
+        PyObject* v = PyList_GET_ITEM(views, j);
+        if (Py_REFCNT(v) != 1) return false;
+        const Py_ssize_t i = PyLong_AsSsize_t(PyTuple_GET_ITEM(PyList_GET_ITEM(rows, j), 0));
+        if (!THPVariable_Unpack(v).sizes().equals(THPVariable_Unpack(PyList_GET_ITEM(lg, i)).sizes())) return false;
+    }
+    return true;
+}
+
+constexpr Py_ssize_t UPDATES_CACHE = 2;  // output buffers kept for reuse (one may still be held by the caller)
+
+// updates_out(grads, lg, lm, rows, table_address[, cache]) -> updates tree
 //
 // Update-only (Optax) mode after a successful refresh(): one f32 device
 // buffer holds every row's updates (each leaf 16-byte aligned), row j's
 // `updates` pointer is set to its slice and the updates tree is the grads
 // tree with, per leaf, that slice viewed in the grad's shape, or the
 // passthrough leaf (the moment's MaskedNode / None, else the grad's).
+// `cache` (a list owned by the caller, at most UPDATES_CACHE entries
+// [flat buffer, views]): a reusable entry (see reusable()) gives its buffer
+// and view objects to this call instead of a new allocation and nrows new
+// views; a new buffer is appended to it, the oldest entry dropped.  The
+// kernel that writes the buffer again is stream-ordered after whatever read
+// it before, as with the caching allocator's reuse.
 PyObject* py_updates_out(PyObject*, PyObject* args)
 {
     PyObject *g, *lg, *lm, *rows;
+    PyObject* cache = nullptr;
     unsigned long long table_addr = 0;
-    if (!PyArg_ParseTuple(args, "OO!O!O!K", &g, &PyList_Type, &lg, &PyList_Type, &lm, &PyList_Type, &rows,
-                          &table_addr))
+    if (!PyArg_ParseTuple(args, "OO!O!O!K|O!", &g, &PyList_Type, &lg, &PyList_Type, &lm, &PyList_Type, &rows,
+                          &table_addr, &PyList_Type, &cache))
         return nullptr;
     const Py_ssize_t n = PyList_GET_SIZE(lg);
     const Py_ssize_t nrows = PyList_GET_SIZE(rows);
@@ -302,10 +334,36 @@ PyObject* py_updates_out(PyObject*, PyObject* args)
         Py_INCREF(v);
         PyList_SET_ITEM(vals, i, v);
     }
-    if (nrows > 0) {
+    PyObject* entry = nullptr;  // the cache entry this call writes (borrowed)
+    if (nrows > 0 && cache) {
+        const at::Tensor& g0 = THPVariable_Unpack(PyList_GET_ITEM(lg, PyLong_AsSsize_t(PyTuple_GET_ITEM(
+                                                                          PyList_GET_ITEM(rows, 0), 0))));
+        for (Py_ssize_t c = 0; c < PyList_GET_SIZE(cache) && !entry; ++c) {
+            PyObject* e = PyList_GET_ITEM(cache, c);
+            if (PyList_CheckExact(e) && PyList_GET_SIZE(e) == 2 && reusable(e, lg, rows) &&
+                THPVariable_Unpack(PyList_GET_ITEM(e, 0)).device() == g0.device())
+                entry = e;
+        }
+        if (entry) {
+            PyObject* views = PyList_GET_ITEM(entry, 1);
+            for (Py_ssize_t j = 0; j < nrows; ++j) {
+                const Py_ssize_t i = PyLong_AsSsize_t(PyTuple_GET_ITEM(PyList_GET_ITEM(rows, j), 0));
+                PyObject* v = PyList_GET_ITEM(views, j);
+                table[j].updates = THPVariable_Unpack(v).data_ptr<float>();
+                Py_INCREF(v);
+                PyList_SetItem(vals, i, v);
+            }
+        }
+    }
+    if (nrows > 0 && !entry) {
         const at::Tensor& g0 = THPVariable_Unpack(PyList_GET_ITEM(lg, PyLong_AsSsize_t(PyTuple_GET_ITEM(
                                                                           PyList_GET_ITEM(rows, 0), 0))));
         at::Tensor flat = at::empty({total}, g0.options().dtype(at::kFloat));
+        PyObject* views = cache ? PyList_New(nrows) : nullptr;
+        if (cache && !views) {
+            Py_DECREF(vals);
+            return nullptr;
+        }
         for (Py_ssize_t j = 0; j < nrows; ++j) {
             const Py_ssize_t i = PyLong_AsSsize_t(PyTuple_GET_ITEM(PyList_GET_ITEM(rows, j), 0));
             const at::Tensor& gi = THPVariable_Unpack(PyList_GET_ITEM(lg, i));
@@ -313,10 +371,34 @@ PyObject* py_updates_out(PyObject*, PyObject* args)
             table[j].updates = view.data_ptr<float>();
             PyObject* obj = THPVariable_Wrap(std::move(view));
             if (!obj) {
+                Py_XDECREF(views);
                 Py_DECREF(vals);
                 return nullptr;
             }
+            if (views) {
+                Py_INCREF(obj);
+                PyList_SET_ITEM(views, j, obj);
+            }
             PyList_SetItem(vals, i, obj);  // steals obj, drops the passthrough placeholder
+        }
+        if (cache) {
+            PyObject* flat_obj = THPVariable_Wrap(std::move(flat));
+            PyObject* e = flat_obj ? PyList_New(2) : nullptr;
+            if (!e) {
+                Py_XDECREF(flat_obj);
+                Py_DECREF(views);
+                Py_DECREF(vals);
+                return nullptr;
+            }
+            PyList_SET_ITEM(e, 0, flat_obj);
+            PyList_SET_ITEM(e, 1, views);
+            if (PyList_Append(cache, e) < 0 ||
+                (PyList_GET_SIZE(cache) > UPDATES_CACHE && PySequence_DelItem(cache, 0) < 0)) {
+                Py_DECREF(e);
+                Py_DECREF(vals);
+                return nullptr;
+            }
+            Py_DECREF(e);
         }
     }
     Py_ssize_t k = 0;

@@ -480,6 +480,15 @@ class _LeafPlan:
     def wait_prepass(self):
         _lib.check(_lib.lib().rf_adam8_plan_wait_prepass(self.handle), "rf_adam8_plan_wait_prepass")
 
+    def stream_probe(self, stream) -> int:
+        """Enqueue the plan's stream probe (the fused step's bytes, no
+        arithmetic) over its creation-time buffers; returns the 2048-element
+        blocks it moves."""
+        blocks = ctypes.c_int64(0)
+        _lib.check(_lib.lib().rf_adam8_plan_stream_probe(self.handle, stream, ctypes.byref(blocks)),
+                   "rf_adam8_plan_stream_probe")
+        return int(blocks.value)
+
     def __del__(self):
         h = getattr(self, "handle", None)
         if h is not None and h.value:
@@ -820,9 +829,10 @@ class _Engine:
             addr = ctypes.addressof(last["table"])
             if lists is not None and host.refresh(*lists, last["refs"], addr, last["device"].index):
                 out_tree = None
-                if not apply:  # f32 outputs: one buffer, a view per leaf
+                if not apply:  # f32 outputs: one buffer, a view per leaf (reused once nothing holds it)
                     with torch.cuda.device(last["device"]):
-                        out_tree = host.updates_out(updates, lists[0], lists[1], last["refs"], addr)
+                        out_tree = host.updates_out(updates, lists[0], lists[1], last["refs"], addr,
+                                                    last.setdefault("ucache", []))
                 self._launch(last["table"], last["n"], last["device"], last["plan"], count_inc, key_mu, key_nu,
                              apply=apply, decay_mask=decay_mask, weight_decay=weight_decay, neg_lr=neg_lr,
                              param_key=param_key, param_sr=param_sr, random_bits=None,

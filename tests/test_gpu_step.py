@@ -131,14 +131,14 @@ def _compare_params(spec, tree, dev_params, exact, what, before):
 
 
 def _run(spec, *, steps=3, exact=False, block_size=2048, min_size=4096, wd=0.01, lr=1e-3, msr=False,
-         psr=False, nesterov=False, fallback=None, seed=0, eps_root=0.0):
+         psr=False, nesterov=False, fallback=None, seed=0, eps_root=0.0, key=None):
     import torch
 
     rf = _rf()
     host_params, params = _build(spec, seed)
     tx = rf.adamw8(learning_rate=lr, weight_decay=wd, block_size=block_size, min_size=min_size,
                    stochastic_rounding=msr, nesterov=nesterov, exact=exact, eps_root=eps_root,
-                   fallback_dtype=fallback, key=rf.prng.PRNGKey(7))
+                   fallback_dtype=fallback, key=rf.prng.PRNGKey(7) if key is None else key)
     state = tx.init(params)
     for step in range(steps):
         ghost, gdev = _grads(spec, seed + 1000 + step)
@@ -243,6 +243,14 @@ def test_weight_decay_schedule():
     value multiplies the params in f32 (bf16 params included)."""
     sched = lambda c: 0.05 / (1.0 + np.float32(c))  # noqa: E731
     _run(MIXED, steps=3, wd=sched, exact=True)
+
+
+def test_fold_in_group_key_drives_moment_sr():
+    """adamw8(key=jax.random.fold_in(root, index)), the fine-tune builders'
+    per-group key (finetune/builders.py:1582), with moment and param
+    stochastic rounding: the in-kernel bits follow that key's stream."""
+    rf = _rf()
+    _run(MIXED, steps=2, msr=True, psr=True, exact=True, key=rf.prng.fold_in(rf.prng.PRNGKey(1234), 3))
 
 
 def test_fast_direction_over_twenty_steps():
