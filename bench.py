@@ -740,20 +740,20 @@ def main(argv=None):
         wl.step()
     torch.cuda.synchronize()
 
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    # One event pair around the timed steps (on the launch stream): markers
+    # between steps would add idle gaps of their own to short steps.
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     print(f"[bench] timing {args.steps} steps", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    start.record()
     for k in range(args.steps):
-        starts[k].record()
         wl.step()
-        ends[k].record()
+    end.record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_per_step = (t1 - t0) * 1e3 / args.steps
-    kernel_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    kernel_ms_avg = sum(kernel_ms) / len(kernel_ms)
+    kernel_ms_avg = start.elapsed_time(end) / args.steps
     achieved = wl.nbytes / (kernel_ms_avg * 1e-3)
     value = wl.units / (ms_per_step * 1e-3)
     print(f"[bench] {ms_per_step:.3f} ms/step wall, {kernel_ms_avg:.3f} ms/step events, "
@@ -765,16 +765,15 @@ def main(argv=None):
         # step's arithmetic: what this memory placement gives the byte mix.
         for _ in range(2):
             wl.probe()
-        pstart = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-        pend = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+        pstart, pend = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         pbytes = 0
+        pstart.record()
         for k in range(args.steps):
-            pstart[k].record()
             pbytes = wl.probe()
-            pend[k].record()
+        pend.record()
         torch.cuda.synchronize()
-        probe_ms = sum(s.elapsed_time(e) for s, e in zip(pstart, pend)) / args.steps
+        probe_ms = pstart.elapsed_time(pend) / args.steps
         ceiling = pbytes / (probe_ms * 1e-3)
         print(f"[bench] stream probe: {probe_ms:.3f} ms, {ceiling / 1e9:.1f} GB/s", file=sys.stderr, flush=True)
 

@@ -1126,6 +1126,12 @@ namespace {
 // recorded after the call's last launch guards its next use, and a slot is
 // held by one call at a time.  Steady-state calls allocate nothing.
 constexpr int STAGE_RING = 4;
+// Events that only order work -- the host waits on them before it reuses a
+// table buffer, or another stream waits on them -- and guard no data the
+// host reads: no timing and no system-scope release (no cache writeback
+// between steps).  The pre-pass event, which guards the finite flag's copy
+// to host memory, keeps the default fences.
+constexpr unsigned ORDER_EVENT_FLAGS = hipEventDisableTiming | hipEventDisableSystemFence;
 struct StageSlot {
     std::mutex mu;  // held from acquire to release
     uint8_t* host = nullptr;
@@ -1170,7 +1176,7 @@ public:
             HIP_TRY(hipEventSynchronize(slot_->ev));
             slot_->pending = false;
         }
-        if (!slot_->ev) HIP_TRY(hipEventCreateWithFlags(&slot_->ev, hipEventDisableTiming));
+        if (!slot_->ev) HIP_TRY(hipEventCreateWithFlags(&slot_->ev, ORDER_EVENT_FLAGS));
         host_bytes = std::max<size_t>(host_bytes, 256);
         dev_bytes = std::max<size_t>(dev_bytes, host_bytes);
         if (slot_->host_cap < host_bytes) {
@@ -1243,7 +1249,7 @@ rf_status device_state(DevState** out)
         HIP_TRY(hipGetSymbolAddress((void**)&d.scratch_ptr, HIP_SYMBOL(scratch)));
         if (!d.tables || !d.search || !d.scratch_ptr)
             return fail(RF_ERR_HIP, "hipGetSymbolAddress returned a null address");
-        HIP_TRY(hipEventCreateWithFlags(&d.noalloc_ev, hipEventDisableTiming));
+        HIP_TRY(hipEventCreateWithFlags(&d.noalloc_ev, ORDER_EVENT_FLAGS));
         HIP_TRY(hipMemcpy(d.tables, ht.bytes.data(), TABLE_BYTES, hipMemcpyHostToDevice));
         HIP_TRY(hipMemcpy(d.search, hs.bytes.data(), SEARCH_BYTES, hipMemcpyHostToDevice));
         d.ready = true;
@@ -1747,7 +1753,7 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
     for (RingSlot& slot : p->ring) {
         if (e == hipSuccess) e = hipHostMalloc((void**)&slot.host, slot_bytes, hipHostMallocDefault);
         if (e == hipSuccess) e = hipMalloc((void**)&slot.dev, slot_bytes);
-        if (e == hipSuccess) e = hipEventCreateWithFlags(&slot.ev, hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&slot.ev, ORDER_EVENT_FLAGS);
     }
     if (e == hipSuccess) e = hipMalloc(&p->d_nsegs, sizeof(Seg) * nsegs.size());
     if (e == hipSuccess) e = hipMalloc(&p->d_npart, sizeof(double) * (size_t)std::max<int64_t>(nunits, 1));
