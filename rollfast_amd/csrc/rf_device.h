@@ -32,6 +32,22 @@
 #include "../../include/rfadam8.h"
 #include "rf_tables.h"
 
+// Global-address-space views of the leaf's buffers.  The leaf table holds
+// generic pointers, and an access through one compiles to a flat
+// instruction, which counts against lgkmcnt as well as vmcnt: every later
+// wait for an LDS read or a scalar load then also waits for the flat loads
+// and stores in flight, and the element paths' batches of loads serialise.
+// Through these views they compile to global_load/global_store, counted
+// only by vmcnt.
+// RF_LDS: the LDS address space (the DMA loads' destination operand).
+#if defined(__HIP_DEVICE_COMPILE__)
+#define RF_GLOBAL __attribute__((address_space(1)))
+#define RF_LDS __attribute__((address_space(3)))
+#else
+#define RF_GLOBAL
+#define RF_LDS
+#endif
+
 namespace rf {
 
 constexpr int WAVE = 64;
@@ -84,6 +100,12 @@ struct KHp {
     // mpart[3 * (msegs[leaf].unit_start + chunk)].
     double* mpart;
     const Seg* msegs;
+    // Learning-rate-folded direction of the fast kernel's nearest-rounding
+    // bf16 step (device-derived by flr_setup, not set by the host):
+    // k1l = k1 / neg_lr, k2l = k2 / neg_lr, wdl = neg_lr * bf16(wd) and
+    // flr = 1 where those are in range for the one-ulp bound.
+    float k1l, k2l, wdl;
+    int32_t flr;
 };
 
 // Work list: unit u belongs to the segment s with
@@ -329,22 +351,48 @@ __device__ __forceinline__ double wave_sum_f64(double x)
     return x;
 }
 
-// Copies the first BYTES of a table image into the workgroup's LDS.  Every
-// load of a thread is issued before its first LDS write, so a workgroup's
-// start waits for one memory latency instead of one per 4 KB of tables.
+// Copies the first BYTES of a table image into the workgroup's LDS.
+// Up to the 22 KB requantization tables: through registers, every load of a
+// thread issued before its first LDS write, so a workgroup's start waits for
+// one memory latency.  The 30 KB search image of moment-SR launches: through
+// the LDS-DMA form of the global load (global_load_lds_dwordx4, gfx950),
+// each lane's 16 bytes going from global memory straight to LDS at the
+// instruction's LDS base + 16 * lane; a wave moves 1 KB per instruction, the
+// waves take the 1 KB pieces in turn, the last piece's lanes past BYTES
+// masked off.  The register form of that image held 32 VGPRs at the
+// kernel's start, where the compiler spilled them (28 KB of scratch writes
+// per workgroup); with the DMA form the moment-SR step ran 1 % faster, while
+// the nearest-rounding step measured 0.3 % slower with it than with
+// registers (same box, alternating runs).
 template <uint32_t BYTES = TABLE_BYTES>
 __device__ __forceinline__ void stage_tables(uint8_t* lds, const uint4* __restrict__ tables)
 {
-    constexpr uint32_t N = BYTES / 16;
-    constexpr uint32_t FULL = N / WG, REM = N % WG;  // whole rounds of the workgroup, then a partial one
-    uint4* dst = (uint4*)lds;
-    uint4 t[FULL + 1];
+    static_assert(BYTES % 16 == 0, "tables are copied in 16-byte words");
+    if constexpr (BYTES > TABLE_BYTES) {
+        constexpr uint32_t PIECE = WAVE * 16;
+        constexpr uint32_t NPIECE = (BYTES + PIECE - 1) / PIECE;
+        const uint32_t wave = uniform_u32(threadIdx.x / WAVE);
+        const uint32_t lane16 = (threadIdx.x & (WAVE - 1)) * 16u;
+        const RF_GLOBAL uint8_t* src = (const RF_GLOBAL uint8_t*)tables;
+        for (uint32_t k = wave; k < NPIECE; k += WAVES_PER_WG) {
+            const uint32_t base = k * PIECE;
+            if (base + lane16 < BYTES)
+                __builtin_amdgcn_global_load_lds((const RF_GLOBAL void*)(src + base + lane16),
+                                                 (RF_LDS void*)(lds + base), 16, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0): the DMA writes have reached LDS
+    } else {
+        constexpr uint32_t N = BYTES / 16;
+        constexpr uint32_t FULL = N / WG, REM = N % WG;  // whole rounds of the workgroup, then a partial one
+        uint4* dst = (uint4*)lds;
+        uint4 t[FULL + 1];
 #pragma unroll
-    for (uint32_t k = 0; k < FULL; ++k) t[k] = tables[threadIdx.x + k * WG];
-    if (REM && threadIdx.x < REM) t[FULL] = tables[threadIdx.x + FULL * WG];
+        for (uint32_t k = 0; k < FULL; ++k) t[k] = tables[threadIdx.x + k * WG];
+        if (REM && threadIdx.x < REM) t[FULL] = tables[threadIdx.x + FULL * WG];
 #pragma unroll
-    for (uint32_t k = 0; k < FULL; ++k) dst[threadIdx.x + k * WG] = t[k];
-    if (REM && threadIdx.x < REM) dst[threadIdx.x + FULL * WG] = t[FULL];
+        for (uint32_t k = 0; k < FULL; ++k) dst[threadIdx.x + k * WG] = t[k];
+        if (REM && threadIdx.x < REM) dst[threadIdx.x + FULL * WG] = t[FULL];
+    }
     __syncthreads();
 }
 
@@ -564,6 +612,45 @@ __device__ __forceinline__ bool rne_bf16_settled(float s, float upd, float p, fl
     return fabsf(s - mid) > b && b < fabsf(s) * 0x1p-10f && fabsf(upd) < c_g;
 }
 
+// The learning-rate-folded step (fast kernel, bf16 params, nearest
+// rounding, hardware direction, eps_root = 0, no Nesterov).  The reference
+// forms p + (-lr) * (m / (sqrt(v/bc2) + eps) / bc1 + bf16(wd * p)) with a
+// rounding after every operation (adam8.py:322-339, optax
+// add_decayed_weights and scale_by_learning_rate, apply_updates).  With
+// D' = sqrt(v) * k1l + k2l (k1l = k1 / -lr, k2l = k2 / -lr) and
+// wdl = -lr * bf16(wd) the same quantity is
+//   s = fma(m, rcp(D'), fma(wdl, p, p)),
+// five instructions per element where the unfolded form takes nine.  Bound
+// against the reference's f32 sum s_ref, for |p| <= 1024 |s| (elements
+// beyond that nearly cancel and are recomputed with IEEE arithmetic):
+// the direction term is within about 2^-20 of |lr a| relative (k1l, k2l,
+// v_sqrt, the FMA, v_rcp, the product: seven roundings of at most one f32
+// ulp, against the reference's 2.5 ulp quotient and two roundings), and
+// |lr a| <= |s| + |p| + |lr wd p| <= 1026 |s|; the decay term differs by the
+// reference's bf16 rounding of wd * p, at most 2^-8 |wd p|, which with
+// |lr wd| <= 2^-14 is below 2^-12 |s|; fma(wdl, p, p) and the final FMA
+// round twice more (2^-24 |p| + 2^-24 |s|).  In all |s - s_ref| < 2^-9.5 |s|,
+// below half a bf16 ulp of s (a bf16 ulp exceeds 2^-8 |s|), so nearest-even
+// and stochastic rounding of s and s_ref land at most one bf16 ulp apart.
+// flr_setup derives the constants and clears flr where they leave that
+// range (lr = 0, non-finite or extreme k1l or k2l, |lr wd| > 2^-14).
+constexpr float FLR_CANCEL = 1024.0f;
+
+__device__ __forceinline__ void flr_setup(KHp& h)
+{
+    const float k1l = h.k1 / h.neg_lr;
+    const float k2l = h.k2 / h.neg_lr;
+    const float wdl = h.neg_lr * h.wd16;
+    h.k1l = k1l;
+    h.k2l = k2l;
+    h.wdl = wdl;
+    const float a1 = fabsf(k1l), a2 = fabsf(k2l);
+    h.flr = (a1 >= 0x1p-100f && a1 <= 0x1p63f && (a2 == 0.0f || (a2 >= 0x1p-100f && a2 <= 0x1p63f)) &&
+             fabsf(wdl) <= 0x1p-14f)
+                ? 1
+                : 0;
+}
+
 // Active lanes where any of 8 sums nearly cancels: each compare's lane mask
 // is OR-ed in scalar registers, with no per-lane flag materialised.
 __device__ __forceinline__ uint64_t cancel_lanes8(const float (&sum)[8], const float (&u)[8])
@@ -586,18 +673,6 @@ __device__ __forceinline__ void ema(const KHp& h, float mp, float vp, float g, f
     v = t3 + t4;
 }
 
-// Global-address-space views of the leaf's buffers.  The leaf table holds
-// generic pointers, and an access through one compiles to a flat
-// instruction, which counts against lgkmcnt as well as vmcnt: every later
-// wait for an LDS read or a scalar load then also waits for the flat loads
-// and stores in flight, and the element paths' batches of loads serialise.
-// Through these views they compile to global_load/global_store, counted
-// only by vmcnt.
-#if defined(__HIP_DEVICE_COMPILE__)
-#define RF_GLOBAL __attribute__((address_space(1)))
-#else
-#define RF_GLOBAL
-#endif
 
 template <typename T>
 __device__ __forceinline__ const RF_GLOBAL T* gload_ptr(const void* p, int64_t byte_off)
@@ -1221,10 +1296,13 @@ __device__ __forceinline__ void issue_chunk(ChunkSlots<PT, GT>& sl, const rf_ada
 // the same leaf; its chunk 0 is loaded into slot 0 while this block is
 // requantized, so the wave keeps memory traffic in flight through the
 // arithmetic-only requantization phase.
-template <typename PT, typename GT, int WDM, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT, bool ER>
+template <typename PT, typename GT, int WDM, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT, bool ER,
+          bool FLR = false>
 __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
                                            ChunkSlots<PT, GT>& sl, bool have0, int64_t next_blk)
 {
+    static_assert(!FLR || (APPLY && IS_BF16<PT> && !NEST && !EXACT && !ER && (WDM == WD_BF16 || WDM == WD_OFF)),
+                  "the learning-rate-folded step covers fused bf16 nearest or SR steps of the hardware direction");
     constexpr int J = FAST_BS / 512;
     constexpr bool NEED_P = APPLY || WDM != WD_OFF;
     constexpr bool H16P = sizeof(PT) == 2;  // bf16 or f16 params
@@ -1279,7 +1357,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
 #pragma unroll
             for (int t = 0; t < 8; ++t) p[t] = 0.0f;
         }
-        float u[8];
+        float u[8], sum[8];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const uint32_t cm = ((t < 4 ? sl.mc[slot].x : sl.mc[slot].y) >> (8 * (t & 3))) & 0xFFu;
@@ -1293,13 +1371,40 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             v[j][t] = vv;
             amf = fmaxf(amf, fabsf(mm));
             av = max(av, __float_as_uint(vv));
-            u[t] = adam_direction<NEST, IEEE_DIR, ER>(h, mm, vv, g[t]);
+            if constexpr (FLR) {
+                const float rr = __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_amdgcn_sqrtf(vv), h.k1l, h.k2l));
+                const float pd = WDM == WD_BF16 ? __builtin_fmaf(h.wdl, p[t], p[t]) : p[t];
+                sum[t] = __builtin_fmaf(mm, rr, pd);
+            } else {
+                u[t] = adam_direction<NEST, IEEE_DIR, ER>(h, mm, vv, g[t]);
+            }
         }
-        decay_and_scale8<WDM>(h, u, p);
-        if constexpr (APPLY) {
-            float sum[8];
+        if constexpr (!FLR) decay_and_scale8<WDM>(h, u, p);
+        if constexpr (FLR) {
+            // |p| > FLR_CANCEL |s|: the sum nearly cancels the param, where
+            // the folded form's few-ulp error could exceed half a bf16 ulp of
+            // s; those elements take the IEEE direction and the reference's
+            // operation order.  fma(-C, |s|, |p|) > 0 is that test exactly
+            // (NaN never passes), its maximum over the chunk one compare.
+            float dmax = __builtin_fmaf(-FLR_CANCEL, fabsf(sum[0]), fabsf(p[0]));
 #pragma unroll
-            for (int t = 0; t < 8; ++t) sum[t] = p[t] + u[t];
+            for (int t = 1; t < 8; ++t) dmax = fmaxf(dmax, __builtin_fmaf(-FLR_CANCEL, fabsf(sum[t]), fabsf(p[t])));
+            if (__builtin_amdgcn_ballot_w64(dmax > 0.0f) != 0) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    if (__builtin_fmaf(-FLR_CANCEL, fabsf(sum[t]), fabsf(p[t])) > 0.0f) {
+                        float ue = adam_direction<NEST, true>(h, m[j][t], v[j][t], g[t]);
+                        ue = decay_and_scale(h, ue, p[t], WDM);
+                        sum[t] = p[t] + ue;
+                    }
+                }
+            }
+        }
+        if constexpr (APPLY) {
+            if constexpr (!FLR) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) sum[t] = p[t] + u[t];
+            }
             if constexpr (SETTLE) {
                 const float wd_eff = WDM == WD_BF16 ? h.wd16 : (WDM == WD_F32 ? h.wd : (WDM == WD_F16 ? h.wdh : 0.0f));
                 const float c_w = fabsf(h.neg_lr * wd_eff) * 0x1p-17f;
@@ -1318,7 +1423,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                     }
                 }
             }
-            if constexpr (!EXACT) {
+            if constexpr (!EXACT && !FLR) {
                 // Hardware rcp/sqrt leave u a few f32 ulps from the IEEE
                 // value; that moves the rounded param by more than one
                 // bf16 ulp only where p + u nearly cancels.  Such chunks
@@ -1531,6 +1636,18 @@ __device__ __forceinline__ void dispatch_qfast_wd(const UnitCtx& c, const rf_ada
                                                   ChunkSlots<PT, GT>& sl, bool have0, int64_t next_blk)
 {
     const int32_t wdm = c.wd_mode;
+    if constexpr (APPLY && IS_BF16<PT> && !NEST && !EXACT && !ER) {
+        if (h.flr) {
+            if (wdm == WD_BF16) {
+                unit_qfast<PT, GT, WD_BF16, APPLY, MSR, PSR, NEST, EXACT, ER, true>(c, L, idx, h, sl, have0, next_blk);
+                return;
+            }
+            if (wdm == WD_OFF) {
+                unit_qfast<PT, GT, WD_OFF, APPLY, MSR, PSR, NEST, EXACT, ER, true>(c, L, idx, h, sl, have0, next_blk);
+                return;
+            }
+        }
+    }
     if constexpr (IS_BF16<PT>) {
         if (wdm == WD_BF16) {
             unit_qfast<PT, GT, WD_BF16, APPLY, MSR, PSR, NEST, EXACT, ER>(c, L, idx, h, sl, have0, next_blk);
@@ -2000,6 +2117,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     c.kmu0 = c.kmu1 = c.knu0 = c.knu1 = c.kp0 = c.kp1 = 0;
     rf_adam8_leaf L;
     KHp hl = h;  // the current leaf's scalars (its group's, in a grouped launch)
+    flr_setup(hl);
     ChunkSlots<PT, GT> sl;
     bool have0 = false;  // slot 0 holds chunk 0 of unit u
     // Wave w takes runs of h.run consecutive units: run r = w, w + nwaves, ...
@@ -2013,7 +2131,10 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
             if (sg.leaf != cur_leaf) {
                 cur_leaf = sg.leaf;
                 L = leaves[cur_leaf];
-                group_hparams(hl, h, L);
+                if (h.groups != nullptr) {
+                    group_hparams(hl, h, L);
+                    flr_setup(hl);
+                }
                 leaf_context<true>(c, L, hl, MSR, PSR);
             }
             // The next unit of this wave, when it is a block of the same leaf
@@ -2136,7 +2257,12 @@ void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
     __shared__ uint32_t red[2 * WAVES_PER_WG];  // absmax bits of a workgroup's block, per wave
-    if (!VEC_ONLY && tables) stage_tables(lds, tables);  // null: the list has no quantized units
+    // The list's leading quantized units go to workgroups blockIdx.x,
+    // blockIdx.x + gridDim.x, ...: only workgroups below nlead code a block,
+    // and only they stage the tables (null: the list has no quantized units).
+    // The others (element-wise units of small leaves) start at once.
+    const int64_t nlead = VEC_ONLY ? 0 : segs[0].lead;
+    if (!VEC_ONLY && tables && (int64_t)blockIdx.x < nlead) stage_tables(lds, tables);
 
     const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
     const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
@@ -2164,7 +2290,6 @@ void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
     // long ones), a workgroup each; then the rest a wave each, handed out
     // from the grid's last waves down so that the workgroups of the first
     // phase take none when the grid covers every unit.
-    const int64_t nlead = VEC_ONLY ? 0 : segs[0].lead;
     for (int64_t q = blockIdx.x; q < nlead; q += gridDim.x) {
         s = seek_seg(segs, nseg, s, q);
         const Seg sg = segs[s];

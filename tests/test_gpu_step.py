@@ -258,6 +258,44 @@ def test_fast_direction_over_twenty_steps():
     _run(spec, steps=20, exact=False)
 
 
+@pytest.mark.parametrize("lr_ulps", [0, 3, -3, 6])
+def test_folded_step_where_updates_cancel_params(lr_ulps):
+    """The default direction folds -lr into the reciprocal and the decay
+    into the param (s = fma(m, rcp(D'), fma(wdl, p, p))).  On the first step
+    u ~ sign(g), so params of magnitude lr nearly cancel: with
+    lr = 2^-7 (1 - k 2^-11) and |p| = 2^-7, |p + U| / |p| is about k 2^-11,
+    on either side of the 2^-10 bound past which the kernel recomputes an
+    element with IEEE arithmetic (k = 0: about 1e-4, recomputed; k = 3, 6:
+    kept, where the folded form's error is largest relative to the sum;
+    k = -3: the sum changes sign).  Half the params are ordinary.  Codes and
+    scales bit-exact, params within one bf16 ulp."""
+    import torch
+
+    rf = _rf()
+    spec = [((64, 2048), "bf16", "bf16")]
+    lr = float(np.float32(2.0 ** -7 * (1.0 - lr_ulps * 2.0 ** -11)))
+    ghost, gdev = _grads(spec, 4242)
+    g = bf16_to_f32(ghost[0])
+    rng = np.random.default_rng(11)
+    p = gaussian(rng, g.shape, 0.02)
+    half = np.arange(g.size) % 2 == 0
+    p[half] = np.where(g[half] >= 0, 2.0 ** -7, -(2.0 ** -7))
+    host = {"l000": bf16_bits(p)}
+    params = {"l000": to_device(host["l000"], "bf16").reshape(spec[0][0])}
+    tx = rf.adamw8(learning_rate=lr, weight_decay=0.01, key=rf.prng.PRNGKey(7))
+    state = tx.init(params)
+    tree = _oracle_from_state(spec, host, state[0])
+    before = [L["param"].copy() for L in tree.leaves]
+    tree.step(ghost, weight_decay=0.01, lr=lr, count=1)
+    want = bf16_to_f32(tree.leaves[0]["param"])
+    ratio = np.abs(want[half]) / 2.0 ** -7
+    assert np.median(ratio) < 2.0 ** -8, "the constructed params must nearly cancel"
+    params, state = rf.adamw8_step(tx, params, gdev, state, stochastic=False)
+    torch.cuda.synchronize()
+    _compare_state(spec, tree, state[0], f"lr_ulps {lr_ulps}")
+    _compare_params(spec, tree, params, False, f"lr_ulps {lr_ulps}", before)
+
+
 # ---------------------------------------------------------- Optax mode --
 def _optax_mode(spec, *, adamw, exact, seed=3):
     import torch
