@@ -225,7 +225,10 @@ RF_API rf_status rf_adam8_plan_run_leaves(rf_adam8_plan* plan, const rf_adam8_le
  * (an empty run never writes finite_host). */
 RF_API rf_status rf_adam8_plan_wait_prepass(const rf_adam8_plan* plan);
 
-/* Number of kernel launches, leaves and 2048-element work units of a plan. */
+/* Number of step-kernel launches, leaves and work units of a plan.  A plan
+ * with full blocks of bf16 params and grads launches its generic units
+ * (partial blocks, small leaves) inside that launch: one launch for such a
+ * tree, one more per other (param, grad) dtype pair with full blocks. */
 RF_API rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64_t* leaves,
                              int64_t* units);
 

@@ -106,6 +106,11 @@ struct KHp {
     // flr = 1 where those are in range for the one-ulp bound.
     float k1l, k2l, wdl;
     int32_t flr;
+    // A generic list riding along with a bf16/bf16 fast launch: its first
+    // gwgs workgroups run gen_list over gsegs (gunits units); 0 = none.
+    const Seg* gsegs;
+    int64_t gunits;
+    int32_t gwgs;
 };
 
 // Work list: unit u belongs to the segment s with
@@ -2080,9 +2085,23 @@ __device__ void reject_units(const rf_adam8_leaf* __restrict__ leaves, const Seg
 
 __device__ __forceinline__ bool gate_rejects(const KHp& h) { return h.gate != nullptr && gld<float>(h.gate, 0) == 0.0f; }
 
+template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT, bool VEC_ONLY>
+__device__ __forceinline__ void gen_list(const rf_adam8_leaf* __restrict__ leaves, const Seg* __restrict__ segs,
+                                         int64_t total_units, const KHp& h, const uint4* __restrict__ tables,
+                                         uint8_t* lds, uint32_t* red, uint32_t bid, uint32_t nbid);
+
 // Full 2048-element blocks of the leaves whose (param, grad) dtypes are
 // (PT, GT) (uint16_t = bf16, float = f32): the hot kernel.  Waves walk the
-// work list with a grid stride of one block per wave.
+// work list with a grid stride of one block per wave.  The bf16/bf16
+// instances without moment SR also carry a step's generic list (partial
+// blocks, small leaves) in their first h.gwgs workgroups (CARRIES_GEN), so
+// that a tree of such leaves is one launch and the generic units'
+// latency-bound work overlaps the blocks' streaming instead of running as a
+// kernel of its own before them.  (With moment SR the added code made the
+// compiler spill in the block path: 194 scratch instructions against 11.)
+template <typename PT, typename GT, bool MSR>
+constexpr bool CARRIES_GEN = IS_BF16<PT> && IS_BF16<GT> && !MSR;
+
 template <typename PT, typename GT, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT>
 __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVES_PER_EU))) void k_adam8(
     const rf_adam8_leaf* __restrict__ leaves, const Seg* __restrict__ segs, int64_t total_units, KHp h,
@@ -2092,11 +2111,24 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     constexpr uint32_t LDS_TABLES = MSR ? SEARCH_BYTES : TABLE_BYTES;
     __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_TABLES];
     __shared__ __attribute__((aligned(16))) float wtab[WAVES_PER_WG][512];
+    uint32_t bid = blockIdx.x, nbid = gridDim.x;
+    if constexpr (CARRIES_GEN<PT, GT, MSR>) {
+        const uint32_t gw = (uint32_t)h.gwgs;
+        if (bid < gw) {
+            // the generic units do not use the per-wave tables: their
+            // workgroup absmax words take the first of them
+            gen_list<APPLY, MSR, PSR, NEST, EXACT, false>(leaves, h.gsegs, h.gunits, h, tables, lds,
+                                                          (uint32_t*)&wtab[0][0], bid, gw);
+            return;
+        }
+        bid -= gw;
+        nbid -= gw;
+    }
     stage_tables<LDS_TABLES>(lds, tables);
 
     const uint32_t wave_in_wg = uniform_u32(threadIdx.x / WAVE);
-    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + wave_in_wg;
-    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    const int64_t wave = (int64_t)bid * WAVES_PER_WG + wave_in_wg;
+    const int64_t nwaves = (int64_t)nbid * WAVES_PER_WG;
     int32_t s = 0;
     const int32_t nseg = segs[0].nseg;
     int32_t cur_leaf = -1;
@@ -2249,23 +2281,24 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
 template <bool MSR, bool PSR, bool NEST, bool VEC_ONLY>
 constexpr int GEN_WAVES_PER_EU = (VEC_ONLY || MSR || PSR || NEST) ? 1 : 4;
 
-template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT, bool VEC_ONLY = false>
-__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(GEN_WAVES_PER_EU<MSR, PSR, NEST, VEC_ONLY>)))
-void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
-                                                  const Seg* __restrict__ segs, int64_t total_units, KHp h,
-                                                  const uint4* __restrict__ tables)
+// The generic list's units over workgroups bid = 0 .. nbid - 1 of a launch:
+// the generic kernel's whole grid, or the leading workgroups of a fast
+// launch the list rides along with (k_adam8, KHp.gsegs).  `lds` holds at
+// least TABLE_BYTES; `red` is 8 words of LDS.
+template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT, bool VEC_ONLY>
+__device__ __forceinline__ void gen_list(const rf_adam8_leaf* __restrict__ leaves, const Seg* __restrict__ segs,
+                                         int64_t total_units, const KHp& h, const uint4* __restrict__ tables,
+                                         uint8_t* lds, uint32_t* red, uint32_t bid, uint32_t nbid)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
-    __shared__ uint32_t red[2 * WAVES_PER_WG];  // absmax bits of a workgroup's block, per wave
-    // The list's leading quantized units go to workgroups blockIdx.x,
-    // blockIdx.x + gridDim.x, ...: only workgroups below nlead code a block,
-    // and only they stage the tables (null: the list has no quantized units).
-    // The others (element-wise units of small leaves) start at once.
+    // The list's leading quantized units go to workgroups bid, bid + nbid,
+    // ...: only workgroups below nlead code a block, and only they stage the
+    // tables (null: the list has no quantized units).  The others
+    // (element-wise units of small leaves) start at once.
     const int64_t nlead = VEC_ONLY ? 0 : segs[0].lead;
-    if (!VEC_ONLY && tables && (int64_t)blockIdx.x < nlead) stage_tables(lds, tables);
+    if (!VEC_ONLY && tables && (int64_t)bid < nlead) stage_tables(lds, tables);
 
-    const int64_t wave = (int64_t)blockIdx.x * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
-    const int64_t nwaves = (int64_t)gridDim.x * WAVES_PER_WG;
+    const int64_t wave = (int64_t)bid * WAVES_PER_WG + uniform_u32(threadIdx.x / WAVE);
+    const int64_t nwaves = (int64_t)nbid * WAVES_PER_WG;
     int32_t s = 0;
     const int32_t nseg = segs[0].nseg;
     int32_t cur_leaf = -1;
@@ -2288,9 +2321,9 @@ void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
     KHp hl = h;  // the current leaf's scalars (its group's, in a grouped launch)
     // The list's leading quantized units (partial and odd-sized blocks, the
     // long ones), a workgroup each; then the rest a wave each, handed out
-    // from the grid's last waves down so that the workgroups of the first
-    // phase take none when the grid covers every unit.
-    for (int64_t q = blockIdx.x; q < nlead; q += gridDim.x) {
+    // from the last waves down so that the workgroups of the first phase
+    // take none when the workgroups cover every unit.
+    for (int64_t q = bid; q < nlead; q += nbid) {
         s = seek_seg(segs, nseg, s, q);
         const Seg sg = segs[s];
         if (sg.leaf != cur_leaf) {
@@ -2322,6 +2355,18 @@ void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
                                                          min(idx * EW_UNIT<APPLY> + EW_UNIT<APPLY>, L.size), hl);
         }
     }
+}
+
+template <bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT, bool VEC_ONLY = false>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(GEN_WAVES_PER_EU<MSR, PSR, NEST, VEC_ONLY>)))
+void k_adam8_gen(const rf_adam8_leaf* __restrict__ leaves,
+                                                  const Seg* __restrict__ segs, int64_t total_units, KHp h,
+                                                  const uint4* __restrict__ tables)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t lds[TABLE_BYTES];
+    __shared__ uint32_t red[2 * WAVES_PER_WG];  // absmax bits of a workgroup's block, per wave
+    gen_list<APPLY, MSR, PSR, NEST, EXACT, VEC_ONLY>(leaves, segs, total_units, h, tables, lds, red, blockIdx.x,
+                                                     gridDim.x);
 }
 
 }  // namespace rf

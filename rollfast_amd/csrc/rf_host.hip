@@ -1656,6 +1656,7 @@ rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_
 }
 
 int64_t step_grid(const DevState* ds, int occ, const PlanGroup& g, int32_t run);
+void find_carrier(const std::vector<PlanGroup>& groups, bool msr, const PlanGroup** gen, const PlanGroup** carrier);
 
 }  // namespace
 
@@ -1781,7 +1782,12 @@ rf_status rf_adam8_plan_create(const rf_adam8_leaf* leaves, int32_t n_leaves, in
 rf_status rf_adam8_plan_info(const rf_adam8_plan* plan, int64_t* launches, int64_t* leaves, int64_t* units)
 {
     if (!plan) return fail(RF_ERR_INVALID, "null plan");
-    if (launches) *launches = (int64_t)plan->groups.size();
+    if (launches) {
+        // the generic list rides along with a bf16/bf16 fast launch (plan_launch)
+        const PlanGroup *gen = nullptr, *carrier = nullptr;
+        find_carrier(plan->groups, false, &gen, &carrier);
+        *launches = (int64_t)plan->groups.size() - (carrier ? 1 : 0);
+    }
     if (leaves) *leaves = plan->n_leaves;
     if (units) *units = plan->total_units;
     return RF_OK;
@@ -1855,6 +1861,19 @@ rf_status magma_sums_finish(const rf_adam8_plan* plan, const rf_adam8_hparams* h
                        plan->n_leaves, plan->d_mpart, hp->magma_sums);
     HIP_TRY(hipGetLastError());
     return RF_OK;
+}
+
+// The generic list and the fast list it rides along with (the bf16/bf16
+// one; not in moment-SR launches), or null carrier when the two launch
+// apart.
+void find_carrier(const std::vector<PlanGroup>& groups, bool msr, const PlanGroup** gen, const PlanGroup** carrier)
+{
+    *gen = *carrier = nullptr;
+    for (const PlanGroup& g : groups) {
+        if (g.combo == -1) *gen = &g;
+        if (g.combo == 3) *carrier = &g;
+    }
+    if (!*gen || msr) *carrier = nullptr;
 }
 
 // Workgroups of one step launch over list g with `run` consecutive units per
@@ -1981,7 +2000,18 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
     k.mpart = hp->magma_sums ? plan->d_mpart : nullptr;
     k.msegs = plan->d_msegs;
 
+    // The generic list (partial blocks, small leaves) rides along with the
+    // bf16/bf16 fast launch when the step has one and no moment SR: its
+    // workgroups lead that grid (k_adam8's KHp.gsegs, CARRIES_GEN), one
+    // launch instead of two.
+    const PlanGroup* gen = nullptr;
+    const PlanGroup* carrier = nullptr;
+    find_carrier(plan->groups, msr, &gen, &carrier);
+    k.gsegs = nullptr;
+    k.gunits = 0;
+    k.gwgs = 0;
     for (const PlanGroup& g : plan->groups) {
+        if (carrier && &g == gen) continue;
         adam_kernel_t fn =
             pick_adam_kernel(plan->apply != 0, msr, psr, (f & RF_NESTEROV) != 0, (f & RF_EXACT) != 0, g.combo);
         if (!fn) return fail(RF_ERR_HIP, "no step kernel instance for this launch");
@@ -1997,9 +2027,19 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         // (the ragged tree's 1,570 workgroups on 768 slots become 1,536,
         // GPT-2-small's 943 become 768).
         k.run = g.combo >= 0 ? (int32_t)STEP_RUN_UNITS : 1;
-        const int64_t grid = step_grid(ds, occ, g, k.run);
+        int64_t grid = step_grid(ds, occ, g, k.run);
+        KHp kg = k;
+        if (&g == carrier) {
+            const int64_t ggrid = step_grid(ds, occ, *gen, 1);
+            if (ggrid > INT32_MAX || grid + ggrid > (int64_t)UINT32_MAX)
+                return fail(RF_ERR_UNSUPPORTED, "step grid beyond 2^32 - 1 workgroups");
+            kg.gsegs = plan->d_segs + gen->seg_offset;
+            kg.gunits = gen->units;
+            kg.gwgs = (int32_t)ggrid;
+            grid += ggrid;
+        }
         hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(WG), 0, (hipStream_t)stream, d_leaves,
-                           plan->d_segs + g.seg_offset, g.units, k,
+                           plan->d_segs + g.seg_offset, g.units, kg,
                            !g.tables ? nullptr : (msr ? ds->search : ds->tables));
         HIP_TRY(hipGetLastError());
     }

@@ -108,7 +108,8 @@ def test_plan_run_on_creation_table_and_info():
     try:
         launches, leaves, units = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
         assert lib.rf_adam8_plan_info(plan, ctypes.byref(launches), ctypes.byref(leaves), ctypes.byref(units)) == 0
-        assert leaves.value == 2 and launches.value == 2 and units.value == 7 + 1
+        # the partial block's generic unit rides in the bf16 fast launch
+        assert leaves.value == 2 and launches.value == 1 and units.value == 7 + 1
         for step in range(1, 3):
             hp, o = _hparams(step)
             assert lib.rf_adam8_plan_run(plan, ctypes.byref(hp), _lib.stream_ptr()) == _lib.RF_OK
