@@ -315,7 +315,8 @@ __device__ __forceinline__ uint32_t packed_param_bits1(uint32_t k0, uint32_t k1,
 // jax.random.uniform(float32) from raw bits: mantissa fill of [1, 2) minus 1.
 __device__ __forceinline__ float uniform_from_bits(uint32_t bits)
 {
-    return __uint_as_float((bits >> 9) | 0x3F800000u) - 1.0f;
+    // (bits >> 9) | 0x3F800000 as one funnel shift of (0x7F : bits) by 9
+    return __uint_as_float(__builtin_amdgcn_alignbit(0x7Fu, bits, 9)) - 1.0f;
 }
 
 template <int CTRL>
