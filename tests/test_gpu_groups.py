@@ -65,17 +65,21 @@ def _assert_same(pa, pb, sa_groups, sb_groups, what):
                 np.testing.assert_array_equal(x, y, err_msg=f"{what} {name} {field}")
 
 
-@pytest.mark.parametrize("msr,bf16_head,psr", [(False, False, False), (True, True, True)])
-def test_grouped_step_equals_groups_one_by_one(msr, bf16_head, psr):
+@pytest.mark.parametrize("msr,bf16_head,psr,exact", [(False, False, False, True), (True, True, True, True),
+                                                     (False, False, False, False), (False, True, True, False)])
+def test_grouped_step_equals_groups_one_by_one(msr, bf16_head, psr, exact):
+    """exact=False: the hardware direction with the learning rate folded in,
+    whose constants a grouped launch derives per group on the device, must
+    give the separate launches' bits too."""
     import torch
 
     import rollfast_amd as rf
 
     _, pa = _tree(1, 0.02)
     _, pb = _tree(1, 0.02)
-    txa = rf.multi_transform(_transforms(rf, msr=msr, bf16_head=bf16_head), LABELS)
+    txa = rf.multi_transform(_transforms(rf, msr=msr, exact=exact, bf16_head=bf16_head), LABELS)
     sa = txa.init(pa)
-    singles = _transforms(rf, msr=msr, bf16_head=bf16_head)
+    singles = _transforms(rf, msr=msr, exact=exact, bf16_head=bf16_head)
     masks = {lab: {name: LABELS[name] == lab for name in LABELS} for lab in singles}
     txb = {lab: rf.masked(tx, masks[lab]) for lab, tx in singles.items()}
     sb = {lab: tx.init(pb) for lab, tx in txb.items()}
