@@ -1166,8 +1166,11 @@ def adamw8_step(tx, params, grads, state, key=None, stochastic: bool = True, *, 
         updates, state = tx.update(grads, state, params)
         params = rollfast.apply_updates(params, updates, key, stochastic)
 
-    for ``tx = adamw8(...)``.  Params are updated in place and returned with
-    the new state.  ``random_bits`` (testing): ``{leaf_index: (mu_bits,
+    for ``tx = adamw8(...)``: the same state bit for bit, and with
+    ``exact=True`` the same params; in the default mode the fused form folds
+    the learning rate into the direction, and both forms stay within one
+    bf16 ulp of the reference's params.  Params are updated in place and
+    returned with the new state.  ``random_bits`` (testing): ``{leaf_index: (mu_bits,
     nu_bits, param_bits)}`` device uint32 arrays replacing in-kernel bits.
 
     ``clip_global_norm``: the grads are first clipped by their global L2 norm
