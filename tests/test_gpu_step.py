@@ -296,6 +296,46 @@ def test_folded_step_where_updates_cancel_params(lr_ulps):
     _compare_params(spec, tree, params, False, f"lr_ulps {lr_ulps}", before)
 
 
+@pytest.mark.parametrize("lr,wd", [(1e-1, 1e-3), (3e-2, 2e-3), (1e-2, 0.0), (1.0, 1e-5), (1e-6, 0.1), (-1e-3, 0.01)])
+def test_folded_direction_wide_hyperparameters(lr, wd):
+    """The learning-rate-folded direction over learning rates and decays
+    either side of its |lr * wd| <= 2^-14 range (3e-2 * bf16(2e-3) is just
+    inside, 1e-1 * 1e-3 outside), without decay, with a negative learning
+    rate, and params whose magnitudes span 1e-6 .. 10 with Student-t grads:
+    codes and scales bit-exact, params within one bf16 ulp, three steps each
+    from the device state."""
+    import torch
+
+    rf = _rf()
+    spec = [((32, 2048), "bf16", "bf16"), ((5000,), "bf16", "bf16")]
+    rng = np.random.default_rng(77)
+    host, params = {}, {}
+    for i, (shape, _pd, _gd) in enumerate(spec):
+        n = int(np.prod(shape))
+        mag = np.exp(rng.uniform(np.log(1e-6), np.log(10.0), n))
+        p = (mag * rng.choice([-1.0, 1.0], n)).astype(np.float32)
+        host[f"l{i:03d}"] = bf16_bits(p)
+        params[f"l{i:03d}"] = to_device(host[f"l{i:03d}"], "bf16").reshape(shape)
+    tx = rf.adamw8(learning_rate=lr, weight_decay=wd, key=rf.prng.PRNGKey(7))
+    state = tx.init(params)
+    for step in range(3):
+        ghost, gdev = [], {}
+        for i, (shape, _pd, _gd) in enumerate(spec):
+            n = int(np.prod(shape))
+            g = bf16_bits((rng.standard_t(3, n) * 1e-3).astype(np.float32))
+            ghost.append(g)
+            gdev[f"l{i:03d}"] = to_device(g, "bf16").reshape(shape)
+        for i in range(len(spec)):
+            host[f"l{i:03d}"] = to_host(params[f"l{i:03d}"]).copy()
+        tree = _oracle_from_state(spec, host, state[0])
+        before = [L["param"].copy() for L in tree.leaves]
+        tree.step(ghost, weight_decay=wd, lr=lr, count=int(state[0].count) + 1)
+        params, state = rf.adamw8_step(tx, params, gdev, state, stochastic=False)
+        torch.cuda.synchronize()
+        _compare_state(spec, tree, state[0], f"lr {lr} wd {wd} step {step + 1}")
+        _compare_params(spec, tree, params, False, f"lr {lr} wd {wd} step {step + 1}", before)
+
+
 # ---------------------------------------------------------- Optax mode --
 def _optax_mode(spec, *, adamw, exact, seed=3):
     import torch
