@@ -108,23 +108,31 @@ def _children(x):
     return ("list", None, list(x))
 
 
+# The walks below are module-level functions that take their accumulator as
+# an argument.  A nested function that calls itself is a reference cycle
+# (the function, its closure cell, the function again) holding everything it
+# closes over -- here the leaves, often device tensors -- until the cyclic
+# garbage collector runs; a caller's update tree would then outlive its last
+# reference by an unpredictable number of steps.
+
+
+def _flatten_rec(x, is_leaf, leaves_: list):
+    if is_leaf is not None and is_leaf(x):
+        leaves_.append(x)
+        return _LEAF
+    node = _children(x)
+    if node is None:
+        leaves_.append(x)
+        return _LEAF
+    kind, aux, children = node
+    return TreeDef(kind, aux, [_flatten_rec(c, is_leaf, leaves_) for c in children])
+
+
 def flatten(tree, is_leaf: Optional[Callable[[Any], bool]] = None):
     """Return ``(leaves, treedef)``."""
-    leaves: list = []
-
-    def rec(x):
-        if is_leaf is not None and is_leaf(x):
-            leaves.append(x)
-            return _LEAF
-        node = _children(x)
-        if node is None:
-            leaves.append(x)
-            return _LEAF
-        kind, aux, children = node
-        return TreeDef(kind, aux, [rec(c) for c in children])
-
-    td = rec(tree)
-    return leaves, td
+    leaves_: list = []
+    td = _flatten_rec(tree, is_leaf, leaves_)
+    return leaves_, td
 
 
 def leaves(tree, is_leaf=None) -> list:
@@ -153,42 +161,42 @@ def _build(td: TreeDef, children):
     raise ValueError(f"unknown node kind {td.kind!r}")
 
 
+def _unflatten_rec(t: TreeDef, it):
+    if t.kind == "leaf":
+        return next(it)
+    return _build(t, [_unflatten_rec(c, it) for c in t.children])
+
+
 def unflatten(td: TreeDef, leaves_) -> Any:
     it = iter(leaves_)
-
-    def rec(t: TreeDef):
-        if t.kind == "leaf":
-            return next(it)
-        return _build(t, [rec(c) for c in t.children])
-
-    out = rec(td)
+    out = _unflatten_rec(td, it)
     rest = list(it)
     if rest:
         raise ValueError(f"too many leaves for the tree structure ({len(rest)} left over)")
     return out
 
 
+def _flatten_up_to_rec(t: TreeDef, x, out: list) -> None:
+    if t.kind == "leaf":
+        out.append(x)
+        return
+    node = _children(x)
+    if node is None:
+        raise ValueError(f"tree structure mismatch: expected a {t.kind} node, got a leaf {type(x)}")
+    kind, aux, children = node
+    if kind != t.kind or len(children) != len(t.children):
+        raise ValueError(f"tree structure mismatch: {t.kind} vs {kind}")
+    if kind in ("dict", "odict") and aux[1] != t.aux[1]:
+        raise ValueError(f"dict keys differ: {t.aux[1]} vs {aux[1]}")
+    for ct, cx in zip(t.children, children):
+        _flatten_up_to_rec(ct, cx, out)
+
+
 def flatten_up_to(td: TreeDef, tree) -> list:
     """Subtrees of ``tree`` at the leaf positions of ``td`` (``td`` must be a
     prefix of ``tree``'s structure), as ``jax`` does for ``tree.map`` rests."""
     out: list = []
-
-    def rec(t: TreeDef, x):
-        if t.kind == "leaf":
-            out.append(x)
-            return
-        node = _children(x)
-        if node is None:
-            raise ValueError(f"tree structure mismatch: expected a {t.kind} node, got a leaf {type(x)}")
-        kind, aux, children = node
-        if kind != t.kind or len(children) != len(t.children):
-            raise ValueError(f"tree structure mismatch: {t.kind} vs {kind}")
-        if kind in ("dict", "odict") and aux[1] != t.aux[1]:
-            raise ValueError(f"dict keys differ: {t.aux[1]} vs {aux[1]}")
-        for ct, cx in zip(t.children, children):
-            rec(ct, cx)
-
-    rec(td, tree)
+    _flatten_up_to_rec(td, tree, out)
     return out
 
 

@@ -78,3 +78,29 @@ def test_updates_out_without_cache_allocates_each_call():
     gc.collect()
     host.updates_out(grads, [grads["w"]], [object()], [(0,)], ctypes.addressof(table))
     assert len(names) == 1 and isinstance(pa, int)
+
+
+def test_tree_walks_leave_no_reference_cycles():
+    """flatten / unflatten / flatten_up_to hold no leaf past their return: a
+    self-calling nested walk would be a reference cycle keeping every leaf
+    (an update tree's views) alive until the cyclic collector runs, and the
+    output buffer of the next update-only step could not be reused."""
+    import weakref
+
+    from rollfast_amd import _tree
+
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        tree = {"a": [torch.zeros(2), torch.zeros(3)], "b": (torch.zeros(1), {"c": torch.zeros(4)})}
+        leaves, td = _tree.flatten(tree)
+        w_leaf = weakref.ref(leaves[0])
+        rebuilt = _tree.unflatten(td, [torch.ones(1) for _ in leaves])
+        w_rebuilt = weakref.ref(rebuilt["b"][1]["c"])
+        ups = _tree.flatten_up_to(td, rebuilt)
+        w_up = weakref.ref(ups[-1])
+        del leaves, tree, rebuilt, ups
+        assert w_leaf() is None and w_rebuilt() is None and w_up() is None
+    finally:
+        if was:
+            gc.enable()
