@@ -397,7 +397,7 @@ def _tree_workload(args, shapes_fn, workload, *, param_sr, grads="normal", optax
                     + (", stochastically rounded storage)" if adam_mu == "bf16" else ")")),
         "param_rounding": (("stochastic" + (" (packed bits: a Threefry block per 4 elements)" if packed else ""))
                            if param_sr else "nearest-even") if pdtype == "bf16" else "f32 add",
-        "moment_rounding": (("stochastic (packed bits: a Threefry block per element for both moments)" if packed
+        "moment_rounding": (("stochastic (packed bits: a Threefry block per pair of elements for both moments)" if packed
                              else "stochastic (in-kernel Threefry bits)") if moment_sr else "nearest"),
         "direction": "ieee" if args.exact else "hw rcp/sqrt",
         "mode": "optax update-only (f32 updates)" if optax else "fused step (params written)",
@@ -709,8 +709,8 @@ def main(argv=None):
     ap.add_argument("--param-sr", action="store_true", help="stochastic rounding of bf16 params")
     ap.add_argument("--sr-bits", choices=("jax", "packed"), default="jax",
                     help="bit source of the stochastic roundings: jax.random.bits' stream (one Threefry block per "
-                         "32-bit word) or the packed one (a block per four param roundings, or per element for "
-                         "both moments)")
+                         "32-bit word) or the packed one (a block per four param roundings, or per pair of "
+                         "elements for both moments)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copies", type=int, default=1,

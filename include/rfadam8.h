@@ -69,11 +69,16 @@ typedef int32_t rf_status;
                             block per 32-bit word.  Param SR of element e takes the 16-bit
                             half (e & 1) of word (e & 2 ? y1 : y0) of threefry(param key,
                             (hi32(e >> 2), lo32(e >> 2))): a block per four elements.
-                            Moment SR (and RF_LEAF_STORE_SR) of element e takes y0 for the
-                            first moment and y1 for the second of threefry(first-moment
-                            key, (hi32(e), lo32(e))): a block per element for both.  Keys
-                            are the per-leaf keys of the default stream.  Exclusive with
-                            RF_FED_BITS */
+                            Element e's moment main halves are the 16-bit halves (e & 1)
+                            of y0 (first moment) and y1 (second) of threefry(first-moment
+                            key, (hi32(e >> 1), lo32(e >> 1))): a block per pair of
+                            elements for both; its fill halves are the same halves of the
+                            block at counter 2^63 + (e >> 1).  Moment SR draws from the
+                            word (main << 16) | fill (its top 23 bits make the uniform;
+                            the fill block is computed only for the 2^-16 of draws the
+                            main half leaves open); RF_LEAF_STORE_SR rounds with the main
+                            half.  Keys are the per-leaf keys of the default stream.
+                            Exclusive with RF_FED_BITS */
 #define RF_SKIP_NONFINITE 512u /* optax.apply_if_finite reject branch (the wrapper of the
                             fine-tune chain, finetune/builders.py:1605-1609): when any
                             grad of the run is Inf or NaN, the launch leaves the moments

@@ -191,11 +191,43 @@ def packed_param_bits(key, n: int, offset: int = 0) -> np.ndarray:
     return np.where((e & np.uint64(1)) != 0, w >> np.uint32(16), w & np.uint32(0xFFFF)).astype(np.uint32)
 
 
+def _packed_moment_halves(key, n: int, offset: int, fill: bool):
+    """16-bit halves (e & 1) of y0 and y1 of the packed source's moment
+    blocks for elements offset .. offset + n - 1: the main block at counter
+    e >> 1, or the fill block at counter 2^63 + (e >> 1)."""
+    e = np.arange(int(offset), int(offset) + n, dtype=np.uint64)
+    q0 = int(offset) >> 1
+    base = q0 + ((1 << 63) if fill else 0)
+    y0, y1 = threefry_blocks(key, ((int(offset) + n - 1) >> 1) - q0 + 1, base)
+    q = (e >> np.uint64(1)).astype(np.int64) - q0
+    odd = (e & np.uint64(1)) != 0
+    pick = lambda y: np.where(odd, y[q] >> np.uint32(16), y[q] & np.uint32(0xFFFF)).astype(np.uint32)
+    return pick(y0), pick(y1)
+
+
 def packed_moment_bits(key, n: int, offset: int = 0):
-    """The packed source's moment draws of elements offset .. offset + n - 1
-    (no reference counterpart): (first-moment words, second-moment words) =
-    (y0, y1) of the block at counter e under the first-moment key."""
-    return threefry_blocks(key, n, offset)
+    """The packed source's moment-code draws of elements offset .. offset +
+    n - 1 (no reference counterpart), as (first-moment words, second-moment
+    words) under the first-moment key: element e's word is (main << 16) |
+    fill, main the 16-bit half (e & 1) of y0 (first) or y1 (second) of the
+    block at counter e >> 1, fill the same half of the block at counter
+    2^63 + (e >> 1).  The draw's uniform takes the word's top 23 bits."""
+    n = int(n)
+    if n == 0:
+        return np.empty(0, np.uint32), np.empty(0, np.uint32)
+    mm, mv = _packed_moment_halves(key, n, offset, False)
+    fm, fv = _packed_moment_halves(key, n, offset, True)
+    return (mm << np.uint32(16)) | fm, (mv << np.uint32(16)) | fv
+
+
+def packed_store_bits(key, n: int, offset: int = 0):
+    """The packed source's bf16 moment-storage noise (RF_LEAF_STORE_SR) of
+    elements offset .. offset + n - 1: the main halves of packed_moment_bits
+    in the low 16 bits (the part sr_bf16 adds)."""
+    n = int(n)
+    if n == 0:
+        return np.empty(0, np.uint32), np.empty(0, np.uint32)
+    return _packed_moment_halves(key, n, offset, False)
 
 
 def split(key, num: int) -> np.ndarray:

@@ -288,10 +288,11 @@ __device__ __forceinline__ void jax_split(uint32_t k0, uint32_t k1, uint32_t i, 
 // one block per 32-bit word.  Param rounding needs 16 bits per element, so
 // element e of a leaf takes the 16-bit half (e & 1) of word (e & 2 ? y1 :
 // y0) of the block at counter (hi32(e >> 2), lo32(e >> 2)) under the leaf's
-// param key: a block per four elements.  The moments' Bernoulli draws take
-// y0 (first moment) and y1 (second moment) of the block at counter
-// (hi32(e), lo32(e)) under the leaf's first-moment key: a block per element
-// for both.  The rounding reads the noise from the low 16 bits of the word.
+// param key: a block per four elements.  The moments' draws take the 16-bit
+// halves (e & 1) of y0 (first moment) and y1 (second moment) of the block at
+// counter (hi32(e >> 1), lo32(e >> 1)) under the leaf's first-moment key: a
+// block per pair of elements for both moments (packed_moment_block).  The
+// param rounding reads the noise from the low 16 bits of the word.
 __device__ __forceinline__ void packed_param_bits4(uint32_t k0, uint32_t k1, uint64_t e0, uint32_t* rb)
 {
     uint32_t y0, y1;
@@ -310,6 +311,31 @@ __device__ __forceinline__ uint32_t packed_param_bits1(uint32_t k0, uint32_t k1,
     threefry2x32(k0, k1, (uint32_t)(q >> 32), (uint32_t)q, y0, y1);
     const uint32_t w = (e & 2) ? y1 : y0;
     return (e & 1) ? (w >> 16) : w;
+}
+
+// The packed source's moment blocks.  Element e's main half is the 16-bit
+// half (e & 1) of y0 (first moment) or y1 (second moment) of the main block,
+// at counter (hi32(e >> 1), lo32(e >> 1)); its fill half is the same half of
+// the fill block, at counter 2^63 + (e >> 1) (both under the leaf's
+// first-moment key; a 2^63 element leaf would be needed for the two to
+// meet).  bf16 storage rounding takes the main half as its 16 bits of
+// noise.  The codes' Bernoulli draw takes the word (main << 16) | fill,
+// whose top 23 bits make the uniform (uniform_from_bits): the main half and
+// the fill's top 7 bits, so each draw takes the upper code with the
+// probability the reference's 23-bit uniform gives.  The main half alone
+// settles a draw unless the probability lies within 127/128 of a main-half
+// step above it (probability 2^-16 per draw; packed_sr_main), and only
+// then is the fill block computed.
+__device__ __forceinline__ void packed_moment_block(uint32_t k0, uint32_t k1, uint64_t e, bool fill, uint32_t& y0,
+                                                    uint32_t& y1)
+{
+    const uint64_t q = e >> 1;
+    threefry2x32(k0, k1, (uint32_t)(q >> 32) | (fill ? 0x80000000u : 0u), (uint32_t)q, y0, y1);
+}
+
+__device__ __forceinline__ uint32_t half16(uint32_t w, uint64_t e)
+{
+    return (e & 1) ? (w >> 16) : (w & 0xFFFFu);
 }
 
 // jax.random.uniform(float32) from raw bits: mantissa fill of [1, 2) minus 1.
@@ -466,25 +492,66 @@ __device__ __forceinline__ uint32_t cand_unsigned(const uint8_t* lds, float n)
 // cell): _quantize_to_codebook's SR branch (adam8.py:549-564).
 // ui = searchsorted_left(cb, n) = cand + (cb[cand] < n), li = ui - 1 (at
 // least 0), p = (n - cb[li]) / (cb[ui] - cb[li]) (0 when the two coincide),
-// upper code iff uniform(bits) < p.  `rec` holds per ui {cb[li], gap, y =
-// RN(1/gap) or 0}: p = fma(r, y, q0) with q0 = a*y and r = fma(-gap, q0, a)
-// (a = n - cb[li]) is the IEEE quotient's Bernoulli decision for every
-// uniform value (a reciprocal correctly rounded and one Markstein
-// correction; the tables test checks it against IEEE division over every
-// gap), and 0 for ui = 0.  Since cb[li] < n <= cb[ui], 0 <= p <= 1 needs no
-// clip.  A value below cb[0] counts no entry (ui = li = 0, p = 0), which is
-// the reference's clip.
-__device__ __forceinline__ uint32_t sr_code(const float* cb, const float4* rec, uint32_t cand, float n,
-                                            uint32_t bits)
+// upper code iff uniform(bits) < p.  sr_upper returns x = 65536 p: `rec`
+// holds per ui >= 1 {cb[li], gap 2^-16, y 2^16} with y = RN(1/gap), and
+// x = fma(r, y', q0) with q0 = a*y' and r = fma(-gap', q0, a) (a = n -
+// cb[li]) is 65536 times a quotient that decides the Bernoulli draw as the
+// IEEE quotient does for every uniform value (a reciprocal correctly
+// rounded and one Markstein correction, scaled by powers of two; the tables
+// test checks it against IEEE division over every gap).  Since cb[li] < n
+// <= cb[ui], 0 <= x <= 65536 needs no clip.  ui = 0 (n <= cb[0], where the
+// reference's clip leaves li = ui = 0) finds {-2, 0, 65536}: a = n + 2 >= 1
+// and x = 2a 65536 exceeds every draw, so "upper" picks ui.  The lower code
+// is written max(ui - 1, 0) all the same: a select of ui and ui - 1 is
+// rewritten by the compiler as ui minus the "lower" bit, which keeps a
+// batch's lane masks in scalar registers across the packed source's fill
+// branch, and the moment-SR kernels then spill.
+__device__ __forceinline__ float sr_upper(const float* cb, const float4* rec, uint32_t& cand, float n)
 {
     const uint32_t ui = cand + (cb[cand] < n ? 1u : 0u);
     const float4 nb = rec[ui];
     const float a = n - nb.x;
     const float q0 = a * nb.z;
     const float r = __builtin_fmaf(-nb.y, q0, a);
-    const float p = __builtin_fmaf(r, nb.z, q0);
-    const uint32_t li = __builtin_elementwise_sub_sat(ui, 1u);
-    return uniform_from_bits(bits) < p ? ui : li;
+    cand = ui;
+    return __builtin_fmaf(r, nb.z, q0);
+}
+
+// uniform_from_bits(bits) * 65536, exactly: (bits >> 9) | 0x47800000 is
+// 65536 (1 + k 2^-23) for k = bits >> 9.
+__device__ __forceinline__ float uniform_from_bits_x65536(uint32_t bits)
+{
+    return __uint_as_float(__builtin_amdgcn_alignbit(0x8Fu, bits, 9)) - 65536.0f;
+}
+
+// The code from ui and x = 65536 p (sr_upper) and a 32-bit draw.
+__device__ __forceinline__ uint32_t sr_decide(uint32_t ui, float x, uint32_t bits)
+{
+    return uniform_from_bits_x65536(bits) < x ? ui : __builtin_elementwise_sub_sat(ui, 1u);
+}
+
+__device__ __forceinline__ uint32_t sr_code(const float* cb, const float4* rec, uint32_t cand, float n,
+                                            uint32_t bits)
+{
+    const float x = sr_upper(cb, rec, cand, n);
+    return sr_decide(cand, x, bits);
+}
+
+// The packed source's draw from its main half m alone (packed_moment_block):
+// the draw is k = 128 m + f (f, the fill's top 7 bits, below 128) and takes
+// the upper code iff k 2^-23 < p, i.e. m + f / 128 < x = 65536 p (sr_upper's
+// result).  m + 127/128 < x settles "upper" whatever f is, and m >= x
+// settles "lower"; between the two `open` is set, and the caller decides
+// with the fill (sr_decide on the whole word).  x - 127/128 is exact where
+// it is not negative (127/128 is a multiple of x's ulp while x < 2^17) and
+// negative otherwise, where "upper" is rightly not settled; the ui = 0
+// record's x >= 131072 settles "upper".
+__device__ __forceinline__ uint32_t packed_sr_main(uint32_t ui, float x, uint32_t m, bool& open)
+{
+    const float hm = (float)m;
+    const bool up = hm < x - 0.9921875f;
+    open = open || (!up && hm < x);
+    return up ? ui : __builtin_elementwise_sub_sat(ui, 1u);
 }
 
 // Signed dynamic codebook code of x in a block with scale s (fast path;
@@ -937,7 +1004,9 @@ __device__ __forceinline__ void param_bits8(const UnitCtx& c, const rf_adam8_lea
     }
 }
 
-// Both moments' bits of element e (quantized: of the padded code arrays).
+// Both moments' bf16 storage-rounding bits of element e (RF_LEAF_STORE_SR;
+// the rounding reads the low 16 bits): fed, the packed source's main halves,
+// or jax.random.bits of the moment keys.
 __device__ __forceinline__ void moment_bits1(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e, uint32_t& bm,
                                              uint32_t& bv)
 {
@@ -945,33 +1014,41 @@ __device__ __forceinline__ void moment_bits1(const UnitCtx& c, const rf_adam8_le
         bm = gld<uint32_t>(L.mu_bits, e);
         bv = gld<uint32_t>(L.nu_bits, e);
     } else if (c.packed) {
-        threefry2x32(c.kmu0, c.kmu1, (uint32_t)((uint64_t)e >> 32), (uint32_t)e, bm, bv);
+        uint32_t y0, y1;
+        packed_moment_block(c.kmu0, c.kmu1, (uint64_t)e, false, y0, y1);
+        bm = half16(y0, (uint64_t)e);
+        bv = half16(y1, (uint64_t)e);
     } else {
         bm = jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
         bv = jax_bits(c.knu0, c.knu1, (uint64_t)e);
     }
 }
 
-// One moment's bits of element e (the literal paths code the moments apart).
+// The packed source's whole code draw of element e (packed_moment_block):
+// (main << 16) | fill from y0 (first moment) or y1 (second moment).
+template <bool SECOND>
+__device__ __forceinline__ uint32_t packed_code_word(const UnitCtx& c, int64_t e)
+{
+    uint32_t y0, y1, z0, z1;
+    packed_moment_block(c.kmu0, c.kmu1, (uint64_t)e, false, y0, y1);
+    packed_moment_block(c.kmu0, c.kmu1, (uint64_t)e, true, z0, z1);
+    return SECOND ? (half16(y1, (uint64_t)e) << 16) | half16(z1, (uint64_t)e)
+                  : (half16(y0, (uint64_t)e) << 16) | half16(z0, (uint64_t)e);
+}
+
+// One moment's code-draw bits of element e (quantized: of the padded code
+// arrays; the literal paths code the moments apart).
 __device__ __forceinline__ uint32_t mu_bits1(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e)
 {
     if (c.fed) return gld<uint32_t>(L.mu_bits, e);
-    if (c.packed) {
-        uint32_t y0, y1;
-        threefry2x32(c.kmu0, c.kmu1, (uint32_t)((uint64_t)e >> 32), (uint32_t)e, y0, y1);
-        return y0;
-    }
+    if (c.packed) return packed_code_word<false>(c, e);
     return jax_bits(c.kmu0, c.kmu1, (uint64_t)e);
 }
 
 __device__ __forceinline__ uint32_t nu_bits1(const UnitCtx& c, const rf_adam8_leaf& L, int64_t e)
 {
     if (c.fed) return gld<uint32_t>(L.nu_bits, e);
-    if (c.packed) {
-        uint32_t y0, y1;
-        threefry2x32(c.kmu0, c.kmu1, (uint32_t)((uint64_t)e >> 32), (uint32_t)e, y0, y1);
-        return y1;
-    }
+    if (c.packed) return packed_code_word<true>(c, e);
     return jax_bits(c.knu0, c.knu1, (uint64_t)e);
 }
 
@@ -1503,9 +1580,11 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
             const float4* srs = (const float4*)(c.lds + L_SRS);
             const float4* sru = (const float4*)(c.lds + L_SRU);
             if (c.packed) {
-                // One block per element feeds both moments: each chunk is
-                // coded for both at once, four elements (four blocks) at a
-                // time so that few blocks' words are live.
+                // A main block per pair of elements feeds both moments; each
+                // chunk is coded for both at once, four elements (two
+                // blocks) at a time so that few words are live.  A batch
+                // whose main halves leave a draw open computes its two fill
+                // blocks and decides every draw on the whole word.
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
                     const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
@@ -1513,13 +1592,11 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                     uint32_t wm[2], wv[2];
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
-                        uint32_t bm[4], bv[4], cm[4], cv[4];
-                        float nm[4], nv[4];
+                        uint32_t ym[2], yv[2], um[4], uv[4], cm[4], cv[4];
+                        float nm[4], nv[4], pm[4], pv[4];
 #pragma unroll
-                        for (int t = 0; t < 4; ++t) {
-                            const uint64_t e = e0 + 4 * hh + t;
-                            threefry2x32(c.kmu0, c.kmu1, (uint32_t)(e >> 32), (uint32_t)e, bm[t], bv[t]);
-                        }
+                        for (int pr = 0; pr < 2; ++pr)
+                            packed_moment_block(c.kmu0, c.kmu1, e0 + 4 * hh + 2 * pr, false, ym[pr], yv[pr]);
 #pragma unroll
                         for (int t = 0; t < 4; ++t) {
                             nm[t] = div_by_scale(m[j][4 * hh + t], sm, rsm);
@@ -1527,13 +1604,30 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                         }
 #pragma unroll
                         for (int t = 0; t < 4; ++t) {
-                            cm[t] = cand_signed(c.lds, nm[t]);
-                            cv[t] = cand_unsigned(c.lds, nv[t]);
+                            um[t] = cand_signed(c.lds, nm[t]);
+                            uv[t] = cand_unsigned(c.lds, nv[t]);
                         }
 #pragma unroll
                         for (int t = 0; t < 4; ++t) {
-                            cm[t] = sr_code(cbs, srs, cm[t], nm[t], bm[t]);
-                            cv[t] = sr_code(cbu, sru, cv[t], nv[t], bv[t]);
+                            pm[t] = sr_upper(cbs, srs, um[t], nm[t]);
+                            pv[t] = sr_upper(cbu, sru, uv[t], nv[t]);
+                        }
+                        bool open = false;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            cm[t] = packed_sr_main(um[t], pm[t], half16(ym[t >> 1], t), open);
+                            cv[t] = packed_sr_main(uv[t], pv[t], half16(yv[t >> 1], t), open);
+                        }
+                        if (__builtin_expect(open, 0)) {
+                            uint32_t zm[2], zv[2];
+#pragma unroll
+                            for (int pr = 0; pr < 2; ++pr)
+                                packed_moment_block(c.kmu0, c.kmu1, e0 + 4 * hh + 2 * pr, true, zm[pr], zv[pr]);
+#pragma unroll
+                            for (int t = 0; t < 4; ++t) {
+                                cm[t] = sr_decide(um[t], pm[t], (half16(ym[t >> 1], t) << 16) | half16(zm[t >> 1], t));
+                                cv[t] = sr_decide(uv[t], pv[t], (half16(yv[t >> 1], t) << 16) | half16(zv[t >> 1], t));
+                            }
                         }
                         wm[hh] = pack4_u8(cm[0], cm[1], cm[2], cm[3]);
                         wv[hh] = pack4_u8(cv[0], cv[1], cv[2], cv[3]);
@@ -1942,12 +2036,26 @@ __device__ __forceinline__ void unit_fallback_vec(const UnitCtx& c, const rf_ada
         if constexpr (H16M) {
             uint32_t hm[8], hv[8];
             if (BF16M && store_sr) {
+                uint32_t bm[8], bv[8];
+                if (c.packed) {
+                    // e0 is a multiple of 8: a packed block per pair
+#pragma unroll
+                    for (int t = 0; t < 8; t += 2) {
+                        uint32_t y0, y1;
+                        packed_moment_block(c.kmu0, c.kmu1, (uint64_t)(e0 + t), false, y0, y1);
+                        bm[t] = y0;
+                        bm[t + 1] = y0 >> 16;
+                        bv[t] = y1;
+                        bv[t + 1] = y1 >> 16;
+                    }
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) moment_bits1(c, L, e0 + t, bm[t], bv[t]);
+                }
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
-                    uint32_t bm, bv;
-                    moment_bits1(c, L, e0 + t, bm, bv);
-                    hm[t] = sr_bf16_hi(m[t], bm);
-                    hv[t] = sr_bf16_hi(v[t], bv);
+                    hm[t] = sr_bf16_hi(m[t], bm[t]);
+                    hv[t] = sr_bf16_hi(v[t], bv[t]);
                 }
                 store8_hi16(L.mu, e0, hm);
                 store8_hi16(L.nu, e0, hv);

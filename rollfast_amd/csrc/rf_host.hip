@@ -1015,16 +1015,23 @@ float rcp_rn(float d)
 }
 
 // Neighbour records of the moment-SR code choice for one codebook: per
-// ui, {cb[li], cb[ui] - cb[li] (f32), RN(1 / that gap) or 0, 0} with
-// li = max(ui - 1, 0).
+// ui >= 1, {cb[ui - 1], (cb[ui] - cb[ui - 1]) 2^-16, RN(1 / that gap) 2^16
+// (0 for an empty gap), 0}, the quotient's operands scaled so that it comes
+// out as 65536 p; for ui = 0, {-2, 0, 65536, 0}, whose quotient exceeds
+// every draw (the kernel's sr_upper).  The gaps (f32 differences of codebook
+// values in [-1, 1]) and their reciprocals stay normal under the scaling.
 void fill_sr_records(const float* cb, float* rec)
 {
-    for (int ui = 0; ui < 256; ++ui) {
-        const float lv = cb[ui > 0 ? ui - 1 : 0];
+    rec[0] = -2.0f;
+    rec[1] = 0.0f;
+    rec[2] = 65536.0f;
+    rec[3] = 0.0f;
+    for (int ui = 1; ui < 256; ++ui) {
+        const float lv = cb[ui - 1];
         const float d = cb[ui] - lv;
         rec[4 * ui + 0] = lv;
-        rec[4 * ui + 1] = d;
-        rec[4 * ui + 2] = d > 0.0f ? rcp_rn(d) : 0.0f;
+        rec[4 * ui + 1] = d * 0x1p-16f;
+        rec[4 * ui + 2] = d > 0.0f ? rcp_rn(d) * 65536.0f : 0.0f;
         rec[4 * ui + 3] = 0.0f;
     }
 }

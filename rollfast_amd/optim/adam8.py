@@ -404,7 +404,9 @@ def _check_sr_bits(sr_bits) -> str:
     default) draws jax.random.bits' stream, one Threefry-2x32-20 block per
     32-bit word (bitwise the reference's layout); "packed" (no reference
     counterpart) spends one block on four param roundings, or on both
-    moments' draws of an element, from the same per-leaf keys."""
+    moments' draws of a pair of elements (16 bits each, completed to the
+    uniform's 23 from a second block only when they leave the draw open),
+    from the same per-leaf keys."""
     if sr_bits not in SR_BITS:
         raise ValueError(f"sr_bits must be one of {SR_BITS}, got {sr_bits!r}")
     return sr_bits
@@ -981,8 +983,8 @@ def scale_by_adam8(
     reciprocal/square-root (moments, codes and scales are bit-exact either
     way).  ``sr_bits`` (extension): the random-bit source of the moments'
     stochastic rounding and of the fused step's param rounding, "jax"
-    (jax.random.bits' layout) or "packed" (one Threefry block per element
-    for both moments, per four elements for params)."""
+    (jax.random.bits' layout) or "packed" (one Threefry block per pair of
+    elements for both moments, per four elements for params)."""
     torch = _torch()
     scale_dtype = torch.float32 if scale_dtype is None else canonicalize_dtype(scale_dtype)
     fallback_dtype = torch.float32 if fallback_dtype is None else canonicalize_dtype(fallback_dtype)

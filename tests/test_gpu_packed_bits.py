@@ -3,9 +3,13 @@
 
 The packed source keeps the reference's per-leaf keys but spends one
 Threefry-2x32-20 block on four param roundings (element e: half e & 1 of word
-e & 2 ? y1 : y0 of the block at counter e >> 2) and one block per element on
-both moments' Bernoulli draws (y0 first moment, y1 second, under the
-first-moment key).
+e & 2 ? y1 : y0 of the block at counter e >> 2) and one main block on both
+moments of a pair of elements (element e: half e & 1 of y0 for the first
+moment, of y1 for the second, of the block at counter e >> 1 under the
+first-moment key).  A moment code's draw is the word (main << 16) | fill,
+with the fill half from the block at counter 2^63 + (e >> 1), which the
+kernel computes only when the main half leaves the decision open; bf16
+moment storage takes the main half alone.
 
 Bars:
 * every packed result is bitwise the oracle's result on the packed stream
@@ -14,7 +18,10 @@ Bars:
 * param rounding is unbiased: over 64 keys the mean relative rounding error
   per magnitude decade is zero within 5 standard errors;
 * moment rounding takes the upper code with probability (n - cb_l) /
-  (cb_u - cb_l), within 5 sigma;
+  (cb_u - cb_l), within 5 sigma, and the draws that share a main block
+  (both moments, a pair of elements) are uncorrelated;
+* on a leaf of 2^22 elements, where some 120 draws per moment and step need
+  their fill block, every code is the oracle's;
 * the four roundings that share a block are independent: the up/down
   decisions of elements e and e + k (k = 1, 2, 3) are uncorrelated within
   5 standard errors.
@@ -84,6 +91,14 @@ def test_packed_moment_sr_fused_step():
     _run_packed(MIXED, steps=2, msr=True, psr=False)
 
 
+def test_packed_moment_sr_fill_blocks_one_big_leaf():
+    """One 2^22-element leaf (2048 fast blocks): about one draw in 2^16 per
+    moment is left open by its main half and decided with the fill block
+    (some 120 per moment and step), so a fill path that decided wrongly, or
+    read the wrong half or block, would change codes the oracle checks."""
+    _run_packed([((2048, 2048), "bf16", "bf16")], steps=2, msr=True, psr=True)
+
+
 def test_packed_both_roundings_block_4096():
     """Blocks of 4096 (the generic kernel, a workgroup per block, literal
     coding) with both roundings from the packed source."""
@@ -118,8 +133,8 @@ def test_packed_optax_form_equals_fused():
 
 def test_packed_full_precision_adamw_bf16_moments():
     """optim/adam.py's bf16 moment storage (RF_LEAF_STORE_SR) on the packed
-    source: leaf i's first- and second-moment noise from one block at counter
-    e under its first-moment storage key."""
+    source: leaf i's first- and second-moment noise from the main halves of
+    the block at counter e >> 1 under its first-moment storage key."""
     import torch
 
     import rollfast_amd as rf
@@ -136,7 +151,7 @@ def test_packed_full_precision_adamw_bf16_moments():
         _next, sr = orc.split(_key(state[0].key), 2)
         k1, _k2 = orc.split(tuple(sr), 2)
         s1 = orc.split(tuple(k1), len(SPEC))
-        pairs = [orc.packed_moment_bits(s1[i], sizes[i]) for i in range(len(SPEC))]
+        pairs = [orc.packed_store_bits(s1[i], sizes[i]) for i in range(len(SPEC))]
         pkey = rf.prng.PRNGKey(50 + step)
         kp = orc.split(_key(pkey), len(SPEC))
         pb = [orc.packed_param_bits(kp[i], sizes[i]) for i in range(len(SPEC))]
@@ -270,3 +285,19 @@ def test_packed_moment_sr_probability():
     up_v = np.mean(vc[inner] == ui)
     assert set(np.unique(vc[inner]).tolist()) <= {ui - 1, ui}
     assert abs(up_v - pv) < 5 * np.sqrt(pv * (1 - pv) / cnt), (up_v, pv)
+
+    # draws that share a main block: the two moments of an element (y0, y1)
+    # and the two elements of a pair (the halves of a word); and across
+    # neighbouring pairs.  Element 0 of each block holds its absmax; the
+    # columns from 2 keep the pairs aligned.
+    zm = (mc.reshape(nb, bs)[:, 2:bs - 2] == 201).astype(np.float64) - pm
+    zv = (vc.reshape(nb, bs)[:, 2:bs - 2] == ui).astype(np.float64) - pv
+    sd_mv = np.sqrt(pm * (1 - pm) * pv * (1 - pv) / zm.size)
+    assert abs(float((zm * zv).mean())) < 5 * sd_mv
+    for z, pp in ((zm, pm), (zv, pv)):
+        for k in (1, 2):
+            for r in (0, 1):  # r = 0, k = 1: the two halves of one word
+                a, b = z[:, r::2], z[:, r + k::2]
+                a, b = a[:, : b.shape[1]], b[:, : a.shape[1]]
+                cov = float((a * b).mean())
+                assert abs(cov) < 5 * pp * (1 - pp) / np.sqrt(a.size), (k, r, cov)

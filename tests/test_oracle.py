@@ -1120,8 +1120,62 @@ def test_packed_param_bits_definition():
 
 
 def test_packed_moment_bits_definition():
+    """The packed source's moment words (no reference counterpart), element
+    by element from the KAT-pinned block function: element e's word is
+    (main << 16) | fill, with main and fill the half (e & 1) of y0 (first
+    moment) or y1 (second) of the blocks at counters e >> 1 and
+    2^63 + (e >> 1); the storage noise is the main half.  Offsets cross
+    2^32 and 2^33 and start on odd elements."""
     key = (7, 11)
-    m, v = orc.packed_moment_bits(key, 6, (1 << 32) - 3)
-    for i in range(6):
-        c = (1 << 32) - 3 + i
-        assert (int(m[i]), int(v[i])) == orc.threefry2x32(key, (c >> 32, c & 0xFFFFFFFF))
+    for offset in (0, 5, (1 << 33) - 3):
+        m, v = orc.packed_moment_bits(key, 7, offset)
+        sm, sv = orc.packed_store_bits(key, 7, offset)
+        for i in range(7):
+            e = offset + i
+            q = e >> 1
+            y0, y1 = orc.threefry2x32(key, (q >> 32, q & 0xFFFFFFFF))
+            z0, z1 = orc.threefry2x32(key, ((q >> 32) | 0x80000000, q & 0xFFFFFFFF))
+            half = (lambda w: w >> 16) if e & 1 else (lambda w: w & 0xFFFF)
+            assert int(m[i]) == (half(y0) << 16) | half(z0)
+            assert int(v[i]) == (half(y1) << 16) | half(z1)
+            assert (int(sm[i]), int(sv[i])) == (half(y0), half(y1))
+    # a pair of elements uses the four halves of one main block, once each
+    y0, y1 = orc.threefry2x32(key, (0, 9))
+    m, v = orc.packed_moment_bits(key, 2, 18)
+    assert [int(w) >> 16 for w in m] + [int(w) >> 16 for w in v] == [y0 & 0xFFFF, y0 >> 16, y1 & 0xFFFF, y1 >> 16]
+
+
+def test_packed_main_half_settles_the_draw():
+    """The kernel decides a packed moment draw from its 16-bit main half m
+    alone when m + 127/128 < x = 65536 p ("upper") or m >= x ("lower"),
+    with x - 127/128 computed in f32, and reads the fill only in between.
+    For every main half and all 128 fill values, a settled decision equals
+    the whole word's (uniform of the top 23 bits < p), over probabilities
+    at and beside every 2^-23 step near sampled main-half boundaries, 0,
+    the smallest subnormal, 1 and random values; and the fill is needed
+    for one main half per probability, none when x's fraction is 0 or
+    above 127/128."""
+    rng = np.random.default_rng(3)
+    ps = [0.0, 1.0, float(np.float32(2.0 ** -149)), float(np.float32(2.0 ** -23)), float(np.float32(0.5))]
+    for m0 in rng.integers(0, 65536, 8).tolist() + [0, 1, 65535]:
+        for f0 in (0, 1, 126, 127, 128):
+            k = m0 * 128 + f0
+            for d in (-1, 0, 1):
+                ps.append(float(np.nextafter(np.float32(k * 2.0 ** -23), np.float32(2.0), dtype=np.float32)
+                                if d > 0 else np.nextafter(np.float32(k * 2.0 ** -23), np.float32(-1.0),
+                                                           dtype=np.float32) if d < 0 else np.float32(k * 2.0 ** -23)))
+    ps += rng.random(32).astype(np.float32).tolist()
+    hm = np.arange(65536, dtype=np.float32)
+    fills = np.arange(128, dtype=np.float64)
+    for p in ps:
+        p32 = np.float32(min(max(p, 0.0), 1.0))
+        x = np.float32(p32 * np.float32(65536.0))
+        up = hm < np.float32(x - np.float32(0.9921875))
+        open_ = ~up & (hm < x)
+        # whole-word decision for every (m, f): (128 m + f) * 2^-23 < p, exact in float64
+        whole = ((hm.astype(np.float64)[:, None] * 128.0 + fills[None, :]) * 2.0 ** -23) < np.float64(p32)
+        settled = ~open_
+        assert np.all(whole[settled & up]), p
+        assert not np.any(whole[settled & ~up]), p
+        frac = float(x) - np.floor(float(x))
+        assert int(open_.sum()) == (1 if 0.0 < frac <= 127.0 / 128.0 else 0), p

@@ -138,26 +138,33 @@ def test_search_index_exhaustive(q, lo, hi):
 
 @pytest.mark.parametrize("q,signed", [(orc.Q_SIGNED, True), (orc.Q_UNSIGNED, False)])
 def test_sr_records_and_reciprocal_quotient(q, signed):
-    """The moment-SR neighbour records: cb[li], the f32 gap cb[ui] - cb[li]
-    and the f32 nearest to 1/gap (exact rationals; 0 for an empty gap); and
-    the kernels' quotient fma(fma(-d, a*y, a), y, a*y) against IEEE a / d
-    (numpy float32) over dense samples of a in [0, d] for every gap: the
-    Bernoulli draw (uniform < p, uniform a multiple of 2^-23,
-    adam8.py:558-564) must decide alike for every uniform value."""
+    """The moment-SR neighbour records: per ui >= 1, cb[li], the f32 gap
+    cb[ui] - cb[li] times 2^-16 and the f32 nearest to 1/gap times 2^16
+    (exact rationals), so that the kernels' quotient fma(fma(-d', a*y',
+    a), y', a*y') comes out as x = 65536 p.  Against IEEE a / d (numpy
+    float32) over dense samples of a in [0, d] for every gap, x / 65536
+    must decide the Bernoulli draw (uniform < p, uniform a multiple of
+    2^-23, adam8.py:558-564) alike for every uniform value.  ui = 0
+    (n <= cb[0]) holds {-2, 0, 65536}: x >= 131072 for every such n, so
+    the kernel's "upper" pick is ui = 0 = li."""
     from fractions import Fraction
 
     cb = orc.codebook(signed)
     rec = _lib.host_sr_records(q)
+    assert rec[0].tolist() == [-2.0, 0.0, 65536.0, 0.0]
+    below = np.array([cb[0], np.nextafter(cb[0], np.float32(-2)), -1.0 if signed else -0.0], np.float32)
+    below = below[below >= -1]
+    x0 = orc.recip_quotient(below - np.float32(rec[0, 0]), float(rec[0, 1]), float(rec[0, 2]))
+    assert (x0 >= 131072.0).all(), x0
     rng = np.random.default_rng(21)
     exact_equal = total = 0
-    for ui in range(256):
-        li = max(ui - 1, 0)
+    for ui in range(1, 256):
+        li = ui - 1
         d = np.float32(cb[ui]) - np.float32(cb[li])
-        assert rec[ui, 0] == cb[li] and rec[ui, 1] == d and rec[ui, 3] == 0.0, ui
-        y = rec[ui, 2]
-        if d == 0.0:
-            assert ui == 0 and y == 0.0
-            continue
+        assert d > 0.0, ui
+        assert rec[ui, 0] == cb[li] and rec[ui, 1] == d * np.float32(2.0 ** -16) and rec[ui, 3] == 0.0, ui
+        y = np.float32(rec[ui, 2] / np.float32(65536.0))
+        assert np.float32(y * np.float32(65536.0)) == rec[ui, 2], ui
         inv = 1 / Fraction(float(d))
         err = abs(Fraction(float(y)) - inv)
         for c in (np.nextafter(y, np.float32(0)), np.nextafter(y, np.float32(np.inf))):
@@ -177,19 +184,18 @@ def test_sr_records_and_reciprocal_quotient(q, signed):
         ends = np.array([0.0, 1e-45, 2e-45, 1.2e-38, d, np.nextafter(d, np.float32(0))], np.float32)
         a = np.concatenate(near + [rand, ends])
         a = a[(a >= 0) & (a <= d)]
-        got = orc.recip_quotient(a, float(d), float(y)).astype(np.float64)
+        got = orc.recip_quotient(a, float(rec[ui, 1]), float(rec[ui, 2])).astype(np.float64)
         want = (a / d).astype(np.float32).astype(np.float64)
-        grid = 2.0 ** 23
-        bad = np.nonzero(np.ceil(got * grid) != np.ceil(want * grid))[0]
-        assert bad.size == 0, f"ui={ui} a={a[bad[0]]!r} p={got[bad[0]]!r} ieee={want[bad[0]]!r}"
-        assert (got >= 0).all() and (got <= 1).all()
+        bad = np.nonzero(np.ceil(got * 2.0 ** 7) != np.ceil(want * 2.0 ** 23))[0]
+        assert bad.size == 0, f"ui={ui} a={a[bad[0]]!r} x={got[bad[0]]!r} ieee={want[bad[0]]!r}"
+        assert (got >= 0).all() and (got <= 65536).all()
         assert ((got > 0) == (want > 0)).all(), ui
-        # the quotient is the IEEE one itself wherever p >= 2^-90; below, a
-        # subnormal a makes the correction term inexact (p < 2^-96 there),
-        # which only the sign of p could show to the draw
+        # x is 65536 times the IEEE quotient itself wherever p >= 2^-90;
+        # below, a subnormal a makes the correction term inexact (p < 2^-96
+        # there), which only the sign of p could show to the draw
         big = want >= 2.0 ** -90
-        diff = np.nonzero(big & (got != want))[0]
-        assert diff.size == 0, f"ui={ui} a={a[diff[0]]!r} p={got[diff[0]]!r} ieee={want[diff[0]]!r}"
-        exact_equal += int(np.sum(got == want))
+        diff = np.nonzero(big & (got != want * 65536.0))[0]
+        assert diff.size == 0, f"ui={ui} a={a[diff[0]]!r} x={got[diff[0]]!r} ieee={want[diff[0]]!r}"
+        exact_equal += int(np.sum(got == want * 65536.0))
         total += a.size
     assert exact_equal > 0.99 * total, (exact_equal, total)
