@@ -762,7 +762,38 @@ __device__ __forceinline__ RF_GLOBAL T* gstore_ptr(void* p, int64_t byte_off)
 // Native vectors for __builtin_nontemporal_store (HIP's uint2 / float4 are
 // structs, which the builtin does not take).
 typedef uint32_t nt_u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
 typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming accesses of the fast block path and the stream probe (params,
+// grads and codes; in update-only launches the updates): nontemporal loads
+// and stores, every byte being touched once per step.
+__device__ __forceinline__ uint4 ld_nt(const RF_GLOBAL uint4* p)
+{
+    const nt_u32x4 v = __builtin_nontemporal_load((const RF_GLOBAL nt_u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint2 ld_nt(const RF_GLOBAL uint2* p)
+{
+    const nt_u32x2 v = __builtin_nontemporal_load((const RF_GLOBAL nt_u32x2*)p);
+    return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ void st_nt(RF_GLOBAL uint4* p, uint4 v)
+{
+    __builtin_nontemporal_store(nt_u32x4{v.x, v.y, v.z, v.w}, (RF_GLOBAL nt_u32x4*)p);
+}
+
+__device__ __forceinline__ void st_nt(RF_GLOBAL uint2* p, uint2 v)
+{
+    __builtin_nontemporal_store(nt_u32x2{v.x, v.y}, (RF_GLOBAL nt_u32x2*)p);
+}
+
+__device__ __forceinline__ void st_nt(RF_GLOBAL float4* p, float4 v)
+{
+    __builtin_nontemporal_store(nt_f32x4{v.x, v.y, v.z, v.w}, (RF_GLOBAL nt_f32x4*)p);
+}
 
 // Element i of a T array, read or written through its global view.
 template <typename T>
@@ -1364,13 +1395,13 @@ __device__ __forceinline__ void issue_chunk(ChunkSlots<PT, GT>& sl, const rf_ada
     const RF_GLOBAL uint8_t* mB = (const RF_GLOBAL uint8_t*)L.mu + base;
     const RF_GLOBAL uint8_t* vB = (const RF_GLOBAL uint8_t*)L.nu + base;
     const uint32_t eo = (uint32_t)(j * 512 + lane * 8);
-    sl.mc[slot] = *(const RF_GLOBAL uint2*)(mB + eo);
-    sl.vc[slot] = *(const RF_GLOBAL uint2*)(vB + eo);
-    sl.graw[slot].w[0] = *(const RF_GLOBAL uint4*)(gB + eo * sizeof(GT));
-    if constexpr (sizeof(GT) == 4) sl.graw[slot].w[1] = *(const RF_GLOBAL uint4*)(gB + eo * 4 + 16);
+    sl.mc[slot] = ld_nt((const RF_GLOBAL uint2*)(mB + eo));
+    sl.vc[slot] = ld_nt((const RF_GLOBAL uint2*)(vB + eo));
+    sl.graw[slot].w[0] = ld_nt((const RF_GLOBAL uint4*)(gB + eo * sizeof(GT)));
+    if constexpr (sizeof(GT) == 4) sl.graw[slot].w[1] = ld_nt((const RF_GLOBAL uint4*)(gB + eo * 4 + 16));
     if constexpr (NEED_P) {
-        sl.praw[slot].w[0] = *(const RF_GLOBAL uint4*)(pB + eo * sizeof(PT));
-        if constexpr (sizeof(PT) == 4) sl.praw[slot].w[1] = *(const RF_GLOBAL uint4*)(pB + eo * 4 + 16);
+        sl.praw[slot].w[0] = ld_nt((const RF_GLOBAL uint4*)(pB + eo * sizeof(PT)));
+        if constexpr (sizeof(PT) == 4) sl.praw[slot].w[1] = ld_nt((const RF_GLOBAL uint4*)(pB + eo * 4 + 16));
     }
 }
 
@@ -1537,16 +1568,16 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
 #pragma unroll
                     for (int t = 0; t < 8; t += 2) w[t / 2] = pack_h16x2_rne<PT>(sum[t], sum[t + 1]);
                 }
-                *(RF_GLOBAL uint4*)(pB + eo * 2) = make_uint4(w[0], w[1], w[2], w[3]);
+                st_nt((RF_GLOBAL uint4*)(pB + eo * 2), make_uint4(w[0], w[1], w[2], w[3]));
             } else {
                 RF_GLOBAL float4* q = (RF_GLOBAL float4*)(pB + eo * 4);
-                q[0] = make_float4(sum[0], sum[1], sum[2], sum[3]);
-                q[1] = make_float4(sum[4], sum[5], sum[6], sum[7]);
+                st_nt(q, make_float4(sum[0], sum[1], sum[2], sum[3]));
+                st_nt(q + 1, make_float4(sum[4], sum[5], sum[6], sum[7]));
             }
         } else {
             RF_GLOBAL float4* q = gstore_ptr<float4>(L.updates, e0 * 4);
-            q[0] = make_float4(u[0], u[1], u[2], u[3]);
-            q[1] = make_float4(u[4], u[5], u[6], u[7]);
+            st_nt(q, make_float4(u[0], u[1], u[2], u[3]));
+            st_nt(q + 1, make_float4(u[4], u[5], u[6], u[7]));
         }
     }
 
@@ -1632,8 +1663,8 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                         wm[hh] = pack4_u8(cm[0], cm[1], cm[2], cm[3]);
                         wv[hh] = pack4_u8(cv[0], cv[1], cv[2], cv[3]);
                     }
-                    *(RF_GLOBAL uint2*)(mW + eo) = make_uint2(wm[0], wm[1]);
-                    *(RF_GLOBAL uint2*)(vW + eo) = make_uint2(wv[0], wv[1]);
+                    st_nt((RF_GLOBAL uint2*)(mW + eo), make_uint2(wm[0], wm[1]));
+                    st_nt((RF_GLOBAL uint2*)(vW + eo), make_uint2(wv[0], wv[1]));
                 }
             } else {
 #pragma unroll
@@ -1656,7 +1687,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                     uint2 w;
                     w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
                     w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
-                    *(RF_GLOBAL uint2*)(mW + eo) = w;
+                    st_nt((RF_GLOBAL uint2*)(mW + eo), w);
                 }
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
@@ -1678,7 +1709,7 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                     uint2 w;
                     w.x = pack4_u8(cc[0], cc[1], cc[2], cc[3]);
                     w.y = pack4_u8(cc[4], cc[5], cc[6], cc[7]);
-                    *(RF_GLOBAL uint2*)(vW + eo) = w;
+                    st_nt((RF_GLOBAL uint2*)(vW + eo), w);
                 }
             }
         } else {
@@ -1715,8 +1746,8 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                 wm.y = pack4_u8(cm[4], cm[5], cm[6], cm[7]);
                 wv.x = pack4_u8(cv[0], cv[1], cv[2], cv[3]);
                 wv.y = pack4_u8(cv[4], cv[5], cv[6], cv[7]);
-                *(RF_GLOBAL uint2*)(mW + eo) = wm;
-                *(RF_GLOBAL uint2*)(vW + eo) = wv;
+                st_nt((RF_GLOBAL uint2*)(mW + eo), wm);
+                st_nt((RF_GLOBAL uint2*)(vW + eo), wv);
             }
         }
         if (lane == 0) {
@@ -2329,14 +2360,14 @@ __device__ __forceinline__ void probe_block(const rf_adam8_leaf& L, int64_t blk)
         opaque(p0);
         opaque(sl.graw[slot].w[0]);
         if constexpr (sizeof(GT) == 4) opaque(sl.graw[slot].w[1]);
-        *(RF_GLOBAL uint4*)(pB + eo * sizeof(PT)) = p0;
+        st_nt((RF_GLOBAL uint4*)(pB + eo * sizeof(PT)), p0);
         if constexpr (sizeof(PT) == 4) {
             uint4 p1 = sl.praw[slot].w[1];
             opaque(p1);
-            *(RF_GLOBAL uint4*)(pB + eo * 4 + 16) = p1;
+            st_nt((RF_GLOBAL uint4*)(pB + eo * 4 + 16), p1);
         }
-        *(RF_GLOBAL uint2*)(mW + eo) = mc;
-        *(RF_GLOBAL uint2*)(vW + eo) = vc;
+        st_nt((RF_GLOBAL uint2*)(mW + eo), mc);
+        st_nt((RF_GLOBAL uint2*)(vW + eo), vc);
     }
     uint32_t smb = __float_as_uint(sm), svb = __float_as_uint(sv);
     opaque(smb);
