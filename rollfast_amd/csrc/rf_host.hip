@@ -261,7 +261,7 @@ __global__ __launch_bounds__(WG) void k_dequantize(int32_t quantizer, const uint
 // jax.random.bits.  Vector path: a wave takes two 1024-element tiles per
 // iteration, each lane four consecutive elements per 256-element row (one
 // 16-byte load; with the packed source exactly one block), all loads of the
-// two tiles issued before the rounding; nontemporal 8-byte stores.
+// two tiles issued before the rounding; nontemporal loads and 8-byte stores.
 template <bool PACKED>
 __global__ __launch_bounds__(WG) void k_sr_bf16(const float* __restrict__ x, int64_t size, uint32_t k0,
                                                 uint32_t k1, const uint32_t* __restrict__ bits,
@@ -281,8 +281,10 @@ __global__ __launch_bounds__(WG) void k_sr_bf16(const float* __restrict__ x, int
             for (int k = 0; k < 4; ++k) {
                 const int64_t e = (t0 + u) * 1024 + k * 256 + lane * 4;
                 if (t0 + u < ntiles) {
-                    xv[u][k] = *(const float4*)(x + e);
-                    if (bits) fb[u][k] = *(const uint4*)(bits + e);
+                    const uint4 w = ldg_nt(x + e);
+                    xv[u][k] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z),
+                                           __uint_as_float(w.w));
+                    if (bits) fb[u][k] = ldg_nt(bits + e);
                 }
             }
         }
