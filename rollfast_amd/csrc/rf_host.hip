@@ -517,21 +517,29 @@ __global__ __launch_bounds__(WG) void k_accumulate(const rf_accum_leaf* __restri
 // scale = min(1, max_norm / (norm + 1e-6)) with NaN propagating.
 constexpr int64_t NORM_UNIT = 16384;
 
-// Work units (blocks or chunks) per wave of a step launch (see plan_launch).
+// Work units per wave of the work-list kernels (worklist_grid).
 constexpr int64_t STEP_UNITS_PER_WAVE = 16;
-// Fast-kernel waves take runs of RUN_UNITS consecutive blocks, and the grid
-// is a whole number of chip-fulls of workgroups.  Measured against one block
-// per run and a free grid (same box, three runs each): Llama-7B 13.47 ->
-// 13.38 ms, with param SR 21.09 -> 20.62 ms, GPT-2-small 0.57 -> 0.52 ms,
-// the ragged tree 0.64 -> 0.57 ms; runs of 2, 8 and 16 were no better
-// overall.
-#ifndef RF_STEP_RUN_UNITS
-#define RF_STEP_RUN_UNITS 4
-#endif
+// Launch shape of a step (step_grid): waves take runs of consecutive blocks
+// before their grid stride, about `per_wave` units each, and the grid is a
+// whole number of chip-fulls of workgroups.  The fused nearest-rounding
+// steps of the hardware direction (the memory-bound instances) take runs of
+// 2 and 8 units per wave; the others (stochastic rounding, the IEEE
+// direction, update-only) runs of 4 and 16.  Both shapes in turn on one box
+// (two processes each): the Llama-7B step 12.78 -> 12.51 ms, with f32
+// params 20.1-20.6 -> 19.1-19.6 ms, the ragged tree 0.467-0.473 -> 0.457-
+// 0.465 ms; under the short shape moment SR ran 1.3 %, exact mode 2 % and
+// the update-only step 0.5 % slower.  Runs of 1 were 1-6 % slower than
+// either, and earlier (plain accesses) runs of 4 beat one block per run and
+// a free grid by 0.7 % (Llama-7B) to 11 % (the ragged tree).
+struct StepShape {
+    int32_t run;
+    int64_t per_wave;
+};
+constexpr StepShape STEP_SHAPE_STREAM = {2, 8};
+constexpr StepShape STEP_SHAPE_HEAVY = {4, 16};
 #ifndef RF_STEP_GRID_ROUNDS
 #define RF_STEP_GRID_ROUNDS 1
 #endif
-constexpr int64_t STEP_RUN_UNITS = RF_STEP_RUN_UNITS;
 constexpr bool STEP_GRID_ROUNDS = RF_STEP_GRID_ROUNDS != 0;
 
 __global__ __launch_bounds__(WG) void k_gnorm_partial(const rf_adam8_leaf* __restrict__ leaves,
@@ -1664,7 +1672,7 @@ rf_status build_work_lists(const rf_adam8_leaf* leaves, int32_t n_leaves, int32_
     return RF_OK;
 }
 
-int64_t step_grid(const DevState* ds, int occ, const PlanGroup& g, int32_t run);
+int64_t step_grid(const DevState* ds, int occ, const PlanGroup& g, int32_t run, int64_t per_wave);
 void find_carrier(const std::vector<PlanGroup>& groups, bool msr, const PlanGroup** gen, const PlanGroup** carrier);
 
 }  // namespace
@@ -1820,8 +1828,9 @@ rf_status rf_adam8_plan_stream_probe(const rf_adam8_plan* plan, void* stream, in
         int occ = 1;
         st = occupancy((const void*)fn, &occ);
         if (st != RF_OK) return st;
-        const int32_t run = (int32_t)STEP_RUN_UNITS;
-        const int64_t grid = step_grid(ds, occ, g, run);
+        // the shape of the default (fused, nearest, hardware direction) step
+        const int32_t run = STEP_SHAPE_STREAM.run;
+        const int64_t grid = step_grid(ds, occ, g, run, STEP_SHAPE_STREAM.per_wave);
         const Seg* segs = plan->d_segs + g.seg_offset;
         const hipStream_t s = (hipStream_t)stream;
         switch (g.combo) {
@@ -1887,13 +1896,13 @@ void find_carrier(const std::vector<PlanGroup>& groups, bool msr, const PlanGrou
 
 // Workgroups of one step launch over list g with `run` consecutive units per
 // wave turn, for a kernel of `occ` workgroups per CU.
-int64_t step_grid(const DevState* ds, int occ, const PlanGroup& g, int32_t run)
+int64_t step_grid(const DevState* ds, int occ, const PlanGroup& g, int32_t run, int64_t per_wave)
 {
     const int64_t runs = (g.units + run - 1) / run;
     const int64_t wg_needed = (runs + WAVES_PER_WG - 1) / WAVES_PER_WG;
     const int64_t wg_resident = (int64_t)ds->num_cus * occ;
-    const int64_t wg_spread = std::min(
-        wg_needed, (g.units + (int64_t)WAVES_PER_WG * STEP_UNITS_PER_WAVE - 1) / (WAVES_PER_WG * STEP_UNITS_PER_WAVE));
+    const int64_t wg_spread =
+        std::min(wg_needed, (g.units + (int64_t)WAVES_PER_WG * per_wave - 1) / ((int64_t)WAVES_PER_WG * per_wave));
     int64_t grid = std::max<int64_t>(1, std::max(std::min(wg_needed, wg_resident), wg_spread));
     const int64_t wg_each = g.lead + (g.units - g.lead + WAVES_PER_WG - 1) / WAVES_PER_WG;
     if (g.combo == -1 && wg_each <= GEN_WAVE_PER_UNIT_MAX_ROUNDS * wg_resident) {
@@ -2027,19 +2036,20 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         int occ = 1;
         st = occupancy((const void*)fn, &occ);
         if (st != RF_OK) return st;
-        // About STEP_UNITS_PER_WAVE units per wave, never fewer workgroups
-        // than fit on the chip at once.  On the Llama-7B tree this measured
-        // 3-5 % faster than one persistent grid (8 to 32 units per wave
-        // within noise of each other); one unit per wave is 26 % slower
-        // (the lookup tables are staged per workgroup).  Rounding the grid to
-        // whole chip-fulls removes a last, mostly idle round of workgroups
-        // (the ragged tree's 1,570 workgroups on 768 slots become 1,536,
-        // GPT-2-small's 943 become 768).
-        k.run = g.combo >= 0 ? (int32_t)STEP_RUN_UNITS : 1;
-        int64_t grid = step_grid(ds, occ, g, k.run);
+        // About shape.per_wave units per wave, never fewer workgroups than
+        // fit on the chip at once.  On the Llama-7B tree this measured 3-5 %
+        // faster than one persistent grid; one unit per wave is 26 % slower
+        // (the lookup tables are staged per workgroup).  Rounding the grid
+        // to whole chip-fulls removes a last, mostly idle round of
+        // workgroups (the ragged tree's 1,570 workgroups on 768 slots become
+        // 1,536, GPT-2-small's 943 become 768).
+        const bool streaming = plan->apply && !msr && !psr && !(f & RF_EXACT);
+        const StepShape shape = streaming ? STEP_SHAPE_STREAM : STEP_SHAPE_HEAVY;
+        k.run = g.combo < 0 ? 1 : shape.run;
+        int64_t grid = step_grid(ds, occ, g, k.run, shape.per_wave);
         KHp kg = k;
         if (&g == carrier) {
-            const int64_t ggrid = step_grid(ds, occ, *gen, 1);
+            const int64_t ggrid = step_grid(ds, occ, *gen, 1, shape.per_wave);
             if (ggrid > INT32_MAX || grid + ggrid > (int64_t)UINT32_MAX)
                 return fail(RF_ERR_UNSUPPORTED, "step grid beyond 2^32 - 1 workgroups");
             kg.gsegs = plan->d_segs + gen->seg_offset;
