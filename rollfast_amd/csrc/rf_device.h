@@ -501,11 +501,8 @@ __device__ __forceinline__ uint32_t cand_unsigned(const uint8_t* lds, float n)
 // test checks it against IEEE division over every gap).  Since cb[li] < n
 // <= cb[ui], 0 <= x <= 65536 needs no clip.  ui = 0 (n <= cb[0], where the
 // reference's clip leaves li = ui = 0) finds {-2, 0, 65536}: a = n + 2 >= 1
-// and x = 2a 65536 exceeds every draw, so "upper" picks ui.  The lower code
-// is written max(ui - 1, 0) all the same: a select of ui and ui - 1 is
-// rewritten by the compiler as ui minus the "lower" bit, which keeps a
-// batch's lane masks in scalar registers across the packed source's fill
-// branch, and the moment-SR kernels then spill.
+// and x = 2a 65536 exceeds every draw, so "upper" picks ui and the code
+// ui - 1 + up needs no clamp (code_of_draw).
 __device__ __forceinline__ float sr_upper(const float* cb, const float4* rec, uint32_t& cand, float n)
 {
     const uint32_t ui = cand + (cb[cand] < n ? 1u : 0u);
@@ -524,10 +521,30 @@ __device__ __forceinline__ float uniform_from_bits_x65536(uint32_t bits)
     return __uint_as_float(__builtin_amdgcn_alignbit(0x8Fu, bits, 9)) - 65536.0f;
 }
 
+// ui - 1 + up, the code of a draw: one v_addc whose carry-in is up's lane
+// mask (the ui = 0 record makes up true there).  Written as asm: from C the
+// compiler emits a select and a clamped subtract, or, as ui minus the
+// "lower" bit, keeps a batch's masks in scalar registers across the packed
+// source's fill branch and spills.  The s_nop gives the two wait states a
+// lane mask written by a vector compare needs before a vector instruction
+// reads it as a carry, which the compiler cannot see inside the asm.
+__device__ __forceinline__ uint32_t code_of_draw(uint32_t ui, uint64_t up_mask)
+{
+    uint32_t r;
+    uint64_t carry_out;
+    __asm__("s_nop 1\n\tv_addc_co_u32_e64 %0, %1, -1, %2, %3" : "=v"(r), "=s"(carry_out) : "v"(ui), "s"(up_mask));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t code_of_draw(uint32_t ui, bool up)
+{
+    return code_of_draw(ui, __builtin_amdgcn_ballot_w64(up));
+}
+
 // The code from ui and x = 65536 p (sr_upper) and a 32-bit draw.
 __device__ __forceinline__ uint32_t sr_decide(uint32_t ui, float x, uint32_t bits)
 {
-    return uniform_from_bits_x65536(bits) < x ? ui : __builtin_elementwise_sub_sat(ui, 1u);
+    return code_of_draw(ui, uniform_from_bits_x65536(bits) < x);
 }
 
 __device__ __forceinline__ uint32_t sr_code(const float* cb, const float4* rec, uint32_t cand, float n,
@@ -541,17 +558,19 @@ __device__ __forceinline__ uint32_t sr_code(const float* cb, const float4* rec, 
 // the draw is k = 128 m + f (f, the fill's top 7 bits, below 128) and takes
 // the upper code iff k 2^-23 < p, i.e. m + f / 128 < x = 65536 p (sr_upper's
 // result).  m + 127/128 < x settles "upper" whatever f is, and m >= x
-// settles "lower"; between the two `open` is set, and the caller decides
-// with the fill (sr_decide on the whole word).  x - 127/128 is exact where
-// it is not negative (127/128 is a multiple of x's ulp while x < 2^17) and
-// negative otherwise, where "upper" is rightly not settled; the ui = 0
-// record's x >= 131072 settles "upper".
-__device__ __forceinline__ uint32_t packed_sr_main(uint32_t ui, float x, uint32_t m, bool& open)
+// settles "lower"; the lanes between the two are added to `open` (a lane
+// mask), and the caller decides them with the fill (sr_decide on the whole
+// word).  x - 127/128 is exact where it is not negative (127/128 is a
+// multiple of x's ulp while x < 2^17) and negative otherwise, where "upper"
+// is rightly not settled; the ui = 0 record's x >= 131072 settles "upper".
+// The two compares stay lane masks, combined in scalar registers.
+__device__ __forceinline__ uint32_t packed_sr_main(uint32_t ui, float x, uint32_t m, uint64_t& open)
 {
     const float hm = (float)m;
-    const bool up = hm < x - 0.9921875f;
-    open = open || (!up && hm < x);
-    return up ? ui : __builtin_elementwise_sub_sat(ui, 1u);
+    const uint64_t up = __builtin_amdgcn_ballot_w64(hm < x - 0.9921875f);
+    const uint64_t below = __builtin_amdgcn_ballot_w64(hm < x);
+    open |= below & ~up;
+    return code_of_draw(ui, up);
 }
 
 // Signed dynamic codebook code of x in a block with scale s (fast path;
@@ -1664,13 +1683,16 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                             pm[t] = sr_upper(cbs, srs, um[t], nm[t]);
                             pv[t] = sr_upper(cbu, sru, uv[t], nv[t]);
                         }
-                        bool open = false;
+                        uint64_t open = 0;
 #pragma unroll
                         for (int t = 0; t < 4; ++t) {
                             cm[t] = packed_sr_main(um[t], pm[t], half16(ym[t >> 1], t), open);
                             cv[t] = packed_sr_main(uv[t], pv[t], half16(yv[t >> 1], t), open);
                         }
-                        if (__builtin_expect(open, 0)) {
+                        // a wave with an open draw decides all of its
+                        // lanes' draws on whole words (the same codes
+                        // wherever the main half settled them)
+                        if (__builtin_expect(open != 0, 0)) {
                             uint32_t zm[2], zv[2];
 #pragma unroll
                             for (int pr = 0; pr < 2; ++pr)
