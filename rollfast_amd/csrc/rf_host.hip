@@ -338,6 +338,42 @@ __device__ __forceinline__ uint32_t apply_bf16(float p, float u, bool stochastic
 // per wave (a ragged tree launches no idle workgroups).
 constexpr int64_t APPLY_UNIT = 8192;
 
+// Four consecutive elements e0 .. e0 + 3 (e0 a multiple of 4, the buffer
+// 16-byte aligned), read and written nontemporally: f32 values, uint32
+// words, or 16-bit patterns as two words.
+__device__ __forceinline__ void ld4_f32_nt(const void* base, int64_t e0, float (&x)[4])
+{
+    const nt_u32x4 v = __builtin_nontemporal_load((const nt_u32x4*)((const float*)base + e0));
+    x[0] = __uint_as_float(v.x);
+    x[1] = __uint_as_float(v.y);
+    x[2] = __uint_as_float(v.z);
+    x[3] = __uint_as_float(v.w);
+}
+
+__device__ __forceinline__ void ld4_u32_nt(const uint32_t* base, int64_t e0, uint32_t (&x)[4])
+{
+    const nt_u32x4 v = __builtin_nontemporal_load((const nt_u32x4*)(base + e0));
+    x[0] = v.x;
+    x[1] = v.y;
+    x[2] = v.z;
+    x[3] = v.w;
+}
+
+__device__ __forceinline__ nt_u32x2 ld4_h16_nt(const void* base, int64_t e0)
+{
+    return __builtin_nontemporal_load((const nt_u32x2*)((const uint16_t*)base + e0));
+}
+
+__device__ __forceinline__ void st4_h16_nt(void* base, int64_t e0, uint32_t w0, uint32_t w1)
+{
+    __builtin_nontemporal_store(nt_u32x2{w0, w1}, (nt_u32x2*)((uint16_t*)base + e0));
+}
+
+__device__ __forceinline__ void st4_f32_nt(void* base, int64_t e0, const float (&x)[4])
+{
+    __builtin_nontemporal_store(nt_f32x4{x[0], x[1], x[2], x[3]}, (nt_f32x4*)((float*)base + e0));
+}
+
 // `factor` (Magma's fused form, or null): each update is first taken as
 // neg_lr * (factor[leaf] * u), the scaling rf_magma_scale would have done.
 // Segment s of `segs` is leaf segs[s].leaf.  SR: stochastic rounding of bf16
@@ -375,48 +411,82 @@ __global__ __launch_bounds__(WG) void k_apply(const rf_apply_leaf* __restrict__ 
         }
         const int64_t e_begin = (u_ - segs[s].unit_start) * APPLY_UNIT;
         const int64_t e_end = min(L.size, e_begin + APPLY_UNIT);
-        // 8 elements per lane and step over the unit's whole groups of 8
-        const int64_t v_end = vec ? e_begin + ((e_end - e_begin) / 8) * 8 : e_begin;
-        for (int64_t e0 = e_begin + lane * 8; e0 < v_end; e0 += WAVE * 8) {
-            float u[8], p[8];
-            load8<float>(L.updates, e0, u);
+        // Whole groups of 512 elements: lane l takes elements 4l .. 4l + 3
+        // and 256 + 4l .. 256 + 4l + 3 of a group, so that each load and
+        // store instruction of the wave covers whole cache lines (16-bit
+        // params 512 bytes, f32 updates and params 1 KB), all of them
+        // nontemporal; the unit's last partial group goes element-wise.
+        // (Eight consecutive elements per lane put each f32 access on half
+        // of every line it touches.)
+        const int64_t v_end = vec ? e_begin + ((e_end - e_begin) / 512) * 512 : e_begin;
+        for (int64_t g0 = e_begin; g0 < v_end; g0 += 512) {
+            int64_t e0[2];
+            float u[2][4], p[2][4];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) e0[hf] = g0 + hf * 256 + lane * 4;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) ld4_f32_nt(L.updates, e0[hf], u[hf]);
+            if (L.param_dtype == RF_F32) {
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) ld4_f32_nt(L.param, e0[hf], p[hf]);
+            } else {
+                nt_u32x2 w[2];
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) w[hf] = ld4_h16_nt(L.param, e0[hf]);
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    const uint32_t d[2] = {w[hf].x, w[hf].y};
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        if (L.param_dtype == RF_F16) {
+                            p[hf][2 * i] = f16_bits_to_f32(d[i] & 0xFFFFu);
+                            p[hf][2 * i + 1] = f16_bits_to_f32(d[i] >> 16);
+                        } else {
+                            p[hf][2 * i] = __uint_as_float(d[i] << 16);
+                            p[hf][2 * i + 1] = __uint_as_float(d[i] & 0xFFFF0000u);
+                        }
+                    }
+                }
+            }
             if (factor) {
 #pragma unroll
-                for (int t = 0; t < 8; ++t) u[t] = neg_lr * (f * u[t]);
-            }
-            if (L.param_dtype == RF_F16) {
-                load8<_Float16>(L.param, e0, p);
-                uint32_t h[8];
+                for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-                for (int t = 0; t < 8; ++t) h[t] = f32_to_f16_rne(p[t] + u[t]);  // no SR below bf16 (utils.py:700)
-                store8_bf16(L.param, e0, h);
-            } else if (L.param_dtype == RF_BF16) {
-                load8<uint16_t>(L.param, e0, p);
-                uint32_t h[8];
-                if constexpr (SR) {
-                    uint32_t rb[8];
-                    if (L.bits) {
-                        load8_u32(L.bits, e0, rb);
-                    } else if constexpr (PACKED) {
-                        packed_param_bits4(lk0, lk1, (uint64_t)e0, rb);  // e0: a multiple of 8
-                        packed_param_bits4(lk0, lk1, (uint64_t)e0 + 4, rb + 4);
+                    for (int t = 0; t < 4; ++t) u[hf][t] = neg_lr * (f * u[hf][t]);
+            }
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                if (L.param_dtype == RF_F16) {
+                    uint32_t h[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) h[t] = f32_to_f16_rne(p[hf][t] + u[hf][t]);  // no SR below bf16 (utils.py:700)
+                    st4_h16_nt(L.param, e0[hf], h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+                } else if (L.param_dtype == RF_BF16) {
+                    uint32_t h[4];
+                    if constexpr (SR) {
+                        uint32_t rb[4];
+                        if (L.bits) {
+                            ld4_u32_nt(L.bits, e0[hf], rb);
+                        } else if constexpr (PACKED) {
+                            packed_param_bits4(lk0, lk1, (uint64_t)e0[hf], rb);  // e0: a multiple of 4
+                        } else {
+#pragma unroll
+                            for (int t = 0; t < 4; ++t) rb[t] = jax_bits(lk0, lk1, (uint64_t)(e0[hf] + t));
+                        }
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) h[t] = sr_bf16_hi(p[hf][t] + u[hf][t], rb[t]);
+                        st4_h16_nt(L.param, e0[hf], pack_hi16x2(h[0], h[1]), pack_hi16x2(h[2], h[3]));
                     } else {
 #pragma unroll
-                        for (int t = 0; t < 8; ++t) rb[t] = jax_bits(lk0, lk1, (uint64_t)(e0 + t));
+                        for (int t = 0; t < 4; ++t) h[t] = f32_to_bf16_rne(p[hf][t] + u[hf][t]);
+                        st4_h16_nt(L.param, e0[hf], h[0] | (h[1] << 16), h[2] | (h[3] << 16));
                     }
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) h[t] = sr_bf16_hi(p[t] + u[t], rb[t]);
-                    store8_hi16(L.param, e0, h);
                 } else {
+                    float o[4];
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) h[t] = f32_to_bf16_rne(p[t] + u[t]);
-                    store8_bf16(L.param, e0, h);
+                    for (int t = 0; t < 4; ++t) o[t] = p[hf][t] + u[hf][t];
+                    st4_f32_nt(L.param, e0[hf], o);
                 }
-            } else {
-                load8<float>(L.param, e0, p);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) p[t] = p[t] + u[t];
-                store8_f32(L.param, e0, p);
             }
         }
         for (int64_t e = v_end + lane; e < e_end; e += WAVE) {
