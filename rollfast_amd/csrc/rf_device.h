@@ -91,6 +91,7 @@ struct KHp {
     float neg_lr;             // f32(-lr), or 1.0 when the chain has no learning-rate scale
     uint32_t flags;
     int32_t run;              // fast kernel: consecutive units a wave takes before its grid stride (>= 1)
+    int32_t upd_nt;           // update-only fast kernel: nontemporal update stores
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;
     const float* clip;        // device (scale, norm) of global-norm clipping, or null
     const float* gate;        // device flag: 1 = every grad finite, 0 = reject the step; null = no gate
@@ -811,6 +812,11 @@ __device__ __forceinline__ void st_nt(RF_GLOBAL uint2* p, uint2 v)
     __builtin_nontemporal_store(nt_u32x2{v.x, v.y}, (RF_GLOBAL nt_u32x2*)p);
 }
 
+__device__ __forceinline__ void st_nt(RF_GLOBAL float4* p, float4 v)
+{
+    __builtin_nontemporal_store(nt_f32x4{v.x, v.y, v.z, v.w}, (RF_GLOBAL nt_f32x4*)p);
+}
+
 
 // A nontemporal 16-byte load through a generic pointer (the standalone
 // stochastic rounding's input).  Plain accesses stay in the vector I/O
@@ -952,6 +958,7 @@ __device__ __forceinline__ void store_scale(float* scales, uint32_t leaf_flags, 
 struct UnitCtx {
     const uint8_t* lds;
     float* wtab;  // this wave's 512-float LDS region (dequant-and-decay tables)
+    float* xbuf;  // update-only fast kernel: this wave's 512-float LDS region for the update stores
     int32_t wd_mode;
     bool fed;
     bool packed;      // RF_PACKED_BITS without fed bits
@@ -1615,9 +1622,32 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                 q[1] = make_float4(sum[4], sum[5], sum[6], sum[7]);
             }
         } else {
-            RF_GLOBAL float4* q = gstore_ptr<float4>(L.updates, e0 * 4);
-            q[0] = make_float4(u[0], u[1], u[2], u[3]);
-            q[1] = make_float4(u[4], u[5], u[6], u[7]);
+            // The chunk's updates pass through this wave's LDS region: a
+            // lane's eight consecutive f32 would put each 16-byte store on
+            // half of every cache line it touches, so lane l stores elements
+            // 4l .. 4l + 3 and 256 + 4l .. 256 + 4l + 3 instead, every store
+            // instruction on whole lines; nontemporal in launches of many
+            // blocks (h.upd_nt), where no cache keeps the updates for the
+            // apply that reads them next.
+            float* xb = c.xbuf;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            *(float4*)(xb + lane * 8) = make_float4(u[0], u[1], u[2], u[3]);
+            *(float4*)(xb + lane * 8 + 4) = make_float4(u[4], u[5], u[6], u[7]);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const float4 a = *(const float4*)(xb + lane * 4);
+            const float4 b = *(const float4*)(xb + 256 + lane * 4);
+            RF_GLOBAL float4* q = gstore_ptr<float4>(L.updates, (base + j * 512) * 4);
+            if (h.upd_nt) {
+                st_nt(q + lane, a);
+                st_nt(q + 64 + lane, b);
+            } else {
+                q[lane] = a;
+                q[64 + lane] = b;
+            }
         }
     }
 
@@ -2318,6 +2348,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     UnitCtx c;
     c.lds = lds;
     c.wtab = wtab[wave_in_wg];
+    c.xbuf = nullptr;
+    if constexpr (!APPLY) {
+        __shared__ __attribute__((aligned(16))) float xbuf[WAVES_PER_WG][512];
+        c.xbuf = xbuf[wave_in_wg];
+    }
     c.fed = (h.flags & RF_FED_BITS) != 0;
     c.packed = !c.fed && (h.flags & RF_PACKED_BITS) != 0;
     c.zero = false;  // quantized blocks only: RF_LEAF_ZERO_DECAY is refused for them
