@@ -335,8 +335,11 @@ __device__ __forceinline__ uint32_t apply_bf16(float p, float u, bool stochastic
 }
 
 // Work units of apply_updates: APPLY_UNIT consecutive elements of one leaf
-// per wave (a ragged tree launches no idle workgroups).
-constexpr int64_t APPLY_UNIT = 8192;
+// per wave (a ragged tree launches no idle workgroups).  On the Llama-7B
+// tree (packed SR, one box, two processes each) units of 8192, 4096 and
+// 2048 elements ran 10.50-10.59, 10.12-10.13 and 10.02-10.05 ms (the grid
+// grows with the unit count); GPT-2-small's launch 215-222 us in each.
+constexpr int64_t APPLY_UNIT = 2048;
 
 // Four consecutive elements e0 .. e0 + 3 (e0 a multiple of 4, the buffer
 // 16-byte aligned), read and written nontemporally: f32 values, uint32
