@@ -396,7 +396,7 @@ __device__ __forceinline__ double wave_sum_f64(double x)
 // kernel's start, where the compiler spilled them (28 KB of scratch writes
 // per workgroup); with the DMA form the moment-SR step ran 1 % faster, while
 // the nearest-rounding step measured 0.3 % slower with it than with
-// registers (same box, alternating runs).
+// registers (same GPU, alternating runs).
 template <uint32_t BYTES = TABLE_BYTES>
 __device__ __forceinline__ void stage_tables(uint8_t* lds, const uint4* __restrict__ tables)
 {

@@ -336,7 +336,7 @@ __device__ __forceinline__ uint32_t apply_bf16(float p, float u, bool stochastic
 
 // Work units of apply_updates: APPLY_UNIT consecutive elements of one leaf
 // per wave (a ragged tree launches no idle workgroups).  On the Llama-7B
-// tree (packed SR, one box, two processes each) units of 8192, 4096 and
+// tree (packed SR, one GPU, two processes each) units of 8192, 4096 and
 // 2048 elements ran 10.50-10.59, 10.12-10.13 and 10.02-10.05 ms (the grid
 // grows with the unit count); GPT-2-small's launch 215-222 us in each.
 constexpr int64_t APPLY_UNIT = 2048;
@@ -597,7 +597,7 @@ constexpr int64_t STEP_UNITS_PER_WAVE = 16;
 // whole number of chip-fulls of workgroups.  The fused nearest-rounding
 // steps of the hardware direction (the memory-bound instances) take runs of
 // 2 and 8 units per wave; the others (stochastic rounding, the IEEE
-// direction, update-only) runs of 4 and 16.  Both shapes in turn on one box
+// direction, update-only) runs of 4 and 16.  Both shapes in turn on one GPU
 // (two processes each): the Llama-7B step 12.78 -> 12.51 ms, with f32
 // params 20.1-20.6 -> 19.1-19.6 ms, the ragged tree 0.467-0.473 -> 0.457-
 // 0.465 ms; under the short shape moment SR ran 1.3 %, exact mode 2 % and
@@ -2125,7 +2125,7 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         k.run = g.combo < 0 ? 1 : shape.run;
         // Update-only launches store their f32 updates on whole cache lines;
         // nontemporally from UPD_NT_MIN_BLOCKS_PER_CU blocks per CU on.
-        // Three store forms on one box (old half-line plain / whole-line
+        // Three store forms on one GPU (old half-line plain / whole-line
         // nontemporal / whole-line plain): the Llama-7B update-only step
         // 13.98-14.77 / 13.17-13.22 / 13.50-13.56 ms, GPT-2-small's launch
         // 265 / 294 / 256 us.
