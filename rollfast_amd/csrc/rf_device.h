@@ -91,7 +91,7 @@ struct KHp {
     float neg_lr;             // f32(-lr), or 1.0 when the chain has no learning-rate scale
     uint32_t flags;
     int32_t run;              // fast kernel: consecutive units a wave takes before its grid stride (>= 1)
-    int32_t upd_nt;           // update-only fast kernel: nontemporal update stores
+    int32_t upd_nt;           // fast kernel: nontemporal f32 update and param stores (store8_f32_lines)
     uint32_t kmu0, kmu1, knu0, knu1, kp0, kp1;
     const float* clip;        // device (scale, norm) of global-norm clipping, or null
     const float* gate;        // device flag: 1 = every grad finite, 0 = reject the step; null = no gate
@@ -1457,6 +1457,34 @@ __device__ __forceinline__ void issue_chunk(ChunkSlots<PT, GT>& sl, const rf_ada
 // the same leaf; its chunk 0 is loaded into slot 0 while this block is
 // requantized, so the wave keeps memory traffic in flight through the
 // arithmetic-only requantization phase.
+// A lane's eight consecutive f32 values (chunk elements 8l .. 8l + 7) stored
+// on whole cache lines: they pass through the wave's 512-float LDS region
+// `xb`, and lane l stores elements 4l .. 4l + 3 and 256 + 4l .. 256 + 4l + 3
+// of the 512-element chunk at `chunk` (eight consecutive f32 per lane would
+// put each 16-byte store on half of every line it touches); nontemporal if
+// `nt`.
+__device__ __forceinline__ void store8_f32_lines(float* xb, RF_GLOBAL float4* chunk, int lane, const float (&x)[8],
+                                                 bool nt)
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    *(float4*)(xb + lane * 8) = make_float4(x[0], x[1], x[2], x[3]);
+    *(float4*)(xb + lane * 8 + 4) = make_float4(x[4], x[5], x[6], x[7]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float4 a = *(const float4*)(xb + lane * 4);
+    const float4 b = *(const float4*)(xb + 256 + lane * 4);
+    if (nt) {
+        st_nt(chunk + lane, a);
+        st_nt(chunk + 64 + lane, b);
+    } else {
+        chunk[lane] = a;
+        chunk[64 + lane] = b;
+    }
+}
+
 template <typename PT, typename GT, int WDM, bool APPLY, bool MSR, bool PSR, bool NEST, bool EXACT, bool ER,
           bool FLR = false>
 __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf& L, int64_t blk, const KHp& h,
@@ -1617,37 +1645,13 @@ __device__ __forceinline__ void unit_qfast(const UnitCtx& c, const rf_adam8_leaf
                 }
                 st_nt((RF_GLOBAL uint4*)(pB + eo * 2), make_uint4(w[0], w[1], w[2], w[3]));
             } else {
-                RF_GLOBAL float4* q = (RF_GLOBAL float4*)(pB + eo * 4);
-                q[0] = make_float4(sum[0], sum[1], sum[2], sum[3]);
-                q[1] = make_float4(sum[4], sum[5], sum[6], sum[7]);
+                store8_f32_lines(c.xbuf, (RF_GLOBAL float4*)(pB + j * 512 * 4), lane, sum, h.upd_nt != 0);
             }
         } else {
-            // The chunk's updates pass through this wave's LDS region: a
-            // lane's eight consecutive f32 would put each 16-byte store on
-            // half of every cache line it touches, so lane l stores elements
-            // 4l .. 4l + 3 and 256 + 4l .. 256 + 4l + 3 instead, every store
-            // instruction on whole lines; nontemporal in launches of many
-            // blocks (h.upd_nt), where no cache keeps the updates for the
-            // apply that reads them next.
-            float* xb = c.xbuf;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            *(float4*)(xb + lane * 8) = make_float4(u[0], u[1], u[2], u[3]);
-            *(float4*)(xb + lane * 8 + 4) = make_float4(u[4], u[5], u[6], u[7]);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            const float4 a = *(const float4*)(xb + lane * 4);
-            const float4 b = *(const float4*)(xb + 256 + lane * 4);
-            RF_GLOBAL float4* q = gstore_ptr<float4>(L.updates, (base + j * 512) * 4);
-            if (h.upd_nt) {
-                st_nt(q + lane, a);
-                st_nt(q + 64 + lane, b);
-            } else {
-                q[lane] = a;
-                q[64 + lane] = b;
-            }
+            // f32 updates on whole cache lines, nontemporal in launches of
+            // many blocks (h.upd_nt), where no cache keeps them for the
+            // apply that reads them next
+            store8_f32_lines(c.xbuf, gstore_ptr<float4>(L.updates, (base + j * 512) * 4), lane, u, h.upd_nt != 0);
         }
     }
 
@@ -2349,7 +2353,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(RF_STEP_WAVE
     c.lds = lds;
     c.wtab = wtab[wave_in_wg];
     c.xbuf = nullptr;
-    if constexpr (!APPLY) {
+    if constexpr (!APPLY || sizeof(PT) == 4) {  // f32 updates or params: store8_f32_lines
         __shared__ __attribute__((aligned(16))) float xbuf[WAVES_PER_WG][512];
         c.xbuf = xbuf[wave_in_wg];
     }

@@ -610,9 +610,9 @@ struct StepShape {
 };
 constexpr StepShape STEP_SHAPE_STREAM = {2, 8};
 constexpr StepShape STEP_SHAPE_HEAVY = {4, 16};
-// Update-only launches of at least this many fast blocks per CU (64 per
-// resident wave at 3 waves per SIMD: far more updates than the caches hold)
-// store the updates nontemporally (KHp.upd_nt).
+// Launches of at least this many fast blocks per CU (64 per resident wave
+// at 3 waves per SIMD: far more output than the caches hold) store f32
+// updates and params nontemporally (KHp.upd_nt).
 constexpr int64_t UPD_NT_MIN_BLOCKS_PER_CU = 64 * 12;
 #ifndef RF_STEP_GRID_ROUNDS
 #define RF_STEP_GRID_ROUNDS 1
@@ -2123,13 +2123,13 @@ rf_status plan_launch(const rf_adam8_plan* plan, const rf_adam8_leaf* d_leaves, 
         const bool streaming = plan->apply && !msr && !psr && !(f & RF_EXACT);
         const StepShape shape = streaming ? STEP_SHAPE_STREAM : STEP_SHAPE_HEAVY;
         k.run = g.combo < 0 ? 1 : shape.run;
-        // Update-only launches store their f32 updates on whole cache lines;
-        // nontemporally from UPD_NT_MIN_BLOCKS_PER_CU blocks per CU on.
-        // Three store forms on one GPU (old half-line plain / whole-line
-        // nontemporal / whole-line plain): the Llama-7B update-only step
-        // 13.98-14.77 / 13.17-13.22 / 13.50-13.56 ms, GPT-2-small's launch
-        // 265 / 294 / 256 us.
-        k.upd_nt = (!plan->apply && g.combo >= 0 && g.units >= UPD_NT_MIN_BLOCKS_PER_CU * (int64_t)ds->num_cus) ? 1 : 0;
+        // f32 updates (update-only launches) and f32 params are stored on
+        // whole cache lines; nontemporally from UPD_NT_MIN_BLOCKS_PER_CU
+        // blocks per CU on.  Three store forms on one GPU (old half-line
+        // plain / whole-line nontemporal / whole-line plain): the Llama-7B
+        // update-only step 13.98-14.77 / 13.17-13.22 / 13.50-13.56 ms,
+        // GPT-2-small's launch 265 / 294 / 256 us.
+        k.upd_nt = (g.combo >= 0 && g.units >= UPD_NT_MIN_BLOCKS_PER_CU * (int64_t)ds->num_cus) ? 1 : 0;
         int64_t grid = step_grid(ds, occ, g, k.run, shape.per_wave);
         KHp kg = k;
         if (&g == carrier) {
